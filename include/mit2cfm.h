@@ -1,0 +1,207 @@
+/*
+ * mit2cfm.h -- C ABI of the MI355X (gfx950) DiT-CFM mel decoder.
+ *
+ * Drop-in boundary for the acoustic-model hot path of IndexTTS2-Metal: the
+ * CFG Euler solver over the DiT estimator (13 AdaRMSNorm blocks with U-ViT
+ * skips, WaveNet tail, AdaLN final layer).  It replaces the reference's
+ * Metal/MPS backend for this path, i.e. the mit2::MetalContext pass API
+ * (runtime/include/mit2/metal_context.hpp:55-297) as driven by
+ * run_cfm_euler_metal (runtime/impl/dit_cfm_bigvgan.cpp:3121).
+ *
+ * Conventions
+ *  - Plain C types only.  Host buffers are caller-owned, token-major fp32
+ *    ([tokens][channels] row-major), copied in; outputs are written into
+ *    caller buffers.  Device memory is owned by the context.
+ *  - Every call returns MIT2CFM_OK (0) or an error code; the message of the
+ *    last failure is returned by mit2cfm_last_error.  No C++ exception
+ *    crosses this boundary.
+ *  - A context is bound to one GPU and is not thread-safe: use one context
+ *    per thread (the reference's MetalContext has the same rule).  The
+ *    timestep-conditioning tables are per context, so the reference's
+ *    unlocked process-wide table cache has no counterpart here.
+ *  - Tensor names are the reference bundle's names
+ *    ("s2mel.net.cfm.estimator.*").
+ */
+#ifndef MIT2CFM_H
+#define MIT2CFM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIT2CFM_ABI_VERSION 1
+
+typedef struct mit2cfm_ctx mit2cfm_ctx;
+typedef int32_t mit2cfm_status;
+
+enum {
+  MIT2CFM_OK = 0,
+  MIT2CFM_E_ARG = 1,      /* invalid argument (shape, size, range)          */
+  MIT2CFM_E_MODEL = 2,    /* missing / malformed tensor, bad bundle          */
+  MIT2CFM_E_HIP = 3,      /* HIP runtime error or no HIP device              */
+  MIT2CFM_E_INTERNAL = 4  /* anything else                                   */
+};
+
+enum { MIT2CFM_DTYPE_F32 = 0, MIT2CFM_DTYPE_F16 = 1 };
+
+/* One named host tensor (element count, f32 or f16 payload). */
+typedef struct {
+  const char* name;
+  const void* data;
+  uint64_t elems;
+  int32_t dtype;
+} mit2cfm_tensor;
+
+int32_t mit2cfm_abi_version(void);
+
+/* Message of the last failed call on ctx (ctx may be NULL for calls that
+ * failed before a context existed; that message is thread-local). */
+const char* mit2cfm_last_error(const mit2cfm_ctx* ctx);
+
+/* ---- context --------------------------------------------------------------
+ * Replaces MetalContext construction (metal_context.mm:741-745) plus the lazy
+ * resident-weight upload (resident_buffer_f16_from_f32, metal_context.mm:677-694):
+ * all estimator weights are uploaded, weight-normed and laid out once here. */
+mit2cfm_status mit2cfm_create(const mit2cfm_tensor* tensors, uint32_t count, int32_t device,
+                              mit2cfm_ctx** out);
+/* Same, reading an MIT2 bundle directory or single-file bundle with the
+ * bundle loader (replaces mit2::Bundle, runtime/bundle.cpp). */
+mit2cfm_status mit2cfm_create_from_bundle(const char* bundle_path, int32_t device,
+                                          mit2cfm_ctx** out);
+/* Same, with seeded synthetic weights: N(0, stddev) f16 from seed base_seed + i
+ * for the i-th tensor in sorted-name order. */
+mit2cfm_status mit2cfm_create_synthetic(uint64_t base_seed, float stddev, int32_t device,
+                                        mit2cfm_ctx** out);
+void mit2cfm_destroy(mit2cfm_ctx* ctx);
+
+/* ---- decode ----------------------------------------------------------------
+ * Full CFG Euler decode: replaces run_cfm_euler_metal
+ * (dit_cfm_bigvgan.cpp:3121, via run_cfm_euler_metal_impl :2939 and
+ * run_cfm_euler_metal_single_pass :2367); result semantics of
+ * run_cfm_euler_cpu (:2908).  x0 [T][80], prompt [P][80], cond [T][512],
+ * style [192]; x_out [T][80] receives the final mel (prompt rows zero).
+ * cfg_rate > 0 batches the cond/null branches as B = 2; cfg_rate == 0 runs
+ * the cond branch only. */
+mit2cfm_status mit2cfm_decode(mit2cfm_ctx* ctx, const float* x0, const float* prompt,
+                              const float* cond, const float* style, uint32_t tokens,
+                              uint32_t prompt_tokens, uint32_t steps, float cfg_rate,
+                              float* x_out);
+/* The same decode on DEVICE pointers already resident in HBM (x0 [T][80],
+ * prompt [P][80], cond [T][512], style [192], x_out [T][80]).  The work is
+ * enqueued on the context's stream (mit2cfm_stream); with
+ * MIT2CFM_FLAG_SYNC the call waits for it.  No reference counterpart: the
+ * reference's unified memory needs no host/device split. */
+#define MIT2CFM_FLAG_SYNC 1u
+mit2cfm_status mit2cfm_decode_device(mit2cfm_ctx* ctx, const float* x0, const float* prompt,
+                                     const float* cond, const float* style, uint32_t tokens,
+                                     uint32_t prompt_tokens, uint32_t steps, float cfg_rate,
+                                     float* x_out, uint32_t flags);
+/* Decode that also returns every step's guided velocity
+ * v = (1+cfg)*dphi - cfg*null_dphi in v_trace [steps][T][80]; for the
+ * per-step parity check (the reference traces the same quantity in
+ * trace_s2mel_cfm_golden, dit_cfm_bigvgan.cpp:3126-3304). */
+mit2cfm_status mit2cfm_decode_trace(mit2cfm_ctx* ctx, const float* x0, const float* prompt,
+                                    const float* cond, const float* style, uint32_t tokens,
+                                    uint32_t prompt_tokens, uint32_t steps, float cfg_rate,
+                                    float* x_out, float* v_trace);
+/* nreq independent requests right-padded to t_max frames (batched serving):
+ * x0, prompt, x_out [nreq][t_max][80], cond [nreq][t_max][512],
+ * style [nreq][192], tokens[r] = valid frames, prompt_tokens[r].  Each
+ * request's key mask is [t < tokens[r]]; the reference semantics of a masked
+ * estimator (dit_cfm_bigvgan.cpp:1768 with mask) apply at the padded length.
+ * The reference runs one request per call (server.cpp:477-535). */
+mit2cfm_status mit2cfm_decode_batched(mit2cfm_ctx* ctx, uint32_t nreq, uint32_t t_max,
+                                      const uint32_t* tokens, const uint32_t* prompt_tokens,
+                                      const float* x0, const float* prompt, const float* cond,
+                                      const float* style, uint32_t steps, float cfg_rate,
+                                      float* x_out);
+
+/* ---- one estimator forward ---------------------------------------------------
+ * Replaces run_dit_estimator_step_metal (dit_cfm_bigvgan.cpp:2778); semantics
+ * of run_dit_estimator_step_cpu (:1768) for each of `batch` independent
+ * branches: x, prompt_x [B][T][80], cond [B][T][512], style [B][192],
+ * key_mask [B][T] (0/1), t the flow time; dphi_out [B][T][80]. */
+mit2cfm_status mit2cfm_estimator_step(mit2cfm_ctx* ctx, const float* x, const float* prompt_x,
+                                      const float* cond, const float* style,
+                                      const uint32_t* key_mask, float t, uint32_t batch,
+                                      uint32_t tokens, float* dphi_out);
+
+/* ---- stream control ----------------------------------------------------------- */
+void* mit2cfm_stream(mit2cfm_ctx* ctx); /* the context's hipStream_t */
+mit2cfm_status mit2cfm_synchronize(mit2cfm_ctx* ctx);
+/* Whole-decode hipGraph replay on (1, default) or off (0). */
+mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on);
+
+/* ---- stage entry points (parity harness; host pointers, synchronous) ---------
+ * One per reference CPU stage, mirroring the reference's --test-dit-* harnesses
+ * (main.cpp:2909-2989).  rows = batch * tokens; t1/t2 are 512-d embeddings. */
+/* gpt.cpp:5404 run_timestep_embedder_cpu; which = 1 (t_embedder) or 2 (t_embedder2) */
+mit2cfm_status mit2cfm_stage_timestep_embedder(mit2cfm_ctx* ctx, float t, int32_t which,
+                                               float* out512);
+/* dit_cfm_bigvgan.cpp:1 run_dit_input_merge_cpu (per branch b: style[b]) */
+mit2cfm_status mit2cfm_stage_input_merge(mit2cfm_ctx* ctx, const float* x, const float* prompt_x,
+                                         const float* cond, const float* style, uint32_t batch,
+                                         uint32_t tokens, float* out);
+/* :260 run_adaptive_norm_cpu; norm_id 0..12 attention_norm, 13..25 ffn_norm, 26 transformer.norm.
+ * The output is the f16 GEMM operand, widened back to fp32. */
+mit2cfm_status mit2cfm_stage_adaptive_norm(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                           uint32_t rows, int32_t norm_id, float* out);
+/* :469 run_dit_attention_core_cpu_masked_layer (wqkv, RoPE, masked attention, wo) */
+mit2cfm_status mit2cfm_stage_attention_core(mit2cfm_ctx* ctx, const float* in,
+                                            const uint32_t* key_mask, uint32_t batch,
+                                            uint32_t tokens, int32_t layer, float* out);
+/* :727 run_dit_feed_forward_cpu_layer (SwiGLU) */
+mit2cfm_status mit2cfm_stage_feed_forward(mit2cfm_ctx* ctx, const float* in, uint32_t rows,
+                                          int32_t layer, float* out);
+/* :816 run_dit_transformer_block_cpu_layer; skip is NULL for layers 0..6 */
+mit2cfm_status mit2cfm_stage_block(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                   const uint32_t* key_mask, uint32_t batch, uint32_t tokens,
+                                   int32_t layer, const float* skip, float* out);
+/* :868 run_dit_transformer_stack_cpu (13 blocks + final AdaRMSNorm) */
+mit2cfm_status mit2cfm_stage_stack(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                   const uint32_t* key_mask, uint32_t batch, uint32_t tokens,
+                                   float* out);
+/* :1053 run_dit_post_transformer_proj_cpu (long_skip, conv1, res_projection) */
+mit2cfm_status mit2cfm_stage_post(mit2cfm_ctx* ctx, const float* xres, const float* xmel,
+                                  uint32_t rows, float* long_skip, float* conv1,
+                                  float* res_proj);
+/* :1464 run_wavenet_stack_global_cond_cpu */
+mit2cfm_status mit2cfm_stage_wavenet(mit2cfm_ctx* ctx, const float* in, const float* t2,
+                                     const uint32_t* key_mask, uint32_t batch, uint32_t tokens,
+                                     float* out);
+/* :1172 run_dit_final_layer_cpu */
+mit2cfm_status mit2cfm_stage_final_layer(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                         uint32_t rows, float* out);
+/* The MFMA GEMM alone (replaces pass_linear_rows_mps, metal_context.mm:328-378):
+ * out[M][N] = f16(A)[M][K] . f16(W)[N][K]^T + bias (bias may be NULL);
+ * K % 32 == 0, N % 64 == 0. */
+mit2cfm_status mit2cfm_op_linear(mit2cfm_ctx* ctx, const float* a, const float* w,
+                                 const float* bias, uint32_t m, uint32_t n, uint32_t k,
+                                 float* out);
+
+/* ---- seeded synthetic data (tokenizer_tests.cpp:2121 make_deterministic_normal_noise) */
+mit2cfm_status mit2cfm_normal_noise(uint32_t tokens, uint32_t channels, uint64_t seed,
+                                    float temperature, float* out);
+/* Estimator tensor inventory used by mit2cfm_create_synthetic (sorted names). */
+uint32_t mit2cfm_synthetic_tensor_count(void);
+/* name, ndim (<= 4), shape[4], dtype (MIT2CFM_DTYPE_*) and element count of tensor i. */
+mit2cfm_status mit2cfm_synthetic_tensor_info(uint32_t i, const char** name, uint32_t* ndim,
+                                             int64_t* shape4, int32_t* dtype, uint64_t* elems);
+/* Payload of tensor i (elems * 2 bytes for f16, * 4 for f32) into out. */
+mit2cfm_status mit2cfm_synthetic_tensor_fill(uint32_t i, uint64_t base_seed, float stddev,
+                                             void* out);
+/* Opens a bundle with the loader and applies every validation rule of the
+ * format (replaces the --inspect-model-bundle gate, main.cpp; rules in
+ * docs/native_bundle.md "Validation Rules"); verify_sha256 != 0 also checks
+ * each payload's SHA-256.  Needs no GPU. */
+mit2cfm_status mit2cfm_inspect_bundle(const char* bundle_path, uint64_t* tensor_count,
+                                      uint64_t* payload_bytes, uint32_t verify_sha256);
+/* Writes the synthetic estimator weights as an MIT2 bundle directory. */
+mit2cfm_status mit2cfm_write_synthetic_bundle(const char* dir, uint64_t base_seed, float stddev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIT2CFM_H */

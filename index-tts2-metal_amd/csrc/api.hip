@@ -1,0 +1,443 @@
+// api.hip -- extern "C" boundary (include/mit2cfm.h) over the HIP engine.
+// No exception crosses the boundary: every entry point catches, records the
+// message on the context (or thread-locally) and returns a status code.
+#include "../../include/mit2cfm.h"
+
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../runtime/bundle.h"
+#include "../runtime/synth.h"
+#include "engine.h"
+
+struct mit2cfm_ctx {
+  std::unique_ptr<mit2hip::Engine> eng;
+  std::string err;
+  // device staging for the host-pointer decode entry points
+  void* io = nullptr;
+  size_t io_bytes = 0;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+mit2cfm_status fail(mit2cfm_ctx* ctx, mit2cfm_status code, const std::string& msg) {
+  if (ctx)
+    ctx->err = msg;
+  else
+    g_err = msg;
+  return code;
+}
+
+template <typename F>
+mit2cfm_status guarded(mit2cfm_ctx* ctx, F&& f) {
+  try {
+    f();
+    return MIT2CFM_OK;
+  } catch (const std::invalid_argument& e) {
+    return fail(ctx, MIT2CFM_E_ARG, e.what());
+  } catch (const mit2hip::HipError& e) {
+    return fail(ctx, MIT2CFM_E_HIP, e.what());
+  } catch (const std::out_of_range& e) {
+    return fail(ctx, MIT2CFM_E_ARG, e.what());
+  } catch (const std::runtime_error& e) {
+    return fail(ctx, MIT2CFM_E_MODEL, e.what());
+  } catch (const std::exception& e) {
+    return fail(ctx, MIT2CFM_E_INTERNAL, e.what());
+  } catch (...) {
+    return fail(ctx, MIT2CFM_E_INTERNAL, "unknown error");
+  }
+}
+
+void require(bool ok, const char* msg) {
+  if (!ok) throw std::invalid_argument(msg);
+}
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw mit2hip::HipError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+mit2cfm_status make_ctx(const std::vector<mit2hip::HostTensor>& ts, int32_t device,
+                        mit2cfm_ctx** out) {
+  if (!out) return fail(nullptr, MIT2CFM_E_ARG, "out must not be NULL");
+  *out = nullptr;
+  auto* c = new mit2cfm_ctx();
+  const mit2cfm_status st = guarded(nullptr, [&] {
+    int n = 0;
+    hip_check(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (device < 0 || device >= n)
+      throw mit2hip::HipError("HIP device " + std::to_string(device) + " not available (" +
+                              std::to_string(n) + " devices)");
+    c->eng = std::make_unique<mit2hip::Engine>(ts, device);
+  });
+  if (st != MIT2CFM_OK) {
+    delete c;
+    return st;
+  }
+  *out = c;
+  return MIT2CFM_OK;
+}
+
+// Device staging buffer of the context, grown on demand.
+float* staging(mit2cfm_ctx* c, size_t floats) {
+  const size_t bytes = floats * sizeof(float);
+  if (bytes > c->io_bytes) {
+    if (c->io) hip_check(hipFree(c->io), "hipFree");
+    c->io = nullptr;
+    c->io_bytes = 0;
+    hip_check(hipMalloc(&c->io, bytes), "hipMalloc");
+    c->io_bytes = bytes;
+  }
+  return static_cast<float*>(c->io);
+}
+
+// Host-pointer decode for nreq padded requests (x0/prompt/x_out [nreq][T][80]).
+void host_decode(mit2cfm_ctx* c, uint32_t nreq, uint32_t T, const uint32_t* valid,
+                 const uint32_t* P, const float* x0, const float* prompt, const float* cond,
+                 const float* style, uint32_t steps, float cfg, float* x_out, float* v_trace) {
+  const size_t nx = (size_t)nreq * T * 80;
+  const size_t nc = (size_t)nreq * T * 512;
+  const size_t ns = (size_t)nreq * 192;
+  const size_t nv = v_trace ? nx * steps : 0;
+  float* base = staging(c, 3 * nx + nc + ns + nv);
+  float* d_x0 = base;
+  float* d_prompt = d_x0 + nx;
+  float* d_cond = d_prompt + nx;
+  float* d_style = d_cond + nc;
+  float* d_out = d_style + ns;
+  float* d_v = v_trace ? d_out + nx : nullptr;
+  hipStream_t s = c->eng->stream();
+  hip_check(hipMemcpyAsync(d_x0, x0, nx * 4, hipMemcpyHostToDevice, s), "copy x0");
+  hip_check(hipMemcpyAsync(d_prompt, prompt, nx * 4, hipMemcpyHostToDevice, s), "copy prompt");
+  hip_check(hipMemcpyAsync(d_cond, cond, nc * 4, hipMemcpyHostToDevice, s), "copy cond");
+  hip_check(hipMemcpyAsync(d_style, style, ns * 4, hipMemcpyHostToDevice, s), "copy style");
+  c->eng->decode_device(d_x0, d_prompt, d_cond, d_style, (int)nreq, (int)T, valid, P, (int)steps,
+                        cfg, d_out, d_v);
+  hip_check(hipMemcpyAsync(x_out, d_out, nx * 4, hipMemcpyDeviceToHost, s), "copy x_out");
+  if (v_trace) hip_check(hipMemcpyAsync(v_trace, d_v, nv * 4, hipMemcpyDeviceToHost, s), "copy v");
+  c->eng->sync();
+}
+
+// Packs a single request's [P][80] prompt into [T][80].
+std::vector<float> pad_prompt(const float* prompt, uint32_t T, uint32_t P) {
+  std::vector<float> p((size_t)T * 80, 0.0f);
+  if (P) std::memcpy(p.data(), prompt, (size_t)P * 80 * 4);
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t mit2cfm_abi_version(void) { return MIT2CFM_ABI_VERSION; }
+
+const char* mit2cfm_last_error(const mit2cfm_ctx* ctx) {
+  return ctx ? ctx->err.c_str() : g_err.c_str();
+}
+
+mit2cfm_status mit2cfm_create(const mit2cfm_tensor* tensors, uint32_t count, int32_t device,
+                              mit2cfm_ctx** out) {
+  if (!tensors && count) return fail(nullptr, MIT2CFM_E_ARG, "tensors must not be NULL");
+  std::vector<mit2hip::HostTensor> ts;
+  for (uint32_t i = 0; i < count; ++i) {
+    if (!tensors[i].name || !tensors[i].data)
+      return fail(nullptr, MIT2CFM_E_ARG, "tensor " + std::to_string(i) + " has no name or data");
+    ts.push_back({tensors[i].name, tensors[i].data, tensors[i].elems, tensors[i].dtype});
+  }
+  return make_ctx(ts, device, out);
+}
+
+mit2cfm_status mit2cfm_create_from_bundle(const char* bundle_path, int32_t device,
+                                          mit2cfm_ctx** out) {
+  if (!bundle_path || !out) return fail(nullptr, MIT2CFM_E_ARG, "bundle_path/out must not be NULL");
+  std::unique_ptr<mit2::Bundle> b;
+  const mit2cfm_status st = guarded(nullptr, [&] { b = std::make_unique<mit2::Bundle>(bundle_path); });
+  if (st != MIT2CFM_OK) return st;
+  std::vector<mit2hip::HostTensor> ts;
+  for (const auto& info : b->tensors()) {
+    if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0) continue;
+    int dt;
+    if (info.dtype == "f32")
+      dt = 0;
+    else if (info.dtype == "f16")
+      dt = 1;
+    else
+      continue;
+    ts.push_back({info.name, b->tensor_data(info), info.nbytes / (dt ? 2 : 4), dt});
+  }
+  return make_ctx(ts, device, out);
+}
+
+mit2cfm_status mit2cfm_create_synthetic(uint64_t base_seed, float stddev, int32_t device,
+                                        mit2cfm_ctx** out) {
+  std::vector<std::vector<uint8_t>> bufs;
+  std::vector<mit2hip::HostTensor> ts;
+  const mit2cfm_status st = guarded(nullptr, [&] {
+    const auto& specs = mit2::estimator_tensor_specs();
+    bufs.reserve(specs.size());
+    for (size_t i = 0; i < specs.size(); ++i) {
+      bufs.push_back(mit2::synth_tensor_bytes(i, base_seed, stddev));
+      const bool f16 = specs[i].dtype == "f16";
+      ts.push_back({specs[i].name, bufs.back().data(), bufs.back().size() / (f16 ? 2 : 4),
+                    f16 ? 1 : 0});
+    }
+  });
+  if (st != MIT2CFM_OK) return st;
+  return make_ctx(ts, device, out);
+}
+
+void mit2cfm_destroy(mit2cfm_ctx* ctx) {
+  if (!ctx) return;
+  try {
+    if (ctx->io) (void)hipFree(ctx->io);
+    ctx->eng.reset();
+  } catch (...) {
+  }
+  delete ctx;
+}
+
+mit2cfm_status mit2cfm_decode(mit2cfm_ctx* ctx, const float* x0, const float* prompt,
+                              const float* cond, const float* style, uint32_t tokens,
+                              uint32_t prompt_tokens, uint32_t steps, float cfg_rate,
+                              float* x_out) {
+  return mit2cfm_decode_trace(ctx, x0, prompt, cond, style, tokens, prompt_tokens, steps, cfg_rate,
+                              x_out, nullptr);
+}
+
+mit2cfm_status mit2cfm_decode_trace(mit2cfm_ctx* ctx, const float* x0, const float* prompt,
+                                    const float* cond, const float* style, uint32_t tokens,
+                                    uint32_t prompt_tokens, uint32_t steps, float cfg_rate,
+                                    float* x_out, float* v_trace) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(x0 && cond && style && x_out, "x0, cond, style and x_out must not be NULL");
+    require(prompt || prompt_tokens == 0, "prompt must not be NULL when prompt_tokens > 0");
+    require(tokens > 0 && prompt_tokens <= tokens, "need 0 < tokens and prompt_tokens <= tokens");
+    const auto p = pad_prompt(prompt, tokens, prompt_tokens);
+    host_decode(ctx, 1, tokens, &tokens, &prompt_tokens, x0, p.data(), cond, style, steps,
+                cfg_rate, x_out, v_trace);
+  });
+}
+
+mit2cfm_status mit2cfm_decode_device(mit2cfm_ctx* ctx, const float* x0, const float* prompt,
+                                     const float* cond, const float* style, uint32_t tokens,
+                                     uint32_t prompt_tokens, uint32_t steps, float cfg_rate,
+                                     float* x_out, uint32_t flags) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(x0 && cond && style && x_out, "x0, cond, style and x_out must not be NULL");
+    require(prompt || prompt_tokens == 0, "prompt must not be NULL when prompt_tokens > 0");
+    require(tokens > 0 && prompt_tokens <= tokens, "need 0 < tokens and prompt_tokens <= tokens");
+    ctx->eng->decode_device(x0, prompt ? prompt : x0, cond, style, 1, (int)tokens, &tokens,
+                            &prompt_tokens, (int)steps, cfg_rate, x_out, nullptr);
+    if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}
+
+mit2cfm_status mit2cfm_decode_batched(mit2cfm_ctx* ctx, uint32_t nreq, uint32_t t_max,
+                                      const uint32_t* tokens, const uint32_t* prompt_tokens,
+                                      const float* x0, const float* prompt, const float* cond,
+                                      const float* style, uint32_t steps, float cfg_rate,
+                                      float* x_out) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(nreq > 0 && t_max > 0, "nreq and t_max must be positive");
+    require(tokens && prompt_tokens && x0 && prompt && cond && style && x_out,
+            "pointer arguments must not be NULL");
+    host_decode(ctx, nreq, t_max, tokens, prompt_tokens, x0, prompt, cond, style, steps, cfg_rate,
+                x_out, nullptr);
+  });
+}
+
+mit2cfm_status mit2cfm_estimator_step(mit2cfm_ctx* ctx, const float* x, const float* prompt_x,
+                                      const float* cond, const float* style,
+                                      const uint32_t* key_mask, float t, uint32_t batch,
+                                      uint32_t tokens, float* dphi_out) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(x && prompt_x && cond && style && key_mask && dphi_out,
+            "pointer arguments must not be NULL");
+    require(batch > 0 && tokens > 0, "batch and tokens must be positive");
+    const size_t R = (size_t)batch * tokens;
+    float* base = staging(ctx, R * 80 * 3 + R * 512 + (size_t)batch * 192 + R);
+    float* d_x = base;
+    float* d_p = d_x + R * 80;
+    float* d_c = d_p + R * 80;
+    float* d_s = d_c + R * 512;
+    float* d_o = d_s + (size_t)batch * 192;
+    uint32_t* d_m = reinterpret_cast<uint32_t*>(d_o + R * 80);
+    hipStream_t s = ctx->eng->stream();
+    hip_check(hipMemcpyAsync(d_x, x, R * 320, hipMemcpyHostToDevice, s), "copy x");
+    hip_check(hipMemcpyAsync(d_p, prompt_x, R * 320, hipMemcpyHostToDevice, s), "copy prompt_x");
+    hip_check(hipMemcpyAsync(d_c, cond, R * 2048, hipMemcpyHostToDevice, s), "copy cond");
+    hip_check(hipMemcpyAsync(d_s, style, (size_t)batch * 768, hipMemcpyHostToDevice, s), "copy style");
+    hip_check(hipMemcpyAsync(d_m, key_mask, R * 4, hipMemcpyHostToDevice, s), "copy mask");
+    ctx->eng->estimator_step_device(d_x, d_p, d_c, d_s, d_m, t, (int)batch, (int)tokens, d_o);
+    hip_check(hipMemcpyAsync(dphi_out, d_o, R * 320, hipMemcpyDeviceToHost, s), "copy dphi");
+    ctx->eng->sync();
+  });
+}
+
+void* mit2cfm_stream(mit2cfm_ctx* ctx) { return ctx && ctx->eng ? (void*)ctx->eng->stream() : nullptr; }
+
+mit2cfm_status mit2cfm_synchronize(mit2cfm_ctx* ctx) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] { ctx->eng->sync(); });
+}
+
+mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  ctx->eng->set_use_graph(on != 0);
+  return MIT2CFM_OK;
+}
+
+// ---- stages
+#define STAGE_BODY(...)                                                   \
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL"); \
+  return guarded(ctx, [&] { __VA_ARGS__; })
+
+mit2cfm_status mit2cfm_stage_timestep_embedder(mit2cfm_ctx* ctx, float t, int32_t which,
+                                               float* out512) {
+  STAGE_BODY(require(out512 && (which == 1 || which == 2), "bad arguments");
+             ctx->eng->stage_timestep_embedder(t, which, out512));
+}
+
+mit2cfm_status mit2cfm_stage_input_merge(mit2cfm_ctx* ctx, const float* x, const float* prompt_x,
+                                         const float* cond, const float* style, uint32_t batch,
+                                         uint32_t tokens, float* out) {
+  STAGE_BODY(require(x && prompt_x && cond && style && out && batch && tokens, "bad arguments");
+             ctx->eng->stage_input_merge(x, prompt_x, cond, style, (int)batch, (int)tokens, out));
+}
+
+mit2cfm_status mit2cfm_stage_adaptive_norm(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                           uint32_t rows, int32_t norm_id, float* out) {
+  STAGE_BODY(require(in && t1 && out && rows, "bad arguments");
+             ctx->eng->stage_adaptive_norm(in, t1, (int)rows, norm_id, out));
+}
+
+mit2cfm_status mit2cfm_stage_attention_core(mit2cfm_ctx* ctx, const float* in,
+                                            const uint32_t* key_mask, uint32_t batch,
+                                            uint32_t tokens, int32_t layer, float* out) {
+  STAGE_BODY(require(in && key_mask && out && batch && tokens, "bad arguments");
+             ctx->eng->stage_attention_core(in, key_mask, (int)batch, (int)tokens, layer, out));
+}
+
+mit2cfm_status mit2cfm_stage_feed_forward(mit2cfm_ctx* ctx, const float* in, uint32_t rows,
+                                          int32_t layer, float* out) {
+  STAGE_BODY(require(in && out && rows, "bad arguments");
+             ctx->eng->stage_feed_forward(in, (int)rows, layer, out));
+}
+
+mit2cfm_status mit2cfm_stage_block(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                   const uint32_t* key_mask, uint32_t batch, uint32_t tokens,
+                                   int32_t layer, const float* skip, float* out) {
+  STAGE_BODY(require(in && t1 && key_mask && out && batch && tokens, "bad arguments");
+             ctx->eng->stage_block(in, t1, key_mask, (int)batch, (int)tokens, layer, skip, out));
+}
+
+mit2cfm_status mit2cfm_stage_stack(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                   const uint32_t* key_mask, uint32_t batch, uint32_t tokens,
+                                   float* out) {
+  STAGE_BODY(require(in && t1 && key_mask && out && batch && tokens, "bad arguments");
+             ctx->eng->stage_stack(in, t1, key_mask, (int)batch, (int)tokens, out));
+}
+
+mit2cfm_status mit2cfm_stage_post(mit2cfm_ctx* ctx, const float* xres, const float* xmel,
+                                  uint32_t rows, float* long_skip, float* conv1,
+                                  float* res_proj) {
+  STAGE_BODY(require(xres && xmel && long_skip && conv1 && res_proj && rows, "bad arguments");
+             ctx->eng->stage_post(xres, xmel, (int)rows, long_skip, conv1, res_proj));
+}
+
+mit2cfm_status mit2cfm_stage_wavenet(mit2cfm_ctx* ctx, const float* in, const float* t2,
+                                     const uint32_t* key_mask, uint32_t batch, uint32_t tokens,
+                                     float* out) {
+  STAGE_BODY(require(in && t2 && key_mask && out && batch && tokens, "bad arguments");
+             ctx->eng->stage_wavenet(in, t2, key_mask, (int)batch, (int)tokens, out));
+}
+
+mit2cfm_status mit2cfm_stage_final_layer(mit2cfm_ctx* ctx, const float* in, const float* t1,
+                                         uint32_t rows, float* out) {
+  STAGE_BODY(require(in && t1 && out && rows, "bad arguments");
+             ctx->eng->stage_final_layer(in, t1, (int)rows, out));
+}
+
+mit2cfm_status mit2cfm_op_linear(mit2cfm_ctx* ctx, const float* a, const float* w,
+                                 const float* bias, uint32_t m, uint32_t n, uint32_t k,
+                                 float* out) {
+  STAGE_BODY(require(a && w && out, "bad arguments");
+             ctx->eng->op_linear(a, w, bias, (int)m, (int)n, (int)k, out));
+}
+
+// ---- synthetic data
+mit2cfm_status mit2cfm_normal_noise(uint32_t tokens, uint32_t channels, uint64_t seed,
+                                    float temperature, float* out) {
+  if (!out) return fail(nullptr, MIT2CFM_E_ARG, "out must not be NULL");
+  return guarded(nullptr, [&] {
+    const auto v = mit2::make_deterministic_normal_noise(tokens, channels, seed, temperature);
+    std::memcpy(out, v.data(), v.size() * 4);
+  });
+}
+
+uint32_t mit2cfm_synthetic_tensor_count(void) {
+  return (uint32_t)mit2::estimator_tensor_specs().size();
+}
+
+mit2cfm_status mit2cfm_synthetic_tensor_info(uint32_t i, const char** name, uint32_t* ndim,
+                                             int64_t* shape4, int32_t* dtype, uint64_t* elems) {
+  const auto& specs = mit2::estimator_tensor_specs();
+  if (i >= specs.size()) return fail(nullptr, MIT2CFM_E_ARG, "tensor index out of range");
+  const auto& s = specs[i];
+  if (name) *name = s.name.c_str();
+  if (ndim) *ndim = (uint32_t)s.shape.size();
+  uint64_t n = 1;
+  for (size_t d = 0; d < s.shape.size(); ++d) {
+    if (shape4 && d < 4) shape4[d] = s.shape[d];
+    n *= (uint64_t)s.shape[d];
+  }
+  if (dtype) *dtype = s.dtype == "f16" ? MIT2CFM_DTYPE_F16 : MIT2CFM_DTYPE_F32;
+  if (elems) *elems = n;
+  return MIT2CFM_OK;
+}
+
+mit2cfm_status mit2cfm_synthetic_tensor_fill(uint32_t i, uint64_t base_seed, float stddev,
+                                             void* out) {
+  if (!out) return fail(nullptr, MIT2CFM_E_ARG, "out must not be NULL");
+  return guarded(nullptr, [&] {
+    const auto b = mit2::synth_tensor_bytes(i, base_seed, stddev);
+    std::memcpy(out, b.data(), b.size());
+  });
+}
+
+mit2cfm_status mit2cfm_inspect_bundle(const char* bundle_path, uint64_t* tensor_count,
+                                      uint64_t* payload_bytes, uint32_t verify_sha256) {
+  if (!bundle_path) return fail(nullptr, MIT2CFM_E_ARG, "bundle_path must not be NULL");
+  return guarded(nullptr, [&] {
+    mit2::Bundle b(bundle_path);
+    if (verify_sha256) {
+      for (const auto& t : b.tensors()) {
+        if (mit2::sha256_hex(b.tensor_data(t), (size_t)t.nbytes) != t.sha256)
+          throw std::runtime_error("sha256 mismatch: " + t.name);
+      }
+    }
+    if (tensor_count) *tensor_count = b.tensor_count();
+    if (payload_bytes) *payload_bytes = b.total_tensor_bytes();
+  });
+}
+
+mit2cfm_status mit2cfm_write_synthetic_bundle(const char* dir, uint64_t base_seed, float stddev) {
+  if (!dir) return fail(nullptr, MIT2CFM_E_ARG, "dir must not be NULL");
+  return guarded(nullptr, [&] {
+    const auto& specs = mit2::estimator_tensor_specs();
+    std::vector<mit2::TensorPayload> ts;
+    for (size_t i = 0; i < specs.size(); ++i)
+      ts.push_back({specs[i].name, specs[i].shape, specs[i].dtype, "s2mel",
+                    mit2::synth_tensor_bytes(i, base_seed, stddev)});
+    mit2::write_bundle(dir, ts);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+// device_common.h -- shared types and helpers for the gfx950 (CDNA4) kernels
+// of the DiT-CFM decoder.
+//
+// Conventions used by every kernel in this directory:
+//  * activations are token-major row-major; row m = branch * T + t;
+//  * GEMM operands are f16 with fp32 accumulation on the matrix cores
+//    (v_mfma_f32_16x16x32_f16, 64-lane wavefronts);
+//  * the residual streams (transformer x/h, WaveNet x/out) stay fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mit2hip {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// D(16x16, fp32) += A(16x32, f16) * B(32x16, f16).
+// Lane l supplies A row (l % 16) and B column (l % 16), each with the eight
+// K-slots of lane group l / 16.  D element (row 4*(l/16)+i, col l%16) is in
+// component i of lane l.
+__device__ __forceinline__ floatx4 mfma16x16x32(const half8& a, const half8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + __expf(-v)); }
+
+// tanh with the reference kernel's saturation (|a| > 20 -> +-1).
+__device__ __forceinline__ float tanh_sat(float a) {
+  if (a > 20.0f) return 1.0f;
+  if (a < -20.0f) return -1.0f;
+  return tanhf(a);
+}
+
+// Reflect index for padding (k-tap conv, reflect mode).  Any integer maps into
+// [0, T) by repeated mirroring at 0 and T-1; a one-token sequence maps to 0.
+__device__ __forceinline__ int reflect_index(int src, int T) {
+  if (T <= 1) return 0;
+  while (src < 0 || src >= T) {
+    if (src < 0) src = -src;
+    if (src >= T) src = 2 * T - 2 - src;
+  }
+  return src;
+}
+
+}  // namespace mit2hip

@@ -1,0 +1,133 @@
+// engine.h -- host-side engine of the HIP DiT-CFM decoder: resident weights,
+// workspace, kernel sequences for one estimator forward and for a whole Euler
+// decode (captured once per shape as a hipGraph and replayed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "device_common.h"
+
+namespace mit2hip {
+
+struct HipError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+// One named host tensor handed to the engine (f32 or f16 payload).
+struct HostTensor {
+  std::string name;
+  const void* data = nullptr;
+  uint64_t elems = 0;
+  int dtype = 0;  // 0 = f32, 1 = f16
+};
+
+// Device arena: one hipMalloc, bump-allocated, 256-byte aligned slices.
+class Arena {
+ public:
+  Arena() = default;
+  ~Arena();
+  Arena(const Arena&) = delete;
+  Arena& operator=(const Arena&) = delete;
+  void reserve(size_t bytes);  // frees any previous block
+  void* take(size_t bytes);
+  size_t used() const { return used_; }
+  size_t capacity() const { return cap_; }
+
+ private:
+  char* base_ = nullptr;
+  size_t cap_ = 0;
+  size_t used_ = 0;
+};
+
+struct Weights;    // resident weights (engine.hip)
+struct Workspace;  // activations (engine.hip)
+
+class Engine {
+ public:
+  Engine(const std::vector<HostTensor>& tensors, int device);
+  ~Engine();
+
+  int device() const { return device_; }
+  hipStream_t stream() const { return stream_; }
+  size_t weight_bytes() const;
+
+  // Full CFG Euler decode (run_cfm_euler_cpu semantics), nreq independent
+  // requests padded to T tokens.  All pointers are DEVICE pointers:
+  //   x0, prompt: [nreq][T][80]; cond: [nreq][T][512]; style: [nreq][192];
+  //   valid_T, P: per-request valid length and prompt length (host arrays);
+  //   x_out: [nreq][T][80]; vtrace (optional): [steps][nreq][T][80].
+  // Enqueues on stream(); does not synchronise.
+  void decode_device(const float* x0, const float* prompt, const float* cond, const float* style,
+                     int nreq, int T, const uint32_t* valid_T, const uint32_t* P, int steps,
+                     float cfg, float* x_out, float* vtrace);
+
+  // One estimator forward for B independent branches (run_dit_estimator_step_cpu
+  // semantics) on DEVICE pointers: x, prompt_x [B][T][80], cond [B][T][512],
+  // style [B][192], mask [B][T]; dphi [B][T][80].  Synchronous.
+  void estimator_step_device(const float* x, const float* prompt_x, const float* cond,
+                             const float* style, const uint32_t* mask, float t, int B, int T,
+                             float* dphi);
+
+  // ---- stage entry points (host pointers, synchronous), one per reference
+  // CPU stage, used by the parity tests.  rows = B*T.
+  void stage_timestep_embedder(float t, int which, float* out512);
+  void stage_input_merge(const float* x, const float* prompt_x, const float* cond,
+                         const float* style, int B, int T, float* out);
+  void stage_adaptive_norm(const float* in, const float* t1, int rows, int norm_id, float* out);
+  void stage_attention_core(const float* in, const uint32_t* mask, int B, int T, int layer,
+                            float* out);
+  void stage_feed_forward(const float* in, int rows, int layer, float* out);
+  void stage_block(const float* in, const float* t1, const uint32_t* mask, int B, int T,
+                   int layer, const float* skip, float* out);
+  void stage_stack(const float* in, const float* t1, const uint32_t* mask, int B, int T,
+                   float* out);
+  void stage_post(const float* xres, const float* xmel, int rows, float* long_skip, float* conv1,
+                  float* res_proj);
+  void stage_wavenet(const float* in, const float* t2, const uint32_t* mask, int B, int T,
+                     float* out);
+  void stage_final_layer(const float* in, const float* t1, int rows, float* out);
+  // Plain MFMA GEMM on f16-rounded operands: out[M][N] = A . W^T + bias.
+  void op_linear(const float* A, const float* W, const float* bias, int M, int N, int K,
+                 float* out);
+
+  // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
+  void set_use_graph(bool on) { use_graph_ = on; }
+  void sync();
+
+ private:
+  void ensure_workspace(int B, int T, int S, int nreq);
+  void ensure_rope(int T);
+  void enqueue_tables(const float* tvals_dev, int S);
+  void enqueue_layer(int l, int B, int T, const float* tab, float* cur, float* hbuf,
+                     const half_t* skip16, half_t* out16);
+  void enqueue_transformer(int B, int T, const float* tab);
+  void enqueue_estimator(int B, int T, int step_slot);
+  void enqueue_decode(const float* x0, const float* prompt, const float* cond, const float* style,
+                      int nreq, int T, int steps, float cfg, float* vtrace);
+  void upload_stage_tables(const float* t1_host, const float* t2_host);
+
+  int device_ = 0;
+  hipStream_t stream_ = nullptr;
+  bool use_graph_ = true;
+  std::unique_ptr<Weights> w_;
+  std::unique_ptr<Workspace> ws_;
+  struct GraphEntry {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+  };
+  // key: nreq, T, steps, cfg bits, vtrace ptr, io pointers
+  std::map<std::tuple<int, int, int, uint32_t, const void*, const void*, const void*, const void*,
+                      const void*, const void*>,
+           GraphEntry>
+      graphs_;
+  void clear_graphs();
+};
+
+}  // namespace mit2hip

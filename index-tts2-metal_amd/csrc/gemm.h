@@ -1,0 +1,69 @@
+// gemm.h -- f16 MFMA GEMM with fused epilogues for the DiT-CFM decoder.
+//
+// C[M, N] = A[M, K] . W[N, K]^T, fp32 accumulation.  W is a resident f16
+// weight whose rows may be permuted at upload so that an epilogue finds the
+// two operands it combines (SwiGLU halves, WaveNet gate halves, RoPE pairs)
+// in the same lane.  K must be a multiple of 32 and N a multiple of the tile
+// width (weights are zero-padded at upload where the model's K is not).
+#pragma once
+
+#include "device_common.h"
+
+namespace mit2hip {
+
+enum AMode : int {
+  A_PLAIN = 0,   // A[m][k] = A[m*lda + k]
+  A_CONCAT = 1,  // k <  K1: A[m*lda + k];  k >= K1: A2[m*lda2 + k - K1]
+  A_CONV5 = 2,   // k = tap*C + c: A[(b*T + reflect(t + tap - 2))*lda + c], m = b*T + t
+};
+
+enum EpiMode : int {
+  EPI_F32 = 0,        // C32 = acc + bias + res (bias/res optional); optional f16 copy C16
+  EPI_F16 = 1,        // C16 = acc + bias
+  EPI_SWIGLU = 2,     // W rows interleaved [w1 x16 | w3 x16]: C16[m][c] = silu(h1) * h3
+  EPI_GATE = 3,       // W rows interleaved [a x16 | b x16]: C16 = tanh(a+ca) * sigmoid(b+cb)
+  EPI_QKV = 4,        // W rows paired for RoPE: write Q (rotated, x1/8), K (rotated), V^T
+  EPI_RESSKIP = 5,    // WaveNet res/skip update (N = 2*512)
+  EPI_FINALSKIP = 6,  // last WaveNet layer (N = 512), plus the res_projection add
+  EPI_DUAL = 7,       // cols < N/2 -> C32 (+ f16 copy C16); cols >= N/2 -> C32b
+};
+
+struct GemmArgs {
+  int M = 0, N = 0, K = 0;
+  // A operand
+  const half_t* A = nullptr;
+  int lda = 0;
+  const half_t* A2 = nullptr;
+  int lda2 = 0;
+  int K1 = 0;
+  int T = 0;        // tokens per branch (A_CONV5, EPI_QKV)
+  int conv_c = 0;   // input channels per tap (A_CONV5)
+  // weights
+  const half_t* W = nullptr;
+  int ldw = 0;
+  // epilogue
+  const float* bias = nullptr;
+  const float* res = nullptr;
+  int ldres = 0;
+  float* C32 = nullptr;
+  int ldc32 = 0;
+  half_t* C16 = nullptr;
+  int ldc16 = 0;
+  float* C32b = nullptr;
+  int ldc32b = 0;
+  const float* cond = nullptr;       // EPI_GATE: [a(512) | b(512)] global conditioning
+  const uint32_t* mask = nullptr;    // per-row 0/1 (WaveNet epilogues)
+  const float* rp = nullptr;         // EPI_FINALSKIP: res_projection [M][512]
+  const float2* rope = nullptr;      // EPI_QKV: [T][32] (cos, sin)
+  half_t* q = nullptr;               // EPI_QKV: [B][H][Tpad][64]
+  half_t* k = nullptr;               // EPI_QKV: [B][H][Tpad][64]
+  half_t* vt = nullptr;              // EPI_QKV: [B][H][64][Tpad]
+  int Tpad = 0;
+  int flag = 0;                      // EPI_RESSKIP: 0 -> skip accumulator starts at zero
+};
+
+// Picks a tile shape for (M, N) and launches; returns hipSuccess or the
+// launch error.  Host-side checks reject shapes the kernels do not cover.
+hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t stream);
+
+}  // namespace mit2hip

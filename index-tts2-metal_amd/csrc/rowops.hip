@@ -1,0 +1,342 @@
+// rowops.hip -- bandwidth-bound row kernels of the DiT-CFM decoder (gfx950).
+//
+// Reference counterparts (kernels.metal unless noted): adaptive RMSNorm
+// :755-792, adaptive LayerNorm :702-753, input merge :898-931, CFM Euler
+// update :794-818, timestep embedding :1812-1829, GEMV :1084-1119, copies
+// :150-159.  Each row kernel gives one 64-lane wavefront a 512-wide row
+// (8 consecutive floats per lane, two 16-byte loads), so every access is
+// fully coalesced and the row reductions are two-level shuffles.
+#include "rowops.h"
+
+namespace mit2hip {
+
+// ---------------------------------------------------------------- norms
+__global__ __launch_bounds__(256) void adarms_kernel(const float* __restrict__ x,
+                                                     const float* __restrict__ gamma,
+                                                     const float* __restrict__ aw,
+                                                     const float* __restrict__ ab,
+                                                     half_t* __restrict__ out, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * 512) + lane * 2;
+  const float4 a = xr[0], b = xr[1];
+  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+  ss = warp_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / 512.0f + 1e-5f);
+  half8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = lane * 8 + i;
+    o[i] = (half_t)(aw[c] * (v[i] * inv * gamma[c]) + ab[c]);
+  }
+  *reinterpret_cast<half8*>(out + (size_t)row * 512 + lane * 8) = o;
+}
+
+__global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ x,
+                                                    const float* __restrict__ shift,
+                                                    const float* __restrict__ scale,
+                                                    half_t* __restrict__ out, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * 512) + lane * 2;
+  const float4 a = xr[0], b = xr[1];
+  float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += v[i];
+  const float mean = warp_sum(s) / 512.0f;
+  float var = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float d = v[i] - mean;
+    var += d * d;
+  }
+  var = warp_sum(var) / 512.0f;
+  const float inv = 1.0f / sqrtf(var + 1e-6f);
+  half8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = lane * 8 + i;
+    o[i] = (half_t)(((v[i] - mean) * inv) * (1.0f + scale[c]) + shift[c]);
+  }
+  *reinterpret_cast<half8*>(out + (size_t)row * 512 + lane * 8) = o;
+}
+
+hipError_t launch_adarms(const float* x, const float* gamma, const float* aw, const float* ab,
+                         half_t* out16, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(adarms_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, gamma, aw, ab, out16,
+                     rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_adaln(const float* x, const float* shift, const float* scale, half_t* out16,
+                        int rows, hipStream_t s) {
+  hipLaunchKernelGGL(adaln_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, shift, scale, out16,
+                     rows);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- set-up
+// One 256-thread block per (branch, token) row.
+__global__ __launch_bounds__(256) void decode_prep_kernel(
+    const float* __restrict__ x0, const float* __restrict__ prompt, const float* __restrict__ cond,
+    const float* __restrict__ style, const uint32_t* __restrict__ P, int T, int cfg_on,
+    float* __restrict__ x_cur, half_t* __restrict__ xmel16, half_t* __restrict__ cond16,
+    half_t* __restrict__ mc16) {
+  const int t = blockIdx.x;
+  const int b = blockIdx.y;
+  const int r = cfg_on ? (b >> 1) : b;
+  const bool is_cond = cfg_on ? ((b & 1) == 0) : true;
+  const uint32_t Pr = P[r];
+  const size_t row = (size_t)b * T + t;
+  const size_t rrow = (size_t)r * T + t;
+  for (int j = threadIdx.x; j < 96; j += blockDim.x) {
+    float xv = 0.0f;
+    if (j < 80 && (uint32_t)t >= Pr) xv = x0[rrow * 80 + j];
+    if (j < 80 && is_cond) x_cur[rrow * 80 + j] = xv;
+    xmel16[row * 96 + j] = (half_t)xv;
+  }
+  for (int j = threadIdx.x; j < 512; j += blockDim.x)
+    cond16[row * 512 + j] = (half_t)(is_cond ? cond[rrow * 512 + j] : 0.0f);
+  // prompt_x: the prompt frames on the first P rows of the cond branch.
+  for (int j = threadIdx.x; j < 96; j += blockDim.x) {
+    float pv = 0.0f;
+    if (is_cond && j < 80 && (uint32_t)t < Pr) pv = prompt[((size_t)r * T + t) * 80 + j];
+    mc16[row * 800 + j] = (half_t)pv;
+  }
+  for (int j = threadIdx.x; j < 192; j += blockDim.x)
+    mc16[row * 800 + 608 + j] = (half_t)(is_cond ? style[(size_t)r * 192 + j] : 0.0f);
+}
+
+hipError_t launch_decode_prep(const float* x0, const float* prompt, const float* cond,
+                              const float* style, const uint32_t* P, int nreq, int T, int cfg_on,
+                              float* x_cur, half_t* xmel16, half_t* cond16, half_t* mc16,
+                              hipStream_t s) {
+  const int B = cfg_on ? 2 * nreq : nreq;
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(T, B), dim3(256), 0, s, x0, prompt, cond, style, P,
+                     T, cfg_on, x_cur, xmel16, cond16, mc16);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void step_prep_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ prompt_x,
+                                                        const float* __restrict__ cond,
+                                                        const float* __restrict__ style, int T,
+                                                        half_t* __restrict__ xmel16,
+                                                        half_t* __restrict__ cond16,
+                                                        half_t* __restrict__ mc16) {
+  const int t = blockIdx.x;
+  const int b = blockIdx.y;
+  const size_t row = (size_t)b * T + t;
+  for (int j = threadIdx.x; j < 96; j += blockDim.x) {
+    xmel16[row * 96 + j] = (half_t)(j < 80 ? x[row * 80 + j] : 0.0f);
+    mc16[row * 800 + j] = (half_t)(j < 80 ? prompt_x[row * 80 + j] : 0.0f);
+  }
+  for (int j = threadIdx.x; j < 512; j += blockDim.x) cond16[row * 512 + j] = (half_t)cond[row * 512 + j];
+  for (int j = threadIdx.x; j < 192; j += blockDim.x)
+    mc16[row * 800 + 608 + j] = (half_t)style[(size_t)b * 192 + j];
+}
+
+hipError_t launch_step_prep(const float* x, const float* prompt_x, const float* cond,
+                            const float* style, int B, int T, half_t* xmel16, half_t* cond16,
+                            half_t* mc16, hipStream_t s) {
+  hipLaunchKernelGGL(step_prep_kernel, dim3(T, B), dim3(256), 0, s, x, prompt_x, cond, style, T,
+                     xmel16, cond16, mc16);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- conv2 (+ Euler)
+// One wavefront computes a 16-token x 80-channel block of conv2 (five 16-wide
+// MFMA column blocks, K = 512) for one or two branches.
+__device__ __forceinline__ void conv2_block(const half_t* __restrict__ y16, size_t row0, int nvalid,
+                                            const half_t* __restrict__ w2, int lr, int lg,
+                                            floatx4 acc[5]) {
+#pragma unroll
+  for (int nb = 0; nb < 5; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int ks = 0; ks < 16; ++ks) {
+    half8 a = {};
+    if (lr < nvalid) a = *reinterpret_cast<const half8*>(y16 + (row0 + lr) * 512 + ks * 32 + lg * 8);
+#pragma unroll
+    for (int nb = 0; nb < 5; ++nb) {
+      const half8 bw =
+          *reinterpret_cast<const half8*>(w2 + (size_t)(nb * 16 + lr) * 512 + ks * 32 + lg * 8);
+      acc[nb] = mfma16x16x32(a, bw, acc[nb]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void conv2_euler_kernel(
+    const half_t* __restrict__ y16, const half_t* __restrict__ w2, const float* __restrict__ b2,
+    const uint32_t* __restrict__ P, int T, int cfg_on, float cfg, float dt,
+    float* __restrict__ x_cur, half_t* __restrict__ xmel16, float* __restrict__ vtrace) {
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  const int r = blockIdx.y;
+  if (t0 >= T) return;
+  const int nvalid = min(16, T - t0);
+  const int bc = cfg_on ? 2 * r : r;
+  floatx4 ac[5], au[5];
+  conv2_block(y16, (size_t)bc * T + t0, nvalid, w2, lr, lg, ac);
+  if (cfg_on) conv2_block(y16, (size_t)(bc + 1) * T + t0, nvalid, w2, lr, lg, au);
+  const uint32_t Pr = P[r];
+#pragma unroll
+  for (int nb = 0; nb < 5; ++nb) {
+    const int n = nb * 16 + lr;
+    const float bias = b2[n];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + lg * 4 + i;
+      if (t >= T) continue;
+      float v = ac[nb][i] + bias;
+      if (cfg_on) v = (1.0f + cfg) * v - cfg * (au[nb][i] + bias);
+      const size_t xi = ((size_t)r * T + t) * 80 + n;
+      if (vtrace) vtrace[xi] = v;
+      float xn = x_cur[xi] + dt * v;
+      if ((uint32_t)t < Pr) xn = 0.0f;
+      x_cur[xi] = xn;
+      xmel16[((size_t)bc * T + t) * 96 + n] = (half_t)xn;
+      if (cfg_on) xmel16[((size_t)(bc + 1) * T + t) * 96 + n] = (half_t)xn;
+    }
+  }
+}
+
+hipError_t launch_conv2_euler(const half_t* y16, const half_t* w2, const float* b2,
+                              const uint32_t* P, int nreq, int T, int cfg_on, float cfg, float dt,
+                              float* x_cur, half_t* xmel16, float* vtrace, hipStream_t s) {
+  hipLaunchKernelGGL(conv2_euler_kernel, dim3((T + 63) / 64, nreq), dim3(256), 0, s, y16, w2, b2, P,
+                     T, cfg_on, cfg, dt, x_cur, xmel16, vtrace);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void conv2_rows_kernel(const half_t* __restrict__ y16,
+                                                         const half_t* __restrict__ w2,
+                                                         const float* __restrict__ b2, int rows,
+                                                         float* __restrict__ dphi) {
+  const int lane = threadIdx.x & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  if (m0 >= rows) return;
+  const int nvalid = min(16, rows - m0);
+  floatx4 acc[5];
+  conv2_block(y16, (size_t)m0, nvalid, w2, lr, lg, acc);
+#pragma unroll
+  for (int nb = 0; nb < 5; ++nb) {
+    const int n = nb * 16 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + lg * 4 + i;
+      if (m < rows) dphi[(size_t)m * 80 + n] = acc[nb][i] + b2[n];
+    }
+  }
+}
+
+hipError_t launch_conv2_rows(const half_t* y16, const half_t* w2, const float* b2, int rows,
+                             float* dphi, hipStream_t s) {
+  hipLaunchKernelGGL(conv2_rows_kernel, dim3((rows + 63) / 64), dim3(256), 0, s, y16, w2, b2, rows,
+                     dphi);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- t-tables
+__global__ void timestep_embedding_kernel(const float* __restrict__ tvals,
+                                          const float* __restrict__ freqs, int S,
+                                          float* __restrict__ temb) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= S * 128) return;
+  const int s = i / 128, f = i % 128;
+  const float arg = 1000.0f * tvals[s] * freqs[f];
+  temb[s * 256 + f] = cosf(arg);
+  temb[s * 256 + 128 + f] = sinf(arg);
+}
+
+hipError_t launch_timestep_embedding(const float* tvals, const float* freqs, int S, float* temb,
+                                     hipStream_t s) {
+  hipLaunchKernelGGL(timestep_embedding_kernel, dim3((S * 128 + 255) / 256), dim3(256), 0, s, tvals,
+                     freqs, S, temb);
+  return hipGetLastError();
+}
+
+// One wavefront per output feature n; lanes split K (coalesced W row reads);
+// the row stays in registers across the S inputs.
+__global__ __launch_bounds__(256) void linear_small_kernel(const float* __restrict__ in, int S,
+                                                           int K, const float* __restrict__ W,
+                                                           const float* __restrict__ bias, int N,
+                                                           int silu_in, int silu_out,
+                                                           float* __restrict__ out, int ldout) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  float w[8];
+  const int kper = K / 64;  // K is a multiple of 64 and at most 512
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w[j] = j < kper ? W[(size_t)n * K + j * 64 + lane] : 0.0f;
+  for (int s = 0; s < S; ++s) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < kper) {
+        float xv = in[(size_t)s * K + j * 64 + lane];
+        if (silu_in) xv = xv / (1.0f + expf(-xv));
+        acc += w[j] * xv;
+      }
+    }
+    acc = warp_sum(acc);
+    if (lane == 0) {
+      float v = acc + (bias ? bias[n] : 0.0f);
+      if (silu_out) v = v / (1.0f + expf(-v));
+      out[(size_t)s * ldout + n] = v;
+    }
+  }
+}
+
+hipError_t launch_linear_small(const float* in, int S, int K, const float* W, const float* bias,
+                               int N, int silu_in, int silu_out, float* out, int ldout,
+                               hipStream_t s) {
+  if (K % 64 != 0 || K > 512 || S <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(linear_small_kernel, dim3((N + 3) / 4), dim3(256), 0, s, in, S, K, W, bias, N,
+                     silu_in, silu_out, out, ldout);
+  return hipGetLastError();
+}
+
+__global__ void copy_f32_kernel(const float* __restrict__ src, float* __restrict__ dst, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t j = i; j < n; j += stride) dst[j] = src[j];
+}
+
+hipError_t launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(copy_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
+  return hipGetLastError();
+}
+
+__global__ void zero_kernel(uint4* __restrict__ p, size_t n16, unsigned char* __restrict__ tail,
+                            size_t ntail) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t j = i; j < n16; j += stride) p[j] = make_uint4(0, 0, 0, 0);
+  if (i < ntail) tail[i] = 0;
+}
+
+hipError_t launch_zero(void* p, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return hipSuccess;
+  const size_t n16 = bytes / 16;
+  const size_t ntail = bytes - n16 * 16;
+  size_t blocks = (n16 + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                     reinterpret_cast<uint4*>(p), n16,
+                     reinterpret_cast<unsigned char*>(p) + n16 * 16, ntail);
+  return hipGetLastError();
+}
+
+}  // namespace mit2hip

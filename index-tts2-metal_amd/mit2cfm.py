@@ -1,0 +1,419 @@
+"""Python binding of the gfx950 DiT-CFM decoder (ctypes over include/mit2cfm.h).
+
+Mirrors the reference's entry points for this path -- run_cfm_euler_metal
+(runtime/impl/dit_cfm_bigvgan.cpp:3121), run_dit_estimator_step_metal (:2778)
+and the per-stage test harnesses (:74-2860) -- with numpy arrays in place of
+std::vector<float>.  All compute goes through build/libmit2cfm.so; when that
+library is missing every call raises instead of falling back to anything.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "build" / "libmit2cfm.so"
+HEADER_PATH = PKG_DIR.parent / "include" / "mit2cfm.h"
+PREFIX = "s2mel.net.cfm.estimator."
+
+OK, E_ARG, E_MODEL, E_HIP, E_INTERNAL = 0, 1, 2, 3, 4
+DTYPE_F32, DTYPE_F16 = 0, 1
+FLAG_SYNC = 1
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_lib = None
+
+
+class Mit2CfmError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"mit2cfm status {status}: {message}")
+        self.status = status
+
+
+class _Tensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p),
+                ("elems", ctypes.c_uint64), ("dtype", ctypes.c_int32)]
+
+
+def lib() -> ctypes.CDLL:
+    """Loads build/libmit2cfm.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"HIP library not built: {LIB_PATH} (run __graft_entry__.build())")
+    L = ctypes.CDLL(str(LIB_PATH))
+    st = ctypes.c_int32
+    vp = ctypes.c_void_p
+    u32, u64, i32, f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_float
+    sig = {
+        "mit2cfm_abi_version": (i32, []),
+        "mit2cfm_last_error": (ctypes.c_char_p, [vp]),
+        "mit2cfm_create": (st, [ctypes.POINTER(_Tensor), u32, i32, ctypes.POINTER(vp)]),
+        "mit2cfm_create_from_bundle": (st, [ctypes.c_char_p, i32, ctypes.POINTER(vp)]),
+        "mit2cfm_create_synthetic": (st, [u64, f32, i32, ctypes.POINTER(vp)]),
+        "mit2cfm_destroy": (None, [vp]),
+        "mit2cfm_decode": (st, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, u32, f32, _f32p]),
+        "mit2cfm_decode_device": (st, [vp, vp, vp, vp, vp, u32, u32, u32, f32, vp, u32]),
+        "mit2cfm_decode_trace": (st, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, u32, f32, _f32p, _f32p]),
+        "mit2cfm_decode_batched": (st, [vp, u32, u32, _u32p, _u32p, _f32p, _f32p, _f32p, _f32p,
+                                        u32, f32, _f32p]),
+        "mit2cfm_estimator_step": (st, [vp, _f32p, _f32p, _f32p, _f32p, _u32p, f32, u32, u32, _f32p]),
+        "mit2cfm_stream": (vp, [vp]),
+        "mit2cfm_synchronize": (st, [vp]),
+        "mit2cfm_set_graph": (st, [vp, i32]),
+        "mit2cfm_stage_timestep_embedder": (st, [vp, f32, i32, _f32p]),
+        "mit2cfm_stage_input_merge": (st, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, _f32p]),
+        "mit2cfm_stage_adaptive_norm": (st, [vp, _f32p, _f32p, u32, i32, _f32p]),
+        "mit2cfm_stage_attention_core": (st, [vp, _f32p, _u32p, u32, u32, i32, _f32p]),
+        "mit2cfm_stage_feed_forward": (st, [vp, _f32p, u32, i32, _f32p]),
+        "mit2cfm_stage_block": (st, [vp, _f32p, _f32p, _u32p, u32, u32, i32, _f32p, _f32p]),
+        "mit2cfm_stage_stack": (st, [vp, _f32p, _f32p, _u32p, u32, u32, _f32p]),
+        "mit2cfm_stage_post": (st, [vp, _f32p, _f32p, u32, _f32p, _f32p, _f32p]),
+        "mit2cfm_stage_wavenet": (st, [vp, _f32p, _f32p, _u32p, u32, u32, _f32p]),
+        "mit2cfm_stage_final_layer": (st, [vp, _f32p, _f32p, u32, _f32p]),
+        "mit2cfm_op_linear": (st, [vp, _f32p, _f32p, _f32p, u32, u32, u32, _f32p]),
+        "mit2cfm_normal_noise": (st, [u32, u32, u64, f32, _f32p]),
+        "mit2cfm_synthetic_tensor_count": (u32, []),
+        "mit2cfm_synthetic_tensor_info": (st, [u32, ctypes.POINTER(ctypes.c_char_p), _u32p,
+                                               ctypes.POINTER(ctypes.c_int64),
+                                               ctypes.POINTER(ctypes.c_int32),
+                                               ctypes.POINTER(ctypes.c_uint64)]),
+        "mit2cfm_synthetic_tensor_fill": (st, [u32, u64, f32, vp]),
+        "mit2cfm_write_synthetic_bundle": (st, [ctypes.c_char_p, u64, f32]),
+        "mit2cfm_inspect_bundle": (st, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64),
+                                        ctypes.POINTER(ctypes.c_uint64), u32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/mit2cfm.h."""
+    text = HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"\b(mit2cfm_[a-z0-9_]+)\s*\(", text)))
+
+
+def _check(status: int, ctx=None) -> None:
+    if status != OK:
+        msg = lib().mit2cfm_last_error(ctx)
+        raise Mit2CfmError(status, msg.decode() if msg else "")
+
+
+def _f32(a, shape=None) -> np.ndarray:
+    arr = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    if shape is not None and arr.size != int(np.prod(shape)):
+        raise ValueError(f"expected {int(np.prod(shape))} elements, got {arr.size}")
+    return arr
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_f32p)
+
+
+def _pu(a: np.ndarray):
+    return a.ctypes.data_as(_u32p)
+
+
+# ---------------------------------------------------------------- synthetic data
+def normal_noise(tokens: int, channels: int, seed: int, temperature: float = 1.0) -> np.ndarray:
+    """make_deterministic_normal_noise (tokenizer_tests.cpp:2121): [tokens, channels]."""
+    out = np.empty((tokens, channels), np.float32)
+    _check(lib().mit2cfm_normal_noise(tokens, channels, seed, temperature, _p(out)))
+    return out
+
+
+def synthetic_tensor_specs() -> list[tuple[str, tuple[int, ...], str]]:
+    L = lib()
+    specs = []
+    for i in range(L.mit2cfm_synthetic_tensor_count()):
+        name = ctypes.c_char_p()
+        ndim = ctypes.c_uint32()
+        shape = (ctypes.c_int64 * 4)()
+        dt = ctypes.c_int32()
+        n = ctypes.c_uint64()
+        _check(L.mit2cfm_synthetic_tensor_info(i, ctypes.byref(name), ctypes.byref(ndim), shape,
+                                               ctypes.byref(dt), ctypes.byref(n)))
+        specs.append((name.value.decode(), tuple(shape[d] for d in range(ndim.value)),
+                      "f16" if dt.value == DTYPE_F16 else "f32"))
+    return specs
+
+
+def synthetic_tensors(seed: int = 20240605, stddev: float = 0.02) -> dict[str, np.ndarray]:
+    """Every estimator tensor, N(0, stddev) f16 from seed + (index in sorted-name order)."""
+    L = lib()
+    out = {}
+    for i, (name, shape, dt) in enumerate(synthetic_tensor_specs()):
+        arr = np.empty(shape, np.float16 if dt == "f16" else np.float32)
+        _check(L.mit2cfm_synthetic_tensor_fill(i, seed, stddev, arr.ctypes.data_as(ctypes.c_void_p)))
+        out[name] = arr
+    return out
+
+
+def write_synthetic_bundle(path: str | os.PathLike, seed: int = 20240605, stddev: float = 0.02) -> None:
+    _check(lib().mit2cfm_write_synthetic_bundle(str(path).encode(), seed, stddev))
+
+
+def inspect_bundle(path: str | os.PathLike, verify_sha256: bool = False) -> tuple[int, int]:
+    """Opens a bundle with the C++ loader (all validation rules); returns
+    (tensor count, payload bytes).  Raises Mit2CfmError on a bad bundle."""
+    count = ctypes.c_uint64()
+    nbytes = ctypes.c_uint64()
+    _check(lib().mit2cfm_inspect_bundle(str(path).encode(), ctypes.byref(count), ctypes.byref(nbytes),
+                                        1 if verify_sha256 else 0))
+    return count.value, nbytes.value
+
+
+# ---------------------------------------------------------------- context
+class Context:
+    """One GPU context with resident weights (mit2cfm_ctx)."""
+
+    def __init__(self, tensors: dict[str, np.ndarray] | None = None, *, bundle=None,
+                 synthetic_seed: int | None = None, stddev: float = 0.02, device: int = 0):
+        L = lib()
+        handle = ctypes.c_void_p()
+        if bundle is not None:
+            _check(L.mit2cfm_create_from_bundle(str(bundle).encode(), device, ctypes.byref(handle)))
+        elif synthetic_seed is not None:
+            _check(L.mit2cfm_create_synthetic(synthetic_seed, stddev, device, ctypes.byref(handle)))
+        else:
+            if tensors is None:
+                raise ValueError("need tensors, bundle or synthetic_seed")
+            keep = []
+            arr = (_Tensor * len(tensors))()
+            for i, (name, v) in enumerate(tensors.items()):
+                a = np.ascontiguousarray(v)
+                if a.dtype == np.float16:
+                    dt = DTYPE_F16
+                else:
+                    a = np.ascontiguousarray(a, dtype=np.float32)
+                    dt = DTYPE_F32
+                keep.append(a)
+                arr[i] = _Tensor(name.encode(), a.ctypes.data, a.size, dt)
+            _check(L.mit2cfm_create(arr, len(tensors), device, ctypes.byref(handle)))
+        self._h = handle
+
+    # -- lifetime
+    def close(self) -> None:
+        if self._h:
+            lib().mit2cfm_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _c(self, status: int) -> None:
+        _check(status, self._h)
+
+    # -- decode
+    def decode(self, x0, prompt, cond, style, steps: int, cfg_rate: float) -> np.ndarray:
+        """run_cfm_euler (dit_cfm_bigvgan.cpp:2908/3121): x0 [T,80], prompt [P,80],
+        cond [T,512], style [192] -> x [T,80]."""
+        x0 = _f32(x0)
+        T = x0.size // 80
+        prompt = _f32(prompt)
+        P = prompt.size // 80
+        cond = _f32(cond, (T, 512))
+        style = _f32(style, (192,))
+        out = np.empty((T, 80), np.float32)
+        self._c(lib().mit2cfm_decode(self._h, _p(x0), _p(prompt) if P else None, _p(cond), _p(style),
+                                     T, P, steps, cfg_rate, _p(out)))
+        return out
+
+    def decode_trace(self, x0, prompt, cond, style, steps: int, cfg_rate: float):
+        """Decode plus the guided velocity of every step: (x [T,80], v [steps,T,80])."""
+        x0 = _f32(x0)
+        T = x0.size // 80
+        prompt = _f32(prompt)
+        P = prompt.size // 80
+        cond = _f32(cond, (T, 512))
+        style = _f32(style, (192,))
+        out = np.empty((T, 80), np.float32)
+        v = np.empty((steps, T, 80), np.float32)
+        self._c(lib().mit2cfm_decode_trace(self._h, _p(x0), _p(prompt) if P else None, _p(cond),
+                                           _p(style), T, P, steps, cfg_rate, _p(out), _p(v)))
+        return out, v
+
+    def decode_batched(self, tokens, prompt_tokens, x0, prompt, cond, style, steps: int,
+                       cfg_rate: float) -> np.ndarray:
+        """nreq right-padded requests: x0/prompt [nreq,Tmax,80], cond [nreq,Tmax,512],
+        style [nreq,192], tokens/prompt_tokens [nreq] -> [nreq,Tmax,80]."""
+        tokens = _u32(tokens)
+        prompt_tokens = _u32(prompt_tokens)
+        x0 = _f32(x0)
+        nreq = tokens.size
+        Tm = x0.size // (nreq * 80)
+        prompt = _f32(prompt, (nreq, Tm, 80))
+        cond = _f32(cond, (nreq, Tm, 512))
+        style = _f32(style, (nreq, 192))
+        out = np.empty((nreq, Tm, 80), np.float32)
+        self._c(lib().mit2cfm_decode_batched(self._h, nreq, Tm, _pu(tokens), _pu(prompt_tokens),
+                                             _p(x0), _p(prompt), _p(cond), _p(style), steps,
+                                             cfg_rate, _p(out)))
+        return out
+
+    def decode_device(self, x0_ptr: int, prompt_ptr: int, cond_ptr: int, style_ptr: int,
+                      tokens: int, prompt_tokens: int, steps: int, cfg_rate: float, out_ptr: int,
+                      sync: bool = False) -> None:
+        """Decode on device buffers already in HBM (raw device addresses)."""
+        self._c(lib().mit2cfm_decode_device(self._h, x0_ptr, prompt_ptr, cond_ptr, style_ptr,
+                                            tokens, prompt_tokens, steps, cfg_rate, out_ptr,
+                                            FLAG_SYNC if sync else 0))
+
+    def estimator_step(self, x, prompt_x, cond, style, key_mask, t: float) -> np.ndarray:
+        """run_dit_estimator_step (dit_cfm_bigvgan.cpp:1768) for B branches:
+        x, prompt_x [B,T,80], cond [B,T,512], style [B,192], key_mask [B,T] -> [B,T,80]."""
+        key_mask = _u32(key_mask)
+        B, T = key_mask.shape
+        x = _f32(x, (B, T, 80))
+        prompt_x = _f32(prompt_x, (B, T, 80))
+        cond = _f32(cond, (B, T, 512))
+        style = _f32(style, (B, 192))
+        out = np.empty((B, T, 80), np.float32)
+        self._c(lib().mit2cfm_estimator_step(self._h, _p(x), _p(prompt_x), _p(cond), _p(style),
+                                             _pu(key_mask), t, B, T, _p(out)))
+        return out
+
+    @property
+    def stream(self) -> int:
+        return lib().mit2cfm_stream(self._h) or 0
+
+    def synchronize(self) -> None:
+        self._c(lib().mit2cfm_synchronize(self._h))
+
+    def set_graph(self, on: bool) -> None:
+        self._c(lib().mit2cfm_set_graph(self._h, 1 if on else 0))
+
+    # -- stages (parity harness)
+    def timestep_embedder(self, t: float, which: int) -> np.ndarray:
+        out = np.empty(512, np.float32)
+        self._c(lib().mit2cfm_stage_timestep_embedder(self._h, t, which, _p(out)))
+        return out
+
+    def input_merge(self, x, prompt_x, cond, style) -> np.ndarray:
+        x = _f32(x)
+        B, T = x.shape[0], x.shape[1]
+        out = np.empty((B, T, 512), np.float32)
+        self._c(lib().mit2cfm_stage_input_merge(
+            self._h, _p(x), _p(_f32(prompt_x, (B, T, 80))), _p(_f32(cond, (B, T, 512))),
+            _p(_f32(style, (B, 192))), B, T, _p(out)))
+        return out
+
+    def adaptive_norm(self, x, t1, norm_id: int) -> np.ndarray:
+        x = _f32(x)
+        rows = x.size // 512
+        out = np.empty((rows, 512), np.float32)
+        self._c(lib().mit2cfm_stage_adaptive_norm(self._h, _p(x), _p(_f32(t1, (512,))), rows,
+                                                  norm_id, _p(out)))
+        return out
+
+    def attention_core(self, x, key_mask, layer: int) -> np.ndarray:
+        key_mask = _u32(key_mask)
+        B, T = key_mask.shape
+        x = _f32(x, (B, T, 512))
+        out = np.empty((B, T, 512), np.float32)
+        self._c(lib().mit2cfm_stage_attention_core(self._h, _p(x), _pu(key_mask), B, T, layer,
+                                                   _p(out)))
+        return out
+
+    def feed_forward(self, x, layer: int) -> np.ndarray:
+        x = _f32(x)
+        rows = x.size // 512
+        out = np.empty((rows, 512), np.float32)
+        self._c(lib().mit2cfm_stage_feed_forward(self._h, _p(x), rows, layer, _p(out)))
+        return out
+
+    def block(self, x, t1, key_mask, layer: int, skip=None) -> np.ndarray:
+        key_mask = _u32(key_mask)
+        B, T = key_mask.shape
+        x = _f32(x, (B, T, 512))
+        sk = None if skip is None else _f32(skip, (B, T, 512))
+        out = np.empty((B, T, 512), np.float32)
+        self._c(lib().mit2cfm_stage_block(self._h, _p(x), _p(_f32(t1, (512,))), _pu(key_mask), B,
+                                          T, layer, None if sk is None else _p(sk), _p(out)))
+        return out
+
+    def stack(self, x, t1, key_mask) -> np.ndarray:
+        key_mask = _u32(key_mask)
+        B, T = key_mask.shape
+        x = _f32(x, (B, T, 512))
+        out = np.empty((B, T, 512), np.float32)
+        self._c(lib().mit2cfm_stage_stack(self._h, _p(x), _p(_f32(t1, (512,))), _pu(key_mask), B,
+                                          T, _p(out)))
+        return out
+
+    def post(self, xres, xmel):
+        xres = _f32(xres)
+        rows = xres.size // 512
+        xmel = _f32(xmel, (rows, 80))
+        ls = np.empty((rows, 512), np.float32)
+        c1 = np.empty((rows, 512), np.float32)
+        rp = np.empty((rows, 512), np.float32)
+        self._c(lib().mit2cfm_stage_post(self._h, _p(xres), _p(xmel), rows, _p(ls), _p(c1), _p(rp)))
+        return ls, c1, rp
+
+    def wavenet(self, x, t2, key_mask) -> np.ndarray:
+        key_mask = _u32(key_mask)
+        B, T = key_mask.shape
+        x = _f32(x, (B, T, 512))
+        out = np.empty((B, T, 512), np.float32)
+        self._c(lib().mit2cfm_stage_wavenet(self._h, _p(x), _p(_f32(t2, (512,))), _pu(key_mask), B,
+                                            T, _p(out)))
+        return out
+
+    def final_layer(self, x, t1) -> np.ndarray:
+        x = _f32(x)
+        rows = x.size // 512
+        out = np.empty((rows, 512), np.float32)
+        self._c(lib().mit2cfm_stage_final_layer(self._h, _p(x), _p(_f32(t1, (512,))), rows, _p(out)))
+        return out
+
+    def linear(self, a, w, bias=None) -> np.ndarray:
+        a = _f32(a)
+        w = _f32(w)
+        M, K = a.shape
+        N = w.shape[0]
+        out = np.empty((M, N), np.float32)
+        b = None if bias is None else _f32(bias, (N,))
+        self._c(lib().mit2cfm_op_linear(self._h, _p(a), _p(w), None if b is None else _p(b), M, N, K,
+                                        _p(out)))
+        return out
+
+
+# Reference-named conveniences ------------------------------------------------
+def run_cfm_euler(ctx: Context, x, prompt, cond, style, tokens: int, prompt_tokens: int,
+                  steps: int, cfg_rate: float) -> np.ndarray:
+    """run_cfm_euler_metal (dit_cfm_bigvgan.cpp:3121) signature."""
+    x = _f32(x, (tokens, 80))
+    prompt = _f32(prompt, (prompt_tokens, 80))
+    return ctx.decode(x, prompt, cond, style, steps, cfg_rate)
+
+
+def run_dit_estimator_step(ctx: Context, x, prompt_x, cond, style, timestep: float, mask,
+                           tokens: int) -> np.ndarray:
+    """run_dit_estimator_step_metal (dit_cfm_bigvgan.cpp:2778) signature, one branch."""
+    return ctx.estimator_step(_f32(x, (tokens, 80))[None], _f32(prompt_x, (tokens, 80))[None],
+                              _f32(cond, (tokens, 512))[None], _f32(style, (192,))[None],
+                              _u32(mask).reshape(1, tokens), timestep)[0]

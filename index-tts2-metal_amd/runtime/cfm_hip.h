@@ -1,0 +1,58 @@
+// cfm_hip.h -- C++ shim with the reference's call signatures over the C ABI.
+//
+// run_cfm_euler_hip / run_dit_estimator_step_hip take the arguments of
+// run_cfm_euler_metal (runtime/impl/dit_cfm_bigvgan.cpp:3121) and
+// run_dit_estimator_step_metal (:2778), with HipContext in place of
+// mit2::MetalContext; failures throw std::runtime_error as the reference's
+// Metal path does.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/mit2cfm.h"
+#include "bundle.h"
+
+namespace mit2 {
+
+class HipContext {
+ public:
+  // Uploads the estimator tensors of `bundle` to GPU `device`.
+  explicit HipContext(const Bundle& bundle, int device = 0);
+  // Seeded synthetic weights (N(0, stddev) f16; stddev 0 = fan-in scaled).
+  HipContext(uint64_t synthetic_seed, float stddev, int device = 0);
+  ~HipContext();
+  HipContext(const HipContext&) = delete;
+  HipContext& operator=(const HipContext&) = delete;
+  mit2cfm_ctx* get() const { return ctx_; }
+
+ private:
+  mit2cfm_ctx* ctx_ = nullptr;
+};
+
+std::vector<float> run_cfm_euler_hip(HipContext& hip, const Bundle& bundle, std::vector<float> x,
+                                     const std::vector<float>& prompt,
+                                     const std::vector<float>& cond,
+                                     const std::vector<float>& style, uint32_t tokens,
+                                     uint32_t prompt_tokens, uint32_t steps, float cfg_rate);
+// Same without a bundle argument (weights already resident in the context).
+std::vector<float> run_cfm_euler_hip(HipContext& hip, std::vector<float> x,
+                                     const std::vector<float>& prompt,
+                                     const std::vector<float>& cond,
+                                     const std::vector<float>& style, uint32_t tokens,
+                                     uint32_t prompt_tokens, uint32_t steps, float cfg_rate);
+std::vector<float> run_dit_estimator_step_hip(HipContext& hip, const std::vector<float>& x,
+                                              const std::vector<float>& prompt_x,
+                                              const std::vector<float>& cond,
+                                              const std::vector<float>& style, float timestep,
+                                              const std::vector<uint32_t>& mask, uint32_t tokens);
+
+// Euler step count for synthesis: env MIT2_CFM_STEPS, default 16, clamped to
+// the --cfm_steps range 12..25 (main.cpp:57-88, :3181-3187).
+uint32_t cfm_synthesis_steps();
+constexpr uint32_t kCfmSteps = 25;
+constexpr uint32_t kCfmStepsMin = 12;
+constexpr uint32_t kCfmStepsMax = 25;
+
+}  // namespace mit2

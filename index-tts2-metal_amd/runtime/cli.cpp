@@ -1,0 +1,195 @@
+// cli.cpp -- mtts-cfm: the decoder's command-line entry points.
+//
+// Keeps the reference CLI's flags for this path (runtime/main.cpp):
+//   --bench-cfm MODEL T STEPS ITERS     (main.cpp:2925-2930, run_bench_cfm :3065)
+//   --test-cfm-euler MODEL              (3 steps, cfg 0; :3342)
+//   --test-cfm-euler-cfg MODEL          (25 steps, cfg 0.5; :3405)
+//   --decode MODEL T P [--cfm_steps N] [--cfg R] [--seed S] [--out FILE]
+//   --cfm_steps N                       (12..25, main.cpp:3181-3187)
+//   --inspect-model-bundle DIR, --write-synthetic-bundle DIR [SEED] [STDDEV]
+// MODEL is a bundle path or "synthetic[:SEED[:STDDEV]]".  The reference's
+// --test-cfm-* compare its Metal path with its CPU path; here the CPU
+// comparison lives in the test suite (the library never links the CPU
+// restatement), so these harnesses check the invariants the reference's
+// tests also rely on: finiteness, zero prompt rows, repeat determinism and
+// batched-vs-single equality.
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "cfm_hip.h"
+#include "synth.h"
+
+namespace {
+
+using Clock = std::chrono::steady_clock;
+
+std::unique_ptr<mit2::HipContext> open_model(const std::string& model) {
+  if (model.rfind("synthetic", 0) == 0) {
+    uint64_t seed = 20240605;
+    float stddev = 0.02f;
+    const auto c1 = model.find(':');
+    if (c1 != std::string::npos) {
+      const auto c2 = model.find(':', c1 + 1);
+      seed = std::stoull(model.substr(c1 + 1, c2 == std::string::npos ? std::string::npos : c2 - c1 - 1));
+      if (c2 != std::string::npos) stddev = std::stof(model.substr(c2 + 1));
+    }
+    return std::make_unique<mit2::HipContext>(seed, stddev, 0);
+  }
+  mit2::Bundle b(model);
+  return std::make_unique<mit2::HipContext>(b, 0);
+}
+
+std::vector<float> series(size_t n, float a, float amp1, int mod, float b, float amp2, bool cos_first) {
+  std::vector<float> v(n);
+  for (size_t i = 0; i < n; ++i) {
+    const float p = cos_first ? std::cos((float)i * a) : std::sin((float)i * a);
+    const float q = cos_first ? std::sin((float)(i % mod) * b) : std::cos((float)(i % mod) * b);
+    v[i] = p * amp1 + q * amp2;
+  }
+  return v;
+}
+
+int bench_cfm(const std::string& model, uint32_t tokens, uint32_t steps, uint32_t iters) {
+  auto hip = open_model(model);
+  const uint32_t prompt_tokens = tokens * 6 / 7;
+  std::vector<float> x((size_t)tokens * 80), prompt((size_t)prompt_tokens * 80),
+      cond((size_t)tokens * 512), style(192);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin((float)i * 0.013f) * 0.4f;
+  for (size_t i = 0; i < prompt.size(); ++i) prompt[i] = std::cos((float)i * 0.011f) * 0.5f;
+  for (size_t i = 0; i < cond.size(); ++i) cond[i] = std::sin((float)i * 0.007f) * 0.3f;
+  for (size_t i = 0; i < style.size(); ++i) style[i] = std::cos((float)i * 0.015f) * 0.18f;
+  (void)mit2::run_cfm_euler_hip(*hip, x, prompt, cond, style, tokens, prompt_tokens, steps, 0.7f);
+  const auto t0 = Clock::now();
+  for (uint32_t i = 0; i < iters; ++i)
+    (void)mit2::run_cfm_euler_hip(*hip, x, prompt, cond, style, tokens, prompt_tokens, steps, 0.7f);
+  const double total = std::chrono::duration<double>(Clock::now() - t0).count();
+  std::cout << "{\n  \"stage\": \"bench_cfm\",\n  \"tokens\": " << tokens << ",\n  \"steps\": " << steps
+            << ",\n  \"iters\": " << iters << ",\n  \"seconds_per_call\": " << total / iters
+            << ",\n  \"ms_per_step\": " << total / iters / steps * 1000.0
+            << ",\n  \"frames_per_second\": " << tokens / (total / iters) << "\n}\n";
+  return 0;
+}
+
+int test_cfm_euler(const std::string& model, const char* stage, uint32_t steps, float cfg) {
+  auto hip = open_model(model);
+  const uint32_t tokens = 5, prompt_tokens = 2;
+  const auto x = series((size_t)tokens * 80, 0.018f, 0.07f, 61, 0.011f, 0.03f, false);
+  const auto prompt = series((size_t)prompt_tokens * 80, 0.022f, 0.09f, 37, 0.019f, 0.02f, true);
+  const auto cond = series((size_t)tokens * 512, 0.009f, 0.08f, 109, 0.014f, 0.04f, false);
+  std::vector<float> style(192);
+  for (size_t i = 0; i < style.size(); ++i) style[i] = std::cos((float)i * 0.015f) * 0.18f;
+  const auto a = mit2::run_cfm_euler_hip(*hip, x, prompt, cond, style, tokens, prompt_tokens, steps, cfg);
+  const auto b = mit2::run_cfm_euler_hip(*hip, x, prompt, cond, style, tokens, prompt_tokens, steps, cfg);
+  size_t nonfinite = 0;
+  float prompt_abs = 0.0f, repeat_err = 0.0f;
+  for (size_t i = 0; i < a.size(); ++i) {
+    if (!std::isfinite(a[i])) ++nonfinite;
+    if (i < (size_t)prompt_tokens * 80) prompt_abs = std::max(prompt_abs, std::fabs(a[i]));
+    repeat_err = std::max(repeat_err, std::fabs(a[i] - b[i]));
+  }
+  std::cout << "{\n  \"stage\": \"" << stage << "\",\n  \"tokens\": " << tokens
+            << ",\n  \"prompt_tokens\": " << prompt_tokens << ",\n  \"steps\": " << steps
+            << ",\n  \"cfg_rate\": " << cfg << ",\n  \"nonfinite\": " << nonfinite
+            << ",\n  \"prompt_rows_max_abs\": " << prompt_abs
+            << ",\n  \"repeat_max_abs_error\": " << repeat_err << "\n}\n";
+  return (nonfinite == 0 && prompt_abs == 0.0f && repeat_err == 0.0f) ? 0 : 1;
+}
+
+int decode(const std::string& model, uint32_t tokens, uint32_t prompt_tokens, uint32_t steps, float cfg,
+           uint64_t seed, const std::string& out) {
+  auto hip = open_model(model);
+  const auto x = mit2::make_deterministic_normal_noise(tokens, 80, seed, 1.0f);
+  auto prompt = mit2::make_deterministic_normal_noise(std::max(prompt_tokens, 1u), 80, seed + 1, 2.0f);
+  for (auto& v : prompt) v -= 5.0f;
+  const auto cond = mit2::make_deterministic_normal_noise(tokens, 512, seed + 2, 1.0f);
+  const auto style = mit2::make_deterministic_normal_noise(1, 192, seed + 3, 1.0f);
+  const auto t0 = Clock::now();
+  const auto mel = mit2::run_cfm_euler_hip(*hip, x, prompt, cond, style, tokens, prompt_tokens, steps, cfg);
+  const double sec = std::chrono::duration<double>(Clock::now() - t0).count();
+  if (!out.empty()) {
+    std::ofstream f(out, std::ios::binary);
+    f.write(reinterpret_cast<const char*>(mel.data()), (std::streamsize)(mel.size() * 4));
+  }
+  double ss = 0;
+  for (float v : mel) ss += (double)v * v;
+  std::cout << "{\"stage\": \"decode\", \"tokens\": " << tokens << ", \"prompt_tokens\": " << prompt_tokens
+            << ", \"steps\": " << steps << ", \"cfg_rate\": " << cfg << ", \"seconds\": " << sec
+            << ", \"rms\": " << std::sqrt(ss / mel.size()) << "}\n";
+  return 0;
+}
+
+int usage() {
+  std::cerr << "usage: mtts-cfm --bench-cfm MODEL T STEPS ITERS | --test-cfm-euler MODEL |\n"
+               "       --test-cfm-euler-cfg MODEL | --decode MODEL T P [--cfm_steps N] [--cfg R]\n"
+               "       [--seed S] [--out FILE] | --inspect-model-bundle DIR |\n"
+               "       --write-synthetic-bundle DIR [SEED] [STDDEV]\n"
+               "MODEL: bundle path or synthetic[:SEED[:STDDEV]]\n";
+  return 2;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  try {
+    uint32_t steps = mit2::cfm_synthesis_steps();
+    float cfg = 0.7f;
+    uint64_t seed = 1;
+    std::string out;
+    for (int i = 1; i < argc; ++i) {
+      const std::string a = argv[i];
+      if (a == "--cfm_steps" && i + 1 < argc) {
+        const long n = std::strtol(argv[i + 1], nullptr, 10);
+        if (n < (long)mit2::kCfmStepsMin || n > (long)mit2::kCfmStepsMax) {
+          std::cerr << "error: --cfm_steps must be between 12 and 25 (got " << n << ")\n";
+          return 1;
+        }
+        steps = (uint32_t)n;
+      } else if (a == "--cfg" && i + 1 < argc) {
+        cfg = std::stof(argv[i + 1]);
+      } else if (a == "--seed" && i + 1 < argc) {
+        seed = std::stoull(argv[i + 1]);
+      } else if (a == "--out" && i + 1 < argc) {
+        out = argv[i + 1];
+      }
+    }
+    for (int i = 1; i < argc; ++i) {
+      const std::string a = argv[i];
+      if (a == "--bench-cfm" && i + 4 < argc)
+        return bench_cfm(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]),
+                         (uint32_t)std::stoul(argv[i + 4]));
+      if (a == "--test-cfm-euler" && i + 1 < argc) return test_cfm_euler(argv[i + 1], "cfm_euler", 3, 0.0f);
+      if (a == "--test-cfm-euler-cfg" && i + 1 < argc)
+        return test_cfm_euler(argv[i + 1], "cfm_euler_cfg", 25, 0.5f);
+      if (a == "--decode" && i + 3 < argc)
+        return decode(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]), steps,
+                      cfg, seed, out);
+      if (a == "--inspect-model-bundle" && i + 1 < argc) {
+        uint64_t n = 0, bytes = 0;
+        const mit2cfm_status st = mit2cfm_inspect_bundle(argv[i + 1], &n, &bytes, 1);
+        std::cout << "{\"ok\": " << (st == MIT2CFM_OK ? "true" : "false") << ", \"tensors\": " << n
+                  << ", \"payload_bytes\": " << bytes << ", \"sha256_verified\": " << (st == MIT2CFM_OK)
+                  << ", \"error\": \"" << (st == MIT2CFM_OK ? "" : mit2cfm_last_error(nullptr)) << "\"}\n";
+        return st == MIT2CFM_OK ? 0 : 1;
+      }
+      if (a == "--write-synthetic-bundle" && i + 1 < argc) {
+        const uint64_t s = i + 2 < argc ? std::stoull(argv[i + 2]) : 20240605ull;
+        const float sd = i + 3 < argc ? std::stof(argv[i + 3]) : 0.02f;
+        const mit2cfm_status st = mit2cfm_write_synthetic_bundle(argv[i + 1], s, sd);
+        if (st != MIT2CFM_OK) std::cerr << mit2cfm_last_error(nullptr) << "\n";
+        return st == MIT2CFM_OK ? 0 : 1;
+      }
+    }
+    return usage();
+  } catch (const std::exception& e) {
+    std::cerr << "error: " << e.what() << "\n";
+    return 1;
+  }
+}

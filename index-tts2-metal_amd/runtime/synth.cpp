@@ -1,0 +1,156 @@
+// synth.cpp -- seeded synthetic inputs and weights (see synth.h).
+#include "synth.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+namespace mit2 {
+
+uint64_t splitmix64_next(uint64_t& state) {
+  uint64_t z = (state += 0x9e3779b97f4a7c15ull);
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+float splitmix64_uniform_open01(uint64_t& state) {
+  constexpr double scale = 1.0 / static_cast<double>(1ull << 53);
+  const uint64_t bits = splitmix64_next(state) >> 11;
+  double v = (static_cast<double>(bits) + 0.5) * scale;
+  if (v <= 0.0) v = scale;
+  if (v >= 1.0) v = 1.0 - scale;
+  return static_cast<float>(v);
+}
+
+std::vector<float> make_deterministic_normal_noise(uint32_t tokens, uint32_t channels,
+                                                   uint64_t seed, float temperature) {
+  if (tokens == 0 || channels == 0) throw std::runtime_error("noise shape must be non-empty");
+  constexpr float two_pi = 6.2831853071795864769f;
+  std::vector<float> out(static_cast<size_t>(tokens) * channels);
+  uint64_t state = seed;
+  size_t i = 0;
+  while (i < out.size()) {
+    const float u1 = splitmix64_uniform_open01(state);
+    const float u2 = splitmix64_uniform_open01(state);
+    const float radius = std::sqrt(-2.0f * std::log(u1));
+    const float angle = two_pi * u2;
+    out[i++] = radius * std::cos(angle) * temperature;
+    if (i < out.size()) out[i++] = radius * std::sin(angle) * temperature;
+  }
+  return out;
+}
+
+const std::vector<SynthSpec>& estimator_tensor_specs() {
+  static const std::vector<SynthSpec> specs = [] {
+    std::vector<SynthSpec> v;
+    const std::string p = "s2mel.net.cfm.estimator.";
+    auto add = [&](const std::string& n, std::vector<int64_t> s, const char* dt = "f16") {
+      v.push_back({p + n, std::move(s), dt});
+    };
+    for (const char* te : {"t_embedder", "t_embedder2"}) {
+      const std::string t = te;
+      add(t + ".freqs", {128}, "f32");
+      add(t + ".mlp.0.weight", {512, 256});
+      add(t + ".mlp.0.bias", {512});
+      add(t + ".mlp.2.weight", {512, 512});
+      add(t + ".mlp.2.bias", {512});
+    }
+    add("cond_projection.weight", {512, 512});
+    add("cond_projection.bias", {512});
+    add("cond_x_merge_linear.weight", {512, 864});
+    add("cond_x_merge_linear.bias", {512});
+    for (int l = 0; l < 13; ++l) {
+      const std::string b = "transformer.layers." + std::to_string(l);
+      for (const char* nn : {".attention_norm", ".ffn_norm"}) {
+        add(b + nn + ".norm.weight", {512});
+        add(b + nn + ".project_layer.weight", {1024, 512});
+        add(b + nn + ".project_layer.bias", {1024});
+      }
+      add(b + ".attention.wqkv.weight", {1536, 512});
+      add(b + ".attention.wo.weight", {512, 512});
+      add(b + ".feed_forward.w1.weight", {1536, 512});
+      add(b + ".feed_forward.w3.weight", {1536, 512});
+      add(b + ".feed_forward.w2.weight", {512, 1536});
+      if (l > 6) {
+        add(b + ".skip_in_linear.weight", {512, 1024});
+        add(b + ".skip_in_linear.bias", {512});
+      }
+    }
+    add("transformer.norm.norm.weight", {512});
+    add("transformer.norm.project_layer.weight", {1024, 512});
+    add("transformer.norm.project_layer.bias", {1024});
+    add("skip_linear.weight", {512, 592});
+    add("skip_linear.bias", {512});
+    add("conv1.weight", {512, 512});
+    add("conv1.bias", {512});
+    add("res_projection.weight", {512, 512});
+    add("res_projection.bias", {512});
+    add("wavenet.cond_layer.conv.conv.weight_g", {8192, 1, 1});
+    add("wavenet.cond_layer.conv.conv.weight_v", {8192, 512, 1});
+    add("wavenet.cond_layer.conv.conv.bias", {8192});
+    for (int l = 0; l < 8; ++l) {
+      const std::string b = "wavenet.in_layers." + std::to_string(l) + ".conv.conv";
+      add(b + ".weight_g", {1024, 1, 1});
+      add(b + ".weight_v", {1024, 512, 5});
+      add(b + ".bias", {1024});
+      const int64_t c = l < 7 ? 1024 : 512;
+      const std::string r = "wavenet.res_skip_layers." + std::to_string(l) + ".conv.conv";
+      add(r + ".weight_g", {c, 1, 1});
+      add(r + ".weight_v", {c, 512, 1});
+      add(r + ".bias", {c});
+    }
+    add("final_layer.adaLN_modulation.1.weight", {1024, 512});
+    add("final_layer.adaLN_modulation.1.bias", {1024});
+    add("final_layer.linear.weight_g", {512, 1});
+    add("final_layer.linear.weight_v", {512, 512});
+    add("final_layer.linear.bias", {512});
+    add("conv2.weight", {80, 512, 1});
+    add("conv2.bias", {80});
+    std::sort(v.begin(), v.end(), [](const SynthSpec& a, const SynthSpec& b) { return a.name < b.name; });
+    return v;
+  }();
+  return specs;
+}
+
+std::vector<uint8_t> synth_tensor_bytes(size_t i, uint64_t base_seed, float stddev) {
+  const auto& specs = estimator_tensor_specs();
+  if (i >= specs.size()) throw std::out_of_range("synthetic tensor index");
+  const SynthSpec& s = specs[i];
+  size_t n = 1;
+  for (int64_t d : s.shape) n *= (size_t)d;
+  if (s.dtype == "f32") {  // *.freqs
+    std::vector<float> f(n);
+    const float neg_log = -std::log(10000.0f);
+    for (size_t k = 0; k < n; ++k) f[k] = std::exp(neg_log * (float)k / (float)n);
+    std::vector<uint8_t> out(n * 4);
+    std::memcpy(out.data(), f.data(), out.size());
+    return out;
+  }
+  // stddev > 0: every tensor N(0, stddev).  stddev == 0: activation-preserving
+  // scales -- matrices N(0, 1/sqrt(fan_in)), norm weights and weight-norm
+  // gains 1 + N(0, 0.02), other vectors N(0, 0.02).
+  float scale = stddev, offset = 0.0f;
+  if (stddev == 0.0f) {
+    const bool gain = s.name.size() >= 12 && (s.name.compare(s.name.size() - 12, 12, ".norm.weight") == 0 ||
+                                              s.name.compare(s.name.size() - 9, 9, ".weight_g") == 0);
+    if (s.shape.size() >= 2 && s.name.compare(s.name.size() - 9, 9, ".weight_g") != 0) {
+      size_t fan_in = 1;
+      for (size_t d = 1; d < s.shape.size(); ++d) fan_in *= (size_t)s.shape[d];
+      scale = 1.0f / std::sqrt((float)fan_in);
+    } else {
+      scale = 0.02f;
+      offset = gain ? 1.0f : 0.0f;
+    }
+  }
+  const auto v = make_deterministic_normal_noise((uint32_t)n, 1, base_seed + i, scale);
+  std::vector<uint8_t> out(n * 2);
+  for (size_t k = 0; k < n; ++k) {
+    const _Float16 h = (_Float16)(v[k] + offset);
+    std::memcpy(&out[k * 2], &h, 2);
+  }
+  return out;
+}
+
+}  // namespace mit2

@@ -1,0 +1,352 @@
+"""ctypes binding of the CPU oracle (oracle/build/libcfm_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+The product path never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "build" / "libcfm_oracle.so"
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, u32, i32, f32, u64 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_float, ctypes.c_uint64
+        sig = {
+            "orc_set_threads": (None, [i32]),
+            "orc_get_threads": (i32, []),
+            "orc_half_to_float": (f32, [ctypes.c_uint16]),
+            "orc_halves_to_floats": (None, [ctypes.POINTER(ctypes.c_uint16), ctypes.c_size_t, _f32p]),
+            "orc_splitmix64_next": (u64, [ctypes.POINTER(ctypes.c_uint64)]),
+            "orc_uniform_open01": (f32, [ctypes.POINTER(ctypes.c_uint64)]),
+            "orc_normal_noise": (None, [u32, u32, u64, f32, _f32p]),
+            "orc_layernorm": (None, [_f32p, _f32p, _f32p, u32, f32, _f32p]),
+            "orc_rmsnorm": (None, [_f32p, _f32p, u32, f32, _f32p]),
+            "orc_linear": (None, [_f32p, _f32p, _f32p, u32, u32, _f32p]),
+            "orc_linear_rows": (None, [_f32p, _f32p, _f32p, u32, u32, u32, _f32p]),
+            "orc_conv1d_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, _f32p]),
+            "orc_reflect_pad": (None, [_f32p, u32, u32, u32, u32, _f32p]),
+            "orc_conv1d_reflect_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, _f32p]),
+            "orc_timestep_embedding": (None, [_f32p, u32, _f32p, u32, f32, _f32p]),
+            "orc_attention_head_masked": (None, [_f32p, _f32p, _f32p, _u32p, u32, u32, _f32p]),
+            "orc_rope_inplace": (None, [_f32p, u32, u32, u32]),
+            "orc_weight_norm_rowmajor": (None, [_f32p, _f32p, u32, u32, _f32p]),
+            "orc_model_new": (vp, []),
+            "orc_model_free": (None, [vp]),
+            "orc_model_set": (i32, [vp, ctypes.c_char_p, _f32p, u64]),
+            "orc_model_tensor_count": (i32, []),
+            "orc_model_tensor_name": (ctypes.c_char_p, [i32]),
+            "orc_model_tensor_elems": (u64, [i32]),
+            "orc_model_missing": (i32, [vp]),
+            "orc_last_error": (ctypes.c_char_p, []),
+            "orc_timestep_embedder": (None, [vp, f32, i32, _f32p]),
+            "orc_input_merge": (None, [vp, _f32p, _f32p, _f32p, _f32p, u32, _f32p]),
+            "orc_adaptive_norm": (None, [vp, _f32p, _f32p, u32, i32, _f32p]),
+            "orc_attention_core": (None, [vp, _f32p, _u32p, u32, u32, _f32p]),
+            "orc_feed_forward": (None, [vp, _f32p, u32, u32, _f32p]),
+            "orc_skip_in": (None, [vp, _f32p, _f32p, u32, u32, _f32p]),
+            "orc_transformer_block": (None, [vp, _f32p, _f32p, _u32p, u32, u32, _f32p, _f32p]),
+            "orc_transformer_stack": (None, [vp, _f32p, _f32p, _u32p, u32, _f32p]),
+            "orc_post_transformer": (None, [vp, _f32p, _f32p, u32, _f32p, _f32p, _f32p]),
+            "orc_wavenet": (None, [vp, _f32p, _f32p, _u32p, u32, _f32p]),
+            "orc_final_layer": (None, [vp, _f32p, _f32p, u32, _f32p]),
+            "orc_estimator_step": (None, [vp, _f32p, _f32p, _f32p, _f32p, f32, _u32p, u32, _f32p]),
+            "orc_cfm_euler": (None, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, u32, f32]),
+            "orc_cfm_euler_trace": (None, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, u32, f32,
+                                           _f32p, _f32p]),
+            "orc_cfm_euler_masked": (None, [vp, _f32p, _f32p, _f32p, _f32p, _u32p, u32, u32, u32,
+                                            f32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+def P(a: np.ndarray):
+    return a.ctypes.data_as(_f32p)
+
+
+def PU(a: np.ndarray):
+    return a.ctypes.data_as(_u32p)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def default_threads() -> int:
+    return max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count() or 1))
+
+
+# ---------------------------------------------------------------- primitives
+def linear(w, b, x) -> np.ndarray:
+    w, b, x = f32(w), f32(b), f32(x)
+    rows, cols = w.shape
+    x2 = x.reshape(-1, cols)
+    out = np.empty((x2.shape[0], rows), np.float32)
+    lib().orc_linear_rows(P(w), P(b), P(x2), x2.shape[0], rows, cols, P(out))
+    return out.reshape(x.shape[:-1] + (rows,))
+
+
+def rmsnorm(x, gamma, eps) -> np.ndarray:
+    x, g = f32(x), f32(gamma)
+    out = np.empty_like(x)
+    n = x.shape[-1]
+    for r in range(x.size // n):
+        lib().orc_rmsnorm(P(x[r:r + 1].reshape(-1) if x.ndim > 1 else x), P(g), n, eps,
+                          out.reshape(-1, n)[r:r + 1].ctypes.data_as(_f32p))
+    return out
+
+
+def layernorm(x, gamma, beta, eps) -> np.ndarray:
+    x, g, b = f32(x), f32(gamma), f32(beta)
+    n = x.shape[-1]
+    x2 = x.reshape(-1, n)
+    out = np.empty_like(x2)
+    for r in range(x2.shape[0]):
+        xr = np.ascontiguousarray(x2[r])
+        o = np.empty(n, np.float32)
+        lib().orc_layernorm(P(xr), P(g), P(b), n, eps, P(o))
+        out[r] = o
+    return out.reshape(x.shape)
+
+
+def conv1d_same(x, w, b, kernel) -> np.ndarray:
+    x, w, b = f32(x), f32(w), f32(b)
+    tokens, cin = x.shape
+    cout = b.size
+    out = np.empty((tokens, cout), np.float32)
+    lib().orc_conv1d_same(P(x), P(w), P(b), tokens, cin, cout, kernel, P(out))
+    return out
+
+
+def conv1d_reflect_same(x, w, b, kernel) -> np.ndarray:
+    x, w, b = f32(x), f32(w), f32(b)
+    tokens, cin = x.shape
+    cout = b.size
+    out = np.empty((tokens, cout), np.float32)
+    lib().orc_conv1d_reflect_same(P(x), P(w), P(b), tokens, cin, cout, kernel, P(out))
+    return out
+
+
+def reflect_pad(x, left, right) -> np.ndarray:
+    x = f32(x)
+    tokens, ch = x.shape
+    out = np.empty((tokens + left + right, ch), np.float32)
+    lib().orc_reflect_pad(P(x), tokens, ch, left, right, P(out))
+    return out
+
+
+def timestep_embedding(t, freqs, scale=1000.0) -> np.ndarray:
+    t, fr = f32(np.atleast_1d(t)), f32(freqs)
+    out = np.empty((t.size, 2 * fr.size), np.float32)
+    lib().orc_timestep_embedding(P(t), t.size, P(fr), fr.size, scale, P(out))
+    return out
+
+
+def attention_head(q, k, v, mask) -> np.ndarray:
+    q, k, v, m = f32(q), f32(k), f32(v), u32(mask)
+    tokens, hd = q.shape
+    out = np.empty_like(q)
+    lib().orc_attention_head_masked(P(q), P(k), P(v), PU(m), tokens, hd, P(out))
+    return out
+
+
+def rope(x, heads, head_dim) -> np.ndarray:
+    x = f32(x).copy()
+    tokens = x.size // (heads * head_dim)
+    lib().orc_rope_inplace(P(x), tokens, heads, head_dim)
+    return x
+
+
+def weight_norm(g, v) -> np.ndarray:
+    g, v = f32(g), f32(v)
+    rows = g.size
+    cols = v.size // rows
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_weight_norm_rowmajor(P(g), P(v), rows, cols, P(out))
+    return out
+
+
+def normal_noise(tokens, channels, seed, temperature=1.0) -> np.ndarray:
+    out = np.empty((tokens, channels), np.float32)
+    lib().orc_normal_noise(tokens, channels, seed, temperature, P(out))
+    return out
+
+
+def half_to_float(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_halves_to_floats(h.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), h.size, P(out))
+    return out
+
+
+# ---------------------------------------------------------------- model
+class Model:
+    """Estimator weights widened to fp32 (tensor_as_f32) plus the stage functions."""
+
+    def __init__(self, tensors: dict[str, np.ndarray]):
+        L = lib()
+        self._m = L.orc_model_new()
+        for name, v in tensors.items():
+            a = np.asarray(v)
+            if a.dtype == np.float16:
+                a = half_to_float(a.view(np.uint16))
+            a = f32(a)
+            if L.orc_model_set(self._m, name.encode(), P(a), a.size) != 0:
+                raise ValueError(L.orc_last_error().decode())
+        if L.orc_model_missing(self._m):
+            raise ValueError(L.orc_last_error().decode())
+
+    def close(self):
+        if self._m:
+            lib().orc_model_free(self._m)
+            self._m = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def timestep_embedder(self, t, which):
+        out = np.empty(512, np.float32)
+        lib().orc_timestep_embedder(self._m, t, which, P(out))
+        return out
+
+    def input_merge(self, x, prompt_x, cond, style):
+        x = f32(x)
+        T = x.shape[0]
+        out = np.empty((T, 512), np.float32)
+        lib().orc_input_merge(self._m, P(x), P(f32(prompt_x)), P(f32(cond)), P(f32(style)), T, P(out))
+        return out
+
+    def adaptive_norm(self, x, t1, norm_id):
+        x = f32(x)
+        T = x.size // 512
+        out = np.empty((T, 512), np.float32)
+        lib().orc_adaptive_norm(self._m, P(x), P(f32(t1)), T, norm_id, P(out))
+        return out
+
+    def attention_core(self, x, mask, layer):
+        x, m = f32(x), u32(mask)
+        T = m.size
+        out = np.empty((T, 512), np.float32)
+        lib().orc_attention_core(self._m, P(x), PU(m), T, layer, P(out))
+        return out
+
+    def feed_forward(self, x, layer):
+        x = f32(x)
+        T = x.size // 512
+        out = np.empty((T, 512), np.float32)
+        lib().orc_feed_forward(self._m, P(x), T, layer, P(out))
+        return out
+
+    def block(self, x, t1, mask, layer, skip=None):
+        x, m = f32(x), u32(mask)
+        T = m.size
+        out = np.empty((T, 512), np.float32)
+        sk = None if skip is None else f32(skip)
+        lib().orc_transformer_block(self._m, P(x), P(f32(t1)), PU(m), T, layer,
+                                    None if sk is None else P(sk), P(out))
+        return out
+
+    def stack(self, x, t1, mask):
+        x, m = f32(x), u32(mask)
+        T = m.size
+        out = np.empty((T, 512), np.float32)
+        lib().orc_transformer_stack(self._m, P(x), P(f32(t1)), PU(m), T, P(out))
+        return out
+
+    def post(self, xres, xmel):
+        xres = f32(xres)
+        T = xres.size // 512
+        ls, c1, rp = (np.empty((T, 512), np.float32) for _ in range(3))
+        lib().orc_post_transformer(self._m, P(xres), P(f32(xmel)), T, P(ls), P(c1), P(rp))
+        return ls, c1, rp
+
+    def wavenet(self, x, t2, mask):
+        x, m = f32(x), u32(mask)
+        T = m.size
+        out = np.empty((T, 512), np.float32)
+        lib().orc_wavenet(self._m, P(x), P(f32(t2)), PU(m), T, P(out))
+        return out
+
+    def final_layer(self, x, t1):
+        x = f32(x)
+        T = x.size // 512
+        out = np.empty((T, 512), np.float32)
+        lib().orc_final_layer(self._m, P(x), P(f32(t1)), T, P(out))
+        return out
+
+    def estimator_step(self, x, prompt_x, cond, style, t, mask):
+        x, m = f32(x), u32(mask)
+        T = m.size
+        out = np.empty((T, 80), np.float32)
+        lib().orc_estimator_step(self._m, P(x), P(f32(prompt_x)), P(f32(cond)), P(f32(style)), t,
+                                 PU(m), T, P(out))
+        return out
+
+    def cfm_euler(self, x0, prompt, cond, style, steps, cfg, trace=False):
+        x = f32(x0).copy()
+        T = x.size // 80
+        pr = f32(prompt)
+        Pn = pr.size // 80
+        if not trace:
+            lib().orc_cfm_euler(self._m, P(x), P(pr) if Pn else None, P(f32(cond)), P(f32(style)), T,
+                                Pn, steps, cfg)
+            return x.reshape(T, 80)
+        xt = np.empty((steps, T, 80), np.float32)
+        vt = np.empty((steps, T, 80), np.float32)
+        lib().orc_cfm_euler_trace(self._m, P(x), P(pr) if Pn else None, P(f32(cond)), P(f32(style)),
+                                  T, Pn, steps, cfg, P(xt), P(vt))
+        return x.reshape(T, 80), xt, vt
+
+    def cfm_euler_masked(self, x0, prompt, cond, style, mask, steps, cfg):
+        """Euler decode at the padded length with key mask (one request)."""
+        x = f32(x0).copy()
+        m = u32(mask)
+        T = m.size
+        pr = f32(prompt)
+        Pn = pr.size // 80
+        lib().orc_cfm_euler_masked(self._m, P(x), P(pr) if Pn else None, P(f32(cond)), P(f32(style)),
+                                   PU(m), T, Pn, steps, cfg)
+        return x.reshape(T, 80)
+
+
+def rel_l2(got, ref) -> float:
+    """metal_indextts2/metrics.py:40-54 relative_l2_error."""
+    g = np.asarray(got, np.float64).reshape(-1)
+    r = np.asarray(ref, np.float64).reshape(-1)
+    return float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
