@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Benchmark: DiT-CFM mel decode on one MI355X.
+
+Workload (one bench "step" = one full decode): T = 860 mel frames (258 prompt
++ 602 generated), 25 Euler steps, CFG rate 0.7 with the cond/null pair
+batched as B = 2, hidden 512, 13 AdaRMSNorm blocks (8 heads x 64), 8-layer
+WaveNet (k=5, 512 ch); synthetic f16 weights N(0, 0.02) from seed 20240605;
+x0, content, style ~ N(0,1), prompt mel ~ N(-5, 2).  Inputs are resident in
+HBM before the timed region; the decode runs on the library's stream through
+the C ABI (mit2cfm_decode_device) and is timed with host wall clock around
+`--steps` decodes, bracketed by device synchronisation.
+
+Prints ONE JSON line.  Extra fields:
+  roofline      the dominant kernel's algorithmic TFLOP/s (flops per launch /
+                average launch time from HIP events on the library stream)
+                against the f16 dense MFMA peak; traffic from committed
+                rocprofv3 FETCH_SIZE / WRITE_SIZE runs when present.
+  cpu_baseline  the CPU restatement of the reference path on this host:
+                one Euler step (cond + null forward) at T = 860, extrapolated
+                to the 25-step decode.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "index-tts2-metal_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "DiT-CFM mel frames/sec at 25 steps, B=2 CFG, T=860; MFMA util %"
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA
+PEAK_HBM_GBS = 8000.0
+# Algorithmic FLOPs per estimator forward: 148,373,504 per valid row + 26,624 * sum_b T_b^2.
+FLOPS_PER_ROW = 148_373_504
+FLOPS_PER_T2 = 26_624
+KERNEL_IDS = {"w13": 0, "conv": 1, "qkv": 2, "w2": 3, "attention": 4, "adarms": 5}
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10, help="timed decodes")
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--tokens", type=int, default=860)
+    p.add_argument("--prompt", type=int, default=258)
+    p.add_argument("--cfm-steps", type=int, default=25)
+    p.add_argument("--cfg", type=float, default=0.7)
+    p.add_argument("--kernel", default="conv", choices=sorted(KERNEL_IDS),
+                   help="kernel reported in `roofline`")
+    p.add_argument("--kernel-launches", type=int, default=200)
+    p.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, available cores)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def traffic_from_profiles(kernel_name: str, tokens: int):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
+    committed under profiles/ as JSON; None when not measured."""
+    f = ROOT / "profiles" / f"traffic_{kernel_name}_T{tokens}.json"
+    if not f.exists():
+        return None
+    try:
+        return float(json.loads(f.read_text())["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(tensors, T, P, cfm_steps, cfg, threads):
+    import numpy as np
+    import mit2cfm
+    from oracle import oracle
+
+    oracle.set_threads(threads)
+    model = oracle.Model(tensors)
+    x0 = mit2cfm.normal_noise(T, 80, 1)
+    cond = mit2cfm.normal_noise(T, 512, 2)
+    style = mit2cfm.normal_noise(1, 192, 3)[0]
+    prompt = mit2cfm.normal_noise(P, 80, 4, 2.0) - 5.0
+    x = x0.copy()
+    x[:P] = 0
+    px = np.zeros((T, 80), np.float32)
+    px[:P] = prompt
+    mask = np.ones(T, np.uint32)
+    t0 = time.perf_counter()
+    model.estimator_step(x, px, cond, style, 0.0, mask)
+    if cfg > 0:
+        model.estimator_step(x, np.zeros_like(px), np.zeros_like(cond), np.zeros_like(style), 0.0, mask)
+    step_s = time.perf_counter() - t0
+    model.close()
+    decode_s = step_s * cfm_steps
+    return {
+        "value": T / decode_s,
+        "unit": "mel frames/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"1 of {cfm_steps} Euler steps (cond + null estimator forwards) at T={T}, "
+                  f"{step_s:.1f} s measured, decode time extrapolated x{cfm_steps}",
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {a.gpus} is not supported "
+              "(multi-GPU sharding is design-only).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch  # first: the library then shares torch's HIP runtime
+    import mit2cfm
+
+    T, P, S, cfg = a.tokens, a.prompt, a.cfm_steps, a.cfg
+    dev = torch.device("cuda:0")
+    tensors = mit2cfm.synthetic_tensors(20240605, 0.02)
+    ctx = mit2cfm.Context(tensors, device=0)
+
+    x0 = mit2cfm.normal_noise(T, 80, 1)
+    cond = mit2cfm.normal_noise(T, 512, 2)
+    style = mit2cfm.normal_noise(1, 192, 3)[0]
+    prompt = mit2cfm.normal_noise(P, 80, 4, 2.0) - 5.0
+    d_x0 = torch.from_numpy(x0).to(dev)
+    d_prompt = torch.from_numpy(np.ascontiguousarray(prompt)).to(dev)
+    d_cond = torch.from_numpy(cond).to(dev)
+    d_style = torch.from_numpy(style).to(dev)
+    d_out = torch.empty((T, 80), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def decode():
+        ctx.decode_device(d_x0.data_ptr(), d_prompt.data_ptr(), d_cond.data_ptr(), d_style.data_ptr(),
+                          T, P, S, cfg, d_out.data_ptr(), sync=False)
+
+    stream = torch.cuda.ExternalStream(ctx.stream, device=dev)
+    for _ in range(a.warmup):
+        decode()
+    ctx.synchronize()
+    torch.cuda.synchronize()
+
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(a.steps):
+        decode()
+    ev1.record(stream)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_decode = wall * 1e3 / a.steps
+    ev_ms = ev0.elapsed_time(ev1) / a.steps
+    out = d_out.cpu().numpy()
+    if not np.isfinite(out).all():
+        raise RuntimeError("decode produced non-finite values")
+
+    flops_decode = S * (FLOPS_PER_ROW * 2 * T + FLOPS_PER_T2 * 2 * T * T)
+    frames_per_s = T / (ms_per_decode / 1e3)
+
+    # Dominant kernel: average launch time from events on the library stream.
+    kid = KERNEL_IDS[a.kernel]
+    name, kflops, kbytes = ctx.profile_launch(kid, 0)
+    ctx.profile_launch(kid, 10)  # warm
+    ctx.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    ctx.profile_launch(kid, a.kernel_launches)
+    e1.record(stream)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    k_ms = e0.elapsed_time(e1) / a.kernel_launches
+    if kflops > 0:
+        achieved = kflops / (k_ms / 1e3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_F16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16_TFLOPS, 4)}
+    else:
+        achieved = kbytes / (k_ms / 1e3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    roof.update({"traffic": traffic_from_profiles(name, T), "kernel": name,
+                 "avg_launch_us": round(k_ms * 1e3, 2), "algorithmic_flops": kflops,
+                 "algorithmic_bytes": kbytes})
+
+    # Host-pointer decode (PCIe-inclusive; reported, never the headline value).
+    ctx.decode(x0, prompt, cond, style, S, cfg)
+    t1 = time.perf_counter()
+    for _ in range(3):
+        ctx.decode(x0, prompt, cond, style, S, cfg)
+    pcie_ms = (time.perf_counter() - t1) * 1e3 / 3
+    ctx.close()
+
+    result = {
+        "metric": METRIC,
+        "value": round(frames_per_s, 1),
+        "unit": "mel frames/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_decode, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"cfm_decode_T{T}_P{P}_S{S}_cfg{cfg}_B2", "tokens": T,
+                   "prompt_tokens": P, "cfm_steps": S, "cfg_rate": cfg, "branches": 2,
+                   "weights": "synthetic f16 N(0,0.02) seed 20240605",
+                   "step": "one full decode"},
+        "cfm_steps_per_s": round(S / (ms_per_decode / 1e3), 1),
+        "generated_frames_per_s": round((T - P) / (ms_per_decode / 1e3), 1),
+        "event_ms_per_decode": round(ev_ms, 4),
+        "decode_mfma_util": round(flops_decode / (ms_per_decode / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4),
+        "algorithmic_tflop_per_decode": round(flops_decode / 1e12, 4),
+        "pcie_inclusive_frames_per_s": round(T / (pcie_ms / 1e3), 1),
+        "roofline": roof,
+    }
+    if not a.no_cpu_baseline:
+        try:
+            n = len(os.sched_getaffinity(0))
+        except AttributeError:
+            n = os.cpu_count() or 1
+        threads = a.cpu_threads or max(1, min(16, n))
+        result["cpu_baseline"] = cpu_baseline(tensors, T, P, S, cfg, threads)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

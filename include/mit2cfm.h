@@ -134,6 +134,19 @@ mit2cfm_status mit2cfm_synchronize(mit2cfm_ctx* ctx);
 /* Whole-decode hipGraph replay on (1, default) or off (0). */
 mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on);
 
+/* ---- measurement hook ------------------------------------------------------------
+ * Enqueues `count` back-to-back launches of one decode kernel at the shape of
+ * the context's last decode (operands: that decode's workspace), on the
+ * context stream, without waiting, so a caller can bracket them with events
+ * on mit2cfm_stream.  Reports the kernel's algorithmic flops and HBM bytes per
+ * launch and its name.  Kernel ids: 0 FFN w1|w3 GEMM + SwiGLU, 1 WaveNet
+ * k=5 conv GEMM + gate, 2 QKV GEMM + RoPE, 3 FFN w2 GEMM + residual,
+ * 4 masked attention, 5 AdaRMSNorm.  No reference counterpart (the reference
+ * times whole command buffers, metal_context.mm:463-477). */
+mit2cfm_status mit2cfm_profile_launch(mit2cfm_ctx* ctx, int32_t kernel, uint32_t count,
+                                      double* flops_per_launch, double* bytes_per_launch,
+                                      const char** name);
+
 /* ---- stage entry points (parity harness; host pointers, synchronous) ---------
  * One per reference CPU stage, mirroring the reference's --test-dit-* harnesses
  * (main.cpp:2909-2989).  rows = batch * tokens; t1/t2 are 512-d embeddings. */
@@ -176,7 +189,7 @@ mit2cfm_status mit2cfm_stage_final_layer(mit2cfm_ctx* ctx, const float* in, cons
                                          uint32_t rows, float* out);
 /* The MFMA GEMM alone (replaces pass_linear_rows_mps, metal_context.mm:328-378):
  * out[M][N] = f16(A)[M][K] . f16(W)[N][K]^T + bias (bias may be NULL);
- * K % 32 == 0, N % 64 == 0. */
+ * K % 128 == 0, N % 64 == 0. */
 mit2cfm_status mit2cfm_op_linear(mit2cfm_ctx* ctx, const float* a, const float* w,
                                  const float* bias, uint32_t m, uint32_t n, uint32_t k,
                                  float* out);

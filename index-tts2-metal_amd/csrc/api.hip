@@ -294,6 +294,17 @@ mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on) {
   return MIT2CFM_OK;
 }
 
+mit2cfm_status mit2cfm_profile_launch(mit2cfm_ctx* ctx, int32_t kernel, uint32_t count,
+                                      double* flops_per_launch, double* bytes_per_launch,
+                                      const char** name) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    static thread_local std::string nm;
+    ctx->eng->profile_launch(kernel, (int)count, flops_per_launch, bytes_per_launch, &nm);
+    if (name) *name = nm.c_str();
+  });
+}
+
 // ---- stages
 #define STAGE_BODY(...)                                                   \
   if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL"); \

@@ -21,6 +21,14 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Padded operand widths (every GEMM K is a multiple of 128 so that K stages
+// of 64/128/256 divide it and concatenated operands switch source on a stage
+// boundary).
+constexpr int kMelPad = 128;   // f16 mel rows: 80 values + 48 zeros
+constexpr int kMcWidth = 896;  // merge-constant rows: [prompt 128 | content 512 | style 192 | 0 x 64]
+constexpr int kMcContent = 128;
+constexpr int kMcStyle = 640;
+
 // D(16x16, fp32) += A(16x32, f16) * B(32x16, f16).
 // Lane l supplies A row (l % 16) and B column (l % 16), each with the eight
 // K-slots of lane group l / 16.  D element (row 4*(l/16)+i, col l%16) is in

@@ -97,6 +97,12 @@ class Engine {
   void op_linear(const float* A, const float* W, const float* bias, int M, int N, int K,
                  float* out);
 
+  // Enqueues `count` launches of one decode kernel at the shape of the last
+  // decode (its workspace contents as operands), on stream(), without
+  // synchronising; returns the kernel's algorithmic flops and HBM bytes per
+  // launch.  A measurement hook: kernel ids are listed in mit2cfm.h.
+  void profile_launch(int kernel, int count, double* flops, double* bytes, std::string* name);
+
   // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
   void set_use_graph(bool on) { use_graph_ = on; }
   void sync();
@@ -114,6 +120,7 @@ class Engine {
   void upload_stage_tables(const float* t1_host, const float* t2_host);
 
   int device_ = 0;
+  int last_B_ = 0, last_T_ = 0;
   hipStream_t stream_ = nullptr;
   bool use_graph_ = true;
   std::unique_ptr<Weights> w_;

@@ -80,14 +80,14 @@ struct Weights {
   float* gamma[27];
   // GEMM weights (f16)
   half_t* cp_w;  float* cp_b;
-  half_t* mx_w;                // [512][96]
-  half_t* mc_w;  float* mc_b;  // [512][800]
+  half_t* mx_w;                // [512][kMelPad]
+  half_t* mc_w;  float* mc_b;  // [512][kMcWidth]
   half_t* qkv_w[13];
   half_t* wo_w[13];
   half_t* w13_w[13];
   half_t* w2_w[13];
   half_t* si_w[13]; float* si_b[13];
-  half_t* sl_w;  float* sl_b;  // [512][608]
+  half_t* sl_w;  float* sl_b;  // [512][512 + kMelPad]
   half_t* c1rp_w; float* c1rp_b;  // [1024][512]
   half_t* in_w[8]; float* in_b[8];  // [1024][2560]
   half_t* rs_w[8]; float* rs_b[8];
@@ -295,11 +295,11 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
   W.cp_b = up.f32(hm.get("cond_projection.bias", 512));
   {
     const auto& mw = hm.get("cond_x_merge_linear.weight", 512 * 864);
-    std::vector<float> mx((size_t)512 * 96, 0.f), mc((size_t)512 * 800, 0.f);
-    copy_cols(mw, 512, 864, 0, 80, mx, 96, 0);      // x
-    copy_cols(mw, 512, 864, 80, 80, mc, 800, 0);    // prompt_x
-    copy_cols(mw, 512, 864, 160, 512, mc, 800, 96); // content projection
-    copy_cols(mw, 512, 864, 672, 192, mc, 800, 608);// style
+    std::vector<float> mx((size_t)512 * kMelPad, 0.f), mc((size_t)512 * kMcWidth, 0.f);
+    copy_cols(mw, 512, 864, 0, 80, mx, kMelPad, 0);               // x
+    copy_cols(mw, 512, 864, 80, 80, mc, kMcWidth, 0);             // prompt_x
+    copy_cols(mw, 512, 864, 160, 512, mc, kMcWidth, kMcContent);  // content projection
+    copy_cols(mw, 512, 864, 672, 192, mc, kMcWidth, kMcStyle);    // style
     W.mx_w = up.f16(mx);
     W.mc_w = up.f16(mc);
     W.mc_b = up.f32(hm.get("cond_x_merge_linear.bias", 512));
@@ -328,8 +328,8 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
   }
   {
     const auto& sw = hm.get("skip_linear.weight", 512 * 592);
-    std::vector<float> s((size_t)512 * 608, 0.f);
-    copy_cols(sw, 512, 592, 0, 592, s, 608, 0);
+    std::vector<float> s((size_t)512 * (512 + kMelPad), 0.f);
+    copy_cols(sw, 512, 592, 0, 592, s, 512 + kMelPad, 0);
     W.sl_w = up.f16(s);
     W.sl_b = up.f32(hm.get("skip_linear.bias", 512));
   }
@@ -414,7 +414,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   size_t bytes = 0;
   auto f = [&](size_t n) { bytes += ((n * 4) + 255) / 256 * 256; };
   auto h = [&](size_t n) { bytes += ((n * 2) + 255) / 256 * 256; };
-  f((size_t)cReq * cT * 80); h(r * 96); h(r * 512); h(r * 800); f(r * 512); f(r * 512); f(r * 512);
+  f((size_t)cReq * cT * 80); h(r * kMelPad); h(r * 512); h(r * kMcWidth); f(r * 512); f(r * 512); f(r * 512);
   for (int i = 0; i < 6; ++i) h(r * 512);
   h(r * 512); h(r * 512);
   h((size_t)cRpad * 512); h((size_t)cRpad * 512); h((size_t)cRpad * 512);
@@ -433,9 +433,9 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   auto F = [&](size_t n) { return static_cast<float*>(a.take(n * 4)); };
   auto H = [&](size_t n) { return static_cast<half_t*>(a.take(n * 2)); };
   ws.x_cur = F((size_t)cReq * cT * 80);
-  ws.xmel16 = H(r * 96);
+  ws.xmel16 = H(r * kMelPad);
   ws.cond16 = H(r * 512);
-  ws.mc16 = H(r * 800);
+  ws.mc16 = H(r * kMcWidth);
   ws.xin_const = F(r * 512);
   ws.xa = F(r * 512);
   ws.xb = F(r * 512);
@@ -599,9 +599,9 @@ void Engine::enqueue_estimator(int B, int T, int slot) {
   enqueue_transformer(B, T, tab);
   {
     GemmArgs g;  // skip_linear on [x_normed | x_mel]
-    g.M = R; g.N = 512; g.K = 608; g.K1 = 512;
-    g.A = ws.n16; g.lda = 512; g.A2 = ws.xmel16; g.lda2 = 96;
-    g.W = W.sl_w; g.ldw = 608; g.bias = W.sl_b; g.C16 = ws.ls16; g.ldc16 = 512;
+    g.M = R; g.N = 512; g.K = 512 + kMelPad; g.K1 = 512;
+    g.A = ws.n16; g.lda = 512; g.A2 = ws.xmel16; g.lda2 = kMelPad;
+    g.W = W.sl_w; g.ldw = 512 + kMelPad; g.bias = W.sl_b; g.C16 = ws.ls16; g.ldc16 = 512;
     HIP_OK(launch_gemm(g, A_CONCAT, EPI_F16, s));
   }
   {
@@ -641,24 +641,24 @@ void Engine::enqueue_estimator(int B, int T, int slot) {
   }
 }
 
-// Input merge constant part: cond projection into mc16[:, 96:608], then
+// Input merge constant part: cond projection into mc16[:, kMcContent:+512], then
 // xin_const = mc16 . Wc^T + b_merge.
 static void enqueue_merge_const(Weights& W, Workspace& ws, int R, hipStream_t s) {
   GemmArgs g;
   g.M = R; g.N = 512; g.K = 512; g.A = ws.cond16; g.lda = 512;
-  g.W = W.cp_w; g.ldw = 512; g.bias = W.cp_b; g.C16 = ws.mc16 + 96; g.ldc16 = 800;
+  g.W = W.cp_w; g.ldw = 512; g.bias = W.cp_b; g.C16 = ws.mc16 + kMcContent; g.ldc16 = kMcWidth;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F16, s));
   GemmArgs c;
-  c.M = R; c.N = 512; c.K = 800; c.A = ws.mc16; c.lda = 800;
-  c.W = W.mc_w; c.ldw = 800; c.bias = W.mc_b; c.C32 = ws.xin_const; c.ldc32 = 512;
+  c.M = R; c.N = 512; c.K = kMcWidth; c.A = ws.mc16; c.lda = kMcWidth;
+  c.W = W.mc_w; c.ldw = kMcWidth; c.bias = W.mc_b; c.C32 = ws.xin_const; c.ldc32 = 512;
   HIP_OK(launch_gemm(c, A_PLAIN, EPI_F32, s));
 }
 
 // Per-step merge: x = xin_const + xmel16 . Wx^T
 static void enqueue_merge_step(Weights& W, Workspace& ws, int R, hipStream_t s) {
   GemmArgs g;
-  g.M = R; g.N = 512; g.K = 96; g.A = ws.xmel16; g.lda = 96;
-  g.W = W.mx_w; g.ldw = 96; g.res = ws.xin_const; g.ldres = 512; g.C32 = ws.xa; g.ldc32 = 512;
+  g.M = R; g.N = 512; g.K = kMelPad; g.A = ws.xmel16; g.lda = kMelPad;
+  g.W = W.mx_w; g.ldw = kMelPad; g.res = ws.xin_const; g.ldres = 512; g.C32 = ws.xa; g.ldc32 = 512;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
 }
 
@@ -709,6 +709,8 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
   const int cfg_on = cfg > 0.0f ? 1 : 0;
   const int B = cfg_on ? 2 * nreq : nreq;
   ensure_workspace(B, T, steps, nreq);
+  last_B_ = B;
+  last_T_ = T;
   Workspace& ws = *ws_;
   ensure_rope(T);
   {
@@ -778,6 +780,83 @@ void Engine::estimator_step_device(const float* x, const float* prompt_x, const 
   enqueue_estimator(B, T, 0);
   HIP_OK(launch_conv2_rows(ws.y16, W.c2_w, W.c2_b, R, dphi, stream_));
   HIP_OK(hipStreamSynchronize(stream_));
+}
+
+// ------------------------------------------------------------------ profiling hook
+void Engine::profile_launch(int kernel, int count, double* flops, double* bytes, std::string* name) {
+  if (last_B_ == 0) throw std::invalid_argument("profile_launch: run a decode first");
+  const int B = last_B_, T = last_T_, R = B * T;
+  const int Tpad = (T + 63) / 64 * 64;
+  Weights& W = *w_;
+  Workspace& ws = *ws_;
+  const float* tab = ws.tab;
+  double f = 0, by = 0;
+  std::string nm;
+  auto loop = [&](auto&& launch) {
+    for (int i = 0; i < count; ++i) launch();
+  };
+  switch (kernel) {
+    case 0: {  // FFN w1|w3 GEMM + SwiGLU (N = 3072, K = 512)
+      GemmArgs g;
+      g.M = R; g.N = 3072; g.K = 512; g.A = ws.n16; g.lda = 512;
+      g.W = W.w13_w[0]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = 1536;
+      loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, stream_)); });
+      f = 2.0 * R * 3072 * 512;
+      by = 2.0 * R * 512 + 2.0 * 3072 * 512 + 2.0 * R * 1536;
+      nm = "gemm_w13_swiglu";
+      break;
+    }
+    case 1: {  // WaveNet k=5 conv as implicit GEMM + gate (N = 1024, K = 2560)
+      GemmArgs g;
+      g.M = R; g.N = 1024; g.K = 2560; g.A = ws.wn_x16; g.lda = 512; g.T = T; g.conv_c = 512;
+      g.W = W.in_w[0]; g.ldw = 2560; g.bias = W.in_b[0]; g.cond = tab + kWnCondOff;
+      g.C16 = ws.gate16; g.ldc16 = 512;
+      loop([&] { HIP_OK(launch_gemm(g, A_CONV5, EPI_GATE, stream_)); });
+      f = 2.0 * R * 1024 * 2560;
+      by = 2.0 * R * 512 + 2.0 * 1024 * 2560 + 2.0 * R * 512;
+      nm = "gemm_wavenet_conv_gate";
+      break;
+    }
+    case 2: {  // QKV GEMM + RoPE (N = 1536, K = 512)
+      GemmArgs g;
+      g.M = R; g.N = 1536; g.K = 512; g.A = ws.n16; g.lda = 512; g.W = W.qkv_w[0]; g.ldw = 512;
+      g.T = T; g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
+      loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, stream_)); });
+      f = 2.0 * R * 1536 * 512;
+      by = 2.0 * R * 512 + 2.0 * 1536 * 512 + 2.0 * R * 1536;
+      nm = "gemm_qkv_rope";
+      break;
+    }
+    case 3: {  // FFN w2 GEMM + residual (N = 512, K = 1536)
+      GemmArgs g;
+      g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = 1536; g.W = W.w2_w[0]; g.ldw = 1536;
+      g.res = ws.xb; g.ldres = 512; g.C32 = ws.stage_a; g.ldc32 = 512;
+      loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, stream_)); });
+      f = 2.0 * R * 512 * 1536;
+      by = 2.0 * R * 1536 + 2.0 * 512 * 1536 + 8.0 * R * 512;
+      nm = "gemm_w2_residual";
+      break;
+    }
+    case 4: {  // masked flash attention
+      loop([&] { HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.mask, ws.o16, B, T, Tpad, stream_)); });
+      f = 4.0 * 64.0 * 8.0 * B * (double)T * (double)T;
+      by = 2.0 * 3.0 * B * 8 * (double)T * 64 + 2.0 * R * 512 + 4.0 * R;
+      nm = "attention";
+      break;
+    }
+    case 5: {  // AdaRMSNorm row kernel
+      loop([&] { HIP_OK(launch_adarms(ws.xa, W.gamma[0], tab, tab + 512, ws.n16, R, stream_)); });
+      f = 0;
+      by = 4.0 * R * 512 + 2.0 * R * 512 + 3.0 * 512 * 4;
+      nm = "adarms";
+      break;
+    }
+    default:
+      throw std::invalid_argument("profile_launch: unknown kernel id");
+  }
+  if (flops) *flops = f;
+  if (bytes) *bytes = by;
+  if (name) *name = nm;
 }
 
 // ------------------------------------------------------------------ stages
@@ -954,7 +1033,7 @@ void Engine::stage_post(const float* xres, const float* xmel, int rows, float* l
   Workspace& ws = *ws_;
   h2d(ws.stage_a, xres, (size_t)rows * 512 * 4, stream_);
   to_f16(ws.stage_a, ws.n16, (size_t)rows * 512, stream_);
-  // xmel16 rows of 96 (80 + zero pad): reuse step prep with zero prompt/cond/style.
+  // xmel16 rows (80 + zero pad): reuse step prep with zero prompt/cond/style.
   std::vector<float> zeros((size_t)rows * 512, 0.0f);
   h2d(ws.in_x, xmel, (size_t)rows * 80 * 4, stream_);
   h2d(ws.in_prompt, zeros.data(), (size_t)rows * 80 * 4, stream_);
@@ -963,9 +1042,9 @@ void Engine::stage_post(const float* xres, const float* xmel, int rows, float* l
   HIP_OK(launch_step_prep(ws.in_x, ws.in_prompt, ws.in_cond, ws.in_style, 1, rows, ws.xmel16,
                           ws.cond16, ws.mc16, stream_));
   GemmArgs g;
-  g.M = rows; g.N = 512; g.K = 608; g.K1 = 512;
-  g.A = ws.n16; g.lda = 512; g.A2 = ws.xmel16; g.lda2 = 96;
-  g.W = W.sl_w; g.ldw = 608; g.bias = W.sl_b; g.C16 = ws.ls16; g.ldc16 = 512;
+  g.M = rows; g.N = 512; g.K = 512 + kMelPad; g.K1 = 512;
+  g.A = ws.n16; g.lda = 512; g.A2 = ws.xmel16; g.lda2 = kMelPad;
+  g.W = W.sl_w; g.ldw = 512 + kMelPad; g.bias = W.sl_b; g.C16 = ws.ls16; g.ldc16 = 512;
   HIP_OK(launch_gemm(g, A_CONCAT, EPI_F16, stream_));
   GemmArgs c;
   c.M = rows; c.N = 1024; c.K = 512; c.A = ws.ls16; c.lda = 512;
@@ -1029,8 +1108,8 @@ void Engine::stage_final_layer(const float* in, const float* t1, int rows, float
 
 void Engine::op_linear(const float* A, const float* Wt, const float* bias, int M, int N, int K,
                        float* out) {
-  if (M <= 0 || N <= 0 || K <= 0 || K % 32 != 0 || N % 64 != 0)
-    throw std::invalid_argument("op_linear: need M > 0, K % 32 == 0, N % 64 == 0");
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0 || N % 64 != 0)
+    throw std::invalid_argument("op_linear: need M > 0, K % 128 == 0, N % 64 == 0");
   HIP_OK(hipSetDevice(device_));
   DevBuf a32((size_t)M * K * 4), w32((size_t)N * K * 4), a16((size_t)M * K * 2),
       w16((size_t)N * K * 2), b((size_t)N * 4), c((size_t)M * N * 4);

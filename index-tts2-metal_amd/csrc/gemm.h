@@ -3,7 +3,7 @@
 // C[M, N] = A[M, K] . W[N, K]^T, fp32 accumulation.  W is a resident f16
 // weight whose rows may be permuted at upload so that an epilogue finds the
 // two operands it combines (SwiGLU halves, WaveNet gate halves, RoPE pairs)
-// in the same lane.  K must be a multiple of 32 and N a multiple of the tile
+// in the same lane.  K must be a multiple of 128 and N a multiple of the tile
 // width (weights are zero-padded at upload where the model's K is not).
 #pragma once
 

@@ -2,29 +2,112 @@
 //
 // Replaces the reference's MPS GEMM dispatch (runtime/metal_context.mm:328-378)
 // and the kernels fused around it (bias pre-fill kernels.metal:227, residual
-// add :161, SwiGLU :131, WaveNet gate :411, res/skip update :436, RoPE :2390).
+// add :161, SwiGLU :131, WaveNet gate :411, res/skip update :436, RoPE :2390,
+// reflect-pad + im2col :175-225 for the k=5 conv).
 //
-// Tiling: a 256-thread workgroup (4 wavefronts in a 2x2 grid) owns a BM x BN
-// output tile; K advances 32 at a time.  Global -> register prefetch of tile
-// k+1 overlaps the MFMAs of tile k, and LDS is double buffered so there is a
-// single barrier per K step.  LDS rows are padded to 40 halves (80 bytes) so
-// the 16 lanes of each 128-bit fragment read hit 64 distinct banks.
+// Pipeline.  A 256-thread workgroup (4 wavefronts, 2x2) owns a BM x BN tile.
+// K is consumed in stages of SK halves; NST stages live in a ring of LDS
+// buffers, each its own __shared__ object.  Operands move global -> LDS with
+// gfx950's direct loads (global_load_lds_dwordx4: each lane's 16 bytes land
+// at M0 + 16*lane), so NST-1 stages (tens of KB per CU) are in flight while
+// the current one feeds the MFMAs, with no register staging.  Because every
+// stage buffer is a distinct LDS object the compiler can tell the in-flight
+// DMA from the buffer being read and keeps only the explicit vmcnt waits.
+//
+// LDS layout.  A stage row is SK halves = CPR 16-byte slots; the slot holding
+// global chunk c of row r is c ^ key(r) (key = r & 15, or (r >> 1) & 7 for
+// 8-slot rows), so the 16 lanes of a ds_read_b128 that read 16 consecutive
+// rows at one chunk hit 64 distinct banks.
+//
+// Tile -> workgroup map.  Workgroups are dealt to the 8 XCDs round-robin; the
+// map gives each XCD a rectangle of tiles (Xm x Xn split of the tile grid,
+// chosen on the host to minimise A and W re-reads across XCDs) so that the
+// operands a rectangle shares stay in that XCD's L2.
+#include <algorithm>
+#include <type_traits>
+
 #include "gemm.h"
 
 namespace mit2hip {
 
-constexpr int kBK = 32;
-constexpr int kLdsStride = kBK + 8;  // halves per LDS row
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int BM, int BN, int AM, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
-  constexpr int MI = BM / 32;  // 16-row MFMA blocks per wave (2 waves along M)
-  constexpr int NI = BN / 32;  // 16-col MFMA blocks per wave (2 waves along N)
-  constexpr int A_CHUNKS = BM * 4 / 256;
-  constexpr int B_CHUNKS = BN * 4 / 256;
-  static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for 256 threads");
-  __shared__ __attribute__((aligned(16))) half_t As[2][BM * kLdsStride];
-  __shared__ __attribute__((aligned(16))) half_t Bs[2][BN * kLdsStride];
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// s_waitcnt lgkmcnt(0): this wave's LDS reads have returned.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));
+}
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+struct TileMap {
+  int nM, nN;  // tile grid
+  int Xm, Xn;  // XCD rectangle grid, Xm * Xn == 8
+  int per_xcd; // workgroups per XCD (grid = 8 * per_xcd)
+  __device__ __forceinline__ bool map(int b, int& tm, int& tn) const {
+    const int xcd = b & 7, slot = b >> 3;
+    const int rx = xcd / Xn, ry = xcd - (xcd / Xn) * Xn;
+    const int mlo = rx * nM / Xm, mhi = (rx + 1) * nM / Xm;
+    const int nlo = ry * nN / Xn, nhi = (ry + 1) * nN / Xn;
+    const int rn = nhi - nlo;
+    if (rn <= 0 || slot >= (mhi - mlo) * rn) return false;
+    tm = mlo + slot / rn;
+    tn = nlo + slot % rn;
+    return true;
+  }
+};
+
+template <int BM, int BN, int SK, int NST, int AM, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
+  constexpr int CPR = SK / 8;                // 16-byte slots per stage row
+  constexpr int LA = BM * CPR / 256;         // DMA instructions per wave per stage (A)
+  constexpr int LB = BN * CPR / 256;         // (W)
+  constexpr int L = LA + LB;
+  constexpr int MI = BM / 32;                // 16-row MFMA blocks per wave
+  constexpr int NI = BN / 32;                // 16-col MFMA blocks per wave
+  static_assert(LA >= 1 && LB >= 1, "tile too small for 256 threads");
+  static_assert(L * (NST - 1) < 64, "too many loads in flight");
+  static_assert(CPR == 8 || CPR >= 16, "stage width");
+
+  // One __shared__ object per stage and operand, declared here so each kernel
+  // instantiation owns its own objects (the per-object alias scopes are what
+  // let the compiler keep only the explicit vmcnt waits).
+  __shared__ __attribute__((aligned(1024))) half_t sA0[BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA1[BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB0[BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB1[BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? BN * SK : 8];
+  static_assert(NST >= 2 && NST <= 4, "two to four stages");
+  auto bufA = [&](auto st) -> half_t* {
+    constexpr int s = decltype(st)::value;
+    if constexpr (s == 0) return sA0; else if constexpr (s == 1) return sA1;
+    else if constexpr (s == 2) return sA2; else return sA3;
+  };
+  auto bufB = [&](auto st) -> half_t* {
+    constexpr int s = decltype(st)::value;
+    if constexpr (s == 0) return sB0; else if constexpr (s == 1) return sB1;
+    else if constexpr (s == 2) return sB2; else return sB3;
+  };
+
+  int tile_m, tile_n;
+  if (!tmap.map(blockIdx.x, tile_m, tile_n)) return;
+  const int m0 = tile_m * BM;
+  const int n0 = tile_n * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -33,60 +116,47 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
   const int wn = wave & 1;
   const int lr = lane & 15;
   const int lg = lane >> 4;
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
-  const int KT = p.K / kBK;
+  const int KT = p.K / SK;
 
-  half8 ra[A_CHUNKS];
-  half8 rb[B_CHUNKS];
+  auto swz = [](int row) { return CPR >= 16 ? (row & 15) : ((row >> 1) & 7); };
 
-  auto load_tiles = [&](int kt) {
-    const int k0 = kt * kBK;
-#pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      const int r = c >> 2;
-      const int kc = c & 3;
-      const int m = m0 + r;
-      half8 v = {};
-      if (m < p.M) {
-        const half_t* src;
-        if constexpr (AM == A_PLAIN) {
-          src = p.A + (size_t)m * p.lda + k0 + kc * 8;
-        } else if constexpr (AM == A_CONCAT) {
-          src = (k0 < p.K1) ? p.A + (size_t)m * p.lda + k0 + kc * 8
-                            : p.A2 + (size_t)m * p.lda2 + (k0 - p.K1) + kc * 8;
-        } else {
-          const int tap = k0 / p.conv_c;
-          const int c0 = k0 - tap * p.conv_c;
-          const int b = m / p.T;
-          const int t = m - b * p.T;
-          const int s = reflect_index(t + tap - 2, p.T);
-          src = p.A + (size_t)(b * p.T + s) * p.lda + c0 + kc * 8;
-        }
-        v = *reinterpret_cast<const half8*>(src);
-      }
-      ra[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      const int r = c >> 2;
-      const int kc = c & 3;
-      rb[i] = *reinterpret_cast<const half8*>(p.W + (size_t)(n0 + r) * p.ldw + k0 + kc * 8);
+  auto a_src = [&](int m, int k) -> const half_t* {
+    if constexpr (AM == A_PLAIN) {
+      return p.A + (size_t)m * p.lda + k;
+    } else if constexpr (AM == A_CONCAT) {
+      return k < p.K1 ? p.A + (size_t)m * p.lda + k : p.A2 + (size_t)m * p.lda2 + (k - p.K1);
+    } else {
+      const int tap = k / p.conv_c;
+      const int c = k - tap * p.conv_c;
+      const int b = m / p.T;
+      const int t = m - b * p.T;
+      return p.A + (size_t)(b * p.T + reflect_index(t + tap - 2, p.T)) * p.lda + c;
     }
   };
 
-  auto store_tiles = [&](int buf) {
+  auto issue = [&](auto st, int kt) {
+    half_t* sa = bufA(st);
+    half_t* sb = bufB(st);
+    const int k0 = kt * SK;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      *reinterpret_cast<half8*>(&As[buf][(c >> 2) * kLdsStride + (c & 3) * 8]) = ra[i];
+    for (int j = 0; j < LA; ++j) {
+      const int q0 = (wave * LA + j) * 64;
+      const int q = q0 + lane;
+      const int row = q / CPR;
+      const int c = (q % CPR) ^ swz(row);
+      int m = m0 + row;
+      if (m > p.M - 1) m = p.M - 1;  // rows past M load a valid row; never stored
+      __builtin_amdgcn_global_load_lds((const void*)a_src(m, k0 + c * 8),
+                                       (lds_void_t*)(sa + q0 * 8), 16, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) {
-      const int c = tid + i * 256;
-      *reinterpret_cast<half8*>(&Bs[buf][(c >> 2) * kLdsStride + (c & 3) * 8]) = rb[i];
+    for (int j = 0; j < LB; ++j) {
+      const int q0 = (wave * LB + j) * 64;
+      const int q = q0 + lane;
+      const int row = q / CPR;
+      const int c = (q % CPR) ^ swz(row);
+      __builtin_amdgcn_global_load_lds((const void*)(p.W + (size_t)(n0 + row) * p.ldw + k0 + c * 8),
+                                       (lds_void_t*)(sb + q0 * 8), 16, 0, 0);
     }
   };
 
@@ -96,30 +166,54 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  load_tiles(0);
-  store_tiles(0);
-  __syncthreads();
+  auto compute = [&](auto st) {
+    const half_t* sa = bufA(st);
+    const half_t* sb = bufB(st);
+#pragma unroll
+    for (int kk = 0; kk < SK / 32; ++kk) {
+      const int c = kk * 4 + lg;
+      half8 af[MI];
+      half8 bf[NI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int row = wm * (BM / 2) + i * 16 + lr;
+        af[i] = *reinterpret_cast<const half8*>(sa + row * SK + ((c ^ swz(row)) << 3));
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int row = wn * (BN / 2) + j * 16 + lr;
+        bf[j] = *reinterpret_cast<const half8*>(sb + row * SK + ((c ^ swz(row)) << 3));
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+    }
+  };
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) load_tiles(kt + 1);
-    half8 af[MI];
-    half8 bf[NI];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-      af[i] = *reinterpret_cast<const half8*>(
-          &As[buf][(wm * (BM / 2) + i * 16 + lr) * kLdsStride + lg * 8]);
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-      bf[j] = *reinterpret_cast<const half8*>(
-          &Bs[buf][(wn * (BN / 2) + j * 16 + lr) * kLdsStride + lg * 8]);
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < NI; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
-    if (kt + 1 < KT) store_tiles(buf ^ 1);
-    __syncthreads();
+  // Pipeline: every steady-state iteration issues one stage and waits for the
+  // oldest, so NST-1 stages stay in flight.  The body is branch-free (an
+  // issue past the last stage repeats stage KT-1, an L2 hit, into a buffer
+  // that is not read again), which keeps the compiler from adding waits of
+  // its own; the last KT % NST stages are resident when the loop exits.
+  static_for<0, NST - 1>([&](auto st) { issue(st, min((int)decltype(st)::value, KT - 1)); });
+  int kt0 = 0;
+  for (; kt0 + NST <= KT; kt0 += NST) {
+    static_for<0, NST>([&](auto st) {
+      constexpr int s = decltype(st)::value;
+      wait_lgkmcnt0();               // this wave's reads of the previous stage are done,
+      __builtin_amdgcn_s_barrier();  // and every wave's: the buffer reloaded next is free
+      issue(std::integral_constant<int, (s + NST - 1) % NST>{}, min(kt0 + s + NST - 1, KT - 1));
+      wait_vmcnt<L * (NST - 1)>();   // this wave's share of stage kt0+s has landed
+      __builtin_amdgcn_s_barrier();  // ... and every other wave's
+      compute(st);
+    });
   }
+  wait_vmcnt<0>();  // the tail stages have landed; no DMA outstanding at exit
+  __builtin_amdgcn_s_barrier();
+  static_for<0, NST - 1>([&](auto st) {
+    if (kt0 + (int)decltype(st)::value < KT) compute(st);
+  });
 
   // ---------------------------------------------------------------- epilogue
   const int row_base = m0 + wm * (BM / 2) + lg * 4;
@@ -173,6 +267,48 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
       }
     }
   } else {
+    if constexpr (EPI == EPI_QKV) {
+      if (n0 >= 1024) {
+        // V tile = one head (64 channels) x BM tokens.  Transpose through LDS
+        // so that V^T[d][t] is written by consecutive lanes at consecutive t.
+        static_assert(BN == 64, "a v tile must be exactly one head");
+        half_t* st = sA0;  // [64 d][BM rows], free once every wave is past its last MFMA
+        wait_lgkmcnt0();
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int q = 0; q < NI / 2; ++q) {
+          // Blocks (2q, 2q+1) hold the even/odd channels of the RoPE pairing
+          // (the v rows are permuted like the q and k rows).
+          const int ce = col_base + q * 32;
+          const int d = (ce & 63) + 2 * lr;  // channel within the head
+          const float be = p.bias ? p.bias[ce + lr] : 0.0f;
+          const float bo = p.bias ? p.bias[ce + 16 + lr] : 0.0f;
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int rl = wm * (BM / 2) + i * 16 + lg * 4 + r;
+              st[d * BM + rl] = (half_t)(acc[i][2 * q][r] + be);
+              st[(d + 1) * BM + rl] = (half_t)(acc[i][2 * q + 1][r] + bo);
+            }
+        }
+        wait_lgkmcnt0();  // this wave's stores have landed before the barrier releases readers
+        __builtin_amdgcn_s_barrier();
+        const int hh = (n0 - 1024) >> 6;
+#pragma unroll
+        for (int rr = 0; rr < BM; rr += 64) {
+          const int rl = rr + lane;
+          const int m = m0 + rl;
+          if (m < p.M) {
+            const int b = m / p.T;
+            const int t = m - b * p.T;
+            half_t* dst = p.vt + ((size_t)b * 8 + hh) * 64 * p.Tpad + t;
+            for (int d = wave; d < 64; d += 4) dst[(size_t)d * p.Tpad] = st[d * BM + rl];
+          }
+        }
+        return;
+      }
+    }
     // Paired epilogues: MFMA blocks (2q, 2q+1) of a wave hold, in the same
     // lane, the two operands for output channel c = 16*group + lr.
     static_assert(NI % 2 == 0, "paired epilogue needs an even block count");
@@ -198,30 +334,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
             const float a = ve + p.cond[c];
             const float b = vo + p.cond[512 + c];
             p.C16[(size_t)m * p.ldc16 + c] = (half_t)(tanh_sat(a) * sigmoid_f(b));
-          } else {  // EPI_QKV
+          } else {  // EPI_QKV, q and k sections (v tiles are written below)
             const int o = group * 32 + 2 * lr;  // original column of the even element
-            const int sec = o >> 9;             // 0 = q, 1 = k, 2 = v
+            const int sec = o >> 9;             // 0 = q, 1 = k
             const int hh = (o & 511) >> 6;
             const int d = o & 63;
             const int b = m / p.T;
             const int t = m - b * p.T;
             const size_t head = (size_t)b * 8 + hh;
-            if (sec < 2) {
-              const float2 cs = p.rope[t * 32 + (d >> 1)];
-              float re = ve * cs.x - vo * cs.y;
-              float ro = vo * cs.x + ve * cs.y;
-              if (sec == 0) {
-                re *= 0.125f;  // 1/sqrt(64): a power of two, so the scaling is exact
-                ro *= 0.125f;
-              }
-              half_t* dst = (sec == 0 ? p.q : p.k) + (head * p.Tpad + t) * 64 + d;
-              half2v pr = {(half_t)re, (half_t)ro};
-              *reinterpret_cast<half2v*>(dst) = pr;
-            } else {
-              half_t* dst = p.vt + (head * 64 + d) * p.Tpad + t;
-              dst[0] = (half_t)ve;
-              dst[p.Tpad] = (half_t)vo;
+            const float2 cs = p.rope[t * 32 + (d >> 1)];
+            float re = ve * cs.x - vo * cs.y;
+            float ro = vo * cs.x + ve * cs.y;
+            if (sec == 0) {
+              re *= 0.125f;  // 1/sqrt(64): a power of two, so the scaling is exact
+              ro *= 0.125f;
             }
+            half_t* dst = (sec == 0 ? p.q : p.k) + (head * p.Tpad + t) * 64 + d;
+            half2v pr = {(half_t)re, (half_t)ro};
+            *reinterpret_cast<half2v*>(dst) = pr;
           }
         }
       }
@@ -229,49 +359,88 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
   }
 }
 
-template <int BM, int BN, int AM, int EPI>
+// Chooses the XCD rectangle split minimising the bytes the XCDs re-read:
+// A (M x K) is read once per rectangle column, W (N x K) once per row.
+static TileMap make_tile_map(int M, int N, int K, int BM, int BN) {
+  TileMap t;
+  t.nM = (M + BM - 1) / BM;
+  t.nN = N / BN;
+  const double a_bytes = 2.0 * M * K, w_bytes = 2.0 * N * K;
+  const int opts[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
+  double best = 1e300;
+  t.Xm = 8;
+  t.Xn = 1;
+  for (const auto& o : opts) {
+    const int xm = o[0], xn = o[1];
+    if (xm > t.nM || xn > t.nN) continue;
+    const double cost = a_bytes * xn + w_bytes * xm;
+    if (cost < best) {
+      best = cost;
+      t.Xm = xm;
+      t.Xn = xn;
+    }
+  }
+  if (t.Xm > t.nM || t.Xn > t.nN) {  // tiny grids: fall back to whatever fits
+    t.Xm = t.nM >= 8 ? 8 : 1;
+    t.Xn = 8 / t.Xm;
+  }
+  int mx = 0;
+  for (int x = 0; x < 8; ++x) {
+    const int rx = x / t.Xn, ry = x % t.Xn;
+    const int rm = (rx + 1) * t.nM / t.Xm - rx * t.nM / t.Xm;
+    const int rn = (ry + 1) * t.nN / t.Xn - ry * t.nN / t.Xn;
+    mx = std::max(mx, rm * rn);
+  }
+  t.per_xcd = mx;
+  return t;
+}
+
+template <int BM, int BN, int SK, int NST, int AM, int EPI>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
-  dim3 grid(a.N / BN, (a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, AM, EPI>), grid, dim3(256), 0, s, a);
+  const TileMap tm = make_tile_map(a.M, a.N, a.K, BM, BN);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI>), dim3(8 * tm.per_xcd), dim3(256), 0, s,
+                     a, tm);
   return hipGetLastError();
 }
 
+// Tile and stage choice per shape (measured at M = 1720 on MI355X): 64x64
+// tiles with 64-wide K stages in a 3-buffer ring (48 KB of LDS, three
+// workgroups per CU) for most shapes; 64x128 for the widest N; 128-wide
+// stages for the K = 2560 conv.  QKV keeps BN = 64 so a v tile is one head.
 template <int AM, int EPI>
 static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
-  // 64x64 tiles keep >= 200 workgroups in flight at M = 1720 for N = 512;
-  // wider N gets 64x128 (fewer A re-reads).
-  if (a.N % 128 == 0 && a.N >= 1024) return launch_tile<64, 128, AM, EPI>(a, s);
-  return launch_tile<64, 64, AM, EPI>(a, s);
-}
-
-template <int AM>
-static hipError_t launch_am(const GemmArgs& a, EpiMode epi, hipStream_t s) {
-  switch (epi) {
-    case EPI_F32: return launch_am_epi<AM, EPI_F32>(a, s);
-    case EPI_F16: return launch_am_epi<AM, EPI_F16>(a, s);
-    case EPI_SWIGLU: return launch_am_epi<AM, EPI_SWIGLU>(a, s);
-    case EPI_GATE: return launch_am_epi<AM, EPI_GATE>(a, s);
-    case EPI_QKV: return launch_am_epi<AM, EPI_QKV>(a, s);
-    case EPI_RESSKIP: return launch_am_epi<AM, EPI_RESSKIP>(a, s);
-    case EPI_FINALSKIP: return launch_am_epi<AM, EPI_FINALSKIP>(a, s);
-    case EPI_DUAL: return launch_am_epi<AM, EPI_DUAL>(a, s);
+  if constexpr (EPI != EPI_QKV) {
+    if (a.N >= 3072 && a.N % 128 == 0) return launch_tile<64, 128, 64, 2, AM, EPI>(a, s);
   }
-  return hipErrorInvalidValue;
+  if (a.K >= 2048) return launch_tile<64, 64, 128, 2, AM, EPI>(a, s);
+  return launch_tile<64, 64, 64, 3, AM, EPI>(a, s);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t stream) {
-  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % kBK != 0 || a.N % 64 != 0 || !a.A || !a.W)
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 128 != 0 || a.N % 64 != 0 || !a.A || !a.W)
     return hipErrorInvalidValue;
-  if (amode == A_CONCAT && (a.K1 % kBK != 0 || a.K1 <= 0 || a.K1 >= a.K || !a.A2))
+  if (amode == A_CONCAT && (a.K1 % 128 != 0 || a.K1 <= 0 || a.K1 >= a.K || !a.A2))
     return hipErrorInvalidValue;
-  if (amode == A_CONV5 && (a.T <= 0 || a.conv_c % kBK != 0 || a.K != 5 * a.conv_c))
+  if (amode == A_CONV5 && (a.T <= 0 || a.conv_c % 128 != 0 || a.K != 5 * a.conv_c))
     return hipErrorInvalidValue;
-  switch (amode) {
-    case A_PLAIN: return launch_am<A_PLAIN>(a, epi, stream);
-    case A_CONCAT: return launch_am<A_CONCAT>(a, epi, stream);
-    case A_CONV5: return launch_am<A_CONV5>(a, epi, stream);
+  if (amode == A_PLAIN) {
+    switch (epi) {
+      case EPI_F32: return launch_am_epi<A_PLAIN, EPI_F32>(a, stream);
+      case EPI_F16: return launch_am_epi<A_PLAIN, EPI_F16>(a, stream);
+      case EPI_SWIGLU: return launch_am_epi<A_PLAIN, EPI_SWIGLU>(a, stream);
+      case EPI_QKV: return launch_am_epi<A_PLAIN, EPI_QKV>(a, stream);
+      case EPI_RESSKIP: return launch_am_epi<A_PLAIN, EPI_RESSKIP>(a, stream);
+      case EPI_FINALSKIP: return launch_am_epi<A_PLAIN, EPI_FINALSKIP>(a, stream);
+      case EPI_DUAL: return launch_am_epi<A_PLAIN, EPI_DUAL>(a, stream);
+      default: break;
+    }
+  } else if (amode == A_CONCAT) {
+    if (epi == EPI_F32) return launch_am_epi<A_CONCAT, EPI_F32>(a, stream);
+    if (epi == EPI_F16) return launch_am_epi<A_CONCAT, EPI_F16>(a, stream);
+  } else if (amode == A_CONV5) {
+    if (epi == EPI_GATE) return launch_am_epi<A_CONV5, EPI_GATE>(a, stream);
   }
-  return hipErrorInvalidValue;
+  return hipErrorInvalidValue;  // combination not built
 }
 
 }  // namespace mit2hip

@@ -19,18 +19,18 @@ hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
 // Decode set-up for nreq requests of T tokens (branches b = 2r (cond), 2r+1 (null)
 // when cfg is on, b = r when off):
 //   x_cur[r][t][80] = x0 with rows t < P[r] zeroed,
-//   xmel16[b][t][96] = f16(x_cur) (cols 80..95 zero),
+//   xmel16[b][t][kMelPad] = f16(x_cur) (cols 80.. zero),
 //   cond16[b][t][512] = f16(cond[r]) for cond branches, 0 for null branches,
-//   mc16[b][t][0..95 | 608..799] = [prompt_x (zero pad) | style]; the
-//   cond-projection GEMM fills columns 96..607 afterwards.
+//   mc16[b][t][kMcWidth] = [prompt_x (zero pad) | . | style | 0]; the
+//   cond-projection GEMM fills columns kMcContent..kMcContent+511 afterwards.
 hipError_t launch_decode_prep(const float* x0, const float* prompt, const float* cond,
                               const float* style, const uint32_t* P, int nreq, int T, int cfg_on,
                               float* x_cur, half_t* xmel16, half_t* cond16, half_t* mc16,
                               hipStream_t s);
 
 // Estimator-step set-up for B independent branches (caller supplies every branch):
-//   xmel16[m][96] = f16(x[m]), cond16[m] = f16(cond[m]),
-//   mc16[m] = [prompt_x[m] (zero pad) | . | style[b]].
+//   xmel16[m][kMelPad] = f16(x[m]), cond16[m] = f16(cond[m]),
+//   mc16[m] = [prompt_x[m] (zero pad) | . | style[b] | 0].
 hipError_t launch_step_prep(const float* x, const float* prompt_x, const float* cond,
                             const float* style, int B, int T, half_t* xmel16, half_t* cond16,
                             half_t* mc16, hipStream_t s);

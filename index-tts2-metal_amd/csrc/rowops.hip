@@ -95,22 +95,23 @@ __global__ __launch_bounds__(256) void decode_prep_kernel(
   const uint32_t Pr = P[r];
   const size_t row = (size_t)b * T + t;
   const size_t rrow = (size_t)r * T + t;
-  for (int j = threadIdx.x; j < 96; j += blockDim.x) {
+  for (int j = threadIdx.x; j < kMelPad; j += blockDim.x) {
     float xv = 0.0f;
     if (j < 80 && (uint32_t)t >= Pr) xv = x0[rrow * 80 + j];
     if (j < 80 && is_cond) x_cur[rrow * 80 + j] = xv;
-    xmel16[row * 96 + j] = (half_t)xv;
+    xmel16[row * kMelPad + j] = (half_t)xv;
   }
   for (int j = threadIdx.x; j < 512; j += blockDim.x)
     cond16[row * 512 + j] = (half_t)(is_cond ? cond[rrow * 512 + j] : 0.0f);
   // prompt_x: the prompt frames on the first P rows of the cond branch.
-  for (int j = threadIdx.x; j < 96; j += blockDim.x) {
+  for (int j = threadIdx.x; j < kMcContent; j += blockDim.x) {
     float pv = 0.0f;
     if (is_cond && j < 80 && (uint32_t)t < Pr) pv = prompt[((size_t)r * T + t) * 80 + j];
-    mc16[row * 800 + j] = (half_t)pv;
+    mc16[row * kMcWidth + j] = (half_t)pv;
   }
-  for (int j = threadIdx.x; j < 192; j += blockDim.x)
-    mc16[row * 800 + 608 + j] = (half_t)(is_cond ? style[(size_t)r * 192 + j] : 0.0f);
+  for (int j = threadIdx.x; j < kMcWidth - kMcStyle; j += blockDim.x)
+    mc16[row * kMcWidth + kMcStyle + j] =
+        (half_t)(is_cond && j < 192 ? style[(size_t)r * 192 + j] : 0.0f);
 }
 
 hipError_t launch_decode_prep(const float* x0, const float* prompt, const float* cond,
@@ -133,13 +134,13 @@ __global__ __launch_bounds__(256) void step_prep_kernel(const float* __restrict_
   const int t = blockIdx.x;
   const int b = blockIdx.y;
   const size_t row = (size_t)b * T + t;
-  for (int j = threadIdx.x; j < 96; j += blockDim.x) {
-    xmel16[row * 96 + j] = (half_t)(j < 80 ? x[row * 80 + j] : 0.0f);
-    mc16[row * 800 + j] = (half_t)(j < 80 ? prompt_x[row * 80 + j] : 0.0f);
+  for (int j = threadIdx.x; j < kMelPad; j += blockDim.x) {
+    xmel16[row * kMelPad + j] = (half_t)(j < 80 ? x[row * 80 + j] : 0.0f);
+    mc16[row * kMcWidth + j] = (half_t)(j < 80 ? prompt_x[row * 80 + j] : 0.0f);
   }
   for (int j = threadIdx.x; j < 512; j += blockDim.x) cond16[row * 512 + j] = (half_t)cond[row * 512 + j];
-  for (int j = threadIdx.x; j < 192; j += blockDim.x)
-    mc16[row * 800 + 608 + j] = (half_t)style[(size_t)b * 192 + j];
+  for (int j = threadIdx.x; j < kMcWidth - kMcStyle; j += blockDim.x)
+    mc16[row * kMcWidth + kMcStyle + j] = (half_t)(j < 192 ? style[(size_t)b * 192 + j] : 0.0f);
 }
 
 hipError_t launch_step_prep(const float* x, const float* prompt_x, const float* cond,
@@ -200,8 +201,8 @@ __global__ __launch_bounds__(256) void conv2_euler_kernel(
       float xn = x_cur[xi] + dt * v;
       if ((uint32_t)t < Pr) xn = 0.0f;
       x_cur[xi] = xn;
-      xmel16[((size_t)bc * T + t) * 96 + n] = (half_t)xn;
-      if (cfg_on) xmel16[((size_t)(bc + 1) * T + t) * 96 + n] = (half_t)xn;
+      xmel16[((size_t)bc * T + t) * kMelPad + n] = (half_t)xn;
+      if (cfg_on) xmel16[((size_t)(bc + 1) * T + t) * kMelPad + n] = (half_t)xn;
     }
   }
 }

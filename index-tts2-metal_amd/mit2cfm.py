@@ -86,6 +86,9 @@ def lib() -> ctypes.CDLL:
                                                ctypes.POINTER(ctypes.c_uint64)]),
         "mit2cfm_synthetic_tensor_fill": (st, [u32, u64, f32, vp]),
         "mit2cfm_write_synthetic_bundle": (st, [ctypes.c_char_p, u64, f32]),
+        "mit2cfm_profile_launch": (st, [vp, i32, u32, ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_char_p)]),
         "mit2cfm_inspect_bundle": (st, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64),
                                         ctypes.POINTER(ctypes.c_uint64), u32]),
     }
@@ -305,6 +308,16 @@ class Context:
 
     def set_graph(self, on: bool) -> None:
         self._c(lib().mit2cfm_set_graph(self._h, 1 if on else 0))
+
+    def profile_launch(self, kernel: int, count: int):
+        """Enqueues `count` launches of decode kernel `kernel` on self.stream (no sync);
+        returns (name, flops per launch, HBM bytes per launch)."""
+        f = ctypes.c_double()
+        b = ctypes.c_double()
+        n = ctypes.c_char_p()
+        self._c(lib().mit2cfm_profile_launch(self._h, kernel, count, ctypes.byref(f), ctypes.byref(b),
+                                             ctypes.byref(n)))
+        return n.value.decode(), f.value, b.value
 
     # -- stages (parity harness)
     def timestep_embedder(self, t: float, which: int) -> np.ndarray:

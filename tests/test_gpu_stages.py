@@ -48,8 +48,8 @@ def f16r(a):
 
 # ------------------------------------------------------------------ GEMM
 HOT_SHAPES = [  # (N, K) of every GEMM in one estimator step
-    (512, 512), (512, 96), (512, 800), (1536, 512), (3072, 512), (512, 1536), (512, 1024),
-    (512, 608), (1024, 512), (1024, 2560), (512, 512),
+    (512, 512), (512, 128), (512, 896), (1536, 512), (3072, 512), (512, 1536), (512, 1024),
+    (512, 640), (1024, 512), (1024, 2560), (512, 512),
 ]
 
 
