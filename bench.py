@@ -55,6 +55,8 @@ def parse():
     p.add_argument("--kernel-launches", type=int, default=200)
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, available cores)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--calib-mib", type=int, default=256,
+                   help="size of the counter-calibration copy (0 = skip)")
     return p.parse_args()
 
 
@@ -184,6 +186,20 @@ def main():
     roof.update({"traffic": traffic_from_profiles(name, T), "kernel": name,
                  "avg_launch_us": round(k_ms * 1e3, 2), "algorithmic_flops": kflops,
                  "algorithmic_bytes": kbytes})
+
+    # Counter calibration: a plain streaming copy of known size (reads and
+    # writes calib_mib MiB once each).  Under rocprofv3 --pmc FETCH_SIZE /
+    # WRITE_SIZE its readings give the KiB-per-byte factor that turns the
+    # dominant kernel's readings into HBM bytes.
+    if a.calib_mib > 0:
+        n = a.calib_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     # Host-pointer decode (PCIe-inclusive; reported, never the headline value).
     ctx.decode(x0, prompt, cond, style, S, cfg)
