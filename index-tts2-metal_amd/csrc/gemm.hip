@@ -118,6 +118,47 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
   const int lg = lane >> 4;
   const int KT = p.K / SK;
 
+  // Output ownership.  The MFMA is issued with W as its first operand, so the
+  // accumulator is C^T: lane (lr, lg) of block (i, j) holds the four
+  // consecutive columns n = col_base + 16 j + 4 lg + r (r = 0..3) of row
+  // m = row_base + 16 i + lr.  Every epilogue access is then a 16-byte
+  // (fp32) or 8-byte (f16) vector per lane.
+  const int row_base = m0 + wm * (BM / 2) + lr;
+  const int col_base = n0 + wn * (BN / 2) + 4 * lg;
+
+  // Epilogue operands that do not depend on the product are fetched now, so
+  // their latency hides behind the K loop.
+  constexpr bool kPreA = EPI == EPI_F32 || EPI == EPI_RESSKIP || EPI == EPI_FINALSKIP;
+  constexpr bool kPreB = EPI == EPI_FINALSKIP;
+  float4 pre_a[kPreA ? MI : 1][kPreA ? NI : 1];
+  float4 pre_b[kPreB ? MI : 1][kPreB ? NI : 1];
+  if constexpr (kPreA) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = row_base + 16 * i;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int n = col_base + 16 * j;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m < p.M) {
+          if constexpr (EPI == EPI_F32) {
+            if (p.res) v = *reinterpret_cast<const float4*>(p.res + (size_t)m * p.ldres + n);
+          } else if constexpr (EPI == EPI_RESSKIP) {
+            if (n < 512) v = *reinterpret_cast<const float4*>(p.C32 + (size_t)m * p.ldc32 + n);
+            else if (p.flag) v = *reinterpret_cast<const float4*>(p.C32b + (size_t)m * p.ldc32b + (n - 512));
+          } else {
+            v = *reinterpret_cast<const float4*>(p.C32b + (size_t)m * p.ldc32b + n);
+          }
+        }
+        pre_a[i][j] = v;
+        if constexpr (kPreB) {
+          pre_b[i][j] = m < p.M ? *reinterpret_cast<const float4*>(p.rp + (size_t)m * 512 + n)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+  }
+
   auto swz = [](int row) { return CPR >= 16 ? (row & 15) : ((row >> 1) & 7); };
 
   auto a_src = [&](int m, int k) -> const half_t* {
@@ -187,25 +228,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < NI; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
     }
   };
 
-  // Pipeline: every steady-state iteration issues one stage and waits for the
-  // oldest, so NST-1 stages stay in flight.  The body is branch-free (an
-  // issue past the last stage repeats stage KT-1, an L2 hit, into a buffer
-  // that is not read again), which keeps the compiler from adding waits of
-  // its own; the last KT % NST stages are resident when the loop exits.
+  // Pipeline, one barrier per stage.  At the top of stage kt this wave waits
+  // for its own share of stage kt (NST-2 younger stages may stay in flight);
+  // the barrier then says every wave's share has landed AND every wave has
+  // finished reading stage kt-1, whose buffer is refilled with stage
+  // kt+NST-1 before stage kt is computed.  The body is branch-free (an issue
+  // past the last stage repeats stage KT-1, an L2 hit, into a buffer that is
+  // not read again), which keeps the compiler from adding waits of its own;
+  // the last KT % NST stages are resident when the loop exits.
   static_for<0, NST - 1>([&](auto st) { issue(st, min((int)decltype(st)::value, KT - 1)); });
   int kt0 = 0;
   for (; kt0 + NST <= KT; kt0 += NST) {
     static_for<0, NST>([&](auto st) {
       constexpr int s = decltype(st)::value;
-      wait_lgkmcnt0();               // this wave's reads of the previous stage are done,
-      __builtin_amdgcn_s_barrier();  // and every wave's: the buffer reloaded next is free
+      wait_vmcnt<L * (NST - 2)>();   // this wave's share of stage kt0+s has landed
+      wait_lgkmcnt0();               // this wave's reads of stage kt0+s-1 have returned
+      __builtin_amdgcn_s_barrier();  // ... for every wave
       issue(std::integral_constant<int, (s + NST - 1) % NST>{}, min(kt0 + s + NST - 1, KT - 1));
-      wait_vmcnt<L * (NST - 1)>();   // this wave's share of stage kt0+s has landed
-      __builtin_amdgcn_s_barrier();  // ... and every other wave's
       compute(st);
     });
   }
@@ -216,53 +259,65 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
   });
 
   // ---------------------------------------------------------------- epilogue
-  const int row_base = m0 + wm * (BM / 2) + lg * 4;
-  const int col_base = n0 + wn * (BN / 2);
+  auto bias4 = [&](int n) -> float4 {
+    return p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto st16 = [](half_t* dst, float a, float b, float c, float d) {
+    half4 h;
+    h[0] = (half_t)a; h[1] = (half_t)b; h[2] = (half_t)c; h[3] = (half_t)d;
+    *reinterpret_cast<half4*>(dst) = h;
+  };
 
   if constexpr (EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_DUAL || EPI == EPI_RESSKIP ||
                 EPI == EPI_FINALSKIP) {
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
+    for (int j = 0; j < NI; ++j) {
+      const int n = col_base + 16 * j;
+      const float4 bv = bias4(n);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = row_base + i * 16 + r;
+      for (int i = 0; i < MI; ++i) {
+        const int m = row_base + 16 * i;
         if (m >= p.M) continue;
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const int n = col_base + j * 16 + lr;
-          float v = acc[i][j][r];
-          if (p.bias) v += p.bias[n];
-          if constexpr (EPI == EPI_F32) {
-            if (p.res) v = p.res[(size_t)m * p.ldres + n] + v;
-            p.C32[(size_t)m * p.ldc32 + n] = v;
-            if (p.C16) p.C16[(size_t)m * p.ldc16 + n] = (half_t)v;
-          } else if constexpr (EPI == EPI_F16) {
-            p.C16[(size_t)m * p.ldc16 + n] = (half_t)v;
-          } else if constexpr (EPI == EPI_DUAL) {
-            const int half_n = p.N >> 1;
-            if (n < half_n) {
-              p.C32[(size_t)m * p.ldc32 + n] = v;
-              p.C16[(size_t)m * p.ldc16 + n] = (half_t)v;
-            } else {
-              p.C32b[(size_t)m * p.ldc32b + (n - half_n)] = v;
-            }
-          } else if constexpr (EPI == EPI_RESSKIP) {
-            // v is the res_skip conv output (bias included).
-            const float mk = p.mask[m] ? 1.0f : 0.0f;
-            if (n < 512) {
-              float* xs = p.C32 + (size_t)m * p.ldc32 + n;
-              const float xn = (*xs + v) * mk;
-              *xs = xn;
-              p.C16[(size_t)m * p.ldc16 + n] = (half_t)xn;
-            } else {
-              float* os = p.C32b + (size_t)m * p.ldc32b + (n - 512);
-              *os = p.flag ? (*os + v) : v;
-            }
-          } else {  // EPI_FINALSKIP: out = (out + rs) * mask; final_in = out + rp
-            const float mk = p.mask[m] ? 1.0f : 0.0f;
-            const float o = (p.C32b[(size_t)m * p.ldc32b + n] + v) * mk;
-            p.C32[(size_t)m * p.ldc32 + n] = o + p.rp[(size_t)m * 512 + n];
+        float4 v = make_float4(acc[i][j][0] + bv.x, acc[i][j][1] + bv.y, acc[i][j][2] + bv.z,
+                               acc[i][j][3] + bv.w);
+        if constexpr (EPI == EPI_F32) {
+          if (p.res) {
+            const float4 r = pre_a[i][j];
+            v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
           }
+          *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
+          if (p.C16) st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
+        } else if constexpr (EPI == EPI_F16) {
+          st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
+        } else if constexpr (EPI == EPI_DUAL) {
+          const int half_n = p.N >> 1;
+          if (n < half_n) {
+            *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
+            st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
+          } else {
+            *reinterpret_cast<float4*>(p.C32b + (size_t)m * p.ldc32b + (n - half_n)) = v;
+          }
+        } else if constexpr (EPI == EPI_RESSKIP) {
+          // v is the res_skip conv output (bias included).
+          const float mk = p.mask[m] ? 1.0f : 0.0f;
+          const float4 o = pre_a[i][j];
+          if (n < 512) {
+            const float4 xn = make_float4((o.x + v.x) * mk, (o.y + v.y) * mk, (o.z + v.z) * mk,
+                                          (o.w + v.w) * mk);
+            *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = xn;
+            st16(p.C16 + (size_t)m * p.ldc16 + n, xn.x, xn.y, xn.z, xn.w);
+          } else {
+            // pre_a is zero when the skip accumulator starts at zero (flag 0)
+            *reinterpret_cast<float4*>(p.C32b + (size_t)m * p.ldc32b + (n - 512)) =
+                make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+          }
+        } else {  // EPI_FINALSKIP: out = (out + rs) * mask; final_in = out + rp
+          const float mk = p.mask[m] ? 1.0f : 0.0f;
+          const float4 o = pre_a[i][j];
+          const float4 r = pre_b[i][j];
+          *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) =
+              make_float4((o.x + v.x) * mk + r.x, (o.y + v.y) * mk + r.y, (o.z + v.z) * mk + r.z,
+                          (o.w + v.w) * mk + r.w);
         }
       }
     }
@@ -272,26 +327,26 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
         // V tile = one head (64 channels) x BM tokens.  Transpose through LDS
         // so that V^T[d][t] is written by consecutive lanes at consecutive t.
         static_assert(BN == 64, "a v tile must be exactly one head");
+        static_assert(SK >= 64, "the V^T staging tile reuses the first A stage buffer");
         half_t* st = sA0;  // [64 d][BM rows], free once every wave is past its last MFMA
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
+        // Blocks (0, 1) of this wave hold the even / odd channels of its
+        // 32-channel group (v rows are permuted like the q and k rows):
+        // channel d = 32 wn + 2 (4 lg + r) (+1 for the odd block).
+        const float4 be = bias4(col_base);
+        const float4 bo = bias4(col_base + 16);
+        const float bev[4] = {be.x, be.y, be.z, be.w};
+        const float bov[4] = {bo.x, bo.y, bo.z, bo.w};
 #pragma unroll
-        for (int q = 0; q < NI / 2; ++q) {
-          // Blocks (2q, 2q+1) hold the even/odd channels of the RoPE pairing
-          // (the v rows are permuted like the q and k rows).
-          const int ce = col_base + q * 32;
-          const int d = (ce & 63) + 2 * lr;  // channel within the head
-          const float be = p.bias ? p.bias[ce + lr] : 0.0f;
-          const float bo = p.bias ? p.bias[ce + 16 + lr] : 0.0f;
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-          for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int rl = wm * (BM / 2) + i * 16 + lg * 4 + r;
-              st[d * BM + rl] = (half_t)(acc[i][2 * q][r] + be);
-              st[(d + 1) * BM + rl] = (half_t)(acc[i][2 * q + 1][r] + bo);
-            }
-        }
+          for (int r = 0; r < 4; ++r) {
+            const int rl = wm * (BM / 2) + i * 16 + lr;
+            const int d = 32 * wn + 2 * (4 * lg + r);
+            st[d * BM + rl] = (half_t)(acc[i][0][r] + bev[r]);
+            st[(d + 1) * BM + rl] = (half_t)(acc[i][1][r] + bov[r]);
+          }
         wait_lgkmcnt0();  // this wave's stores have landed before the barrier releases readers
         __builtin_amdgcn_s_barrier();
         const int hh = (n0 - 1024) >> 6;
@@ -309,50 +364,58 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
         return;
       }
     }
-    // Paired epilogues: MFMA blocks (2q, 2q+1) of a wave hold, in the same
-    // lane, the two operands for output channel c = 16*group + lr.
+    // Paired epilogues: blocks (2q, 2q+1) of a wave hold, in the same lane and
+    // slot r, the two operands of output channel c = 16 group + 4 lg + r.
     static_assert(NI % 2 == 0, "paired epilogue needs an even block count");
 #pragma unroll
     for (int q = 0; q < NI / 2; ++q) {
-      const int ce = col_base + q * 32;  // GEMM column of the even block start
-      const int group = ce >> 5;
-      const float be = p.bias ? p.bias[ce + lr] : 0.0f;
-      const float bo = p.bias ? p.bias[ce + 16 + lr] : 0.0f;
+      const int ce = col_base + q * 32;  // GEMM column of this lane's even-block values
+      const int group = (ce - 4 * lg) >> 5;
+      const float4 be = bias4(ce);
+      const float4 bo = bias4(ce + 16);
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
+        const int m = row_base + 16 * i;
+        if (m >= p.M) continue;
+        const float ve[4] = {acc[i][2 * q][0] + be.x, acc[i][2 * q][1] + be.y,
+                             acc[i][2 * q][2] + be.z, acc[i][2 * q][3] + be.w};
+        const float vo[4] = {acc[i][2 * q + 1][0] + bo.x, acc[i][2 * q + 1][1] + bo.y,
+                             acc[i][2 * q + 1][2] + bo.z, acc[i][2 * q + 1][3] + bo.w};
+        if constexpr (EPI == EPI_SWIGLU) {
+          const int c = group * 16 + 4 * lg;
+          float y[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = row_base + i * 16 + r;
-          if (m >= p.M) continue;
-          const float ve = acc[i][2 * q][r] + be;
-          const float vo = acc[i][2 * q + 1][r] + bo;
-          if constexpr (EPI == EPI_SWIGLU) {
-            const int c = group * 16 + lr;
-            p.C16[(size_t)m * p.ldc16 + c] = (half_t)((ve / (1.0f + __expf(-ve))) * vo);
-          } else if constexpr (EPI == EPI_GATE) {
-            const int c = group * 16 + lr;
-            const float a = ve + p.cond[c];
-            const float b = vo + p.cond[512 + c];
-            p.C16[(size_t)m * p.ldc16 + c] = (half_t)(tanh_sat(a) * sigmoid_f(b));
-          } else {  // EPI_QKV, q and k sections (v tiles are written below)
-            const int o = group * 32 + 2 * lr;  // original column of the even element
-            const int sec = o >> 9;             // 0 = q, 1 = k
-            const int hh = (o & 511) >> 6;
-            const int d = o & 63;
-            const int b = m / p.T;
-            const int t = m - b * p.T;
-            const size_t head = (size_t)b * 8 + hh;
-            const float2 cs = p.rope[t * 32 + (d >> 1)];
-            float re = ve * cs.x - vo * cs.y;
-            float ro = vo * cs.x + ve * cs.y;
-            if (sec == 0) {
-              re *= 0.125f;  // 1/sqrt(64): a power of two, so the scaling is exact
-              ro *= 0.125f;
-            }
-            half_t* dst = (sec == 0 ? p.q : p.k) + (head * p.Tpad + t) * 64 + d;
-            half2v pr = {(half_t)re, (half_t)ro};
-            *reinterpret_cast<half2v*>(dst) = pr;
+          for (int r = 0; r < 4; ++r) y[r] = (ve[r] / (1.0f + __expf(-ve[r]))) * vo[r];
+          st16(p.C16 + (size_t)m * p.ldc16 + c, y[0], y[1], y[2], y[3]);
+        } else if constexpr (EPI == EPI_GATE) {
+          const int c = group * 16 + 4 * lg;
+          const float4 ca = *reinterpret_cast<const float4*>(p.cond + c);
+          const float4 cb = *reinterpret_cast<const float4*>(p.cond + 512 + c);
+          const float cav[4] = {ca.x, ca.y, ca.z, ca.w};
+          const float cbv[4] = {cb.x, cb.y, cb.z, cb.w};
+          float y[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = tanh_sat(ve[r] + cav[r]) * sigmoid_f(vo[r] + cbv[r]);
+          st16(p.C16 + (size_t)m * p.ldc16 + c, y[0], y[1], y[2], y[3]);
+        } else {  // EPI_QKV, q and k sections (v tiles are written above)
+          const int o = group * 32 + 8 * lg;  // original column of the first even element
+          const int sec = o >> 9;             // 0 = q, 1 = k
+          const int hh = (o & 511) >> 6;
+          const int d0 = o & 63;
+          const int b = m / p.T;
+          const int t = m - b * p.T;
+          const size_t head = (size_t)b * 8 + hh;
+          const float2* cs = p.rope + t * 32 + (d0 >> 1);
+          const float sc = sec == 0 ? 0.125f : 1.0f;  // 1/sqrt(64): a power of two, exact
+          half8 h;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float2 c2 = cs[r];
+            h[2 * r] = (half_t)((ve[r] * c2.x - vo[r] * c2.y) * sc);
+            h[2 * r + 1] = (half_t)((vo[r] * c2.x + ve[r] * c2.y) * sc);
           }
+          half_t* dst = (sec == 0 ? p.q : p.k) + (head * p.Tpad + t) * 64 + d0;
+          *reinterpret_cast<half8*>(dst) = h;
         }
       }
     }
@@ -360,12 +423,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
 }
 
 // Chooses the XCD rectangle split minimising the bytes the XCDs re-read:
-// A (M x K) is read once per rectangle column, W (N x K) once per row.
-static TileMap make_tile_map(int M, int N, int K, int BM, int BN) {
+// A (M x a_cols distinct values; a_cols < K for the k=5 conv, whose taps
+// re-read the same rows) is read once per rectangle column, W (N x K) once
+// per rectangle row.
+static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
   TileMap t;
   t.nM = (M + BM - 1) / BM;
   t.nN = N / BN;
-  const double a_bytes = 2.0 * M * K, w_bytes = 2.0 * N * K;
+  const double a_bytes = 2.0 * M * a_cols, w_bytes = 2.0 * N * K;
   const int opts[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
   double best = 1e300;
   t.Xm = 8;
@@ -397,7 +462,7 @@ static TileMap make_tile_map(int M, int N, int K, int BM, int BN) {
 
 template <int BM, int BN, int SK, int NST, int AM, int EPI>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
-  const TileMap tm = make_tile_map(a.M, a.N, a.K, BM, BN);
+  const TileMap tm = make_tile_map(a.M, a.N, a.K, AM == A_CONV5 ? a.conv_c : a.K, BM, BN);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI>), dim3(8 * tm.per_xcd), dim3(256), 0, s,
                      a, tm);
   return hipGetLastError();
