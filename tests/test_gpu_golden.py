@@ -134,3 +134,101 @@ def test_config2_batched_three_requests_properties(mit2, golden_ctx):
           flush=True)
     assert np.array_equal(out[0, :T], single)
     assert np.isfinite(out).all()
+
+
+def _make_golden():
+    """tests/golden/make_golden.py as a module (shared input recipes)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("make_golden", GOLDEN / "make_golden.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_config4_long_form_velocity(mit2, orc, golden_ctx):
+    """T=3000 (P=258): the CFG-pair velocity at t=0 on x0 and at step 12 of 25
+    on a mid-flow state, against the oracle (Tpad > 2048 takes the one-group
+    attention path)."""
+    mg = _make_golden()
+    meta, ref = load("config4")
+    T, P, steps, cfg = meta["T"], meta["P"], meta["steps"], meta["cfg"]
+    x0, prompt, cond, style = inputs(mit2, T, P, meta["seed"])
+    mask = np.ones((2, T), np.uint32)
+    tm = step_time(meta["mid_step"], steps)
+    x = x0.copy()
+    x[:P] = 0
+    for key, state, t in (("v_t0", x, 0.0), ("v_mid", mg.mid_state(x0, T, P, meta["seed"], tm), tm)):
+        X, PX, C, S = branches(state, prompt, cond, style, T, P)
+        d = golden_ctx.estimator_step(X, PX, C, S, mask, t)
+        v = np.float32(1 + cfg) * d[0] - np.float32(cfg) * d[1]
+        err = orc.rel_l2(v, ref[key])
+        print(f"config4 {key} (t={t:.4f}): velocity rel-L2 {err:.3e}", flush=True)
+        assert err <= VEL_TOL
+
+
+def test_config4_long_form_decode_properties(mit2, golden_ctx):
+    """The full 25-step T=3000 decode: finite, prompt rows zero, repeatable bit
+    for bit, and unchanged when batched with a shorter request."""
+    meta, _ = load("config4")
+    T, P, steps, cfg = meta["T"], meta["P"], meta["steps"], meta["cfg"]
+    x0, prompt, cond, style = inputs(mit2, T, P, meta["seed"])
+    a = golden_ctx.decode(x0, prompt, cond, style, steps, cfg)
+    b = golden_ctx.decode(x0, prompt, cond, style, steps, cfg)
+    assert np.isfinite(a).all()
+    assert np.all(a[:P] == 0)
+    assert np.array_equal(a, b)
+    X0 = np.zeros((2, T, 80), np.float32)
+    PR = np.zeros((2, T, 80), np.float32)
+    CO = np.zeros((2, T, 512), np.float32)
+    ST = np.zeros((2, 192), np.float32)
+    X0[0], PR[0, :P], CO[0], ST[0] = x0, prompt, cond, style
+    s0, s1, s2, s3 = inputs(mit2, 900, 100, 77)
+    X0[1, :900], PR[1, :100], CO[1, :900], ST[1] = s0, s1, s2, s3
+    out = golden_ctx.decode_batched([T, 900], [P, 100], X0, PR, CO, ST, steps, cfg)
+    assert np.array_equal(out[0], a)
+
+
+def test_config5_padded_batch_velocity(mit2, orc, golden_ctx):
+    """8 right-padded requests (P=258, T_max=1348): the masked CFG-pair velocity
+    at t=0 of the shortest and the longest request at the padded length, run as
+    one B=4 forward, against the oracle's masked estimator."""
+    mg = _make_golden()
+    meta, ref = load("config5")
+    c = dict(meta)
+    toks, tmax, X0, PR, CO, ST = mg.padded_requests(c)
+    assert toks == meta["tokens"] and tmax == meta["t_max"]
+    P, cfg = meta["P"], meta["cfg"]
+    Xs, PXs, Cs, Ss, Ms = [], [], [], [], []
+    for r in meta["picked"]:
+        x = X0[r].copy()
+        x[:P] = 0
+        X, PX, C, S = branches(x, PR[r][:P], CO[r], ST[r], tmax, P)
+        m = (np.arange(tmax) < toks[r]).astype(np.uint32)
+        Xs.append(X); PXs.append(PX); Cs.append(C); Ss.append(S); Ms += [m, m]
+    d = golden_ctx.estimator_step(np.concatenate(Xs), np.concatenate(PXs), np.concatenate(Cs),
+                                  np.concatenate(Ss), np.stack(Ms), 0.0)
+    for i, r in enumerate(meta["picked"]):
+        v = np.float32(1 + cfg) * d[2 * i] - np.float32(cfg) * d[2 * i + 1]
+        err = orc.rel_l2(v[:toks[r]], ref[f"v_t0_req{r}"])
+        print(f"config5 request {r} (T={toks[r]}): velocity rel-L2 {err:.3e}", flush=True)
+        assert err <= VEL_TOL
+
+
+def test_config5_padded_batch_decode(mit2, golden_ctx):
+    """The B=16 batched decode (16 steps): finite, prompt rows zero, and each
+    checked request equal bit for bit to its own decode at the padded length."""
+    mg = _make_golden()
+    meta, _ = load("config5")
+    toks, tmax, X0, PR, CO, ST = mg.padded_requests(dict(meta))
+    P, steps, cfg = meta["P"], meta["steps"], meta["cfg"]
+    n = len(toks)
+    out = golden_ctx.decode_batched(toks, [P] * n, X0, PR, CO, ST, steps, cfg)
+    assert out.shape == (n, tmax, 80)
+    for r in range(n):
+        assert np.isfinite(out[r, :toks[r]]).all()
+        assert np.all(out[r, :P] == 0)
+    for r in meta["picked"]:
+        one = golden_ctx.decode_batched(toks[r:r + 1], [P], X0[r:r + 1], PR[r:r + 1], CO[r:r + 1],
+                                        ST[r:r + 1], steps, cfg)
+        assert np.array_equal(one[0], out[r])
