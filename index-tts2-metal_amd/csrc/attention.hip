@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256 * SPLIT) void attention_kernel(const half_t* __
                                                         const uint32_t* __restrict__ mask,
                                                         half_t* __restrict__ O, int T, int Tpad) {
   static_assert(NBUF >= 2 && NBUF <= 4, "2..4 tile buffers");
-  static_assert(SPLIT == 1 || SPLIT == 2, "key split");
+  static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "key split");
   // One __shared__ object per buffer (K, V^T, and one mask copy per wave);
   // each key group g has its own region inside every buffer.
   constexpr int KV = 64 * 64 * SPLIT;
@@ -78,8 +78,10 @@ __global__ __launch_bounds__(256 * SPLIT) void attention_kernel(const half_t* __
   __shared__ __attribute__((aligned(1024))) uint32_t sM1[4 * 64 * SPLIT];
   __shared__ __attribute__((aligned(1024))) uint32_t sM2[NBUF > 2 ? 4 * 64 * SPLIT : 4];
   __shared__ __attribute__((aligned(1024))) uint32_t sM3[NBUF > 3 ? 4 * 64 * SPLIT : 4];
-  // (m, l, O) of key group 1 for the merge: 4 waves x 64 lanes x 18 floats.
-  __shared__ __attribute__((aligned(1024))) float sPark[SPLIT > 1 ? 4 * 64 * 18 : 4];
+  // (m, l, O) of key group 1 for the two-group merge: 4 waves x 64 lanes x
+  // 18 floats.  With four groups, groups 1..3 park in the K0 / V0 / K1 tile
+  // buffers instead (each holds 32 KB then), which are free after the loop.
+  __shared__ __attribute__((aligned(1024))) float sPark[SPLIT == 2 ? 4 * 64 * 18 : 4];
   auto bufK = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
     if constexpr (s == 0) return sK0; else if constexpr (s == 1) return sK1;
@@ -254,11 +256,23 @@ __global__ __launch_bounds__(256 * SPLIT) void attention_kernel(const half_t* __
   l_run += __shfl_xor(l_run, 16, kWave);
   l_run += __shfl_xor(l_run, 32, kWave);
   if constexpr (SPLIT > 1) {
-    // Merge the key groups: group 1 parks (m, l, O) in LDS; group 0
-    // rescales both parts to the common max.
-    float* park = sPark;
+    // Merge the key groups: groups 1.. park (m, l, O) in LDS; group 0
+    // rescales every part to the common max.
+    auto park_of = [&](int g) -> float* {
+      if constexpr (SPLIT == 2) {
+        return sPark + (wave * 64 + lane) * 18;
+      } else {
+        float* base = reinterpret_cast<float*>(g == 1 ? sK0 : g == 2 ? sV0 : sK1);
+        return base + (wave * 64 + lane) * 18;
+      }
+    };
+    if constexpr (SPLIT == 4) {
+      // every wave's last tile reads are done before tile buffers are reused
+      attn_wait_lgkmcnt0();
+      __syncthreads();
+    }
     if (grp > 0) {
-      float* p = park + (((grp - 1) * 4 + wave) * 64 + lane) * 18;
+      float* p = park_of(grp);
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -271,7 +285,7 @@ __global__ __launch_bounds__(256 * SPLIT) void attention_kernel(const half_t* __
     if (grp > 0) return;
     float mstar = m_run;
 #pragma unroll
-    for (int g = 1; g < SPLIT; ++g) mstar = fmaxf(mstar, park[(((g - 1) * 4 + wave) * 64 + lane) * 18 + 16]);
+    for (int g = 1; g < SPLIT; ++g) mstar = fmaxf(mstar, park_of(g)[16]);
     const float mref = mstar == -INFINITY ? 0.0f : mstar;
     const float w0 = __expf(m_run - mref);
     l_run *= w0;
@@ -279,7 +293,7 @@ __global__ __launch_bounds__(256 * SPLIT) void attention_kernel(const half_t* __
     for (int db = 0; db < 4; ++db) o[db] *= w0;
 #pragma unroll
     for (int g = 1; g < SPLIT; ++g) {
-      const float* p = park + (((g - 1) * 4 + wave) * 64 + lane) * 18;
+      const float* p = park_of(g);
       const float wg = __expf(p[16] - mref);
       l_run += wg * p[17];
 #pragma unroll
@@ -309,10 +323,11 @@ hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             hipStream_t stream) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
   dim3 grid((T + 63) / 64, 8, B);
-  // Short sequences give few query tiles and leave most SIMDs with one wave:
-  // split the keys of each workgroup over two wave groups.  The choice depends
-  // on the sequence length only, never on the batch, so a request's output
-  // does not depend on what it is batched with.
+  // Short and medium sequences give few query tiles and leave most SIMDs with
+  // one wave: split the keys of each workgroup over two wave groups (a
+  // four-group split, also built, measured slower at T = 860 on MI355X).
+  // The choice depends on the sequence length only, never on the batch, so a
+  // request's output does not depend on what it is batched with.
   if (Tpad <= kAttnSplitMaxTpad)
     hipLaunchKernelGGL((attention_kernel<kAttnBuffers, 2>), grid, dim3(512), 0, stream, Q, K, Vt,
                        mask, O, T, Tpad);

@@ -111,9 +111,10 @@ class Engine {
   void ensure_workspace(int B, int T, int S, int nreq);
   void ensure_rope(int T);
   void enqueue_tables(const float* tvals_dev, int S);
-  void enqueue_layer(int l, int B, int T, const float* tab, float* cur, float* hbuf,
-                     const half_t* skip16, half_t* out16);
-  void enqueue_transformer(int B, int T, const float* tab);
+  void enqueue_norm_bias(int S);
+  void enqueue_layer(int l, int B, int T, const float* tab, const float* nbq, const float* nbw,
+                     float* cur, float* hbuf, const half_t* skip16, half_t* out16);
+  void enqueue_transformer(int B, int T, const float* tab, const float* nbq, const float* nbw);
   void enqueue_estimator(int B, int T, int step_slot);
   void enqueue_decode(const float* x0, const float* prompt, const float* cond, const float* style,
                       int nreq, int T, int steps, float cfg, float* vtrace);

@@ -219,6 +219,9 @@ struct Workspace {
   float* t1;
   float* t2;
   float* tab;
+  float* ssq;   // [R][kSsqParts] partial row sums of squares (folded AdaRMSNorm)
+  float* nbq;   // [S][13][1536] folded attention-norm column bias (ab . Wqkv^T)
+  float* nbw;   // [S][13][3072] folded ffn-norm column bias (ab . W13^T)
   // staging for host-pointer entry points
   float* in_x;
   float* in_prompt;
@@ -424,6 +427,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   f((size_t)cT * 64);
   f(cS); f((size_t)cS * 256); f((size_t)cS * 512); f((size_t)cS * 512); f((size_t)cS * 512);
   f((size_t)cS * kTcondPerStep);
+  f(r * kSsqParts); f((size_t)cS * 13 * 1536); f((size_t)cS * 13 * 3072);
   f(r * 80); f(r * 80); f(r * 512); f((size_t)cB * 192); f(r * 80); f(r * 80);
   f(r * 1024); f(r * 1024); f(r * 1024);
   bytes += 64 * 256;
@@ -464,6 +468,9 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   ws.t1 = F((size_t)cS * 512);
   ws.t2 = F((size_t)cS * 512);
   ws.tab = F((size_t)cS * kTcondPerStep);
+  ws.ssq = F(r * kSsqParts);
+  ws.nbq = F((size_t)cS * 13 * 1536);
+  ws.nbw = F((size_t)cS * 13 * 3072);
   ws.in_x = F(r * 80);
   ws.in_prompt = F(r * 80);
   ws.in_cond = F(r * 512);
@@ -518,33 +525,60 @@ void Engine::enqueue_tables(const float* tvals_dev, int S) {
                              kTcondPerStep, stream_));
   HIP_OK(launch_linear_small(ws.t2, S, 512, W.wnc_w, W.wnc_b, 8192, 0, 0, ws.tab + kWnCondOff,
                              kTcondPerStep, stream_));
+  enqueue_norm_bias(S);
+}
+
+// Column biases of the folded AdaRMSNorms (ab . W^T) for every layer and
+// step slot of ws.tab.
+void Engine::enqueue_norm_bias(int S) {
+  Weights& W = *w_;
+  Workspace& ws = *ws_;
+  for (int l = 0; l < 13; ++l) {
+    HIP_OK(launch_norm_bias(ws.tab + l * 1024 + 512, kTcondPerStep, S, W.qkv_w[l], 1536,
+                            ws.nbq + l * 1536, 13 * 1536, stream_));
+    HIP_OK(launch_norm_bias(ws.tab + (13 + l) * 1024 + 512, kTcondPerStep, S, W.w13_w[l], 3072,
+                            ws.nbw + l * 3072, 13 * 3072, stream_));
+  }
 }
 
 // One transformer block (dit_cfm_bigvgan.cpp:816-832 / pass version :1901-1996):
 //   [l > 6] x = skip_in([x | skip]);  h = x + wo . Attn(RoPE(wqkv . AdaRMS(x)));
 //   out = h + w2 . SwiGLU(w13 . AdaRMS(h)).
-// cur holds x on entry and out on exit (fp32); x16 must hold f16(x) when l > 6;
-// out16 receives f16(out).
-void Engine::enqueue_layer(int l, int B, int T, const float* tab, float* cur, float* hbuf,
-                           const half_t* skip16, half_t* out16) {
+// Both AdaRMSNorms are folded into GEMM pairs (see GemmArgs): the GEMM that
+// produces a normed row block also writes ws.n16 = f16(x * aw * gamma) and
+// the row's partial sums of squares ws.ssq; the QKV / w13 GEMM scales by
+// rs and adds ab . W^T (nbq / nbw, this step's slot).
+// cur holds x on entry and out on exit (fp32).  On entry ws.n16 / ws.ssq
+// hold block l's attention-norm operand when l <= 6 (written by the merge
+// GEMM or block l-1); x16 must hold f16(x) when l > 6.  out16 receives
+// f16(out); for l < 6 the w2 GEMM also leaves block l+1's operand.
+void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* nbq,
+                           const float* nbw, float* cur, float* hbuf, const half_t* skip16,
+                           half_t* out16) {
   Weights& W = *w_;
   Workspace& ws = *ws_;
   hipStream_t s = stream_;
   const int R = B * T;
   const int Tpad = (T + 63) / 64 * 64;
+  auto norm_out = [&](GemmArgs& g, int norm_id) {
+    g.C16s = ws.n16; g.ldc16s = 512;
+    g.sc_a = tab + norm_id * 1024; g.sc_g = W.gamma[norm_id];
+    g.ssq_out = ws.ssq;
+  };
   if (l > 6) {
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 1024; g.K1 = 512;
     g.A = ws.x16; g.lda = 512; g.A2 = skip16; g.lda2 = 512;
     g.W = W.si_w[l]; g.ldw = 1024; g.bias = W.si_b[l];
     g.C32 = cur; g.ldc32 = 512;
+    norm_out(g, l);
     HIP_OK(launch_gemm(g, A_CONCAT, EPI_F32, s));
   }
-  HIP_OK(launch_adarms(cur, W.gamma[l], tab + l * 1024, tab + l * 1024 + 512, ws.n16, R, s));
   {
     GemmArgs g;
     g.M = R; g.N = 1536; g.K = 512; g.A = ws.n16; g.lda = 512;
     g.W = W.qkv_w[l]; g.ldw = 512; g.T = T;
+    g.bias = nbq + l * 1536; g.ssq_in = ws.ssq;
     g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, s));
   }
@@ -554,14 +588,14 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, float* cur, fl
     g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
     g.W = W.wo_w[l]; g.ldw = 512; g.res = cur; g.ldres = 512;
     g.C32 = hbuf; g.ldc32 = 512;
+    norm_out(g, 13 + l);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
   }
-  HIP_OK(launch_adarms(hbuf, W.gamma[13 + l], tab + (13 + l) * 1024, tab + (13 + l) * 1024 + 512,
-                       ws.n16, R, s));
   {
     GemmArgs g;
     g.M = R; g.N = 3072; g.K = 512; g.A = ws.n16; g.lda = 512;
     g.W = W.w13_w[l]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = 1536;
+    g.bias = nbw + l * 3072; g.ssq_in = ws.ssq;
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, s));
   }
   {
@@ -569,18 +603,21 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, float* cur, fl
     g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = 1536;
     g.W = W.w2_w[l]; g.ldw = 1536; g.res = hbuf; g.ldres = 512;
     g.C32 = cur; g.ldc32 = 512; g.C16 = out16; g.ldc16 = 512;
+    if (l < 6) norm_out(g, l + 1);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
   }
 }
 
 // The 13-block U-ViT stack (dit_cfm_bigvgan.cpp:868-886): outputs of blocks
 // 0..5 are kept (f16) as the skip inputs of blocks 12..7; the final AdaRMSNorm
-// leaves f16(norm(x)) in ws.n16.  x enters in ws.xa.
-void Engine::enqueue_transformer(int B, int T, const float* tab) {
+// leaves f16(norm(x)) in ws.n16.  x enters in ws.xa, with block 0's folded
+// norm operand in ws.n16 / ws.ssq.
+void Engine::enqueue_transformer(int B, int T, const float* tab, const float* nbq,
+                                 const float* nbw) {
   Weights& W = *w_;
   Workspace& ws = *ws_;
   for (int l = 0; l < 13; ++l)
-    enqueue_layer(l, B, T, tab, ws.xa, ws.xb, l > 6 ? ws.skip16[12 - l] : nullptr,
+    enqueue_layer(l, B, T, tab, nbq, nbw, ws.xa, ws.xb, l > 6 ? ws.skip16[12 - l] : nullptr,
                   l < 6 ? ws.skip16[l] : ws.x16);
   HIP_OK(launch_adarms(ws.xa, W.gamma[26], tab + 26 * 1024, tab + 26 * 1024 + 512, ws.n16, B * T,
                        stream_));
@@ -596,7 +633,8 @@ void Engine::enqueue_estimator(int B, int T, int slot) {
   const float* tab = ws.tab + (size_t)slot * kTcondPerStep;
   hipStream_t s = stream_;
 
-  enqueue_transformer(B, T, tab);
+  enqueue_transformer(B, T, tab, ws.nbq + (size_t)slot * 13 * 1536,
+                      ws.nbw + (size_t)slot * 13 * 3072);
   {
     GemmArgs g;  // skip_linear on [x_normed | x_mel]
     g.M = R; g.N = 512; g.K = 512 + kMelPad; g.K1 = 512;
@@ -654,11 +692,17 @@ static void enqueue_merge_const(Weights& W, Workspace& ws, int R, hipStream_t s)
   HIP_OK(launch_gemm(c, A_PLAIN, EPI_F32, s));
 }
 
-// Per-step merge: x = xin_const + xmel16 . Wx^T
-static void enqueue_merge_step(Weights& W, Workspace& ws, int R, hipStream_t s) {
+// Per-step merge: x = xin_const + xmel16 . Wx^T.  With tab (the step's
+// table row) it also leaves block 0's folded attention-norm operand in
+// ws.n16 / ws.ssq.
+static void enqueue_merge_step(Weights& W, Workspace& ws, int R, hipStream_t s,
+                               const float* tab) {
   GemmArgs g;
   g.M = R; g.N = 512; g.K = kMelPad; g.A = ws.xmel16; g.lda = kMelPad;
   g.W = W.mx_w; g.ldw = kMelPad; g.res = ws.xin_const; g.ldres = 512; g.C32 = ws.xa; g.ldc32 = 512;
+  if (tab) {
+    g.C16s = ws.n16; g.ldc16s = 512; g.sc_a = tab; g.sc_g = W.gamma[0]; g.ssq_out = ws.ssq;
+  }
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
 }
 
@@ -687,7 +731,7 @@ void Engine::enqueue_decode(const float* x0, const float* prompt, const float* c
                             ws.cond16, ws.mc16, stream_));
   enqueue_merge_const(W, ws, R, stream_);
   for (int s = 0; s < steps; ++s) {
-    enqueue_merge_step(W, ws, R, stream_);
+    enqueue_merge_step(W, ws, R, stream_, ws.tab + (size_t)s * kTcondPerStep);
     enqueue_estimator(B, T, s);
     HIP_OK(launch_conv2_euler(ws.y16, W.c2_w, W.c2_b, ws.P, nreq, T, cfg_on, cfg, dt, ws.x_cur,
                               ws.xmel16, vtrace ? vtrace + (size_t)s * nreq * T * 80 : nullptr,
@@ -776,7 +820,7 @@ void Engine::estimator_step_device(const float* x, const float* prompt_x, const 
   enqueue_tables(ws.tvals, 1);
   HIP_OK(launch_step_prep(x, prompt_x, cond, style, B, T, ws.xmel16, ws.cond16, ws.mc16, stream_));
   enqueue_merge_const(W, ws, R, stream_);
-  enqueue_merge_step(W, ws, R, stream_);
+  enqueue_merge_step(W, ws, R, stream_, ws.tab);
   enqueue_estimator(B, T, 0);
   HIP_OK(launch_conv2_rows(ws.y16, W.c2_w, W.c2_b, R, dphi, stream_));
   HIP_OK(hipStreamSynchronize(stream_));
@@ -800,6 +844,7 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
       GemmArgs g;
       g.M = R; g.N = 3072; g.K = 512; g.A = ws.n16; g.lda = 512;
       g.W = W.w13_w[0]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = 1536;
+      g.bias = ws.nbw; g.ssq_in = ws.ssq;
       loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, stream_)); });
       f = 2.0 * R * 3072 * 512;
       by = 2.0 * R * 512 + 2.0 * 3072 * 512 + 2.0 * R * 1536;
@@ -821,6 +866,7 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
       GemmArgs g;
       g.M = R; g.N = 1536; g.K = 512; g.A = ws.n16; g.lda = 512; g.W = W.qkv_w[0]; g.ldw = 512;
       g.T = T; g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
+      g.bias = ws.nbq; g.ssq_in = ws.ssq;
       loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, stream_)); });
       f = 2.0 * R * 1536 * 512;
       by = 2.0 * R * 512 + 2.0 * 1536 * 512 + 2.0 * R * 1536;
@@ -895,6 +941,7 @@ void Engine::upload_stage_tables(const float* t1_host, const float* t2_host) {
                                kTcondPerStep, stream_));
     HIP_OK(launch_linear_small(ws.t1, 1, 512, W.ada_w, W.ada_b, 1024, 1, 0, ws.tab + kFinalSsOff,
                                kTcondPerStep, stream_));
+    enqueue_norm_bias(1);
   }
   if (t2_host) {
     h2d(ws.t2, t2_host, 512 * 4, stream_);
@@ -928,7 +975,7 @@ void Engine::stage_input_merge(const float* x, const float* prompt_x, const floa
   HIP_OK(launch_step_prep(ws.in_x, ws.in_prompt, ws.in_cond, ws.in_style, B, T, ws.xmel16,
                           ws.cond16, ws.mc16, stream_));
   enqueue_merge_const(W, ws, R, stream_);
-  enqueue_merge_step(W, ws, R, stream_);
+  enqueue_merge_step(W, ws, R, stream_, nullptr);
   d2h(out, ws.xa, (size_t)R * 512 * 4, stream_);
 }
 
@@ -996,6 +1043,7 @@ void Engine::stage_block(const float* in, const float* t1, const uint32_t* mask,
   if ((layer > 6) != (skip != nullptr))
     throw std::invalid_argument("layers 7..12 take a skip input, layers 0..6 do not");
   ensure_workspace(B, T, 1, 1);
+  Weights& W = *w_;
   Workspace& ws = *ws_;
   const int R = B * T;
   ensure_rope(T);
@@ -1007,12 +1055,16 @@ void Engine::stage_block(const float* in, const float* t1, const uint32_t* mask,
     to_f16(ws.stage_a, ws.skip16[0], (size_t)R * 512, stream_);
     to_f16(ws.xa, ws.x16, (size_t)R * 512, stream_);
   }
-  enqueue_layer(layer, B, T, ws.tab, ws.xa, ws.xb, ws.skip16[0], ws.skip16[1]);
+  if (layer <= 6)  // block 0..6 inputs come straight from x here, not from a producer GEMM
+    HIP_OK(launch_norm_prep(ws.xa, ws.tab + layer * 1024, W.gamma[layer], ws.n16, ws.ssq, R,
+                            stream_));
+  enqueue_layer(layer, B, T, ws.tab, ws.nbq, ws.nbw, ws.xa, ws.xb, ws.skip16[0], ws.skip16[1]);
   d2h(out, ws.xa, (size_t)R * 512 * 4, stream_);
 }
 
 void Engine::stage_stack(const float* in, const float* t1, const uint32_t* mask, int B, int T,
                          float* out) {
+  Weights& W = *w_;
   ensure_workspace(B, T, 1, 1);
   Workspace& ws = *ws_;
   const int R = B * T;
@@ -1020,7 +1072,8 @@ void Engine::stage_stack(const float* in, const float* t1, const uint32_t* mask,
   upload_stage_tables(t1, nullptr);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
   h2d(ws.xa, in, (size_t)R * 512 * 4, stream_);
-  enqueue_transformer(B, T, ws.tab);
+  HIP_OK(launch_norm_prep(ws.xa, ws.tab, W.gamma[0], ws.n16, ws.ssq, R, stream_));
+  enqueue_transformer(B, T, ws.tab, ws.nbq, ws.nbw);
   std::vector<_Float16> h((size_t)R * 512);
   d2h(h.data(), ws.n16, h.size() * 2, stream_);
   for (size_t i = 0; i < h.size(); ++i) out[i] = (float)h[i];

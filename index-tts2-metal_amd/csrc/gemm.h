@@ -11,14 +11,18 @@
 
 namespace mit2hip {
 
+// Channels per tap of the k=5 WaveNet conv (the model's hidden width).
+constexpr int kConvC = 512;
+
 enum AMode : int {
   A_PLAIN = 0,   // A[m][k] = A[m*lda + k]
   A_CONCAT = 1,  // k <  K1: A[m*lda + k];  k >= K1: A2[m*lda2 + k - K1]
-  A_CONV5 = 2,   // k = tap*C + c: A[(b*T + reflect(t + tap - 2))*lda + c], m = b*T + t
+  A_CONV5 = 2,   // k = tap*kConvC + c: A[(b*T + reflect(t + tap - 2))*lda + c], m = b*T + t
 };
 
 enum EpiMode : int {
-  EPI_F32 = 0,        // C32 = acc + bias + res (bias/res optional); optional f16 copy C16
+  EPI_F32 = 0,        // C32 = acc + bias + res (bias/res optional); optional f16 copy C16,
+                      // optional normalised-operand outputs (C16s, ssq_out; see below)
   EPI_F16 = 1,        // C16 = acc + bias
   EPI_SWIGLU = 2,     // W rows interleaved [w1 x16 | w3 x16]: C16[m][c] = silu(h1) * h3
   EPI_GATE = 3,       // W rows interleaved [a x16 | b x16]: C16 = tanh(a+ca) * sigmoid(b+cb)
@@ -60,7 +64,26 @@ struct GemmArgs {
   half_t* vt = nullptr;              // EPI_QKV: [B][H][64][Tpad]
   int Tpad = 0;
   int flag = 0;                      // EPI_RESSKIP: 0 -> skip accumulator starts at zero
+
+  // AdaRMSNorm folded into a producer / consumer GEMM pair.  For the norm
+  // y = aw*(x*rs*gamma) + ab, rs = 1/sqrt(mean(x^2) + 1e-5) of each row, the
+  // consumer's product with W is rs * ((x*aw*gamma) . W^T) + ab . W^T, so:
+  //  * the producer (EPI_F32, N = 512) also writes C16s = f16(v * sc_a * sc_g)
+  //    (sc_a = aw, sc_g = gamma, per column) and, into ssq_out[m][N/32], the
+  //    row's sum of squares over each 32-column block of v;
+  //  * the consumer (EPI_SWIGLU, EPI_QKV) reads those partials (ssq_in, 16
+  //    per row, K = 512), scales its accumulator by rs and adds bias, which
+  //    holds ab . W^T for that step.
+  half_t* C16s = nullptr;
+  int ldc16s = 0;
+  const float* sc_a = nullptr;
+  const float* sc_g = nullptr;
+  float* ssq_out = nullptr;
+  const float* ssq_in = nullptr;
 };
+
+// Number of per-row partial sums of squares a 512-wide producer writes.
+constexpr int kSsqParts = 16;
 
 // Picks a tile shape for (M, N) and launches; returns hipSuccess or the
 // launch error.  Host-side checks reject shapes the kernels do not cover.

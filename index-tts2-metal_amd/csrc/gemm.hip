@@ -69,15 +69,20 @@ struct TileMap {
   }
 };
 
-template <int BM, int BN, int SK, int NST, int AM, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
+template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap tmap) {
+  constexpr int NW = WM * WN;                // wavefronts, WM along M x WN along N
   constexpr int CPR = SK / 8;                // 16-byte slots per stage row
-  constexpr int LA = BM * CPR / 256;         // DMA instructions per wave per stage (A)
-  constexpr int LB = BN * CPR / 256;         // (W)
+  constexpr int LA = BM * CPR / (64 * NW);   // DMA instructions per wave per stage (A)
+  constexpr int LB = BN * CPR / (64 * NW);   // (W)
   constexpr int L = LA + LB;
-  constexpr int MI = BM / 32;                // 16-row MFMA blocks per wave
-  constexpr int NI = BN / 32;                // 16-col MFMA blocks per wave
-  static_assert(LA >= 1 && LB >= 1, "tile too small for 256 threads");
+  constexpr int WTM = BM / WM;               // rows of a wave's sub-tile
+  constexpr int WTN = BN / WN;               // columns of a wave's sub-tile
+  constexpr int MI = WTM / 16;               // 16-row MFMA blocks per wave
+  constexpr int NI = WTN / 16;               // 16-col MFMA blocks per wave
+  static_assert(LA >= 1 && LB >= 1, "tile too small for the workgroup");
+  static_assert(LA * 64 * NW == BM * CPR && LB * 64 * NW == BN * CPR, "uneven DMA split");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave sub-tile must be whole MFMA blocks");
   static_assert(L * (NST - 1) < 64, "too many loads in flight");
   static_assert(CPR == 8 || CPR >= 16, "stage width");
 
@@ -112,8 +117,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int wm = wave / WN;
+  const int wn = wave - wm * WN;
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int KT = p.K / SK;
@@ -123,8 +128,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
   // consecutive columns n = col_base + 16 j + 4 lg + r (r = 0..3) of row
   // m = row_base + 16 i + lr.  Every epilogue access is then a 16-byte
   // (fp32) or 8-byte (f16) vector per lane.
-  const int row_base = m0 + wm * (BM / 2) + lr;
-  const int col_base = n0 + wn * (BN / 2) + 4 * lg;
+  const int row_base = m0 + wm * WTM + lr;
+  const int col_base = n0 + wn * WTN + 4 * lg;
 
   // Epilogue operands that do not depend on the product are fetched now, so
   // their latency hides behind the K loop.
@@ -159,19 +164,60 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
     }
   }
 
+  // Consumer side of a folded AdaRMSNorm: the producer's kSsqParts partial
+  // sums of squares of each of this lane's rows (K = 512 values) are fetched
+  // ahead of the first K stages and reduced to rs once those are in flight.
+  constexpr bool kNormIn = EPI == EPI_SWIGLU || EPI == EPI_QKV;
+  float4 ssq_pre[kNormIn ? MI : 1][kSsqParts / 4];
+  if constexpr (kNormIn) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = row_base + 16 * i;
+#pragma unroll
+      for (int u = 0; u < kSsqParts / 4; ++u)
+        ssq_pre[i][u] = (p.ssq_in && m < p.M)
+                            ? reinterpret_cast<const float4*>(p.ssq_in + (size_t)m * kSsqParts)[u]
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
   auto swz = [](int row) { return CPR >= 16 ? (row & 15) : ((row >> 1) & 7); };
 
-  auto a_src = [&](int m, int k) -> const half_t* {
+  // A_CONV5: a K stage never straddles a tap (kConvC % SK == 0), so each of
+  // this lane's load slots needs one of five source rows, fixed for the
+  // kernel: they are computed once here (five named offsets per slot, never
+  // an indexed table) and picked per stage with the wave-uniform tap.
+  struct ConvRows {
+    int r0, r1, r2, r3, r4;  // element offset of row reflect(t + tap - 2), tap 0..4
+  };
+  ConvRows conv_rows[AM == A_CONV5 ? LA : 1];
+  if constexpr (AM == A_CONV5) {
+    static_assert(kConvC % SK == 0, "a K stage must lie within one conv tap");
+#pragma unroll
+    for (int j = 0; j < LA; ++j) {
+      const int row = ((wave * LA + j) * 64 + lane) / CPR;
+      const int m = min(m0 + row, p.M - 1);
+      const int b = m / p.T;
+      const int t = m - b * p.T;
+      const int base = b * p.T;
+      conv_rows[j].r0 = (base + reflect_index(t - 2, p.T)) * p.lda;
+      conv_rows[j].r1 = (base + reflect_index(t - 1, p.T)) * p.lda;
+      conv_rows[j].r2 = (base + t) * p.lda;
+      conv_rows[j].r3 = (base + reflect_index(t + 1, p.T)) * p.lda;
+      conv_rows[j].r4 = (base + reflect_index(t + 2, p.T)) * p.lda;
+    }
+  }
+
+  auto a_src = [&](int j, int m, int k0, int kc) -> const half_t* {
+    const int k = k0 + kc;
     if constexpr (AM == A_PLAIN) {
       return p.A + (size_t)m * p.lda + k;
     } else if constexpr (AM == A_CONCAT) {
       return k < p.K1 ? p.A + (size_t)m * p.lda + k : p.A2 + (size_t)m * p.lda2 + (k - p.K1);
     } else {
-      const int tap = k / p.conv_c;
-      const int c = k - tap * p.conv_c;
-      const int b = m / p.T;
-      const int t = m - b * p.T;
-      return p.A + (size_t)(b * p.T + reflect_index(t + tap - 2, p.T)) * p.lda + c;
+      const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);  // stage start: uniform
+      const ConvRows& cr = conv_rows[j];
+      const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : tap == 2 ? cr.r2 : tap == 3 ? cr.r3 : cr.r4;
+      return p.A + ro + (k - tap * kConvC);
     }
   };
 
@@ -187,7 +233,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
       const int c = (q % CPR) ^ swz(row);
       int m = m0 + row;
       if (m > p.M - 1) m = p.M - 1;  // rows past M load a valid row; never stored
-      __builtin_amdgcn_global_load_lds((const void*)a_src(m, k0 + c * 8),
+      __builtin_amdgcn_global_load_lds((const void*)a_src(j, m, k0, c * 8),
                                        (lds_void_t*)(sa + q0 * 8), 16, 0, 0);
     }
 #pragma unroll
@@ -217,12 +263,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
       half8 bf[NI];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int row = wm * (BM / 2) + i * 16 + lr;
+        const int row = wm * WTM + i * 16 + lr;
         af[i] = *reinterpret_cast<const half8*>(sa + row * SK + ((c ^ swz(row)) << 3));
       }
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const int row = wn * (BN / 2) + j * 16 + lr;
+        const int row = wn * WTN + j * 16 + lr;
         bf[j] = *reinterpret_cast<const half8*>(sb + row * SK + ((c ^ swz(row)) << 3));
       }
 #pragma unroll
@@ -241,6 +287,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
   // not read again), which keeps the compiler from adding waits of its own;
   // the last KT % NST stages are resident when the loop exits.
   static_for<0, NST - 1>([&](auto st) { issue(st, min((int)decltype(st)::value, KT - 1)); });
+  float rsv[kNormIn ? MI : 1];
+  if constexpr (kNormIn) {
+    wait_vmcnt<L * (NST - 1)>();  // the partials (issued before the stages) have landed
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kSsqParts / 4; ++u)
+        ss += (ssq_pre[i][u].x + ssq_pre[i][u].y) + (ssq_pre[i][u].z + ssq_pre[i][u].w);
+      rsv[i] = p.ssq_in ? 1.0f / sqrtf(ss / 512.0f + 1e-5f) : 1.0f;
+    }
+  }
   int kt0 = 0;
   for (; kt0 + NST <= KT; kt0 += NST) {
     static_for<0, NST>([&](auto st) {
@@ -252,6 +310,28 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
       compute(st);
     });
   }
+  // Late prefetch: the small per-column epilogue operands are requested
+  // before the resident tail stages are computed, so their latency overlaps
+  // that compute without holding registers through the K loop.
+  float4 bv[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+    bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + col_base + 16 * j)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr bool kNormOut = EPI == EPI_F32;
+  float4 nsc[kNormOut ? NI : 1];  // producer of a folded norm: aw * gamma per column
+  if constexpr (kNormOut) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      if (p.C16s) {
+        const float4 a = *reinterpret_cast<const float4*>(p.sc_a + col_base + 16 * j);
+        const float4 g = *reinterpret_cast<const float4*>(p.sc_g + col_base + 16 * j);
+        nsc[j] = make_float4(a.x * g.x, a.y * g.y, a.z * g.z, a.w * g.w);
+      } else {
+        nsc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
   wait_vmcnt<0>();  // the tail stages have landed; no DMA outstanding at exit
   __builtin_amdgcn_s_barrier();
   static_for<0, NST - 1>([&](auto st) {
@@ -259,9 +339,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
   });
 
   // ---------------------------------------------------------------- epilogue
-  auto bias4 = [&](int n) -> float4 {
-    return p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
-  };
   auto st16 = [](half_t* dst, float a, float b, float c, float d) {
     half4 h;
     h[0] = (half_t)a; h[1] = (half_t)b; h[2] = (half_t)c; h[3] = (half_t)d;
@@ -271,23 +348,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
   if constexpr (EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_DUAL || EPI == EPI_RESSKIP ||
                 EPI == EPI_FINALSKIP) {
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int n = col_base + 16 * j;
-      const float4 bv = bias4(n);
+    for (int i = 0; i < MI; ++i) {
+      const int m = row_base + 16 * i;
+      const bool live = m < p.M;
+      float ssq[(NI + 1) / 2];  // EPI_F32 with ssq_out: this lane's share per 32-column block
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int m = row_base + 16 * i;
-        if (m >= p.M) continue;
-        float4 v = make_float4(acc[i][j][0] + bv.x, acc[i][j][1] + bv.y, acc[i][j][2] + bv.z,
-                               acc[i][j][3] + bv.w);
+      for (int q = 0; q < (NI + 1) / 2; ++q) ssq[q] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int n = col_base + 16 * j;
+        float4 v = make_float4(acc[i][j][0] + bv[j].x, acc[i][j][1] + bv[j].y,
+                               acc[i][j][2] + bv[j].z, acc[i][j][3] + bv[j].w);
         if constexpr (EPI == EPI_F32) {
           if (p.res) {
             const float4 r = pre_a[i][j];
             v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
           }
+          ssq[j / 2] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+          if (!live) continue;
           *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
           if (p.C16) st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
-        } else if constexpr (EPI == EPI_F16) {
+          if (p.C16s)
+            st16(p.C16s + (size_t)m * p.ldc16s + n, v.x * nsc[j].x, v.y * nsc[j].y,
+                 v.z * nsc[j].z, v.w * nsc[j].w);
+          continue;
+        }
+        if (!live) continue;
+        if constexpr (EPI == EPI_F16) {
           st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
         } else if constexpr (EPI == EPI_DUAL) {
           const int half_n = p.N >> 1;
@@ -320,45 +407,61 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
                           (o.w + v.w) * mk + r.w);
         }
       }
+      if constexpr (EPI == EPI_F32) {
+        if (p.ssq_out) {
+          static_assert(WTN % 32 == 0, "a folded-norm producer covers whole 32-column blocks");
+          // The four lanes of a row (lane groups lg) hold each 32-column block.
+#pragma unroll
+          for (int q = 0; q < NI / 2; ++q) {
+            float t = ssq[q];
+            t += __shfl_xor(t, 16, kWave);
+            t += __shfl_xor(t, 32, kWave);
+            if (live && lg == 0)
+              p.ssq_out[(size_t)m * kSsqParts + ((n0 + wn * WTN + 32 * q) >> 5)] = t;
+          }
+        }
+      }
     }
   } else {
     if constexpr (EPI == EPI_QKV) {
       if (n0 >= 1024) {
-        // V tile = one head (64 channels) x BM tokens.  Transpose through LDS
-        // so that V^T[d][t] is written by consecutive lanes at consecutive t.
-        static_assert(BN == 64, "a v tile must be exactly one head");
-        static_assert(SK >= 64, "the V^T staging tile reuses the first A stage buffer");
-        half_t* st = sA0;  // [64 d][BM rows], free once every wave is past its last MFMA
+        // V tile = BN/64 heads x BM tokens.  Transpose through LDS so that
+        // V^T[d][t] is written by consecutive lanes at consecutive t.
+        static_assert(BN % 64 == 0, "a v tile must hold whole heads");
+        static_assert(SK >= BM, "the V^T staging tile reuses the first W stage buffer");
+        half_t* st = sB0;  // [BN channels][BM rows], free once every wave is past its last MFMA
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
-        // Blocks (0, 1) of this wave hold the even / odd channels of its
+        // Blocks (2q, 2q+1) of this wave hold the even / odd channels of one
         // 32-channel group (v rows are permuted like the q and k rows):
-        // channel d = 32 wn + 2 (4 lg + r) (+1 for the odd block).
-        const float4 be = bias4(col_base);
-        const float4 bo = bias4(col_base + 16);
-        const float bev[4] = {be.x, be.y, be.z, be.w};
-        const float bov[4] = {bo.x, bo.y, bo.z, bo.w};
+        // tile channel c = 32 g + 2 (4 lg + r) (+1 for the odd block).
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
+        for (int q = 0; q < NI / 2; ++q) {
+          const int g = (wn * WTN + 32 * q) >> 5;
+          const float bev[4] = {bv[2 * q].x, bv[2 * q].y, bv[2 * q].z, bv[2 * q].w};
+          const float bov[4] = {bv[2 * q + 1].x, bv[2 * q + 1].y, bv[2 * q + 1].z, bv[2 * q + 1].w};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int rl = wm * (BM / 2) + i * 16 + lr;
-            const int d = 32 * wn + 2 * (4 * lg + r);
-            st[d * BM + rl] = (half_t)(acc[i][0][r] + bev[r]);
-            st[(d + 1) * BM + rl] = (half_t)(acc[i][1][r] + bov[r]);
-          }
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int rl = wm * WTM + i * 16 + lr;
+              const int c = 32 * g + 2 * (4 * lg + r);
+              st[c * BM + rl] = (half_t)(rsv[i] * acc[i][2 * q][r] + bev[r]);
+              st[(c + 1) * BM + rl] = (half_t)(rsv[i] * acc[i][2 * q + 1][r] + bov[r]);
+            }
+        }
         wait_lgkmcnt0();  // this wave's stores have landed before the barrier releases readers
         __builtin_amdgcn_s_barrier();
-        const int hh = (n0 - 1024) >> 6;
+        const int h0 = (n0 - 1024) >> 6;
 #pragma unroll
         for (int rr = 0; rr < BM; rr += 64) {
           const int rl = rr + lane;
           const int m = m0 + rl;
-          if (m < p.M) {
+          if (rl < BM && m < p.M) {
             const int b = m / p.T;
             const int t = m - b * p.T;
-            half_t* dst = p.vt + ((size_t)b * 8 + hh) * 64 * p.Tpad + t;
-            for (int d = wave; d < 64; d += 4) dst[(size_t)d * p.Tpad] = st[d * BM + rl];
+            for (int c = wave; c < BN; c += NW)
+              p.vt[(((size_t)b * 8 + h0 + (c >> 6)) * 64 + (c & 63)) * p.Tpad + t] = st[c * BM + rl];
           }
         }
         return;
@@ -371,16 +474,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p, TileMap tmap) {
     for (int q = 0; q < NI / 2; ++q) {
       const int ce = col_base + q * 32;  // GEMM column of this lane's even-block values
       const int group = (ce - 4 * lg) >> 5;
-      const float4 be = bias4(ce);
-      const float4 bo = bias4(ce + 16);
+      const float4 be = bv[2 * q];
+      const float4 bo = bv[2 * q + 1];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = row_base + 16 * i;
         if (m >= p.M) continue;
-        const float ve[4] = {acc[i][2 * q][0] + be.x, acc[i][2 * q][1] + be.y,
-                             acc[i][2 * q][2] + be.z, acc[i][2 * q][3] + be.w};
-        const float vo[4] = {acc[i][2 * q + 1][0] + bo.x, acc[i][2 * q + 1][1] + bo.y,
-                             acc[i][2 * q + 1][2] + bo.z, acc[i][2 * q + 1][3] + bo.w};
+        float rs_row = 1.0f;  // rs of the row when the AdaRMSNorm is folded in
+        if constexpr (kNormIn) rs_row = rsv[i];
+        const float ve[4] = {rs_row * acc[i][2 * q][0] + be.x, rs_row * acc[i][2 * q][1] + be.y,
+                             rs_row * acc[i][2 * q][2] + be.z, rs_row * acc[i][2 * q][3] + be.w};
+        const float vo[4] = {rs_row * acc[i][2 * q + 1][0] + bo.x,
+                             rs_row * acc[i][2 * q + 1][1] + bo.y,
+                             rs_row * acc[i][2 * q + 1][2] + bo.z,
+                             rs_row * acc[i][2 * q + 1][3] + bo.w};
         if constexpr (EPI == EPI_SWIGLU) {
           const int c = group * 16 + 4 * lg;
           float y[4];
@@ -460,24 +567,38 @@ static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
   return t;
 }
 
-template <int BM, int BN, int SK, int NST, int AM, int EPI>
+template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
   const TileMap tm = make_tile_map(a.M, a.N, a.K, AM == A_CONV5 ? a.conv_c : a.K, BM, BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI>), dim3(8 * tm.per_xcd), dim3(256), 0, s,
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN>), dim3(8 * tm.per_xcd),
+                     dim3(64 * WM * WN), 0, s,
                      a, tm);
   return hipGetLastError();
 }
 
-// Tile and stage choice per shape (measured at M = 1720 on MI355X): 64x64
-// tiles with 64-wide K stages in a 3-buffer ring (48 KB of LDS, three
-// workgroups per CU) for most shapes; 64x128 for the widest N; 128-wide
-// stages for the K = 2560 conv.  QKV keeps BN = 64 so a v tile is one head.
+// Tile, stage and wavefront choice, swept at M = 1720 (B = 2, T = 860) on
+// MI355X.  Two limits decide it: the L2 -> CU path delivers about 48 B/clk
+// per CU whatever the load method or depth, so a K loop's time is its total
+// operand bytes, 2MNK (1/BM + 1/BN), spread over the CUs; and a workgroup of
+// four wavefronts alone on a CU cannot hide its LDS and MFMA latencies.
+//  * wide outputs use big tiles with eight wavefronts (two per SIMD) and
+//    about one tile per CU: w1|w3 (N = 3072) 128x192, 11.8 vs 15.4 us for
+//    64x64; the k=5 conv (N = 1024, K = 2560) 64x128 with 128-wide stages,
+//    17.4 vs 21.3 us; res/skip and conv1|res_projection (N = 1024) 64x128;
+//  * N = 512 outputs and QKV keep 64x64 tiles with four wavefronts in a
+//    3-stage ring (three workgroups per CU): larger tiles leave too few
+//    tiles to cover the CUs.
 template <int AM, int EPI>
 static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
-  if constexpr (EPI != EPI_QKV) {
-    if (a.N >= 3072 && a.N % 128 == 0) return launch_tile<64, 128, 64, 2, AM, EPI>(a, s);
+  if constexpr (EPI == EPI_SWIGLU) {
+    if (a.N % 192 == 0) return launch_tile<128, 192, 64, 3, AM, EPI, 4, 2>(a, s);
   }
-  if (a.K >= 2048) return launch_tile<64, 64, 128, 2, AM, EPI>(a, s);
+  if constexpr (AM == A_CONV5) {
+    if (a.N % 128 == 0) return launch_tile<64, 128, 128, 3, AM, EPI, 2, 4>(a, s);
+  }
+  if constexpr (EPI == EPI_RESSKIP || EPI == EPI_DUAL) {
+    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
+  }
   return launch_tile<64, 64, 64, 3, AM, EPI>(a, s);
 }
 
@@ -486,7 +607,7 @@ hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t 
     return hipErrorInvalidValue;
   if (amode == A_CONCAT && (a.K1 % 128 != 0 || a.K1 <= 0 || a.K1 >= a.K || !a.A2))
     return hipErrorInvalidValue;
-  if (amode == A_CONV5 && (a.T <= 0 || a.conv_c % 128 != 0 || a.K != 5 * a.conv_c))
+  if (amode == A_CONV5 && (a.T <= 0 || a.conv_c != kConvC || a.K != 5 * kConvC))
     return hipErrorInvalidValue;
   if (amode == A_PLAIN) {
     switch (epi) {

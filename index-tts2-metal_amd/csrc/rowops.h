@@ -8,6 +8,15 @@ namespace mit2hip {
 // AdaRMSNorm: out16[m] = aw * (x[m] * rsqrt(mean(x[m]^2) + 1e-5) * gamma) + ab  (width 512)
 hipError_t launch_adarms(const float* x, const float* gamma, const float* aw, const float* ab,
                          half_t* out16, int rows, hipStream_t s);
+// The producer half of a folded AdaRMSNorm for a row block that no GEMM
+// produced (stage entry points): n16[m] = f16(x[m] * aw * gamma) and the
+// row's 16 partial sums of squares over 32-column blocks, ssq[m][16].
+hipError_t launch_norm_prep(const float* x, const float* aw, const float* gamma, half_t* n16,
+                            float* ssq, int rows, hipStream_t s);
+// Column bias of a folded AdaRMSNorm, per step: out[s][n] = sum_k ab_s[k] *
+// W[n][k] (K = 512, W f16 [N][512] as resident), ab_s = ab + s * ab_ld.
+hipError_t launch_norm_bias(const float* ab, int ab_ld, int S, const half_t* W, int N, float* out,
+                            int out_ld, hipStream_t s);
 // Final-layer AdaLN: LayerNorm (no affine, eps 1e-6), then * (1 + scale) + shift (width 512)
 hipError_t launch_adaln(const float* x, const float* shift, const float* scale, half_t* out16,
                         int rows, hipStream_t s);

@@ -67,6 +67,66 @@ __global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ x,
   *reinterpret_cast<half8*>(out + (size_t)row * 512 + lane * 8) = o;
 }
 
+__global__ __launch_bounds__(256) void norm_prep_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ aw,
+                                                        const float* __restrict__ gamma,
+                                                        half_t* __restrict__ n16,
+                                                        float* __restrict__ ssq, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * 512) + lane * 2;
+  const float4 a = xr[0], b = xr[1];
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  float ss = 0.f;
+  half8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = lane * 8 + i;
+    ss += v[i] * v[i];
+    o[i] = (half_t)(v[i] * (aw[c] * gamma[c]));
+  }
+  *reinterpret_cast<half8*>(n16 + (size_t)row * 512 + lane * 8) = o;
+  // four lanes hold one 32-column block
+  ss += __shfl_xor(ss, 1, kWave);
+  ss += __shfl_xor(ss, 2, kWave);
+  if ((lane & 3) == 0) ssq[(size_t)row * 16 + (lane >> 2)] = ss;
+}
+
+hipError_t launch_norm_prep(const float* x, const float* aw, const float* gamma, half_t* n16,
+                            float* ssq, int rows, hipStream_t s) {
+  hipLaunchKernelGGL(norm_prep_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, aw, gamma, n16,
+                     ssq, rows);
+  return hipGetLastError();
+}
+
+// One wavefront per output column n: the f16 weight row stays in registers
+// (8 values per lane) across the S steps.
+__global__ __launch_bounds__(256) void norm_bias_kernel(const float* __restrict__ ab, int ab_ld,
+                                                        int S, const half_t* __restrict__ W, int N,
+                                                        float* __restrict__ out, int out_ld) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const half8 w = *reinterpret_cast<const half8*>(W + (size_t)n * 512 + lane * 8);
+  for (int st = 0; st < S; ++st) {
+    const float4* ar = reinterpret_cast<const float4*>(ab + (size_t)st * ab_ld) + lane * 2;
+    const float4 a = ar[0], b = ar[1];
+    float acc = a.x * (float)w[0] + a.y * (float)w[1] + a.z * (float)w[2] + a.w * (float)w[3] +
+                b.x * (float)w[4] + b.y * (float)w[5] + b.z * (float)w[6] + b.w * (float)w[7];
+    acc = warp_sum(acc);
+    if (lane == 0) out[(size_t)st * out_ld + n] = acc;
+  }
+}
+
+hipError_t launch_norm_bias(const float* ab, int ab_ld, int S, const half_t* W, int N, float* out,
+                            int out_ld, hipStream_t s) {
+  if (S <= 0 || ab_ld % 4 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(norm_bias_kernel, dim3((N + 3) / 4), dim3(256), 0, s, ab, ab_ld, S, W, N, out,
+                     out_ld);
+  return hipGetLastError();
+}
+
 hipError_t launch_adarms(const float* x, const float* gamma, const float* aw, const float* ab,
                          half_t* out16, int rows, hipStream_t s) {
   hipLaunchKernelGGL(adarms_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, gamma, aw, ab, out16,
@@ -171,46 +231,77 @@ __device__ __forceinline__ void conv2_block(const half_t* __restrict__ y16, size
   }
 }
 
+// conv2 + CFG blend + Euler update.  One workgroup per 16-token block of
+// one request: wave w computes the partial product over K = [128 w, 128 w +
+// 128) for both branches (five 16-wide MFMA column blocks each), the
+// partials meet in LDS, and the 256 threads apply the update to the
+// 16 x 80 block.
 __global__ __launch_bounds__(256) void conv2_euler_kernel(
     const half_t* __restrict__ y16, const half_t* __restrict__ w2, const float* __restrict__ b2,
     const uint32_t* __restrict__ P, int T, int cfg_on, float cfg, float dt,
     float* __restrict__ x_cur, half_t* __restrict__ xmel16, float* __restrict__ vtrace) {
+  // red[wave][branch][block nb][lane][i]: partial of token 4*(lane/16)+i, channel 16*nb + lane%16
+  __shared__ float red[4][2][5][64][4];
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  const int t0 = blockIdx.x * 16;
   const int r = blockIdx.y;
-  if (t0 >= T) return;
   const int nvalid = min(16, T - t0);
   const int bc = cfg_on ? 2 * r : r;
-  floatx4 ac[5], au[5];
-  conv2_block(y16, (size_t)bc * T + t0, nvalid, w2, lr, lg, ac);
-  if (cfg_on) conv2_block(y16, (size_t)(bc + 1) * T + t0, nvalid, w2, lr, lg, au);
-  const uint32_t Pr = P[r];
+  const int nbr = cfg_on ? 2 : 1;
+  for (int br = 0; br < nbr; ++br) {
+    const size_t row0 = (size_t)(bc + br) * T + t0;
+    floatx4 acc[5];
 #pragma unroll
-  for (int nb = 0; nb < 5; ++nb) {
-    const int n = nb * 16 + lr;
-    const float bias = b2[n];
+    for (int nb = 0; nb < 5; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + lg * 4 + i;
-      if (t >= T) continue;
-      float v = ac[nb][i] + bias;
-      if (cfg_on) v = (1.0f + cfg) * v - cfg * (au[nb][i] + bias);
-      const size_t xi = ((size_t)r * T + t) * 80 + n;
-      if (vtrace) vtrace[xi] = v;
-      float xn = x_cur[xi] + dt * v;
-      if ((uint32_t)t < Pr) xn = 0.0f;
-      x_cur[xi] = xn;
-      xmel16[((size_t)bc * T + t) * kMelPad + n] = (half_t)xn;
-      if (cfg_on) xmel16[((size_t)(bc + 1) * T + t) * kMelPad + n] = (half_t)xn;
+    for (int ks = 0; ks < 4; ++ks) {
+      const int k = wave * 128 + ks * 32 + lg * 8;
+      half8 av = {};
+      if (lr < nvalid) av = *reinterpret_cast<const half8*>(y16 + (row0 + lr) * 512 + k);
+#pragma unroll
+      for (int nb = 0; nb < 5; ++nb) {
+        const half8 bw = *reinterpret_cast<const half8*>(w2 + (size_t)(nb * 16 + lr) * 512 + k);
+        acc[nb] = mfma16x16x32(av, bw, acc[nb]);
+      }
     }
+#pragma unroll
+    for (int nb = 0; nb < 5; ++nb)
+      *reinterpret_cast<floatx4*>(&red[wave][br][nb][lane][0]) = acc[nb];
+  }
+  __syncthreads();
+  const uint32_t Pr = P[r];
+  for (int idx = threadIdx.x; idx < 16 * 80; idx += 256) {
+    const int tok = idx / 80;
+    const int n = idx - tok * 80;
+    const int t = t0 + tok;
+    if (t >= T) continue;
+    const int nb = n >> 4, ln = (tok >> 2) * 16 + (n & 15), i = tok & 3;
+    const float bias = b2[n];
+    float v = bias;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v += red[w][0][nb][ln][i];
+    if (cfg_on) {
+      float u = bias;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) u += red[w][1][nb][ln][i];
+      v = (1.0f + cfg) * v - cfg * u;
+    }
+    const size_t xi = ((size_t)r * T + t) * 80 + n;
+    if (vtrace) vtrace[xi] = v;
+    float xn = x_cur[xi] + dt * v;
+    if ((uint32_t)t < Pr) xn = 0.0f;
+    x_cur[xi] = xn;
+    xmel16[((size_t)bc * T + t) * kMelPad + n] = (half_t)xn;
+    if (cfg_on) xmel16[((size_t)(bc + 1) * T + t) * kMelPad + n] = (half_t)xn;
   }
 }
 
 hipError_t launch_conv2_euler(const half_t* y16, const half_t* w2, const float* b2,
                               const uint32_t* P, int nreq, int T, int cfg_on, float cfg, float dt,
                               float* x_cur, half_t* xmel16, float* vtrace, hipStream_t s) {
-  hipLaunchKernelGGL(conv2_euler_kernel, dim3((T + 63) / 64, nreq), dim3(256), 0, s, y16, w2, b2, P,
+  hipLaunchKernelGGL(conv2_euler_kernel, dim3((T + 15) / 16, nreq), dim3(256), 0, s, y16, w2, b2, P,
                      T, cfg_on, cfg, dt, x_cur, xmel16, vtrace);
   return hipGetLastError();
 }

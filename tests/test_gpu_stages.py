@@ -113,7 +113,7 @@ def _masks(T):
     return m
 
 
-@pytest.mark.parametrize("T", [5, 6, 64, 65, 173, 300])
+@pytest.mark.parametrize("T", [5, 6, 64, 65, 173, 300, 520, 900])
 def test_attention_core(orc, model_unit, ctx_unit, T):
     masks = _masks(T) if T != 5 else np.ones((2, 5), np.uint32)
     x = np.stack([sincos_series(T * 512, 0.017, 0.011, 0.13, 0.09, 97),
