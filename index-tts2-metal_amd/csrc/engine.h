@@ -49,6 +49,20 @@ class Arena {
 struct Weights;    // resident weights (engine.hip)
 struct Workspace;  // activations (engine.hip)
 
+// Device buffers of the timestep-conditioning tables for S step slots:
+// t values, their embeddings and MLP intermediates, the per-step table rows
+// (kTcondPerStep floats each) and the folded-norm column biases.
+struct TableBufs {
+  float* tvals = nullptr;  // [S]
+  float* temb = nullptr;   // [S][256]
+  float* th = nullptr;     // [S][512]
+  float* t1 = nullptr;     // [S][512]
+  float* t2 = nullptr;     // [S][512]
+  float* tab = nullptr;    // [S][36864]
+  float* nbq = nullptr;    // [S][13][1536]
+  float* nbw = nullptr;    // [S][13][3072]
+};
+
 class Engine {
  public:
   Engine(const std::vector<HostTensor>& tensors, int device);
@@ -110,14 +124,15 @@ class Engine {
  private:
   void ensure_workspace(int B, int T, int S, int nreq);
   void ensure_rope(int T);
-  void enqueue_tables(const float* tvals_dev, int S);
-  void enqueue_norm_bias(int S);
+  void enqueue_tables(const TableBufs& tb, int S);
+  void enqueue_norm_bias(const TableBufs& tb, int S);
+  const TableBufs& decode_tables(int steps);
   void enqueue_layer(int l, int B, int T, const float* tab, const float* nbq, const float* nbw,
                      float* cur, float* hbuf, const half_t* skip16, half_t* out16);
   void enqueue_transformer(int B, int T, const float* tab, const float* nbq, const float* nbw);
-  void enqueue_estimator(int B, int T, int step_slot);
+  void enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw);
   void enqueue_decode(const float* x0, const float* prompt, const float* cond, const float* style,
-                      int nreq, int T, int steps, float cfg, float* vtrace);
+                      int nreq, int T, int steps, float cfg, float* vtrace, const TableBufs& tb);
   void upload_stage_tables(const float* t1_host, const float* t2_host);
 
   int device_ = 0;
@@ -126,6 +141,12 @@ class Engine {
   bool use_graph_ = true;
   std::unique_ptr<Weights> w_;
   std::unique_ptr<Workspace> ws_;
+  // Decode tables per step count, computed once per context (decode_tables).
+  struct TableSet {
+    Arena arena;
+    TableBufs bufs;
+  };
+  std::map<int, std::unique_ptr<TableSet>> table_cache_;
   struct GraphEntry {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;

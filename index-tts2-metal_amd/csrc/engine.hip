@@ -222,6 +222,8 @@ struct Workspace {
   float* ssq;   // [R][kSsqParts] partial row sums of squares (folded AdaRMSNorm)
   float* nbq;   // [S][13][1536] folded attention-norm column bias (ab . Wqkv^T)
   float* nbw;   // [S][13][3072] folded ffn-norm column bias (ab . W13^T)
+  // The workspace's own one-step tables (estimator forwards, stage entry points).
+  TableBufs one() const { return TableBufs{tvals, temb, th, t1, t2, tab, nbq, nbw}; }
   // staging for host-pointer entry points
   float* in_x;
   float* in_prompt;
@@ -233,6 +235,9 @@ struct Workspace {
   float* stage_b;
   float* stage_c;
   int Tcur = 0;  // T the rope table currently holds
+  // What ws.mask / ws.P hold for the decode path (every other writer of
+  // ws.mask clears mask_host).
+  std::vector<uint32_t> mask_host, P_host;
 };
 
 // ------------------------------------------------------------------ engine
@@ -485,6 +490,8 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   HIP_OK(hipStreamSynchronize(stream_));
   ws.capR = cR; ws.capT = cT; ws.capTpad = cTpad; ws.capB = cB; ws.capS = cS; ws.capReq = cReq;
   ws.Tcur = 0;
+  ws.mask_host.clear();
+  ws.P_host.clear();
 }
 
 // RoPE table [T][32] of (cos, sin), theta = t / 10000^(2i/64)
@@ -510,35 +517,71 @@ void Engine::ensure_rope(int T) {
 }
 
 // ------------------------------------------------------------------ tables
-void Engine::enqueue_tables(const float* tvals_dev, int S) {
-  Weights& W = *w_;
-  Workspace& ws = *ws_;
-  for (int i = 0; i < 2; ++i) {
-    float* out = i == 0 ? ws.t1 : ws.t2;
-    HIP_OK(launch_timestep_embedding(tvals_dev, W.te_freqs[i], S, ws.temb, stream_));
-    HIP_OK(launch_linear_small(ws.temb, S, 256, W.te_w0[i], W.te_b0[i], 512, 0, 1, ws.th, 512, stream_));
-    HIP_OK(launch_linear_small(ws.th, S, 512, W.te_w2[i], W.te_b2[i], 512, 0, 0, out, 512, stream_));
+static std::vector<float> euler_times(int steps) {
+  std::vector<float> tv(steps);
+  float t = 0.0f;
+  const float dt = 1.0f / (float)steps;
+  for (int s = 0; s < steps; ++s) {
+    tv[s] = t;
+    t += dt;  // accumulated in float like run_cfm_euler_cpu
   }
-  HIP_OK(launch_linear_small(ws.t1, S, 512, W.proj_w, W.proj_b, 27 * 1024, 0, 0, ws.tab,
+  return tv;
+}
+
+void Engine::enqueue_tables(const TableBufs& tb, int S) {
+  Weights& W = *w_;
+  for (int i = 0; i < 2; ++i) {
+    float* out = i == 0 ? tb.t1 : tb.t2;
+    HIP_OK(launch_timestep_embedding(tb.tvals, W.te_freqs[i], S, tb.temb, stream_));
+    HIP_OK(launch_linear_small(tb.temb, S, 256, W.te_w0[i], W.te_b0[i], 512, 0, 1, tb.th, 512, stream_));
+    HIP_OK(launch_linear_small(tb.th, S, 512, W.te_w2[i], W.te_b2[i], 512, 0, 0, out, 512, stream_));
+  }
+  HIP_OK(launch_linear_small(tb.t1, S, 512, W.proj_w, W.proj_b, 27 * 1024, 0, 0, tb.tab,
                              kTcondPerStep, stream_));
-  HIP_OK(launch_linear_small(ws.t1, S, 512, W.ada_w, W.ada_b, 1024, 1, 0, ws.tab + kFinalSsOff,
+  HIP_OK(launch_linear_small(tb.t1, S, 512, W.ada_w, W.ada_b, 1024, 1, 0, tb.tab + kFinalSsOff,
                              kTcondPerStep, stream_));
-  HIP_OK(launch_linear_small(ws.t2, S, 512, W.wnc_w, W.wnc_b, 8192, 0, 0, ws.tab + kWnCondOff,
+  HIP_OK(launch_linear_small(tb.t2, S, 512, W.wnc_w, W.wnc_b, 8192, 0, 0, tb.tab + kWnCondOff,
                              kTcondPerStep, stream_));
-  enqueue_norm_bias(S);
+  enqueue_norm_bias(tb, S);
 }
 
 // Column biases of the folded AdaRMSNorms (ab . W^T) for every layer and
-// step slot of ws.tab.
-void Engine::enqueue_norm_bias(int S) {
+// step slot of tb.tab.
+void Engine::enqueue_norm_bias(const TableBufs& tb, int S) {
   Weights& W = *w_;
-  Workspace& ws = *ws_;
   for (int l = 0; l < 13; ++l) {
-    HIP_OK(launch_norm_bias(ws.tab + l * 1024 + 512, kTcondPerStep, S, W.qkv_w[l], 1536,
-                            ws.nbq + l * 1536, 13 * 1536, stream_));
-    HIP_OK(launch_norm_bias(ws.tab + (13 + l) * 1024 + 512, kTcondPerStep, S, W.w13_w[l], 3072,
-                            ws.nbw + l * 3072, 13 * 3072, stream_));
+    HIP_OK(launch_norm_bias(tb.tab + l * 1024 + 512, kTcondPerStep, S, W.qkv_w[l], 1536,
+                            tb.nbq + l * 1536, 13 * 1536, stream_));
+    HIP_OK(launch_norm_bias(tb.tab + (13 + l) * 1024 + 512, kTcondPerStep, S, W.w13_w[l], 3072,
+                            tb.nbw + l * 3072, 13 * 3072, stream_));
   }
+}
+
+// The tables of a `steps`-step Euler decode (t = 0, dt, 2 dt, ... accumulated
+// in fp32).  They depend only on the step count, so each context computes
+// them once per count, outside any captured graph, and every later decode
+// reads them: the reference caches the same tables per step count in a
+// process-wide map (dit_cfm_bigvgan.cpp:2954-2959); here the cache is per
+// context, so it needs no lock.
+const TableBufs& Engine::decode_tables(int steps) {
+  auto it = table_cache_.find(steps);
+  if (it != table_cache_.end()) return it->second->bufs;
+  auto set = std::make_unique<TableSet>();
+  const size_t S = (size_t)steps;
+  size_t bytes = 0;
+  const size_t counts[8] = {S, S * 256, S * 512, S * 512, S * 512, S * kTcondPerStep, S * 13 * 1536,
+                            S * 13 * 3072};
+  for (size_t c : counts) bytes += (c * 4 + 255) / 256 * 256;
+  set->arena.reserve(bytes);
+  auto F = [&](size_t n) { return static_cast<float*>(set->arena.take(n * 4)); };
+  TableBufs& tb = set->bufs;
+  tb.tvals = F(counts[0]); tb.temb = F(counts[1]); tb.th = F(counts[2]); tb.t1 = F(counts[3]);
+  tb.t2 = F(counts[4]); tb.tab = F(counts[5]); tb.nbq = F(counts[6]); tb.nbw = F(counts[7]);
+  const std::vector<float> tv = euler_times(steps);
+  HIP_OK(hipMemcpyAsync(tb.tvals, tv.data(), tv.size() * 4, hipMemcpyHostToDevice, stream_));
+  enqueue_tables(tb, steps);
+  HIP_OK(hipStreamSynchronize(stream_));  // tv outlives the copy
+  return table_cache_.emplace(steps, std::move(set)).first->second->bufs;
 }
 
 // One transformer block (dit_cfm_bigvgan.cpp:816-832 / pass version :1901-1996):
@@ -626,15 +669,13 @@ void Engine::enqueue_transformer(int B, int T, const float* tab, const float* nb
 // ------------------------------------------------------------------ estimator body
 // Runs the estimator from x (ws.xa, fp32, already merged) to y16 (final
 // linear output, f16) for B branches of T rows, using table row `slot`.
-void Engine::enqueue_estimator(int B, int T, int slot) {
+void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw) {
   Weights& W = *w_;
   Workspace& ws = *ws_;
   const int R = B * T;
-  const float* tab = ws.tab + (size_t)slot * kTcondPerStep;
   hipStream_t s = stream_;
 
-  enqueue_transformer(B, T, tab, ws.nbq + (size_t)slot * 13 * 1536,
-                      ws.nbw + (size_t)slot * 13 * 3072);
+  enqueue_transformer(B, T, tab, nbq, nbw);
   {
     GemmArgs g;  // skip_linear on [x_normed | x_mel]
     g.M = R; g.N = 512; g.K = 512 + kMelPad; g.K1 = 512;
@@ -706,33 +747,22 @@ static void enqueue_merge_step(Weights& W, Workspace& ws, int R, hipStream_t s,
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
 }
 
-static std::vector<float> euler_times(int steps) {
-  std::vector<float> tv(steps);
-  float t = 0.0f;
-  const float dt = 1.0f / (float)steps;
-  for (int s = 0; s < steps; ++s) {
-    tv[s] = t;
-    t += dt;  // accumulated in float like run_cfm_euler_cpu
-  }
-  return tv;
-}
-
 void Engine::enqueue_decode(const float* x0, const float* prompt, const float* cond,
                             const float* style, int nreq, int T, int steps, float cfg,
-                            float* vtrace) {
+                            float* vtrace, const TableBufs& tb) {
   Weights& W = *w_;
   Workspace& ws = *ws_;
   const int cfg_on = cfg > 0.0f ? 1 : 0;
   const int B = cfg_on ? 2 * nreq : nreq;
   const int R = B * T;
   const float dt = 1.0f / (float)steps;
-  enqueue_tables(ws.tvals, steps);
   HIP_OK(launch_decode_prep(x0, prompt, cond, style, ws.P, nreq, T, cfg_on, ws.x_cur, ws.xmel16,
                             ws.cond16, ws.mc16, stream_));
   enqueue_merge_const(W, ws, R, stream_);
   for (int s = 0; s < steps; ++s) {
-    enqueue_merge_step(W, ws, R, stream_, ws.tab + (size_t)s * kTcondPerStep);
-    enqueue_estimator(B, T, s);
+    const float* tab = tb.tab + (size_t)s * kTcondPerStep;
+    enqueue_merge_step(W, ws, R, stream_, tab);
+    enqueue_estimator(B, T, tab, tb.nbq + (size_t)s * 13 * 1536, tb.nbw + (size_t)s * 13 * 3072);
     HIP_OK(launch_conv2_euler(ws.y16, W.c2_w, W.c2_b, ws.P, nreq, T, cfg_on, cfg, dt, ws.x_cur,
                               ws.xmel16, vtrace ? vtrace + (size_t)s * nreq * T * 80 : nullptr,
                               stream_));
@@ -752,28 +782,34 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
   HIP_OK(hipSetDevice(device_));
   const int cfg_on = cfg > 0.0f ? 1 : 0;
   const int B = cfg_on ? 2 * nreq : nreq;
-  ensure_workspace(B, T, steps, nreq);
+  ensure_workspace(B, T, 1, nreq);
   last_B_ = B;
   last_T_ = T;
   Workspace& ws = *ws_;
   ensure_rope(T);
+  const TableBufs& tb = decode_tables(steps);
   {
+    // Key mask and prompt lengths: uploaded only when they differ from what
+    // the workspace already holds, so back-to-back decodes of one shape never
+    // wait for the device here.
     std::vector<uint32_t> mask((size_t)B * T);
     for (int b = 0; b < B; ++b) {
       const int r = cfg_on ? b / 2 : b;
       for (int t = 0; t < T; ++t) mask[(size_t)b * T + t] = (uint32_t)t < valid_T[r] ? 1u : 0u;
     }
-    auto tv = euler_times(steps);
-    HIP_OK(hipMemcpyAsync(ws.mask, mask.data(), mask.size() * 4, hipMemcpyHostToDevice, stream_));
-    HIP_OK(hipMemcpyAsync(ws.P, P, (size_t)nreq * 4, hipMemcpyHostToDevice, stream_));
-    HIP_OK(hipMemcpyAsync(ws.tvals, tv.data(), tv.size() * 4, hipMemcpyHostToDevice, stream_));
-    // Host staging vectors must outlive the copies.
-    HIP_OK(hipStreamSynchronize(stream_));
+    std::vector<uint32_t> pv(P, P + nreq);
+    if (mask != ws.mask_host || pv != ws.P_host) {
+      HIP_OK(hipMemcpyAsync(ws.mask, mask.data(), mask.size() * 4, hipMemcpyHostToDevice, stream_));
+      HIP_OK(hipMemcpyAsync(ws.P, pv.data(), pv.size() * 4, hipMemcpyHostToDevice, stream_));
+      HIP_OK(hipStreamSynchronize(stream_));  // the host vectors outlive the copies
+      ws.mask_host = std::move(mask);
+      ws.P_host = std::move(pv);
+    }
   }
 
   // The Euler state lives in ws.x_cur; x_out receives a copy at the end.
   auto enqueue_all = [&]() {
-    enqueue_decode(x0, prompt, cond, style, nreq, T, steps, cfg, vtrace);
+    enqueue_decode(x0, prompt, cond, style, nreq, T, steps, cfg, vtrace, tb);
     HIP_OK(launch_copy_f32(ws.x_cur, x_out, (size_t)nreq * T * 80, stream_));
   };
   if (!use_graph_) {
@@ -815,13 +851,14 @@ void Engine::estimator_step_device(const float* x, const float* prompt_x, const 
   const int R = B * T;
   ensure_rope(T);
   HIP_OK(hipMemcpyAsync(ws.mask, mask, (size_t)R * 4, hipMemcpyDeviceToDevice, stream_));
+  ws.mask_host.clear();
   HIP_OK(hipMemcpyAsync(ws.tvals, &t, 4, hipMemcpyHostToDevice, stream_));
   HIP_OK(hipStreamSynchronize(stream_));
-  enqueue_tables(ws.tvals, 1);
+  enqueue_tables(ws.one(), 1);
   HIP_OK(launch_step_prep(x, prompt_x, cond, style, B, T, ws.xmel16, ws.cond16, ws.mc16, stream_));
   enqueue_merge_const(W, ws, R, stream_);
   enqueue_merge_step(W, ws, R, stream_, ws.tab);
-  enqueue_estimator(B, T, 0);
+  enqueue_estimator(B, T, ws.tab, ws.nbq, ws.nbw);
   HIP_OK(launch_conv2_rows(ws.y16, W.c2_w, W.c2_b, R, dphi, stream_));
   HIP_OK(hipStreamSynchronize(stream_));
 }
@@ -941,7 +978,7 @@ void Engine::upload_stage_tables(const float* t1_host, const float* t2_host) {
                                kTcondPerStep, stream_));
     HIP_OK(launch_linear_small(ws.t1, 1, 512, W.ada_w, W.ada_b, 1024, 1, 0, ws.tab + kFinalSsOff,
                                kTcondPerStep, stream_));
-    enqueue_norm_bias(1);
+    enqueue_norm_bias(ws.one(), 1);
   }
   if (t2_host) {
     h2d(ws.t2, t2_host, 512 * 4, stream_);
@@ -1005,6 +1042,7 @@ void Engine::stage_attention_core(const float* in, const uint32_t* mask, int B, 
   const int Tpad = (T + 63) / 64 * 64;
   ensure_rope(T);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
+  ws.mask_host.clear();
   h2d(ws.stage_a, in, (size_t)R * 512 * 4, stream_);
   to_f16(ws.stage_a, ws.n16, (size_t)R * 512, stream_);
   GemmArgs g;
@@ -1049,6 +1087,7 @@ void Engine::stage_block(const float* in, const float* t1, const uint32_t* mask,
   ensure_rope(T);
   upload_stage_tables(t1, nullptr);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
+  ws.mask_host.clear();
   h2d(ws.xa, in, (size_t)R * 512 * 4, stream_);
   if (skip) {
     h2d(ws.stage_a, skip, (size_t)R * 512 * 4, stream_);
@@ -1071,6 +1110,7 @@ void Engine::stage_stack(const float* in, const float* t1, const uint32_t* mask,
   ensure_rope(T);
   upload_stage_tables(t1, nullptr);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
+  ws.mask_host.clear();
   h2d(ws.xa, in, (size_t)R * 512 * 4, stream_);
   HIP_OK(launch_norm_prep(ws.xa, ws.tab, W.gamma[0], ws.n16, ws.ssq, R, stream_));
   enqueue_transformer(B, T, ws.tab, ws.nbq, ws.nbw);
@@ -1119,6 +1159,7 @@ void Engine::stage_wavenet(const float* in, const float* t2, const uint32_t* mas
   const int R = B * T;
   upload_stage_tables(nullptr, t2);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
+  ws.mask_host.clear();
   h2d(ws.wn_x, in, (size_t)R * 512 * 4, stream_);
   to_f16(ws.wn_x, ws.wn_x16, (size_t)R * 512, stream_);
   // zero res_projection so FINALSKIP yields the bare WaveNet output
