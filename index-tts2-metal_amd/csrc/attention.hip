@@ -8,29 +8,30 @@
 //
 // Layout: Q, K are [B][8][Tpad][64] f16 (Q already scaled by 1/8 and both
 // RoPE-rotated by the QKV GEMM epilogue); V is stored transposed,
-// Vt [B][8][64][Tpad].  Output O is token-major [B*T][512] f16, heads
+// Vt [B][8][64][Tpad].  The key mask arrives as kbias [B][Tpad] fp32 (0 for
+// a valid key, -inf for a masked or padding key; key_bias_kernel builds it
+// once per mask).  Output O is token-major [B*T][512] f16, heads
 // concatenated in head order.
 //
-// One workgroup = 4 wavefronts = 64 queries of one (branch, head).  Keys are
-// consumed in tiles of 64: the K tile, the V^T tile and the tile's key-mask
-// words are copied global -> LDS with direct loads into a ring of NBUF
-// buffers, so NBUF-1 tiles are in flight while one is computed.  Per wavefront
-// (16 queries) and tile:
-//   S^T(64 keys x 16 queries) = K . Q^T        8 MFMA 16x16x32
+// Keys are consumed in tiles of 64: the K tile, the V^T tile and the tile's
+// bias words are copied global -> LDS with direct loads into a ring of NBUF
+// buffers, so NBUF-1 tiles are in flight while one is computed.  Per
+// wavefront (32 queries) and tile:
+//   S^T(64 keys x 32 queries) = K . Q^T        16 MFMA 16x16x32
 //   running max per query: two xor-shuffles (the 4 lanes sharing a query)
-//   O^T(64 d x 16 queries) += V^T . P^T        8 MFMA 16x16x32
-// Computing both products transposed leaves every query's probabilities,
-// running denominator and 64 outputs in the lanes of that query, so the
-// rescale by exp(m_old - m_new) and the denominator are lane-local and only
-// the max crosses lanes.  A query whose keys are all masked produces zeros.
+//   O^T(64 d x 32 queries) += V^T . P^T        16 MFMA 16x16x32
+//   denominator (ones row) . P^T                4 MFMA 16x16x32
+// Computing the products transposed leaves every query's probabilities,
+// denominator and 64 outputs in the lanes of that query, so the rescale is
+// lane-local and only the max crosses lanes.  A query whose keys are all
+// masked produces zeros, as the reference Metal kernel does.
 #include <type_traits>
 
 #include "device_common.h"
 
 namespace mit2hip {
 
-constexpr int kAttnBuffers = 2;  // K/V^T tile buffers per key group (1 in flight)
-constexpr int kAttnSplitMaxTpad = 2048;  // longest padded sequence that splits its keys
+constexpr int kAttnSplitMaxTpad = 2048;  // longest padded sequence run with two key groups
 
 typedef __attribute__((address_space(3))) void attn_lds_t;
 
@@ -43,10 +44,6 @@ __device__ __forceinline__ void attn_wait_lgkmcnt0() {
   __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));
 }
 
-// 16-byte slot of chunk c in a 128-byte LDS row r (8 slots): conflict-free
-// ds_read_b128 for 16 consecutive rows at one chunk.
-__device__ __forceinline__ int attn_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
-
 template <int I, int N, typename F>
 __device__ __forceinline__ void attn_static_for(F&& f) {
   if constexpr (I < N) {
@@ -55,194 +52,230 @@ __device__ __forceinline__ void attn_static_for(F&& f) {
   }
 }
 
-template <int NBUF, int SPLIT>
-__global__ __launch_bounds__(256 * SPLIT) void attention_kernel(const half_t* __restrict__ Q,
-                                                        const half_t* __restrict__ K,
-                                                        const half_t* __restrict__ Vt,
-                                                        const uint32_t* __restrict__ mask,
-                                                        half_t* __restrict__ O, int T, int Tpad) {
-  static_assert(NBUF >= 2 && NBUF <= 4, "2..4 tile buffers");
-  static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "key split");
-  // One __shared__ object per buffer (K, V^T, and one mask copy per wave);
-  // each key group g has its own region inside every buffer.
-  constexpr int KV = 64 * 64 * SPLIT;
-  __shared__ __attribute__((aligned(1024))) half_t sK0[KV];
-  __shared__ __attribute__((aligned(1024))) half_t sK1[KV];
-  __shared__ __attribute__((aligned(1024))) half_t sK2[NBUF > 2 ? KV : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sK3[NBUF > 3 ? KV : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sV0[KV];
-  __shared__ __attribute__((aligned(1024))) half_t sV1[KV];
-  __shared__ __attribute__((aligned(1024))) half_t sV2[NBUF > 2 ? KV : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sV3[NBUF > 3 ? KV : 8];
-  __shared__ __attribute__((aligned(1024))) uint32_t sM0[4 * 64 * SPLIT];
-  __shared__ __attribute__((aligned(1024))) uint32_t sM1[4 * 64 * SPLIT];
-  __shared__ __attribute__((aligned(1024))) uint32_t sM2[NBUF > 2 ? 4 * 64 * SPLIT : 4];
-  __shared__ __attribute__((aligned(1024))) uint32_t sM3[NBUF > 3 ? 4 * 64 * SPLIT : 4];
-  // (m, l, O) of key group 1 for the two-group merge: 4 waves x 64 lanes x
-  // 18 floats.  With four groups, groups 1..3 park in the K0 / V0 / K1 tile
-  // buffers instead (each holds 32 KB then), which are free after the loop.
-  __shared__ __attribute__((aligned(1024))) float sPark[SPLIT == 2 ? 4 * 64 * 18 : 4];
+// ---------------------------------------------------------------------------
+// One wavefront = 32 queries (two 16-query MFMA blocks),
+// so every K and V^T fragment read from LDS feeds two MFMAs.  A workgroup is
+// G key groups x 2 query waves = 64 queries of one (branch, head); group g
+// walks its own share of the key tiles with its own LDS ring, and the groups
+// merge (m, l, O) at the end.
+//
+// Softmax arithmetic per score is what bounds this kernel (the matrix cores
+// have slack), so it is kept to one FMA, a share of a max, a subtract and an
+// exp2:
+//  * scores are kept in log2 units, s2 = s * log2(e) + kbias[key], where the
+//    per-key bias is 0 for a valid key and -inf for a masked or padding key
+//    (built once per mask by key_bias_kernel), so masking costs nothing;
+//  * the running max m moves only when a tile's max exceeds it by more than
+//    8: probabilities exp2(s2 - m) then stay <= 2^8, well inside f16, and the
+//    O rescale is skipped for the whole wave in the common case;
+//  * the denominator is a fifth MFMA block whose A operand is a row of ones:
+//    l = sum of the f16 probabilities the PV product used, accumulated in
+//    fp32 by the matrix core.
+//
+// Key order inside a 64-key tile.  S^T block kb (16 keys) loads K row
+//   krow(kb, r) = 32 (kb >> 1) + 8 (r >> 2) + 4 (kb & 1) + (r & 3)
+// into MFMA row r, so the 4 scores a lane holds for blocks 2c and 2c+1 belong
+// to the 8 consecutive keys 32 c + 8 lg + (0..7): exactly the K-slots the
+// lane supplies to O^T += V^T . P^T, whose V^T fragment is then one 16-byte
+// LDS read.  The permutation only reorders the keys within a tile.
+//
+// LDS swizzles (16-byte slot of chunk c in a 128-byte row r): K rows are read
+// in the permuted order, V^T rows in natural order, each with its own key.
+__device__ __forceinline__ int attn_kslot(int r, int c) { return c ^ ((r & 3) | (((r >> 3) & 1) << 2)); }
+__device__ __forceinline__ int attn_vslot(int r, int c) { return c ^ (r & 7); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyMax = 8.0f;  // log2 headroom before the running max moves
+
+template <int NBUF, int G>
+__global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __restrict__ Q,
+                                                             const half_t* __restrict__ K,
+                                                             const half_t* __restrict__ Vt,
+                                                             const float* __restrict__ kbias,
+                                                             half_t* __restrict__ O, int T, int Tpad) {
+  static_assert(NBUF >= 2 && NBUF <= 3, "2..3 tile buffers");
+  static_assert(G == 1 || G == 2 || G == 4, "key groups");
+  constexpr int TILE = 64 * 64;  // halves in one K or V^T tile
+  __shared__ __attribute__((aligned(1024))) half_t sK0[G * TILE];
+  __shared__ __attribute__((aligned(1024))) half_t sK1[G * TILE];
+  __shared__ __attribute__((aligned(1024))) half_t sK2[NBUF > 2 ? G * TILE : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sV0[G * TILE];
+  __shared__ __attribute__((aligned(1024))) half_t sV1[G * TILE];
+  __shared__ __attribute__((aligned(1024))) half_t sV2[NBUF > 2 ? G * TILE : 8];
+  // key-bias words of the tile, one copy per wave (so each wave's own vmcnt covers it)
+  __shared__ __attribute__((aligned(1024))) float sB0[G * 2 * 64];
+  __shared__ __attribute__((aligned(1024))) float sB1[G * 2 * 64];
+  __shared__ __attribute__((aligned(1024))) float sB2[NBUF > 2 ? G * 2 * 64 : 4];
   auto bufK = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
-    if constexpr (s == 0) return sK0; else if constexpr (s == 1) return sK1;
-    else if constexpr (s == 2) return sK2; else return sK3;
+    if constexpr (s == 0) return sK0; else if constexpr (s == 1) return sK1; else return sK2;
   };
   auto bufV = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
-    if constexpr (s == 0) return sV0; else if constexpr (s == 1) return sV1;
-    else if constexpr (s == 2) return sV2; else return sV3;
+    if constexpr (s == 0) return sV0; else if constexpr (s == 1) return sV1; else return sV2;
   };
-  auto bufM = [&](auto st) -> uint32_t* {
+  auto bufB = [&](auto st) -> float* {
     constexpr int s = decltype(st)::value;
-    if constexpr (s == 0) return sM0; else if constexpr (s == 1) return sM1;
-    else if constexpr (s == 2) return sM2; else return sM3;
+    if constexpr (s == 0) return sB0; else if constexpr (s == 1) return sB1; else return sB2;
   };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = (tid >> 6) & 3;  // query block of this wave within the workgroup
-  const int grp = tid >> 8;         // key group (SPLIT groups share the 64 queries)
+  const int qw = (tid >> 6) & 1;  // query wave within the group
+  const int grp = tid >> 7;       // key group
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int b = blockIdx.z;
   const int h = blockIdx.y;
-  const int q0 = blockIdx.x * 64 + wave * 16;
+  const int q0 = blockIdx.x * 64 + qw * 32;
   const size_t head = (size_t)b * 8 + h;
   const half_t* Qh = Q + head * Tpad * 64;
   const half_t* Kh = K + head * Tpad * 64;
   const half_t* Vh = Vt + head * 64 * Tpad;
-  const uint32_t* mrow = mask + (size_t)b * T;
+  const float* brow = kbias + (size_t)b * Tpad;
   const int ntiles = Tpad / 64;
-  // Key group grp walks tiles [grp*tpg, grp*tpg + tpg); tiles past the end
-  // are loaded clamped and contribute nothing (every key >= T is masked), so
-  // all groups run the same iterations and meet at the same barriers.
-  const int tpg = (ntiles + SPLIT - 1) / SPLIT;
+  // Group grp walks tiles [grp*tpg, grp*tpg + tpg).  A tile index past the
+  // end loads the last tile again (clamped) and its scores are forced to
+  // -inf, so every group runs the same iterations and meets at the same
+  // barriers.
+  const int tpg = (ntiles + G - 1) / G;
   const int tbase = grp * tpg;
 
-  // Each wave moves 2 KB of K, 2 KB of V^T and its own 256-byte mask copy:
-  // 5 direct loads per wave per tile.
+  // Per tile each wave moves half of the K and V^T tiles (4 + 4 direct loads
+  // of 1 KB) and its own copy of the 64 bias words: 9 loads.
+  constexpr int kLoads = 9;
   auto issue = [&](auto st, int j) {
     const int kt = min(tbase + j, ntiles - 1);
-    half_t* sk = bufK(st) + grp * 64 * 64;
-    half_t* sv = bufV(st) + grp * 64 * 64;
-    uint32_t* sm = bufM(st) + grp * 256;
+    half_t* sk = bufK(st) + grp * TILE;
+    half_t* sv = bufV(st) + grp * TILE;
+    float* sb = bufB(st) + (grp * 2 + qw) * 64;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int qq0 = (wave * 2 + j) * 64;
-      const int q = qq0 + lane;
+    for (int u = 0; u < 4; ++u) {
+      const int s0 = (qw * 4 + u) * 64;  // first 16-byte slot of this load
+      const int q = s0 + lane;
       const int row = q >> 3;
-      const int c = attn_slot(row, q & 7);
-      __builtin_amdgcn_global_load_lds((const void*)(Kh + (size_t)(kt * 64 + row) * 64 + c * 8),
-                                       (attn_lds_t*)(sk + qq0 * 8), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(Vh + (size_t)row * Tpad + kt * 64 + c * 8),
-                                       (attn_lds_t*)(sv + qq0 * 8), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(Kh + (size_t)(kt * 64 + row) * 64 + attn_kslot(row, q & 7) * 8),
+          (attn_lds_t*)(sk + s0 * 8), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(Vh + (size_t)row * Tpad + kt * 64 + attn_vslot(row, q & 7) * 8),
+          (attn_lds_t*)(sv + s0 * 8), 16, 0, 0);
     }
-    const int key = min(kt * 64 + lane, T - 1);  // keys >= T are rejected at use
-    __builtin_amdgcn_global_load_lds((const void*)(mrow + key), (attn_lds_t*)(sm + wave * 64), 4, 0,
-                                     0);
+    __builtin_amdgcn_global_load_lds((const void*)(brow + kt * 64 + lane), (attn_lds_t*)sb, 4, 0, 0);
   };
 
-  // B operand of S^T = K.Q^T: this lane's query row, d-slots of lane group lg.
-  const half8 qf0 = *reinterpret_cast<const half8*>(Qh + (size_t)(q0 + lr) * 64 + lg * 8);
-  const half8 qf1 = *reinterpret_cast<const half8*>(Qh + (size_t)(q0 + lr) * 64 + 32 + lg * 8);
-
-  floatx4 o[4];  // o[db][i] = O[query q0+lr][d = 16*db + 4*lg + i] (unnormalised)
+  // B operands of S^T = K.Q^T: query rows q0 + 16 qb + lr, d-slots of lane group lg.
+  half8 qf[2][2];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max of query lr (same in its 4 lanes)
-  float l_run = 0.0f;       // this lane's share of the running denominator
+  for (int qb = 0; qb < 2; ++qb) {
+    const half_t* qp = Qh + (size_t)(q0 + 16 * qb + lr) * 64 + lg * 8;
+    qf[qb][0] = *reinterpret_cast<const half8*>(qp);
+    qf[qb][1] = *reinterpret_cast<const half8*>(qp + 32);
+  }
+  // A operand of the denominator block: row 0 all ones, rows 1..15 zero.
+  half8 ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = lr == 0 ? (half_t)1.0f : (half_t)0.0f;
+
+  floatx4 o[4][2];  // o[db][qb][i] = O[query q0+16qb+lr][d = 16 db + 4 lg + i] (unnormalised)
+  floatx4 o5[2];    // o5[qb][0] in lane group 0: the running denominator of query q0+16qb+lr
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    o5[qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  float m_run[2] = {-INFINITY, -INFINITY};  // running max (log2 units), same in a query's 4 lanes
 
   auto compute = [&](auto st, int j) {
-    const int kt = tbase + j;  // unclamped: a tile past the end has every key >= T
-    const half_t* sk = bufK(st) + grp * 64 * 64;
-    const half_t* sv = bufV(st) + grp * 64 * 64;
-    const uint32_t* sm = bufM(st) + grp * 256 + wave * 64;
-    // Scores: sc[kb][i] = S[key kt*64 + kb*16 + 4*lg + i][query q0 + lr]
-    floatx4 sc[4];
+    const int kt = tbase + j;  // unclamped: a tile past the end is masked out entirely
+    const half_t* sk = bufK(st) + grp * TILE;
+    const half_t* sv = bufV(st) + grp * TILE;
+    const float* sb = bufB(st) + (grp * 2 + qw) * 64;
+    // sc[kb][qb][i] = S[key kt*64 + 32 (kb>>1) + 8 lg + 4 (kb&1) + i][query q0 + 16 qb + lr]
+    floatx4 sc[4][2];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const int row = kb * 16 + lr;
-      const half8 kf0 = *reinterpret_cast<const half8*>(sk + row * 64 + attn_slot(row, lg) * 8);
-      const half8 kf1 = *reinterpret_cast<const half8*>(sk + row * 64 + attn_slot(row, 4 + lg) * 8);
-      floatx4 z = {0.f, 0.f, 0.f, 0.f};
-      z = mfma16x16x32(kf0, qf0, z);
-      sc[kb] = mfma16x16x32(kf1, qf1, z);
+      const int row = 32 * (kb >> 1) + 8 * (lr >> 2) + 4 * (kb & 1) + (lr & 3);
+      const half8 kf0 = *reinterpret_cast<const half8*>(sk + row * 64 + attn_kslot(row, lg) * 8);
+      const half8 kf1 = *reinterpret_cast<const half8*>(sk + row * 64 + attn_kslot(row, 4 + lg) * 8);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        floatx4 z = {0.f, 0.f, 0.f, 0.f};
+        z = mfma16x16x32(kf0, qf[qb][0], z);
+        sc[kb][qb] = mfma16x16x32(kf1, qf[qb][1], z);
+      }
     }
-    float tmax = -INFINITY;
+    const float past = kt < ntiles ? 0.0f : -INFINITY;  // a clamped tile past the end
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const uint4 mk = *reinterpret_cast<const uint4*>(sm + kb * 16 + lg * 4);
-      const uint32_t mv[4] = {mk.x, mk.y, mk.z, mk.w};
+      const float4 bb = *reinterpret_cast<const float4*>(sb + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1));
+      const float bv[4] = {bb.x + past, bb.y + past, bb.z + past, bb.w + past};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kt * 64 + kb * 16 + lg * 4 + i;
-        const bool valid = (key < T) & (mv[i] != 0u);
-        const float v = valid ? sc[kb][i] : -INFINITY;
-        sc[kb][i] = v;
-        tmax = fmaxf(tmax, v);
-      }
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[kb][qb][i] = fmaf(sc[kb][qb][i], kLog2e, bv[i]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;  // all keys so far masked
-    const float alpha = __expf(m_run - m_use);                  // m_run = -inf -> 0
-    float psum = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int qb = 0; qb < 2; ++qb) {
+      float tmax = fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3]));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pv = __expf(sc[kb][i] - m_use);  // masked -> 0
-        sc[kb][i] = pv;
-        psum += pv;
+      for (int kb = 1; kb < 4; ++kb)
+        tmax = fmaxf(tmax, fmaxf(fmaxf(sc[kb][qb][0], sc[kb][qb][1]), fmaxf(sc[kb][qb][2], sc[kb][qb][3])));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+      // Lazy max: move m only when this tile's max exceeds it by > kLazyMax
+      // (from -inf: as soon as any key is valid).
+      const float m_old = m_run[qb];
+      const bool need = tmax > m_old + kLazyMax;
+      if (__any(need)) {
+        const float m_new = need ? tmax : m_old;
+        const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);  // -inf -> 0; unchanged -> 1
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
+        o5[qb] *= alpha;
+        m_run[qb] = m_new;
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+      const float m_use = m_run[qb] == -INFINITY ? 0.0f : m_run[qb];  // nothing valid yet
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] *= alpha;
-    // O^T += V^T . P^T over two 32-key chunks.  K-slot j of lane group lg is
-    // key 32c + 4*lg + j (j < 4) or 32c + 16 + 4*lg + (j - 4) (j >= 4): the
-    // keys this lane's probabilities belong to; V^T rows are read with the
-    // same map.
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[kb][qb][i] = __builtin_amdgcn_exp2f(sc[kb][qb][i] - m_use);
+    }
+    // O^T += V^T . P^T over two 32-key chunks; K-slot j of lane group lg is
+    // key 32 c + 8 lg + j in both operands.  The ones block sums P.
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      half8 pb;
+      half8 pb[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pb[j] = (half_t)sc[2 * c][j];
-        pb[4 + j] = (half_t)sc[2 * c + 1][j];
-      }
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pb[qb][i] = (half_t)sc[2 * c][qb][i];
+          pb[qb][4 + i] = (half_t)sc[2 * c + 1][qb][i];
+        }
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const int row = db * 16 + lr;
-        const int k0 = c * 32 + lg * 4;       // keys k0..k0+3 and k0+16..k0+19
-        const half4 v0 = *reinterpret_cast<const half4*>(
-            sv + row * 64 + attn_slot(row, k0 >> 3) * 8 + (k0 & 7));
-        const half4 v1 = *reinterpret_cast<const half4*>(
-            sv + row * 64 + attn_slot(row, (k0 + 16) >> 3) * 8 + (k0 & 7));
-        half8 va;
-        va[0] = v0[0]; va[1] = v0[1]; va[2] = v0[2]; va[3] = v0[3];
-        va[4] = v1[0]; va[5] = v1[1]; va[6] = v1[2]; va[7] = v1[3];
-        o[db] = mfma16x16x32(va, pb, o[db]);
+        const half8 va = *reinterpret_cast<const half8*>(sv + row * 64 + attn_vslot(row, 4 * c + lg) * 8);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) o[db][qb] = mfma16x16x32(va, pb[qb], o[db][qb]);
       }
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) o5[qb] = mfma16x16x32(ones, pb[qb], o5[qb]);
     }
   };
 
-  // NBUF-buffer pipeline.  The steady-state body is branch-free (the issue
-  // past the last tile repeats the last tile into a buffer that is not read
-  // again), so the compiler keeps only the explicit vmcnt waits; the last
-  // ntiles % NBUF tiles are already resident when the loop exits.
   attn_static_for<0, NBUF - 1>([&](auto st) { issue(st, min((int)decltype(st)::value, tpg - 1)); });
-  attn_wait_vmcnt<5 * (NBUF - 1)>();  // the Q fragments (issued before the prologue) have landed
+  attn_wait_vmcnt<kLoads * (NBUF - 1)>();  // the Q fragments (issued before the prologue) have landed
   int kt0 = 0;
   for (; kt0 + NBUF <= tpg; kt0 += NBUF) {
     attn_static_for<0, NBUF>([&](auto st) {
       constexpr int s = decltype(st)::value;
-      attn_wait_lgkmcnt0();
-      __builtin_amdgcn_s_barrier();
+      attn_wait_vmcnt<kLoads * (NBUF - 2)>();  // this wave's share of tile kt0+s has landed
+      attn_wait_lgkmcnt0();                    // its reads of tile kt0+s-1 have returned
+      __builtin_amdgcn_s_barrier();            // ... for every wave
       issue(std::integral_constant<int, (s + NBUF - 1) % NBUF>{}, min(kt0 + s + NBUF - 1, tpg - 1));
-      attn_wait_vmcnt<5 * (NBUF - 1)>();
-      __builtin_amdgcn_s_barrier();
       compute(st, kt0 + s);
     });
   }
@@ -252,88 +285,113 @@ __global__ __launch_bounds__(256 * SPLIT) void attention_kernel(const half_t* __
     if (kt0 + (int)decltype(st)::value < tpg) compute(st, kt0 + decltype(st)::value);
   });
 
-  // Denominator: sum of the 4 lane shares of the query.
-  l_run += __shfl_xor(l_run, 16, kWave);
-  l_run += __shfl_xor(l_run, 32, kWave);
-  if constexpr (SPLIT > 1) {
-    // Merge the key groups: groups 1.. park (m, l, O) in LDS; group 0
-    // rescales every part to the common max.
-    auto park_of = [&](int g) -> float* {
-      if constexpr (SPLIT == 2) {
-        return sPark + (wave * 64 + lane) * 18;
-      } else {
-        float* base = reinterpret_cast<float*>(g == 1 ? sK0 : g == 2 ? sV0 : sK1);
-        return base + (wave * 64 + lane) * 18;
-      }
+  // Denominator of each query: component 0 of the ones block in lane group 0.
+  float l_run[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) l_run[qb] = __shfl(o5[qb][0], lr, kWave);
+  if constexpr (G > 1) {
+    // Groups 1.. park (m, l, O) in the tile buffers, free once every wave is
+    // past its last tile: the 32 O values of group g's lane in 16 KB of sK0
+    // (g = 1, 2; sK0 holds G x 8 KB) or sK1 (g = 3), its two (m, l) pairs in
+    // sV0.  Group 0 then rescales every part to the common max.
+    auto park_o = [&](int g) -> float* {
+      float* base = reinterpret_cast<float*>(g <= 2 ? sK0 : sK1);
+      return base + ((g - 1) & 1) * 4096 + (qw * 64 + lane) * 32;
     };
-    if constexpr (SPLIT == 4) {
-      // every wave's last tile reads are done before tile buffers are reused
-      attn_wait_lgkmcnt0();
-      __syncthreads();
-    }
+    auto park_ml = [&](int g) -> float* {
+      return reinterpret_cast<float*>(sV0) + ((g - 1) * 128 + qw * 64 + lane) * 4;
+    };
+    attn_wait_lgkmcnt0();
+    __syncthreads();
     if (grp > 0) {
-      float* p = park_of(grp);
+      float* po = park_o(grp);
+      float* pm = park_ml(grp);
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[db * 4 + i] = o[db][i];
-      p[16] = m_run;
-      p[17] = l_run;
+        for (int db = 0; db < 4; ++db)
+          *reinterpret_cast<floatx4*>(po + qb * 16 + db * 4) = o[db][qb];
+        pm[qb * 2] = m_run[qb];
+        pm[qb * 2 + 1] = l_run[qb];
+      }
     }
-    attn_wait_lgkmcnt0();  // the parked values are in LDS before any wave passes the barrier
-    __builtin_amdgcn_s_barrier();
+    attn_wait_lgkmcnt0();
+    __syncthreads();
     if (grp > 0) return;
-    float mstar = m_run;
 #pragma unroll
-    for (int g = 1; g < SPLIT; ++g) mstar = fmaxf(mstar, park_of(g)[16]);
-    const float mref = mstar == -INFINITY ? 0.0f : mstar;
-    const float w0 = __expf(m_run - mref);
-    l_run *= w0;
+    for (int qb = 0; qb < 2; ++qb) {
+      float mstar = m_run[qb];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] *= w0;
+      for (int g = 1; g < G; ++g) mstar = fmaxf(mstar, park_ml(g)[qb * 2]);
+      const float mref = mstar == -INFINITY ? 0.0f : mstar;
+      const float w0 = __builtin_amdgcn_exp2f(m_run[qb] - mref);
+      l_run[qb] *= w0;
 #pragma unroll
-    for (int g = 1; g < SPLIT; ++g) {
-      const float* p = park_of(g);
-      const float wg = __expf(p[16] - mref);
-      l_run += wg * p[17];
+      for (int db = 0; db < 4; ++db) o[db][qb] *= w0;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int g = 1; g < G; ++g) {
+        const float* po = park_o(g) + qb * 16;
+        const float* pm = park_ml(g) + qb * 2;
+        const float wg = __builtin_amdgcn_exp2f(pm[0] - mref);
+        l_run[qb] += wg * pm[1];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[db][i] += wg * p[db * 4 + i];
+        for (int db = 0; db < 4; ++db) o[db][qb] += wg * *reinterpret_cast<const floatx4*>(po + db * 4);
+      }
     }
   }
-  const int q = q0 + lr;
-  if (q < T) {
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    half_t* dst = O + ((size_t)b * T + q) * 512 + h * 64 + lg * 4;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      half4 v;
-      v[0] = (half_t)(o[db][0] * inv);
-      v[1] = (half_t)(o[db][1] * inv);
-      v[2] = (half_t)(o[db][2] * inv);
-      v[3] = (half_t)(o[db][3] * inv);
-      *reinterpret_cast<half4*>(dst + db * 16) = v;
+  for (int qb = 0; qb < 2; ++qb) {
+    const int q = q0 + 16 * qb + lr;
+    if (q < T) {
+      const float inv = l_run[qb] > 0.0f ? 1.0f / l_run[qb] : 0.0f;
+      half_t* dst = O + ((size_t)b * T + q) * 512 + h * 64 + lg * 4;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        half4 v;
+        v[0] = (half_t)(o[db][qb][0] * inv);
+        v[1] = (half_t)(o[db][qb][1] * inv);
+        v[2] = (half_t)(o[db][qb][2] * inv);
+        v[3] = (half_t)(o[db][qb][3] * inv);
+        *reinterpret_cast<half4*>(dst + db * 16) = v;
+      }
     }
   }
 }
 
+// kbias[b][t] = 0 for a valid key (t < T, mask != 0), -inf otherwise, for
+// t < Tpad: the additive key mask of attention32_kernel (log2 units).
+__global__ void key_bias_kernel(const uint32_t* __restrict__ mask, int B, int T, int Tpad,
+                                float* __restrict__ kbias) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * Tpad) return;
+  const int b = i / Tpad, t = i - b * Tpad;
+  kbias[i] = (t < T && mask[(size_t)b * T + t] != 0u) ? 0.0f : -INFINITY;
+}
+
+hipError_t launch_key_bias(const uint32_t* mask, int B, int T, int Tpad, float* kbias,
+                           hipStream_t stream) {
+  if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
+  const int n = B * Tpad;
+  hipLaunchKernelGGL(key_bias_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, mask, B, T, Tpad,
+                     kbias);
+  return hipGetLastError();
+}
+
 hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
-                            const uint32_t* mask, half_t* O, int B, int T, int Tpad,
+                            const float* kbias, half_t* O, int B, int T, int Tpad,
                             hipStream_t stream) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
   dim3 grid((T + 63) / 64, 8, B);
-  // Short and medium sequences give few query tiles and leave most SIMDs with
-  // one wave: split the keys of each workgroup over two wave groups (a
-  // four-group split, also built, measured slower at T = 860 on MI355X).
-  // The choice depends on the sequence length only, never on the batch, so a
-  // request's output does not depend on what it is batched with.
+  // Two key groups fill the CUs best up to Tpad = 2048 (T = 860: 224
+  // workgroups); longer sequences split the keys four ways.  The choice
+  // depends on the sequence length only, never on the batch, so a request's
+  // output does not depend on what it is batched with.
   if (Tpad <= kAttnSplitMaxTpad)
-    hipLaunchKernelGGL((attention_kernel<kAttnBuffers, 2>), grid, dim3(512), 0, stream, Q, K, Vt,
-                       mask, O, T, Tpad);
+    hipLaunchKernelGGL((attention32_kernel<2, 2>), grid, dim3(256), 0, stream, Q, K, Vt, kbias, O,
+                       T, Tpad);
   else
-    hipLaunchKernelGGL((attention_kernel<kAttnBuffers, 1>), grid, dim3(256), 0, stream, Q, K, Vt,
-                       mask, O, T, Tpad);
+    hipLaunchKernelGGL((attention32_kernel<2, 4>), grid, dim3(512), 0, stream, Q, K, Vt, kbias, O,
+                       T, Tpad);
   return hipGetLastError();
 }
 

@@ -211,6 +211,7 @@ struct Workspace {
   float* fin;
   half_t* y16;
   uint32_t* mask;
+  float* kbias;  // [B][Tpad] attention key bias (0 valid, -inf masked/padding), from mask
   uint32_t* P;
   float2* rope;
   float* tvals;
@@ -429,6 +430,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   h(r * 512); h(r * 1536); h(r * 512);
   f(r * 512); h(r * 512); f(r * 512); f(r * 512); h(r * 512); f(r * 512); h(r * 512);
   bytes += (r * 4 + 255) / 256 * 256 + ((size_t)cReq * 4 + 255) / 256 * 256;
+  f((size_t)cRpad);
   f((size_t)cT * 64);
   f(cS); f((size_t)cS * 256); f((size_t)cS * 512); f((size_t)cS * 512); f((size_t)cS * 512);
   f((size_t)cS * kTcondPerStep);
@@ -465,6 +467,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   ws.fin = F(r * 512);
   ws.y16 = H(r * 512);
   ws.mask = static_cast<uint32_t*>(a.take(r * 4));
+  ws.kbias = F((size_t)cRpad);
   ws.P = static_cast<uint32_t*>(a.take((size_t)cReq * 4));
   ws.rope = reinterpret_cast<float2*>(F((size_t)cT * 64));
   ws.tvals = F(cS);
@@ -625,7 +628,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, s));
   }
-  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.mask, ws.o16, B, T, Tpad, s));
+  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, s));
   {
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
@@ -758,6 +761,7 @@ void Engine::enqueue_decode(const float* x0, const float* prompt, const float* c
   const float dt = 1.0f / (float)steps;
   HIP_OK(launch_decode_prep(x0, prompt, cond, style, ws.P, nreq, T, cfg_on, ws.x_cur, ws.xmel16,
                             ws.cond16, ws.mc16, stream_));
+  HIP_OK(launch_key_bias(ws.mask, B, T, (T + 63) / 64 * 64, ws.kbias, stream_));
   enqueue_merge_const(W, ws, R, stream_);
   for (int s = 0; s < steps; ++s) {
     const float* tab = tb.tab + (size_t)s * kTcondPerStep;
@@ -852,6 +856,7 @@ void Engine::estimator_step_device(const float* x, const float* prompt_x, const 
   ensure_rope(T);
   HIP_OK(hipMemcpyAsync(ws.mask, mask, (size_t)R * 4, hipMemcpyDeviceToDevice, stream_));
   ws.mask_host.clear();
+  HIP_OK(launch_key_bias(ws.mask, B, T, (T + 63) / 64 * 64, ws.kbias, stream_));
   HIP_OK(hipMemcpyAsync(ws.tvals, &t, 4, hipMemcpyHostToDevice, stream_));
   HIP_OK(hipStreamSynchronize(stream_));
   enqueue_tables(ws.one(), 1);
@@ -921,7 +926,7 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
       break;
     }
     case 4: {  // masked flash attention
-      loop([&] { HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.mask, ws.o16, B, T, Tpad, stream_)); });
+      loop([&] { HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, stream_)); });
       f = 4.0 * 64.0 * 8.0 * B * (double)T * (double)T;
       by = 2.0 * 3.0 * B * 8 * (double)T * 64 + 2.0 * R * 512 + 4.0 * R;
       nm = "attention";
@@ -1043,13 +1048,14 @@ void Engine::stage_attention_core(const float* in, const uint32_t* mask, int B, 
   ensure_rope(T);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
   ws.mask_host.clear();
+  HIP_OK(launch_key_bias(ws.mask, B, T, (T + 63) / 64 * 64, ws.kbias, stream_));
   h2d(ws.stage_a, in, (size_t)R * 512 * 4, stream_);
   to_f16(ws.stage_a, ws.n16, (size_t)R * 512, stream_);
   GemmArgs g;
   g.M = R; g.N = 1536; g.K = 512; g.A = ws.n16; g.lda = 512; g.W = W.qkv_w[layer]; g.ldw = 512;
   g.T = T; g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, stream_));
-  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.mask, ws.o16, B, T, Tpad, stream_));
+  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, stream_));
   GemmArgs o;
   o.M = R; o.N = 512; o.K = 512; o.A = ws.o16; o.lda = 512; o.W = W.wo_w[layer]; o.ldw = 512;
   o.C32 = ws.stage_b; o.ldc32 = 512;
@@ -1088,6 +1094,7 @@ void Engine::stage_block(const float* in, const float* t1, const uint32_t* mask,
   upload_stage_tables(t1, nullptr);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
   ws.mask_host.clear();
+  HIP_OK(launch_key_bias(ws.mask, B, T, (T + 63) / 64 * 64, ws.kbias, stream_));
   h2d(ws.xa, in, (size_t)R * 512 * 4, stream_);
   if (skip) {
     h2d(ws.stage_a, skip, (size_t)R * 512 * 4, stream_);
@@ -1111,6 +1118,7 @@ void Engine::stage_stack(const float* in, const float* t1, const uint32_t* mask,
   upload_stage_tables(t1, nullptr);
   h2d(ws.mask, mask, (size_t)R * 4, stream_);
   ws.mask_host.clear();
+  HIP_OK(launch_key_bias(ws.mask, B, T, (T + 63) / 64 * 64, ws.kbias, stream_));
   h2d(ws.xa, in, (size_t)R * 512 * 4, stream_);
   HIP_OK(launch_norm_prep(ws.xa, ws.tab, W.gamma[0], ws.n16, ws.ssq, R, stream_));
   enqueue_transformer(B, T, ws.tab, ws.nbq, ws.nbw);

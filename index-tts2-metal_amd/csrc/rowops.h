@@ -20,10 +20,14 @@ hipError_t launch_norm_bias(const float* ab, int ab_ld, int S, const half_t* W, 
 // Final-layer AdaLN: LayerNorm (no affine, eps 1e-6), then * (1 + scale) + shift (width 512)
 hipError_t launch_adaln(const float* x, const float* shift, const float* scale, half_t* out16,
                         int rows, hipStream_t s);
-// Masked attention (attention.hip).
+// Masked attention (attention.hip).  kbias [B][Tpad]: 0 for a valid key,
+// -inf for a masked or padding key, as launch_key_bias builds it from the
+// [B][T] 0/1 key mask.
 hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
-                            const uint32_t* mask, half_t* O, int B, int T, int Tpad,
+                            const float* kbias, half_t* O, int B, int T, int Tpad,
                             hipStream_t stream);
+hipError_t launch_key_bias(const uint32_t* mask, int B, int T, int Tpad, float* kbias,
+                           hipStream_t stream);
 
 // Decode set-up for nreq requests of T tokens (branches b = 2r (cond), 2r+1 (null)
 // when cfg is on, b = r when off):
