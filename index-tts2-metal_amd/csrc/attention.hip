@@ -31,7 +31,7 @@
 
 namespace mit2hip {
 
-constexpr int kAttnSplitMaxTpad = 2048;  // longest padded sequence run with two key groups
+constexpr int kAttnWideMinTpad = 2048;  // longer padded sequences use 32-query waves
 
 typedef __attribute__((address_space(3))) void attn_lds_t;
 
@@ -87,15 +87,20 @@ __device__ __forceinline__ int attn_vslot(int r, int c) { return c ^ (r & 7); }
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;  // log2 headroom before the running max moves
 
-template <int NBUF, int G>
-__global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __restrict__ Q,
-                                                             const half_t* __restrict__ K,
-                                                             const half_t* __restrict__ Vt,
-                                                             const float* __restrict__ kbias,
-                                                             half_t* __restrict__ O, int T, int Tpad) {
+template <int NBUF, int G, int QB, int NQW>
+__global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* __restrict__ Q,
+                                                                const half_t* __restrict__ K,
+                                                                const half_t* __restrict__ Vt,
+                                                                const float* __restrict__ kbias,
+                                                                half_t* __restrict__ O, int T, int Tpad) {
   static_assert(NBUF >= 2 && NBUF <= 3, "2..3 tile buffers");
   static_assert(G == 1 || G == 2 || G == 4, "key groups");
-  constexpr int TILE = 64 * 64;  // halves in one K or V^T tile
+  static_assert(QB == 1 || QB == 2, "16-query blocks per wave");
+  static_assert(NQW == 1 || NQW == 2 || NQW == 4, "query waves per group");
+  static_assert(NQW * QB <= 4, "the merge parks at most 64 queries per group");
+  constexpr int TILE = 64 * 64;      // halves in one K or V^T tile
+  constexpr int QWG = 16 * QB * NQW; // queries per workgroup
+  constexpr int NW = NQW * G;        // waves per workgroup
   __shared__ __attribute__((aligned(1024))) half_t sK0[G * TILE];
   __shared__ __attribute__((aligned(1024))) half_t sK1[G * TILE];
   __shared__ __attribute__((aligned(1024))) half_t sK2[NBUF > 2 ? G * TILE : 8];
@@ -103,9 +108,9 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
   __shared__ __attribute__((aligned(1024))) half_t sV1[G * TILE];
   __shared__ __attribute__((aligned(1024))) half_t sV2[NBUF > 2 ? G * TILE : 8];
   // key-bias words of the tile, one copy per wave (so each wave's own vmcnt covers it)
-  __shared__ __attribute__((aligned(1024))) float sB0[G * 2 * 64];
-  __shared__ __attribute__((aligned(1024))) float sB1[G * 2 * 64];
-  __shared__ __attribute__((aligned(1024))) float sB2[NBUF > 2 ? G * 2 * 64 : 4];
+  __shared__ __attribute__((aligned(1024))) float sB0[NW * 64];
+  __shared__ __attribute__((aligned(1024))) float sB1[NW * 64];
+  __shared__ __attribute__((aligned(1024))) float sB2[NBUF > 2 ? NW * 64 : 4];
   auto bufK = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
     if constexpr (s == 0) return sK0; else if constexpr (s == 1) return sK1; else return sK2;
@@ -121,13 +126,14 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int qw = (tid >> 6) & 1;  // query wave within the group
-  const int grp = tid >> 7;       // key group
+  const int wv = tid >> 6;
+  const int qw = wv % NQW;  // query wave within the group
+  const int grp = wv / NQW; // key group
   const int lr = lane & 15;
   const int lg = lane >> 4;
   const int b = blockIdx.z;
   const int h = blockIdx.y;
-  const int q0 = blockIdx.x * 64 + qw * 32;
+  const int q0 = blockIdx.x * QWG + qw * 16 * QB;
   const size_t head = (size_t)b * 8 + h;
   const half_t* Qh = Q + head * Tpad * 64;
   const half_t* Kh = K + head * Tpad * 64;
@@ -141,17 +147,19 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
   const int tpg = (ntiles + G - 1) / G;
   const int tbase = grp * tpg;
 
-  // Per tile each wave moves half of the K and V^T tiles (4 + 4 direct loads
-  // of 1 KB) and its own copy of the 64 bias words: 9 loads.
-  constexpr int kLoads = 9;
+  // Per tile the NQW waves of a group split its K and V^T tiles (8 KB each,
+  // 8 / NQW direct loads of 1 KB per wave and tile), and each wave loads its
+  // own copy of the 64 bias words.
+  constexpr int kPer = 8 / NQW;
+  constexpr int kLoads = 2 * kPer + 1;
   auto issue = [&](auto st, int j) {
     const int kt = min(tbase + j, ntiles - 1);
     half_t* sk = bufK(st) + grp * TILE;
     half_t* sv = bufV(st) + grp * TILE;
-    float* sb = bufB(st) + (grp * 2 + qw) * 64;
+    float* sb = bufB(st) + wv * 64;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int s0 = (qw * 4 + u) * 64;  // first 16-byte slot of this load
+    for (int u = 0; u < kPer; ++u) {
+      const int s0 = (qw * kPer + u) * 64;  // first 16-byte slot of this load
       const int q = s0 + lane;
       const int row = q >> 3;
       __builtin_amdgcn_global_load_lds(
@@ -165,9 +173,9 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
   };
 
   // B operands of S^T = K.Q^T: query rows q0 + 16 qb + lr, d-slots of lane group lg.
-  half8 qf[2][2];
+  half8 qf[QB][2];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const half_t* qp = Qh + (size_t)(q0 + 16 * qb + lr) * 64 + lg * 8;
     qf[qb][0] = *reinterpret_cast<const half8*>(qp);
     qf[qb][1] = *reinterpret_cast<const half8*>(qp + 32);
@@ -177,30 +185,31 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
 #pragma unroll
   for (int j = 0; j < 8; ++j) ones[j] = lr == 0 ? (half_t)1.0f : (half_t)0.0f;
 
-  floatx4 o[4][2];  // o[db][qb][i] = O[query q0+16qb+lr][d = 16 db + 4 lg + i] (unnormalised)
-  floatx4 o5[2];    // o5[qb][0] in lane group 0: the running denominator of query q0+16qb+lr
+  floatx4 o[4][QB];  // o[db][qb][i] = O[query q0+16qb+lr][d = 16 db + 4 lg + i] (unnormalised)
+  floatx4 o5[QB];    // o5[qb][0] in lane group 0: the running denominator of query q0+16qb+lr
+  float m_run[QB];   // running max (log2 units), same in a query's 4 lanes
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     o5[qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    m_run[qb] = -INFINITY;
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  float m_run[2] = {-INFINITY, -INFINITY};  // running max (log2 units), same in a query's 4 lanes
 
   auto compute = [&](auto st, int j) {
     const int kt = tbase + j;  // unclamped: a tile past the end is masked out entirely
     const half_t* sk = bufK(st) + grp * TILE;
     const half_t* sv = bufV(st) + grp * TILE;
-    const float* sb = bufB(st) + (grp * 2 + qw) * 64;
+    const float* sb = bufB(st) + wv * 64;
     // sc[kb][qb][i] = S[key kt*64 + 32 (kb>>1) + 8 lg + 4 (kb&1) + i][query q0 + 16 qb + lr]
-    floatx4 sc[4][2];
+    floatx4 sc[4][QB];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int row = 32 * (kb >> 1) + 8 * (lr >> 2) + 4 * (kb & 1) + (lr & 3);
       const half8 kf0 = *reinterpret_cast<const half8*>(sk + row * 64 + attn_kslot(row, lg) * 8);
       const half8 kf1 = *reinterpret_cast<const half8*>(sk + row * 64 + attn_kslot(row, 4 + lg) * 8);
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         floatx4 z = {0.f, 0.f, 0.f, 0.f};
         z = mfma16x16x32(kf0, qf[qb][0], z);
         sc[kb][qb] = mfma16x16x32(kf1, qf[qb][1], z);
@@ -212,12 +221,12 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
       const float4 bb = *reinterpret_cast<const float4*>(sb + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1));
       const float bv[4] = {bb.x + past, bb.y + past, bb.z + past, bb.w + past};
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[kb][qb][i] = fmaf(sc[kb][qb][i], kLog2e, bv[i]);
     }
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       float tmax = fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3]));
 #pragma unroll
       for (int kb = 1; kb < 4; ++kb)
@@ -246,9 +255,9 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
     // key 32 c + 8 lg + j in both operands.  The ones block sums P.
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      half8 pb[2];
+      half8 pb[QB];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           pb[qb][i] = (half_t)sc[2 * c][qb][i];
@@ -259,10 +268,10 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
         const int row = db * 16 + lr;
         const half8 va = *reinterpret_cast<const half8*>(sv + row * 64 + attn_vslot(row, 4 * c + lg) * 8);
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) o[db][qb] = mfma16x16x32(va, pb[qb], o[db][qb]);
+        for (int qb = 0; qb < QB; ++qb) o[db][qb] = mfma16x16x32(va, pb[qb], o[db][qb]);
       }
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) o5[qb] = mfma16x16x32(ones, pb[qb], o5[qb]);
+      for (int qb = 0; qb < QB; ++qb) o5[qb] = mfma16x16x32(ones, pb[qb], o5[qb]);
     }
   };
 
@@ -286,20 +295,21 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
   });
 
   // Denominator of each query: component 0 of the ones block in lane group 0.
-  float l_run[2];
+  float l_run[QB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) l_run[qb] = __shfl(o5[qb][0], lr, kWave);
+  for (int qb = 0; qb < QB; ++qb) l_run[qb] = __shfl(o5[qb][0], lr, kWave);
   if constexpr (G > 1) {
     // Groups 1.. park (m, l, O) in the tile buffers, free once every wave is
-    // past its last tile: the 32 O values of group g's lane in 16 KB of sK0
-    // (g = 1, 2; sK0 holds G x 8 KB) or sK1 (g = 3), its two (m, l) pairs in
-    // sV0.  Group 0 then rescales every part to the common max.
+    // past its last tile: group g's O values (NQW*QB*4 KB) in sK0 (g = 1, 2;
+    // sK0 holds G x 8 KB) or sK1 (g = 3), its (m, l) pairs in sV0.  Group 0
+    // then rescales every part to the common max.
+    constexpr int kParkO = NQW * QB * 64 * 16;  // floats of O parked per group
     auto park_o = [&](int g) -> float* {
       float* base = reinterpret_cast<float*>(g <= 2 ? sK0 : sK1);
-      return base + ((g - 1) & 1) * 4096 + (qw * 64 + lane) * 32;
+      return base + ((g - 1) & 1) * kParkO + (qw * 64 + lane) * (16 * QB);
     };
     auto park_ml = [&](int g) -> float* {
-      return reinterpret_cast<float*>(sV0) + ((g - 1) * 128 + qw * 64 + lane) * 4;
+      return reinterpret_cast<float*>(sV0) + (((g - 1) * NQW + qw) * 64 + lane) * (2 * QB);
     };
     attn_wait_lgkmcnt0();
     __syncthreads();
@@ -307,7 +317,7 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
       float* po = park_o(grp);
       float* pm = park_ml(grp);
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
         for (int db = 0; db < 4; ++db)
           *reinterpret_cast<floatx4*>(po + qb * 16 + db * 4) = o[db][qb];
@@ -319,7 +329,7 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
     __syncthreads();
     if (grp > 0) return;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       float mstar = m_run[qb];
 #pragma unroll
       for (int g = 1; g < G; ++g) mstar = fmaxf(mstar, park_ml(g)[qb * 2]);
@@ -340,7 +350,7 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
     }
   }
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const int q = q0 + 16 * qb + lr;
     if (q < T) {
       const float inv = l_run[qb] > 0.0f ? 1.0f / l_run[qb] : 0.0f;
@@ -359,7 +369,7 @@ __global__ __launch_bounds__(128 * G) void attention32_kernel(const half_t* __re
 }
 
 // kbias[b][t] = 0 for a valid key (t < T, mask != 0), -inf otherwise, for
-// t < Tpad: the additive key mask of attention32_kernel (log2 units).
+// t < Tpad: the additive key mask of attention_kernel (log2 units).
 __global__ void key_bias_kernel(const uint32_t* __restrict__ mask, int B, int T, int Tpad,
                                 float* __restrict__ kbias) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -377,21 +387,32 @@ hipError_t launch_key_bias(const uint32_t* mask, int B, int T, int Tpad, float* 
   return hipGetLastError();
 }
 
+template <int NBUF, int G, int QB, int NQW>
+static void launch_attention_shape(const half_t* Q, const half_t* K, const half_t* Vt,
+                                   const float* kbias, half_t* O, int B, int T, int Tpad,
+                                   hipStream_t stream) {
+  constexpr int qwg = 16 * QB * NQW;
+  hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW>), dim3((T + qwg - 1) / qwg, 8, B),
+                     dim3(64 * G * NQW), 0, stream, Q, K, Vt, kbias, O, T, Tpad);
+}
+
 hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             const float* kbias, half_t* O, int B, int T, int Tpad,
                             hipStream_t stream) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
-  dim3 grid((T + 63) / 64, 8, B);
-  // Two key groups fill the CUs best up to Tpad = 2048 (T = 860: 224
-  // workgroups); longer sequences split the keys four ways.  The choice
-  // depends on the sequence length only, never on the batch, so a request's
-  // output does not depend on what it is batched with.
-  if (Tpad <= kAttnSplitMaxTpad)
-    hipLaunchKernelGGL((attention32_kernel<2, 2>), grid, dim3(256), 0, stream, Q, K, Vt, kbias, O,
-                       T, Tpad);
+  // Shapes swept on MI355X (B = 2, us per launch):
+  //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves   3.4 / 5.3
+  //   T = 860:        64 queries x 2 key groups, 16-query waves  11.2
+  //   T = 3000:       64 queries x 2 key groups, 32-query waves  75.9
+  // Every shape splits the keys into the same two groups, so the result is
+  // bit-identical whichever is chosen; the choice depends on the padded
+  // length only, never on the batch.
+  if (Tpad <= 512)
+    launch_attention_shape<2, 2, 1, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
+  else if (Tpad <= kAttnWideMinTpad)
+    launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
   else
-    hipLaunchKernelGGL((attention32_kernel<2, 4>), grid, dim3(512), 0, stream, Q, K, Vt, kbias, O,
-                       T, Tpad);
+    launch_attention_shape<2, 2, 2, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
   return hipGetLastError();
 }
 

@@ -583,8 +583,9 @@ static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
 // four wavefronts alone on a CU cannot hide its LDS and MFMA latencies.
 //  * wide outputs use big tiles with eight wavefronts (two per SIMD) and
 //    about one tile per CU: w1|w3 (N = 3072) 128x192, 11.8 vs 15.4 us for
-//    64x64; the k=5 conv (N = 1024, K = 2560) 64x128 with 128-wide stages,
-//    17.4 vs 21.3 us; res/skip and conv1|res_projection (N = 1024) 64x128;
+//    64x64; the k=5 conv (N = 1024, K = 2560) 64x128 with 64-wide stages,
+//    16.5 us (17.2 with 128-wide stages, 21.3 with 64x64 tiles); res/skip
+//    and conv1|res_projection (N = 1024) 64x128;
 //  * N = 512 outputs and QKV keep 64x64 tiles with four wavefronts in a
 //    3-stage ring (three workgroups per CU): larger tiles leave too few
 //    tiles to cover the CUs.
@@ -594,7 +595,7 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
     if (a.N % 192 == 0) return launch_tile<128, 192, 64, 3, AM, EPI, 4, 2>(a, s);
   }
   if constexpr (AM == A_CONV5) {
-    if (a.N % 128 == 0) return launch_tile<64, 128, 128, 3, AM, EPI, 2, 4>(a, s);
+    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
   }
   if constexpr (EPI == EPI_RESSKIP || EPI == EPI_DUAL) {
     if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
