@@ -69,9 +69,9 @@ struct TileMap {
   }
 };
 
-template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap tmap) {
-  constexpr int NW = WM * WN;                // wavefronts, WM along M x WN along N
+template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN, int KG>
+__global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, TileMap tmap) {
+  constexpr int NW = WM * WN;                // wavefronts per K group, WM along M x WN along N
   constexpr int CPR = SK / 8;                // 16-byte slots per stage row
   constexpr int LA = BM * CPR / (64 * NW);   // DMA instructions per wave per stage (A)
   constexpr int LB = BN * CPR / (64 * NW);   // (W)
@@ -85,28 +85,35 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap 
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave sub-tile must be whole MFMA blocks");
   static_assert(L * (NST - 1) < 64, "too many loads in flight");
   static_assert(CPR == 8 || CPR >= 16, "stage width");
+  static_assert(KG == 1 || (KG == 2 && EPI != EPI_QKV), "K groups: the QKV epilogue needs every wave");
 
   // One __shared__ object per stage and operand, declared here so each kernel
   // instantiation owns its own objects (the per-object alias scopes are what
   // let the compiler keep only the explicit vmcnt waits).
-  __shared__ __attribute__((aligned(1024))) half_t sA0[BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA1[BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB0[BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB1[BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? BN * SK : 8];
+  // With KG = 2 K groups, each group has its own region in every buffer.
+  __shared__ __attribute__((aligned(1024))) half_t sA0[KG * BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA1[KG * BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB0[KG * BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB1[KG * BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? KG * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? KG * BN * SK : 8];
   static_assert(NST >= 2 && NST <= 4, "two to four stages");
+  const int kg = threadIdx.x / (64 * NW);  // K group of this wave
   auto bufA = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
-    if constexpr (s == 0) return sA0; else if constexpr (s == 1) return sA1;
-    else if constexpr (s == 2) return sA2; else return sA3;
+    half_t* b;
+    if constexpr (s == 0) b = sA0; else if constexpr (s == 1) b = sA1;
+    else if constexpr (s == 2) b = sA2; else b = sA3;
+    return KG == 1 ? b : b + kg * BM * SK;
   };
   auto bufB = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
-    if constexpr (s == 0) return sB0; else if constexpr (s == 1) return sB1;
-    else if constexpr (s == 2) return sB2; else return sB3;
+    half_t* b;
+    if constexpr (s == 0) b = sB0; else if constexpr (s == 1) b = sB1;
+    else if constexpr (s == 2) b = sB2; else b = sB3;
+    return KG == 1 ? b : b + kg * BN * SK;
   };
 
   int tile_m, tile_n;
@@ -116,12 +123,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = (tid >> 6) % NW;  // wave within its K group
   const int wm = wave / WN;
   const int wn = wave - wm * WN;
   const int lr = lane & 15;
   const int lg = lane >> 4;
-  const int KT = p.K / SK;
+  // K group kg walks stages [kg * KT, kg * KT + KT) (the host makes K / SK a
+  // multiple of KG, so both groups meet the same barriers).
+  const int KT = p.K / SK / KG;
+  const int kt_lo = kg * KT;
 
   // Output ownership.  The MFMA is issued with W as its first operand, so the
   // accumulator is C^T: lane (lr, lg) of block (i, j) holds the four
@@ -145,7 +155,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap 
       for (int j = 0; j < NI; ++j) {
         const int n = col_base + 16 * j;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m < p.M) {
+        if (m < p.M && kg == 0) {
           if constexpr (EPI == EPI_F32) {
             if (p.res) v = *reinterpret_cast<const float4*>(p.res + (size_t)m * p.ldres + n);
           } else if constexpr (EPI == EPI_RESSKIP) {
@@ -157,8 +167,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap 
         }
         pre_a[i][j] = v;
         if constexpr (kPreB) {
-          pre_b[i][j] = m < p.M ? *reinterpret_cast<const float4*>(p.rp + (size_t)m * 512 + n)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+          pre_b[i][j] = m < p.M && kg == 0 ? *reinterpret_cast<const float4*>(p.rp + (size_t)m * 512 + n)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
       }
     }
@@ -175,7 +185,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap 
       const int m = row_base + 16 * i;
 #pragma unroll
       for (int u = 0; u < kSsqParts / 4; ++u)
-        ssq_pre[i][u] = (p.ssq_in && m < p.M)
+        ssq_pre[i][u] = (p.ssq_in && m < p.M && kg == 0)
                             ? reinterpret_cast<const float4*>(p.ssq_in + (size_t)m * kSsqParts)[u]
                             : make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -224,7 +234,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap 
   auto issue = [&](auto st, int kt) {
     half_t* sa = bufA(st);
     half_t* sb = bufB(st);
-    const int k0 = kt * SK;
+    const int k0 = (kt_lo + kt) * SK;
 #pragma unroll
     for (int j = 0; j < LA; ++j) {
       const int q0 = (wave * LA + j) * 64;
@@ -337,6 +347,26 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs p, TileMap 
   static_for<0, NST - 1>([&](auto st) {
     if (kt0 + (int)decltype(st)::value < KT) compute(st);
   });
+
+  // K groups: group 1 hands its partial tile to group 0 through LDS and
+  // leaves; group 0 adds it (a fixed order, so the sum is deterministic) and
+  // runs the epilogue.
+  if constexpr (KG == 2) {
+    __shared__ __attribute__((aligned(1024))) floatx4 red[NW * MI * NI * 64];
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) red[((wave * MI + i) * NI + j) * 64 + lane] = acc[i][j];
+    }
+    wait_lgkmcnt0();
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] += red[((wave * MI + i) * NI + j) * 64 + lane];
+  }
 
   // ---------------------------------------------------------------- epilogue
   auto st16 = [](half_t* dst, float a, float b, float c, float d) {
@@ -567,11 +597,12 @@ static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
   return t;
 }
 
-template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2>
+template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2, int KG = 1>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
+  if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K groups need equal stage counts
   const TileMap tm = make_tile_map(a.M, a.N, a.K, AM == A_CONV5 ? a.conv_c : a.K, BM, BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN>), dim3(8 * tm.per_xcd),
-                     dim3(64 * WM * WN), 0, s,
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG>), dim3(8 * tm.per_xcd),
+                     dim3(64 * WM * WN * KG), 0, s,
                      a, tm);
   return hipGetLastError();
 }
@@ -588,7 +619,10 @@ static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
 //    and conv1|res_projection (N = 1024) 64x128;
 //  * N = 512 outputs and QKV keep 64x64 tiles with four wavefronts in a
 //    3-stage ring (three workgroups per CU): larger tiles leave too few
-//    tiles to cover the CUs.
+//    tiles to cover the CUs.  The long-K ones (K >= 1024) add a second
+//    group of four wavefronts that takes half of the K stages.
+// The choice depends on N and K only, never on M, so a request's result
+// does not depend on the batch it is decoded with.
 template <int AM, int EPI>
 static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
   if constexpr (EPI == EPI_SWIGLU) {
@@ -599,6 +633,11 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
   }
   if constexpr (EPI == EPI_RESSKIP || EPI == EPI_DUAL) {
     if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
+  }
+  if constexpr (EPI == EPI_F32) {
+    // Long-K N = 512 products (w2 K = 1536, skip-in K = 1024) split K over
+    // two wave groups: 9.4 vs 9.8 us and 7.25 vs 7.7 us.
+    if (a.K >= 1024 && (a.K / 64) % 2 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
   }
   return launch_tile<64, 64, 64, 3, AM, EPI>(a, s);
 }
