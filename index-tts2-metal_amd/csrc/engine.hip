@@ -93,6 +93,9 @@ struct Weights {
   half_t* rs_w[8]; float* rs_b[8];
   half_t* fin_w; float* fin_b;
   half_t* c2_w;  float* c2_b;   // [80][512]
+  // conv2 . final_layer.linear as one map (both are linear and nothing reads
+  // the 512-wide final-layer output in between): [80][512] and [80].
+  half_t* c2f_w; float* c2f_b;
 };
 
 namespace {
@@ -209,7 +212,6 @@ struct Workspace {
   float* wn_out;
   half_t* gate16;
   float* fin;
-  half_t* y16;
   uint32_t* mask;
   float* kbias;  // [B][Tpad] attention key bias (0 valid, -inf masked/padding), from mask
   uint32_t* P;
@@ -377,11 +379,35 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
                                    rc, 512));
     W.rs_b[l] = up.f32(hm.get(q + ".bias", rc));
   }
-  W.fin_w = up.f16(weight_norm(hm.get("final_layer.linear.weight_g", 512),
-                               hm.get("final_layer.linear.weight_v", 512 * 512), 512, 512));
-  W.fin_b = up.f32(hm.get("final_layer.linear.bias", 512));
-  W.c2_w = up.f16(hm.get("conv2.weight", 80 * 512));
-  W.c2_b = up.f32(hm.get("conv2.bias", 80));
+  {
+    // dphi = Wc2 (Wf y + bf) + bc2 = (Wc2 Wf) y + (Wc2 bf + bc2), summed in
+    // double from the fp32 weights (weight norm applied), rounded once to f16.
+    const std::vector<float> wf = weight_norm(hm.get("final_layer.linear.weight_g", 512),
+                                              hm.get("final_layer.linear.weight_v", 512 * 512), 512, 512);
+    const std::vector<float>& bf = hm.get("final_layer.linear.bias", 512);
+    const std::vector<float>& wc = hm.get("conv2.weight", 80 * 512);
+    const std::vector<float>& bc = hm.get("conv2.bias", 80);
+    W.fin_w = up.f16(wf);
+    W.fin_b = up.f32(bf);
+    W.c2_w = up.f16(wc);
+    W.c2_b = up.f32(bc);
+    std::vector<double> acc((size_t)80 * 512, 0.0);
+    std::vector<float> wcf((size_t)80 * 512), bcf(80);
+    for (int n = 0; n < 80; ++n) {
+      double bsum = bc[n];
+      for (int j = 0; j < 512; ++j) {
+        const double c = wc[(size_t)n * 512 + j];
+        bsum += c * bf[j];
+        const float* wrow = wf.data() + (size_t)j * 512;
+        double* arow = acc.data() + (size_t)n * 512;
+        for (int k = 0; k < 512; ++k) arow[k] += c * wrow[k];
+      }
+      bcf[n] = (float)bsum;
+      for (int k = 0; k < 512; ++k) wcf[(size_t)n * 512 + k] = (float)acc[(size_t)n * 512 + k];
+    }
+    W.c2f_w = up.f16(wcf);
+    W.c2f_b = up.f32(bcf);
+  }
 
   ws_ = std::make_unique<Workspace>();
 }
@@ -428,7 +454,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   h(r * 512); h(r * 512);
   h((size_t)cRpad * 512); h((size_t)cRpad * 512); h((size_t)cRpad * 512);
   h(r * 512); h(r * 1536); h(r * 512);
-  f(r * 512); h(r * 512); f(r * 512); f(r * 512); h(r * 512); f(r * 512); h(r * 512);
+  f(r * 512); h(r * 512); f(r * 512); f(r * 512); h(r * 512); f(r * 512);
   bytes += (r * 4 + 255) / 256 * 256 + ((size_t)cReq * 4 + 255) / 256 * 256;
   f((size_t)cRpad);
   f((size_t)cT * 64);
@@ -465,7 +491,6 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   ws.wn_out = F(r * 512);
   ws.gate16 = H(r * 512);
   ws.fin = F(r * 512);
-  ws.y16 = H(r * 512);
   ws.mask = static_cast<uint32_t*>(a.take(r * 4));
   ws.kbias = F((size_t)cRpad);
   ws.P = static_cast<uint32_t*>(a.take((size_t)cReq * 4));
@@ -670,8 +695,9 @@ void Engine::enqueue_transformer(int B, int T, const float* tab, const float* nb
 }
 
 // ------------------------------------------------------------------ estimator body
-// Runs the estimator from x (ws.xa, fp32, already merged) to y16 (final
-// linear output, f16) for B branches of T rows, using table row `slot`.
+// Runs the estimator from x (ws.xa, fp32, already merged) to the final
+// layer's AdaLN output (ws.n16, f16) for B branches of T rows, using one
+// step's tables; the caller applies the folded final linear + conv2.
 void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw) {
   Weights& W = *w_;
   Workspace& ws = *ws_;
@@ -714,13 +740,9 @@ void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq,
       HIP_OK(launch_gemm(g, A_PLAIN, EPI_FINALSKIP, s));
     }
   }
+  // The final layer's AdaLN output stays in ws.n16; its linear map is folded
+  // into conv2 (W.c2f_w), which the caller applies.
   HIP_OK(launch_adaln(ws.fin, tab + kFinalSsOff, tab + kFinalSsOff + 512, ws.n16, R, s));
-  {
-    GemmArgs g;
-    g.M = R; g.N = 512; g.K = 512; g.A = ws.n16; g.lda = 512;
-    g.W = W.fin_w; g.ldw = 512; g.bias = W.fin_b; g.C16 = ws.y16; g.ldc16 = 512;
-    HIP_OK(launch_gemm(g, A_PLAIN, EPI_F16, s));
-  }
 }
 
 // Input merge constant part: cond projection into mc16[:, kMcContent:+512], then
@@ -767,7 +789,7 @@ void Engine::enqueue_decode(const float* x0, const float* prompt, const float* c
     const float* tab = tb.tab + (size_t)s * kTcondPerStep;
     enqueue_merge_step(W, ws, R, stream_, tab);
     enqueue_estimator(B, T, tab, tb.nbq + (size_t)s * 13 * 1536, tb.nbw + (size_t)s * 13 * 3072);
-    HIP_OK(launch_conv2_euler(ws.y16, W.c2_w, W.c2_b, ws.P, nreq, T, cfg_on, cfg, dt, ws.x_cur,
+    HIP_OK(launch_conv2_euler(ws.n16, W.c2f_w, W.c2f_b, ws.P, nreq, T, cfg_on, cfg, dt, ws.x_cur,
                               ws.xmel16, vtrace ? vtrace + (size_t)s * nreq * T * 80 : nullptr,
                               stream_));
   }
@@ -864,7 +886,7 @@ void Engine::estimator_step_device(const float* x, const float* prompt_x, const 
   enqueue_merge_const(W, ws, R, stream_);
   enqueue_merge_step(W, ws, R, stream_, ws.tab);
   enqueue_estimator(B, T, ws.tab, ws.nbq, ws.nbw);
-  HIP_OK(launch_conv2_rows(ws.y16, W.c2_w, W.c2_b, R, dphi, stream_));
+  HIP_OK(launch_conv2_rows(ws.n16, W.c2f_w, W.c2f_b, R, dphi, stream_));
   HIP_OK(hipStreamSynchronize(stream_));
 }
 
