@@ -88,7 +88,9 @@ struct Weights {
   half_t* w2_w[13];
   half_t* si_w[13]; float* si_b[13];
   half_t* sl_w;  float* sl_b;  // [512][512 + kMelPad]
-  half_t* c1rp_w; float* c1rp_b;  // [1024][512]
+  // conv1|res_projection . skip_linear as one map (nothing else reads the
+  // skip_linear output): [1024][512 + kMelPad] and [1024].
+  half_t* post_w; float* post_b;
   half_t* in_w[8]; float* in_b[8];  // [1024][2560]
   half_t* rs_w[8]; float* rs_b[8];
   half_t* fin_w; float* fin_b;
@@ -354,8 +356,28 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
     const auto& rpb = hm.get("res_projection.bias", 512);
     std::memcpy(b.data(), c1b.data(), 512 * sizeof(float));
     std::memcpy(b.data() + 512, rpb.data(), 512 * sizeof(float));
-    W.c1rp_w = up.f16(w);
-    W.c1rp_b = up.f32(b);
+    // [c1; rp] (W_sl x + b_sl) + [b_c1; b_rp], summed in double from the fp32
+    // weights, rounded once to f16.
+    const auto& sw = hm.get("skip_linear.weight", 512 * 592);
+    const auto& sb = hm.get("skip_linear.bias", 512);
+    constexpr int kw = 512 + kMelPad;
+    std::vector<float> pw((size_t)1024 * kw, 0.f), pb(1024);
+    std::vector<double> row(592);
+    for (int n = 0; n < 1024; ++n) {
+      std::fill(row.begin(), row.end(), 0.0);
+      double bsum = b[n];
+      const float* wn = w.data() + (size_t)n * 512;
+      for (int j = 0; j < 512; ++j) {
+        const double c = wn[j];
+        bsum += c * sb[j];
+        const float* srow = sw.data() + (size_t)j * 592;
+        for (int k = 0; k < 592; ++k) row[k] += c * srow[k];
+      }
+      pb[n] = (float)bsum;
+      for (int k = 0; k < 592; ++k) pw[(size_t)n * kw + k] = (float)row[k];
+    }
+    W.post_w = up.f16(pw);
+    W.post_b = up.f32(pb);
   }
   for (int l = 0; l < 8; ++l) {
     const std::string p = "wavenet.in_layers." + std::to_string(l) + ".conv.conv";
@@ -706,19 +728,14 @@ void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq,
 
   enqueue_transformer(B, T, tab, nbq, nbw);
   {
-    GemmArgs g;  // skip_linear on [x_normed | x_mel]
-    g.M = R; g.N = 512; g.K = 512 + kMelPad; g.K1 = 512;
+    // conv1 | res_projection of skip_linear([x_normed | x_mel]) as one product
+    GemmArgs g;
+    g.M = R; g.N = 1024; g.K = 512 + kMelPad; g.K1 = 512;
     g.A = ws.n16; g.lda = 512; g.A2 = ws.xmel16; g.lda2 = kMelPad;
-    g.W = W.sl_w; g.ldw = 512 + kMelPad; g.bias = W.sl_b; g.C16 = ws.ls16; g.ldc16 = 512;
-    HIP_OK(launch_gemm(g, A_CONCAT, EPI_F16, s));
-  }
-  {
-    GemmArgs g;  // conv1 | res_projection
-    g.M = R; g.N = 1024; g.K = 512; g.A = ws.ls16; g.lda = 512;
-    g.W = W.c1rp_w; g.ldw = 512; g.bias = W.c1rp_b;
+    g.W = W.post_w; g.ldw = 512 + kMelPad; g.bias = W.post_b;
     g.C32 = ws.wn_x; g.ldc32 = 512; g.C16 = ws.wn_x16; g.ldc16 = 512;
     g.C32b = ws.rp; g.ldc32b = 512;
-    HIP_OK(launch_gemm(g, A_PLAIN, EPI_DUAL, s));
+    HIP_OK(launch_gemm(g, A_CONCAT, EPI_DUAL, s));
   }
   for (int l = 0; l < 8; ++l) {
     {
@@ -1169,11 +1186,14 @@ void Engine::stage_post(const float* xres, const float* xmel, int rows, float* l
   g.A = ws.n16; g.lda = 512; g.A2 = ws.xmel16; g.lda2 = kMelPad;
   g.W = W.sl_w; g.ldw = 512 + kMelPad; g.bias = W.sl_b; g.C16 = ws.ls16; g.ldc16 = 512;
   HIP_OK(launch_gemm(g, A_CONCAT, EPI_F16, stream_));
+  // conv1 / res_projection as the decode computes them: one product with the
+  // folded weights (the long-skip output above is reported, not consumed).
   GemmArgs c;
-  c.M = rows; c.N = 1024; c.K = 512; c.A = ws.ls16; c.lda = 512;
-  c.W = W.c1rp_w; c.ldw = 512; c.bias = W.c1rp_b;
+  c.M = rows; c.N = 1024; c.K = 512 + kMelPad; c.K1 = 512;
+  c.A = ws.n16; c.lda = 512; c.A2 = ws.xmel16; c.lda2 = kMelPad;
+  c.W = W.post_w; c.ldw = 512 + kMelPad; c.bias = W.post_b;
   c.C32 = ws.wn_x; c.ldc32 = 512; c.C16 = ws.wn_x16; c.ldc16 = 512; c.C32b = ws.rp; c.ldc32b = 512;
-  HIP_OK(launch_gemm(c, A_PLAIN, EPI_DUAL, stream_));
+  HIP_OK(launch_gemm(c, A_CONCAT, EPI_DUAL, stream_));
   std::vector<_Float16> h((size_t)rows * 512);
   d2h(h.data(), ws.ls16, h.size() * 2, stream_);
   for (size_t i = 0; i < h.size(); ++i) long_skip[i] = (float)h[i];

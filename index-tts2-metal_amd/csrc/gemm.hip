@@ -663,6 +663,7 @@ hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t 
   } else if (amode == A_CONCAT) {
     if (epi == EPI_F32) return launch_am_epi<A_CONCAT, EPI_F32>(a, stream);
     if (epi == EPI_F16) return launch_am_epi<A_CONCAT, EPI_F16>(a, stream);
+    if (epi == EPI_DUAL) return launch_am_epi<A_CONCAT, EPI_DUAL>(a, stream);
   } else if (amode == A_CONV5) {
     if (epi == EPI_GATE) return launch_am_epi<A_CONV5, EPI_GATE>(a, stream);
   }
