@@ -31,7 +31,7 @@
 
 namespace mit2hip {
 
-constexpr int kAttnWideMinTpad = 2048;  // longer padded sequences use 32-query waves
+constexpr int kAttnDeepMaxTpad = 2048;  // longest padded sequence with a 3-tile ring
 
 typedef __attribute__((address_space(3))) void attn_lds_t;
 
@@ -131,9 +131,14 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
   const int grp = wv / NQW; // key group
   const int lr = lane & 15;
   const int lg = lane >> 4;
-  const int b = blockIdx.z;
-  const int h = blockIdx.y;
-  const int q0 = blockIdx.x * QWG + qw * 16 * QB;
+  // Workgroups are dealt to the 8 XCDs round-robin; XCD i runs head i of
+  // every branch, so a head's K and V^T tiles are fetched into one XCD's L2
+  // and every query block of that head hits there.
+  const int nqb = (T + QWG - 1) / QWG;
+  const int h = blockIdx.x & 7;
+  const int slot = blockIdx.x >> 3;
+  const int b = slot / nqb;
+  const int q0 = (slot - b * nqb) * QWG + qw * 16 * QB;
   const size_t head = (size_t)b * 8 + h;
   const half_t* Qh = Q + head * Tpad * 64;
   const half_t* Kh = K + head * Tpad * 64;
@@ -392,7 +397,7 @@ static void launch_attention_shape(const half_t* Q, const half_t* K, const half_
                                    const float* kbias, half_t* O, int B, int T, int Tpad,
                                    hipStream_t stream) {
   constexpr int qwg = 16 * QB * NQW;
-  hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW>), dim3((T + qwg - 1) / qwg, 8, B),
+  hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW>), dim3((T + qwg - 1) / qwg * 8 * B),
                      dim3(64 * G * NQW), 0, stream, Q, K, Vt, kbias, O, T, Tpad);
 }
 
@@ -400,19 +405,19 @@ hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             const float* kbias, half_t* O, int B, int T, int Tpad,
                             hipStream_t stream) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
-  // Shapes swept on MI355X (B = 2, us per launch):
-  //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves   3.4 / 5.3
-  //   T = 860:        64 queries x 2 key groups, 16-query waves  11.2
-  //   T = 3000:       64 queries x 2 key groups, 32-query waves  75.9
+  // Shapes swept on MI355X (B = 2, us per launch, head-per-XCD mapping):
+  //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves, 2 buffers   3.5 / 5.4
+  //   T = 860:        64 queries x 2 key groups, 16-query waves, 3 buffers  10.3
+  //   T = 3000:       64 queries x 2 key groups, 16-query waves, 2 buffers  69.7
   // Every shape splits the keys into the same two groups, so the result is
   // bit-identical whichever is chosen; the choice depends on the padded
   // length only, never on the batch.
   if (Tpad <= 512)
     launch_attention_shape<2, 2, 1, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
-  else if (Tpad <= kAttnWideMinTpad)
-    launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
+  else if (Tpad <= kAttnDeepMaxTpad)
+    launch_attention_shape<3, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
   else
-    launch_attention_shape<2, 2, 2, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
+    launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
   return hipGetLastError();
 }
 
