@@ -214,6 +214,46 @@ mit2cfm_status mit2cfm_inspect_bundle(const char* bundle_path, uint64_t* tensor_
 /* Writes the synthetic estimator weights as an MIT2 bundle directory. */
 mit2cfm_status mit2cfm_write_synthetic_bundle(const char* dir, uint64_t base_seed, float stddev);
 
+/* ---- condition and noise producer (the step before the decode) -----------
+ * These need the s2mel length regulator's tensors
+ * ("s2mel.net.length_regulator.*", 20 tensors) in the context's weight table;
+ * without them they return MIT2CFM_E_MODEL. */
+
+/* Replaces run_length_regulator_full_metal (runtime/impl/gpt.cpp:5313; CPU
+ * definition run_length_regulator_full_cpu :5298): s_infer [in_tokens][1024]
+ * (the GPT semantic latent plus its VQ embedding) -> out [out_tokens][512]:
+ * content_in_proj, nearest interpolation to out_tokens, 4 x (conv k=3 zero
+ * padded, GroupNorm with one group, Mish), conv k=1.  Host pointers,
+ * synchronous. */
+mit2cfm_status mit2cfm_length_regulator(mit2cfm_ctx* ctx, const float* s_infer,
+                                        uint32_t in_tokens, uint32_t out_tokens, float* out);
+/* The decode condition: replaces the length-regulator and
+ * hot_condition_merge_f32 steps of build_hot_codes_condition_inputs_shared
+ * (runtime/impl/tts_synthesis/synthesis_pipeline.cpp:1012-1035; merge kernel
+ * kernels.metal:843-864).  generated = floor(codes * 1.72f) frames;
+ * cond_out [prompt_tokens + generated][512] = the first prompt_tokens rows of
+ * prompt_cond followed by the length regulator of s_infer [codes][1024].
+ * *generated_out receives generated.  Host pointers, synchronous. */
+mit2cfm_status mit2cfm_condition(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                 const float* prompt_cond, uint32_t prompt_tokens,
+                                 float* cond_out, uint32_t* generated_out);
+/* The same on DEVICE pointers, enqueued on the context's stream (flags as for
+ * mit2cfm_decode_device), so cond_out can feed mit2cfm_decode_device without
+ * a host round trip.  No reference counterpart (unified memory there). */
+mit2cfm_status mit2cfm_condition_device(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                        const float* prompt_cond, uint32_t prompt_tokens,
+                                        float* cond_out, uint32_t* generated_out, uint32_t flags);
+/* Frames the condition producer makes from `codes` semantic tokens:
+ * floor(codes * 1.72f) (synthesis_pipeline.cpp:1012). */
+uint32_t mit2cfm_generated_frames(uint32_t codes);
+/* Seeded decode noise on the GPU: make_deterministic_normal_noise
+ * (runtime/impl/tokenizer_tests.cpp:2121) into the DEVICE buffer out
+ * [tokens][channels]; the uniforms are bit-identical to the host generator,
+ * the Box-Muller transcendentals are the GPU's.  Enqueued on the context's
+ * stream (flags as for mit2cfm_decode_device). */
+mit2cfm_status mit2cfm_noise_device(mit2cfm_ctx* ctx, uint32_t tokens, uint32_t channels,
+                                    uint64_t seed, float temperature, float* out, uint32_t flags);
+
 #ifdef __cplusplus
 }
 #endif

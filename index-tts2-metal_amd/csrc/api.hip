@@ -452,3 +452,55 @@ mit2cfm_status mit2cfm_write_synthetic_bundle(const char* dir, uint64_t base_see
 }
 
 }  // extern "C"
+
+mit2cfm_status mit2cfm_length_regulator(mit2cfm_ctx* ctx, const float* s_infer,
+                                        uint32_t in_tokens, uint32_t out_tokens, float* out) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(s_infer && out, "s_infer and out must not be NULL");
+    require(in_tokens > 0 && out_tokens > 0, "in_tokens and out_tokens must be positive");
+    ctx->eng->length_regulator_host(s_infer, (int)in_tokens, (int)out_tokens, out);
+  });
+}
+
+mit2cfm_status mit2cfm_condition(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                 const float* prompt_cond, uint32_t prompt_tokens,
+                                 float* cond_out, uint32_t* generated_out) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(s_infer && prompt_cond && cond_out, "s_infer, prompt_cond and cond_out must not be NULL");
+    require(codes > 0 && prompt_tokens > 0, "codes and prompt_tokens must be positive");
+    const int gen = ctx->eng->condition_host(s_infer, (int)codes, prompt_cond, (int)prompt_tokens,
+                                             cond_out);
+    if (generated_out) *generated_out = (uint32_t)gen;
+  });
+}
+
+mit2cfm_status mit2cfm_condition_device(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                        const float* prompt_cond, uint32_t prompt_tokens,
+                                        float* cond_out, uint32_t* generated_out, uint32_t flags) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(s_infer && prompt_cond && cond_out, "s_infer, prompt_cond and cond_out must not be NULL");
+    require(codes > 0 && prompt_tokens > 0, "codes and prompt_tokens must be positive");
+    const int gen = ctx->eng->condition_device(s_infer, (int)codes, prompt_cond, (int)prompt_tokens,
+                                               cond_out);
+    if (generated_out) *generated_out = (uint32_t)gen;
+    if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}
+
+uint32_t mit2cfm_generated_frames(uint32_t codes) {
+  return (uint32_t)mit2hip::Engine::generated_frames((int)codes);
+}
+
+mit2cfm_status mit2cfm_noise_device(mit2cfm_ctx* ctx, uint32_t tokens, uint32_t channels,
+                                    uint64_t seed, float temperature, float* out, uint32_t flags) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(out != nullptr, "out must not be NULL");
+    require(tokens > 0 && channels > 0, "noise shape must be non-empty");
+    ctx->eng->normal_noise_device((size_t)tokens * channels, seed, temperature, out);
+    if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}

@@ -1,0 +1,37 @@
+// condition.h -- kernels of the condition and noise producer that feeds the
+// DiT-CFM decode: the s2mel length regulator's element-wise stages (its
+// GEMMs run on gemm.hip) and the seeded normal-noise generator.
+#pragma once
+
+#include "device_common.h"
+
+namespace mit2hip {
+
+// dst[t] = src[min(floor(t * scale), in_tokens - 1)] for t < out_tokens,
+// 512-wide f16 rows (cpu_nearest_interpolate, tokenizer_tests.cpp:3127, with
+// scale = (float)in_tokens / (float)out_tokens formed by the caller); also
+// zeroes row out_tokens of dst, the padding row of the zero-padded k = 3 conv.
+hipError_t launch_nearest_rows(const half_t* src, int in_tokens, int out_tokens, float scale,
+                               half_t* dst, hipStream_t s);
+
+// GroupNorm with one group over rows x 512 values: the mean and 1/sqrt(var +
+// eps) from the per-row, per-32-column partial sums and sums of squares the
+// producing GEMM wrote ([rows][16] each), reduced in double.  stats[0] =
+// mean, stats[1] = inverse standard deviation.
+hipError_t launch_gn_stats(const float* sum_parts, const float* ssq_parts, int rows, float eps,
+                           float* stats, hipStream_t s);
+
+// out[r][c] = f16(mish((y[r][c] - mean) * rstd * gamma[c] + beta[c])) for
+// r < rows (cpu_groupnorm1 + cpu_mish, tokenizer_tests.cpp:3874-3904).
+hipError_t launch_gn_mish(const float* y, const float* stats, const float* gamma,
+                          const float* beta, int rows, half_t* out, hipStream_t s);
+
+// make_deterministic_normal_noise (tokenizer_tests.cpp:2121-2140) on the GPU:
+// out[n] for n = tokens * channels values.  splitmix64 is a counter: value
+// pair j draws its two uniforms from states seed + (2j+1) g and seed + (2j+2) g
+// (g the splitmix64 increment), so every pair is computed independently and
+// the uniforms are bit-identical to the sequential generator.
+hipError_t launch_normal_noise(size_t n, uint64_t seed, float temperature, float* out,
+                               hipStream_t s);
+
+}  // namespace mit2hip

@@ -1,0 +1,147 @@
+// condition.hip -- element-wise kernels of the condition and noise producer
+// (the s2mel length regulator, gpt.cpp:5271-5340, and the seeded noise of
+// tokenizer_tests.cpp:2102-2140).  All of them are HBM-bound row passes.
+#include "condition.h"
+
+namespace mit2hip {
+
+// One wave per output row: 64 lanes x 8 halves = the 512 channels.
+__global__ __launch_bounds__(256) void nearest_rows_kernel(const half_t* __restrict__ src,
+                                                           int in_tokens, int out_tokens,
+                                                           float scale,
+                                                           half_t* __restrict__ dst) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t > out_tokens) return;
+  half8 v;
+  if (t == out_tokens) {
+    for (int i = 0; i < 8; ++i) v[i] = (half_t)0.0f;
+  } else {
+    int s = (int)floorf((float)t * scale);
+    if (s >= in_tokens) s = in_tokens - 1;
+    v = *reinterpret_cast<const half8*>(src + (size_t)s * 512 + lane * 8);
+  }
+  *reinterpret_cast<half8*>(dst + (size_t)t * 512 + lane * 8) = v;
+}
+
+hipError_t launch_nearest_rows(const half_t* src, int in_tokens, int out_tokens, float scale,
+                               half_t* dst, hipStream_t s) {
+  if (in_tokens <= 0 || out_tokens <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(nearest_rows_kernel, dim3((out_tokens + 1 + 3) / 4), dim3(256), 0, s, src,
+                     in_tokens, out_tokens, scale, dst);
+  return hipGetLastError();
+}
+
+// One workgroup of 1024 threads: each thread folds a strided share of the
+// partials in double, then a tree over the workgroup.
+__global__ __launch_bounds__(1024) void gn_stats_kernel(const float* __restrict__ sum_parts,
+                                                        const float* __restrict__ ssq_parts,
+                                                        int nparts, double count, float eps,
+                                                        float* __restrict__ stats) {
+  __shared__ double s1[1024], s2[1024];
+  double a = 0.0, b = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += 1024) {
+    a += (double)sum_parts[i];
+    b += (double)ssq_parts[i];
+  }
+  s1[threadIdx.x] = a;
+  s2[threadIdx.x] = b;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) {
+      s1[threadIdx.x] += s1[threadIdx.x + w];
+      s2[threadIdx.x] += s2[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double mean = s1[0] / count;
+    double var = s2[0] / count - mean * mean;
+    if (var < 0.0) var = 0.0;
+    stats[0] = (float)mean;
+    stats[1] = (float)(1.0 / sqrt(var + (double)eps));
+  }
+}
+
+hipError_t launch_gn_stats(const float* sum_parts, const float* ssq_parts, int rows, float eps,
+                           float* stats, hipStream_t s) {
+  if (rows <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gn_stats_kernel, dim3(1), dim3(1024), 0, s, sum_parts, ssq_parts, rows * 16,
+                     (double)rows * 512.0, eps, stats);
+  return hipGetLastError();
+}
+
+__device__ __forceinline__ float mish_f(float x) { return x * tanhf(log1pf(expf(x))); }
+
+__global__ __launch_bounds__(256) void gn_mish_kernel(const float* __restrict__ y,
+                                                      const float* __restrict__ stats,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta, int rows,
+                                                      half_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float mean = stats[0], rstd = stats[1];
+  const float4* yr = reinterpret_cast<const float4*>(y + (size_t)r * 512) + lane * 2;
+  const float4 a = yr[0], b = yr[1];
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  half8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = lane * 8 + i;
+    o[i] = (half_t)mish_f((v[i] - mean) * rstd * gamma[c] + beta[c]);
+  }
+  *reinterpret_cast<half8*>(out + (size_t)r * 512 + lane * 8) = o;
+}
+
+hipError_t launch_gn_mish(const float* y, const float* stats, const float* gamma,
+                          const float* beta, int rows, half_t* out, hipStream_t s) {
+  if (rows <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gn_mish_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, y, stats, gamma, beta,
+                     rows, out);
+  return hipGetLastError();
+}
+
+// splitmix64 output for the state reached after `steps` increments of seed.
+__device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t steps) {
+  uint64_t z = seed + steps * 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// Uniform in (0, 1) from the top 53 bits, as splitmix64_uniform_open01
+// (tokenizer_tests.cpp:2109-2119) forms it, then rounded to float.
+__device__ __forceinline__ float uniform_open01(uint64_t bits64) {
+  constexpr double scale = 1.0 / 9007199254740992.0;  // 2^-53
+  double v = ((double)(bits64 >> 11) + 0.5) * scale;
+  if (v <= 0.0) v = scale;
+  else if (v >= 1.0) v = 1.0 - scale;
+  return (float)v;
+}
+
+__global__ __launch_bounds__(256) void normal_noise_kernel(size_t n, uint64_t seed,
+                                                           float temperature,
+                                                           float* __restrict__ out) {
+  const size_t pair = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t i = 2 * pair;
+  if (i >= n) return;
+  const float u1 = uniform_open01(splitmix64_at(seed, 2 * (uint64_t)pair + 1));
+  const float u2 = uniform_open01(splitmix64_at(seed, 2 * (uint64_t)pair + 2));
+  constexpr float two_pi = 6.2831853071795864769f;
+  const float radius = sqrtf(-2.0f * logf(u1));
+  const float angle = two_pi * u2;
+  out[i] = radius * cosf(angle) * temperature;
+  if (i + 1 < n) out[i + 1] = radius * sinf(angle) * temperature;
+}
+
+hipError_t launch_normal_noise(size_t n, uint64_t seed, float temperature, float* out,
+                               hipStream_t s) {
+  if (n == 0) return hipErrorInvalidValue;
+  const size_t pairs = (n + 1) / 2;
+  hipLaunchKernelGGL(normal_noise_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s,
+                     n, seed, temperature, out);
+  return hipGetLastError();
+}
+
+}  // namespace mit2hip

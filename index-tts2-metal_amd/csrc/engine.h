@@ -117,6 +117,28 @@ class Engine {
   // launch.  A measurement hook: kernel ids are listed in mit2cfm.h.
   void profile_launch(int kernel, int count, double* flops, double* bytes, std::string* name);
 
+  // ---- condition and noise producer (the step before the decode).
+  bool has_length_regulator() const;
+  // run_length_regulator_full (gpt.cpp:5298/5313) on DEVICE pointers:
+  // s_infer [in_tokens][1024] fp32 -> out [out_tokens][512] fp32.  Enqueued
+  // on stream(), not synchronised.
+  void length_regulator_device(const float* s_infer, int in_tokens, int out_tokens, float* out);
+  // The decode condition (synthesis_pipeline.cpp:1027-1035): generated =
+  // floor(codes * 1.72f) frames; cond [prompt_tokens + generated][512] =
+  // [prompt_cond rows 0..prompt_tokens-1 ; length_regulator(s_infer)].
+  // DEVICE pointers, enqueued on stream(); returns generated.
+  int condition_device(const float* s_infer, int codes, const float* prompt_cond,
+                       int prompt_tokens, float* cond);
+  // Host-pointer versions of the two above (synchronous).
+  void length_regulator_host(const float* s_infer, int in_tokens, int out_tokens, float* out);
+  int condition_host(const float* s_infer, int codes, const float* prompt_cond,
+                     int prompt_tokens, float* cond);
+  // make_deterministic_normal_noise (tokenizer_tests.cpp:2121) into a DEVICE
+  // buffer of n floats, on stream().
+  void normal_noise_device(size_t n, uint64_t seed, float temperature, float* out);
+  // Frames the condition producer makes from `codes` semantic tokens.
+  static int generated_frames(int codes);
+
   // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
   void set_use_graph(bool on) { use_graph_ = on; }
   void sync();
@@ -141,6 +163,24 @@ class Engine {
   bool use_graph_ = true;
   std::unique_ptr<Weights> w_;
   std::unique_ptr<Workspace> ws_;
+  // Length-regulator buffers, grown on demand (separate from the decode's
+  // workspace so a condition call never invalidates captured decode graphs).
+  struct LrBufs {
+    Arena arena;
+    int cap_in = 0, cap_out = 0;
+    float* in32;   // [cap_in][1024]  host staging
+    half_t* s16;   // [cap_in][1024]
+    half_t* p16;   // [cap_in][512]   content_in_proj output
+    half_t* x16;   // [cap_out + 1][512] conv operand (last used row all zero)
+    float* y32;    // [cap_out][512]  conv output
+    float* sum_p;  // [cap_out][16]   per-row partial sums
+    float* ssq_p;  // [cap_out][16]   per-row partial sums of squares
+    float* stats;  // [2]             GroupNorm mean, 1/std
+    float* out32;  // [cap_out + prompt][512] host staging of the result
+    int cap_cond = 0;
+  };
+  LrBufs lr_;
+  void ensure_lr(int in_tokens, int out_tokens, int cond_rows);
   // Decode tables per step count, computed once per context (decode_tables).
   struct TableSet {
     Arena arena;

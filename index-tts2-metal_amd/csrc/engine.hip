@@ -22,6 +22,7 @@
 #include <cstring>
 #include <unordered_map>
 
+#include "condition.h"
 #include "gemm.h"
 #include "rowops.h"
 
@@ -98,12 +99,29 @@ struct Weights {
   // conv2 . final_layer.linear as one map (both are linear and nothing reads
   // the 512-wide final-layer output in between): [80][512] and [80].
   half_t* c2f_w; float* c2f_b;
+  // Length regulator (condition producer), present when the bundle has it:
+  // content_in_proj [512][1024]; conv k=3 taps tap-major [512][3 * 512];
+  // GroupNorm affine [512]; the k=1 output conv [512][512].
+  bool has_lr = false;
+  half_t* lr_proj_w; float* lr_proj_b;
+  half_t* lr_conv_w[4]; float* lr_conv_b[4];
+  float* lr_gn_w[4]; float* lr_gn_b[4];
+  half_t* lr_out_w; float* lr_out_b;
 };
 
 namespace {
 
 struct HostModel {
   std::unordered_map<std::string, std::vector<float>> t;
+  bool has(const std::string& full) const { return t.count(full) != 0; }
+  const std::vector<float>& get_full(const std::string& full, size_t elems) const {
+    auto it = t.find(full);
+    if (it == t.end()) throw std::invalid_argument("missing tensor: " + full);
+    if (it->second.size() != elems)
+      throw std::invalid_argument("tensor " + full + " has " + std::to_string(it->second.size()) +
+                                  " elements, expected " + std::to_string(elems));
+    return it->second;
+  }
   const std::vector<float>& get(const std::string& tail, size_t elems) const {
     auto it = t.find(std::string(kPfx) + tail);
     if (it == t.end()) throw std::invalid_argument("missing tensor: " + std::string(kPfx) + tail);
@@ -429,6 +447,39 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
     }
     W.c2f_w = up.f16(wcf);
     W.c2f_b = up.f32(bcf);
+  }
+
+  // Length regulator (gpt.cpp:5271-5340): all of its tensors or none.
+  {
+    const std::string lp = "s2mel.net.length_regulator.";
+    int present = 0;
+    for (const auto& kv : hm.t) present += kv.first.compare(0, lp.size(), lp) == 0;
+    if (present) {
+      W.lr_proj_w = up.f16(hm.get_full(lp + "content_in_proj.weight", 512 * 1024));
+      W.lr_proj_b = up.f32(hm.get_full(lp + "content_in_proj.bias", 512));
+      const int conv_i[4] = {0, 3, 6, 9}, norm_i[4] = {1, 4, 7, 10};
+      for (int b = 0; b < 4; ++b) {
+        const std::string c = lp + "model." + std::to_string(conv_i[b]);
+        const std::string n = lp + "model." + std::to_string(norm_i[b]);
+        // PyTorch [oc][ic][k] -> tap-major [oc][k * 512 + ic]
+        const auto& w = hm.get_full(c + ".weight", (size_t)512 * 512 * 3);
+        std::vector<float> tw((size_t)512 * 1536);
+        for (int oc = 0; oc < 512; ++oc)
+          for (int ic = 0; ic < 512; ++ic)
+            for (int k = 0; k < 3; ++k)
+              tw[(size_t)oc * 1536 + k * 512 + ic] = w[((size_t)oc * 512 + ic) * 3 + k];
+        W.lr_conv_w[b] = up.f16(tw);
+        W.lr_conv_b[b] = up.f32(hm.get_full(c + ".bias", 512));
+        W.lr_gn_w[b] = up.f32(hm.get_full(n + ".weight", 512));
+        W.lr_gn_b[b] = up.f32(hm.get_full(n + ".bias", 512));
+      }
+      W.lr_out_w = up.f16(hm.get_full(lp + "model.12.weight", 512 * 512));
+      W.lr_out_b = up.f32(hm.get_full(lp + "model.12.bias", 512));
+      if (present != 20)
+        throw std::invalid_argument("length regulator: expected 20 tensors, found " +
+                                    std::to_string(present));
+      W.has_lr = true;
+    }
   }
 
   ws_ = std::make_unique<Workspace>();
@@ -1267,6 +1318,125 @@ void Engine::op_linear(const float* A, const float* Wt, const float* bias, int M
   g.bias = bias ? b.as<float>() : nullptr; g.C32 = c.as<float>(); g.ldc32 = N;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, stream_));
   d2h(out, c.p, (size_t)M * N * 4, stream_);
+}
+
+// ------------------------------------------------------------------ condition producer
+bool Engine::has_length_regulator() const { return w_->has_lr; }
+
+int Engine::generated_frames(int codes) {
+  // static_cast<uint32_t>(static_cast<float>(codes) * 1.72f), synthesis_pipeline.cpp:1012
+  return (int)(uint32_t)((float)codes * 1.72f);
+}
+
+void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
+  if (in_tokens <= lr_.cap_in && out_tokens <= lr_.cap_out && cond_rows <= lr_.cap_cond) return;
+  HIP_OK(hipStreamSynchronize(stream_));
+  const int ci = std::max(in_tokens, lr_.cap_in), co = std::max(out_tokens, lr_.cap_out);
+  const int cc = std::max(cond_rows, lr_.cap_cond);
+  size_t bytes = 0;
+  auto f = [&](size_t n) { bytes += (n * 4 + 255) / 256 * 256; };
+  auto h = [&](size_t n) { bytes += (n * 2 + 255) / 256 * 256; };
+  f((size_t)ci * 1024); h((size_t)ci * 1024); h((size_t)ci * 512); h((size_t)(co + 1) * 512);
+  f((size_t)co * 512); f((size_t)co * 16); f((size_t)co * 16); f(2); f((size_t)cc * 512);
+  lr_.arena.reserve(bytes);
+  Arena& a = lr_.arena;
+  lr_.in32 = static_cast<float*>(a.take((size_t)ci * 1024 * 4));
+  lr_.s16 = static_cast<half_t*>(a.take((size_t)ci * 1024 * 2));
+  lr_.p16 = static_cast<half_t*>(a.take((size_t)ci * 512 * 2));
+  lr_.x16 = static_cast<half_t*>(a.take((size_t)(co + 1) * 512 * 2));
+  lr_.y32 = static_cast<float*>(a.take((size_t)co * 512 * 4));
+  lr_.sum_p = static_cast<float*>(a.take((size_t)co * 16 * 4));
+  lr_.ssq_p = static_cast<float*>(a.take((size_t)co * 16 * 4));
+  lr_.stats = static_cast<float*>(a.take(2 * 4));
+  lr_.out32 = static_cast<float*>(a.take((size_t)cc * 512 * 4));
+  lr_.cap_in = ci;
+  lr_.cap_out = co;
+  lr_.cap_cond = cc;
+}
+
+// run_length_regulator_full (gpt.cpp:5271-5313):
+//   content_in_proj GEMM (f16 out) -> nearest rows (+ the zero padding row)
+//   -> 4 x [k=3 zero-padded conv GEMM writing fp32 rows and per-row partial
+//      sums / sums of squares; GroupNorm statistics; GroupNorm + Mish -> f16]
+//   -> k=1 conv GEMM into `out`.
+void Engine::length_regulator_device(const float* s_infer, int in_tokens, int out_tokens,
+                                     float* out) {
+  Weights& W = *w_;
+  if (!W.has_lr)
+    throw std::runtime_error("length regulator: the context has no s2mel.net.length_regulator.* tensors");
+  if (in_tokens <= 0 || out_tokens <= 0)
+    throw std::invalid_argument("length regulator: token counts must be positive");
+  HIP_OK(hipSetDevice(device_));
+  ensure_lr(in_tokens, out_tokens, 0);
+  hipStream_t s = stream_;
+  to_f16(s_infer, lr_.s16, (size_t)in_tokens * 1024, s);
+  {
+    GemmArgs g;
+    g.M = in_tokens; g.N = 512; g.K = 1024; g.A = lr_.s16; g.lda = 1024;
+    g.W = W.lr_proj_w; g.ldw = 1024; g.bias = W.lr_proj_b; g.C16 = lr_.p16; g.ldc16 = 512;
+    HIP_OK(launch_gemm(g, A_PLAIN, EPI_F16, s));
+  }
+  HIP_OK(launch_nearest_rows(lr_.p16, in_tokens, out_tokens, (float)in_tokens / (float)out_tokens,
+                             lr_.x16, s));
+  for (int b = 0; b < 4; ++b) {
+    GemmArgs g;
+    g.M = out_tokens; g.N = 512; g.K = 3 * 512; g.T = out_tokens; g.conv_c = 512;
+    g.A = lr_.x16; g.lda = 512;
+    g.W = W.lr_conv_w[b]; g.ldw = 3 * 512; g.bias = W.lr_conv_b[b];
+    g.C32 = lr_.y32; g.ldc32 = 512; g.sum_out = lr_.sum_p; g.ssq_out = lr_.ssq_p;
+    HIP_OK(launch_gemm(g, A_CONV3Z, EPI_F32, s));
+    HIP_OK(launch_gn_stats(lr_.sum_p, lr_.ssq_p, out_tokens, 1e-5f, lr_.stats, s));
+    HIP_OK(launch_gn_mish(lr_.y32, lr_.stats, W.lr_gn_w[b], W.lr_gn_b[b], out_tokens, lr_.x16, s));
+  }
+  GemmArgs g;
+  g.M = out_tokens; g.N = 512; g.K = 512; g.A = lr_.x16; g.lda = 512;
+  g.W = W.lr_out_w; g.ldw = 512; g.bias = W.lr_out_b; g.C32 = out; g.ldc32 = 512;
+  HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
+}
+
+int Engine::condition_device(const float* s_infer, int codes, const float* prompt_cond,
+                             int prompt_tokens, float* cond) {
+  if (codes <= 0 || prompt_tokens <= 0)
+    throw std::invalid_argument("condition: codes and prompt_tokens must be positive");
+  const int gen = generated_frames(codes);
+  if (gen <= 0) throw std::invalid_argument("condition: generated frame count is zero");
+  HIP_OK(hipSetDevice(device_));
+  HIP_OK(hipMemcpyAsync(cond, prompt_cond, (size_t)prompt_tokens * 512 * 4,
+                        hipMemcpyDeviceToDevice, stream_));
+  length_regulator_device(s_infer, codes, gen, cond + (size_t)prompt_tokens * 512);
+  return gen;
+}
+
+void Engine::length_regulator_host(const float* s_infer, int in_tokens, int out_tokens,
+                                   float* out) {
+  if (in_tokens <= 0 || out_tokens <= 0)
+    throw std::invalid_argument("length regulator: token counts must be positive");
+  HIP_OK(hipSetDevice(device_));
+  ensure_lr(in_tokens, out_tokens, out_tokens);
+  h2d(lr_.in32, s_infer, (size_t)in_tokens * 1024 * 4, stream_);
+  length_regulator_device(lr_.in32, in_tokens, out_tokens, lr_.out32);
+  d2h(out, lr_.out32, (size_t)out_tokens * 512 * 4, stream_);
+}
+
+int Engine::condition_host(const float* s_infer, int codes, const float* prompt_cond,
+                           int prompt_tokens, float* cond) {
+  if (codes <= 0 || prompt_tokens <= 0)
+    throw std::invalid_argument("condition: codes and prompt_tokens must be positive");
+  const int gen = generated_frames(codes);
+  if (gen <= 0) throw std::invalid_argument("condition: generated frame count is zero");
+  HIP_OK(hipSetDevice(device_));
+  ensure_lr(codes, gen, prompt_tokens + gen);
+  h2d(lr_.in32, s_infer, (size_t)codes * 1024 * 4, stream_);
+  h2d(lr_.out32, prompt_cond, (size_t)prompt_tokens * 512 * 4, stream_);
+  length_regulator_device(lr_.in32, codes, gen, lr_.out32 + (size_t)prompt_tokens * 512);
+  d2h(cond, lr_.out32, (size_t)(prompt_tokens + gen) * 512 * 4, stream_);
+  return gen;
+}
+
+void Engine::normal_noise_device(size_t n, uint64_t seed, float temperature, float* out) {
+  if (n == 0) throw std::invalid_argument("noise: empty shape");
+  HIP_OK(hipSetDevice(device_));
+  HIP_OK(launch_normal_noise(n, seed, temperature, out, stream_));
 }
 
 }  // namespace mit2hip

@@ -18,6 +18,8 @@ enum AMode : int {
   A_PLAIN = 0,   // A[m][k] = A[m*lda + k]
   A_CONCAT = 1,  // k <  K1: A[m*lda + k];  k >= K1: A2[m*lda2 + k - K1]
   A_CONV5 = 2,   // k = tap*kConvC + c: A[(b*T + reflect(t + tap - 2))*lda + c], m = b*T + t
+  A_CONV3Z = 3,  // k = tap*kConvC + c: A[(b*T + t + tap - 1)*lda + c], zero outside [0, T):
+                 // A holds M + 1 rows and row M is all zero (the padding taps read it)
 };
 
 enum EpiMode : int {
@@ -80,6 +82,9 @@ struct GemmArgs {
   const float* sc_g = nullptr;
   float* ssq_out = nullptr;
   const float* ssq_in = nullptr;
+  // EPI_F32: per-row sums of each 32-column block of the output (layout of
+  // ssq_out), for a norm whose statistics span whole rows or the whole tensor.
+  float* sum_out = nullptr;
 };
 
 // Number of per-row partial sums of squares a 512-wide producer writes.

@@ -199,7 +199,25 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   struct ConvRows {
     int r0, r1, r2, r3, r4;  // element offset of row reflect(t + tap - 2), tap 0..4
   };
-  ConvRows conv_rows[AM == A_CONV5 ? LA : 1];
+  constexpr bool kConv = AM == A_CONV5 || AM == A_CONV3Z;
+  ConvRows conv_rows[kConv ? LA : 1];
+  if constexpr (AM == A_CONV3Z) {
+    // k = 3 with zero padding: taps t-1, t, t+1; a tap outside the sequence
+    // reads row M, which the caller keeps all zero.
+    static_assert(kConvC % SK == 0, "a K stage must lie within one conv tap");
+#pragma unroll
+    for (int j = 0; j < LA; ++j) {
+      const int row = ((wave * LA + j) * 64 + lane) / CPR;
+      const int m = min(m0 + row, p.M - 1);
+      const int b = m / p.T;
+      const int t = m - b * p.T;
+      const int base = b * p.T;
+      conv_rows[j].r0 = (t > 0 ? base + t - 1 : p.M) * p.lda;
+      conv_rows[j].r1 = (base + t) * p.lda;
+      conv_rows[j].r2 = (t + 1 < p.T ? base + t + 1 : p.M) * p.lda;
+      conv_rows[j].r3 = conv_rows[j].r4 = 0;
+    }
+  }
   if constexpr (AM == A_CONV5) {
     static_assert(kConvC % SK == 0, "a K stage must lie within one conv tap");
 #pragma unroll
@@ -223,10 +241,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       return p.A + (size_t)m * p.lda + k;
     } else if constexpr (AM == A_CONCAT) {
       return k < p.K1 ? p.A + (size_t)m * p.lda + k : p.A2 + (size_t)m * p.lda2 + (k - p.K1);
-    } else {
+    } else if constexpr (AM == A_CONV5) {
       const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);  // stage start: uniform
       const ConvRows& cr = conv_rows[j];
       const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : tap == 2 ? cr.r2 : tap == 3 ? cr.r3 : cr.r4;
+      return p.A + ro + (k - tap * kConvC);
+    } else {
+      const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);
+      const ConvRows& cr = conv_rows[j];
+      const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : cr.r2;
       return p.A + ro + (k - tap * kConvC);
     }
   };
@@ -382,8 +405,9 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       const int m = row_base + 16 * i;
       const bool live = m < p.M;
       float ssq[(NI + 1) / 2];  // EPI_F32 with ssq_out: this lane's share per 32-column block
+      float s1[(NI + 1) / 2];   // ... and with sum_out
 #pragma unroll
-      for (int q = 0; q < (NI + 1) / 2; ++q) ssq[q] = 0.0f;
+      for (int q = 0; q < (NI + 1) / 2; ++q) ssq[q] = s1[q] = 0.0f;
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         const int n = col_base + 16 * j;
@@ -395,6 +419,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
             v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
           }
           ssq[j / 2] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+          s1[j / 2] += (v.x + v.y) + (v.z + v.w);
           if (!live) continue;
           *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
           if (p.C16) st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
@@ -448,6 +473,16 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
             t += __shfl_xor(t, 32, kWave);
             if (live && lg == 0)
               p.ssq_out[(size_t)m * kSsqParts + ((n0 + wn * WTN + 32 * q) >> 5)] = t;
+          }
+        }
+        if (p.sum_out) {
+#pragma unroll
+          for (int q = 0; q < NI / 2; ++q) {
+            float t = s1[q];
+            t += __shfl_xor(t, 16, kWave);
+            t += __shfl_xor(t, 32, kWave);
+            if (live && lg == 0)
+              p.sum_out[(size_t)m * kSsqParts + ((n0 + wn * WTN + 32 * q) >> 5)] = t;
           }
         }
       }
@@ -600,7 +635,8 @@ static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
 template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2, int KG = 1>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
   if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K groups need equal stage counts
-  const TileMap tm = make_tile_map(a.M, a.N, a.K, AM == A_CONV5 ? a.conv_c : a.K, BM, BN);
+  const TileMap tm = make_tile_map(a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z ? a.conv_c : a.K,
+                                   BM, BN);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG>), dim3(8 * tm.per_xcd),
                      dim3(64 * WM * WN * KG), 0, s,
                      a, tm);
@@ -649,6 +685,8 @@ hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t 
     return hipErrorInvalidValue;
   if (amode == A_CONV5 && (a.T <= 0 || a.conv_c != kConvC || a.K != 5 * kConvC))
     return hipErrorInvalidValue;
+  if (amode == A_CONV3Z && (a.T <= 0 || a.M % a.T != 0 || a.conv_c != kConvC || a.K != 3 * kConvC))
+    return hipErrorInvalidValue;
   if (amode == A_PLAIN) {
     switch (epi) {
       case EPI_F32: return launch_am_epi<A_PLAIN, EPI_F32>(a, stream);
@@ -666,6 +704,8 @@ hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t 
     if (epi == EPI_DUAL) return launch_am_epi<A_CONCAT, EPI_DUAL>(a, stream);
   } else if (amode == A_CONV5) {
     if (epi == EPI_GATE) return launch_am_epi<A_CONV5, EPI_GATE>(a, stream);
+  } else if (amode == A_CONV3Z) {
+    if (epi == EPI_F32) return launch_am_epi<A_CONV3Z, EPI_F32>(a, stream);
   }
   return hipErrorInvalidValue;  // combination not built
 }

@@ -91,6 +91,11 @@ def lib() -> ctypes.CDLL:
                                         ctypes.POINTER(ctypes.c_char_p)]),
         "mit2cfm_inspect_bundle": (st, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64),
                                         ctypes.POINTER(ctypes.c_uint64), u32]),
+        "mit2cfm_length_regulator": (st, [vp, _f32p, u32, u32, _f32p]),
+        "mit2cfm_condition": (st, [vp, _f32p, u32, _f32p, u32, _f32p, _u32p]),
+        "mit2cfm_condition_device": (st, [vp, vp, u32, vp, u32, vp, _u32p, u32]),
+        "mit2cfm_generated_frames": (u32, [u32]),
+        "mit2cfm_noise_device": (st, [vp, u32, u32, u64, f32, vp, u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -163,6 +168,37 @@ def synthetic_tensors(seed: int = 20240605, stddev: float = 0.02) -> dict[str, n
         arr = np.empty(shape, np.float16 if dt == "f16" else np.float32)
         _check(L.mit2cfm_synthetic_tensor_fill(i, seed, stddev, arr.ctypes.data_as(ctypes.c_void_p)))
         out[name] = arr
+    return out
+
+
+LR_PREFIX = "s2mel.net.length_regulator."
+
+
+def generated_frames(codes: int) -> int:
+    """floor(codes * 1.72f): frames the condition producer makes from `codes` tokens."""
+    return int(lib().mit2cfm_generated_frames(codes))
+
+
+def length_regulator_specs() -> list[tuple[str, tuple[int, ...]]]:
+    """The s2mel length regulator's tensors (gpt.cpp:5271-5340), sorted by name."""
+    specs = [("content_in_proj.weight", (512, 1024)), ("content_in_proj.bias", (512,)),
+             ("model.12.weight", (512, 512, 1)), ("model.12.bias", (512,))]
+    for i in (0, 3, 6, 9):
+        specs += [(f"model.{i}.weight", (512, 512, 3)), (f"model.{i}.bias", (512,))]
+    for i in (1, 4, 7, 10):
+        specs += [(f"model.{i}.weight", (512,)), (f"model.{i}.bias", (512,))]
+    return sorted((LR_PREFIX + n, shape) for n, shape in specs)
+
+
+def synthetic_lr_tensors(seed: int = 20240606, stddev: float = 0.02) -> dict[str, np.ndarray]:
+    """Length-regulator weights, f16: N(0, stddev) from seed + (index in sorted-name
+    order); GroupNorm weights are 1 + N(0, stddev)."""
+    out = {}
+    for i, (name, shape) in enumerate(length_regulator_specs()):
+        n = int(np.prod(shape))
+        v = normal_noise(1, n, seed + i, stddev).reshape(shape)
+        gn_weight = name.endswith(".weight") and len(shape) == 1
+        out[name] = (v + 1.0 if gn_weight else v).astype(np.float16)
     return out
 
 
@@ -318,6 +354,45 @@ class Context:
         self._c(lib().mit2cfm_profile_launch(self._h, kernel, count, ctypes.byref(f), ctypes.byref(b),
                                              ctypes.byref(n)))
         return n.value.decode(), f.value, b.value
+
+    # -- condition and noise producer
+    def length_regulator(self, s_infer, out_tokens: int) -> np.ndarray:
+        """run_length_regulator_full (gpt.cpp:5298/5313): s_infer [in_tokens, 1024]
+        -> [out_tokens, 512]."""
+        x = _f32(s_infer)
+        in_tokens = x.size // 1024
+        out = np.empty((out_tokens, 512), np.float32)
+        self._c(lib().mit2cfm_length_regulator(self._h, _p(x), in_tokens, out_tokens, _p(out)))
+        return out
+
+    def condition(self, s_infer, prompt_cond, prompt_tokens: int) -> np.ndarray:
+        """The decode condition (synthesis_pipeline.cpp:1012-1035): [prompt_cond[:P];
+        length_regulator(s_infer, floor(codes * 1.72))] -> [P + generated, 512]."""
+        x = _f32(s_infer)
+        codes = x.size // 1024
+        pc = _f32(prompt_cond)
+        if pc.size < prompt_tokens * 512:
+            raise ValueError("prompt_cond holds fewer than prompt_tokens rows")
+        gen = generated_frames(codes)
+        out = np.empty((prompt_tokens + gen, 512), np.float32)
+        g = np.zeros(1, np.uint32)
+        self._c(lib().mit2cfm_condition(self._h, _p(x), codes, _p(pc), prompt_tokens, _p(out), _pu(g)))
+        assert int(g[0]) == gen
+        return out
+
+    def condition_device(self, s_infer_ptr: int, codes: int, prompt_ptr: int, prompt_tokens: int,
+                         cond_ptr: int, sync: bool = False) -> int:
+        """The condition on device buffers (raw addresses); returns the generated frames."""
+        g = np.zeros(1, np.uint32)
+        self._c(lib().mit2cfm_condition_device(self._h, s_infer_ptr, codes, prompt_ptr, prompt_tokens,
+                                               cond_ptr, _pu(g), FLAG_SYNC if sync else 0))
+        return int(g[0])
+
+    def noise_device(self, tokens: int, channels: int, seed: int, temperature: float, out_ptr: int,
+                     sync: bool = False) -> None:
+        """make_deterministic_normal_noise (tokenizer_tests.cpp:2121) into a device buffer."""
+        self._c(lib().mit2cfm_noise_device(self._h, tokens, channels, seed, temperature, out_ptr,
+                                           FLAG_SYNC if sync else 0))
 
     # -- stages (parity harness)
     def timestep_embedder(self, t: float, which: int) -> np.ndarray:

@@ -187,6 +187,73 @@ void orc_linear_rows(const float* w, const float* b, const float* x, uint32_t to
 }
 
 /* ------------------------------------------------------------------------ */
+/* length regulator pieces                                                    */
+/* ------------------------------------------------------------------------ */
+/* cpu_nearest_interpolate (tokenizer_tests.cpp:3127-3140): in_t =
+ * floor(out_t * (in/out)) with the scale and the product in float, clamped. */
+void orc_nearest_interpolate(const float* x, uint32_t in_tokens, uint32_t out_tokens,
+                             uint32_t width, float* out) {
+    const float scale = (float)in_tokens / (float)out_tokens;
+    for (uint32_t t = 0; t < out_tokens; ++t) {
+        uint32_t src = (uint32_t)floorf((float)t * scale);
+        if (src >= in_tokens) src = in_tokens - 1;
+        memcpy(out + (size_t)t * width, x + (size_t)src * width, width * sizeof(float));
+    }
+}
+
+/* cpu_groupnorm1 (tokenizer_tests.cpp:3874-3896): one group over all
+ * tokens x channels; mean and variance are single fp32 accumulators walked in
+ * memory order, as the reference does. */
+void orc_groupnorm1(const float* x, const float* gamma, const float* beta, uint32_t tokens,
+                    uint32_t channels, float eps, float* out) {
+    const size_t count = (size_t)tokens * channels;
+    float mean = 0.0f;
+    for (size_t i = 0; i < count; ++i) mean += x[i];
+    mean /= (float)count;
+    float var = 0.0f;
+    for (size_t i = 0; i < count; ++i) {
+        const float d = x[i] - mean;
+        var += d * d;
+    }
+    var /= (float)count;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    for (uint32_t t = 0; t < tokens; ++t)
+        for (uint32_t c = 0; c < channels; ++c) {
+            const size_t i = (size_t)t * channels + c;
+            out[i] = (x[i] - mean) * inv_std * gamma[c] + beta[c];
+        }
+}
+
+/* cpu_mish (tokenizer_tests.cpp:3898-3904): x * tanh(log1p(exp(x))). */
+void orc_mish(const float* x, size_t n, float* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = x[i] * tanhf(log1pf(expf(x[i])));
+}
+
+/* run_length_regulator_full_cpu (gpt.cpp:5298-5313) with its front
+ * (gpt.cpp:5271-5281): content_in_proj per input token, nearest
+ * interpolation, 4 x (conv k=3, groupnorm1 eps 1e-5, mish), conv k=1. */
+void orc_length_regulator(const float* input, uint32_t in_tokens, uint32_t out_tokens,
+                          const float* proj_w, const float* proj_b,
+                          const float* const* conv_w, const float* const* conv_b,
+                          const float* const* gn_w, const float* const* gn_b,
+                          const float* out_w, const float* out_b, float* out) {
+    float* projected = fbuf((size_t)in_tokens * 512);
+    orc_linear_rows(proj_w, proj_b, input, in_tokens, 512, 1024, projected);
+    float* x = fbuf((size_t)out_tokens * 512);
+    float* y = fbuf((size_t)out_tokens * 512);
+    orc_nearest_interpolate(projected, in_tokens, out_tokens, 512, x);
+    for (int blk = 0; blk < 4; ++blk) {
+        orc_conv1d_same(x, conv_w[blk], conv_b[blk], out_tokens, 512, 512, 3, y);
+        orc_groupnorm1(y, gn_w[blk], gn_b[blk], out_tokens, 512, 1e-5f, x);
+        orc_mish(x, (size_t)out_tokens * 512, x);
+    }
+    orc_conv1d_same(x, out_w, out_b, out_tokens, 512, 512, 1, out);
+    free(projected);
+    free(x);
+    free(y);
+}
+
+/* ------------------------------------------------------------------------ */
 /* conv1d, tokenizer_tests.cpp:3142-3161, 3836-3872                          */
 /* ------------------------------------------------------------------------ */
 /* One output token of cpu_conv1d_same: acc = bias; for in_c: for k: acc += x*w

@@ -54,6 +54,20 @@ void orc_reflect_pad(const float* x, uint32_t tokens, uint32_t channels,
 void orc_conv1d_reflect_same(const float* x, const float* w, const float* b,
                              uint32_t tokens, uint32_t in_ch, uint32_t out_ch,
                              uint32_t kernel, float* out);         /* tokenizer_tests.cpp:3866 */
+/* ---- condition producer: the s2mel length regulator (gpt.cpp:5271-5340) -- */
+void orc_nearest_interpolate(const float* x, uint32_t in_tokens, uint32_t out_tokens,
+                             uint32_t width, float* out);          /* tokenizer_tests.cpp:3127 */
+void orc_groupnorm1(const float* x, const float* gamma, const float* beta, uint32_t tokens,
+                    uint32_t channels, float eps, float* out);     /* tokenizer_tests.cpp:3874 */
+void orc_mish(const float* x, size_t n, float* out);               /* tokenizer_tests.cpp:3898 */
+/* run_length_regulator_full_cpu (gpt.cpp:5298): input [in_tokens, 1024] ->
+ * out [out_tokens, 512].  proj_w [512, 1024]; conv_w[b] [512, 512, 3] (PyTorch
+ * [out, in, k]); gn_w[b], gn_b[b], conv_b[b] [512]; out_w [512, 512] (k = 1). */
+void orc_length_regulator(const float* input, uint32_t in_tokens, uint32_t out_tokens,
+                          const float* proj_w, const float* proj_b,
+                          const float* const* conv_w, const float* const* conv_b,
+                          const float* const* gn_w, const float* const* gn_b,
+                          const float* out_w, const float* out_b, float* out);
 void orc_timestep_embedding(const float* t, uint32_t n_t, const float* freqs,
                             uint32_t half, float scale, float* out); /* tokenizer_tests.cpp:3947 */
 void orc_attention_head_masked(const float* q, const float* k, const float* v,

@@ -46,6 +46,12 @@ def lib() -> ctypes.CDLL:
             "orc_linear_rows": (None, [_f32p, _f32p, _f32p, u32, u32, u32, _f32p]),
             "orc_conv1d_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, _f32p]),
             "orc_reflect_pad": (None, [_f32p, u32, u32, u32, u32, _f32p]),
+            "orc_nearest_interpolate": (None, [_f32p, u32, u32, u32, _f32p]),
+            "orc_groupnorm1": (None, [_f32p, _f32p, _f32p, u32, u32, f32, _f32p]),
+            "orc_mish": (None, [_f32p, ctypes.c_size_t, _f32p]),
+            "orc_length_regulator": (None, [_f32p, u32, u32, _f32p, _f32p, ctypes.POINTER(_f32p),
+                                            ctypes.POINTER(_f32p), ctypes.POINTER(_f32p),
+                                            ctypes.POINTER(_f32p), _f32p, _f32p, _f32p]),
             "orc_conv1d_reflect_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, _f32p]),
             "orc_timestep_embedding": (None, [_f32p, u32, _f32p, u32, f32, _f32p]),
             "orc_attention_head_masked": (None, [_f32p, _f32p, _f32p, _u32p, u32, u32, _f32p]),
@@ -148,6 +154,50 @@ def conv1d_same(x, w, b, kernel) -> np.ndarray:
     cout = b.size
     out = np.empty((tokens, cout), np.float32)
     lib().orc_conv1d_same(P(x), P(w), P(b), tokens, cin, cout, kernel, P(out))
+    return out
+
+
+def nearest_interpolate(x, out_tokens) -> np.ndarray:
+    x = f32(x)
+    in_tokens, width = x.shape
+    out = np.empty((out_tokens, width), np.float32)
+    lib().orc_nearest_interpolate(P(x), in_tokens, out_tokens, width, P(out))
+    return out
+
+
+def groupnorm1(x, gamma, beta, eps=1e-5) -> np.ndarray:
+    x, g, b = f32(x), f32(gamma), f32(beta)
+    tokens, channels = x.shape
+    out = np.empty_like(x)
+    lib().orc_groupnorm1(P(x), P(g), P(b), tokens, channels, eps, P(out))
+    return out
+
+
+def mish(x) -> np.ndarray:
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().orc_mish(P(x), x.size, P(out))
+    return out
+
+
+LR_PREFIX = "s2mel.net.length_regulator."
+
+
+def length_regulator(tensors: dict, s_infer, out_tokens: int) -> np.ndarray:
+    """run_length_regulator_full_cpu (gpt.cpp:5298): s_infer [in_tokens, 1024]
+    -> [out_tokens, 512]; tensors holds the s2mel.net.length_regulator.* weights."""
+    t = {k[len(LR_PREFIX):]: f32(v) for k, v in tensors.items() if k.startswith(LR_PREFIX)}
+    x = f32(s_infer)
+    in_tokens = x.shape[0]
+    conv = [t[f"model.{i}.weight"] for i in (0, 3, 6, 9)]
+    conv_b = [t[f"model.{i}.bias"] for i in (0, 3, 6, 9)]
+    gn = [t[f"model.{i}.weight"] for i in (1, 4, 7, 10)]
+    gn_b = [t[f"model.{i}.bias"] for i in (1, 4, 7, 10)]
+    arrs = lambda lst: (_f32p * 4)(*[P(a) for a in lst])
+    out = np.empty((out_tokens, 512), np.float32)
+    lib().orc_length_regulator(P(x), in_tokens, out_tokens, P(t["content_in_proj.weight"]),
+                               P(t["content_in_proj.bias"]), arrs(conv), arrs(conv_b), arrs(gn),
+                               arrs(gn_b), P(t["model.12.weight"]), P(t["model.12.bias"]), P(out))
     return out
 
 

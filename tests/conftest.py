@@ -7,6 +7,14 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+# torch is imported before the HIP library is loaded so that both share one
+# HIP runtime in the process (tests hand torch-allocated device buffers to the
+# library); importing it does not touch the GPU.
+try:
+    import torch  # noqa: F401
+except ImportError:  # the CPU-only checks do not need it
+    torch = None
+
 ROOT = Path(__file__).resolve().parent.parent
 for p in (ROOT, ROOT / "index-tts2-metal_amd", ROOT / "tests"):
     if str(p) not in sys.path:

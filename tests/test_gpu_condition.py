@@ -1,0 +1,125 @@
+"""GPU parity of the condition and noise producer -- the step before the decode
+(the s2mel length regulator, gpt.cpp:5271-5340; the prompt/condition merge,
+synthesis_pipeline.cpp:1012-1035; the seeded noise, tokenizer_tests.cpp:2121)
+-- through the C ABI, against the CPU oracle on identical seeded inputs.
+
+Bar: the length regulator's output within rel-L2 5e-3 of the oracle.  The
+reference computes this stage in fp32; here the five GEMMs take f16 operands
+with fp32 accumulation (GroupNorm statistics, GroupNorm and Mish stay fp32),
+and each GroupNorm renormalises, so the f16 rounding does not compound.  The
+merge is a copy and is checked bit for bit; the noise's uniforms are integer
+work and bit-identical, so the normals differ only by the GPU's log/cos/sin.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LR_TOL = 5e-3
+
+
+@pytest.fixture(scope="module")
+def lr_tensors(mit2):
+    return mit2.synthetic_lr_tensors(20240606, 0.02)
+
+
+@pytest.fixture(scope="module")
+def ctx_lr(mit2, tensors, lr_tensors):
+    c = mit2.Context({**tensors, **lr_tensors}, device=0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("in_tokens,out_tokens", [(1, 3), (11, 18), (20, 34), (300, 516), (500, 860),
+                                                  (40, 25)])
+def test_length_regulator_matches_oracle(mit2, orc, ctx_lr, lr_tensors, in_tokens, out_tokens):
+    s_infer = mit2.normal_noise(in_tokens, 1024, 7 + in_tokens)
+    print(f"length regulator in={in_tokens} out={out_tokens}", flush=True)
+    got = ctx_lr.length_regulator(s_infer, out_tokens)
+    ref = orc.length_regulator(lr_tensors, s_infer, out_tokens)
+    err = orc.rel_l2(got, ref)
+    print(f"length regulator in={in_tokens} out={out_tokens}: rel-L2 {err:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= LR_TOL
+
+
+def test_length_regulator_repeatable_and_shape_independent(mit2, ctx_lr):
+    """Same input twice -> same bits; a larger call in between (the buffers grow)
+    does not change a later small call."""
+    s_small = mit2.normal_noise(20, 1024, 3)
+    a = ctx_lr.length_regulator(s_small, 34)
+    ctx_lr.length_regulator(mit2.normal_noise(600, 1024, 4), 1032)
+    b = ctx_lr.length_regulator(s_small, 34)
+    assert np.array_equal(a, b)
+
+
+def test_condition_merge(mit2, ctx_lr):
+    codes, P = 500, 258
+    s_infer = mit2.normal_noise(codes, 1024, 11)
+    prompt_all = mit2.normal_noise(300, 512, 12)  # the voice's s2mel_prompt holds >= P rows
+    gen = mit2.generated_frames(codes)
+    assert gen == int(np.float32(codes) * np.float32(1.72)) == 860
+    cond = ctx_lr.condition(s_infer, prompt_all, P)
+    assert cond.shape == (P + gen, 512)
+    assert np.array_equal(cond[:P], prompt_all[:P])
+    assert np.array_equal(cond[P:], ctx_lr.length_regulator(s_infer, gen))
+
+
+def test_condition_device_feeds_decode(mit2, ctx_lr):
+    """Condition and noise made on the GPU feed the device decode directly and
+    give the same decode, bit for bit, as the host-side inputs."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda:0")
+    codes, P, steps, cfg = 20, 6, 2, 0.7
+    gen = mit2.generated_frames(codes)
+    T = P + gen
+    s_infer = mit2.normal_noise(codes, 1024, 21)
+    prompt_cond = mit2.normal_noise(P, 512, 22)
+    prompt_mel = mit2.normal_noise(P, 80, 23, 2.0) - 5.0
+    style = mit2.normal_noise(1, 192, 24)[0]
+    d_s = torch.from_numpy(s_infer).to(dev)
+    d_pc = torch.from_numpy(prompt_cond).to(dev)
+    d_cond = torch.empty((T, 512), dtype=torch.float32, device=dev)
+    d_x0 = torch.empty((T, 80), dtype=torch.float32, device=dev)
+    d_prompt = torch.from_numpy(np.ascontiguousarray(prompt_mel)).to(dev)
+    d_style = torch.from_numpy(style).to(dev)
+    d_out = torch.empty((T, 80), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    assert ctx_lr.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, d_cond.data_ptr()) == gen
+    ctx_lr.noise_device(T, 80, 1234, 1.0, d_x0.data_ptr())
+    ctx_lr.decode_device(d_x0.data_ptr(), d_prompt.data_ptr(), d_cond.data_ptr(), d_style.data_ptr(),
+                         T, P, steps, cfg, d_out.data_ptr(), sync=True)
+    got = d_out.cpu().numpy()
+    cond = ctx_lr.condition(s_infer, prompt_cond, P)
+    assert np.array_equal(d_cond.cpu().numpy(), cond)
+    x0 = d_x0.cpu().numpy()
+    ref = ctx_lr.decode(x0, prompt_mel, cond, style, steps, cfg)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("tokens,channels,seed,temp", [(860, 80, 1, 1.0), (7, 9, 20240605, 0.5),
+                                                       (1, 1, 42, 1.0)])
+def test_noise_device_matches_host_generator(mit2, orc, ctx_lr, tokens, channels, seed, temp):
+    torch = pytest.importorskip("torch")
+    out = torch.empty((tokens, channels), dtype=torch.float32, device="cuda:0")
+    ctx_lr.noise_device(tokens, channels, seed, temp, out.data_ptr(), sync=True)
+    got = out.cpu().numpy()
+    ref = orc.normal_noise(tokens, channels, seed, temp)
+    diff = np.abs(got - ref)
+    print(f"noise {tokens}x{channels}: max |diff| {diff.max():.3e}", flush=True)
+    assert diff.max() <= 4e-6 * max(1.0, float(np.abs(ref).max()))
+
+
+def test_missing_length_regulator_is_a_model_error(mit2, ctx):
+    with pytest.raises(mit2.Mit2CfmError) as e:
+        ctx.length_regulator(mit2.normal_noise(4, 1024, 1), 6)
+    assert e.value.status == mit2.E_MODEL
+
+
+@pytest.fixture(scope="module")
+def ctx(mit2, tensors):
+    c = mit2.Context(tensors, device=0)
+    yield c
+    c.close()
