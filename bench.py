@@ -18,6 +18,13 @@ Prints ONE JSON line.  Extra fields:
   cpu_baseline  the CPU restatement of the reference path on this host:
                 one Euler step (cond + null forward) at T = 860, extrapolated
                 to the 25-step decode.
+  condition_producer
+                the step before the decode, on the GPU: the length regulator
+                on the semantic codes that make this decode's T - P frames,
+                merged with the P prompt rows (mit2cfm_condition_device); time
+                per call from HIP events on the library stream, its
+                algorithmic TFLOP/s, and the oracle's time for one call on
+                the host cores.
 """
 from __future__ import annotations
 
@@ -55,6 +62,7 @@ def parse():
     p.add_argument("--kernel-launches", type=int, default=200)
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, available cores)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cond-calls", type=int, default=50, help="timed condition-producer calls")
     p.add_argument("--calib-mib", type=int, default=256,
                    help="size of the counter-calibration copy (0 = skip)")
     return p.parse_args()
@@ -105,6 +113,36 @@ def cpu_baseline(tensors, T, P, cfm_steps, cfg, threads):
     }
 
 
+def cpu_threads(a) -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return a.cpu_threads or max(1, min(16, n))
+
+
+def condition_codes(generated: int) -> int:
+    """Smallest semantic-token count whose floor(codes * 1.72f) is `generated`
+    (0 when none is)."""
+    import mit2cfm
+
+    for codes in range(max(1, int(generated / 1.72) - 2), int(generated / 1.72) + 3):
+        if mit2cfm.generated_frames(codes) == generated:
+            return codes
+    return 0
+
+
+def condition_cpu_baseline(lr_tensors, s_infer, gen, threads):
+    from oracle import oracle
+
+    oracle.set_threads(threads)
+    t0 = time.perf_counter()
+    oracle.length_regulator(lr_tensors, s_infer, gen)
+    ms = (time.perf_counter() - t0) * 1e3
+    return {"value": round(ms, 1), "unit": "ms per call", "cores": threads, "kind": "port",
+            "sample": f"one length-regulator call ({s_infer.shape[0]} codes -> {gen} frames)"}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -119,7 +157,8 @@ def main():
     T, P, S, cfg = a.tokens, a.prompt, a.cfm_steps, a.cfg
     dev = torch.device("cuda:0")
     tensors = mit2cfm.synthetic_tensors(20240605, 0.02)
-    ctx = mit2cfm.Context(tensors, device=0)
+    lr_tensors = mit2cfm.synthetic_lr_tensors(20240606, 0.02)
+    ctx = mit2cfm.Context({**tensors, **lr_tensors}, device=0)
 
     x0 = mit2cfm.normal_noise(T, 80, 1)
     cond = mit2cfm.normal_noise(T, 512, 2)
@@ -201,6 +240,37 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    # Condition producer (the step before the decode): the length regulator on
+    # `codes` semantic tokens plus the merge with the prompt rows, sized so the
+    # condition is exactly this decode's T frames.
+    codes = condition_codes(T - P)
+    cp = None
+    if codes:
+        gen = mit2cfm.generated_frames(codes)
+        s_infer = mit2cfm.normal_noise(codes, 1024, 6)
+        d_s = torch.from_numpy(s_infer).to(dev)
+        d_pc = torch.from_numpy(mit2cfm.normal_noise(P, 512, 7)).to(dev)
+        d_c = torch.empty((P + gen, 512), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            ctx.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, d_c.data_ptr())
+        ctx.synchronize()
+        c0 = torch.cuda.Event(enable_timing=True)
+        c1 = torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        for _ in range(a.cond_calls):
+            ctx.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, d_c.data_ptr())
+        c1.record(stream)
+        ctx.synchronize()
+        torch.cuda.synchronize()
+        c_ms = c0.elapsed_time(c1) / a.cond_calls
+        lr_flops = 2.0 * codes * 512 * 1024 + 4 * 2.0 * gen * 512 * 1536 + 2.0 * gen * 512 * 512
+        cp = {"workload": f"length regulator {codes} codes -> {gen} frames + merge with {P} prompt rows",
+              "us_per_call": round(c_ms * 1e3, 2), "algorithmic_gflop": round(lr_flops / 1e9, 3),
+              "tflops": round(lr_flops / (c_ms / 1e3) / 1e12, 2)}
+        if not a.no_cpu_baseline:
+            cp["cpu_baseline"] = condition_cpu_baseline(lr_tensors, s_infer, gen, cpu_threads(a))
+
     # Host-pointer decode (PCIe-inclusive; reported, never the headline value).
     ctx.decode(x0, prompt, cond, style, S, cfg)
     t1 = time.perf_counter()
@@ -234,13 +304,10 @@ def main():
         "pcie_inclusive_frames_per_s": round(T / (pcie_ms / 1e3), 1),
         "roofline": roof,
     }
+    if cp:
+        result["condition_producer"] = cp
     if not a.no_cpu_baseline:
-        try:
-            n = len(os.sched_getaffinity(0))
-        except AttributeError:
-            n = os.cpu_count() or 1
-        threads = a.cpu_threads or max(1, min(16, n))
-        result["cpu_baseline"] = cpu_baseline(tensors, T, P, S, cfg, threads)
+        result["cpu_baseline"] = cpu_baseline(tensors, T, P, S, cfg, cpu_threads(a))
     print(json.dumps(result), flush=True)
 
 
