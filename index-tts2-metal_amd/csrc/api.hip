@@ -158,7 +158,9 @@ mit2cfm_status mit2cfm_create_from_bundle(const char* bundle_path, int32_t devic
   if (st != MIT2CFM_OK) return st;
   std::vector<mit2hip::HostTensor> ts;
   for (const auto& info : b->tensors()) {
-    if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0) continue;
+    if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0 &&
+        info.name.rfind("s2mel.net.length_regulator.", 0) != 0)
+      continue;
     int dt;
     if (info.dtype == "f32")
       dt = 0;

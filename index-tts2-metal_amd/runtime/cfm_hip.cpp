@@ -14,7 +14,9 @@ void check(mit2cfm_status st, const mit2cfm_ctx* ctx) {
 HipContext::HipContext(const Bundle& bundle, int device) {
   std::vector<mit2cfm_tensor> ts;
   for (const auto& info : bundle.tensors()) {
-    if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0) continue;
+    if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0 &&
+        info.name.rfind("s2mel.net.length_regulator.", 0) != 0)
+      continue;
     if (info.dtype != "f32" && info.dtype != "f16") continue;
     const bool f16 = info.dtype == "f16";
     ts.push_back({info.name.c_str(), bundle.tensor_data(info), info.nbytes / (f16 ? 2 : 4),
@@ -64,6 +66,17 @@ std::vector<float> run_dit_estimator_step_hip(HipContext& hip, const std::vector
   std::vector<float> out((size_t)tokens * 80);
   check(mit2cfm_estimator_step(hip.get(), x.data(), prompt_x.data(), cond.data(), style.data(),
                                mask.data(), timestep, 1, tokens, out.data()),
+        hip.get());
+  return out;
+}
+
+std::vector<float> run_length_regulator_full_hip(HipContext& hip, const Bundle& /*bundle*/,
+                                                 const std::vector<float>& input,
+                                                 uint32_t in_tokens, uint32_t out_tokens) {
+  if (input.size() != (size_t)in_tokens * 1024)
+    throw std::runtime_error("run_length_regulator_full_hip: input size mismatch");
+  std::vector<float> out((size_t)out_tokens * 512);
+  check(mit2cfm_length_regulator(hip.get(), input.data(), in_tokens, out_tokens, out.data()),
         hip.get());
   return out;
 }

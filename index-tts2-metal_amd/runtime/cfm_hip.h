@@ -18,7 +18,8 @@ namespace mit2 {
 
 class HipContext {
  public:
-  // Uploads the estimator tensors of `bundle` to GPU `device`.
+  // Uploads the estimator tensors of `bundle` (and the length regulator's,
+  // when the bundle holds them) to GPU `device`.
   explicit HipContext(const Bundle& bundle, int device = 0);
   // Seeded synthetic weights (N(0, stddev) f16; stddev 0 = fan-in scaled).
   HipContext(uint64_t synthetic_seed, float stddev, int device = 0);
@@ -47,6 +48,13 @@ std::vector<float> run_dit_estimator_step_hip(HipContext& hip, const std::vector
                                               const std::vector<float>& cond,
                                               const std::vector<float>& style, float timestep,
                                               const std::vector<uint32_t>& mask, uint32_t tokens);
+// run_length_regulator_full_metal (runtime/impl/gpt.cpp:4517, :5313): the
+// s2mel length regulator, input [in_tokens][1024] -> [out_tokens][512].  The
+// context needs the bundle's "s2mel.net.length_regulator.*" tensors (loaded
+// with the estimator by the Bundle constructor above).
+std::vector<float> run_length_regulator_full_hip(HipContext& hip, const Bundle& bundle,
+                                                 const std::vector<float>& input,
+                                                 uint32_t in_tokens, uint32_t out_tokens);
 
 // Euler step count for synthesis: env MIT2_CFM_STEPS, default 16, clamped to
 // the --cfm_steps range 12..25 (main.cpp:57-88, :3181-3187).
