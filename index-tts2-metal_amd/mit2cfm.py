@@ -202,6 +202,94 @@ def synthetic_lr_tensors(seed: int = 20240606, stddev: float = 0.02) -> dict[str
     return out
 
 
+# BigVGAN v2 (22 kHz, 80 bands, 256x) as the reference runs it
+# (dit_cfm_bigvgan.cpp:3606-4062): upsamplers (prefix, in, out, kernel, stride,
+# padding) and resblocks (prefix, channels, kernel).
+BIGVGAN_UPSAMPLERS = [("bigvgan.ups.0.0", 1536, 768, 8, 4, 2), ("bigvgan.ups.1.0", 768, 384, 8, 4, 2),
+                      ("bigvgan.ups.2.0", 384, 192, 4, 2, 1), ("bigvgan.ups.3.0", 192, 96, 4, 2, 1),
+                      ("bigvgan.ups.4.0", 96, 48, 4, 2, 1), ("bigvgan.ups.5.0", 48, 24, 4, 2, 1)]
+BIGVGAN_RESBLOCKS = [(f"bigvgan.resblocks.{3 * g + i}", 768 >> g, (3, 7, 11)[i])
+                     for g in range(6) for i in range(3)]
+
+
+def bigvgan_specs() -> list[tuple[str, tuple[int, ...]]]:
+    """The vocoder's tensors with their checkpoint shapes, sorted by name.  Convs are
+    weight-normed (weight_g, weight_v); a transposed conv's weight_v is [in, out, kernel]
+    and its weight_g [in, 1, 1]; each anti-aliased activation holds a 12-tap upsample
+    and low-pass filter and SnakeBeta's log-scale alpha and beta."""
+    specs = []
+
+    def conv(prefix, rows, cols, k, bias=True):
+        specs.extend([(prefix + ".weight_g", (rows, 1, 1)), (prefix + ".weight_v", (rows, cols, k))])
+        if bias:
+            specs.append((prefix + ".bias", (cols if prefix.startswith("bigvgan.ups") else rows,)))
+
+    def act(prefix, c):
+        specs.extend([(prefix + ".upsample.filter", (1, 1, 12)),
+                      (prefix + ".downsample.lowpass.filter", (1, 1, 12)),
+                      (prefix + ".act.alpha", (c,)), (prefix + ".act.beta", (c,))])
+
+    conv("bigvgan.conv_pre", 1536, 80, 7)
+    for prefix, cin, cout, k, _, _ in BIGVGAN_UPSAMPLERS:
+        conv(prefix, cin, cout, k)
+    for prefix, c, k in BIGVGAN_RESBLOCKS:
+        for p in range(3):
+            conv(f"{prefix}.convs1.{p}", c, c, k)
+            conv(f"{prefix}.convs2.{p}", c, c, k)
+        for a in range(6):
+            act(f"{prefix}.activations.{a}", c)
+    act("bigvgan.activation_post", 24)
+    conv("bigvgan.conv_post", 1, 24, 7, bias=False)
+    return sorted(specs)
+
+
+def kaiser_sinc_filter(kernel: int = 12, cutoff: float = 0.25, half_width: float = 0.3) -> np.ndarray:
+    """The anti-aliasing filter of BigVGAN's alias-free activation for ratio 2: a
+    Kaiser-windowed sinc low-pass, normalised to unit DC gain (Kaiser's
+    empirical beta for the attenuation A = 2.285 (N/2 - 1) pi (4 half_width) + 7.95)."""
+    half = kernel // 2
+    a = 2.285 * (half - 1) * np.pi * (4 * half_width) + 7.95
+    if a > 50.0:
+        beta = 0.1102 * (a - 8.7)
+    elif a >= 21.0:
+        beta = 0.5842 * (a - 21.0) ** 0.4 + 0.07886 * (a - 21.0)
+    else:
+        beta = 0.0
+    window = np.kaiser(kernel, beta)
+    time = (np.arange(-half, half) + 0.5) if kernel % 2 == 0 else (np.arange(kernel) - half)
+    f = 2 * cutoff * window * np.sinc(2 * cutoff * time)
+    return (f / f.sum()).astype(np.float32)
+
+
+def synthetic_bigvgan_tensors(seed: int = 20240607, stddev: float = 0.02,
+                              gain: float = 0.6) -> dict[str, np.ndarray]:
+    """Vocoder weights: weight_v and biases N(0, stddev) f16 from seed + (index in
+    sorted-name order); weight_g = gain * (1 + N(0, stddev)) for the resblock convs
+    (the per-row norm of the normalised weight, so the stack neither explodes nor
+    vanishes), 1 + N(0, stddev) for conv_pre and the upsamplers, 0.1 (1 + N(0,
+    stddev)) for conv_post; the filters are
+    the closed-form Kaiser-sinc filter (f32); SnakeBeta's log alpha and log beta are
+    N(0, 0.1) (f32)."""
+    filt = kaiser_sinc_filter()
+    out = {}
+    for i, (name, shape) in enumerate(bigvgan_specs()):
+        n = int(np.prod(shape))
+        if name.endswith(".filter"):
+            out[name] = filt.reshape(shape).copy()
+            continue
+        if name.endswith((".act.alpha", ".act.beta")):
+            out[name] = normal_noise(1, n, seed + i, 0.1).reshape(shape)
+            continue
+        v = normal_noise(1, n, seed + i, stddev).reshape(shape)
+        if name.endswith(".weight_g"):
+            g = 1.0 if name.startswith(("bigvgan.conv_pre", "bigvgan.ups")) else gain
+            if name.startswith("bigvgan.conv_post"):
+                g = 0.1  # keeps the waveform mostly inside the final clamp
+            v = g * (1.0 + v)
+        out[name] = v.astype(np.float16)
+    return out
+
+
 def write_synthetic_bundle(path: str | os.PathLike, seed: int = 20240605, stddev: float = 0.02) -> None:
     _check(lib().mit2cfm_write_synthetic_bundle(str(path).encode(), seed, stddev))
 

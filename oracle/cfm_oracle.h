@@ -54,6 +54,16 @@ void orc_reflect_pad(const float* x, uint32_t tokens, uint32_t channels,
 void orc_conv1d_reflect_same(const float* x, const float* w, const float* b,
                              uint32_t tokens, uint32_t in_ch, uint32_t out_ch,
                              uint32_t kernel, float* out);         /* tokenizer_tests.cpp:3866 */
+/* ---- BigVGAN vocoder primitives (bigvgan_oracle.c) ----------------------- */
+void orc_conv1d_dilated_same(const float* x, const float* w, const float* b, uint32_t tokens,
+                             uint32_t in_ch, uint32_t out_ch, uint32_t kernel, uint32_t dilation,
+                             float* out);                          /* tokenizer_tests.cpp:3739 */
+void orc_conv_transpose1d(const float* x, const float* w, const float* b, uint32_t tokens,
+                          uint32_t in_ch, uint32_t out_ch, uint32_t kernel, uint32_t stride,
+                          uint32_t padding, float* out);           /* tokenizer_tests.cpp:3760 */
+void orc_bigvgan_activation(const float* x, const float* up_filter, const float* down_filter,
+                            const float* alpha_log, const float* beta_log, uint32_t tokens,
+                            uint32_t channels, float* out);        /* tokenizer_tests.cpp:3811 */
 /* ---- condition producer: the s2mel length regulator (gpt.cpp:5271-5340) -- */
 void orc_nearest_interpolate(const float* x, uint32_t in_tokens, uint32_t out_tokens,
                              uint32_t width, float* out);          /* tokenizer_tests.cpp:3127 */

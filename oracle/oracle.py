@@ -53,6 +53,9 @@ def lib() -> ctypes.CDLL:
                                             ctypes.POINTER(_f32p), ctypes.POINTER(_f32p),
                                             ctypes.POINTER(_f32p), _f32p, _f32p, _f32p]),
             "orc_conv1d_reflect_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, _f32p]),
+            "orc_conv1d_dilated_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, u32, _f32p]),
+            "orc_conv_transpose1d": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, u32, u32, _f32p]),
+            "orc_bigvgan_activation": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, u32, u32, _f32p]),
             "orc_timestep_embedding": (None, [_f32p, u32, _f32p, u32, f32, _f32p]),
             "orc_attention_head_masked": (None, [_f32p, _f32p, _f32p, _u32p, u32, u32, _f32p]),
             "orc_rope_inplace": (None, [_f32p, u32, u32, u32]),
@@ -400,3 +403,127 @@ def rel_l2(got, ref) -> float:
     g = np.asarray(got, np.float64).reshape(-1)
     r = np.asarray(ref, np.float64).reshape(-1)
     return float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
+
+
+# ---------------------------------------------------------------- BigVGAN vocoder
+def conv1d_dilated_same(x, w, b, kernel, dilation) -> np.ndarray:
+    """cpu_conv1d_dilated_same (tokenizer_tests.cpp:3739): x [tokens, in], w [out, in, kernel]."""
+    x, w, b = f32(x), f32(w), f32(b)
+    tokens, cin = x.shape
+    out = np.empty((tokens, b.size), np.float32)
+    lib().orc_conv1d_dilated_same(P(x), P(w), P(b), tokens, cin, b.size, kernel, dilation, P(out))
+    return out
+
+
+def conv_transpose1d(x, w, b, kernel, stride, padding) -> np.ndarray:
+    """cpu_conv_transpose1d (tokenizer_tests.cpp:3760): x [tokens, in], w [in, out, kernel]."""
+    x, w, b = f32(x), f32(w), f32(b)
+    tokens, cin = x.shape
+    out_tokens = (tokens - 1) * stride + kernel - 2 * padding
+    out = np.empty((out_tokens, b.size), np.float32)
+    lib().orc_conv_transpose1d(P(x), P(w), P(b), tokens, cin, b.size, kernel, stride, padding, P(out))
+    return out
+
+
+def bigvgan_activation(x, up_filter, down_filter, alpha_log, beta_log) -> np.ndarray:
+    """cpu_bigvgan_activation (tokenizer_tests.cpp:3811): anti-aliased SnakeBeta, x [tokens, C]."""
+    x, up, down, a, bt = f32(x), f32(up_filter), f32(down_filter), f32(alpha_log), f32(beta_log)
+    tokens, channels = x.shape
+    out = np.empty_like(x)
+    lib().orc_bigvgan_activation(P(x), P(up), P(down), P(a), P(bt), tokens, channels, P(out))
+    return out
+
+
+# kBigVGANUpsamplers (dit_cfm_bigvgan.cpp:3681-3688): prefix, in, out, kernel, stride, padding.
+BIGVGAN_UPSAMPLERS = [("bigvgan.ups.0.0", 1536, 768, 8, 4, 2), ("bigvgan.ups.1.0", 768, 384, 8, 4, 2),
+                      ("bigvgan.ups.2.0", 384, 192, 4, 2, 1), ("bigvgan.ups.3.0", 192, 96, 4, 2, 1),
+                      ("bigvgan.ups.4.0", 96, 48, 4, 2, 1), ("bigvgan.ups.5.0", 48, 24, 4, 2, 1)]
+# kBigVGANResblocks (dit_cfm_bigvgan.cpp:3960-3979): prefix, channels, kernel.
+BIGVGAN_RESBLOCKS = [(f"bigvgan.resblocks.{3 * g + i}", 768 >> g, (3, 7, 11)[i])
+                     for g in range(6) for i in range(3)]
+BIGVGAN_DILATIONS = (1, 3, 5)
+
+
+class BigVGAN:
+    """The reference's fp32 CPU vocoder (dit_cfm_bigvgan.cpp:3606-4062) composed from the
+    oracle primitives; element-wise adds, the /3 average and the clamp are float32 numpy
+    operations in the reference's order.  tensors: the bigvgan.* weights (any float dtype)."""
+
+    def __init__(self, tensors: dict):
+        self.t = {k: f32(v) for k, v in tensors.items() if k.startswith("bigvgan.")}
+        self._wn = {}
+
+    def conv_weight(self, prefix, out_ch, in_ch, kernel):
+        """weight_norm_conv_weight (gpt.cpp:5126): rows = output channels."""
+        if prefix not in self._wn:
+            w = weight_norm(self.t[prefix + ".weight_g"].reshape(out_ch),
+                            self.t[prefix + ".weight_v"].reshape(out_ch, in_ch * kernel))
+            self._wn[prefix] = w.reshape(out_ch, in_ch, kernel)
+        return self._wn[prefix]
+
+    def conv_transpose_weight(self, prefix, in_ch, out_ch, kernel):
+        """weight_norm_conv_transpose_weight (gpt.cpp:5132): rows = input channels."""
+        if prefix not in self._wn:
+            w = weight_norm(self.t[prefix + ".weight_g"].reshape(in_ch),
+                            self.t[prefix + ".weight_v"].reshape(in_ch, out_ch * kernel))
+            self._wn[prefix] = w.reshape(in_ch, out_ch, kernel)
+        return self._wn[prefix]
+
+    def conv_pre(self, mel):
+        """run_bigvgan_conv_pre_cpu (:3606): conv k=7 zero-padded, 80 -> 1536."""
+        return conv1d_same(mel, self.conv_weight("bigvgan.conv_pre", 1536, 80, 7),
+                           self.t["bigvgan.conv_pre.bias"], 7)
+
+    def upsample(self, x, i):
+        """run_bigvgan_upsample_cpu (:3690)."""
+        prefix, cin, cout, k, stride, pad = BIGVGAN_UPSAMPLERS[i]
+        return conv_transpose1d(x, self.conv_transpose_weight(prefix, cin, cout, k),
+                                self.t[prefix + ".bias"], k, stride, pad)
+
+    def activation(self, prefix, x):
+        """run_bigvgan_activation_cpu (:3810)."""
+        t = self.t
+        return bigvgan_activation(x, t[prefix + ".upsample.filter"].reshape(-1),
+                                  t[prefix + ".downsample.lowpass.filter"].reshape(-1),
+                                  t[prefix + ".act.alpha"], t[prefix + ".act.beta"])
+
+    def resblock_pair(self, prefix, x, pair, kernel, dilation):
+        """run_bigvgan_resblock_pair_cpu (:3885): act, dilated conv, act, conv, + x."""
+        c = x.shape[1]
+        xt = self.activation(f"{prefix}.activations.{2 * pair}", x)
+        xt = conv1d_dilated_same(xt, self.conv_weight(f"{prefix}.convs1.{pair}", c, c, kernel),
+                                 self.t[f"{prefix}.convs1.{pair}.bias"], kernel, dilation)
+        xt = self.activation(f"{prefix}.activations.{2 * pair + 1}", xt)
+        xt = conv1d_dilated_same(xt, self.conv_weight(f"{prefix}.convs2.{pair}", c, c, kernel),
+                                 self.t[f"{prefix}.convs2.{pair}.bias"], kernel, 1)
+        return xt + f32(x)
+
+    def resblock(self, prefix, x, kernel):
+        """run_bigvgan_resblock_cpu (:3939): dilations 1, 3, 5."""
+        for i, d in enumerate(BIGVGAN_DILATIONS):
+            x = self.resblock_pair(prefix, x, i, kernel, d)
+        return x
+
+    def resblock_group(self, x, group):
+        """run_bigvgan_resblock_group_cpu (:3982): out += rb / 3 over the three kernels."""
+        out = np.zeros_like(f32(x))
+        for prefix, _, kernel in BIGVGAN_RESBLOCKS[3 * group:3 * group + 3]:
+            out += self.resblock(prefix, x, kernel) / np.float32(3.0)
+        return out
+
+    def body(self, mel):
+        """run_bigvgan_body_cpu (:4008): conv_pre, then 6 x (upsampler, resblock group)."""
+        x = self.conv_pre(mel)
+        for i in range(6):
+            x = self.resblock_group(self.upsample(x, i), i)
+        return x
+
+    def post(self, x):
+        """run_bigvgan_post_cpu (:4030): activation_post, conv k=7 24 -> 1 (zero bias), clamp."""
+        x = self.activation("bigvgan.activation_post", x)
+        x = conv1d_same(x, self.conv_weight("bigvgan.conv_post", 1, 24, 7), np.zeros(1, np.float32), 7)
+        return np.clip(x, np.float32(-1.0), np.float32(1.0))
+
+    def vocoder(self, mel):
+        """run_bigvgan_vocoder_cpu (:4058): mel [tokens, 80] -> waveform [256 * tokens]."""
+        return self.post(self.body(mel)).reshape(-1)
