@@ -25,6 +25,13 @@ Prints ONE JSON line.  Extra fields:
                 per call from HIP events on the library stream, its
                 algorithmic TFLOP/s, and the oracle's time for one call on
                 the host cores.
+  vocoder       the step after the decode, on the GPU: the BigVGAN vocoder on
+                this decode's mel (T frames -> 256 T samples,
+                mit2cfm_bigvgan_device) with synthetic weights (seed
+                20240607); time per call from HIP events on the library
+                stream, output samples/s, algorithmic conv TFLOP/s, and the
+                oracle on the host cores over a bounded sample (two mel
+                frames).
 """
 from __future__ import annotations
 
@@ -63,6 +70,7 @@ def parse():
     p.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, available cores)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cond-calls", type=int, default=50, help="timed condition-producer calls")
+    p.add_argument("--voc-calls", type=int, default=10, help="timed vocoder calls (0 = skip)")
     p.add_argument("--calib-mib", type=int, default=256,
                    help="size of the counter-calibration copy (0 = skip)")
     return p.parse_args()
@@ -143,6 +151,19 @@ def condition_cpu_baseline(lr_tensors, s_infer, gen, threads):
             "sample": f"one length-regulator call ({s_infer.shape[0]} codes -> {gen} frames)"}
 
 
+def vocoder_cpu_baseline(bv_tensors, mel, threads):
+    from oracle import oracle
+
+    oracle.set_threads(threads)
+    bv = oracle.BigVGAN(bv_tensors)
+    frames = 2
+    t0 = time.perf_counter()
+    bv.vocoder(mel[:frames])
+    s = time.perf_counter() - t0
+    return {"value": round(256 * frames / s, 1), "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": f"the vocoder on the first {frames} mel frames ({256 * frames} samples)"}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -158,7 +179,8 @@ def main():
     dev = torch.device("cuda:0")
     tensors = mit2cfm.synthetic_tensors(20240605, 0.02)
     lr_tensors = mit2cfm.synthetic_lr_tensors(20240606, 0.02)
-    ctx = mit2cfm.Context({**tensors, **lr_tensors}, device=0)
+    bv_tensors = mit2cfm.synthetic_bigvgan_tensors(20240607) if a.voc_calls else {}
+    ctx = mit2cfm.Context({**tensors, **lr_tensors, **bv_tensors}, device=0)
 
     x0 = mit2cfm.normal_noise(T, 80, 1)
     cond = mit2cfm.normal_noise(T, 512, 2)
@@ -271,6 +293,32 @@ def main():
         if not a.no_cpu_baseline:
             cp["cpu_baseline"] = condition_cpu_baseline(lr_tensors, s_infer, gen, cpu_threads(a))
 
+    # Vocoder (the step after the decode) on this decode's mel.
+    voc = None
+    if a.voc_calls:
+        d_wav = torch.empty(256 * T, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            ctx.bigvgan_device(d_out.data_ptr(), T, d_wav.data_ptr())
+        ctx.synchronize()
+        v0 = torch.cuda.Event(enable_timing=True)
+        v1 = torch.cuda.Event(enable_timing=True)
+        v0.record(stream)
+        for _ in range(a.voc_calls):
+            ctx.bigvgan_device(d_out.data_ptr(), T, d_wav.data_ptr())
+        v1.record(stream)
+        ctx.synchronize()
+        torch.cuda.synchronize()
+        v_ms = v0.elapsed_time(v1) / a.voc_calls
+        vflops = mit2cfm.bigvgan_flops(T)
+        voc = {"workload": f"BigVGAN v2 256x, {T} mel frames -> {256 * T} samples",
+               "ms_per_call": round(v_ms, 3), "samples_per_s": round(256 * T / (v_ms / 1e3), 1),
+               "algorithmic_tflop": round(vflops / 1e12, 4),
+               "tflops": round(vflops / (v_ms / 1e3) / 1e12, 1),
+               "mfma_util": round(vflops / (v_ms / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4)}
+        if not a.no_cpu_baseline:
+            voc["cpu_baseline"] = vocoder_cpu_baseline(bv_tensors, d_out.cpu().numpy(), cpu_threads(a))
+
     # Host-pointer decode (PCIe-inclusive; reported, never the headline value).
     ctx.decode(x0, prompt, cond, style, S, cfg)
     t1 = time.perf_counter()
@@ -306,6 +354,8 @@ def main():
     }
     if cp:
         result["condition_producer"] = cp
+    if voc:
+        result["vocoder"] = voc
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(tensors, T, P, S, cfg, cpu_threads(a))
     print(json.dumps(result), flush=True)

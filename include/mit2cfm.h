@@ -254,6 +254,37 @@ uint32_t mit2cfm_generated_frames(uint32_t codes);
 mit2cfm_status mit2cfm_noise_device(mit2cfm_ctx* ctx, uint32_t tokens, uint32_t channels,
                                     uint64_t seed, float temperature, float* out, uint32_t flags);
 
+/* ---- BigVGAN vocoder (the consumer of the mel) ----------------------------
+ * These need the vocoder's 783 "bigvgan.*" tensors (weight-normed convs as
+ * weight_g / weight_v / bias, the activations' filters and SnakeBeta
+ * alpha / beta) in the context's weight table; without them they return
+ * MIT2CFM_E_MODEL. */
+
+/* Replaces run_bigvgan_vocoder_metal (runtime/impl/dit_cfm_bigvgan.cpp:4196;
+ * CPU definition run_bigvgan_vocoder_cpu :4058): mel [tokens][80] ->
+ * wav [256 * tokens], clamped to [-1, 1].  Host pointers, synchronous. */
+mit2cfm_status mit2cfm_bigvgan(mit2cfm_ctx* ctx, const float* mel, uint32_t tokens, float* wav);
+/* The same on DEVICE pointers, enqueued on the context's stream (flags as for
+ * mit2cfm_decode_device), so the decode's mel can feed it directly. */
+mit2cfm_status mit2cfm_bigvgan_device(mit2cfm_ctx* ctx, const float* mel, uint32_t tokens, float* wav,
+                                      uint32_t flags);
+/* One vocoder stage on host pointers, as the reference's stage tests run them
+ * (dit_cfm_bigvgan.cpp:3627-4469):
+ *   stage 0 conv_pre (run_bigvgan_conv_pre, :3606)      [T][80]   -> [T][1536]
+ *   stage 1 upsampler `index` 0..5 (:3690)              [T][Cin]  -> [s T][Cout]
+ *   stage 2 activation `index` = 6 j + a for resblock j's activation a, 108
+ *           for activation_post (:3810)                 [T][C]    -> [T][C]
+ *   stage 3 resblock `index` 0..17 (:3939)              [T][C]    -> [T][C]
+ *   stage 4 resblock group `index` 0..5 (:3982)         [T][C]    -> [T][C]
+ *   stage 5 post: activation_post, conv_post, clamp (:4030) [T][24] -> [T]
+ *   stage 6 body: conv_pre, 6 x (upsampler, group) (:4008) [T][80] -> [256 T][24]
+ * out_capacity is the size of out in floats. */
+mit2cfm_status mit2cfm_bigvgan_stage(mit2cfm_ctx* ctx, int32_t stage, int32_t index, const float* in,
+                                     uint32_t tokens, float* out, uint64_t out_capacity);
+/* Floats of a stage's input (output = 0) or output (output = 1) for `tokens`
+ * input rows; 0 for an unknown stage or index. */
+uint64_t mit2cfm_bigvgan_stage_floats(int32_t stage, int32_t index, uint32_t tokens, int32_t output);
+
 #ifdef __cplusplus
 }
 #endif

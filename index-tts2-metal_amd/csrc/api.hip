@@ -11,6 +11,7 @@
 #include "../runtime/bundle.h"
 #include "../runtime/synth.h"
 #include "engine.h"
+#include "vocoder.h"
 
 struct mit2cfm_ctx {
   std::unique_ptr<mit2hip::Engine> eng;
@@ -159,7 +160,7 @@ mit2cfm_status mit2cfm_create_from_bundle(const char* bundle_path, int32_t devic
   std::vector<mit2hip::HostTensor> ts;
   for (const auto& info : b->tensors()) {
     if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0 &&
-        info.name.rfind("s2mel.net.length_regulator.", 0) != 0)
+        info.name.rfind("s2mel.net.length_regulator.", 0) != 0 && info.name.rfind("bigvgan.", 0) != 0)
       continue;
     int dt;
     if (info.dtype == "f32")
@@ -504,5 +505,45 @@ mit2cfm_status mit2cfm_noise_device(mit2cfm_ctx* ctx, uint32_t tokens, uint32_t 
     require(tokens > 0 && channels > 0, "noise shape must be non-empty");
     ctx->eng->normal_noise_device((size_t)tokens * channels, seed, temperature, out);
     if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}
+
+// ---- BigVGAN vocoder ------------------------------------------------------
+mit2cfm_status mit2cfm_bigvgan(mit2cfm_ctx* ctx, const float* mel, uint32_t tokens, float* wav) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(mel && wav, "mel and wav must not be NULL");
+    require(tokens > 0 && tokens <= (1u << 20), "tokens must be in [1, 2^20]");
+    ctx->eng->vocode_host(mel, (int)tokens, wav);
+  });
+}
+
+mit2cfm_status mit2cfm_bigvgan_device(mit2cfm_ctx* ctx, const float* mel, uint32_t tokens, float* wav,
+                                      uint32_t flags) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(mel && wav, "mel and wav must not be NULL");
+    require(tokens > 0 && tokens <= (1u << 20), "tokens must be in [1, 2^20]");
+    ctx->eng->vocode_device(mel, (int)tokens, wav);
+    if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}
+
+uint64_t mit2cfm_bigvgan_stage_floats(int32_t stage, int32_t index, uint32_t tokens, int32_t output) {
+  if (tokens == 0 || tokens > (1u << 20)) return 0;
+  return output ? mit2hip::Vocoder::stage_out_floats(stage, index, (int)tokens)
+                : mit2hip::Vocoder::stage_in_floats(stage, index, (int)tokens);
+}
+
+mit2cfm_status mit2cfm_bigvgan_stage(mit2cfm_ctx* ctx, int32_t stage, int32_t index, const float* in,
+                                     uint32_t tokens, float* out, uint64_t out_capacity) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(in && out, "in and out must not be NULL");
+    require(tokens > 0 && tokens <= (1u << 20), "tokens must be in [1, 2^20]");
+    const uint64_t n = mit2cfm_bigvgan_stage_floats(stage, index, tokens, 1);
+    require(n > 0, "unknown vocoder stage or index");
+    require(out_capacity >= n, "out is smaller than the stage output");
+    ctx->eng->vocoder_stage_host(stage, index, in, (int)tokens, out);
   });
 }

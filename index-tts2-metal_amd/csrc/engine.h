@@ -48,6 +48,7 @@ class Arena {
 
 struct Weights;    // resident weights (engine.hip)
 struct Workspace;  // activations (engine.hip)
+class Vocoder;     // BigVGAN (vocoder.hip)
 
 // Device buffers of the timestep-conditioning tables for S step slots:
 // t values, their embeddings and MLP intermediates, the per-step table rows
@@ -139,6 +140,17 @@ class Engine {
   // Frames the condition producer makes from `codes` semantic tokens.
   static int generated_frames(int codes);
 
+  // ---- BigVGAN vocoder (the consumer of the mel), present when the tensor
+  // table holds the "bigvgan.*" weights.
+  bool has_vocoder() const { return voc_ != nullptr; }
+  // mel [tokens][80] -> wav [256 tokens], DEVICE pointers, on stream().
+  void vocode_device(const float* mel, int tokens, float* wav);
+  // Host-pointer version (synchronous).
+  void vocode_host(const float* mel, int tokens, float* wav);
+  // One vocoder stage on host pointers (stage ids in vocoder.h); returns the
+  // output floats written.
+  size_t vocoder_stage_host(int stage, int index, const float* in, int tokens, float* out);
+
   // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
   void set_use_graph(bool on) { use_graph_ = on; }
   void sync();
@@ -163,6 +175,9 @@ class Engine {
   bool use_graph_ = true;
   std::unique_ptr<Weights> w_;
   std::unique_ptr<Workspace> ws_;
+  std::unique_ptr<Vocoder> voc_;
+  float* voc_io_ = nullptr;  // host-path staging: mel, then wav
+  size_t voc_io_floats_ = 0;
   // Length-regulator buffers, grown on demand (separate from the decode's
   // workspace so a condition call never invalidates captured decode graphs).
   struct LrBufs {

@@ -25,6 +25,7 @@
 #include "condition.h"
 #include "gemm.h"
 #include "rowops.h"
+#include "vocoder.h"
 
 namespace mit2hip {
 
@@ -482,17 +483,22 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
     }
   }
 
+  if (Vocoder::present(hm.t)) voc_ = std::make_unique<Vocoder>(hm.t, stream_);
   ws_ = std::make_unique<Workspace>();
 }
 
 Engine::~Engine() {
   clear_graphs();
+  if (voc_io_) (void)hipFree(voc_io_);
+  voc_.reset();
   ws_.reset();
   w_.reset();
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
-size_t Engine::weight_bytes() const { return w_->arena.used(); }
+size_t Engine::weight_bytes() const {
+  return w_->arena.used() + (voc_ ? voc_->weight_bytes() : 0);
+}
 
 void Engine::clear_graphs() {
   for (auto& kv : graphs_) {
@@ -1437,6 +1443,46 @@ void Engine::normal_noise_device(size_t n, uint64_t seed, float temperature, flo
   if (n == 0) throw std::invalid_argument("noise: empty shape");
   HIP_OK(hipSetDevice(device_));
   HIP_OK(launch_normal_noise(n, seed, temperature, out, stream_));
+}
+
+}  // namespace mit2hip
+
+// ------------------------------------------------------------------ vocoder
+namespace mit2hip {
+
+static Vocoder& need_vocoder(const std::unique_ptr<Vocoder>& v) {
+  if (!v) throw std::runtime_error("vocoder: the context has no bigvgan.* tensors");
+  return *v;
+}
+
+void Engine::vocode_device(const float* mel, int tokens, float* wav) {
+  HIP_OK(hipSetDevice(device_));
+  need_vocoder(voc_).vocode_device(mel, tokens, wav);
+}
+
+void Engine::vocode_host(const float* mel, int tokens, float* wav) {
+  HIP_OK(hipSetDevice(device_));
+  Vocoder& v = need_vocoder(voc_);
+  if (tokens <= 0) throw std::invalid_argument("vocoder: tokens must be positive");
+  const size_t need = (size_t)tokens * (80 + 256);
+  if (need > voc_io_floats_) {
+    HIP_OK(hipStreamSynchronize(stream_));
+    if (voc_io_) HIP_OK(hipFree(voc_io_));
+    voc_io_ = nullptr;
+    HIP_OK(hipMalloc(&voc_io_, need * sizeof(float)));
+    voc_io_floats_ = need;
+  }
+  float* dmel = voc_io_;
+  float* dwav = voc_io_ + (size_t)tokens * 80;
+  HIP_OK(hipMemcpyAsync(dmel, mel, (size_t)tokens * 80 * sizeof(float), hipMemcpyHostToDevice, stream_));
+  v.vocode_device(dmel, tokens, dwav);
+  HIP_OK(hipMemcpyAsync(wav, dwav, (size_t)tokens * 256 * sizeof(float), hipMemcpyDeviceToHost, stream_));
+  HIP_OK(hipStreamSynchronize(stream_));
+}
+
+size_t Engine::vocoder_stage_host(int stage, int index, const float* in, int tokens, float* out) {
+  HIP_OK(hipSetDevice(device_));
+  return need_vocoder(voc_).stage_host(stage, index, in, tokens, out);
 }
 
 }  // namespace mit2hip

@@ -20,6 +20,9 @@ enum AMode : int {
   A_CONV5 = 2,   // k = tap*kConvC + c: A[(b*T + reflect(t + tap - 2))*lda + c], m = b*T + t
   A_CONV3Z = 3,  // k = tap*kConvC + c: A[(b*T + t + tap - 1)*lda + c], zero outside [0, T):
                  // A holds M + 1 rows and row M is all zero (the padding taps read it)
+  A_CONVP = 4,   // any zero-padded conv, k = tap*conv_c + c (conv_c a multiple of 8, K padded
+                 // to the stage width): A[(b*T + t + tap*conv_d - conv_pad)*lda + c], zero
+                 // (read from A_zero) outside [0, T) and for tap >= conv_k
 };
 
 enum EpiMode : int {
@@ -32,6 +35,8 @@ enum EpiMode : int {
   EPI_RESSKIP = 5,    // WaveNet res/skip update (N = 2*512)
   EPI_FINALSKIP = 6,  // last WaveNet layer (N = 512), plus the res_projection add
   EPI_DUAL = 7,       // cols < N/2 -> C32 (+ f16 copy C16); cols >= N/2 -> C32b
+  EPI_RESAVG = 8,     // v = acc + bias + res; C32 = v (optional); g = (flag ? C32b : 0) + v / 3
+                      // -> C32b, and its f16 copy -> C16 (optional)
 };
 
 struct GemmArgs {
@@ -43,7 +48,13 @@ struct GemmArgs {
   int lda2 = 0;
   int K1 = 0;
   int T = 0;        // tokens per branch (A_CONV5, EPI_QKV)
-  int conv_c = 0;   // input channels per tap (A_CONV5)
+  int conv_c = 0;   // input channels per tap (A_CONV5, A_CONV3Z, A_CONVP)
+  int conv_k = 0;   // A_CONVP: taps, dilation, left zero padding, 1 / conv_c
+  int conv_d = 1;
+  int conv_pad = 0;
+  float conv_inv_c = 0.f;
+  int n_store = 0;  // if nonzero: only columns < n_store are stored (weights zero-padded to N)
+  const half_t* A_zero = nullptr;  // A_CONVP: >= conv_c zero halves, read by the padding taps
   // weights
   const half_t* W = nullptr;
   int ldw = 0;

@@ -143,7 +143,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
 
   // Epilogue operands that do not depend on the product are fetched now, so
   // their latency hides behind the K loop.
-  constexpr bool kPreA = EPI == EPI_F32 || EPI == EPI_RESSKIP || EPI == EPI_FINALSKIP;
+  constexpr bool kPreA =
+      EPI == EPI_F32 || EPI == EPI_RESSKIP || EPI == EPI_FINALSKIP || EPI == EPI_RESAVG;
   constexpr bool kPreB = EPI == EPI_FINALSKIP;
   float4 pre_a[kPreA ? MI : 1][kPreA ? NI : 1];
   float4 pre_b[kPreB ? MI : 1][kPreB ? NI : 1];
@@ -155,8 +156,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       for (int j = 0; j < NI; ++j) {
         const int n = col_base + 16 * j;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m < p.M && kg == 0) {
-          if constexpr (EPI == EPI_F32) {
+        if (m < p.M && kg == 0 && (p.n_store == 0 || n < p.n_store)) {
+          if constexpr (EPI == EPI_F32 || EPI == EPI_RESAVG) {
             if (p.res) v = *reinterpret_cast<const float4*>(p.res + (size_t)m * p.ldres + n);
           } else if constexpr (EPI == EPI_RESSKIP) {
             if (n < 512) v = *reinterpret_cast<const float4*>(p.C32 + (size_t)m * p.ldc32 + n);
@@ -235,6 +236,21 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     }
   }
 
+  // A_CONVP: the token (and sequence start) of each load slot's row, fixed
+  // for the kernel; the tap and channel of a 16-byte chunk follow from its K
+  // position, so one loader covers every kernel size, dilation and width.
+  int cp_t[AM == A_CONVP ? LA : 1], cp_base[AM == A_CONVP ? LA : 1];
+  if constexpr (AM == A_CONVP) {
+#pragma unroll
+    for (int j = 0; j < LA; ++j) {
+      const int row = ((wave * LA + j) * 64 + lane) / CPR;
+      const int m = min(m0 + row, p.M - 1);
+      const int b = m / p.T;
+      cp_base[j] = b * p.T;
+      cp_t[j] = m - b * p.T;
+    }
+  }
+
   auto a_src = [&](int j, int m, int k0, int kc) -> const half_t* {
     const int k = k0 + kc;
     if constexpr (AM == A_PLAIN) {
@@ -246,11 +262,25 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       const ConvRows& cr = conv_rows[j];
       const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : tap == 2 ? cr.r2 : tap == 3 ? cr.r3 : cr.r4;
       return p.A + ro + (k - tap * kConvC);
-    } else {
+    } else if constexpr (AM == A_CONV3Z) {
       const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);
       const ConvRows& cr = conv_rows[j];
       const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : cr.r2;
       return p.A + ro + (k - tap * kConvC);
+    } else {
+      // tap = k / conv_c through a float reciprocal, corrected by one either way
+      int tap = (int)((float)k * p.conv_inv_c);
+      int c = k - tap * p.conv_c;
+      if (c < 0) {
+        --tap;
+        c += p.conv_c;
+      } else if (c >= p.conv_c) {
+        ++tap;
+        c -= p.conv_c;
+      }
+      const int src = cp_t[j] + tap * p.conv_d - p.conv_pad;
+      const bool ok = tap < p.conv_k && src >= 0 && src < p.T;
+      return ok ? p.A + (size_t)(cp_base[j] + src) * p.lda + c : p.A_zero + c;
     }
   };
 
@@ -399,7 +429,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   };
 
   if constexpr (EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_DUAL || EPI == EPI_RESSKIP ||
-                EPI == EPI_FINALSKIP) {
+                EPI == EPI_FINALSKIP || EPI == EPI_RESAVG) {
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int m = row_base + 16 * i;
@@ -413,6 +443,20 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
         const int n = col_base + 16 * j;
         float4 v = make_float4(acc[i][j][0] + bv[j].x, acc[i][j][1] + bv[j].y,
                                acc[i][j][2] + bv[j].z, acc[i][j][3] + bv[j].w);
+        if constexpr (EPI == EPI_RESAVG) {
+          if (!live || (p.n_store && n >= p.n_store)) continue;
+          const float4 r = pre_a[i][j];
+          v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+          if (p.C32) *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
+          float4* g = reinterpret_cast<float4*>(p.C32b + (size_t)m * p.ldc32b + n);
+          const float4 g0 = p.flag ? *g : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 g1 = make_float4(g0.x + v.x / 3.0f, g0.y + v.y / 3.0f, g0.z + v.z / 3.0f,
+                                        g0.w + v.w / 3.0f);
+          *g = g1;
+          if (p.C16) st16(p.C16 + (size_t)m * p.ldc16 + n, g1.x, g1.y, g1.z, g1.w);
+          continue;
+        }
+        if (p.n_store && n >= p.n_store) continue;  // zero-padded weight rows
         if constexpr (EPI == EPI_F32) {
           if (p.res) {
             const float4 r = pre_a[i][j];
@@ -635,8 +679,8 @@ static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
 template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2, int KG = 1>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
   if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K groups need equal stage counts
-  const TileMap tm = make_tile_map(a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z ? a.conv_c : a.K,
-                                   BM, BN);
+  const TileMap tm = make_tile_map(
+      a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z || AM == A_CONVP ? a.conv_c : a.K, BM, BN);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG>), dim3(8 * tm.per_xcd),
                      dim3(64 * WM * WN * KG), 0, s,
                      a, tm);
@@ -661,6 +705,14 @@ static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
 // does not depend on the batch it is decoded with.
 template <int AM, int EPI>
 static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
+  if constexpr (AM == A_CONVP) {
+    // The vocoder's convs: M is long (thousands to hundreds of thousands of
+    // samples), N is the channel count (zero-padded to the tile width).
+    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
+    if (a.N % 64 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2>(a, s);
+    if (a.N % 32 == 0) return launch_tile<64, 32, 64, 3, AM, EPI, 4, 1>(a, s);
+    return hipErrorInvalidValue;
+  }
   if constexpr (EPI == EPI_SWIGLU) {
     if (a.N % 192 == 0) return launch_tile<128, 192, 64, 3, AM, EPI, 4, 2>(a, s);
   }
@@ -679,6 +731,19 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t stream) {
+  if (amode == A_CONVP) {
+    if (a.M <= 0 || a.N <= 0 || a.N % 32 != 0 || a.K <= 0 || a.K % 64 != 0 || !a.A || !a.W ||
+        a.T <= 0 || a.M % a.T != 0 || a.conv_c <= 0 || a.conv_c % 8 != 0 || a.lda < a.conv_c ||
+        a.conv_k <= 0 || a.conv_d <= 0 || a.conv_pad < 0 || a.K < a.conv_k * a.conv_c ||
+        a.conv_inv_c != 1.0f / (float)a.conv_c || !a.A_zero || a.n_store < 0 || a.n_store > a.N ||
+        a.n_store % 4 != 0)
+      return hipErrorInvalidValue;
+    if (epi == EPI_F32) return launch_am_epi<A_CONVP, EPI_F32>(a, stream);
+    if (epi == EPI_F16) return launch_am_epi<A_CONVP, EPI_F16>(a, stream);
+    if (epi == EPI_RESAVG && a.C32b) return launch_am_epi<A_CONVP, EPI_RESAVG>(a, stream);
+    return hipErrorInvalidValue;
+  }
+  if (a.n_store != 0 || epi == EPI_RESAVG) return hipErrorInvalidValue;
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 128 != 0 || a.N % 64 != 0 || !a.A || !a.W)
     return hipErrorInvalidValue;
   if (amode == A_CONCAT && (a.K1 % 128 != 0 || a.K1 <= 0 || a.K1 >= a.K || !a.A2))

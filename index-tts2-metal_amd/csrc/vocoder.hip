@@ -1,0 +1,534 @@
+// vocoder.hip -- BigVGAN vocoder on gfx950 (see vocoder.h).
+//
+// Replaces run_bigvgan_vocoder_metal / _single_pass
+// (runtime/impl/dit_cfm_bigvgan.cpp:4102-4223) and its kernels
+// (kernels.metal:1607-1749: conv1d, transposed conv, anti-aliased activation,
+// add, avg3, clamp).
+//
+// Differences in HOW, not WHAT:
+//  * convs are implicit GEMMs on the matrix cores with f16 operands and fp32
+//    accumulation; weights are weight-normed once at create and laid out
+//    tap-major [out][tap * in + ic];
+//  * a transposed conv with stride s, kernel 2s and padding s/2 is a k = 3
+//    conv over the input (taps q-1, q, q+1) whose s * out output columns are
+//    the s phases of the upsampled signal: output row q, column r * out + oc
+//    is sample s q + r, so the GEMM writes the token-major upsampled tensor;
+//  * the residual add of each AMP pair and the /3 average of the three
+//    resblocks are fused into the second conv's epilogue (EPI_RESAVG), which
+//    also writes the f16 operand of the next upsampler;
+//  * the activation keeps the two-times-upsampled, snake'd signal of a tile in
+//    LDS, so each upsampled value is computed once.
+#include "vocoder.h"
+
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+#include "engine.h"
+#include "gemm.h"
+
+namespace mit2hip {
+
+#define VOC_OK(expr)                                                                      \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess)                                                                 \
+      throw HipError(std::string(#expr) + " failed: " + hipGetErrorString(e_) + " (" +   \
+                     __FILE__ + ":" + std::to_string(__LINE__) + ")");                    \
+  } while (0)
+
+namespace {
+
+// kBigVGANUpsamplers (dit_cfm_bigvgan.cpp:3681-3688) and kBigVGANResblocks
+// (:3960-3979).
+struct UpsSpec {
+  const char* prefix;
+  int cin, cout, kernel, stride, padding;
+};
+constexpr UpsSpec kUps[6] = {{"bigvgan.ups.0.0", 1536, 768, 8, 4, 2}, {"bigvgan.ups.1.0", 768, 384, 8, 4, 2},
+                             {"bigvgan.ups.2.0", 384, 192, 4, 2, 1},  {"bigvgan.ups.3.0", 192, 96, 4, 2, 1},
+                             {"bigvgan.ups.4.0", 96, 48, 4, 2, 1},    {"bigvgan.ups.5.0", 48, 24, 4, 2, 1}};
+constexpr int kRbKernel[3] = {3, 7, 11};
+constexpr int kDil[3] = {1, 3, 5};
+inline int rb_channels(int j) { return 768 >> (j / 3); }
+inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// ---------------------------------------------------------------- kernels
+// Anti-aliased SnakeBeta (cpu_bigvgan_activation, tokenizer_tests.cpp:3811):
+//   U(u) = 2 sum_{k: (u+15-k) even} x[clamp((u+15-k)/2 - 5)] up[k]
+//   Z(u) = U + sin(alpha U)^2 / (beta + 1e-9)
+//   out[t] = sum_k Z(clamp(2t + k - 5, 0, 2T-1)) down[k]
+// A workgroup owns TT tokens x CC channels.  Its x window (tokens t0-6 ..
+// t0+TT+5, clamped) and the Z values it needs (u = 2 t0 - 5 .. 2 t0 + 2 TT + 4,
+// clamped) live in LDS; every Z is computed once.
+constexpr int kActTT = 64;
+
+template <int CC, bool OUT16>
+__global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ upf,
+                                                       const float* __restrict__ dnf,
+                                                       const float* __restrict__ alpha,
+                                                       const float* __restrict__ inv_beta, int T,
+                                                       int C, void* __restrict__ out) {
+  constexpr int XR = kActTT + 12;      // x window rows
+  constexpr int ZR = 2 * kActTT + 10;  // Z window rows
+  __shared__ float xs[XR * CC];
+  __shared__ float zs[ZR * CC];
+  __shared__ float fu[12], fd[12];
+  const int t0 = blockIdx.x * kActTT;
+  const int c0 = blockIdx.y * CC;
+  const int tid = threadIdx.x;
+  if (tid < 12) fu[tid] = upf[tid];
+  else if (tid < 24) fd[tid - 12] = dnf[tid - 12];
+  for (int idx = tid; idx < XR * CC; idx += 256) {
+    const int i = idx / CC, c = idx - (idx / CC) * CC;
+    int src = t0 - 6 + i;
+    src = src < 0 ? 0 : (src >= T ? T - 1 : src);
+    xs[idx] = x[(size_t)src * C + c0 + c];
+  }
+  __syncthreads();
+  const int u_lo = 2 * t0 - 5;
+  for (int idx = tid; idx < ZR * CC; idx += 256) {
+    const int i = idx / CC, c = idx - (idx / CC) * CC;
+    int u = u_lo + i;
+    u = u < 0 ? 0 : (u >= 2 * T ? 2 * T - 1 : u);
+    const int full = u + 15;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+      if (((full - k) & 1) == 0) {
+        const int src = ((full - k) >> 1) - 5;  // within the window for every clamped u
+        acc += xs[(src - (t0 - 6)) * CC + c] * fu[k];
+      }
+    }
+    const float y = 2.0f * acc;
+    const float s = __sinf(y * alpha[c0 + c]);
+    zs[idx] = y + (s * s) * inv_beta[c0 + c];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kActTT * CC; idx += 256) {
+    const int tt = idx / CC, c = idx - (idx / CC) * CC;
+    const int t = t0 + tt;
+    if (t >= T) continue;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 12; ++k) acc += zs[(2 * tt + k) * CC + c] * fd[k];
+    if constexpr (OUT16)
+      static_cast<half_t*>(out)[(size_t)t * C + c0 + c] = (half_t)acc;
+    else
+      static_cast<float*>(out)[(size_t)t * C + c0 + c] = acc;
+  }
+}
+
+// conv_post (k = 7, 24 -> 1, zero bias) and the final clamp
+// (run_bigvgan_post_cpu, dit_cfm_bigvgan.cpp:4030-4039).
+__global__ __launch_bounds__(256) void conv_post_clamp_kernel(const float* __restrict__ a,
+                                                              const float* __restrict__ w, int T,
+                                                              float* __restrict__ wav) {
+  __shared__ float ws[24 * 7];
+  if (threadIdx.x < 24 * 7) ws[threadIdx.x] = w[threadIdx.x];
+  __syncthreads();
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= T) return;
+  float acc = 0.0f;
+  for (int ic = 0; ic < 24; ++ic) {
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+      const int src = t + k - 3;
+      if (src >= 0 && src < T) acc += a[(size_t)src * 24 + ic] * ws[ic * 7 + k];
+    }
+  }
+  wav[t] = fminf(1.0f, fmaxf(-1.0f, acc));
+}
+
+__global__ void voc_f32_to_f16_kernel(const float* __restrict__ in, half_t* __restrict__ out,
+                                      size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = (half_t)in[i];
+}
+
+const std::vector<float>& get(const std::unordered_map<std::string, std::vector<float>>& t,
+                              const std::string& name, size_t elems) {
+  auto it = t.find(name);
+  if (it == t.end()) throw std::invalid_argument("missing tensor: " + name);
+  if (it->second.size() != elems)
+    throw std::invalid_argument("tensor " + name + " has " + std::to_string(it->second.size()) +
+                                " elements, expected " + std::to_string(elems));
+  return it->second;
+}
+
+// weight_norm_rowmajor (gpt.cpp:5109): w = g * v / ||v|| per row.
+std::vector<float> wnorm(const std::vector<float>& g, const std::vector<float>& v, size_t rows,
+                         size_t cols) {
+  std::vector<float> w(rows * cols);
+  for (size_t r = 0; r < rows; ++r) {
+    float n = 0.f;
+    for (size_t c = 0; c < cols; ++c) n += v[r * cols + c] * v[r * cols + c];
+    n = std::sqrt(n);
+    const float s = g[r] / n;
+    for (size_t c = 0; c < cols; ++c) w[r * cols + c] = v[r * cols + c] * s;
+  }
+  return w;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- weights
+struct Vocoder::Conv {
+  half_t* w = nullptr;  // [N][K] f16, tap-major, zero-padded
+  float* b = nullptr;   // [N]
+  int N = 0, n_out = 0, K = 0, cin = 0, k = 0;
+};
+
+struct Vocoder::Act {
+  float* upf = nullptr;
+  float* dnf = nullptr;
+  float* alpha = nullptr;     // exp(alpha_log) [C]
+  float* inv_beta = nullptr;  // 1 / (exp(beta_log) + 1e-9) [C]
+  int C = 0;
+};
+
+struct Vocoder::Impl {
+  hipStream_t s;
+  Arena wa;
+  Conv pre, ups[6], rb[18][3][2];
+  Act act[18][6], act_post;
+  float* post_w = nullptr;   // [24 * 7]
+  half_t* zero = nullptr;    // 2048 zero halves: the padding taps of every conv
+  size_t bytes = 0;
+  // workspace, sized for cap mel tokens
+  Arena ws;
+  int cap = 0;
+  half_t *mel16, *pre16, *a16, *g16;
+  float *x32, *h32, *t32, *g32, *act32;
+
+  void upload_f16(half_t*& d, const std::vector<float>& v) {
+    std::vector<_Float16> h(v.size());
+    for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
+    d = static_cast<half_t*>(wa.take(h.size() * 2));
+    VOC_OK(hipMemcpy(d, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+  }
+  void upload_f32(float*& d, const std::vector<float>& v) {
+    d = static_cast<float*>(wa.take(v.size() * 4));
+    VOC_OK(hipMemcpy(d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+  }
+
+  // Zero-padded conv (weight_v [out][in][k], weight_g [out]).
+  void make_conv(Conv& c, const std::unordered_map<std::string, std::vector<float>>& t,
+                 const std::string& prefix, int cout, int cin, int k, bool bias) {
+    const auto w = wnorm(get(t, prefix + ".weight_g", cout), get(t, prefix + ".weight_v", (size_t)cout * cin * k),
+                         cout, (size_t)cin * k);
+    c.n_out = cout;
+    c.N = round_up(cout, 32);
+    c.K = round_up(k * cin, 64);
+    c.cin = cin;
+    c.k = k;
+    std::vector<float> wt((size_t)c.N * c.K, 0.f), bt(c.N, 0.f);
+    for (int oc = 0; oc < cout; ++oc)
+      for (int ic = 0; ic < cin; ++ic)
+        for (int tap = 0; tap < k; ++tap)
+          wt[(size_t)oc * c.K + tap * cin + ic] = w[((size_t)oc * cin + ic) * k + tap];
+    if (bias) {
+      const auto& b = get(t, prefix + ".bias", cout);
+      for (int oc = 0; oc < cout; ++oc) bt[oc] = b[oc];
+    }
+    upload_f16(c.w, wt);
+    upload_f32(c.b, bt);
+  }
+
+  // Transposed conv (weight_v [in][out][kernel], weight_g [in]) as a k = 3
+  // conv: output column r * cout + oc of row q is sample s q + r; input tap
+  // i = q - 1 + tap contributes w[ic][oc][kk] with kk = s (1 - tap) + r + p.
+  void make_ups(Conv& c, const std::unordered_map<std::string, std::vector<float>>& t, const UpsSpec& u) {
+    const int s = u.stride;
+    if (u.kernel != 2 * s || 2 * u.padding != s)
+      throw std::invalid_argument(std::string(u.prefix) + ": upsampler must have kernel 2s and padding s/2");
+    const auto w = wnorm(get(t, std::string(u.prefix) + ".weight_g", u.cin),
+                         get(t, std::string(u.prefix) + ".weight_v", (size_t)u.cin * u.cout * u.kernel), u.cin,
+                         (size_t)u.cout * u.kernel);
+    const auto& b = get(t, std::string(u.prefix) + ".bias", u.cout);
+    c.n_out = s * u.cout;
+    c.N = round_up(c.n_out, 32);
+    c.K = round_up(3 * u.cin, 64);
+    c.cin = u.cin;
+    c.k = 3;
+    std::vector<float> wt((size_t)c.N * c.K, 0.f), bt(c.N, 0.f);
+    for (int r = 0; r < s; ++r)
+      for (int oc = 0; oc < u.cout; ++oc) {
+        const int n = r * u.cout + oc;
+        bt[n] = b[oc];
+        for (int tap = 0; tap < 3; ++tap) {
+          const int kk = s * (1 - tap) + r + u.padding;
+          if (kk < 0 || kk >= u.kernel) continue;
+          for (int ic = 0; ic < u.cin; ++ic)
+            wt[(size_t)n * c.K + tap * u.cin + ic] = w[((size_t)ic * u.cout + oc) * u.kernel + kk];
+        }
+      }
+    upload_f16(c.w, wt);
+    upload_f32(c.b, bt);
+  }
+
+  void make_act(Act& a, const std::unordered_map<std::string, std::vector<float>>& t, const std::string& prefix,
+                int C) {
+    a.C = C;
+    upload_f32(a.upf, get(t, prefix + ".upsample.filter", 12));
+    upload_f32(a.dnf, get(t, prefix + ".downsample.lowpass.filter", 12));
+    const auto& al = get(t, prefix + ".act.alpha", C);
+    const auto& bl = get(t, prefix + ".act.beta", C);
+    std::vector<float> alpha(C), ib(C);
+    for (int c = 0; c < C; ++c) {
+      alpha[c] = std::exp(al[c]);
+      ib[c] = 1.0f / (std::exp(bl[c]) + 1e-9f);
+    }
+    upload_f32(a.alpha, alpha);
+    upload_f32(a.inv_beta, ib);
+  }
+
+  void ensure(int T) {
+    if (T <= cap) return;
+    const size_t big = (size_t)T * 6144;  // C * T_s of every stage from the second on
+    const size_t need = (size_t)T * 80 * 2 + (size_t)T * 1536 * 2 + 2 * big * 2 + 5 * big * 4 + 9 * 256;
+    VOC_OK(hipStreamSynchronize(s));
+    ws.reserve(need + 4096);
+    mel16 = static_cast<half_t*>(ws.take((size_t)T * 80 * 2));
+    pre16 = static_cast<half_t*>(ws.take((size_t)T * 1536 * 2));
+    a16 = static_cast<half_t*>(ws.take(big * 2));
+    g16 = static_cast<half_t*>(ws.take(big * 2));
+    x32 = static_cast<float*>(ws.take(big * 4));
+    h32 = static_cast<float*>(ws.take(big * 4));
+    t32 = static_cast<float*>(ws.take(big * 4));
+    g32 = static_cast<float*>(ws.take(big * 4));
+    act32 = static_cast<float*>(ws.take(big * 4));
+    cap = T;
+  }
+
+  // ---------------------------------------------------------- launches
+  void conv(const Conv& c, const half_t* A, int T, int d, int pad, int epi, float* C32, const float* res,
+            float* C32b, half_t* C16, int flag) {
+    GemmArgs g;
+    g.M = T;
+    g.N = c.N;
+    g.K = c.K;
+    g.A = A;
+    g.lda = c.cin;
+    g.T = T;
+    g.conv_c = c.cin;
+    g.conv_k = c.k;
+    g.conv_d = d;
+    g.conv_pad = pad;
+    g.conv_inv_c = 1.0f / (float)c.cin;
+    g.A_zero = zero;
+    g.W = c.w;
+    g.ldw = c.K;
+    g.bias = c.b;
+    g.n_store = c.N == c.n_out ? 0 : c.n_out;
+    g.C32 = C32;
+    g.ldc32 = c.n_out;
+    g.res = res;
+    g.ldres = c.n_out;
+    g.C32b = C32b;
+    g.ldc32b = c.n_out;
+    g.C16 = C16;
+    g.ldc16 = c.n_out;
+    g.flag = flag;
+    VOC_OK(launch_gemm(g, A_CONVP, (EpiMode)epi, s));
+  }
+
+  void activation(const Act& a, const float* in, int T, void* out, bool out16) {
+    const dim3 grid((T + kActTT - 1) / kActTT, 1);
+    auto go = [&](auto cc) {
+      constexpr int CC = decltype(cc)::value;
+      const dim3 gr(grid.x, a.C / CC);
+      if (out16)
+        hipLaunchKernelGGL((snake_aa_kernel<CC, true>), gr, dim3(256), 0, s, in, a.upf, a.dnf, a.alpha,
+                           a.inv_beta, T, a.C, out);
+      else
+        hipLaunchKernelGGL((snake_aa_kernel<CC, false>), gr, dim3(256), 0, s, in, a.upf, a.dnf, a.alpha,
+                           a.inv_beta, T, a.C, out);
+    };
+    if (a.C % 32 == 0) go(std::integral_constant<int, 32>{});
+    else if (a.C == 48) go(std::integral_constant<int, 48>{});
+    else if (a.C == 24) go(std::integral_constant<int, 24>{});
+    else throw std::invalid_argument("activation: unsupported channel count");
+    VOC_OK(hipGetLastError());
+  }
+
+  // One resblock j over x [T][C]: three (act, dilated conv, act, conv, + res)
+  // pairs.  The last pair folds into the group mean g (flag: add to g rather
+  // than start it) and, when given, writes the block output to out32 and the
+  // updated mean's f16 copy to g16o.
+  void resblock(int j, const float* x, int T, float* out32, float* g, int flag, half_t* g16o) {
+    const int k = kRbKernel[j % 3];
+    const float* h = x;
+    for (int pr = 0; pr < 3; ++pr) {
+      activation(act[j][2 * pr], h, T, a16, true);
+      const int d = kDil[pr];
+      conv(rb[j][pr][0], a16, T, d, (k - 1) * d / 2, EPI_F32, t32, nullptr, nullptr, nullptr, 0);
+      activation(act[j][2 * pr + 1], t32, T, a16, true);
+      if (pr < 2) {
+        conv(rb[j][pr][1], a16, T, 1, (k - 1) / 2, EPI_F32, h32, h, nullptr, nullptr, 0);
+        h = h32;
+      } else {
+        conv(rb[j][pr][1], a16, T, 1, (k - 1) / 2, EPI_RESAVG, out32, h, g, g16o, flag);
+      }
+    }
+  }
+
+  // Resblock group i over the upsampled x [T][C]: g = mean of the three
+  // resblocks; g16o receives its f16 copy (the next upsampler's operand).
+  void group(int i, const float* x, int T, float* g, half_t* g16o) {
+    for (int r = 0; r < 3; ++r) resblock(3 * i + r, x, T, nullptr, g, r > 0, r == 2 ? g16o : nullptr);
+  }
+
+  void to_f16(const float* in, half_t* out, size_t n) {
+    hipLaunchKernelGGL(voc_f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n);
+    VOC_OK(hipGetLastError());
+  }
+
+  void post(const float* x, int T, float* wav) {
+    activation(act_post, x, T, act32, false);
+    hipLaunchKernelGGL(conv_post_clamp_kernel, dim3((T + 255) / 256), dim3(256), 0, s, act32, post_w, T, wav);
+    VOC_OK(hipGetLastError());
+  }
+
+  // mel [T][80] (device) -> g32 [256 T][24] (the body's output).
+  void body(const float* mel, int T) {
+    to_f16(mel, mel16, (size_t)T * 80);
+    conv(pre, mel16, T, 1, 3, EPI_F16, nullptr, nullptr, nullptr, pre16, 0);
+    const half_t* cur = pre16;
+    int Ts = T;
+    for (int i = 0; i < 6; ++i) {
+      conv(ups[i], cur, Ts, 1, 1, EPI_F32, x32, nullptr, nullptr, nullptr, 0);
+      Ts *= kUps[i].stride;
+      group(i, x32, Ts, g32, g16);
+      cur = g16;
+    }
+  }
+};
+
+bool Vocoder::present(const std::unordered_map<std::string, std::vector<float>>& t) {
+  for (const auto& kv : t)
+    if (kv.first.compare(0, 8, "bigvgan.") == 0) return true;
+  return false;
+}
+
+Vocoder::Vocoder(const std::unordered_map<std::string, std::vector<float>>& t, hipStream_t stream)
+    : d_(new Impl) {
+  Impl& d = *d_;
+  d.s = stream;
+  d.wa.reserve(size_t(300) << 20);
+  try {
+    d.make_conv(d.pre, t, "bigvgan.conv_pre", 1536, 80, 7, true);
+    for (int i = 0; i < 6; ++i) d.make_ups(d.ups[i], t, kUps[i]);
+    for (int j = 0; j < 18; ++j) {
+      const int C = rb_channels(j), k = kRbKernel[j % 3];
+      const std::string p = "bigvgan.resblocks." + std::to_string(j);
+      for (int pr = 0; pr < 3; ++pr) {
+        d.make_conv(d.rb[j][pr][0], t, p + ".convs1." + std::to_string(pr), C, C, k, true);
+        d.make_conv(d.rb[j][pr][1], t, p + ".convs2." + std::to_string(pr), C, C, k, true);
+      }
+      for (int a = 0; a < 6; ++a) d.make_act(d.act[j][a], t, p + ".activations." + std::to_string(a), C);
+    }
+    d.make_act(d.act_post, t, "bigvgan.activation_post", 24);
+    d.upload_f32(d.post_w, wnorm(get(t, "bigvgan.conv_post.weight_g", 1),
+                                 get(t, "bigvgan.conv_post.weight_v", 24 * 7), 1, 24 * 7));
+    d.zero = static_cast<half_t*>(d.wa.take(2048 * 2));
+    VOC_OK(hipMemset(d.zero, 0, 2048 * 2));
+    d.bytes = d.wa.used();
+  } catch (...) {
+    delete d_;
+    throw;
+  }
+}
+
+Vocoder::~Vocoder() { delete d_; }
+
+size_t Vocoder::weight_bytes() const { return d_->bytes; }
+
+void Vocoder::vocode_device(const float* mel, int tokens, float* wav) {
+  if (tokens <= 0) throw std::invalid_argument("vocoder: tokens must be positive");
+  d_->ensure(tokens);
+  d_->body(mel, tokens);
+  d_->post(d_->g32, tokens * 256, wav);
+}
+
+size_t Vocoder::stage_in_floats(int stage, int index, int tokens) {
+  switch (stage) {
+    case 0: return (size_t)tokens * 80;
+    case 1: return index >= 0 && index < 6 ? (size_t)tokens * kUps[index].cin : 0;
+    case 2: return index >= 0 && index < 108 ? (size_t)tokens * rb_channels(index / 6)
+                                             : index == 108 ? (size_t)tokens * 24 : 0;
+    case 3: return index >= 0 && index < 18 ? (size_t)tokens * rb_channels(index) : 0;
+    case 4: return index >= 0 && index < 6 ? (size_t)tokens * kUps[index].cout : 0;
+    case 5: return (size_t)tokens * 24;
+    case 6: return (size_t)tokens * 80;
+    default: return 0;
+  }
+}
+
+size_t Vocoder::stage_out_floats(int stage, int index, int tokens) {
+  switch (stage) {
+    case 0: return (size_t)tokens * 1536;
+    case 1: return index >= 0 && index < 6 ? (size_t)tokens * kUps[index].stride * kUps[index].cout : 0;
+    case 2: case 3: case 4: return stage_in_floats(stage, index, tokens);
+    case 5: return (size_t)tokens;
+    case 6: return (size_t)tokens * 256 * 24;
+    default: return 0;
+  }
+}
+
+size_t Vocoder::stage_host(int stage, int index, const float* in, int tokens, float* out) {
+  const size_t nin = stage_in_floats(stage, index, tokens), nout = stage_out_floats(stage, index, tokens);
+  if (tokens <= 0 || nin == 0 || nout == 0) throw std::invalid_argument("vocoder stage: bad stage/index/tokens");
+  Impl& d = *d_;
+  // The stage buffers hold 6144 floats per mel token of capacity: size them
+  // so this stage's input and output fit (conv_pre and the body take mel
+  // tokens, whose own buffers are per token).
+  const int cap_tokens = (int)((std::max(nin, nout) + 6143) / 6144) + 1;
+  d.ensure(stage == 0 || stage == 6 ? std::max(tokens, cap_tokens) : cap_tokens);
+  float* din = nullptr;
+  float* dout = nullptr;
+  VOC_OK(hipMalloc(&din, nin * 4));
+  VOC_OK(hipMalloc(&dout, nout * 4));
+  try {
+    VOC_OK(hipMemcpyAsync(din, in, nin * 4, hipMemcpyHostToDevice, d.s));
+    switch (stage) {
+      case 0:
+        d.to_f16(din, d.mel16, nin);
+        d.conv(d.pre, d.mel16, tokens, 1, 3, EPI_F32, dout, nullptr, nullptr, nullptr, 0);
+        break;
+      case 1:
+        d.to_f16(din, d.a16, nin);
+        d.conv(d.ups[index], d.a16, tokens, 1, 1, EPI_F32, dout, nullptr, nullptr, nullptr, 0);
+        break;
+      case 2:
+        d.activation(index == 108 ? d.act_post : d.act[index / 6][index % 6], din, tokens, dout, false);
+        break;
+      case 3:
+        d.resblock(index, din, tokens, dout, d.g32, 0, nullptr);
+        break;
+      case 4:
+        d.group(index, din, tokens, dout, nullptr);
+        break;
+      case 5:
+        d.post(din, tokens, dout);
+        break;
+      case 6:
+        d.body(din, tokens);
+        VOC_OK(hipMemcpyAsync(dout, d.g32, nout * 4, hipMemcpyDeviceToDevice, d.s));
+        break;
+    }
+    VOC_OK(hipMemcpyAsync(out, dout, nout * 4, hipMemcpyDeviceToHost, d.s));
+    VOC_OK(hipStreamSynchronize(d.s));
+  } catch (...) {
+    (void)hipStreamSynchronize(d.s);
+    (void)hipFree(din);
+    (void)hipFree(dout);
+    throw;
+  }
+  VOC_OK(hipFree(din));
+  VOC_OK(hipFree(dout));
+  return nout;
+}
+
+}  // namespace mit2hip

@@ -96,6 +96,10 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_condition_device": (st, [vp, vp, u32, vp, u32, vp, _u32p, u32]),
         "mit2cfm_generated_frames": (u32, [u32]),
         "mit2cfm_noise_device": (st, [vp, u32, u32, u64, f32, vp, u32]),
+        "mit2cfm_bigvgan": (st, [vp, _f32p, u32, _f32p]),
+        "mit2cfm_bigvgan_device": (st, [vp, vp, u32, vp, u32]),
+        "mit2cfm_bigvgan_stage": (st, [vp, i32, i32, _f32p, u32, _f32p, u64]),
+        "mit2cfm_bigvgan_stage_floats": (u64, [i32, i32, u32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -290,6 +294,20 @@ def synthetic_bigvgan_tensors(seed: int = 20240607, stddev: float = 0.02,
     return out
 
 
+def bigvgan_flops(tokens: int) -> float:
+    """Algorithmic conv FLOPs of the vocoder on `tokens` mel frames: 2 MACs per weight
+    tap per output (conv_pre, the six transposed convs counted on their input,
+    the 108 resblock convs, conv_post); the activations are element-wise work."""
+    f = 2.0 * tokens * 1536 * 80 * 7
+    t = tokens
+    for (_, cin, cout, k, s, _), g in zip(BIGVGAN_UPSAMPLERS, range(6)):
+        f += 2.0 * t * cin * cout * k
+        t *= s
+        c = cout
+        f += sum(6 * 2.0 * t * c * c * kk for kk in (3, 7, 11))
+    return f + 2.0 * t * 24 * 7
+
+
 def write_synthetic_bundle(path: str | os.PathLike, seed: int = 20240605, stddev: float = 0.02) -> None:
     _check(lib().mit2cfm_write_synthetic_bundle(str(path).encode(), seed, stddev))
 
@@ -481,6 +499,42 @@ class Context:
         """make_deterministic_normal_noise (tokenizer_tests.cpp:2121) into a device buffer."""
         self._c(lib().mit2cfm_noise_device(self._h, tokens, channels, seed, temperature, out_ptr,
                                            FLAG_SYNC if sync else 0))
+
+    # -- BigVGAN vocoder
+    def bigvgan(self, mel) -> np.ndarray:
+        """run_bigvgan_vocoder (dit_cfm_bigvgan.cpp:4058/4196): mel [tokens, 80] -> wav [256 tokens]."""
+        x = _f32(mel)
+        tokens = x.size // 80
+        out = np.empty(256 * tokens, np.float32)
+        self._c(lib().mit2cfm_bigvgan(self._h, _p(x), tokens, _p(out)))
+        return out
+
+    def bigvgan_device(self, mel_ptr: int, tokens: int, wav_ptr: int, sync: bool = False) -> None:
+        self._c(lib().mit2cfm_bigvgan_device(self._h, mel_ptr, tokens, wav_ptr, FLAG_SYNC if sync else 0))
+
+    BIGVGAN_STAGES = {"conv_pre": 0, "upsample": 1, "activation": 2, "resblock": 3, "group": 4, "post": 5,
+                      "body": 6}
+
+    def bigvgan_stage(self, stage: str, index: int, x) -> np.ndarray:
+        """One vocoder stage (ids in mit2cfm.h); x is [tokens, channels]; returns
+        [out_tokens, out_channels] (post: [tokens])."""
+        sid = self.BIGVGAN_STAGES[stage]
+        x = _f32(x)
+        tokens = x.shape[0]
+        n_in = lib().mit2cfm_bigvgan_stage_floats(sid, index, tokens, 0)
+        n_out = lib().mit2cfm_bigvgan_stage_floats(sid, index, tokens, 1)
+        if n_in != x.size:
+            raise ValueError(f"stage {stage}[{index}] takes {n_in} floats for {tokens} tokens, got {x.size}")
+        out = np.empty(n_out, np.float32)
+        self._c(lib().mit2cfm_bigvgan_stage(self._h, sid, index, _p(x), tokens, _p(out), n_out))
+        if stage == "post":
+            return out
+        if stage == "upsample":
+            s = 4 if index < 2 else 2
+            return out.reshape(tokens * s, -1)
+        if stage == "body":
+            return out.reshape(tokens * 256, 24)
+        return out.reshape(tokens, -1)
 
     # -- stages (parity harness)
     def timestep_embedder(self, t: float, which: int) -> np.ndarray:

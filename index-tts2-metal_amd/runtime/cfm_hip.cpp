@@ -15,7 +15,7 @@ HipContext::HipContext(const Bundle& bundle, int device) {
   std::vector<mit2cfm_tensor> ts;
   for (const auto& info : bundle.tensors()) {
     if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0 &&
-        info.name.rfind("s2mel.net.length_regulator.", 0) != 0)
+        info.name.rfind("s2mel.net.length_regulator.", 0) != 0 && info.name.rfind("bigvgan.", 0) != 0)
       continue;
     if (info.dtype != "f32" && info.dtype != "f16") continue;
     const bool f16 = info.dtype == "f16";

@@ -1,0 +1,172 @@
+"""GPU parity of the BigVGAN vocoder (the consumer of the decoded mel,
+dit_cfm_bigvgan.cpp:3606-4512) through the C ABI, stage by stage and end to
+end, against the CPU oracle on identical seeded inputs.
+
+The reference runs the vocoder in fp32 and holds its Metal path to max-abs
+1e-3 against its CPU path (run_bigvgan_vocoder_test, :4469-4490, on a
+one-frame mel of small amplitude; test_vocoder_reference_input repeats that
+case at that bar).  Here every conv takes f16 operands with fp32 accumulation
+(the activations, residual sums, the resblock mean and the clamp stay fp32),
+so each conv carries the f16 rounding of its input and weight: measured
+rel-L2 about 3e-4 per conv and 1e-3 for the waveform of a loud, many-frame
+mel, whose max-abs error is then about 1e-3.  The bars below are stated per
+stage in rel-L2 and, for the waveform, also in max-abs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import sincos_series
+
+pytestmark = pytest.mark.gpu
+
+ACT_TOL = 1e-6       # fp32 activation (the GPU's sin), rel-L2
+CONV_TOL = 1e-3      # one f16-operand conv, rel-L2
+BLOCK_TOL = 1e-3     # a resblock / group: six f16-operand convs (residual), rel-L2
+WAV_TOL = 2e-3       # the whole vocoder, rel-L2 ...
+WAV_MAXABS = 2.5e-3  # ... and max-abs on a waveform in [-1, 1]
+
+
+@pytest.fixture(scope="module")
+def bv_tensors(mit2):
+    return mit2.synthetic_bigvgan_tensors()
+
+
+@pytest.fixture(scope="module")
+def ctx_bv(mit2, tensors, bv_tensors):
+    c = mit2.Context({**tensors, **bv_tensors}, device=0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def bv(orc, bv_tensors):
+    return orc.BigVGAN(bv_tensors)
+
+
+def _x(tokens, channels, seed, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal((tokens, channels)) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("index,tokens", [(0, 1), (0, 37), (20, 130), (58, 64), (75, 200), (90, 65),
+                                          (107, 301), (108, 513)])
+def test_activation(orc, ctx_bv, bv, index, tokens):
+    j, a = divmod(index, 6)
+    prefix = "bigvgan.activation_post" if index == 108 else f"bigvgan.resblocks.{j}.activations.{a}"
+    C = 24 if index == 108 else 768 >> (j // 3)
+    x = _x(tokens, C, index + tokens, 2.0)
+    print(f"activation {index} ({prefix}) T={tokens} C={C}", flush=True)
+    got = ctx_bv.bigvgan_stage("activation", index, x)
+    ref = bv.activation(prefix, x)
+    err = orc.rel_l2(got, ref)
+    print(f"  rel-L2 {err:.3e}", flush=True)
+    assert err <= ACT_TOL
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 70])
+def test_conv_pre(orc, ctx_bv, bv, tokens):
+    mel = sincos_series(tokens * 80, 0.017, 0.029, 2.0, 1.0, 71).reshape(tokens, 80) - 5.0
+    got = ctx_bv.bigvgan_stage("conv_pre", 0, mel)
+    ref = bv.conv_pre(mel)
+    err = orc.rel_l2(got, ref)
+    print(f"conv_pre T={tokens}: rel-L2 {err:.3e}", flush=True)
+    assert err <= CONV_TOL
+
+
+@pytest.mark.parametrize("index,tokens", [(0, 1), (0, 9), (1, 33), (2, 70), (3, 129), (4, 64), (5, 257)])
+def test_upsample(orc, ctx_bv, bv, index, tokens):
+    cin = [1536, 768, 384, 192, 96, 48][index]
+    x = _x(tokens, cin, 100 + index)
+    print(f"upsample {index} T={tokens} Cin={cin}", flush=True)
+    got = ctx_bv.bigvgan_stage("upsample", index, x)
+    ref = bv.upsample(x, index)
+    assert got.shape == ref.shape
+    err = orc.rel_l2(got, ref)
+    print(f"  rel-L2 {err:.3e}", flush=True)
+    assert err <= CONV_TOL
+
+
+@pytest.mark.parametrize("index,tokens", [(0, 12), (2, 40), (4, 64), (8, 100), (10, 257), (14, 300),
+                                          (17, 512)])
+def test_resblock(orc, ctx_bv, bv, index, tokens):
+    C = 768 >> (index // 3)
+    k = (3, 7, 11)[index % 3]
+    x = _x(tokens, C, 200 + index)
+    print(f"resblock {index} T={tokens} C={C} k={k}", flush=True)
+    got = ctx_bv.bigvgan_stage("resblock", index, x)
+    ref = bv.resblock(f"bigvgan.resblocks.{index}", x, k)
+    err = orc.rel_l2(got, ref)
+    print(f"  rel-L2 {err:.3e}", flush=True)
+    assert err <= BLOCK_TOL
+
+
+@pytest.mark.parametrize("index,tokens", [(0, 16), (3, 128), (5, 600)])
+def test_resblock_group(orc, ctx_bv, bv, index, tokens):
+    C = 768 >> index
+    x = _x(tokens, C, 300 + index)
+    print(f"group {index} T={tokens} C={C}", flush=True)
+    got = ctx_bv.bigvgan_stage("group", index, x)
+    ref = bv.resblock_group(x, index)
+    err = orc.rel_l2(got, ref)
+    print(f"  rel-L2 {err:.3e}", flush=True)
+    assert err <= BLOCK_TOL
+
+
+@pytest.mark.parametrize("tokens", [1, 256, 1000])
+def test_post(orc, ctx_bv, bv, tokens):
+    x = sincos_series(tokens * 24, 0.011, 0.021, 3.0, 1.0, 83).reshape(tokens, 24)
+    got = ctx_bv.bigvgan_stage("post", 0, x)
+    ref = bv.post(x).reshape(-1)
+    err = float(np.abs(got - ref).max())
+    print(f"post T={tokens}: max-abs {err:.3e}", flush=True)
+    assert err <= 1e-5
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 8])
+def test_vocoder_matches_oracle(orc, ctx_bv, bv, tokens):
+    mel = (sincos_series(tokens * 80, 0.017, 0.029, 2.0, 1.0, 71).reshape(tokens, 80) - 5.0).astype(np.float32)
+    print(f"vocoder T={tokens}", flush=True)
+    got = ctx_bv.bigvgan(mel)
+    ref = bv.vocoder(mel)
+    assert got.shape == (256 * tokens,)
+    err, mx = orc.rel_l2(got, ref), float(np.abs(got - ref).max())
+    print(f"  rel-L2 {err:.3e}  max-abs {mx:.3e}  |wav| max {np.abs(ref).max():.3f}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= WAV_TOL and mx <= WAV_MAXABS
+
+
+def test_vocoder_reference_input(orc, ctx_bv, bv):
+    """run_bigvgan_vocoder_test's input (dit_cfm_bigvgan.cpp:4469-4490): one mel
+    frame, mel[i] = sin(0.017 i) 0.10 + cos(0.029 (i % 71)) 0.025; its bar max-abs 1e-3."""
+    mel = sincos_series(80, 0.017, 0.029, 0.10, 0.025, 71).reshape(1, 80)
+    got = ctx_bv.bigvgan(mel)
+    ref = bv.vocoder(mel)
+    mx = float(np.abs(got - ref).max())
+    print(f"vocoder (reference input): max-abs {mx:.3e}  rel-L2 {orc.rel_l2(got, ref):.3e}", flush=True)
+    assert mx <= 1e-3
+
+
+def test_vocoder_device_matches_host_and_repeats(mit2, ctx_bv):
+    torch = pytest.importorskip("torch")
+    tokens = 40
+    mel = (np.random.default_rng(5).standard_normal((tokens, 80)) * 2.0 - 5.0).astype(np.float32)
+    host = ctx_bv.bigvgan(mel)
+    d_mel = torch.from_numpy(mel).to("cuda:0")
+    d_wav = torch.empty(256 * tokens, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    ctx_bv.bigvgan_device(d_mel.data_ptr(), tokens, d_wav.data_ptr(), sync=True)
+    assert np.array_equal(d_wav.cpu().numpy(), host)
+    # a longer call in between (the workspace grows) does not change a later short one
+    ctx_bv.bigvgan(np.zeros((200, 80), np.float32) - 4.0)
+    assert np.array_equal(ctx_bv.bigvgan(mel), host)
+
+
+def test_missing_vocoder_is_a_model_error(mit2, tensors):
+    c = mit2.Context(tensors, device=0)
+    try:
+        with pytest.raises(mit2.Mit2CfmError) as e:
+            c.bigvgan(np.zeros((2, 80), np.float32))
+        assert e.value.status == mit2.E_MODEL
+    finally:
+        c.close()
