@@ -16,8 +16,8 @@
 //  * the residual add of each AMP pair and the /3 average of the three
 //    resblocks are fused into the second conv's epilogue (EPI_RESAVG), which
 //    also writes the f16 operand of the next upsampler;
-//  * the activation keeps the two-times-upsampled, snake'd signal of a tile in
-//    LDS, so each upsampled value is computed once.
+//  * the activation keeps the two-times-upsampled, snake'd signal of a run of
+//    tokens in registers, so each upsampled value is computed once.
 #include "vocoder.h"
 
 #include <cmath>
@@ -54,89 +54,113 @@ inline int rb_channels(int j) { return 768 >> (j / 3); }
 inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 // ---------------------------------------------------------------- kernels
+// The two 12-tap filters of one anti-aliased activation, passed by value so
+// every tap is a scalar operand.
+struct ActFilters {
+  float up[12];
+  float down[12];
+};
+
 // Anti-aliased SnakeBeta (cpu_bigvgan_activation, tokenizer_tests.cpp:3811):
 //   U(u) = 2 sum_{k: (u+15-k) even} x[clamp((u+15-k)/2 - 5)] up[k]
 //   Z(u) = U + sin(alpha U)^2 / (beta + 1e-9)
 //   out[t] = sum_k Z(clamp(2t + k - 5, 0, 2T-1)) down[k]
-// A workgroup owns TT tokens x CC channels.  Its x window (tokens t0-6 ..
-// t0+TT+5, clamped) and the Z values it needs (u = 2 t0 - 5 .. 2 t0 + 2 TT + 4,
-// clamped) live in LDS; every Z is computed once.
-constexpr int kActTT = 64;
+// By parity, U(2v) = 2 sum_j x[v+2-j] up[2j+1] and U(2v+1) = 2 sum_j x[v+3-j]
+// up[2j] (j = 0..5).  A lane owns one channel and R consecutive tokens; its
+// x window (tokens t0-6 .. t0+R+5, clamped) and the 2R+10 Z values its
+// outputs need stay in registers, so each Z is computed once and nothing
+// goes through LDS.  The 64 lanes of a wave take 64 consecutive channels of
+// the same tokens (coalesced row segments).
+constexpr int kActR = 16;
 
-template <int CC, bool OUT16>
-__global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__ x,
-                                                       const float* __restrict__ upf,
-                                                       const float* __restrict__ dnf,
+template <bool OUT16>
+__global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__ x, ActFilters f,
                                                        const float* __restrict__ alpha,
                                                        const float* __restrict__ inv_beta, int T,
                                                        int C, void* __restrict__ out) {
-  constexpr int XR = kActTT + 12;      // x window rows
-  constexpr int ZR = 2 * kActTT + 10;  // Z window rows
-  __shared__ float xs[XR * CC];
-  __shared__ float zs[ZR * CC];
-  __shared__ float fu[12], fd[12];
-  const int t0 = blockIdx.x * kActTT;
-  const int c0 = blockIdx.y * CC;
-  const int tid = threadIdx.x;
-  if (tid < 12) fu[tid] = upf[tid];
-  else if (tid < 24) fd[tid - 12] = dnf[tid - 12];
-  for (int idx = tid; idx < XR * CC; idx += 256) {
-    const int i = idx / CC, c = idx - (idx / CC) * CC;
+  constexpr int R = kActR;
+  constexpr int XW = R + 12;      // x window
+  constexpr int ZW = 2 * R + 10;  // Z window: u = 2 t0 - 5 + i
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int groups = (C + 63) >> 6;
+  const int run = wave / groups;
+  const int c = (wave - run * groups) * 64 + lane;
+  const int t0 = run * R;
+  if (t0 >= T || c >= C) return;
+  float xw[XW];
+#pragma unroll
+  for (int i = 0; i < XW; ++i) {
     int src = t0 - 6 + i;
     src = src < 0 ? 0 : (src >= T ? T - 1 : src);
-    xs[idx] = x[(size_t)src * C + c0 + c];
+    xw[i] = x[(size_t)src * C + c];
   }
-  __syncthreads();
-  const int u_lo = 2 * t0 - 5;
-  for (int idx = tid; idx < ZR * CC; idx += 256) {
-    const int i = idx / CC, c = idx - (idx / CC) * CC;
-    int u = u_lo + i;
-    u = u < 0 ? 0 : (u >= 2 * T ? 2 * T - 1 : u);
-    const int full = u + 15;
-    float acc = 0.0f;
+  const float a = alpha[c], ib = inv_beta[c];
+  float z[ZW];
 #pragma unroll
-    for (int k = 0; k < 12; ++k) {
-      if (((full - k) & 1) == 0) {
-        const int src = ((full - k) >> 1) - 5;  // within the window for every clamped u
-        acc += xs[(src - (t0 - 6)) * CC + c] * fu[k];
-      }
+  for (int i = 0; i < ZW; ++i) {
+    float acc = 0.0f;
+    if (i & 1) {  // u even: x window index (i-5)/2 + 8 - j, taps up[2j+1]
+#pragma unroll
+      for (int j = 0; j < 6; ++j) acc += xw[(i - 5) / 2 + 8 - j] * f.up[2 * j + 1];
+    } else {      // u odd: x window index (i-6)/2 + 9 - j, taps up[2j]
+#pragma unroll
+      for (int j = 0; j < 6; ++j) acc += xw[(i - 6) / 2 + 9 - j] * f.up[2 * j];
     }
     const float y = 2.0f * acc;
-    const float s = __sinf(y * alpha[c0 + c]);
-    zs[idx] = y + (s * s) * inv_beta[c0 + c];
+    const float sn = __sinf(y * a);
+    z[i] = y + (sn * sn) * ib;
   }
-  __syncthreads();
-  for (int idx = tid; idx < kActTT * CC; idx += 256) {
-    const int tt = idx / CC, c = idx - (idx / CC) * CC;
-    const int t = t0 + tt;
-    if (t >= T) continue;
+  // Upsampled positions outside [0, 2T) take the value at the nearest end.
+  if (t0 == 0) {
+#pragma unroll
+    for (int i = 0; i < 5; ++i) z[i] = z[5];
+  }
+  const int i_end = 2 * (T - t0) + 4;  // slot of u = 2T - 1
+  if (i_end < ZW - 1) {
+    float ze = z[0];
+#pragma unroll
+    for (int i = 0; i < ZW; ++i) ze = i == i_end ? z[i] : ze;
+#pragma unroll
+    for (int i = 0; i < ZW; ++i) z[i] = i > i_end ? ze : z[i];
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (t0 + r >= T) break;
     float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 12; ++k) acc += zs[(2 * tt + k) * CC + c] * fd[k];
+    for (int k = 0; k < 12; ++k) acc += z[2 * r + k] * f.down[k];
     if constexpr (OUT16)
-      static_cast<half_t*>(out)[(size_t)t * C + c0 + c] = (half_t)acc;
+      static_cast<half_t*>(out)[(size_t)(t0 + r) * C + c] = (half_t)acc;
     else
-      static_cast<float*>(out)[(size_t)t * C + c0 + c] = acc;
+      static_cast<float*>(out)[(size_t)(t0 + r) * C + c] = acc;
   }
 }
 
 // conv_post (k = 7, 24 -> 1, zero bias) and the final clamp
-// (run_bigvgan_post_cpu, dit_cfm_bigvgan.cpp:4030-4039).
+// (run_bigvgan_post_cpu, dit_cfm_bigvgan.cpp:4030-4039).  A workgroup stages
+// its 256 + 6 input rows (one contiguous block) in LDS, row stride 25 so the
+// lanes' reads fall in distinct banks.
 __global__ __launch_bounds__(256) void conv_post_clamp_kernel(const float* __restrict__ a,
                                                               const float* __restrict__ w, int T,
                                                               float* __restrict__ wav) {
+  constexpr int RS = 25;
   __shared__ float ws[24 * 7];
+  __shared__ float as[262 * RS];
+  const int t0 = blockIdx.x * 256;
   if (threadIdx.x < 24 * 7) ws[threadIdx.x] = w[threadIdx.x];
+  for (int idx = threadIdx.x; idx < 262 * 24; idx += 256) {
+    const int row = idx / 24, ic = idx - (idx / 24) * 24;
+    const int src = t0 - 3 + row;
+    as[row * RS + ic] = (src >= 0 && src < T) ? a[(size_t)src * 24 + ic] : 0.0f;
+  }
   __syncthreads();
-  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int t = t0 + threadIdx.x;
   if (t >= T) return;
   float acc = 0.0f;
   for (int ic = 0; ic < 24; ++ic) {
 #pragma unroll
-    for (int k = 0; k < 7; ++k) {
-      const int src = t + k - 3;
-      if (src >= 0 && src < T) acc += a[(size_t)src * 24 + ic] * ws[ic * 7 + k];
-    }
+    for (int k = 0; k < 7; ++k) acc += as[(threadIdx.x + k) * RS + ic] * ws[ic * 7 + k];
   }
   wav[t] = fminf(1.0f, fmaxf(-1.0f, acc));
 }
@@ -181,8 +205,7 @@ struct Vocoder::Conv {
 };
 
 struct Vocoder::Act {
-  float* upf = nullptr;
-  float* dnf = nullptr;
+  ActFilters filt;
   float* alpha = nullptr;     // exp(alpha_log) [C]
   float* inv_beta = nullptr;  // 1 / (exp(beta_log) + 1e-9) [C]
   int C = 0;
@@ -271,8 +294,12 @@ struct Vocoder::Impl {
   void make_act(Act& a, const std::unordered_map<std::string, std::vector<float>>& t, const std::string& prefix,
                 int C) {
     a.C = C;
-    upload_f32(a.upf, get(t, prefix + ".upsample.filter", 12));
-    upload_f32(a.dnf, get(t, prefix + ".downsample.lowpass.filter", 12));
+    const auto& fu = get(t, prefix + ".upsample.filter", 12);
+    const auto& fd = get(t, prefix + ".downsample.lowpass.filter", 12);
+    for (int k = 0; k < 12; ++k) {
+      a.filt.up[k] = fu[k];
+      a.filt.down[k] = fd[k];
+    }
     const auto& al = get(t, prefix + ".act.alpha", C);
     const auto& bl = get(t, prefix + ".act.beta", C);
     std::vector<float> alpha(C), ib(C);
@@ -335,21 +362,14 @@ struct Vocoder::Impl {
   }
 
   void activation(const Act& a, const float* in, int T, void* out, bool out16) {
-    const dim3 grid((T + kActTT - 1) / kActTT, 1);
-    auto go = [&](auto cc) {
-      constexpr int CC = decltype(cc)::value;
-      const dim3 gr(grid.x, a.C / CC);
-      if (out16)
-        hipLaunchKernelGGL((snake_aa_kernel<CC, true>), gr, dim3(256), 0, s, in, a.upf, a.dnf, a.alpha,
-                           a.inv_beta, T, a.C, out);
-      else
-        hipLaunchKernelGGL((snake_aa_kernel<CC, false>), gr, dim3(256), 0, s, in, a.upf, a.dnf, a.alpha,
-                           a.inv_beta, T, a.C, out);
-    };
-    if (a.C % 32 == 0) go(std::integral_constant<int, 32>{});
-    else if (a.C == 48) go(std::integral_constant<int, 48>{});
-    else if (a.C == 24) go(std::integral_constant<int, 24>{});
-    else throw std::invalid_argument("activation: unsupported channel count");
+    const size_t waves = (size_t)((T + kActR - 1) / kActR) * ((a.C + 63) / 64);
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (out16)
+      hipLaunchKernelGGL(snake_aa_kernel<true>, grid, dim3(256), 0, s, in, a.filt, a.alpha, a.inv_beta,
+                         T, a.C, out);
+    else
+      hipLaunchKernelGGL(snake_aa_kernel<false>, grid, dim3(256), 0, s, in, a.filt, a.alpha, a.inv_beta,
+                         T, a.C, out);
     VOC_OK(hipGetLastError());
   }
 
