@@ -32,6 +32,15 @@ Prints ONE JSON line.  Extra fields:
                 stream, output samples/s, algorithmic conv TFLOP/s, and the
                 oracle on the host cores over a bounded sample (two mel
                 frames).
+  acoustic_stage
+                the whole acoustic stage of one synthesis segment on the GPU
+                (mit2cfm_acoustic_device: condition, seeded noise, CFG decode,
+                vocoder), at the reference's published steady-state segment:
+                553 semantic codes -> 951 generated frames after a 629-frame
+                voice prompt (T = 1580), 16 steps, CFG 0.7, 11.0 s of audio;
+                time per call from HIP events, its real-time factor, and the
+                reference's published time for that segment on its own
+                hardware (a different machine and the real weights).
 """
 from __future__ import annotations
 
@@ -71,6 +80,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cond-calls", type=int, default=50, help="timed condition-producer calls")
     p.add_argument("--voc-calls", type=int, default=10, help="timed vocoder calls (0 = skip)")
+    p.add_argument("--acoustic-calls", type=int, default=5,
+                   help="timed acoustic-stage calls (0 = skip; needs the vocoder)")
     p.add_argument("--calib-mib", type=int, default=256,
                    help="size of the counter-calibration copy (0 = skip)")
     return p.parse_args()
@@ -319,6 +330,44 @@ def main():
         if not a.no_cpu_baseline:
             voc["cpu_baseline"] = vocoder_cpu_baseline(bv_tensors, d_out.cpu().numpy(), cpu_threads(a))
 
+    # The whole acoustic stage at the reference's published segment
+    # (docs/evolution.md:27: 553 codes, 11.0 s audio, 16 steps, acoustic 5.39 s;
+    # the voice prompt is 629 frames, docs/evolution.md:14).
+    ac = None
+    if a.acoustic_calls and a.voc_calls:
+        codes_a, P_a, S_a = 553, 629, 16
+        gen_a = mit2cfm.generated_frames(codes_a)
+        d_si = torch.from_numpy(mit2cfm.normal_noise(codes_a, 1024, 8)).to(dev)
+        d_pc_a = torch.from_numpy(mit2cfm.normal_noise(P_a, 512, 9)).to(dev)
+        d_pm_a = torch.from_numpy(mit2cfm.normal_noise(P_a, 80, 10, 2.0) - 5.0).to(dev)
+        d_wav_a = torch.empty(256 * gen_a, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+
+        def acoustic():
+            return ctx.acoustic_device(d_si.data_ptr(), codes_a, d_pc_a.data_ptr(), d_pm_a.data_ptr(), P_a,
+                                       d_style.data_ptr(), 20240608, 1.0, S_a, cfg, d_wav_a.data_ptr())
+
+        for _ in range(2):
+            acoustic()
+        ctx.synchronize()
+        a0 = torch.cuda.Event(enable_timing=True)
+        a1 = torch.cuda.Event(enable_timing=True)
+        a0.record(stream)
+        for _ in range(a.acoustic_calls):
+            acoustic()
+        a1.record(stream)
+        ctx.synchronize()
+        torch.cuda.synchronize()
+        a_ms = a0.elapsed_time(a1) / a.acoustic_calls
+        audio_s = 256 * gen_a / 22050.0
+        ac = {"workload": f"{codes_a} codes -> {gen_a} frames after a {P_a}-frame prompt (T={P_a + gen_a}), "
+                          f"{S_a} steps, cfg {cfg}, vocoder -> {256 * gen_a} samples",
+              "ms_per_call": round(a_ms, 3), "audio_s": round(audio_s, 3),
+              "rtf": round(a_ms / 1e3 / audio_s, 5),
+              "reference_published": {"acoustic_s": 5.39, "hardware": "Apple M3 Ultra (Metal/MPS)",
+                                      "source": "docs/evolution.md:27, segment 1"},
+              "speedup_vs_published": round(5390.0 / a_ms, 1)}
+
     # Host-pointer decode (PCIe-inclusive; reported, never the headline value).
     ctx.decode(x0, prompt, cond, style, S, cfg)
     t1 = time.perf_counter()
@@ -356,6 +405,8 @@ def main():
         result["condition_producer"] = cp
     if voc:
         result["vocoder"] = voc
+    if ac:
+        result["acoustic_stage"] = ac
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(tensors, T, P, S, cfg, cpu_threads(a))
     print(json.dumps(result), flush=True)

@@ -285,6 +285,27 @@ mit2cfm_status mit2cfm_bigvgan_stage(mit2cfm_ctx* ctx, int32_t stage, int32_t in
  * input rows; 0 for an unknown stage or index. */
 uint64_t mit2cfm_bigvgan_stage_floats(int32_t stage, int32_t index, uint32_t tokens, int32_t output);
 
+/* ---- the whole acoustic stage ----------------------------------------------
+ * Replaces the acoustic half of the reference's hot synthesis path on the
+ * GPU, with no host round trip: the length regulator and prompt merge of
+ * build_hot_codes_condition_inputs_shared (runtime/impl/tts_synthesis/
+ * synthesis_pipeline.cpp:1012-1035), the seeded noise
+ * make_deterministic_normal_noise(T, 80, seed, temperature) (:1333), and
+ * synthesize_hot_condition_vectors_wav_shared (:1038-1097: the CFG decode,
+ * the generated rows sliced off, the vocoder) without the WAV file write.
+ * DEVICE pointers: s_infer [codes][1024]; prompt_cond [>= P][512] (the
+ * voice's s2mel_prompt); prompt_mel [P][80] token-major (the voice's mel
+ * transposed); style [192]; wav_out [256 * generated], generated =
+ * floor(codes * 1.72f); mel_out (optional) [P + generated][80].  Needs the
+ * estimator, length-regulator and vocoder tensors.  Enqueued on the context's
+ * stream (flags as for mit2cfm_decode_device). */
+mit2cfm_status mit2cfm_acoustic_device(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                       const float* prompt_cond, const float* prompt_mel,
+                                       uint32_t prompt_tokens, const float* style, uint64_t noise_seed,
+                                       float noise_temperature, uint32_t steps, float cfg_rate,
+                                       float* wav_out, float* mel_out, uint32_t* generated_out,
+                                       uint32_t flags);
+
 #ifdef __cplusplus
 }
 #endif

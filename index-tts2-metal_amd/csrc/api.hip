@@ -547,3 +547,26 @@ mit2cfm_status mit2cfm_bigvgan_stage(mit2cfm_ctx* ctx, int32_t stage, int32_t in
     ctx->eng->vocoder_stage_host(stage, index, in, (int)tokens, out);
   });
 }
+
+// ---- the whole acoustic stage ---------------------------------------------
+mit2cfm_status mit2cfm_acoustic_device(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                       const float* prompt_cond, const float* prompt_mel,
+                                       uint32_t prompt_tokens, const float* style, uint64_t noise_seed,
+                                       float noise_temperature, uint32_t steps, float cfg_rate,
+                                       float* wav_out, float* mel_out, uint32_t* generated_out,
+                                       uint32_t flags) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(s_infer && prompt_cond && prompt_mel && style && wav_out,
+            "s_infer, prompt_cond, prompt_mel, style and wav_out must not be NULL");
+    require(codes > 0 && codes <= (1u << 20) && prompt_tokens > 0 && prompt_tokens <= (1u << 20),
+            "codes and prompt_tokens must be in [1, 2^20]");
+    require(steps > 0 && steps <= 1000, "steps must be in [1, 1000]");
+    require(cfg_rate >= 0.0f, "cfg_rate must be >= 0");
+    const int gen = ctx->eng->acoustic_device(s_infer, (int)codes, prompt_cond, prompt_mel,
+                                              (int)prompt_tokens, style, noise_seed, noise_temperature,
+                                              (int)steps, cfg_rate, wav_out, mel_out);
+    if (generated_out) *generated_out = (uint32_t)gen;
+    if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}

@@ -151,6 +151,20 @@ class Engine {
   // output floats written.
   size_t vocoder_stage_host(int stage, int index, const float* in, int tokens, float* out);
 
+  // ---- the whole acoustic stage on the device (synthesis_pipeline.cpp:
+  // build_hot_codes_condition_inputs_shared :1012-1035, the seeded noise :1333,
+  // synthesize_hot_condition_vectors_wav_shared :1038-1097): condition from
+  // s_infer [codes][1024] and the voice's prompt_cond rows, x0 =
+  // make_deterministic_normal_noise(T, 80, seed, temperature), the CFG decode
+  // with the voice's prompt_mel [P][80] (token-major) and style [192], then the
+  // vocoder on the generated rows.  DEVICE pointers; wav [256 * generated];
+  // mel (optional) receives the full decoded mel [T][80].  Enqueued on
+  // stream(); returns generated.
+  int acoustic_device(const float* s_infer, int codes, const float* prompt_cond,
+                      const float* prompt_mel, int prompt_tokens, const float* style,
+                      uint64_t seed, float temperature, int steps, float cfg, float* wav,
+                      float* mel);
+
   // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
   void set_use_graph(bool on) { use_graph_ = on; }
   void sync();
@@ -178,6 +192,11 @@ class Engine {
   std::unique_ptr<Vocoder> voc_;
   float* voc_io_ = nullptr;  // host-path staging: mel, then wav
   size_t voc_io_floats_ = 0;
+  // Acoustic-stage buffers (condition [T][512], x0 and mel [T][80]), grown on
+  // demand and kept, so the decode graphs captured on them stay valid.
+  Arena ac_;
+  int ac_cap_ = 0;
+  float *ac_cond_ = nullptr, *ac_x0_ = nullptr, *ac_mel_ = nullptr;
   // Length-regulator buffers, grown on demand (separate from the decode's
   // workspace so a condition call never invalidates captured decode graphs).
   struct LrBufs {

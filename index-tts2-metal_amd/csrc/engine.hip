@@ -1480,6 +1480,38 @@ void Engine::vocode_host(const float* mel, int tokens, float* wav) {
   HIP_OK(hipStreamSynchronize(stream_));
 }
 
+int Engine::acoustic_device(const float* s_infer, int codes, const float* prompt_cond,
+                            const float* prompt_mel, int prompt_tokens, const float* style,
+                            uint64_t seed, float temperature, int steps, float cfg, float* wav,
+                            float* mel) {
+  if (codes <= 0 || prompt_tokens <= 0 || steps <= 0)
+    throw std::invalid_argument("acoustic: codes, prompt_tokens and steps must be positive");
+  need_vocoder(voc_);
+  if (!w_->has_lr)
+    throw std::runtime_error("acoustic: the context has no s2mel.net.length_regulator.* tensors");
+  const int gen = generated_frames(codes);
+  if (gen <= 0) throw std::invalid_argument("acoustic: generated frame count is zero");
+  const int T = prompt_tokens + gen;
+  HIP_OK(hipSetDevice(device_));
+  if (T > ac_cap_) {
+    HIP_OK(hipStreamSynchronize(stream_));
+    clear_graphs();  // graphs captured on the old buffers
+    ac_.reserve((size_t)T * (512 + 80 + 80) * sizeof(float) + 3 * 256);
+    ac_cond_ = static_cast<float*>(ac_.take((size_t)T * 512 * sizeof(float)));
+    ac_x0_ = static_cast<float*>(ac_.take((size_t)T * 80 * sizeof(float)));
+    ac_mel_ = static_cast<float*>(ac_.take((size_t)T * 80 * sizeof(float)));
+    ac_cap_ = T;
+  }
+  condition_device(s_infer, codes, prompt_cond, prompt_tokens, ac_cond_);
+  normal_noise_device((size_t)T * 80, seed, temperature, ac_x0_);
+  const uint32_t vt = (uint32_t)T, pt = (uint32_t)prompt_tokens;
+  decode_device(ac_x0_, prompt_mel, ac_cond_, style, 1, T, &vt, &pt, steps, cfg, ac_mel_, nullptr);
+  voc_->vocode_device(ac_mel_ + (size_t)prompt_tokens * 80, gen, wav);
+  if (mel)
+    HIP_OK(hipMemcpyAsync(mel, ac_mel_, (size_t)T * 80 * sizeof(float), hipMemcpyDeviceToDevice, stream_));
+  return gen;
+}
+
 size_t Engine::vocoder_stage_host(int stage, int index, const float* in, int tokens, float* out) {
   HIP_OK(hipSetDevice(device_));
   return need_vocoder(voc_).stage_host(stage, index, in, tokens, out);

@@ -85,7 +85,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave sub-tile must be whole MFMA blocks");
   static_assert(L * (NST - 1) < 64, "too many loads in flight");
   static_assert(CPR == 8 || CPR >= 16, "stage width");
-  static_assert(KG == 1 || (KG == 2 && EPI != EPI_QKV), "K groups: the QKV epilogue needs every wave");
+  static_assert(KG == 1 || ((KG == 2 || KG == 4) && EPI != EPI_QKV),
+                "K groups: 2 or 4, and the QKV epilogue needs every wave");
 
   // One __shared__ object per stage and operand, declared here so each kernel
   // instantiation owns its own objects (the per-object alias scopes are what
@@ -401,20 +402,31 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     if (kt0 + (int)decltype(st)::value < KT) compute(st);
   });
 
-  // K groups: group 1 hands its partial tile to group 0 through LDS and
-  // leaves; group 0 adds it (a fixed order, so the sum is deterministic) and
-  // runs the epilogue.
-  if constexpr (KG == 2) {
-    // The partial tile (BM x BN fp32) goes into the first W stage buffer when
-    // it fits (the ring is idle by now), else into a buffer of its own.
-    constexpr bool kRedInRing = BM * BN * 4 <= KG * BN * SK * 2;
-    __shared__ __attribute__((aligned(1024))) floatx4 red_own[kRedInRing ? 1 : NW * MI * NI * 64];
-    floatx4* red = kRedInRing ? reinterpret_cast<floatx4*>(sB0) : red_own;
+  // K groups: groups 1..KG-1 hand their partial tiles to group 0 through LDS
+  // and leave; group 0 adds them in group order (a fixed order, so the sum is
+  // deterministic) and runs the epilogue.  Each partial (BM x BN fp32) goes
+  // into one of the idle ring buffers sB0, sA0, sB1 when those hold a tile,
+  // else into a buffer of its own.
+  if constexpr (KG > 1) {
+    constexpr int kTileBytes = BM * BN * 4;
+    constexpr bool kRedInRing = kTileBytes <= KG * BN * SK * 2 &&
+                                (KG < 3 || kTileBytes <= KG * BM * SK * 2) && (KG < 4 || NST >= 2);
+    constexpr int kPart = NW * MI * NI * 64;  // floatx4 per partial tile
+    __shared__ __attribute__((aligned(1024))) floatx4 red_own[kRedInRing ? 1 : (KG - 1) * kPart];
+    auto red_buf = [&](int g) -> floatx4* {
+      if constexpr (kRedInRing) {
+        half_t* b = g == 1 ? sB0 : g == 2 ? sA0 : sB1;
+        return reinterpret_cast<floatx4*>(b);
+      } else {
+        return red_own + (g - 1) * kPart;
+      }
+    };
     if constexpr (kRedInRing) {
       wait_lgkmcnt0();
       __syncthreads();  // every wave has finished reading the ring
     }
-    if (kg == 1) {
+    if (kg > 0) {
+      floatx4* red = red_buf(kg);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -422,11 +434,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     }
     wait_lgkmcnt0();
     __syncthreads();
-    if (kg == 1) return;
+    if (kg > 0) return;
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int g = 1; g < KG; ++g) {
+      const floatx4* red = red_buf(g);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) acc[i][j] += red[((wave * MI + i) * NI + j) * 64 + lane];
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] += red[((wave * MI + i) * NI + j) * 64 + lane];
+    }
   }
 
   // ---------------------------------------------------------------- epilogue

@@ -100,6 +100,8 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_bigvgan_device": (st, [vp, vp, u32, vp, u32]),
         "mit2cfm_bigvgan_stage": (st, [vp, i32, i32, _f32p, u32, _f32p, u64]),
         "mit2cfm_bigvgan_stage_floats": (u64, [i32, i32, u32, i32]),
+        "mit2cfm_acoustic_device": (st, [vp, vp, u32, vp, vp, u32, vp, u64, f32, u32, f32, vp, vp, _u32p,
+                                         u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -511,6 +513,18 @@ class Context:
 
     def bigvgan_device(self, mel_ptr: int, tokens: int, wav_ptr: int, sync: bool = False) -> None:
         self._c(lib().mit2cfm_bigvgan_device(self._h, mel_ptr, tokens, wav_ptr, FLAG_SYNC if sync else 0))
+
+    def acoustic_device(self, s_infer_ptr: int, codes: int, prompt_cond_ptr: int, prompt_mel_ptr: int,
+                        prompt_tokens: int, style_ptr: int, seed: int, temperature: float, steps: int,
+                        cfg: float, wav_ptr: int, mel_ptr: int = 0, sync: bool = False) -> int:
+        """The whole acoustic stage on device buffers (raw addresses): condition,
+        seeded noise, CFG decode, vocoder on the generated rows; returns the
+        generated frame count (the waveform has 256 samples per frame)."""
+        g = np.zeros(1, np.uint32)
+        self._c(lib().mit2cfm_acoustic_device(self._h, s_infer_ptr, codes, prompt_cond_ptr, prompt_mel_ptr,
+                                              prompt_tokens, style_ptr, seed, temperature, steps, cfg, wav_ptr,
+                                              mel_ptr or None, _pu(g), FLAG_SYNC if sync else 0))
+        return int(g[0])
 
     BIGVGAN_STAGES = {"conv_pre": 0, "upsample": 1, "activation": 2, "resblock": 3, "group": 4, "post": 5,
                       "body": 6}
