@@ -205,6 +205,28 @@ mit2cfm_status mit2cfm_synthetic_tensor_info(uint32_t i, const char** name, uint
 /* Payload of tensor i (elems * 2 bytes for f16, * 4 for f32) into out. */
 mit2cfm_status mit2cfm_synthetic_tensor_fill(uint32_t i, uint64_t base_seed, float stddev,
                                              void* out);
+/* Synthetic tensor sets beyond the estimator (the functions above are set 0):
+ * MIT2CFM_SYNTH_LENGTH_REGULATOR, the s2mel length regulator's 20 tensors
+ * (N(0, stddev) f16 from base_seed + index, GroupNorm weights 1 + N(0, stddev));
+ * MIT2CFM_SYNTH_BIGVGAN, the vocoder's 783 tensors (weight_v and biases
+ * N(0, stddev) f16; weight_g = g (1 + N(0, stddev)) with g = 1 for conv_pre
+ * and the upsamplers, 0.1 for conv_post, 0.6 for the resblock convs; the
+ * 12-tap Kaiser-sinc filters and SnakeBeta's log alpha / log beta N(0, 0.1)
+ * in f32).  Tensors are sorted by name.  No reference counterpart: the
+ * reference's tests use its real weights; these give every run the same
+ * random-init model. */
+#define MIT2CFM_SYNTH_ESTIMATOR 0
+#define MIT2CFM_SYNTH_LENGTH_REGULATOR 1
+#define MIT2CFM_SYNTH_BIGVGAN 2
+uint32_t mit2cfm_synthetic_set_count(int32_t set);
+mit2cfm_status mit2cfm_synthetic_set_info(int32_t set, uint32_t i, const char** name, uint32_t* ndim,
+                                          int64_t* shape4, int32_t* dtype, uint64_t* elems);
+mit2cfm_status mit2cfm_synthetic_set_fill(int32_t set, uint32_t i, uint64_t base_seed, float stddev,
+                                          void* out);
+/* A context with every synthetic set: estimator (base_seed), length
+ * regulator (base_seed + 1), vocoder (base_seed + 2). */
+mit2cfm_status mit2cfm_create_synthetic_acoustic(uint64_t base_seed, float stddev, int32_t device,
+                                                 mit2cfm_ctx** out);
 /* Opens a bundle with the loader and applies every validation rule of the
  * format (replaces the --inspect-model-bundle gate, main.cpp; rules in
  * docs/native_bundle.md "Validation Rules"); verify_sha256 != 0 also checks

@@ -192,6 +192,41 @@ mit2cfm_status mit2cfm_create_synthetic(uint64_t base_seed, float stddev, int32_
   return make_ctx(ts, device, out);
 }
 
+namespace {
+const std::vector<mit2::SynthSpec>* synth_set(int32_t set) {
+  switch (set) {
+    case MIT2CFM_SYNTH_ESTIMATOR: return &mit2::estimator_tensor_specs();
+    case MIT2CFM_SYNTH_LENGTH_REGULATOR: return &mit2::length_regulator_tensor_specs();
+    case MIT2CFM_SYNTH_BIGVGAN: return &mit2::bigvgan_tensor_specs();
+    default: return nullptr;
+  }
+}
+std::vector<uint8_t> synth_set_bytes(int32_t set, size_t i, uint64_t base_seed, float stddev) {
+  if (set == MIT2CFM_SYNTH_ESTIMATOR) return mit2::synth_tensor_bytes(i, base_seed, stddev);
+  if (set == MIT2CFM_SYNTH_LENGTH_REGULATOR) return mit2::synth_lr_tensor_bytes(i, base_seed, stddev);
+  return mit2::synth_bigvgan_tensor_bytes(i, base_seed, stddev);
+}
+}  // namespace
+
+mit2cfm_status mit2cfm_create_synthetic_acoustic(uint64_t base_seed, float stddev, int32_t device,
+                                                 mit2cfm_ctx** out) {
+  std::vector<std::vector<uint8_t>> bufs;
+  std::vector<mit2hip::HostTensor> ts;
+  const mit2cfm_status st = guarded(nullptr, [&] {
+    for (int32_t set = MIT2CFM_SYNTH_ESTIMATOR; set <= MIT2CFM_SYNTH_BIGVGAN; ++set) {
+      const auto& specs = *synth_set(set);
+      bufs.reserve(bufs.size() + specs.size());
+      for (size_t i = 0; i < specs.size(); ++i) {
+        bufs.push_back(synth_set_bytes(set, i, base_seed + (uint64_t)set, stddev));
+        const bool f16 = specs[i].dtype == "f16";
+        ts.push_back({specs[i].name, bufs.back().data(), bufs.back().size() / (f16 ? 2 : 4), f16 ? 1 : 0});
+      }
+    }
+  });
+  if (st != MIT2CFM_OK) return st;
+  return make_ctx(ts, device, out);
+}
+
 void mit2cfm_destroy(mit2cfm_ctx* ctx) {
   if (!ctx) return;
   try {
@@ -422,6 +457,41 @@ mit2cfm_status mit2cfm_synthetic_tensor_fill(uint32_t i, uint64_t base_seed, flo
   if (!out) return fail(nullptr, MIT2CFM_E_ARG, "out must not be NULL");
   return guarded(nullptr, [&] {
     const auto b = mit2::synth_tensor_bytes(i, base_seed, stddev);
+    std::memcpy(out, b.data(), b.size());
+  });
+}
+
+
+uint32_t mit2cfm_synthetic_set_count(int32_t set) {
+  const auto* specs = synth_set(set);
+  return specs ? (uint32_t)specs->size() : 0u;
+}
+
+mit2cfm_status mit2cfm_synthetic_set_info(int32_t set, uint32_t i, const char** name, uint32_t* ndim,
+                                          int64_t* shape4, int32_t* dtype, uint64_t* elems) {
+  const auto* specs = synth_set(set);
+  if (!specs) return fail(nullptr, MIT2CFM_E_ARG, "unknown synthetic tensor set");
+  if (i >= specs->size()) return fail(nullptr, MIT2CFM_E_ARG, "tensor index out of range");
+  const auto& s = (*specs)[i];
+  if (name) *name = s.name.c_str();
+  if (ndim) *ndim = (uint32_t)s.shape.size();
+  uint64_t n = 1;
+  for (size_t d = 0; d < s.shape.size(); ++d) {
+    if (shape4 && d < 4) shape4[d] = s.shape[d];
+    n *= (uint64_t)s.shape[d];
+  }
+  if (dtype) *dtype = s.dtype == "f16" ? MIT2CFM_DTYPE_F16 : MIT2CFM_DTYPE_F32;
+  if (elems) *elems = n;
+  return MIT2CFM_OK;
+}
+
+mit2cfm_status mit2cfm_synthetic_set_fill(int32_t set, uint32_t i, uint64_t base_seed, float stddev,
+                                          void* out) {
+  if (!out) return fail(nullptr, MIT2CFM_E_ARG, "out must not be NULL");
+  const auto* specs = synth_set(set);
+  if (!specs) return fail(nullptr, MIT2CFM_E_ARG, "unknown synthetic tensor set");
+  return guarded(nullptr, [&] {
+    const auto b = synth_set_bytes(set, i, base_seed, stddev);
     std::memcpy(out, b.data(), b.size());
   });
 }

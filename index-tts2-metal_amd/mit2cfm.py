@@ -102,6 +102,12 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_bigvgan_stage_floats": (u64, [i32, i32, u32, i32]),
         "mit2cfm_acoustic_device": (st, [vp, vp, u32, vp, vp, u32, vp, u64, f32, u32, f32, vp, vp, _u32p,
                                          u32]),
+        "mit2cfm_synthetic_set_count": (u32, [i32]),
+        "mit2cfm_synthetic_set_info": (st, [i32, u32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(u32),
+                                            ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(i32),
+                                            ctypes.POINTER(u64)]),
+        "mit2cfm_synthetic_set_fill": (st, [i32, u32, u64, f32, vp]),
+        "mit2cfm_create_synthetic_acoustic": (st, [u64, f32, i32, ctypes.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -185,27 +191,47 @@ def generated_frames(codes: int) -> int:
     return int(lib().mit2cfm_generated_frames(codes))
 
 
+SYNTH_ESTIMATOR, SYNTH_LENGTH_REGULATOR, SYNTH_BIGVGAN = 0, 1, 2
+
+
+def synthetic_set_specs(set_id: int) -> list[tuple[str, tuple[int, ...], str]]:
+    """(name, shape, dtype) of every tensor of a synthetic set, sorted by name."""
+    L = lib()
+    specs = []
+    for i in range(L.mit2cfm_synthetic_set_count(set_id)):
+        name = ctypes.c_char_p()
+        ndim = ctypes.c_uint32()
+        shape = (ctypes.c_int64 * 4)()
+        dt = ctypes.c_int32()
+        n = ctypes.c_uint64()
+        _check(L.mit2cfm_synthetic_set_info(set_id, i, ctypes.byref(name), ctypes.byref(ndim), shape,
+                                            ctypes.byref(dt), ctypes.byref(n)))
+        specs.append((name.value.decode(), tuple(shape[d] for d in range(ndim.value)),
+                      "f16" if dt.value == DTYPE_F16 else "f32"))
+    return specs
+
+
+def synthetic_set(set_id: int, seed: int, stddev: float) -> dict[str, np.ndarray]:
+    """Every tensor of a synthetic set, generated by the library (one generator for
+    the C++ runtime, the tests and the bench)."""
+    L = lib()
+    out = {}
+    for i, (name, shape, dt) in enumerate(synthetic_set_specs(set_id)):
+        arr = np.empty(shape, np.float16 if dt == "f16" else np.float32)
+        _check(L.mit2cfm_synthetic_set_fill(set_id, i, seed, stddev, arr.ctypes.data_as(ctypes.c_void_p)))
+        out[name] = arr
+    return out
+
+
 def length_regulator_specs() -> list[tuple[str, tuple[int, ...]]]:
     """The s2mel length regulator's tensors (gpt.cpp:5271-5340), sorted by name."""
-    specs = [("content_in_proj.weight", (512, 1024)), ("content_in_proj.bias", (512,)),
-             ("model.12.weight", (512, 512, 1)), ("model.12.bias", (512,))]
-    for i in (0, 3, 6, 9):
-        specs += [(f"model.{i}.weight", (512, 512, 3)), (f"model.{i}.bias", (512,))]
-    for i in (1, 4, 7, 10):
-        specs += [(f"model.{i}.weight", (512,)), (f"model.{i}.bias", (512,))]
-    return sorted((LR_PREFIX + n, shape) for n, shape in specs)
+    return [(n, shape) for n, shape, _ in synthetic_set_specs(SYNTH_LENGTH_REGULATOR)]
 
 
 def synthetic_lr_tensors(seed: int = 20240606, stddev: float = 0.02) -> dict[str, np.ndarray]:
     """Length-regulator weights, f16: N(0, stddev) from seed + (index in sorted-name
     order); GroupNorm weights are 1 + N(0, stddev)."""
-    out = {}
-    for i, (name, shape) in enumerate(length_regulator_specs()):
-        n = int(np.prod(shape))
-        v = normal_noise(1, n, seed + i, stddev).reshape(shape)
-        gn_weight = name.endswith(".weight") and len(shape) == 1
-        out[name] = (v + 1.0 if gn_weight else v).astype(np.float16)
-    return out
+    return synthetic_set(SYNTH_LENGTH_REGULATOR, seed, stddev)
 
 
 # BigVGAN v2 (22 kHz, 80 bands, 256x) as the reference runs it
@@ -223,36 +249,14 @@ def bigvgan_specs() -> list[tuple[str, tuple[int, ...]]]:
     weight-normed (weight_g, weight_v); a transposed conv's weight_v is [in, out, kernel]
     and its weight_g [in, 1, 1]; each anti-aliased activation holds a 12-tap upsample
     and low-pass filter and SnakeBeta's log-scale alpha and beta."""
-    specs = []
-
-    def conv(prefix, rows, cols, k, bias=True):
-        specs.extend([(prefix + ".weight_g", (rows, 1, 1)), (prefix + ".weight_v", (rows, cols, k))])
-        if bias:
-            specs.append((prefix + ".bias", (cols if prefix.startswith("bigvgan.ups") else rows,)))
-
-    def act(prefix, c):
-        specs.extend([(prefix + ".upsample.filter", (1, 1, 12)),
-                      (prefix + ".downsample.lowpass.filter", (1, 1, 12)),
-                      (prefix + ".act.alpha", (c,)), (prefix + ".act.beta", (c,))])
-
-    conv("bigvgan.conv_pre", 1536, 80, 7)
-    for prefix, cin, cout, k, _, _ in BIGVGAN_UPSAMPLERS:
-        conv(prefix, cin, cout, k)
-    for prefix, c, k in BIGVGAN_RESBLOCKS:
-        for p in range(3):
-            conv(f"{prefix}.convs1.{p}", c, c, k)
-            conv(f"{prefix}.convs2.{p}", c, c, k)
-        for a in range(6):
-            act(f"{prefix}.activations.{a}", c)
-    act("bigvgan.activation_post", 24)
-    conv("bigvgan.conv_post", 1, 24, 7, bias=False)
-    return sorted(specs)
+    return [(n, shape) for n, shape, _ in synthetic_set_specs(SYNTH_BIGVGAN)]
 
 
 def kaiser_sinc_filter(kernel: int = 12, cutoff: float = 0.25, half_width: float = 0.3) -> np.ndarray:
     """The anti-aliasing filter of BigVGAN's alias-free activation for ratio 2: a
     Kaiser-windowed sinc low-pass, normalised to unit DC gain (Kaiser's
-    empirical beta for the attenuation A = 2.285 (N/2 - 1) pi (4 half_width) + 7.95)."""
+    empirical beta for the attenuation A = 2.285 (N/2 - 1) pi (4 half_width) + 7.95).
+    numpy's own restatement, against which the library's filter is checked."""
     half = kernel // 2
     a = 2.285 * (half - 1) * np.pi * (4 * half_width) + 7.95
     if a > 50.0:
@@ -267,33 +271,14 @@ def kaiser_sinc_filter(kernel: int = 12, cutoff: float = 0.25, half_width: float
     return (f / f.sum()).astype(np.float32)
 
 
-def synthetic_bigvgan_tensors(seed: int = 20240607, stddev: float = 0.02,
-                              gain: float = 0.6) -> dict[str, np.ndarray]:
-    """Vocoder weights: weight_v and biases N(0, stddev) f16 from seed + (index in
-    sorted-name order); weight_g = gain * (1 + N(0, stddev)) for the resblock convs
-    (the per-row norm of the normalised weight, so the stack neither explodes nor
-    vanishes), 1 + N(0, stddev) for conv_pre and the upsamplers, 0.1 (1 + N(0,
-    stddev)) for conv_post; the filters are
-    the closed-form Kaiser-sinc filter (f32); SnakeBeta's log alpha and log beta are
-    N(0, 0.1) (f32)."""
-    filt = kaiser_sinc_filter()
-    out = {}
-    for i, (name, shape) in enumerate(bigvgan_specs()):
-        n = int(np.prod(shape))
-        if name.endswith(".filter"):
-            out[name] = filt.reshape(shape).copy()
-            continue
-        if name.endswith((".act.alpha", ".act.beta")):
-            out[name] = normal_noise(1, n, seed + i, 0.1).reshape(shape)
-            continue
-        v = normal_noise(1, n, seed + i, stddev).reshape(shape)
-        if name.endswith(".weight_g"):
-            g = 1.0 if name.startswith(("bigvgan.conv_pre", "bigvgan.ups")) else gain
-            if name.startswith("bigvgan.conv_post"):
-                g = 0.1  # keeps the waveform mostly inside the final clamp
-            v = g * (1.0 + v)
-        out[name] = v.astype(np.float16)
-    return out
+def synthetic_bigvgan_tensors(seed: int = 20240607, stddev: float = 0.02) -> dict[str, np.ndarray]:
+    """Vocoder weights from the library's generator: weight_v and biases N(0, stddev)
+    f16 from seed + (index in sorted-name order); weight_g = g (1 + N(0, stddev)) with
+    g = 0.6 for the resblock convs (the per-row norm of the normalised weight, so the
+    stack neither explodes nor vanishes), 1 for conv_pre and the upsamplers, 0.1 for
+    conv_post; the filters the Kaiser-sinc low-pass (f32); SnakeBeta's log alpha and
+    log beta N(0, 0.1) (f32)."""
+    return synthetic_set(SYNTH_BIGVGAN, seed, stddev)
 
 
 def bigvgan_flops(tokens: int) -> float:

@@ -25,8 +25,10 @@ HipContext::HipContext(const Bundle& bundle, int device) {
   check(mit2cfm_create(ts.data(), (uint32_t)ts.size(), device, &ctx_), nullptr);
 }
 
-HipContext::HipContext(uint64_t synthetic_seed, float stddev, int device) {
-  check(mit2cfm_create_synthetic(synthetic_seed, stddev, device, &ctx_), nullptr);
+HipContext::HipContext(uint64_t synthetic_seed, float stddev, int device, bool acoustic) {
+  check(acoustic ? mit2cfm_create_synthetic_acoustic(synthetic_seed, stddev, device, &ctx_)
+                 : mit2cfm_create_synthetic(synthetic_seed, stddev, device, &ctx_),
+        nullptr);
 }
 
 HipContext::~HipContext() { mit2cfm_destroy(ctx_); }
@@ -79,6 +81,20 @@ std::vector<float> run_length_regulator_full_hip(HipContext& hip, const Bundle& 
   check(mit2cfm_length_regulator(hip.get(), input.data(), in_tokens, out_tokens, out.data()),
         hip.get());
   return out;
+}
+
+std::vector<float> run_bigvgan_vocoder_hip(HipContext& hip, const std::vector<float>& mel,
+                                           uint32_t tokens) {
+  if (tokens == 0 || mel.size() != (size_t)tokens * 80)
+    throw std::runtime_error("run_bigvgan_vocoder_hip: mel must have shape [tokens,80]");
+  std::vector<float> wav((size_t)tokens * 256);
+  check(mit2cfm_bigvgan(hip.get(), mel.data(), tokens, wav.data()), hip.get());
+  return wav;
+}
+
+std::vector<float> run_bigvgan_vocoder_hip(HipContext& hip, const Bundle& /*bundle*/,
+                                           const std::vector<float>& mel, uint32_t tokens) {
+  return run_bigvgan_vocoder_hip(hip, mel, tokens);
 }
 
 uint32_t cfm_synthesis_steps() {

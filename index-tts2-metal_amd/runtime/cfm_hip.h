@@ -21,8 +21,9 @@ class HipContext {
   // Uploads the estimator tensors of `bundle` (and the length regulator's,
   // when the bundle holds them) to GPU `device`.
   explicit HipContext(const Bundle& bundle, int device = 0);
-  // Seeded synthetic weights (N(0, stddev) f16; stddev 0 = fan-in scaled).
-  HipContext(uint64_t synthetic_seed, float stddev, int device = 0);
+  // Seeded synthetic weights (N(0, stddev) f16; stddev 0 = fan-in scaled);
+  // with acoustic, also the length regulator's and the vocoder's.
+  HipContext(uint64_t synthetic_seed, float stddev, int device = 0, bool acoustic = false);
   ~HipContext();
   HipContext(const HipContext&) = delete;
   HipContext& operator=(const HipContext&) = delete;
@@ -55,6 +56,15 @@ std::vector<float> run_dit_estimator_step_hip(HipContext& hip, const std::vector
 std::vector<float> run_length_regulator_full_hip(HipContext& hip, const Bundle& bundle,
                                                  const std::vector<float>& input,
                                                  uint32_t in_tokens, uint32_t out_tokens);
+
+// run_bigvgan_vocoder_metal (runtime/impl/dit_cfm_bigvgan.cpp:4196): mel
+// [tokens][80] -> waveform [256 * tokens] in [-1, 1].  The context needs the
+// bundle's "bigvgan.*" tensors.
+std::vector<float> run_bigvgan_vocoder_hip(HipContext& hip, const Bundle& bundle,
+                                           const std::vector<float>& mel, uint32_t tokens);
+// Same without a bundle argument (weights already resident in the context).
+std::vector<float> run_bigvgan_vocoder_hip(HipContext& hip, const std::vector<float>& mel,
+                                           uint32_t tokens);
 
 // Euler step count for synthesis: env MIT2_CFM_STEPS, default 16, clamped to
 // the --cfm_steps range 12..25 (main.cpp:57-88, :3181-3187).

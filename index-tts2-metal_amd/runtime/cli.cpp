@@ -7,6 +7,9 @@
 //   --decode MODEL T P [--cfm_steps N] [--cfg R] [--seed S] [--out FILE]
 //   --cfm_steps N                       (12..25, main.cpp:3181-3187)
 //   --inspect-model-bundle DIR, --write-synthetic-bundle DIR [SEED] [STDDEV]
+//   --bench-bigvgan MODEL T ITERS       (main.cpp:2931, run_bench_bigvgan
+//                                        dit_cfm_bigvgan.cpp:4225)
+//   --test-bigvgan-vocoder MODEL        (one mel frame, :4469)
 // MODEL is a bundle path or "synthetic[:SEED[:STDDEV]]".  The reference's
 // --test-cfm-* compare its Metal path with its CPU path; here the CPU
 // comparison lives in the test suite (the library never links the CPU
@@ -31,7 +34,7 @@ namespace {
 
 using Clock = std::chrono::steady_clock;
 
-std::unique_ptr<mit2::HipContext> open_model(const std::string& model) {
+std::unique_ptr<mit2::HipContext> open_model(const std::string& model, bool acoustic = false) {
   if (model.rfind("synthetic", 0) == 0) {
     uint64_t seed = 20240605;
     float stddev = 0.02f;
@@ -41,7 +44,7 @@ std::unique_ptr<mit2::HipContext> open_model(const std::string& model) {
       seed = std::stoull(model.substr(c1 + 1, c2 == std::string::npos ? std::string::npos : c2 - c1 - 1));
       if (c2 != std::string::npos) stddev = std::stof(model.substr(c2 + 1));
     }
-    return std::make_unique<mit2::HipContext>(seed, stddev, 0);
+    return std::make_unique<mit2::HipContext>(seed, stddev, 0, acoustic);
   }
   mit2::Bundle b(model);
   return std::make_unique<mit2::HipContext>(b, 0);
@@ -76,6 +79,52 @@ int bench_cfm(const std::string& model, uint32_t tokens, uint32_t steps, uint32_
             << ",\n  \"ms_per_step\": " << total / iters / steps * 1000.0
             << ",\n  \"frames_per_second\": " << tokens / (total / iters) << "\n}\n";
   return 0;
+}
+
+// The reference's vocoder bench input (dit_cfm_bigvgan.cpp:4228-4231).
+std::vector<float> bigvgan_bench_mel(uint32_t tokens) {
+  std::vector<float> mel((size_t)tokens * 80);
+  for (size_t i = 0; i < mel.size(); ++i)
+    mel[i] = std::sin((float)i * 0.017f) * 0.35f + std::cos((float)(i % 97) * 0.013f) * 0.12f;
+  return mel;
+}
+
+int bench_bigvgan(const std::string& model, uint32_t tokens, uint32_t iters) {
+  auto hip = open_model(model, true);
+  const auto mel = bigvgan_bench_mel(tokens);
+  (void)mit2::run_bigvgan_vocoder_hip(*hip, mel, tokens);
+  size_t samples = 0;
+  const auto t0 = Clock::now();
+  for (uint32_t i = 0; i < iters; ++i) samples = mit2::run_bigvgan_vocoder_hip(*hip, mel, tokens).size();
+  const double total = std::chrono::duration<double>(Clock::now() - t0).count();
+  std::cout << "{\n  \"stage\": \"bench_bigvgan\",\n  \"tokens\": " << tokens << ",\n  \"samples\": " << samples
+            << ",\n  \"iters\": " << iters << ",\n  \"seconds_per_call\": " << total / iters
+            << ",\n  \"rtf_vocoder_only\": " << (total / iters) / ((double)samples / 22050.0) << "\n}\n";
+  return 0;
+}
+
+// Vocoder invariants on run_bigvgan_vocoder_test's input (one mel frame,
+// dit_cfm_bigvgan.cpp:4469-4490): finite, inside the clamp, repeatable.  The
+// comparison with the CPU path lives in the test suite.
+int test_bigvgan_vocoder(const std::string& model) {
+  auto hip = open_model(model, true);
+  const uint32_t tokens = 1;
+  std::vector<float> mel(80);
+  for (size_t i = 0; i < mel.size(); ++i)
+    mel[i] = std::sin((float)i * 0.017f) * 0.10f + std::cos((float)(i % 71) * 0.029f) * 0.025f;
+  const auto a = mit2::run_bigvgan_vocoder_hip(*hip, mel, tokens);
+  const auto b = mit2::run_bigvgan_vocoder_hip(*hip, mel, tokens);
+  size_t nonfinite = 0;
+  float peak = 0.0f, repeat_err = 0.0f;
+  for (size_t i = 0; i < a.size(); ++i) {
+    if (!std::isfinite(a[i])) ++nonfinite;
+    peak = std::max(peak, std::fabs(a[i]));
+    repeat_err = std::max(repeat_err, std::fabs(a[i] - b[i]));
+  }
+  std::cout << "{\n  \"stage\": \"bigvgan_vocoder\",\n  \"input_tokens\": " << tokens << ",\n  \"samples\": "
+            << a.size() << ",\n  \"nonfinite\": " << nonfinite << ",\n  \"peak_abs\": " << peak
+            << ",\n  \"repeat_max_abs_error\": " << repeat_err << "\n}\n";
+  return (nonfinite == 0 && peak <= 1.0f && repeat_err == 0.0f && a.size() == 256) ? 0 : 1;
 }
 
 int test_cfm_euler(const std::string& model, const char* stage, uint32_t steps, float cfg) {
@@ -130,7 +179,8 @@ int usage() {
   std::cerr << "usage: mtts-cfm --bench-cfm MODEL T STEPS ITERS | --test-cfm-euler MODEL |\n"
                "       --test-cfm-euler-cfg MODEL | --decode MODEL T P [--cfm_steps N] [--cfg R]\n"
                "       [--seed S] [--out FILE] | --inspect-model-bundle DIR |\n"
-               "       --write-synthetic-bundle DIR [SEED] [STDDEV]\n"
+               "       --write-synthetic-bundle DIR [SEED] [STDDEV] |\n"
+               "       --bench-bigvgan MODEL T ITERS | --test-bigvgan-vocoder MODEL\n"
                "MODEL: bundle path or synthetic[:SEED[:STDDEV]]\n";
   return 2;
 }
@@ -166,6 +216,9 @@ int main(int argc, char** argv) {
         return bench_cfm(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]),
                          (uint32_t)std::stoul(argv[i + 4]));
       if (a == "--test-cfm-euler" && i + 1 < argc) return test_cfm_euler(argv[i + 1], "cfm_euler", 3, 0.0f);
+      if (a == "--bench-bigvgan" && i + 3 < argc)
+        return bench_bigvgan(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]));
+      if (a == "--test-bigvgan-vocoder" && i + 1 < argc) return test_bigvgan_vocoder(argv[i + 1]);
       if (a == "--test-cfm-euler-cfg" && i + 1 < argc)
         return test_cfm_euler(argv[i + 1], "cfm_euler_cfg", 25, 0.5f);
       if (a == "--decode" && i + 3 < argc)
@@ -175,7 +228,8 @@ int main(int argc, char** argv) {
         uint64_t n = 0, bytes = 0;
         const mit2cfm_status st = mit2cfm_inspect_bundle(argv[i + 1], &n, &bytes, 1);
         std::cout << "{\"ok\": " << (st == MIT2CFM_OK ? "true" : "false") << ", \"tensors\": " << n
-                  << ", \"payload_bytes\": " << bytes << ", \"sha256_verified\": " << (st == MIT2CFM_OK)
+                  << ", \"payload_bytes\": " << bytes
+                  << ", \"sha256_verified\": " << (st == MIT2CFM_OK ? "true" : "false")
                   << ", \"error\": \"" << (st == MIT2CFM_OK ? "" : mit2cfm_last_error(nullptr)) << "\"}\n";
         return st == MIT2CFM_OK ? 0 : 1;
       }

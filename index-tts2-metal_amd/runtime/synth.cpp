@@ -153,4 +153,146 @@ std::vector<uint8_t> synth_tensor_bytes(size_t i, uint64_t base_seed, float stdd
   return out;
 }
 
+namespace {
+
+size_t elems_of(const SynthSpec& s) {
+  size_t n = 1;
+  for (int64_t d : s.shape) n *= (size_t)d;
+  return n;
+}
+
+bool ends_with(const std::string& s, const char* suffix) {
+  const size_t n = std::strlen(suffix);
+  return s.size() >= n && s.compare(s.size() - n, n, suffix) == 0;
+}
+
+std::vector<uint8_t> to_f16_bytes(const std::vector<float>& v) {
+  std::vector<uint8_t> out(v.size() * 2);
+  for (size_t k = 0; k < v.size(); ++k) {
+    const _Float16 h = (_Float16)v[k];
+    std::memcpy(&out[k * 2], &h, 2);
+  }
+  return out;
+}
+
+std::vector<uint8_t> to_f32_bytes(const std::vector<float>& v) {
+  std::vector<uint8_t> out(v.size() * 4);
+  std::memcpy(out.data(), v.data(), out.size());
+  return out;
+}
+
+void sort_specs(std::vector<SynthSpec>& v) {
+  std::sort(v.begin(), v.end(), [](const SynthSpec& a, const SynthSpec& b) { return a.name < b.name; });
+}
+
+}  // namespace
+
+const std::vector<SynthSpec>& length_regulator_tensor_specs() {
+  static const std::vector<SynthSpec> specs = [] {
+    std::vector<SynthSpec> v;
+    const std::string p = "s2mel.net.length_regulator.";
+    v.push_back({p + "content_in_proj.weight", {512, 1024}, "f16"});
+    v.push_back({p + "content_in_proj.bias", {512}, "f16"});
+    v.push_back({p + "model.12.weight", {512, 512, 1}, "f16"});
+    v.push_back({p + "model.12.bias", {512}, "f16"});
+    for (int i : {0, 3, 6, 9}) {
+      v.push_back({p + "model." + std::to_string(i) + ".weight", {512, 512, 3}, "f16"});
+      v.push_back({p + "model." + std::to_string(i) + ".bias", {512}, "f16"});
+    }
+    for (int i : {1, 4, 7, 10}) {
+      v.push_back({p + "model." + std::to_string(i) + ".weight", {512}, "f16"});
+      v.push_back({p + "model." + std::to_string(i) + ".bias", {512}, "f16"});
+    }
+    sort_specs(v);
+    return v;
+  }();
+  return specs;
+}
+
+std::vector<uint8_t> synth_lr_tensor_bytes(size_t i, uint64_t base_seed, float stddev) {
+  const auto& specs = length_regulator_tensor_specs();
+  if (i >= specs.size()) throw std::out_of_range("synthetic tensor index");
+  const SynthSpec& s = specs[i];
+  auto v = make_deterministic_normal_noise((uint32_t)elems_of(s), 1, base_seed + i, stddev);
+  if (ends_with(s.name, ".weight") && s.shape.size() == 1)  // GroupNorm weight
+    for (float& x : v) x = x + 1.0f;
+  return to_f16_bytes(v);
+}
+
+const std::vector<SynthSpec>& bigvgan_tensor_specs() {
+  static const std::vector<SynthSpec> specs = [] {
+    std::vector<SynthSpec> v;
+    auto conv = [&](const std::string& p, int64_t rows, int64_t cols, int64_t k, bool bias, int64_t nb) {
+      v.push_back({p + ".weight_g", {rows, 1, 1}, "f16"});
+      v.push_back({p + ".weight_v", {rows, cols, k}, "f16"});
+      if (bias) v.push_back({p + ".bias", {nb}, "f16"});
+    };
+    auto act = [&](const std::string& p, int64_t c) {
+      v.push_back({p + ".upsample.filter", {1, 1, 12}, "f32"});
+      v.push_back({p + ".downsample.lowpass.filter", {1, 1, 12}, "f32"});
+      v.push_back({p + ".act.alpha", {c}, "f32"});
+      v.push_back({p + ".act.beta", {c}, "f32"});
+    };
+    conv("bigvgan.conv_pre", 1536, 80, 7, true, 1536);
+    const int64_t ups[6][4] = {{1536, 768, 8, 0}, {768, 384, 8, 1}, {384, 192, 4, 2},
+                               {192, 96, 4, 3},   {96, 48, 4, 4},   {48, 24, 4, 5}};
+    for (const auto& u : ups)
+      conv("bigvgan.ups." + std::to_string(u[3]) + ".0", u[0], u[1], u[2], true, u[1]);
+    for (int j = 0; j < 18; ++j) {
+      const int64_t c = 768 >> (j / 3), k = (j % 3 == 0) ? 3 : (j % 3 == 1) ? 7 : 11;
+      const std::string p = "bigvgan.resblocks." + std::to_string(j);
+      for (int pr = 0; pr < 3; ++pr) {
+        conv(p + ".convs1." + std::to_string(pr), c, c, k, true, c);
+        conv(p + ".convs2." + std::to_string(pr), c, c, k, true, c);
+      }
+      for (int a = 0; a < 6; ++a) act(p + ".activations." + std::to_string(a), c);
+    }
+    act("bigvgan.activation_post", 24);
+    conv("bigvgan.conv_post", 1, 24, 7, false, 0);
+    sort_specs(v);
+    return v;
+  }();
+  return specs;
+}
+
+std::vector<float> kaiser_sinc_filter12() {
+  constexpr int kTaps = 12, kHalf = 6;
+  const double cutoff = 0.25, half_width = 0.3, pi = 3.14159265358979323846;
+  // Kaiser's empirical beta for attenuation A = 2.285 (N/2 - 1) pi (4 half_width) + 7.95.
+  const double a = 2.285 * (kHalf - 1) * pi * (4.0 * half_width) + 7.95;
+  const double beta = a > 50.0 ? 0.1102 * (a - 8.7)
+                               : (a >= 21.0 ? 0.5842 * std::pow(a - 21.0, 0.4) + 0.07886 * (a - 21.0) : 0.0);
+  const double centre = (kTaps - 1) / 2.0;
+  double f[kTaps], sum = 0.0;
+  for (int n = 0; n < kTaps; ++n) {
+    const double r = (n - centre) / centre;
+    const double window = std::cyl_bessel_i(0.0, beta * std::sqrt(1.0 - r * r)) / std::cyl_bessel_i(0.0, beta);
+    const double x = 2.0 * cutoff * (n - kHalf + 0.5);
+    const double sinc = x == 0.0 ? 1.0 : std::sin(pi * x) / (pi * x);
+    f[n] = 2.0 * cutoff * window * sinc;
+    sum += f[n];
+  }
+  std::vector<float> out(kTaps);
+  for (int n = 0; n < kTaps; ++n) out[n] = (float)(f[n] / sum);
+  return out;
+}
+
+std::vector<uint8_t> synth_bigvgan_tensor_bytes(size_t i, uint64_t base_seed, float stddev) {
+  const auto& specs = bigvgan_tensor_specs();
+  if (i >= specs.size()) throw std::out_of_range("synthetic tensor index");
+  const SynthSpec& s = specs[i];
+  const uint32_t n = (uint32_t)elems_of(s);
+  if (ends_with(s.name, ".filter")) return to_f32_bytes(kaiser_sinc_filter12());
+  if (ends_with(s.name, ".act.alpha") || ends_with(s.name, ".act.beta"))
+    return to_f32_bytes(make_deterministic_normal_noise(n, 1, base_seed + i, 0.1f));
+  auto v = make_deterministic_normal_noise(n, 1, base_seed + i, stddev);
+  if (ends_with(s.name, ".weight_g")) {
+    float g = 0.6f;
+    if (s.name.rfind("bigvgan.conv_pre", 0) == 0 || s.name.rfind("bigvgan.ups", 0) == 0) g = 1.0f;
+    if (s.name.rfind("bigvgan.conv_post", 0) == 0) g = 0.1f;
+    for (float& x : v) x = g * (1.0f + x);
+  }
+  return to_f16_bytes(v);
+}
+
 }  // namespace mit2

@@ -34,4 +34,25 @@ const std::vector<SynthSpec>& estimator_tensor_specs();
 // other vectors N(0, 0.02)).
 std::vector<uint8_t> synth_tensor_bytes(size_t i, uint64_t base_seed, float stddev);
 
+// The s2mel length regulator's 20 tensors (prefix s2mel.net.length_regulator.),
+// sorted by name, all f16: N(0, stddev) from base_seed + i; the GroupNorm
+// weights are 1 + N(0, stddev).
+const std::vector<SynthSpec>& length_regulator_tensor_specs();
+std::vector<uint8_t> synth_lr_tensor_bytes(size_t i, uint64_t base_seed, float stddev);
+
+// The BigVGAN vocoder's 783 tensors (prefix bigvgan.), sorted by name.
+// weight_v and biases N(0, stddev) f16 from base_seed + i; weight_g =
+// g (1 + N(0, stddev)) f16 with g = 1 for conv_pre and the upsamplers, 0.1
+// for conv_post and 0.6 for the resblock convs (so the residual stack
+// neither grows nor vanishes and the waveform stays inside the clamp); the
+// activations' filters are the 12-tap Kaiser-windowed sinc low-pass of the
+// alias-free activation (f32); SnakeBeta's log alpha and log beta are
+// N(0, 0.1) (f32).
+const std::vector<SynthSpec>& bigvgan_tensor_specs();
+std::vector<uint8_t> synth_bigvgan_tensor_bytes(size_t i, uint64_t base_seed, float stddev);
+
+// Kaiser-windowed sinc low-pass (cutoff 0.25, half-width 0.3, 12 taps, unit
+// DC gain): the filter of BigVGAN's alias-free activation for ratio 2.
+std::vector<float> kaiser_sinc_filter12();
+
 }  // namespace mit2

@@ -98,6 +98,15 @@ def test_kaiser_sinc_filter_is_a_half_band_lowpass(mit2):
     assert 0.35 < h < 0.65
 
 
+def test_library_filter_matches_numpy_kaiser(mit2, bv_tensors):
+    """The library's synthetic filter (C++, std::cyl_bessel_i) equals numpy's
+    np.kaiser-based restatement, and the synthetic sets are well formed."""
+    lib_f = bv_tensors["bigvgan.resblocks.0.activations.0.upsample.filter"].reshape(-1)
+    np.testing.assert_allclose(lib_f, mit2.kaiser_sinc_filter(), rtol=0, atol=2e-8)
+    assert len(mit2.synthetic_set_specs(mit2.SYNTH_ESTIMATOR)) == len(mit2.synthetic_tensor_specs())
+    assert len(mit2.synthetic_set_specs(mit2.SYNTH_LENGTH_REGULATOR)) == 20
+
+
 def _torch_vocoder(T, mel):
     """Upstream BigVGAN forward in float64 from torch operators: conv_pre, then per
     stage a transposed-conv upsampler and the mean of three AMP resblocks, then the
