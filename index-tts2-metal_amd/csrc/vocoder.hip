@@ -69,8 +69,9 @@ struct ActFilters {
 // up[2j] (j = 0..5).  A lane owns one channel and R consecutive tokens; its
 // x window (tokens t0-6 .. t0+R+5, clamped) and the 2R+10 Z values its
 // outputs need stay in registers, so each Z is computed once and nothing
-// goes through LDS.  The 64 lanes of a wave take 64 consecutive channels of
-// the same tokens (coalesced row segments).
+// goes through LDS.  Lanes are (run, channel) pairs in channel-fastest
+// order, so a wave reads whole row segments and no lane idles when C is not
+// a multiple of 64 (the 24- and 48-channel stages).
 constexpr int kActR = 16;
 
 template <bool OUT16>
@@ -81,13 +82,11 @@ __global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__
   constexpr int R = kActR;
   constexpr int XW = R + 12;      // x window
   constexpr int ZW = 2 * R + 10;  // Z window: u = 2 t0 - 5 + i
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int groups = (C + 63) >> 6;
-  const int run = wave / groups;
-  const int c = (wave - run * groups) * 64 + lane;
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  const int run = (int)(g / C);
+  const int c = (int)(g - (long)run * C);
   const int t0 = run * R;
-  if (t0 >= T || c >= C) return;
+  if (t0 >= T) return;
   float xw[XW];
 #pragma unroll
   for (int i = 0; i < XW; ++i) {
@@ -362,8 +361,8 @@ struct Vocoder::Impl {
   }
 
   void activation(const Act& a, const float* in, int T, void* out, bool out16) {
-    const size_t waves = (size_t)((T + kActR - 1) / kActR) * ((a.C + 63) / 64);
-    const dim3 grid((unsigned)((waves + 3) / 4));
+    const size_t lanes = (size_t)((T + kActR - 1) / kActR) * a.C;
+    const dim3 grid((unsigned)((lanes + 255) / 256));
     if (out16)
       hipLaunchKernelGGL(snake_aa_kernel<true>, grid, dim3(256), 0, s, in, a.filt, a.alpha, a.inv_beta,
                          T, a.C, out);
