@@ -32,6 +32,10 @@ Prints ONE JSON line.  Extra fields:
                 stream, output samples/s, algorithmic conv TFLOP/s, and the
                 oracle on the host cores over a bounded sample (two mel
                 frames).
+  context_create_s
+                creating the context from the host tensors (f16 -> weight
+                preparation -> upload) and from a device image of the same
+                prepared weights (mit2cfm_create_from_image).
   acoustic_stage
                 the whole acoustic stage of one synthesis segment on the GPU
                 (mit2cfm_acoustic_device: condition, seeded noise, CFG decode,
@@ -191,7 +195,19 @@ def main():
     tensors = mit2cfm.synthetic_tensors(20240605, 0.02)
     lr_tensors = mit2cfm.synthetic_lr_tensors(20240606, 0.02)
     bv_tensors = mit2cfm.synthetic_bigvgan_tensors(20240607) if a.voc_calls else {}
+    c0 = time.perf_counter()
     ctx = mit2cfm.Context({**tensors, **lr_tensors, **bv_tensors}, device=0)
+    create_s = time.perf_counter() - c0
+    # Context creation from the device image of the same weights (no host-side
+    # weight preparation): written once, then timed.
+    import tempfile
+    with tempfile.TemporaryDirectory() as td:
+        img = os.path.join(td, "model.mit2hip")
+        ctx.write_image(img)
+        c0 = time.perf_counter()
+        mit2cfm.Context(image=img, device=0).close()
+        create_img_s = time.perf_counter() - c0
+        img_mb = os.path.getsize(img) / 2**20
 
     x0 = mit2cfm.normal_noise(T, 80, 1)
     cond = mit2cfm.normal_noise(T, 512, 2)
@@ -407,6 +423,8 @@ def main():
         result["vocoder"] = voc
     if ac:
         result["acoustic_stage"] = ac
+    result["context_create_s"] = {"from_host_tensors": round(create_s, 3), "from_device_image": round(create_img_s, 3),
+                                  "image_mib": round(img_mb, 1)}
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(tensors, T, P, S, cfg, cpu_threads(a))
     print(json.dumps(result), flush=True)

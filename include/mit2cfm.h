@@ -205,6 +205,19 @@ mit2cfm_status mit2cfm_synthetic_tensor_info(uint32_t i, const char** name, uint
 /* Payload of tensor i (elems * 2 bytes for f16, * 4 for f32) into out. */
 mit2cfm_status mit2cfm_synthetic_tensor_fill(uint32_t i, uint64_t base_seed, float stddev,
                                              void* out);
+/* ---- device weight image ------------------------------------------------
+ * The offline weight preparation the reference's design notes call for
+ * (docs/model.md:93: weight norm folded into the bundle, conv taps
+ * transposed once; the reference does both at every upload,
+ * metal_context.mm:5056-5075, gpt.cpp:5109-5130): mit2cfm_write_image saves
+ * a context's prepared device weights (weight norm folded, products folded,
+ * rows permuted, taps laid out, f16) with their layout; mit2cfm_create_from_image
+ * creates a context by copying them to the device, with no host-side
+ * preparation.  The image is specific to this library's ABI version; a
+ * malformed, truncated or foreign file is MIT2CFM_E_MODEL. */
+mit2cfm_status mit2cfm_write_image(mit2cfm_ctx* ctx, const char* path);
+mit2cfm_status mit2cfm_create_from_image(const char* path, int32_t device, mit2cfm_ctx** out);
+
 /* Synthetic tensor sets beyond the estimator (the functions above are set 0):
  * MIT2CFM_SYNTH_LENGTH_REGULATOR, the s2mel length regulator's 20 tensors
  * (N(0, stddev) f16 from base_seed + index, GroupNorm weights 1 + N(0, stddev));

@@ -227,6 +227,34 @@ mit2cfm_status mit2cfm_create_synthetic_acoustic(uint64_t base_seed, float stdde
   return make_ctx(ts, device, out);
 }
 
+mit2cfm_status mit2cfm_write_image(mit2cfm_ctx* ctx, const char* path) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(path != nullptr, "path must not be NULL");
+    ctx->eng->write_image(path);
+  });
+}
+
+mit2cfm_status mit2cfm_create_from_image(const char* path, int32_t device, mit2cfm_ctx** out) {
+  if (!path || !out) return fail(nullptr, MIT2CFM_E_ARG, "path/out must not be NULL");
+  *out = nullptr;
+  auto* c = new mit2cfm_ctx();
+  const mit2cfm_status st = guarded(nullptr, [&] {
+    int n = 0;
+    hip_check(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (device < 0 || device >= n)
+      throw mit2hip::HipError("HIP device " + std::to_string(device) + " not available (" +
+                              std::to_string(n) + " devices)");
+    c->eng = std::make_unique<mit2hip::Engine>(std::string(path), device);
+  });
+  if (st != MIT2CFM_OK) {
+    delete c;
+    return st;
+  }
+  *out = c;
+  return MIT2CFM_OK;
+}
+
 void mit2cfm_destroy(mit2cfm_ctx* ctx) {
   if (!ctx) return;
   try {

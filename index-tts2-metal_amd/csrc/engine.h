@@ -39,6 +39,9 @@ class Arena {
   void* take(size_t bytes);
   size_t used() const { return used_; }
   size_t capacity() const { return cap_; }
+  char* base() const { return base_; }
+  // Makes the first `bytes` bytes taken (for an arena filled by a bulk copy).
+  void set_used(size_t bytes) { used_ = bytes; }
 
  private:
   char* base_ = nullptr;
@@ -67,7 +70,15 @@ struct TableBufs {
 class Engine {
  public:
   Engine(const std::vector<HostTensor>& tensors, int device);
+  // From a device image written by write_image: the prepared weights (weight
+  // norm folded, rows permuted, taps laid out, f16) are copied to the device
+  // as they are, with no host-side preparation.
+  Engine(const std::string& image_path, int device);
   ~Engine();
+
+  // Writes the prepared device weights (the decoder's, and the length
+  // regulator's and vocoder's when present) to an image file.
+  void write_image(const std::string& path) const;
 
   int device() const { return device_; }
   hipStream_t stream() const { return stream_; }

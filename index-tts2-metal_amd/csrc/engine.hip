@@ -20,10 +20,13 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
+#include <type_traits>
 #include <unordered_map>
 
 #include "condition.h"
 #include "gemm.h"
+#include "image_io.h"
 #include "rowops.h"
 #include "vocoder.h"
 
@@ -111,6 +114,73 @@ struct Weights {
 };
 
 namespace {
+
+// Every device array of Weights with its element count, in a fixed order
+// (the device image stores their arena offsets in this order).  Arrays a
+// model lacks (the length regulator's, the skip-in of layers 0..6) are null.
+template <typename F>
+void visit_weights(Weights& W, F&& f) {
+  for (int i = 0; i < 2; ++i) {
+    f(W.te_freqs[i], 128);
+    f(W.te_w0[i], 512 * 256);
+    f(W.te_b0[i], 512);
+    f(W.te_w2[i], 512 * 512);
+    f(W.te_b2[i], 512);
+  }
+  f(W.proj_w, (size_t)27 * 1024 * 512);
+  f(W.proj_b, 27 * 1024);
+  f(W.ada_w, 1024 * 512);
+  f(W.ada_b, 1024);
+  f(W.wnc_w, (size_t)8192 * 512);
+  f(W.wnc_b, 8192);
+  for (auto& g : W.gamma) f(g, 512);
+  f(W.cp_w, 512 * 512);
+  f(W.cp_b, 512);
+  f(W.mx_w, 512 * kMelPad);
+  f(W.mc_w, 512 * kMcWidth);
+  f(W.mc_b, 512);
+  for (int l = 0; l < 13; ++l) {
+    f(W.qkv_w[l], 1536 * 512);
+    f(W.wo_w[l], 512 * 512);
+    f(W.w13_w[l], 3072 * 512);
+    f(W.w2_w[l], 512 * 1536);
+    f(W.si_w[l], 512 * 1024);
+    f(W.si_b[l], 512);
+  }
+  f(W.sl_w, 512 * (512 + kMelPad));
+  f(W.sl_b, 512);
+  f(W.post_w, 1024 * (512 + kMelPad));
+  f(W.post_b, 1024);
+  for (int l = 0; l < 8; ++l) {
+    f(W.in_w[l], 1024 * 2560);
+    f(W.in_b[l], 1024);
+    f(W.rs_w[l], (l < 7 ? 1024 : 512) * 512);
+    f(W.rs_b[l], l < 7 ? 1024 : 512);
+  }
+  f(W.fin_w, 512 * 512);
+  f(W.fin_b, 512);
+  f(W.c2_w, 80 * 512);
+  f(W.c2_b, 80);
+  f(W.c2f_w, 80 * 512);
+  f(W.c2f_b, 80);
+  f(W.lr_proj_w, 512 * 1024);
+  f(W.lr_proj_b, 512);
+  for (int b = 0; b < 4; ++b) {
+    f(W.lr_conv_w[b], 512 * 1536);
+    f(W.lr_conv_b[b], 512);
+    f(W.lr_gn_w[b], 512);
+    f(W.lr_gn_b[b], 512);
+  }
+  f(W.lr_out_w, 512 * 512);
+  f(W.lr_out_b, 512);
+}
+
+// Device image layout: "MIT2HIPI", u32 version, u32 has_vocoder, u64 payload
+// bytes, u64 payload checksum, then the payload: the decoder section (u64
+// arena bytes, u8 has_lr, u64 offset per visit_weights array, the arena
+// bytes) and, when present, the vocoder section (Vocoder::append_image).
+constexpr char kImageMagic[8] = {'M', 'I', 'T', '2', 'H', 'I', 'P', 'I'};
+constexpr uint32_t kImageVersion = 1;
 
 struct HostModel {
   std::unordered_map<std::string, std::vector<float>> t;
@@ -485,6 +555,90 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
 
   if (Vocoder::present(hm.t)) voc_ = std::make_unique<Vocoder>(hm.t, stream_);
   ws_ = std::make_unique<Workspace>();
+}
+
+void Engine::write_image(const std::string& path) const {
+  HIP_OK(hipSetDevice(device_));
+  HIP_OK(hipStreamSynchronize(stream_));
+  std::vector<uint8_t> payload;
+  ImageWriter w{payload};
+  Weights& W = *w_;
+  const char* base = W.arena.base();
+  const size_t used = W.arena.used();
+  w.put<uint64_t>(used);
+  w.put<uint8_t>(W.has_lr ? 1 : 0);
+  visit_weights(W, [&](auto* p, size_t) { w.put<uint64_t>(arena_offset(p, base)); });
+  std::vector<uint8_t> host(used);
+  HIP_OK(hipMemcpy(host.data(), base, used, hipMemcpyDeviceToHost));
+  w.bytes(host.data(), used);
+  if (voc_) voc_->append_image(payload);
+  std::vector<uint8_t> head;
+  ImageWriter h{head};
+  h.bytes(kImageMagic, 8);
+  h.put<uint32_t>(kImageVersion);
+  h.put<uint32_t>(voc_ ? 1u : 0u);
+  h.put<uint64_t>(payload.size());
+  h.put<uint64_t>(image_checksum(payload.data(), payload.size()));
+  std::ofstream f(path, std::ios::binary | std::ios::trunc);
+  if (!f) throw std::invalid_argument("device image: cannot write " + path);
+  f.write(reinterpret_cast<const char*>(head.data()), (std::streamsize)head.size());
+  f.write(reinterpret_cast<const char*>(payload.data()), (std::streamsize)payload.size());
+  if (!f) throw std::runtime_error("device image: write failed: " + path);
+}
+
+Engine::Engine(const std::string& image_path, int device) : device_(device) {
+  std::ifstream f(image_path, std::ios::binary | std::ios::ate);
+  if (!f) throw std::runtime_error("device image: cannot open " + image_path);
+  const size_t total = (size_t)f.tellg();
+  f.seekg(0);
+  std::vector<uint8_t> file(total);
+  if (!f.read(reinterpret_cast<char*>(file.data()), (std::streamsize)total))
+    throw std::runtime_error("device image: cannot read " + image_path);
+  ImageReader h{file.data(), file.size()};
+  if (std::memcmp(h.bytes(8), kImageMagic, 8) != 0) throw std::runtime_error("device image: bad magic");
+  if (h.get<uint32_t>() != kImageVersion) throw std::runtime_error("device image: unsupported version");
+  const uint32_t has_voc = h.get<uint32_t>();
+  const uint64_t plen = h.get<uint64_t>();
+  const uint64_t sum = h.get<uint64_t>();
+  const uint8_t* payload = h.bytes(plen);
+  if (h.at != file.size()) throw std::runtime_error("device image: trailing bytes");
+  if (image_checksum(payload, plen) != sum) throw std::runtime_error("device image: checksum mismatch");
+
+  HIP_OK(hipSetDevice(device_));
+  HIP_OK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  try {
+    if (const char* g = std::getenv("MIT2CFM_GRAPH")) use_graph_ = std::atoi(g) != 0;
+    ImageReader r{payload, plen};
+    w_ = std::make_unique<Weights>();
+    Weights& W = *w_;
+    const uint64_t used = r.get<uint64_t>();
+    if (used == 0 || used > (uint64_t(8) << 30)) throw std::runtime_error("device image: bad arena size");
+    W.has_lr = r.get<uint8_t>() != 0;
+    W.arena.reserve(used);
+    W.arena.set_used(used);
+    char* base = W.arena.base();
+    visit_weights(W, [&](auto*& p, size_t n) {
+      using T = std::remove_pointer_t<std::remove_reference_t<decltype(p)>>;
+      const uint64_t off = r.get<uint64_t>();
+      p = off == UINT64_MAX ? nullptr : arena_span<T>(off, n, base, used);
+    });
+    // Arrays every decode reads must be present; the length regulator's all or none.
+    bool ok = W.proj_w && W.wnc_w && W.cp_w && W.mc_w && W.sl_w && W.post_w && W.c2f_w;
+    for (int l = 0; l < 13; ++l) ok = ok && W.qkv_w[l] && W.w13_w[l] && W.w2_w[l] && (l <= 6 || W.si_w[l]);
+    for (int l = 0; l < 8; ++l) ok = ok && W.in_w[l] && W.rs_w[l];
+    ok = ok && (!W.has_lr || (W.lr_proj_w && W.lr_out_w && W.lr_conv_w[3] && W.lr_gn_b[3]));
+    if (!ok) throw std::runtime_error("device image: missing decoder arrays");
+    HIP_OK(hipMemcpy(base, r.bytes(used), used, hipMemcpyHostToDevice));
+    if (has_voc) voc_ = std::make_unique<Vocoder>(payload + r.at, plen - r.at, stream_);
+    else if (r.at != plen) throw std::runtime_error("device image: trailing bytes");
+    ws_ = std::make_unique<Workspace>();
+  } catch (...) {
+    voc_.reset();
+    w_.reset();
+    (void)hipStreamDestroy(stream_);
+    stream_ = nullptr;
+    throw;
+  }
 }
 
 Engine::~Engine() {

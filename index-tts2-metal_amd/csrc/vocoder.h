@@ -22,6 +22,10 @@ class Vocoder {
   // Tensors named "bigvgan.*" (fp32 on the host, any layout the checkpoint
   // has); throws std::invalid_argument when one is missing or misshaped.
   Vocoder(const std::unordered_map<std::string, std::vector<float>>& t, hipStream_t stream);
+  // From the vocoder section of a device image (see append_image).
+  Vocoder(const uint8_t* image, size_t bytes, hipStream_t stream);
+  // Appends the prepared weights (arena bytes and layout) to an image.
+  void append_image(std::vector<uint8_t>& out) const;
   ~Vocoder();
   Vocoder(const Vocoder&) = delete;
   Vocoder& operator=(const Vocoder&) = delete;
@@ -49,9 +53,11 @@ class Vocoder {
   static size_t stage_out_floats(int stage, int index, int tokens);
   static size_t stage_in_floats(int stage, int index, int tokens);
 
- private:
-  struct Conv;
+ public:
+  struct Conv;  // (defined in vocoder.hip)
   struct Act;
+
+ private:
   struct Impl;
   Impl* d_;
 };

@@ -20,12 +20,14 @@
 //    tokens in registers, so each upsampled value is computed once.
 #include "vocoder.h"
 
+#include <array>
 #include <cmath>
 #include <cstring>
 #include <stdexcept>
 
 #include "engine.h"
 #include "gemm.h"
+#include "image_io.h"
 
 namespace mit2hip {
 
@@ -454,6 +456,106 @@ Vocoder::Vocoder(const std::unordered_map<std::string, std::vector<float>>& t, h
     d.zero = static_cast<half_t*>(d.wa.take(2048 * 2));
     VOC_OK(hipMemset(d.zero, 0, 2048 * 2));
     d.bytes = d.wa.used();
+  } catch (...) {
+    delete d_;
+    throw;
+  }
+}
+
+// Image section: arena bytes used, then every conv (weight and bias offsets,
+// N, stored columns, K, input channels, taps) and activation (filters,
+// alpha and 1/beta offsets, channels) in construction order, conv_post and
+// the zero buffer's offsets, then the arena bytes.
+namespace {
+template <typename F>
+void visit_convs(Vocoder::Conv& pre, Vocoder::Conv (&ups)[6], Vocoder::Conv (&rb)[18][3][2], F&& f) {
+  f(pre);
+  for (auto& c : ups) f(c);
+  for (auto& j : rb)
+    for (auto& pr : j)
+      for (auto& c : pr) f(c);
+}
+}  // namespace
+
+void Vocoder::append_image(std::vector<uint8_t>& out) const {
+  Impl& d = *d_;
+  ImageWriter w{out};
+  const char* base = d.wa.base();
+  const size_t used = d.wa.used();
+  w.put<uint64_t>(used);
+  visit_convs(d.pre, d.ups, d.rb, [&](Conv& c) {
+    w.put<uint64_t>(arena_offset(c.w, base));
+    w.put<uint64_t>(arena_offset(c.b, base));
+    w.put<int32_t>(c.N);
+    w.put<int32_t>(c.n_out);
+    w.put<int32_t>(c.K);
+    w.put<int32_t>(c.cin);
+    w.put<int32_t>(c.k);
+  });
+  auto put_act = [&](const Act& a) {
+    w.put(a.filt);
+    w.put<uint64_t>(arena_offset(a.alpha, base));
+    w.put<uint64_t>(arena_offset(a.inv_beta, base));
+    w.put<int32_t>(a.C);
+  };
+  for (auto& j : d.act)
+    for (auto& a : j) put_act(a);
+  put_act(d.act_post);
+  w.put<uint64_t>(arena_offset(d.post_w, base));
+  w.put<uint64_t>(arena_offset(d.zero, base));
+  std::vector<uint8_t> host(used);
+  VOC_OK(hipMemcpy(host.data(), base, used, hipMemcpyDeviceToHost));
+  w.bytes(host.data(), used);
+}
+
+Vocoder::Vocoder(const uint8_t* image, size_t bytes, hipStream_t stream) : d_(new Impl) {
+  Impl& d = *d_;
+  d.s = stream;
+  try {
+    ImageReader r{image, bytes};
+    const uint64_t used = r.get<uint64_t>();
+    if (used == 0 || used > (uint64_t(8) << 30)) throw std::runtime_error("device image: bad vocoder arena size");
+    d.wa.reserve(used);
+    d.wa.set_used(used);
+    char* base = d.wa.base();
+    // The architecture fixes every conv's shape: (stored outputs, inputs, taps)
+    // in visit order; the image must agree before any kernel trusts it.
+    std::vector<std::array<int, 3>> shapes;
+    shapes.push_back({1536, 80, 7});
+    for (const UpsSpec& u : kUps) shapes.push_back({u.stride * u.cout, u.cin, 3});
+    for (int j = 0; j < 18; ++j)
+      for (int n = 0; n < 6; ++n) shapes.push_back({rb_channels(j), rb_channels(j), kRbKernel[j % 3]});
+    size_t ci = 0;
+    visit_convs(d.pre, d.ups, d.rb, [&](Conv& c) {
+      const uint64_t wo = r.get<uint64_t>(), bo = r.get<uint64_t>();
+      c.N = r.get<int32_t>();
+      c.n_out = r.get<int32_t>();
+      c.K = r.get<int32_t>();
+      c.cin = r.get<int32_t>();
+      c.k = r.get<int32_t>();
+      const auto& e = shapes[ci++];
+      if (c.n_out != e[0] || c.cin != e[1] || c.k != e[2] || c.N != round_up(e[0], 32) ||
+          c.K != round_up(e[2] * e[1], 64))
+        throw std::runtime_error("device image: vocoder conv shape differs from the model");
+      c.w = arena_span<half_t>(wo, (size_t)c.N * c.K, base, used);
+      c.b = arena_span<float>(bo, (size_t)c.N, base, used);
+    });
+    auto get_act = [&](Act& a, int C) {
+      a.filt = r.get<ActFilters>();
+      const uint64_t ao = r.get<uint64_t>(), bo = r.get<uint64_t>();
+      a.C = r.get<int32_t>();
+      if (a.C != C) throw std::runtime_error("device image: vocoder activation width differs from the model");
+      a.alpha = arena_span<float>(ao, (size_t)C, base, used);
+      a.inv_beta = arena_span<float>(bo, (size_t)C, base, used);
+    };
+    for (int j = 0; j < 18; ++j)
+      for (auto& a : d.act[j]) get_act(a, rb_channels(j));
+    get_act(d.act_post, 24);
+    d.post_w = arena_span<float>(r.get<uint64_t>(), 24 * 7, base, used);
+    d.zero = arena_span<half_t>(r.get<uint64_t>(), 2048, base, used);
+    VOC_OK(hipMemcpy(base, r.bytes(used), used, hipMemcpyHostToDevice));
+    if (r.at != bytes) throw std::runtime_error("device image: trailing bytes in the vocoder section");
+    d.bytes = used;
   } catch (...) {
     delete d_;
     throw;

@@ -108,6 +108,8 @@ def lib() -> ctypes.CDLL:
                                             ctypes.POINTER(u64)]),
         "mit2cfm_synthetic_set_fill": (st, [i32, u32, u64, f32, vp]),
         "mit2cfm_create_synthetic_acoustic": (st, [u64, f32, i32, ctypes.POINTER(vp)]),
+        "mit2cfm_write_image": (st, [vp, ctypes.c_char_p]),
+        "mit2cfm_create_from_image": (st, [ctypes.c_char_p, i32, ctypes.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -313,14 +315,21 @@ def inspect_bundle(path: str | os.PathLike, verify_sha256: bool = False) -> tupl
 class Context:
     """One GPU context with resident weights (mit2cfm_ctx)."""
 
-    def __init__(self, tensors: dict[str, np.ndarray] | None = None, *, bundle=None,
-                 synthetic_seed: int | None = None, stddev: float = 0.02, device: int = 0):
+    def __init__(self, tensors: dict[str, np.ndarray] | None = None, *, bundle=None, image=None,
+                 synthetic_seed: int | None = None, stddev: float = 0.02, acoustic: bool = False,
+                 device: int = 0):
+        """From a tensor dict, an MIT2 bundle directory, a device image
+        (write_image), or the library's synthetic weights (acoustic: also the
+        length regulator's and the vocoder's, seeds synthetic_seed + 1, + 2)."""
         L = lib()
         handle = ctypes.c_void_p()
         if bundle is not None:
             _check(L.mit2cfm_create_from_bundle(str(bundle).encode(), device, ctypes.byref(handle)))
+        elif image is not None:
+            _check(L.mit2cfm_create_from_image(str(image).encode(), device, ctypes.byref(handle)))
         elif synthetic_seed is not None:
-            _check(L.mit2cfm_create_synthetic(synthetic_seed, stddev, device, ctypes.byref(handle)))
+            create = L.mit2cfm_create_synthetic_acoustic if acoustic else L.mit2cfm_create_synthetic
+            _check(create(synthetic_seed, stddev, device, ctypes.byref(handle)))
         else:
             if tensors is None:
                 raise ValueError("need tensors, bundle or synthetic_seed")
@@ -337,6 +346,10 @@ class Context:
                 arr[i] = _Tensor(name.encode(), a.ctypes.data, a.size, dt)
             _check(L.mit2cfm_create(arr, len(tensors), device, ctypes.byref(handle)))
         self._h = handle
+
+    def write_image(self, path) -> None:
+        """Saves the prepared device weights to a device image file."""
+        self._c(lib().mit2cfm_write_image(self._h, str(path).encode()))
 
     # -- lifetime
     def close(self) -> None:

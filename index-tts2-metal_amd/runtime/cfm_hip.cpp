@@ -31,6 +31,10 @@ HipContext::HipContext(uint64_t synthetic_seed, float stddev, int device, bool a
         nullptr);
 }
 
+HipContext::HipContext(const std::string& image_path, int device) {
+  check(mit2cfm_create_from_image(image_path.c_str(), device, &ctx_), nullptr);
+}
+
 HipContext::~HipContext() { mit2cfm_destroy(ctx_); }
 
 std::vector<float> run_cfm_euler_hip(HipContext& hip, std::vector<float> x,

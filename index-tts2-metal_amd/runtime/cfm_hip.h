@@ -24,6 +24,8 @@ class HipContext {
   // Seeded synthetic weights (N(0, stddev) f16; stddev 0 = fan-in scaled);
   // with acoustic, also the length regulator's and the vocoder's.
   HipContext(uint64_t synthetic_seed, float stddev, int device = 0, bool acoustic = false);
+  // From a device image (mit2cfm_write_image): prepared weights, no host-side preparation.
+  HipContext(const std::string& image_path, int device);
   ~HipContext();
   HipContext(const HipContext&) = delete;
   HipContext& operator=(const HipContext&) = delete;

@@ -10,7 +10,9 @@
 //   --bench-bigvgan MODEL T ITERS       (main.cpp:2931, run_bench_bigvgan
 //                                        dit_cfm_bigvgan.cpp:4225)
 //   --test-bigvgan-vocoder MODEL        (one mel frame, :4469)
-// MODEL is a bundle path or "synthetic[:SEED[:STDDEV]]".  The reference's
+//   --write-image MODEL FILE            (the prepared device weights)
+// MODEL is a bundle path, "synthetic[:SEED[:STDDEV]]" or "image:FILE" (a
+// device image written by --write-image).  The reference's
 // --test-cfm-* compare its Metal path with its CPU path; here the CPU
 // comparison lives in the test suite (the library never links the CPU
 // restatement), so these harnesses check the invariants the reference's
@@ -35,6 +37,7 @@ namespace {
 using Clock = std::chrono::steady_clock;
 
 std::unique_ptr<mit2::HipContext> open_model(const std::string& model, bool acoustic = false) {
+  if (model.rfind("image:", 0) == 0) return std::make_unique<mit2::HipContext>(model.substr(6), 0);
   if (model.rfind("synthetic", 0) == 0) {
     uint64_t seed = 20240605;
     float stddev = 0.02f;
@@ -180,8 +183,9 @@ int usage() {
                "       --test-cfm-euler-cfg MODEL | --decode MODEL T P [--cfm_steps N] [--cfg R]\n"
                "       [--seed S] [--out FILE] | --inspect-model-bundle DIR |\n"
                "       --write-synthetic-bundle DIR [SEED] [STDDEV] |\n"
-               "       --bench-bigvgan MODEL T ITERS | --test-bigvgan-vocoder MODEL\n"
-               "MODEL: bundle path or synthetic[:SEED[:STDDEV]]\n";
+               "       --bench-bigvgan MODEL T ITERS | --test-bigvgan-vocoder MODEL |\n"
+               "       --write-image MODEL FILE\n"
+               "MODEL: bundle path, synthetic[:SEED[:STDDEV]] or image:FILE\n";
   return 2;
 }
 
@@ -216,6 +220,12 @@ int main(int argc, char** argv) {
         return bench_cfm(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]),
                          (uint32_t)std::stoul(argv[i + 4]));
       if (a == "--test-cfm-euler" && i + 1 < argc) return test_cfm_euler(argv[i + 1], "cfm_euler", 3, 0.0f);
+      if (a == "--write-image" && i + 2 < argc) {
+        auto hip = open_model(argv[i + 1], true);
+        const mit2cfm_status st = mit2cfm_write_image(hip->get(), argv[i + 2]);
+        if (st != MIT2CFM_OK) std::cerr << mit2cfm_last_error(hip->get()) << "\n";
+        return st == MIT2CFM_OK ? 0 : 1;
+      }
       if (a == "--bench-bigvgan" && i + 3 < argc)
         return bench_bigvgan(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]));
       if (a == "--test-bigvgan-vocoder" && i + 1 < argc) return test_bigvgan_vocoder(argv[i + 1]);

@@ -58,6 +58,17 @@ def test_decode_and_invariant_harnesses(cli):
 
 
 @pytest.mark.gpu
+def test_image_roundtrip_through_the_cli(cli, tmp_path):
+    img = tmp_path / "m.mit2hip"
+    r = _run(cli, "--write-image", "synthetic", str(img))
+    assert r.returncode == 0, r.stderr
+    a = _run(cli, "--test-bigvgan-vocoder", "synthetic")
+    b = _run(cli, "--test-bigvgan-vocoder", f"image:{img}")
+    assert a.returncode == 0 and b.returncode == 0, a.stderr + b.stderr
+    assert json.loads(a.stdout)["peak_abs"] == json.loads(b.stdout)["peak_abs"]
+
+
+@pytest.mark.gpu
 def test_vocoder_harnesses(cli):
     r = _run(cli, "--test-bigvgan-vocoder", "synthetic")
     assert r.returncode == 0, r.stdout + r.stderr
