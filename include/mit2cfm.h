@@ -225,12 +225,16 @@ mit2cfm_status mit2cfm_create_from_image(const char* path, int32_t device, mit2c
  * N(0, stddev) f16; weight_g = g (1 + N(0, stddev)) with g = 1 for conv_pre
  * and the upsamplers, 0.1 for conv_post, 0.6 for the resblock convs; the
  * 12-tap Kaiser-sinc filters and SnakeBeta's log alpha / log beta N(0, 0.1)
- * in f32).  Tensors are sorted by name.  No reference counterpart: the
- * reference's tests use its real weights; these give every run the same
- * random-init model. */
+ * in f32); MIT2CFM_SYNTH_GPT, the GPT decoder's 296 tensors (24 layers,
+ * ln_f, final_norm, mel_head, the mel and mel-position embeddings; Conv1D
+ * weights [in][out]; N(0, stddev) f16, LayerNorm weights 1 + N(0, stddev)).
+ * Tensors are sorted by name.  No reference counterpart: the reference's
+ * tests use its real weights; these give every run the same random-init
+ * model. */
 #define MIT2CFM_SYNTH_ESTIMATOR 0
 #define MIT2CFM_SYNTH_LENGTH_REGULATOR 1
 #define MIT2CFM_SYNTH_BIGVGAN 2
+#define MIT2CFM_SYNTH_GPT 3
 uint32_t mit2cfm_synthetic_set_count(int32_t set);
 mit2cfm_status mit2cfm_synthetic_set_info(int32_t set, uint32_t i, const char** name, uint32_t* ndim,
                                           int64_t* shape4, int32_t* dtype, uint64_t* elems);
@@ -340,6 +344,60 @@ mit2cfm_status mit2cfm_acoustic_device(mit2cfm_ctx* ctx, const float* s_infer, u
                                        float noise_temperature, uint32_t steps, float cfg_rate,
                                        float* wav_out, float* mel_out, uint32_t* generated_out,
                                        uint32_t flags);
+
+/* ---- GPT mel-code decoder (the producer of the semantic codes) -------------
+ * These need the GPT decoder's tensors in the context's weight table:
+ * "gpt.gpt.h.<l>.{ln_1,attn.c_attn,attn.c_proj,ln_2,mlp.c_fc,mlp.c_proj}.*"
+ * for l = 0..L-1 (the checkpoint has L = 24; Conv1D weights [in][out]),
+ * "gpt.gpt.ln_f.*", "gpt.final_norm.*", "gpt.mel_head.*",
+ * "gpt.mel_embedding.weight" [8194][1280] and
+ * "gpt.mel_pos_embedding.emb.weight" [1818][1280]; without them they return
+ * MIT2CFM_E_MODEL.  Weights are f16 on the device (the checkpoint's own
+ * precision), activations and the key/value caches fp32. */
+
+/* Layers of the context's GPT decoder (0 when it has none). */
+mit2cfm_status mit2cfm_gpt_layers(mit2cfm_ctx* ctx, uint32_t* layers);
+
+/* Replaces run_gpt_kv_greedy_metal (runtime/impl/gpt.cpp:1914; CPU
+ * definition run_gpt_kv_greedy_cpu :1877): prefill the key/value caches
+ * from prefix [prefix_tokens][1280] (the conditioning + text embeddings),
+ * then greedy-decode up to `steps` mel codes from the start token 8192,
+ * stopping at the first stop token 8193.  Positions follow
+ * gpt_cached_generate_position (:1873): step s uses position s, or s + 1 for
+ * s > 0 when hf_generate_positions is nonzero; a `steps` whose last position
+ * passes the 1818-row table is MIT2CFM_E_ARG (the reference throws when it
+ * gets there).  Outputs (host): predicted_tokens [steps] and *n_predicted
+ * (the stop token included), input_tokens [steps + 1] and *n_input (the start
+ * token, then every non-stop prediction), *first_stop_step (-1: none),
+ * last_logits [8194] (the last step's logits; may be NULL), timings_ms [2]
+ * (device time of the prefill and of the decode loop; may be NULL).  Host
+ * pointers, synchronous. */
+mit2cfm_status mit2cfm_gpt_kv_greedy(mit2cfm_ctx* ctx, const float* prefix, uint32_t prefix_tokens,
+                                     uint32_t steps, int32_t hf_generate_positions,
+                                     uint32_t* predicted_tokens, uint32_t* n_predicted,
+                                     uint32_t* input_tokens, uint32_t* n_input, int32_t* first_stop_step,
+                                     float* last_logits, double* timings_ms);
+
+/* Replaces run_gpt_cached_decode_metal (runtime/impl/gpt.cpp:1427; CPU
+ * definition run_gpt_cached_decode_cpu :1400): rows [prefix_tokens + 1][1280];
+ * the first prefix_tokens rows fill the key/value caches, the last row is
+ * decoded against them.  Outputs (host, each may be NULL): ln_f [1280],
+ * final_norm [1280], logits [8194], *argmax.  Synchronous. */
+mit2cfm_status mit2cfm_gpt_cached_decode(mit2cfm_ctx* ctx, const float* rows, uint32_t prefix_tokens,
+                                         float* ln_f, float* final_norm, float* logits, uint32_t* argmax);
+
+/* Measurement hook of the GPT decode step: enqueues `count` launches of one of
+ * its kernels (layer 0's weights) on the context's stream without waiting,
+ * for timing with events on mit2cfm_stream; count 0 launches nothing.
+ * Kernel ids: 0 c_attn GEMV (3840 x 1280, LayerNorm prologue, K/V written to
+ * the cache), 1 attention c_proj GEMV (1280 x 1280, + residual), 2 c_fc GEMV
+ * (5120 x 1280, LayerNorm prologue, gelu_new), 3 MLP c_proj GEMV
+ * (1280 x 5120, + residual), 4 mel_head GEMV (8194 x 1280, ln_f and
+ * final_norm prologue, argmax), 5 cached attention over 1024 keys.  Reports
+ * the kernel's algorithmic HBM bytes per launch and its name.  No reference
+ * counterpart. */
+mit2cfm_status mit2cfm_gpt_profile_launch(mit2cfm_ctx* ctx, int32_t kernel, uint32_t count,
+                                          double* bytes_per_launch, const char** name);
 
 #ifdef __cplusplus
 }

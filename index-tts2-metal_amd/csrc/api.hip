@@ -11,6 +11,7 @@
 #include "../runtime/bundle.h"
 #include "../runtime/synth.h"
 #include "engine.h"
+#include "gpt.h"
 #include "vocoder.h"
 
 struct mit2cfm_ctx {
@@ -151,6 +152,20 @@ mit2cfm_status mit2cfm_create(const mit2cfm_tensor* tensors, uint32_t count, int
   return make_ctx(ts, device, out);
 }
 
+namespace {
+// The bundle tensors a context uses: the DiT-CFM estimator, the length
+// regulator, the vocoder and the GPT decoder (not the GPT's conditioning
+// encoders, text embedding or emotion layers).
+bool wanted_bundle_tensor(const std::string& n) {
+  static const char* const prefixes[] = {"s2mel.net.cfm.estimator.", "s2mel.net.length_regulator.",
+                                         "bigvgan.", "gpt.gpt.h.", "gpt.gpt.ln_f.", "gpt.final_norm.",
+                                         "gpt.mel_head.", "gpt.mel_embedding.", "gpt.mel_pos_embedding."};
+  for (const char* p : prefixes)
+    if (n.rfind(p, 0) == 0) return true;
+  return false;
+}
+}  // namespace
+
 mit2cfm_status mit2cfm_create_from_bundle(const char* bundle_path, int32_t device,
                                           mit2cfm_ctx** out) {
   if (!bundle_path || !out) return fail(nullptr, MIT2CFM_E_ARG, "bundle_path/out must not be NULL");
@@ -159,9 +174,7 @@ mit2cfm_status mit2cfm_create_from_bundle(const char* bundle_path, int32_t devic
   if (st != MIT2CFM_OK) return st;
   std::vector<mit2hip::HostTensor> ts;
   for (const auto& info : b->tensors()) {
-    if (info.name.rfind("s2mel.net.cfm.estimator.", 0) != 0 &&
-        info.name.rfind("s2mel.net.length_regulator.", 0) != 0 && info.name.rfind("bigvgan.", 0) != 0)
-      continue;
+    if (!wanted_bundle_tensor(info.name)) continue;
     int dt;
     if (info.dtype == "f32")
       dt = 0;
@@ -198,12 +211,14 @@ const std::vector<mit2::SynthSpec>* synth_set(int32_t set) {
     case MIT2CFM_SYNTH_ESTIMATOR: return &mit2::estimator_tensor_specs();
     case MIT2CFM_SYNTH_LENGTH_REGULATOR: return &mit2::length_regulator_tensor_specs();
     case MIT2CFM_SYNTH_BIGVGAN: return &mit2::bigvgan_tensor_specs();
+    case MIT2CFM_SYNTH_GPT: return &mit2::gpt_tensor_specs();
     default: return nullptr;
   }
 }
 std::vector<uint8_t> synth_set_bytes(int32_t set, size_t i, uint64_t base_seed, float stddev) {
   if (set == MIT2CFM_SYNTH_ESTIMATOR) return mit2::synth_tensor_bytes(i, base_seed, stddev);
   if (set == MIT2CFM_SYNTH_LENGTH_REGULATOR) return mit2::synth_lr_tensor_bytes(i, base_seed, stddev);
+  if (set == MIT2CFM_SYNTH_GPT) return mit2::synth_gpt_tensor_bytes(i, base_seed, stddev);
   return mit2::synth_bigvgan_tensor_bytes(i, base_seed, stddev);
 }
 }  // namespace
@@ -666,5 +681,67 @@ mit2cfm_status mit2cfm_acoustic_device(mit2cfm_ctx* ctx, const float* s_infer, u
                                               (int)steps, cfg_rate, wav_out, mel_out);
     if (generated_out) *generated_out = (uint32_t)gen;
     if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}
+
+// ---- GPT mel-code decoder
+mit2cfm_status mit2cfm_gpt_layers(mit2cfm_ctx* ctx, uint32_t* layers) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(layers != nullptr, "layers must not be NULL");
+    *layers = ctx->eng->has_gpt() ? (uint32_t)ctx->eng->gpt().layers() : 0u;
+  });
+}
+
+mit2cfm_status mit2cfm_gpt_kv_greedy(mit2cfm_ctx* ctx, const float* prefix, uint32_t prefix_tokens,
+                                     uint32_t steps, int32_t hf_generate_positions,
+                                     uint32_t* predicted_tokens, uint32_t* n_predicted,
+                                     uint32_t* input_tokens, uint32_t* n_input, int32_t* first_stop_step,
+                                     float* last_logits, double* timings_ms) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(prefix_tokens == 0 || prefix != nullptr, "prefix must not be NULL");
+    require(prefix_tokens <= (1u << 16), "prefix_tokens must be <= 65536");
+    require(steps <= (uint32_t)mit2hip::GptDecoder::kPositions, "steps must be <= 1818");
+    require(steps == 0 || (predicted_tokens && n_predicted), "predicted_tokens/n_predicted must not be NULL");
+    require(input_tokens && n_input && first_stop_step, "input_tokens/n_input/first_stop_step must not be NULL");
+    mit2hip::GptDecoder::Greedy g;
+    ctx->eng->gpt().kv_greedy(prefix, (int)prefix_tokens, (int)steps, hf_generate_positions != 0, g);
+    if (n_predicted) *n_predicted = (uint32_t)g.predicted.size();
+    if (!g.predicted.empty()) std::memcpy(predicted_tokens, g.predicted.data(), g.predicted.size() * 4);
+    *n_input = (uint32_t)g.input_tokens.size();
+    std::memcpy(input_tokens, g.input_tokens.data(), g.input_tokens.size() * 4);
+    *first_stop_step = g.first_stop_step;
+    if (last_logits && !g.last_logits.empty())
+      std::memcpy(last_logits, g.last_logits.data(), g.last_logits.size() * sizeof(float));
+    if (timings_ms) {
+      timings_ms[0] = g.prefill_ms;
+      timings_ms[1] = g.decode_ms;
+    }
+  });
+}
+
+mit2cfm_status mit2cfm_gpt_cached_decode(mit2cfm_ctx* ctx, const float* rows, uint32_t prefix_tokens,
+                                         float* ln_f, float* final_norm, float* logits, uint32_t* argmax) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(rows != nullptr, "rows must not be NULL");
+    require(prefix_tokens < (1u << 16), "prefix_tokens must be < 65536");
+    const uint32_t a = ctx->eng->gpt().cached_decode(rows, (int)prefix_tokens, ln_f, final_norm, logits);
+    if (argmax) *argmax = a;
+  });
+}
+
+mit2cfm_status mit2cfm_gpt_profile_launch(mit2cfm_ctx* ctx, int32_t kernel, uint32_t count,
+                                          double* bytes_per_launch, const char** name) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(kernel >= 0 && kernel <= 5, "kernel must be 0..5");
+    require(count <= 100000, "count must be <= 100000");
+    double b = 0;
+    const char* nm = ctx->eng->gpt().profile_launch(kernel, 0, &b);
+    if (count) ctx->eng->gpt().profile_launch(kernel, (int)count, nullptr);
+    if (bytes_per_launch) *bytes_per_launch = b;
+    if (name) *name = nm;
   });
 }

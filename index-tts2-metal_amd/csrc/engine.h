@@ -52,6 +52,7 @@ class Arena {
 struct Weights;    // resident weights (engine.hip)
 struct Workspace;  // activations (engine.hip)
 class Vocoder;     // BigVGAN (vocoder.hip)
+class GptDecoder;  // GPT mel-code decoder (gpt.hip)
 
 // Device buffers of the timestep-conditioning tables for S step slots:
 // t values, their embeddings and MLP intermediates, the per-step table rows
@@ -176,6 +177,12 @@ class Engine {
                       uint64_t seed, float temperature, int steps, float cfg, float* wav,
                       float* mel);
 
+  // ---- GPT mel-code decoder (the producer of the semantic codes), present
+  // when the tensor table holds the "gpt.gpt.h.*" weights.  gpt() makes the
+  // context's device current and throws when the decoder is absent.
+  bool has_gpt() const { return gpt_ != nullptr; }
+  GptDecoder& gpt();
+
   // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
   void set_use_graph(bool on) { use_graph_ = on; }
   void sync();
@@ -201,6 +208,7 @@ class Engine {
   std::unique_ptr<Weights> w_;
   std::unique_ptr<Workspace> ws_;
   std::unique_ptr<Vocoder> voc_;
+  std::unique_ptr<GptDecoder> gpt_;
   float* voc_io_ = nullptr;  // host-path staging: mel, then wav
   size_t voc_io_floats_ = 0;
   // Acoustic-stage buffers (condition [T][512], x0 and mel [T][80]), grown on

@@ -26,6 +26,7 @@
 
 #include "condition.h"
 #include "gemm.h"
+#include "gpt.h"
 #include "image_io.h"
 #include "rowops.h"
 #include "vocoder.h"
@@ -554,6 +555,7 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
   }
 
   if (Vocoder::present(hm.t)) voc_ = std::make_unique<Vocoder>(hm.t, stream_);
+  if (GptDecoder::present(hm.t)) gpt_ = std::make_unique<GptDecoder>(hm.t, stream_);
   ws_ = std::make_unique<Workspace>();
 }
 
@@ -644,6 +646,7 @@ Engine::Engine(const std::string& image_path, int device) : device_(device) {
 Engine::~Engine() {
   clear_graphs();
   if (voc_io_) (void)hipFree(voc_io_);
+  gpt_.reset();
   voc_.reset();
   ws_.reset();
   w_.reset();
@@ -651,7 +654,13 @@ Engine::~Engine() {
 }
 
 size_t Engine::weight_bytes() const {
-  return w_->arena.used() + (voc_ ? voc_->weight_bytes() : 0);
+  return w_->arena.used() + (voc_ ? voc_->weight_bytes() : 0) + (gpt_ ? gpt_->weight_bytes() : 0);
+}
+
+GptDecoder& Engine::gpt() {
+  if (!gpt_) throw std::runtime_error("gpt: the context has no gpt.gpt.h.* tensors");
+  HIP_OK(hipSetDevice(device_));
+  return *gpt_;
 }
 
 void Engine::clear_graphs() {

@@ -1,0 +1,961 @@
+// gpt.hip -- GPT mel-code decoder on gfx950 (see gpt.h).
+//
+// Replaces run_gpt_kv_greedy_metal and its prefill / cached-attention passes
+// (runtime/impl/gpt.cpp:1914-2240, the "ICB greedy decode") and the Metal
+// kernels they record (fused f16-weight GEMV, LayerNorm, gelu, cached
+// attention, argmax).
+//
+// One decode step (one token) is:
+//   embed      x = mel_embedding[token] + mel_pos_embedding[position]
+//              (or a prefix row, while the prefix is prefilled)
+//   per layer  c_attn   qkv = W_attn LN1(x) + b; q -> q buffer, k and v -> the
+//                       caches at row kv (no copy: the cache IS the output)
+//              attention  softmax(q K^T / 8) V over the kv + 1 cached rows,
+//                       per head, split over chunks of 64 keys
+//              c_proj   x += W_proj att + b
+//              c_fc     f = gelu_new(W_fc LN2(x) + b)
+//              c_proj   x += W_mp f + b          (the last layer advances kv)
+//   head       logits = W_head LN_fn(LN_f(x)) + b, argmax, token bookkeeping
+//
+// Every matrix-vector product is HBM-bound: each weight is read once per
+// step (f16, 0.98 GB for 24 layers) and used for one multiply-add.  The GEMV
+// kernel loads the input vector, then streams whole rows into registers
+// (16-byte loads, a group of 32 or 64 lanes per row), computes the LayerNorm
+// of the input while the rows are in flight (each lane group holds the whole
+// vector and computes the statistics by itself, so no barrier or LDS is
+// needed), then reduces the row dot products across the lane group.  Everything the step needs (cache length, step, token,
+// stop flag) lives in a device state block, so a whole step is one replayed
+// HIP graph; the host only checks the stop flag every few steps.
+#include "gpt.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "device_common.h"
+#include "engine.h"
+
+namespace mit2hip {
+
+#define GPT_OK(expr)                                                                      \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess)                                                                 \
+      throw HipError(std::string(#expr) + " failed: " + hipGetErrorString(e_) + " (" +   \
+                     __FILE__ + ":" + std::to_string(__LINE__) + ")");                    \
+  } while (0)
+
+namespace {
+
+constexpr int kW = 1280, kQKV = 3840, kMLP = 5120, kHeads = 20, kHD = 64;
+constexpr int kVocab = GptDecoder::kVocab, kPos = GptDecoder::kPositions;
+constexpr int kStart = (int)GptDecoder::kStartToken, kStop = (int)GptDecoder::kStopToken;
+constexpr int kChunk = 128;   // keys per attention split
+constexpr int kPartF = 2 + kHD;  // per split: max, sum, unnormalised output
+constexpr int kStepsPerCheck = 8;  // decode steps replayed between stop-flag reads
+
+// Device-side decode state.
+struct GptState {
+  int32_t kv;         // rows in the key/value caches
+  int32_t step;       // decode steps taken
+  int32_t n_pred;     // predicted tokens written
+  int32_t n_in;       // input tokens written (the start token included)
+  int32_t stopped;    // 1 once the stop token was predicted
+  int32_t stop_step;  // step of the first stop token, else -1
+  int32_t cur_token;  // the last input token
+  int32_t hf;         // position rule: step s > 0 uses position s + 1
+  int32_t argmax;     // argmax of the last head launch
+  int32_t max_pred;   // capacity of the predicted array (inputs: + 1)
+  int32_t cap;        // rows of each key/value cache
+  int32_t rows;       // rows of the prefix buffer
+  int32_t pad[4];
+};
+
+enum { PRO_PLAIN = 0, PRO_LN = 1, PRO_LN2 = 2 };
+enum { EPI_GELU = 0, EPI_RES = 1, EPI_QKV = 2, EPI_LOGITS = 3 };
+
+struct GemvArgs {
+  const half_t* w = nullptr;  // [N][K] f16
+  const float* bias = nullptr;
+  int N = 0;
+  const float* x = nullptr;   // input vector [K]
+  const float* g1 = nullptr;  // LayerNorm of PRO_LN, the first of PRO_LN2
+  const float* b1 = nullptr;
+  const float* g2 = nullptr;  // the second LayerNorm of PRO_LN2
+  const float* b2 = nullptr;
+  float* y = nullptr;         // GELU: out; RES: residual stream (in place); LOGITS: logits
+  GptState* st = nullptr;
+  float* q = nullptr;         // QKV: query, key cache, value cache
+  float* kc = nullptr;
+  float* vc = nullptr;
+  int advance = 0;            // RES: block 0 advances st->kv
+  int check_stop = 1;         // LOGITS: skip the launch once stopped
+  float* blk_val = nullptr;   // LOGITS: per-block maxima and their rows
+  int* blk_idx = nullptr;
+  float* lnf_out = nullptr;   // LOGITS: block 0 writes the two LayerNorm outputs
+  float* fn_out = nullptr;
+};
+
+__device__ __forceinline__ float gelu_new(float v) {
+  // cpu_gelu_new (tokenizer_tests.cpp:3931-3945)
+  if (v > 10.0f) return v;
+  if (v < -10.0f) return 0.0f;
+  return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+}
+
+// Sum over the LPR lanes of a lane group (every lane gets the sum).
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// The 8-float chunks of a 1280-vector (or any vector a lane group spans) at
+// lane j's positions 8 (j + c LPR) .. +7.
+template <int LPR, int CH>
+__device__ __forceinline__ void load_chunks(float (&v)[CH][8], const float* src, int j) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const float4* p = reinterpret_cast<const float4*>(src + 8 * (j + c * LPR));
+    const float4 lo = p[0], hi = p[1];
+    v[c][0] = lo.x; v[c][1] = lo.y; v[c][2] = lo.z; v[c][3] = lo.w;
+    v[c][4] = hi.x; v[c][5] = hi.y; v[c][6] = hi.z; v[c][7] = hi.w;
+  }
+}
+
+// LayerNorm, in place, of the vector a lane group holds in the chunk layout,
+// as cpu_layernorm (tokenizer_tests.cpp:2992-3010): two passes, eps 1e-5;
+// g and b are the weight and bias at the same positions.
+template <int LPR, int CH>
+__device__ __forceinline__ void group_layernorm(float (&xv)[CH][8], const float (&g)[CH][8],
+                                                const float (&b)[CH][8]) {
+  constexpr float kInvN = 1.0f / (8 * LPR * CH);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += xv[c][e];
+  const float mean = group_sum<LPR>(s) * kInvN;
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = xv[c][e] - mean;
+      q += d * d;
+    }
+  const float inv = 1.0f / sqrtf(group_sum<LPR>(q) * kInvN + 1e-5f);
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv[c][e] = (xv[c][e] - mean) * inv * g[c][e] + b[c][e];
+}
+
+template <int LPR, int CH>
+__device__ __forceinline__ void store_chunks(const float (&xv)[CH][8], float* out, int j) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float4* o = reinterpret_cast<float4*>(out + 8 * (j + c * LPR));
+    o[0] = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
+    o[1] = make_float4(xv[c][4], xv[c][5], xv[c][6], xv[c][7]);
+  }
+}
+
+// y[r] = W[r] . pro(x) + b[r], then the epilogue.  A group of LPR lanes owns a
+// row; lane j of the group handles the 8-half chunks j, j + LPR, ... of it.
+// Each wave works on UR * 64 / LPR rows; a block has WAVES waves.  A
+// LayerNorm prologue normalises the input in registers (its length is the
+// lane group's span, 8 LPR CH).
+template <int K, int LPR, int WAVES, int UR, int PRO, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
+  constexpr int RPW = 64 / LPR;
+  constexpr int CH = K / (8 * LPR);
+  constexpr int ROWS = WAVES * RPW * UR;
+  static_assert(K % (8 * LPR) == 0, "K must be a multiple of 8 * LPR");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, j = lane % LPR;
+  if (EPI == EPI_LOGITS && a.check_stop && a.st->stopped) return;
+  const int rbase = blockIdx.x * ROWS + wave * RPW * UR;
+
+  // 1. the input vector at this lane's positions 8 (j + c LPR) + e (a lane
+  //    group covers the whole vector once) and the first LayerNorm's
+  //    weight and bias there.  Loaded first: loads complete in order, so the
+  //    LayerNorm below can then run while the weight rows are in flight.
+  float xv[CH][8];
+  load_chunks<LPR, CH>(xv, a.x, j);
+  float gv[PRO == PRO_PLAIN ? 1 : CH][8], bv[PRO == PRO_PLAIN ? 1 : CH][8];
+  if constexpr (PRO != PRO_PLAIN) {
+    load_chunks<LPR, CH>(gv, a.g1, j);
+    load_chunks<LPR, CH>(bv, a.b1, j);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. the weight rows (rows past N re-read row N - 1; their results are dropped)
+  half8 w[UR][CH];
+#pragma unroll
+  for (int u = 0; u < UR; ++u) {
+    const int r = min(rbase + u * RPW + sub, a.N - 1);
+    const half8* src = reinterpret_cast<const half8*>(a.w + (size_t)r * K) + j;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) w[u][c] = src[c * LPR];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // LayerNorm prologues (ln_1 / ln_2; ln_f then final_norm for the head).
+  if constexpr (PRO != PRO_PLAIN) {
+    group_layernorm<LPR, CH>(xv, gv, bv);
+    if constexpr (PRO == PRO_LN2) {
+      const bool out = blockIdx.x == 0 && wave == 0 && sub == 0 && a.lnf_out;
+      if (out) store_chunks<LPR, CH>(xv, a.lnf_out, j);
+      load_chunks<LPR, CH>(gv, a.g2, j);
+      load_chunks<LPR, CH>(bv, a.b2, j);
+      group_layernorm<LPR, CH>(xv, gv, bv);
+      if (out) store_chunks<LPR, CH>(xv, a.fn_out, j);
+    }
+  }
+
+  // 3. dot products, reduced over the lane group
+  float acc[UR];
+#pragma unroll
+  for (int u = 0; u < UR; ++u) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        s0 += (float)w[u][c][e] * xv[c][e];
+        s1 += (float)w[u][c][e + 1] * xv[c][e + 1];
+      }
+    }
+    acc[u] = group_sum<LPR>(s0 + s1);
+  }
+
+  // 4. epilogue (lane 0 of each group)
+  float rv[UR];
+#pragma unroll
+  for (int u = 0; u < UR; ++u) {
+    const int r = rbase + u * RPW + sub;
+    rv[u] = -INFINITY;
+    if (j != 0 || r >= a.N) continue;
+    const float v = acc[u] + a.bias[r];
+    if constexpr (EPI == EPI_GELU) {
+      a.y[r] = gelu_new(v);
+    } else if constexpr (EPI == EPI_RES) {
+      a.y[r] = a.y[r] + v;
+    } else if constexpr (EPI == EPI_QKV) {
+      if (r < kW) {
+        a.q[r] = v;
+      } else {
+        const int kv = a.st->kv;
+        if (kv < a.st->cap) {
+          if (r < 2 * kW) a.kc[(size_t)kv * kW + (r - kW)] = v;
+          else a.vc[(size_t)kv * kW + (r - 2 * kW)] = v;
+        }
+      }
+    } else {
+      a.y[r] = v;
+      rv[u] = v;
+    }
+  }
+  if constexpr (EPI == EPI_RES) {
+    if (a.advance && blockIdx.x == 0 && threadIdx.x == 0) a.st->kv += 1;
+  }
+  if constexpr (EPI == EPI_LOGITS) {
+    // argmax_row (gpt.cpp:1297-1308), first stage: each block's first
+    // maximum (argmax_kernel reduces the blocks).
+    __shared__ float sv[ROWS];
+    __shared__ int si[ROWS];
+#pragma unroll
+    for (int u = 0; u < UR; ++u) {
+      if (j == 0) {
+        const int lr = wave * RPW * UR + u * RPW + sub;
+        sv[lr] = rv[u];
+        si[lr] = rbase + u * RPW + sub;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = sv[0];
+      int bi = si[0];
+      for (int i = 1; i < ROWS; ++i)
+        if (sv[i] > bv) { bv = sv[i]; bi = si[i]; }
+      a.blk_val[blockIdx.x] = bv;
+      a.blk_idx[blockIdx.x] = bi;
+    }
+  }
+}
+
+// argmax_row (gpt.cpp:1297-1308), second stage: the first maximum over the
+// head blocks' maxima (ties go to the lower row), then the bookkeeping of the
+// loop of run_gpt_kv_greedy_cpu (gpt.cpp:1890-1909): record the prediction,
+// stop at the stop token, else append it to the inputs.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* blk_val, const int* blk_idx, int nb,
+                                                      GptState* st, uint32_t* predicted, uint32_t* inputs,
+                                                      int check_stop) {
+  if (check_stop && st->stopped) return;
+  __shared__ float wv[16];
+  __shared__ int wi[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  constexpr int kPer = 4;  // up to 4096 blocks in one round trip
+  float vals[kPer];
+  int idxs[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int b = min(tid + 1024 * u, nb - 1);
+    vals[u] = blk_val[b];
+    idxs[u] = blk_idx[b];
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u)
+    if (tid + 1024 * u < nb && (vals[u] > bv || (vals[u] == bv && idxs[u] < bi))) { bv = vals[u]; bi = idxs[u]; }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+  if (lane == 0) { wv[wave] = bv; wi[wave] = bi; }
+  __syncthreads();
+  if (tid != 0) return;
+  for (int w2 = 1; w2 < 16; ++w2)
+    if (wv[w2] > bv || (wv[w2] == bv && wi[w2] < bi)) { bv = wv[w2]; bi = wi[w2]; }
+  st->argmax = bi;
+  if (st->stopped) return;
+  if (st->n_pred < st->max_pred) predicted[st->n_pred] = (uint32_t)bi;
+  st->n_pred += 1;
+  if (bi == kStop) {
+    st->stopped = 1;
+    st->stop_step = st->step;
+  } else {
+    if (st->n_in < st->max_pred + 1) inputs[st->n_in] = (uint32_t)bi;
+    st->n_in += 1;
+    st->cur_token = bi;
+  }
+  st->step += 1;
+}
+
+// x = prefix row st->kv (mode 0), or mel_embedding[token] +
+// mel_pos_embedding[position] (mode 1, build_gpt_greedy_current_cpu,
+// gpt.cpp:1545-1554, with gpt_cached_generate_position, :1873-1875).
+__global__ __launch_bounds__(320) void embed_kernel(const GptState* st, const float* mel_emb,
+                                                     const float* pos_emb, const float* rows, int mode,
+                                                     float* x) {
+  const int i = threadIdx.x;  // float4 index, 320 x 4 = 1280
+  float4 v;
+  if (mode == 0) {
+    const int r = min(st->kv, st->rows - 1);
+    v = reinterpret_cast<const float4*>(rows + (size_t)r * kW)[i];
+  } else {
+    const int tok = min(max(st->cur_token, 0), kVocab - 1);
+    int pos = (st->hf && st->step > 0) ? st->step + 1 : st->step;
+    pos = min(pos, kPos - 1);
+    const float4 e = reinterpret_cast<const float4*>(mel_emb + (size_t)tok * kW)[i];
+    const float4 p = reinterpret_cast<const float4*>(pos_emb + (size_t)pos * kW)[i];
+    v = make_float4(e.x + p.x, e.y + p.y, e.z + p.z, e.w + p.w);
+  }
+  reinterpret_cast<float4*>(x)[i] = v;
+}
+
+// Cached attention of the current query (run_gpt_cached_attention_current_cpu,
+// gpt.cpp:1147-1170, with cpu_attention_single_query, tokenizer_tests.cpp:
+// 4034-4060) over the st->kv + 1 cache rows (the current row included: the
+// c_attn kernel already wrote it).  Block (head h, split s) handles keys
+// 128 s .. 128 s + 127 with 256 threads, every global load of a phase issued
+// before the first is used (the kernel is latency-bound): the scores (8 lanes
+// per key, 8 floats each), their max m and sum l of exp(score - m), and the
+// unnormalised output sum_t exp(score_t - m) v_t (16 lanes per key, 4 dims
+// each).  With one split the block writes the output; otherwise the last
+// split of a head to finish combines the splits.
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float* q, const float* kc, const float* vc,
+                                                          const GptState* st, float* part,
+                                                          unsigned* counters, float* out, int nsplit_max) {
+  const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+  const int kvn = min(st->kv + 1, st->cap);
+  const int nsplit = (kvn + kChunk - 1) / kChunk;
+  if (s >= nsplit) return;
+  const int t0 = s * kChunk, n = min(kChunk, kvn - t0);
+  __shared__ float sc[kChunk];
+  __shared__ float4 red[16][kHD / 4];
+  __shared__ float wm[4], wl[4];
+  __shared__ int is_last;
+  const float* kh = kc + (size_t)t0 * kW + h * kHD;
+  const float* vh = vc + (size_t)t0 * kW + h * kHD;
+
+  // scores: lane e (of 8) of key group g covers dims 8 e .. 8 e + 7
+  {
+    const int g = tid >> 3, e = tid & 7;
+    const float4* q4 = reinterpret_cast<const float4*>(q + h * kHD) + 2 * e;
+    const float4 qa = q4[0], qb = q4[1];
+    constexpr int kPass = kChunk / 32;
+    float4 ka[kPass], kb[kPass];
+#pragma unroll
+    for (int it = 0; it < kPass; ++it) {
+      const int i = min(g + 32 * it, n - 1);  // past the end: re-read the last key, dropped below
+      const float4* k4 = reinterpret_cast<const float4*>(kh + (size_t)i * kW) + 2 * e;
+      ka[it] = k4[0];
+      kb[it] = k4[1];
+    }
+#pragma unroll
+    for (int it = 0; it < kPass; ++it) {
+      float d = ((qa.x * ka[it].x + qa.y * ka[it].y) + (qa.z * ka[it].z + qa.w * ka[it].w)) +
+                ((qb.x * kb[it].x + qb.y * kb[it].y) + (qb.z * kb[it].z + qb.w * kb[it].w));
+      d += __shfl_xor(d, 4, kWave);
+      d += __shfl_xor(d, 2, kWave);
+      d += __shfl_xor(d, 1, kWave);
+      if (e == 0 && g + 32 * it < n) sc[g + 32 * it] = d * 0.125f;  // 1 / sqrt(64)
+    }
+  }
+  // the value loads do not depend on the scores: issue them now
+  const int d4 = tid & 15, g16 = tid >> 4;
+  constexpr int kVPass = kChunk / 16;
+  float4 vv[kVPass];
+#pragma unroll
+  for (int it = 0; it < kVPass; ++it) {
+    const int i = min(g16 + 16 * it, n - 1);
+    vv[it] = reinterpret_cast<const float4*>(vh + (size_t)i * kW)[d4];
+  }
+  __syncthreads();
+  // max and sum over the chunk (two values per lane of each wave, then the 4 waves)
+  const int lane = tid & 63, wave = tid >> 6;
+  float v0 = -INFINITY, v1 = -INFINITY;
+  if (tid < kChunk / 2) {
+    v0 = 2 * tid < n ? sc[2 * tid] : -INFINITY;
+    v1 = 2 * tid + 1 < n ? sc[2 * tid + 1] : -INFINITY;
+  }
+  float m = fmaxf(v0, v1);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  if (lane == 0) wm[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  float l = 0.f;
+  if (tid < kChunk / 2) {
+    const float p0 = 2 * tid < n ? expf(v0 - m) : 0.f;
+    const float p1 = 2 * tid + 1 < n ? expf(v1 - m) : 0.f;
+    sc[2 * tid] = p0;
+    sc[2 * tid + 1] = p1;
+    l = p0 + p1;
+  }
+  l = warp_sum(l);
+  if (lane == 0) wl[wave] = l;
+  __syncthreads();
+  l = (wl[0] + wl[1]) + (wl[2] + wl[3]);
+  // o = sum_t p_t v_t: thread (d4, g16) sums keys g16, g16 + 16, ...
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int it = 0; it < kVPass; ++it) {
+    const int i = g16 + 16 * it;
+    const float p = i < n ? sc[i] : 0.f;
+    o.x += p * vv[it].x; o.y += p * vv[it].y; o.z += p * vv[it].z; o.w += p * vv[it].w;
+  }
+  red[g16][d4] = o;
+  __syncthreads();
+  float od = 0.f;  // output dim tid (tid < 64): the 16 key groups
+  if (tid < kHD) {
+#pragma unroll
+    for (int g = 0; g < 16; ++g) od += reinterpret_cast<const float*>(&red[g][0])[tid];
+  }
+  if (nsplit == 1) {
+    if (tid < kHD) out[h * kHD + tid] = od / l;
+    return;
+  }
+  float* pp = part + ((size_t)h * nsplit_max + s) * kPartF;
+  if (tid < kHD) pp[2 + tid] = od;
+  if (tid == 0) { pp[0] = m; pp[1] = l; }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) is_last = atomicAdd(&counters[h], 1u) == (unsigned)(nsplit - 1);
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  // combine: M = max m_s, out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s;
+  // thread (d = tid % 64, q = tid / 64) takes splits q, q + 4, ...
+  const float* ph = part + (size_t)h * nsplit_max * kPartF;
+  __shared__ float sm[4][kHD + 2];
+  float M = -INFINITY;
+  for (int s2 = tid; s2 < nsplit; s2 += 256) M = fmaxf(M, ph[(size_t)s2 * kPartF]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
+  if (lane == 0) wm[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  const int d = tid & 63, qd = tid >> 6;
+  float L = 0.f, O = 0.f;
+  for (int s2 = qd; s2 < nsplit; s2 += 16) {
+    float mm[4], ll[4], oo[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // four splits per round trip
+      const int sx = min(s2 + 4 * u, nsplit - 1);
+      mm[u] = ph[(size_t)sx * kPartF];
+      ll[u] = ph[(size_t)sx * kPartF + 1];
+      oo[u] = ph[(size_t)sx * kPartF + 2 + d];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (s2 + 4 * u < nsplit) {
+        const float f = expf(mm[u] - M);
+        L += f * ll[u];
+        O += f * oo[u];
+      }
+    }
+  }
+  sm[qd][d] = O;
+  if (d == 0) sm[qd][kHD] = L;
+  __syncthreads();
+  if (tid < kHD) {
+    const float Ls = (sm[0][kHD] + sm[1][kHD]) + (sm[2][kHD] + sm[3][kHD]);
+    out[h * kHD + tid] = ((sm[0][tid] + sm[1][tid]) + (sm[2][tid] + sm[3][tid])) / Ls;
+    if (tid == 0) counters[h] = 0u;
+  }
+}
+
+// Launch shapes: rows per block = WAVES * (64 / LPR) * UR.
+template <int K, int LPR, int WAVES, int UR, int PRO, int EPI>
+void launch_gemv(const GemvArgs& a, hipStream_t s) {
+  constexpr int rows = WAVES * (64 / LPR) * UR;
+  const int blocks = (a.N + rows - 1) / rows;
+  hipLaunchKernelGGL((gemv_kernel<K, LPR, WAVES, UR, PRO, EPI>), dim3(blocks), dim3(WAVES * 64), 0, s, a);
+}
+// Launch shapes (lanes per row, waves per block, rows per lane group); the
+// defaults were chosen by timing whole decode steps.
+#ifndef GPT_QKV_SHAPE
+#define GPT_QKV_SHAPE 32, 4, 1
+#endif
+#ifndef GPT_PROJ_SHAPE
+#define GPT_PROJ_SHAPE 32, 2, 1
+#endif
+#ifndef GPT_FC_SHAPE
+#define GPT_FC_SHAPE 32, 4, 1
+#endif
+#ifndef GPT_MP_SHAPE
+#define GPT_MP_SHAPE 64, 4, 1
+#endif
+#ifndef GPT_HEAD_SHAPE
+#define GPT_HEAD_SHAPE 32, 4, 1
+#endif
+template <int LPR, int WAVES, int UR>
+constexpr int rows_of() { return WAVES * (64 / LPR) * UR; }
+constexpr int head_blocks() { return (kVocab + rows_of<GPT_HEAD_SHAPE>() - 1) / rows_of<GPT_HEAD_SHAPE>(); }
+static_assert(head_blocks() <= 4096, "argmax_kernel reduces at most 4096 block maxima");
+
+void launch_qkv(const GemvArgs& a, hipStream_t s) { launch_gemv<kW, GPT_QKV_SHAPE, PRO_LN, EPI_QKV>(a, s); }
+void launch_attn_proj(const GemvArgs& a, hipStream_t s) { launch_gemv<kW, GPT_PROJ_SHAPE, PRO_PLAIN, EPI_RES>(a, s); }
+void launch_fc(const GemvArgs& a, hipStream_t s) { launch_gemv<kW, GPT_FC_SHAPE, PRO_LN, EPI_GELU>(a, s); }
+void launch_mlp_proj(const GemvArgs& a, hipStream_t s) { launch_gemv<kMLP, GPT_MP_SHAPE, PRO_PLAIN, EPI_RES>(a, s); }
+void launch_head(const GemvArgs& a, hipStream_t s) { launch_gemv<kW, GPT_HEAD_SHAPE, PRO_LN2, EPI_LOGITS>(a, s); }
+
+inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+}  // namespace
+
+// ---------------------------------------------------------------- weights
+struct GptLayerDev {
+  float *ln1_w, *ln1_b, *attn_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *mp_b;
+  half_t *attn_w, *proj_w, *fc_w, *mp_w;  // [out][in]
+};
+
+struct GptDecoder::Impl {
+  hipStream_t s = nullptr;
+  int L = 0;
+  Arena wa;  // weights
+  std::vector<GptLayerDev> layer;
+  float *lnf_w, *lnf_b, *fn_w, *fn_b, *head_b, *mel_emb, *pos_emb;
+  half_t* head_w;
+
+  // workspace (grows)
+  Arena ws;
+  int cap = 0;       // key/value cache rows
+  int rows_cap = 0;  // prefix rows
+  int pred_cap = 0;  // predicted tokens
+  int nsplit_max = 0;
+  GptState* st = nullptr;
+  uint32_t *predicted = nullptr, *inputs = nullptr;
+  float *x, *q, *att, *fc, *logits, *lnf, *fn, *blk_val, *part, *kc, *vc, *rows;
+  int* blk_idx;
+  unsigned* counters;  // [kHeads]: the attention's last-split counters
+  GptState* host_state = nullptr;  // pinned
+  hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // row, row + head, token + head
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  bool use_graph = true;  // env MIT2CFM_GRAPH=0: launch every kernel directly (for profilers)
+
+  ~Impl() {
+    drop_graphs();
+    for (auto& e : ev)
+      if (e) (void)hipEventDestroy(e);
+    if (host_state) (void)hipHostFree(host_state);
+  }
+  void drop_graphs() {
+    for (auto& g : graph) {
+      if (g) (void)hipGraphExecDestroy(g);
+      g = nullptr;
+    }
+  }
+
+  half_t* up_f16(const std::vector<float>& v) {
+    std::vector<_Float16> h(v.size());
+    for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
+    half_t* d = static_cast<half_t*>(wa.take(h.size() * 2));
+    GPT_OK(hipMemcpy(d, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+    return d;
+  }
+  // Conv1D [in][out] -> f16 [out][in] (transpose_gpt_conv1d_weight, gpt.cpp:208-216)
+  half_t* up_conv1d(const std::vector<float>& v, int in, int out) {
+    std::vector<_Float16> h((size_t)in * out);
+    for (int i = 0; i < in; ++i) {
+      const float* src = v.data() + (size_t)i * out;
+      for (int o = 0; o < out; ++o) h[(size_t)o * in + i] = (_Float16)src[o];
+    }
+    half_t* d = static_cast<half_t*>(wa.take(h.size() * 2));
+    GPT_OK(hipMemcpy(d, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+    return d;
+  }
+  float* up_f32(const std::vector<float>& v) {
+    float* d = static_cast<float*>(wa.take(v.size() * 4));
+    GPT_OK(hipMemcpy(d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    return d;
+  }
+
+  // Workspace for `kv_rows` cache rows, `prefix_rows` prefix rows and
+  // `steps` predicted tokens; regrows (and drops the graphs) when needed.
+  void ensure(int kv_rows, int prefix_rows, int steps) {
+    if (kv_rows <= cap && prefix_rows <= rows_cap && steps <= pred_cap && st) return;
+    drop_graphs();
+    cap = std::max(std::max(kv_rows, cap), 256);
+    cap = (cap + kChunk - 1) / kChunk * kChunk;
+    rows_cap = std::max(std::max(prefix_rows, rows_cap), 16);
+    pred_cap = std::max(std::max(steps, pred_cap), 64);
+    nsplit_max = cap / kChunk;
+    const size_t f = sizeof(float);
+    size_t bytes = align256(sizeof(GptState)) + align256((size_t)pred_cap * 4) +
+                   align256(((size_t)pred_cap + 1) * 4) + 3 * align256(kW * f) + align256(kMLP * f) +
+                   align256(kVocab * f) + 2 * align256(kW * f) + align256((size_t)head_blocks() * f) +
+                   align256((size_t)head_blocks() * 4) + align256(kHeads * 4) +
+                   align256((size_t)kHeads * nsplit_max * kPartF * f) +
+                   2 * align256((size_t)L * cap * kW * f) + align256((size_t)rows_cap * kW * f);
+    ws.reserve(bytes);
+    st = static_cast<GptState*>(ws.take(sizeof(GptState)));
+    predicted = static_cast<uint32_t*>(ws.take((size_t)pred_cap * 4));
+    inputs = static_cast<uint32_t*>(ws.take(((size_t)pred_cap + 1) * 4));
+    x = static_cast<float*>(ws.take(kW * f));
+    q = static_cast<float*>(ws.take(kW * f));
+    att = static_cast<float*>(ws.take(kW * f));
+    fc = static_cast<float*>(ws.take(kMLP * f));
+    logits = static_cast<float*>(ws.take(kVocab * f));
+    lnf = static_cast<float*>(ws.take(kW * f));
+    fn = static_cast<float*>(ws.take(kW * f));
+    blk_val = static_cast<float*>(ws.take((size_t)head_blocks() * f));
+    blk_idx = static_cast<int*>(ws.take((size_t)head_blocks() * 4));
+    counters = static_cast<unsigned*>(ws.take(kHeads * 4));
+    part = static_cast<float*>(ws.take((size_t)kHeads * nsplit_max * kPartF * f));
+    kc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
+    vc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
+    rows = static_cast<float*>(ws.take((size_t)rows_cap * kW * f));
+    // The last-block counters start at zero; every user resets its own.
+    GPT_OK(hipMemsetAsync(counters, 0, kHeads * 4, s));
+    GPT_OK(hipStreamSynchronize(s));
+  }
+
+  GemvArgs base_args() const {
+    GemvArgs a;
+    a.st = st;
+    return a;
+  }
+
+  // One token step: embed (mode 0: prefix row, 1: token), the layers, and the
+  // head when `head` is set.
+  void enqueue_step(int mode, bool head) {
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(320), 0, s, st, mel_emb, pos_emb, rows, mode, x);
+    for (int l = 0; l < L; ++l) {
+      const GptLayerDev& w = layer[l];
+      float* K = kc + (size_t)l * cap * kW;
+      float* V = vc + (size_t)l * cap * kW;
+      GemvArgs a = base_args();
+      a.w = w.attn_w; a.bias = w.attn_b; a.N = kQKV; a.x = x; a.g1 = w.ln1_w; a.b1 = w.ln1_b;
+      a.q = q; a.kc = K; a.vc = V;
+      launch_qkv(a, s);
+      hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads, nsplit_max), dim3(256), 0, s, q, K, V, st, part,
+                         counters, att, nsplit_max);
+      a = base_args();
+      a.w = w.proj_w; a.bias = w.proj_b; a.N = kW; a.x = att; a.y = x;
+      launch_attn_proj(a, s);
+      a = base_args();
+      a.w = w.fc_w; a.bias = w.fc_b; a.N = kMLP; a.x = x; a.g1 = w.ln2_w; a.b1 = w.ln2_b; a.y = fc;
+      launch_fc(a, s);
+      a = base_args();
+      a.w = w.mp_w; a.bias = w.mp_b; a.N = kW; a.x = fc; a.y = x; a.advance = l == L - 1;
+      launch_mlp_proj(a, s);
+    }
+    if (head) {
+      GemvArgs a = base_args();
+      a.w = head_w; a.bias = head_b; a.N = kVocab; a.x = x; a.g1 = lnf_w; a.b1 = lnf_b; a.g2 = fn_w;
+      a.b2 = fn_b; a.y = logits; a.blk_val = blk_val; a.blk_idx = blk_idx; a.lnf_out = lnf; a.fn_out = fn;
+      launch_head(a, s);
+      hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, blk_val, blk_idx, head_blocks(), st, predicted,
+                         inputs, 1);
+    }
+    GPT_OK(hipGetLastError());
+  }
+
+  void run_step(int which) {  // 0 row, 1 row + head, 2 token + head
+    if (!use_graph) {
+      enqueue_step(which == 2 ? 1 : 0, which != 0);
+      return;
+    }
+    if (!graph[which]) {
+      hipGraph_t g = nullptr;
+      GPT_OK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      try {
+        enqueue_step(which == 2 ? 1 : 0, which != 0);
+      } catch (...) {
+        (void)hipStreamEndCapture(s, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      GPT_OK(hipStreamEndCapture(s, &g));
+      hipGraphExec_t e = nullptr;
+      const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      GPT_OK(err);
+      graph[which] = e;
+    }
+    GPT_OK(hipGraphLaunch(graph[which], s));
+  }
+
+  void reset_state(int prefix_rows, bool hf, int steps) {
+    GptState h{};
+    h.kv = 0;
+    h.step = 0;
+    h.n_pred = 0;
+    h.n_in = 1;
+    h.stopped = 0;
+    h.stop_step = -1;
+    h.cur_token = kStart;
+    h.hf = hf ? 1 : 0;
+    h.argmax = -1;
+    h.max_pred = pred_cap;
+    h.cap = cap;
+    h.rows = std::max(prefix_rows, 1);
+    (void)steps;
+    *host_state = h;
+    const uint32_t start = (uint32_t)kStart;
+    GPT_OK(hipMemcpyAsync(st, host_state, sizeof(GptState), hipMemcpyHostToDevice, s));
+    GPT_OK(hipMemcpyAsync(inputs, &start, 4, hipMemcpyHostToDevice, s));
+    GPT_OK(hipStreamSynchronize(s));  // host_state and `start` are reused below
+  }
+};
+
+bool GptDecoder::present(const std::unordered_map<std::string, std::vector<float>>& t) {
+  for (const auto& kv : t)
+    if (kv.first.compare(0, 10, "gpt.gpt.h.") == 0) return true;
+  return false;
+}
+
+GptDecoder::GptDecoder(const std::unordered_map<std::string, std::vector<float>>& t, hipStream_t stream)
+    : d_(new Impl) {
+  Impl& d = *d_;
+  d.s = stream;
+  if (const char* g = std::getenv("MIT2CFM_GRAPH")) d.use_graph = std::atoi(g) != 0;
+  try {
+    auto get = [&](const std::string& name, size_t elems) -> const std::vector<float>& {
+      auto it = t.find(name);
+      if (it == t.end()) throw std::invalid_argument("missing tensor: " + name);
+      if (it->second.size() != elems)
+        throw std::invalid_argument("tensor " + name + " has " + std::to_string(it->second.size()) +
+                                    " elements, expected " + std::to_string(elems));
+      return it->second;
+    };
+    int L = 0;
+    while (t.count("gpt.gpt.h." + std::to_string(L) + ".ln_1.weight")) ++L;
+    if (L == 0) throw std::invalid_argument("GPT decoder: no layer tensors (gpt.gpt.h.0.*)");
+    for (const auto& kv : t) {
+      int l = -1;
+      if (std::sscanf(kv.first.c_str(), "gpt.gpt.h.%d.", &l) == 1 && (l < 0 || l >= L))
+        throw std::invalid_argument("GPT decoder: layer tensors must be numbered 0..L-1 (" + kv.first + ")");
+    }
+    d.L = L;
+    const size_t per_layer = 2 * ((size_t)kQKV * kW + (size_t)kW * kW + 2 * (size_t)kMLP * kW) +
+                             4 * (6 * (size_t)kW + kQKV + kMLP) + 12 * 256;
+    d.wa.reserve((size_t)L * per_layer + 2 * (size_t)kVocab * kW + 4 * (size_t)(kVocab + kPos) * kW +
+                 4 * ((size_t)kVocab + 4 * kW) + 16 * 256);
+    d.layer.resize(L);
+    for (int l = 0; l < L; ++l) {
+      const std::string p = "gpt.gpt.h." + std::to_string(l) + ".";
+      GptLayerDev& w = d.layer[l];
+      w.ln1_w = d.up_f32(get(p + "ln_1.weight", kW));
+      w.ln1_b = d.up_f32(get(p + "ln_1.bias", kW));
+      w.attn_w = d.up_conv1d(get(p + "attn.c_attn.weight", (size_t)kW * kQKV), kW, kQKV);
+      w.attn_b = d.up_f32(get(p + "attn.c_attn.bias", kQKV));
+      w.proj_w = d.up_conv1d(get(p + "attn.c_proj.weight", (size_t)kW * kW), kW, kW);
+      w.proj_b = d.up_f32(get(p + "attn.c_proj.bias", kW));
+      w.ln2_w = d.up_f32(get(p + "ln_2.weight", kW));
+      w.ln2_b = d.up_f32(get(p + "ln_2.bias", kW));
+      w.fc_w = d.up_conv1d(get(p + "mlp.c_fc.weight", (size_t)kW * kMLP), kW, kMLP);
+      w.fc_b = d.up_f32(get(p + "mlp.c_fc.bias", kMLP));
+      w.mp_w = d.up_conv1d(get(p + "mlp.c_proj.weight", (size_t)kMLP * kW), kMLP, kW);
+      w.mp_b = d.up_f32(get(p + "mlp.c_proj.bias", kW));
+    }
+    d.lnf_w = d.up_f32(get("gpt.gpt.ln_f.weight", kW));
+    d.lnf_b = d.up_f32(get("gpt.gpt.ln_f.bias", kW));
+    d.fn_w = d.up_f32(get("gpt.final_norm.weight", kW));
+    d.fn_b = d.up_f32(get("gpt.final_norm.bias", kW));
+    d.head_w = d.up_f16(get("gpt.mel_head.weight", (size_t)kVocab * kW));
+    d.head_b = d.up_f32(get("gpt.mel_head.bias", kVocab));
+    d.mel_emb = d.up_f32(get("gpt.mel_embedding.weight", (size_t)kVocab * kW));
+    d.pos_emb = d.up_f32(get("gpt.mel_pos_embedding.emb.weight", (size_t)kPos * kW));
+    GPT_OK(hipHostMalloc(reinterpret_cast<void**>(&d.host_state), sizeof(GptState), hipHostMallocDefault));
+    for (auto& e : d.ev) GPT_OK(hipEventCreate(&e));
+  } catch (...) {
+    delete d_;
+    throw;
+  }
+}
+
+GptDecoder::~GptDecoder() { delete d_; }
+
+size_t GptDecoder::weight_bytes() const { return d_->wa.used(); }
+int GptDecoder::layers() const { return d_->L; }
+
+void GptDecoder::kv_greedy(const float* prefix, int prefix_tokens, int steps, bool hf, Greedy& out) {
+  Impl& d = *d_;
+  if (prefix_tokens < 0 || steps < 0) throw std::invalid_argument("gpt: prefix_tokens and steps must be >= 0");
+  if (prefix_tokens > 0 && !prefix) throw std::invalid_argument("gpt: prefix must not be NULL");
+  if (steps > 0) {
+    const int last = (hf && steps - 1 > 0) ? steps : steps - 1;  // position of the last step
+    if (last >= kPos)
+      throw std::invalid_argument("gpt: " + std::to_string(steps) + " steps pass the " +
+                                  std::to_string(kPos) + "-row mel position table");
+  }
+  d.ensure(prefix_tokens + steps + 1, prefix_tokens + 1, steps);
+  d.reset_state(prefix_tokens, hf, steps);
+  if (prefix_tokens > 0)
+    GPT_OK(hipMemcpyAsync(d.rows, prefix, (size_t)prefix_tokens * kW * sizeof(float), hipMemcpyHostToDevice, d.s));
+  GPT_OK(hipEventRecord(d.ev[0], d.s));
+  for (int i = 0; i < prefix_tokens; ++i) d.run_step(0);
+  GPT_OK(hipEventRecord(d.ev[1], d.s));
+  int done = 0;
+  while (done < steps) {
+    const int n = std::min(kStepsPerCheck, steps - done);
+    for (int i = 0; i < n; ++i) d.run_step(2);
+    done += n;
+    GPT_OK(hipMemcpyAsync(d.host_state, d.st, sizeof(GptState), hipMemcpyDeviceToHost, d.s));
+    GPT_OK(hipStreamSynchronize(d.s));
+    if (d.host_state->stopped) break;
+  }
+  GPT_OK(hipEventRecord(d.ev[2], d.s));
+  GPT_OK(hipMemcpyAsync(d.host_state, d.st, sizeof(GptState), hipMemcpyDeviceToHost, d.s));
+  GPT_OK(hipStreamSynchronize(d.s));
+  const GptState h = *d.host_state;
+  out.first_stop_step = h.stop_step;
+  out.predicted.assign((size_t)h.n_pred, 0);
+  out.input_tokens.assign((size_t)h.n_in, 0);
+  out.last_logits.assign(steps > 0 ? kVocab : 0, 0.f);
+  if (h.n_pred) GPT_OK(hipMemcpy(out.predicted.data(), d.predicted, (size_t)h.n_pred * 4, hipMemcpyDeviceToHost));
+  GPT_OK(hipMemcpy(out.input_tokens.data(), d.inputs, (size_t)h.n_in * 4, hipMemcpyDeviceToHost));
+  if (steps > 0) GPT_OK(hipMemcpy(out.last_logits.data(), d.logits, kVocab * sizeof(float), hipMemcpyDeviceToHost));
+  float ms = 0.f;
+  GPT_OK(hipEventElapsedTime(&ms, d.ev[0], d.ev[1]));
+  out.prefill_ms = ms;
+  GPT_OK(hipEventElapsedTime(&ms, d.ev[1], d.ev[2]));
+  out.decode_ms = ms;
+}
+
+uint32_t GptDecoder::cached_decode(const float* rows, int prefix_tokens, float* ln_f, float* final_norm,
+                                   float* logits) {
+  Impl& d = *d_;
+  if (prefix_tokens < 0) throw std::invalid_argument("gpt: prefix_tokens must be >= 0");
+  if (!rows) throw std::invalid_argument("gpt: rows must not be NULL");
+  d.ensure(prefix_tokens + 1, prefix_tokens + 1, 1);
+  d.reset_state(prefix_tokens + 1, false, 1);
+  GPT_OK(hipMemcpyAsync(d.rows, rows, ((size_t)prefix_tokens + 1) * kW * sizeof(float), hipMemcpyHostToDevice, d.s));
+  for (int i = 0; i < prefix_tokens; ++i) d.run_step(0);
+  d.run_step(1);
+  GPT_OK(hipMemcpyAsync(d.host_state, d.st, sizeof(GptState), hipMemcpyDeviceToHost, d.s));
+  GPT_OK(hipStreamSynchronize(d.s));
+  if (ln_f) GPT_OK(hipMemcpy(ln_f, d.lnf, kW * sizeof(float), hipMemcpyDeviceToHost));
+  if (final_norm) GPT_OK(hipMemcpy(final_norm, d.fn, kW * sizeof(float), hipMemcpyDeviceToHost));
+  if (logits) GPT_OK(hipMemcpy(logits, d.logits, kVocab * sizeof(float), hipMemcpyDeviceToHost));
+  return (uint32_t)d.host_state->argmax;
+}
+
+const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) {
+  Impl& d = *d_;
+  static const char* names[6] = {"gemv c_attn 3840x1280 (LN prologue, K/V to cache)",
+                                 "gemv attn c_proj 1280x1280 (+residual)",
+                                 "gemv c_fc 5120x1280 (LN prologue, gelu_new)",
+                                 "gemv mlp c_proj 1280x5120 (+residual)",
+                                 "gemv mel_head 8194x1280 (two LNs) + argmax",
+                                 "cached attention, 1024 keys x 20 heads"};
+  if (kernel < 0 || kernel > 5) throw std::invalid_argument("gpt profile: kernel must be 0..5");
+  constexpr int kKeys = 1024;
+  d.ensure(kKeys + 1, 1, 1);
+  if (launches == 0) {
+    const double f16 = 2.0, f32 = 4.0;
+    const double b[6] = {
+        kQKV * (double)kW * f16 + (kW * 3.0 + kQKV) * f32 + kQKV * f32,
+        kW * (double)kW * f16 + (kW * 3.0) * f32,
+        kMLP * (double)kW * f16 + (kW * 3.0 + kMLP) * f32 + kMLP * f32,
+        kW * (double)kMLP * f16 + (kMLP + kW * 3.0) * f32,
+        kVocab * (double)kW * f16 + (kW * 5.0 + kVocab) * f32 + kVocab * f32,
+        2.0 * kKeys * kW * f32 + 2.0 * kW * f32};
+    if (bytes) *bytes = b[kernel];
+    return names[kernel];
+  }
+  // A state with kKeys - 1 cached rows; the caches hold whatever they hold
+  // (timing only).
+  d.reset_state(1, false, 1);
+  d.host_state->kv = kKeys - 1;
+  GPT_OK(hipMemcpyAsync(d.st, d.host_state, sizeof(GptState), hipMemcpyHostToDevice, d.s));
+  GPT_OK(hipMemsetAsync(d.x, 0, kW * sizeof(float), d.s));
+  GPT_OK(hipMemsetAsync(d.fc, 0, kMLP * sizeof(float), d.s));
+  GPT_OK(hipMemsetAsync(d.att, 0, kW * sizeof(float), d.s));
+  for (int i = 0; i < launches; ++i) {
+    // cycle through the layers so that, as in a decode step, the weights are
+    // not already in the caches
+    const GptLayerDev& w = d.layer[i % d.L];
+    GemvArgs a = d.base_args();
+    switch (kernel) {
+      case 0:
+        a.w = w.attn_w; a.bias = w.attn_b; a.N = kQKV; a.x = d.x; a.g1 = w.ln1_w; a.b1 = w.ln1_b;
+        a.q = d.q; a.kc = d.kc; a.vc = d.vc;
+        launch_qkv(a, d.s);
+        break;
+      case 1:
+        a.w = w.proj_w; a.bias = w.proj_b; a.N = kW; a.x = d.att; a.y = d.lnf;
+        launch_attn_proj(a, d.s);
+        break;
+      case 2:
+        a.w = w.fc_w; a.bias = w.fc_b; a.N = kMLP; a.x = d.x; a.g1 = w.ln2_w; a.b1 = w.ln2_b; a.y = d.fc;
+        launch_fc(a, d.s);
+        break;
+      case 3:
+        a.w = w.mp_w; a.bias = w.mp_b; a.N = kW; a.x = d.fc; a.y = d.lnf;
+        launch_mlp_proj(a, d.s);
+        break;
+      case 4:
+        a.w = d.head_w; a.bias = d.head_b; a.N = kVocab; a.x = d.x; a.g1 = d.lnf_w; a.b1 = d.lnf_b;
+        a.g2 = d.fn_w; a.b2 = d.fn_b; a.y = d.logits; a.blk_val = d.blk_val; a.blk_idx = d.blk_idx;
+        a.check_stop = 0;
+        launch_head(a, d.s);
+        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, d.s, d.blk_val, d.blk_idx, head_blocks(), d.st,
+                           d.predicted, d.inputs, 0);
+        break;
+      default:
+        hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads, d.nsplit_max), dim3(256), 0, d.s, d.q,
+                           d.kc + (size_t)(i % d.L) * d.cap * kW, d.vc + (size_t)(i % d.L) * d.cap * kW, d.st, d.part,
+                           d.counters, d.att, d.nsplit_max);
+        break;
+    }
+  }
+  GPT_OK(hipGetLastError());
+  if (bytes) *bytes = 0;
+  return names[kernel];
+}
+
+}  // namespace mit2hip

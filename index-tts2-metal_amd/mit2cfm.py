@@ -8,6 +8,7 @@ library is missing every call raises instead of falling back to anything.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import ctypes
 import os
 import re
@@ -110,6 +111,12 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_create_synthetic_acoustic": (st, [u64, f32, i32, ctypes.POINTER(vp)]),
         "mit2cfm_write_image": (st, [vp, ctypes.c_char_p]),
         "mit2cfm_create_from_image": (st, [ctypes.c_char_p, i32, ctypes.POINTER(vp)]),
+        "mit2cfm_gpt_layers": (st, [vp, _u32p]),
+        "mit2cfm_gpt_kv_greedy": (st, [vp, _f32p, u32, u32, i32, _u32p, _u32p, _u32p, _u32p,
+                                       ctypes.POINTER(i32), _f32p, ctypes.POINTER(ctypes.c_double)]),
+        "mit2cfm_gpt_cached_decode": (st, [vp, _f32p, u32, _f32p, _f32p, _f32p, _u32p]),
+        "mit2cfm_gpt_profile_launch": (st, [vp, i32, u32, ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_char_p)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -193,7 +200,7 @@ def generated_frames(codes: int) -> int:
     return int(lib().mit2cfm_generated_frames(codes))
 
 
-SYNTH_ESTIMATOR, SYNTH_LENGTH_REGULATOR, SYNTH_BIGVGAN = 0, 1, 2
+SYNTH_ESTIMATOR, SYNTH_LENGTH_REGULATOR, SYNTH_BIGVGAN, SYNTH_GPT = 0, 1, 2, 3
 
 
 def synthetic_set_specs(set_id: int) -> list[tuple[str, tuple[int, ...], str]]:
@@ -213,15 +220,27 @@ def synthetic_set_specs(set_id: int) -> list[tuple[str, tuple[int, ...], str]]:
     return specs
 
 
-def synthetic_set(set_id: int, seed: int, stddev: float) -> dict[str, np.ndarray]:
-    """Every tensor of a synthetic set, generated by the library (one generator for
-    the C++ runtime, the tests and the bench)."""
+def synthetic_set(set_id: int, seed: int, stddev: float, keep=None) -> dict[str, np.ndarray]:
+    """Every tensor of a synthetic set (or those whose name `keep` accepts),
+    generated by the library (one generator for the C++ runtime, the tests and
+    the bench)."""
     L = lib()
-    out = {}
+    out, jobs = {}, []
     for i, (name, shape, dt) in enumerate(synthetic_set_specs(set_id)):
+        if keep is not None and not keep(name):
+            continue
         arr = np.empty(shape, np.float16 if dt == "f16" else np.float32)
-        _check(L.mit2cfm_synthetic_set_fill(set_id, i, seed, stddev, arr.ctypes.data_as(ctypes.c_void_p)))
         out[name] = arr
+        jobs.append((i, arr))
+
+    def fill(job):  # ctypes releases the GIL, so tensors fill in parallel
+        i, arr = job
+        return L.mit2cfm_synthetic_set_fill(set_id, i, seed, stddev, arr.ctypes.data_as(ctypes.c_void_p))
+
+    workers = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else 4))
+    with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+        for status in pool.map(fill, jobs):
+            _check(status)
     return out
 
 
@@ -295,6 +314,31 @@ def bigvgan_flops(tokens: int) -> float:
         c = cout
         f += sum(6 * 2.0 * t * c * c * kk for kk in (3, 7, 11))
     return f + 2.0 * t * 24 * 7
+
+
+# The GPT-2 stack of IndexTTS2's mel-code decoder (gpt.cpp): width, heads,
+# MLP width, vocabulary (8192 codes + start 8192 + stop 8193), position rows.
+GPT_WIDTH, GPT_HEADS, GPT_MLP, GPT_VOCAB, GPT_POSITIONS = 1280, 20, 5120, 8194, 1818
+GPT_START_TOKEN, GPT_STOP_TOKEN = 8192, 8193
+
+
+def synthetic_gpt_tensors(layers: int = 24, seed: int = 20240608, stddev: float = 0.02) -> dict[str, np.ndarray]:
+    """GPT decoder weights from the library's generator (checkpoint names and
+    layouts, Conv1D weights [in][out], f16): N(0, stddev) from seed + (index in
+    sorted-name order of the 24-layer set), LayerNorm weights 1 + N(0, stddev).
+    `layers` < 24 keeps layers 0..layers-1 (a shallower model for fast tests)."""
+    def keep(name: str) -> bool:
+        if name.startswith("gpt.gpt.h."):
+            return int(name.split(".")[3]) < layers
+        return True
+    return synthetic_set(SYNTH_GPT, seed, stddev, keep)
+
+
+def gpt_step_bytes(layers: int = 24) -> float:
+    """Algorithmic HBM bytes of one decode step's weights (f16): per layer
+    c_attn, attn c_proj, c_fc, mlp c_proj; plus mel_head."""
+    w = GPT_WIDTH
+    return 2.0 * (layers * (3 * w * w + w * w + 2 * GPT_MLP * w) + GPT_VOCAB * w)
 
 
 def write_synthetic_bundle(path: str | os.PathLike, seed: int = 20240605, stddev: float = 0.02) -> None:
@@ -523,6 +567,57 @@ class Context:
                                               prompt_tokens, style_ptr, seed, temperature, steps, cfg, wav_ptr,
                                               mel_ptr or None, _pu(g), FLAG_SYNC if sync else 0))
         return int(g[0])
+
+    # -- GPT mel-code decoder
+    def gpt_layers(self) -> int:
+        """Layers of the context's GPT decoder (0: none)."""
+        n = np.zeros(1, np.uint32)
+        self._c(lib().mit2cfm_gpt_layers(self._h, _pu(n)))
+        return int(n[0])
+
+    def gpt_kv_greedy(self, prefix, steps: int, hf_generate_positions: bool = False) -> dict:
+        """run_gpt_kv_greedy (gpt.cpp:1877): prefix [P, 1280] -> dict with
+        predicted, input_tokens (uint32 arrays), first_stop_step, last_logits
+        [8194] (None when steps == 0) and prefill_ms / decode_ms (device time)."""
+        x = _f32(prefix).reshape(-1, GPT_WIDTH)
+        P = x.shape[0]
+        pred = np.zeros(max(steps, 1), np.uint32)
+        inp = np.zeros(steps + 1, np.uint32)
+        n_pred = np.zeros(1, np.uint32)
+        n_in = np.zeros(1, np.uint32)
+        stop = ctypes.c_int32()
+        logits = np.zeros(GPT_VOCAB, np.float32)
+        t = (ctypes.c_double * 2)()
+        self._c(lib().mit2cfm_gpt_kv_greedy(self._h, _p(x) if P else None, P, steps,
+                                            1 if hf_generate_positions else 0, _pu(pred), _pu(n_pred),
+                                            _pu(inp), _pu(n_in), ctypes.byref(stop), _p(logits), t))
+        return {"predicted": pred[:n_pred[0]].copy(), "input_tokens": inp[:n_in[0]].copy(),
+                "first_stop_step": int(stop.value), "last_logits": logits if steps > 0 else None,
+                "prefill_ms": float(t[0]), "decode_ms": float(t[1])}
+
+    def gpt_cached_decode(self, rows, prefix_tokens: int):
+        """run_gpt_cached_decode (gpt.cpp:1400): rows [P + 1, 1280] -> (ln_f,
+        final_norm, logits, argmax) of the last row."""
+        x = _f32(rows).reshape(-1, GPT_WIDTH)
+        if x.shape[0] != prefix_tokens + 1:
+            raise ValueError(f"rows must hold prefix_tokens + 1 = {prefix_tokens + 1} rows, got {x.shape[0]}")
+        ln_f = np.empty(GPT_WIDTH, np.float32)
+        fn = np.empty(GPT_WIDTH, np.float32)
+        logits = np.empty(GPT_VOCAB, np.float32)
+        am = np.zeros(1, np.uint32)
+        self._c(lib().mit2cfm_gpt_cached_decode(self._h, _p(x), prefix_tokens, _p(ln_f), _p(fn), _p(logits),
+                                                _pu(am)))
+        return ln_f, fn, logits, int(am[0])
+
+    GPT_KERNELS = {"c_attn": 0, "attn_proj": 1, "c_fc": 2, "mlp_proj": 3, "mel_head": 4, "attention": 5}
+
+    def gpt_profile_launch(self, kernel: int, count: int):
+        """Enqueues `count` launches of one GPT decode kernel (ids in mit2cfm.h)
+        on the context stream; returns (name, algorithmic bytes per launch)."""
+        b = ctypes.c_double()
+        nm = ctypes.c_char_p()
+        self._c(lib().mit2cfm_gpt_profile_launch(self._h, kernel, count, ctypes.byref(b), ctypes.byref(nm)))
+        return nm.value.decode(), float(b.value)
 
     BIGVGAN_STAGES = {"conv_pre": 0, "upsample": 1, "activation": 2, "resblock": 3, "group": 4, "post": 5,
                       "body": 6}

@@ -295,4 +295,47 @@ std::vector<uint8_t> synth_bigvgan_tensor_bytes(size_t i, uint64_t base_seed, fl
   return to_f16_bytes(v);
 }
 
+const std::vector<SynthSpec>& gpt_tensor_specs() {
+  static const std::vector<SynthSpec> specs = [] {
+    std::vector<SynthSpec> v;
+    for (int l = 0; l < 24; ++l) {
+      const std::string p = "gpt.gpt.h." + std::to_string(l) + ".";
+      v.push_back({p + "ln_1.weight", {1280}, "f16"});
+      v.push_back({p + "ln_1.bias", {1280}, "f16"});
+      v.push_back({p + "attn.c_attn.weight", {1280, 3840}, "f16"});
+      v.push_back({p + "attn.c_attn.bias", {3840}, "f16"});
+      v.push_back({p + "attn.c_proj.weight", {1280, 1280}, "f16"});
+      v.push_back({p + "attn.c_proj.bias", {1280}, "f16"});
+      v.push_back({p + "ln_2.weight", {1280}, "f16"});
+      v.push_back({p + "ln_2.bias", {1280}, "f16"});
+      v.push_back({p + "mlp.c_fc.weight", {1280, 5120}, "f16"});
+      v.push_back({p + "mlp.c_fc.bias", {5120}, "f16"});
+      v.push_back({p + "mlp.c_proj.weight", {5120, 1280}, "f16"});
+      v.push_back({p + "mlp.c_proj.bias", {1280}, "f16"});
+    }
+    v.push_back({"gpt.gpt.ln_f.weight", {1280}, "f16"});
+    v.push_back({"gpt.gpt.ln_f.bias", {1280}, "f16"});
+    v.push_back({"gpt.final_norm.weight", {1280}, "f16"});
+    v.push_back({"gpt.final_norm.bias", {1280}, "f16"});
+    v.push_back({"gpt.mel_head.weight", {8194, 1280}, "f16"});
+    v.push_back({"gpt.mel_head.bias", {8194}, "f16"});
+    v.push_back({"gpt.mel_embedding.weight", {8194, 1280}, "f16"});
+    v.push_back({"gpt.mel_pos_embedding.emb.weight", {1818, 1280}, "f16"});
+    sort_specs(v);
+    return v;
+  }();
+  return specs;
+}
+
+std::vector<uint8_t> synth_gpt_tensor_bytes(size_t i, uint64_t base_seed, float stddev) {
+  const auto& specs = gpt_tensor_specs();
+  if (i >= specs.size()) throw std::out_of_range("synthetic tensor index");
+  const SynthSpec& s = specs[i];
+  auto v = make_deterministic_normal_noise((uint32_t)elems_of(s), 1, base_seed + i, stddev);
+  const bool norm_weight = s.shape.size() == 1 && ends_with(s.name, ".weight");
+  if (norm_weight)
+    for (float& x : v) x = x + 1.0f;
+  return to_f16_bytes(v);
+}
+
 }  // namespace mit2

@@ -51,6 +51,13 @@ std::vector<uint8_t> synth_lr_tensor_bytes(size_t i, uint64_t base_seed, float s
 const std::vector<SynthSpec>& bigvgan_tensor_specs();
 std::vector<uint8_t> synth_bigvgan_tensor_bytes(size_t i, uint64_t base_seed, float stddev);
 
+// The GPT mel-code decoder's tensors (24 GPT-2 layers, ln_f, final_norm,
+// mel_head, mel and mel-position embeddings), sorted by name, all f16,
+// checkpoint layouts (Conv1D weights [in][out]): N(0, stddev) from
+// base_seed + i; the LayerNorm weights are 1 + N(0, stddev).
+const std::vector<SynthSpec>& gpt_tensor_specs();
+std::vector<uint8_t> synth_gpt_tensor_bytes(size_t i, uint64_t base_seed, float stddev);
+
 // Kaiser-windowed sinc low-pass (cutoff 0.25, half-width 0.3, 12 taps, unit
 // DC gain): the filter of BigVGAN's alias-free activation for ratio 2.
 std::vector<float> kaiser_sinc_filter12();

@@ -150,6 +150,42 @@ void orc_cfm_euler_masked(const orc_model* m, float* x, const float* prompt, con
                           const float* style, const uint32_t* key_mask, uint32_t T, uint32_t P,
                           uint32_t steps, float cfg_rate);
 
+/* ---- GPT mel-code decoder (gpt_oracle.c; runtime/impl/gpt.cpp) ----------- */
+typedef struct orc_gpt orc_gpt;
+orc_gpt* orc_gpt_new(int layers);
+void orc_gpt_free(orc_gpt* m);
+int orc_gpt_set(orc_gpt* m, const char* name, const float* data, uint64_t count);
+int orc_gpt_missing(const orc_gpt* m);
+const char* orc_gpt_last_error(void);
+void orc_gelu_new(const float* x, size_t n, float* out);          /* tokenizer_tests.cpp:3931 */
+void orc_attention_single_query(const float* q, const float* k, const float* v,
+                                uint32_t key_tokens, uint32_t head_dim,
+                                float* out);                       /* tokenizer_tests.cpp:4034 */
+void orc_attention_causal(const float* q, const float* k, const float* v, uint32_t tokens,
+                          uint32_t head_dim, float* out);           /* tokenizer_tests.cpp:4003 */
+void orc_gpt_layer_qkv(const orc_gpt* m, const float* in, uint32_t tokens, uint32_t layer,
+                       float* qkv);                                 /* gpt.cpp:1060 */
+void orc_gpt_block(const orc_gpt* m, const float* in, uint32_t tokens, uint32_t layer,
+                   float* out);                                     /* gpt.cpp:658 */
+void orc_gpt_cached_block_current(const orc_gpt* m, const float* cache_k, const float* cache_v,
+                                  uint32_t cache_tokens, const float* current,
+                                  const float* current_qkv, uint32_t layer,
+                                  float* out);                      /* gpt.cpp:1180 */
+uint32_t orc_gpt_logits(const orc_gpt* m, const float* in, uint32_t tokens, float* final_norm,
+                        float* logits);                             /* gpt.cpp:1310 */
+uint32_t orc_gpt_cached_decode(const orc_gpt* m, const float* input, uint32_t prefix_tokens,
+                               float* ln_f, float* final_norm, float* logits); /* gpt.cpp:1400 */
+typedef struct {
+    uint32_t n_predicted, n_input;
+    int32_t first_stop_step;
+} orc_gpt_greedy_result;
+int orc_gpt_kv_greedy(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens, uint32_t steps,
+                      int hf_generate_positions, uint32_t* predicted, uint32_t* input_tokens,
+                      float* last_logits, orc_gpt_greedy_result* res); /* gpt.cpp:1877 */
+int orc_gpt_greedy_full(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens,
+                        uint32_t steps, uint32_t* predicted, uint32_t* input_tokens,
+                        float* last_logits, orc_gpt_greedy_result* res); /* gpt.cpp:1833 */
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,11 @@ _u32p = ctypes.POINTER(ctypes.c_uint32)
 _lib = None
 
 
+class _GreedyResult(ctypes.Structure):
+    _fields_ = [("n_predicted", ctypes.c_uint32), ("n_input", ctypes.c_uint32),
+                ("first_stop_step", ctypes.c_int32)]
+
+
 def build() -> None:
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
 
@@ -85,6 +90,23 @@ def lib() -> ctypes.CDLL:
                                            _f32p, _f32p]),
             "orc_cfm_euler_masked": (None, [vp, _f32p, _f32p, _f32p, _f32p, _u32p, u32, u32, u32,
                                             f32]),
+            "orc_gpt_new": (vp, [i32]),
+            "orc_gpt_free": (None, [vp]),
+            "orc_gpt_set": (i32, [vp, ctypes.c_char_p, _f32p, u64]),
+            "orc_gpt_missing": (i32, [vp]),
+            "orc_gpt_last_error": (ctypes.c_char_p, []),
+            "orc_gelu_new": (None, [_f32p, ctypes.c_size_t, _f32p]),
+            "orc_attention_single_query": (None, [_f32p, _f32p, _f32p, u32, u32, _f32p]),
+            "orc_attention_causal": (None, [_f32p, _f32p, _f32p, u32, u32, _f32p]),
+            "orc_gpt_layer_qkv": (None, [vp, _f32p, u32, u32, _f32p]),
+            "orc_gpt_block": (None, [vp, _f32p, u32, u32, _f32p]),
+            "orc_gpt_cached_block_current": (None, [vp, _f32p, _f32p, u32, _f32p, _f32p, u32, _f32p]),
+            "orc_gpt_logits": (u32, [vp, _f32p, u32, _f32p, _f32p]),
+            "orc_gpt_cached_decode": (u32, [vp, _f32p, u32, _f32p, _f32p, _f32p]),
+            "orc_gpt_kv_greedy": (i32, [vp, _f32p, u32, u32, i32, _u32p, _u32p, _f32p,
+                                        ctypes.POINTER(_GreedyResult)]),
+            "orc_gpt_greedy_full": (i32, [vp, _f32p, u32, u32, _u32p, _u32p, _f32p,
+                                          ctypes.POINTER(_GreedyResult)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -527,3 +549,117 @@ class BigVGAN:
     def vocoder(self, mel):
         """run_bigvgan_vocoder_cpu (:4058): mel [tokens, 80] -> waveform [256 * tokens]."""
         return self.post(self.body(mel)).reshape(-1)
+
+
+# ---------------------------------------------------------------- GPT decoder
+GPT_W, GPT_VOCAB = 1280, 8194
+
+
+def gelu_new(x) -> np.ndarray:
+    """cpu_gelu_new (tokenizer_tests.cpp:3931)."""
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().orc_gelu_new(P(x), x.size, P(out))
+    return out
+
+
+def attention_single_query(q, k, v) -> np.ndarray:
+    """cpu_attention_single_query (tokenizer_tests.cpp:4034): q [D], k/v [N, D]."""
+    q, k, v = f32(q), f32(k), f32(v)
+    out = np.empty(q.size, np.float32)
+    lib().orc_attention_single_query(P(q), P(k), P(v), k.shape[0], q.size, P(out))
+    return out
+
+
+def attention_causal(q, k, v) -> np.ndarray:
+    """cpu_attention_single_head_causal (tokenizer_tests.cpp:4003): q/k/v [T, D]."""
+    q, k, v = f32(q), f32(k), f32(v)
+    out = np.empty_like(q)
+    lib().orc_attention_causal(P(q), P(k), P(v), q.shape[0], q.shape[1], P(out))
+    return out
+
+
+class GPT:
+    """The reference's fp32 CPU GPT decoder (runtime/impl/gpt.cpp) over the given
+    gpt.* tensors (checkpoint layouts; layers 0..L-1 present)."""
+
+    def __init__(self, tensors: dict):
+        layers = 0
+        while f"gpt.gpt.h.{layers}.ln_1.weight" in tensors:
+            layers += 1
+        self.layers = layers
+        self._h = lib().orc_gpt_new(layers)
+        if not self._h:
+            raise ValueError("GPT oracle: bad layer count")
+        for name, v in tensors.items():
+            if not name.startswith("gpt."):
+                continue
+            a = f32(v)
+            if lib().orc_gpt_set(self._h, name.encode(), P(a), a.size) != 0:
+                raise ValueError(lib().orc_gpt_last_error().decode())
+        if lib().orc_gpt_missing(self._h):
+            raise ValueError(f"GPT oracle: {lib().orc_gpt_missing(self._h)} tensors missing")
+
+    def __del__(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h and _lib is not None:
+            _lib.orc_gpt_free(h)
+
+    def layer_qkv(self, x, layer):
+        """run_gpt_layer_qkv_cpu (gpt.cpp:1060): [T, 1280] -> [T, 3840]."""
+        x = f32(x).reshape(-1, GPT_W)
+        out = np.empty((x.shape[0], 3 * GPT_W), np.float32)
+        lib().orc_gpt_layer_qkv(self._h, P(x), x.shape[0], layer, P(out))
+        return out
+
+    def block(self, x, layer):
+        """run_gpt_transformer_block_cpu_layer (gpt.cpp:658)."""
+        x = f32(x).reshape(-1, GPT_W)
+        out = np.empty_like(x)
+        lib().orc_gpt_block(self._h, P(x), x.shape[0], layer, P(out))
+        return out
+
+    def cached_block_current(self, cache_k, cache_v, current, current_qkv, layer):
+        """run_gpt_cached_block_current_cpu (gpt.cpp:1180)."""
+        ck, cv = f32(cache_k).reshape(-1, GPT_W), f32(cache_v).reshape(-1, GPT_W)
+        cur, cq = f32(current), f32(current_qkv)
+        out = np.empty(GPT_W, np.float32)
+        lib().orc_gpt_cached_block_current(self._h, P(ck), P(cv), ck.shape[0], P(cur), P(cq), layer, P(out))
+        return out
+
+    def logits(self, x):
+        """run_gpt_logits_cpu (gpt.cpp:1310): (final_norm [T, 1280], logits [T, 8194], last argmax)."""
+        x = f32(x).reshape(-1, GPT_W)
+        fn = np.empty_like(x)
+        lg = np.empty((x.shape[0], GPT_VOCAB), np.float32)
+        am = lib().orc_gpt_logits(self._h, P(x), x.shape[0], P(fn), P(lg))
+        return fn, lg, int(am)
+
+    def cached_decode(self, rows, prefix_tokens):
+        """run_gpt_cached_decode_cpu (gpt.cpp:1400): (ln_f, final_norm, logits, argmax)."""
+        x = f32(rows).reshape(-1, GPT_W)
+        ln_f = np.empty(GPT_W, np.float32)
+        fn = np.empty(GPT_W, np.float32)
+        lg = np.empty(GPT_VOCAB, np.float32)
+        am = lib().orc_gpt_cached_decode(self._h, P(x), prefix_tokens, P(ln_f), P(fn), P(lg))
+        return ln_f, fn, lg, int(am)
+
+    def _greedy(self, fn, prefix, steps, *extra):
+        x = f32(prefix).reshape(-1, GPT_W)
+        pred = np.zeros(max(steps, 1), np.uint32)
+        inp = np.zeros(steps + 1, np.uint32)
+        lg = np.zeros(GPT_VOCAB, np.float32)
+        r = _GreedyResult()
+        rc = fn(self._h, P(x), x.shape[0], steps, *extra, PU(pred), PU(inp), P(lg), ctypes.byref(r))
+        if rc != 0:
+            raise ValueError("GPT oracle: position beyond the mel position table")
+        return {"predicted": pred[:r.n_predicted].copy(), "input_tokens": inp[:r.n_input].copy(),
+                "first_stop_step": int(r.first_stop_step), "last_logits": lg if steps > 0 else None}
+
+    def kv_greedy(self, prefix, steps, hf_generate_positions=False):
+        """run_gpt_kv_greedy_cpu (gpt.cpp:1877)."""
+        return self._greedy(lib().orc_gpt_kv_greedy, prefix, steps, 1 if hf_generate_positions else 0)
+
+    def greedy_full(self, prefix, steps):
+        """run_gpt_greedy_cpu (gpt.cpp:1833): the uncached loop (no stop)."""
+        return self._greedy(lib().orc_gpt_greedy_full, prefix, steps)

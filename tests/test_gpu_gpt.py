@@ -1,0 +1,194 @@
+"""GPU parity of the GPT mel-code decoder (runtime/impl/gpt.cpp) through the C
+ABI against the CPU oracle on identical inputs and weights.
+
+The reference holds its Metal decode to max-abs 3e-3 on the last logits and
+identical tokens against its CPU path (run_gpt_kv_greedy_test,
+gpt.cpp:2305-2371), and to 2e-3 on the cached single-row decode
+(run_gpt_kv_decode_test, :1469-1504).  Here the weights are f16 on both
+sides (the checkpoint's precision) and everything else fp32, so the only
+difference is the order of fp32 sums; the bars below are the reference's.
+
+The attention splits its keys into chunks of 64, so prefixes of 63..65 and of
+a few hundred rows exercise one chunk, the chunk boundary and the
+multi-chunk combine.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import sincos_series
+
+pytestmark = pytest.mark.gpu
+
+W = 1280
+LOGITS_TOL = 3e-3   # run_gpt_kv_greedy_test's bar on the last logits (max-abs)
+DECODE_TOL = 2e-3   # run_gpt_kv_decode_test's bar (max-abs)
+
+
+@pytest.fixture(scope="module")
+def gpt24_t(mit2):
+    return mit2.synthetic_gpt_tensors()
+
+
+@pytest.fixture(scope="module")
+def ctx24(mit2, tensors, gpt24_t):
+    c = mit2.Context({**tensors, **gpt24_t}, device=0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def orc24(orc, gpt24_t):
+    return orc.GPT(gpt24_t)
+
+
+@pytest.fixture(scope="module")
+def gpt2_t(mit2):
+    return mit2.synthetic_gpt_tensors(layers=2)
+
+
+@pytest.fixture(scope="module")
+def ctx2(mit2, tensors, gpt2_t):
+    c = mit2.Context({**tensors, **gpt2_t}, device=0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def orc2(orc, gpt2_t):
+    return orc.GPT(gpt2_t)
+
+
+def _prefix(n, seed=None):
+    if seed is None:  # run_gpt_kv_greedy_test's conditioning series (gpt.cpp:2313-2316)
+        return sincos_series(n * W, 0.007, 0.011, 0.045, 0.018, 251).reshape(n, W)
+    return (np.random.default_rng(seed).standard_normal((n, W)) * 0.05).astype(np.float32)
+
+
+def _compare(got, ref, label):
+    err = float(np.abs(got["last_logits"] - ref["last_logits"]).max()) if ref["last_logits"] is not None else 0.0
+    print(f"{label}: tokens {got['predicted'].tolist()[:12]} stop {got['first_stop_step']} "
+          f"logits max-abs {err:.2e} prefill {got['prefill_ms']:.2f} ms decode {got['decode_ms']:.2f} ms",
+          flush=True)
+    assert got["predicted"].tolist() == ref["predicted"].tolist()
+    assert got["input_tokens"].tolist() == ref["input_tokens"].tolist()
+    assert got["first_stop_step"] == ref["first_stop_step"]
+    assert err <= LOGITS_TOL
+
+
+def test_layers(ctx24, ctx2, mit2, tensors):
+    assert ctx24.gpt_layers() == 24 and ctx2.gpt_layers() == 2
+    c = mit2.Context(tensors, device=0)
+    try:
+        assert c.gpt_layers() == 0
+        with pytest.raises(mit2.Mit2CfmError) as e:
+            c.gpt_kv_greedy(_prefix(2), 1)
+        assert e.value.status == mit2.E_MODEL
+    finally:
+        c.close()
+
+
+def test_cached_decode_reference_input(ctx24, orc24):
+    """run_gpt_kv_decode_test (gpt.cpp:1469-1504): 3 prefix rows + 1, its series."""
+    x = sincos_series(4 * W, 0.009, 0.013, 0.065, 0.021, 307).reshape(4, W)
+    ln_f, fn, logits, am = ctx24.gpt_cached_decode(x, 3)
+    r_ln_f, r_fn, r_logits, r_am = orc24.cached_decode(x, 3)
+    errs = [float(np.abs(a - b).max()) for a, b in ((ln_f, r_ln_f), (fn, r_fn), (logits, r_logits))]
+    print(f"cached decode: ln_f {errs[0]:.2e} final_norm {errs[1]:.2e} logits {errs[2]:.2e} argmax {am}/{r_am}",
+          flush=True)
+    assert max(errs) <= DECODE_TOL and am == r_am
+
+
+@pytest.mark.parametrize("P,steps,hf", [(10, 3, False), (20, 12, True), (100, 8, False)])
+def test_kv_greedy_matches_oracle_24_layers(ctx24, orc24, P, steps, hf):
+    prefix = _prefix(P)
+    print(f"kv greedy 24 layers P={P} steps={steps} hf={hf}", flush=True)
+    _compare(ctx24.gpt_kv_greedy(prefix, steps, hf), orc24.kv_greedy(prefix, steps, hf), "  24 layers")
+
+
+@pytest.mark.parametrize("P,steps", [(0, 3), (1, 2), (62, 4), (63, 3), (64, 3), (65, 2), (300, 10)])
+def test_kv_greedy_attention_chunks(ctx2, orc2, P, steps):
+    prefix = _prefix(P, seed=P)
+    print(f"kv greedy 2 layers P={P} steps={steps}", flush=True)
+    _compare(ctx2.gpt_kv_greedy(prefix, steps), orc2.kv_greedy(prefix, steps), "  2 layers")
+
+
+def test_zero_steps(ctx2):
+    r = ctx2.gpt_kv_greedy(_prefix(5), 0)
+    assert r["predicted"].size == 0 and r["input_tokens"].tolist() == [8192]
+    assert r["first_stop_step"] == -1 and r["last_logits"] is None
+
+
+def test_repeatable_and_independent_of_earlier_calls(ctx2):
+    prefix = _prefix(40, seed=9)
+    a = ctx2.gpt_kv_greedy(prefix, 9)
+    ctx2.gpt_kv_greedy(_prefix(500, seed=10), 30)  # a longer call in between grows the caches
+    b = ctx2.gpt_kv_greedy(prefix, 9)
+    assert a["predicted"].tolist() == b["predicted"].tolist()
+    assert np.array_equal(a["last_logits"], b["last_logits"])
+
+
+def test_greedy_last_step_equals_cached_decode(ctx24, gpt24_t):
+    """The decode loop's last logits equal a cached decode of the same sequence
+    (prefix rows, then each input token's embedding at its position)."""
+    prefix = _prefix(150, seed=11)
+    r = ctx24.gpt_kv_greedy(prefix, 40)
+    toks = r["input_tokens"]
+    emb = np.asarray(gpt24_t["gpt.mel_embedding.weight"], np.float32)
+    pos = np.asarray(gpt24_t["gpt.mel_pos_embedding.emb.weight"], np.float32)
+    n = len(r["predicted"])
+    rows = np.concatenate([prefix, np.stack([emb[toks[t]] + pos[t] for t in range(n)])])
+    _, _, logits, am = ctx24.gpt_cached_decode(rows, len(rows) - 1)
+    err = float(np.abs(logits - r["last_logits"]).max())
+    print(f"greedy ({n} steps, {r['decode_ms']:.2f} ms) vs cached decode: logits max-abs {err:.2e}", flush=True)
+    assert am == r["predicted"][-1] and err <= 1e-4
+
+
+def _with_stop_bias(t, delta):
+    t = dict(t)
+    b = np.asarray(t["gpt.mel_head.bias"], np.float32).copy()
+    b[8193] += np.float32(delta)
+    t["gpt.mel_head.bias"] = b
+    return t
+
+
+def _mid_run_stop(g, steps):
+    """A prefix and a stop-token bias increase under which the stop token wins
+    at a step s in 1..steps-1 and at no earlier step (None when no seed tried
+    offers a margin of 0.02 either way)."""
+    for seed in range(12, 40):
+        prefix = _prefix(12, seed=seed)
+        gaps = []  # per step: best other token's logit minus the stop token's
+        for s in range(1, steps + 1):
+            lg = g.kv_greedy(prefix, s)["last_logits"]
+            gaps.append(float(np.delete(lg, 8193).max() - lg[8193]))
+        for s in range(1, steps):
+            earlier = min(gaps[:s])
+            if 0 < gaps[s] < earlier - 0.04:
+                return prefix, s, 0.5 * (gaps[s] + earlier)
+    return None
+
+
+def test_stop_token(mit2, orc, tensors, gpt2_t):
+    """A stop at step 0, and one in the middle of a run (inside a group of
+    steps between the host's stop-flag checks): the bias of the stop token is
+    raised just enough that it wins at one later step and at no earlier one."""
+    found = _mid_run_stop(orc.GPT(gpt2_t), 7)
+    assert found is not None, "no seed offers a clean mid-run stop"
+    prefix, step, delta = found
+    for delta, expect in ((100.0, 0), (delta, step)):
+        t = _with_stop_bias(gpt2_t, delta)
+        ref = orc.GPT(t).kv_greedy(prefix, 12)
+        assert ref["first_stop_step"] == expect
+        c = mit2.Context({**tensors, **t}, device=0)
+        try:
+            _compare(c.gpt_kv_greedy(prefix, 12), ref, f"  stop at {expect}")
+        finally:
+            c.close()
+
+
+def test_position_table_bound(ctx2, mit2):
+    with pytest.raises(mit2.Mit2CfmError) as e:
+        ctx2.gpt_kv_greedy(_prefix(2), 1818, hf_generate_positions=True)
+    assert e.value.status == mit2.E_ARG
