@@ -45,6 +45,14 @@ Prints ONE JSON line.  Extra fields:
                 time per call from HIP events, its real-time factor, and the
                 reference's published time for that segment on its own
                 hardware (a different machine and the real weights).
+  gpt_decode    the GPT mel-code decoder (the stage that makes the semantic
+                codes) on the GPU: greedy decode of 553 codes after a
+                150-row prefix with the 24-layer synthetic model (seed
+                20240608); device time of the prefill and the decode loop,
+                ms per code, the weight stream it implies, the reference's
+                published 5.5 ms per code, its dominant GEMV's bandwidth
+                (c_fc, cycling the layers' weights, HIP events) against HBM
+                peak, and the oracle's decode step on the host cores.
 """
 from __future__ import annotations
 
@@ -86,6 +94,9 @@ def parse():
     p.add_argument("--voc-calls", type=int, default=10, help="timed vocoder calls (0 = skip)")
     p.add_argument("--acoustic-calls", type=int, default=5,
                    help="timed acoustic-stage calls (0 = skip; needs the vocoder)")
+    p.add_argument("--gpt-codes", type=int, default=553,
+                   help="mel codes of the timed GPT greedy decode (0 = skip)")
+    p.add_argument("--gpt-prefix", type=int, default=150, help="prefix rows of the GPT decode")
     p.add_argument("--calib-mib", type=int, default=256,
                    help="size of the counter-calibration copy (0 = skip)")
     return p.parse_args()
@@ -177,6 +188,73 @@ def vocoder_cpu_baseline(bv_tensors, mel, threads):
     s = time.perf_counter() - t0
     return {"value": round(256 * frames / s, 1), "unit": "samples/s", "cores": threads, "kind": "port",
             "sample": f"the vocoder on the first {frames} mel frames ({256 * frames} samples)"}
+
+
+def gpt_cpu_baseline(gpt_tensors, threads):
+    """The oracle's cached decode step (24 layers): the time of 5 greedy steps
+    minus the time of 1, after the same 8-row prefix, over 4."""
+    import numpy as np
+    from oracle import oracle
+
+    oracle.set_threads(threads)
+    g = oracle.GPT(gpt_tensors)
+    prefix = (np.random.default_rng(3).standard_normal((8, 1280)) * 0.05).astype(np.float32)
+    t0 = time.perf_counter()
+    g.kv_greedy(prefix, 1)
+    t1 = time.perf_counter()
+    g.kv_greedy(prefix, 5)
+    t2 = time.perf_counter()
+    per_token = ((t2 - t1) - (t1 - t0)) / 4
+    return {"value": round(1.0 / per_token, 2), "unit": "mel codes/s", "cores": threads, "kind": "port",
+            "sample": "the oracle's 24-layer cached decode: (time of 5 greedy steps - time of 1) / 4 "
+                      "after an 8-row prefix"}
+
+
+def gpt_section(a, mit2cfm, tensors, torch):
+    """GPT mel-code decoder: greedy decode of a.gpt_codes codes after an
+    a.gpt_prefix-row prefix (24 layers, synthetic weights), and its dominant
+    GEMV's bandwidth."""
+    import numpy as np
+
+    gpt_tensors = mit2cfm.synthetic_gpt_tensors()
+    ctx = mit2cfm.Context({**tensors, **gpt_tensors}, device=0)
+    prefix = (np.random.default_rng(2).standard_normal((a.gpt_prefix, 1280)) * 0.05).astype(np.float32)
+    ctx.gpt_kv_greedy(prefix, 16)  # warm-up (captures the step graphs)
+    runs = [ctx.gpt_kv_greedy(prefix, a.gpt_codes) for _ in range(2)]
+    r = min(runs, key=lambda q: q["decode_ms"])
+    n = len(r["predicted"])
+    ms_tok = r["decode_ms"] / n
+    step_bytes = mit2cfm.gpt_step_bytes(24)
+    # the dominant GEMV (c_fc, 5120 x 1280, LayerNorm prologue, gelu_new), cycling the 24 layers' weights
+    stream = torch.cuda.ExternalStream(ctx.stream, device=torch.device("cuda:0"))
+    name, kbytes = ctx.gpt_profile_launch(2, 24)
+    ctx.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    launches = 240
+    e0.record(stream)
+    ctx.gpt_profile_launch(2, launches)
+    e1.record(stream)
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    k_us = e0.elapsed_time(e1) / launches * 1e3
+    achieved = kbytes / (k_us / 1e6) / 1e9
+    ctx.close()
+    out = {"workload": f"GPT-2 24 x 1280 greedy decode: {a.gpt_prefix}-row prefix, {a.gpt_codes} codes "
+                       "(synthetic f16 weights seed 20240608)",
+           "codes": n, "first_stop_step": r["first_stop_step"],
+           "prefill_ms": round(r["prefill_ms"], 3), "decode_ms": round(r["decode_ms"], 3),
+           "ms_per_code": round(ms_tok, 4), "codes_per_s": round(1e3 / ms_tok, 1),
+           "weight_gb_per_code": round(step_bytes / 1e9, 4),
+           "weight_stream_gb_s": round(step_bytes / (ms_tok / 1e3) / 1e9, 1),
+           "reference_published": {"ms_per_code": 5.5, "hardware": "Apple M3 Ultra (Metal, ICB greedy decode)",
+                                   "source": "docs/evolution.md:77"},
+           "speedup_vs_published": round(5.5 / ms_tok, 1),
+           "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                        "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                        "avg_launch_us": round(k_us, 2), "algorithmic_bytes": int(kbytes)}}
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = gpt_cpu_baseline(gpt_tensors, cpu_threads(a))
+    return out
 
 
 def main():
@@ -423,6 +501,8 @@ def main():
         result["vocoder"] = voc
     if ac:
         result["acoustic_stage"] = ac
+    if a.gpt_codes:
+        result["gpt_decode"] = gpt_section(a, mit2cfm, tensors, torch)
     result["context_create_s"] = {"from_host_tensors": round(create_s, 3), "from_device_image": round(create_img_s, 3),
                                   "image_mib": round(img_mb, 1)}
     if not a.no_cpu_baseline:

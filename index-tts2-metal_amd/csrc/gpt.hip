@@ -9,7 +9,9 @@
 //   embed      x = mel_embedding[token] + mel_pos_embedding[position]
 //              (or a prefix row, while the prefix is prefilled)
 //   per layer  c_attn   qkv = W_attn LN1(x) + b; q -> q buffer, k and v -> the
-//                       caches at row kv (no copy: the cache IS the output)
+//                       caches at row kv (no copy: the cache IS the output;
+//                       head-major [head][row][64], so a head's keys are
+//                       contiguous)
 //              attention  softmax(q K^T / 8) V over the kv + 1 cached rows,
 //                       per head, split over chunks of 64 keys
 //              c_proj   x += W_proj att + b
@@ -54,9 +56,9 @@ namespace {
 constexpr int kW = 1280, kQKV = 3840, kMLP = 5120, kHeads = 20, kHD = 64;
 constexpr int kVocab = GptDecoder::kVocab, kPos = GptDecoder::kPositions;
 constexpr int kStart = (int)GptDecoder::kStartToken, kStop = (int)GptDecoder::kStopToken;
-constexpr int kChunk = 128;   // keys per attention split
-constexpr int kPartF = 2 + kHD;  // per split: max, sum, unnormalised output
+constexpr int kChunk = 256;   // keys per attention chunk
 constexpr int kStepsPerCheck = 8;  // decode steps replayed between stop-flag reads
+constexpr int kPrefillRows = 8;    // prefix rows per prefill chunk
 
 // Device-side decode state.
 struct GptState {
@@ -72,7 +74,8 @@ struct GptState {
   int32_t max_pred;   // capacity of the predicted array (inputs: + 1)
   int32_t cap;        // rows of each key/value cache
   int32_t rows;       // rows of the prefix buffer
-  int32_t pad[4];
+  int32_t pend;       // prefix rows the prefill chunks cover (rows 0..pend-1)
+  int32_t pad[3];
 };
 
 enum { PRO_PLAIN = 0, PRO_LN = 1, PRO_LN2 = 2 };
@@ -253,8 +256,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
       } else {
         const int kv = a.st->kv;
         if (kv < a.st->cap) {
-          if (r < 2 * kW) a.kc[(size_t)kv * kW + (r - kW)] = v;
-          else a.vc[(size_t)kv * kW + (r - 2 * kW)] = v;
+          const int c = r - (r < 2 * kW ? kW : 2 * kW);  // head c / 64, dim c % 64
+          float* cache = r < 2 * kW ? a.kc : a.vc;
+          cache[((size_t)(c >> 6) * a.st->cap + kv) * kHD + (c & 63)] = v;
         }
       }
     } else {
@@ -288,6 +292,125 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
       a.blk_idx[blockIdx.x] = bi;
     }
   }
+}
+
+// The prefill's multi-row form of gemv_kernel: y[m] = W pro(x[m]) + b for the
+// rows m < mrows = min(kPrefillRows, pend - kv) of a prefix chunk (rows kv..),
+// so each weight row is read once per chunk instead of once per prefix row.
+// The chunk's inputs (normalised first, for the LayerNorm prologue) are
+// staged in LDS; every sum runs in gemv_kernel's order (the same lane
+// layout, the same two partial sums, the same group reduction and the same
+// LayerNorm statistics), so a prefix row gets the same values either way.
+template <int K, int LPR, int WAVES, int PRO, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs a) {
+  constexpr int MR = kPrefillRows;
+  constexpr int RPW = 64 / LPR;
+  constexpr int CH = K / (8 * LPR);
+  constexpr int ROWS = WAVES * RPW;
+  static_assert(K % (8 * LPR) == 0, "K must be a multiple of 8 * LPR");
+  static_assert(PRO != PRO_LN2 && EPI != EPI_LOGITS, "the prefill has no head");
+  static_assert(PRO == PRO_PLAIN || K == kW, "LayerNorm prologues take the 1280-wide stream");
+  __shared__ float4 xs[MR][K / 4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, j = lane % LPR;
+  const int kv = a.st->kv;
+  const int mrows = min(MR, a.st->pend - kv);
+  const int r = blockIdx.x * ROWS + wave * RPW + sub;
+
+  half8 w[CH];
+  {
+    const half8* src = reinterpret_cast<const half8*>(a.w + (size_t)min(r, a.N - 1) * K) + j;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) w[c] = src[c * LPR];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // stage the chunk's inputs (rows past mrows are zeros)
+  if constexpr (PRO == PRO_PLAIN) {
+    for (int i = threadIdx.x; i < MR * (K / 4); i += WAVES * 64) {
+      const int mm = i / (K / 4), k4 = i % (K / 4);
+      xs[mm][k4] = mm < mrows ? reinterpret_cast<const float4*>(a.x + (size_t)mm * K)[k4]
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  } else {
+    // one wave per row, lanes laid out as a 32-lane group (both halves
+    // compute the same values; the first half stores them)
+    constexpr int CH32 = K / (8 * 32);
+    const int jj = lane & 31;
+    for (int mm = wave; mm < MR; mm += WAVES) {
+      float v[CH32][8];
+      if (mm < mrows) {
+        float g[CH32][8], b[CH32][8];
+        load_chunks<32, CH32>(v, a.x + (size_t)mm * K, jj);
+        load_chunks<32, CH32>(g, a.g1, jj);
+        load_chunks<32, CH32>(b, a.b1, jj);
+        group_layernorm<32, CH32>(v, g, b);
+      } else {
+#pragma unroll
+        for (int c = 0; c < CH32; ++c)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[c][e] = 0.f;
+      }
+      if (lane < 32) {
+#pragma unroll
+        for (int c = 0; c < CH32; ++c) {
+          xs[mm][2 * (jj + 32 * c)] = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+          xs[mm][2 * (jj + 32 * c) + 1] = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  float wf[CH][8];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wf[c][e] = (float)w[c][e];
+  // one chunk row at a time (hoisting every row's LDS reads costs registers)
+#pragma unroll
+  for (int mm = 0; mm < MR; ++mm) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int q4 = 2 * (j + c * LPR);
+      const float4 lo = xs[mm][q4], hi = xs[mm][q4 + 1];
+      s0 += wf[c][0] * lo.x; s1 += wf[c][1] * lo.y;
+      s0 += wf[c][2] * lo.z; s1 += wf[c][3] * lo.w;
+      s0 += wf[c][4] * hi.x; s1 += wf[c][5] * hi.y;
+      s0 += wf[c][6] * hi.z; s1 += wf[c][7] * hi.w;
+    }
+    const float acc = group_sum<LPR>(s0 + s1);
+    if (j == 0 && r < a.N && mm < mrows) {
+      const float v = acc + a.bias[r];
+      if constexpr (EPI == EPI_GELU) {
+        a.y[(size_t)mm * a.N + r] = gelu_new(v);
+      } else if constexpr (EPI == EPI_RES) {
+        a.y[(size_t)mm * a.N + r] += v;
+      } else {
+        if (r < kW) {
+          a.q[(size_t)mm * kW + r] = v;
+        } else if (kv + mm < a.st->cap) {
+          const int c = r - (r < 2 * kW ? kW : 2 * kW);  // head c / 64, dim c % 64
+          float* cache = r < 2 * kW ? a.kc : a.vc;
+          cache[((size_t)(c >> 6) * a.st->cap + kv + mm) * kHD + (c & 63)] = v;
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Rows kv .. kv + mrows - 1 of the prefix into the chunk buffer.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const GptState* st, const float* rows, float* x) {
+  const int mrows = min(kPrefillRows, st->pend - st->kv);
+  const float4* src = reinterpret_cast<const float4*>(rows + (size_t)st->kv * kW);
+  for (int i = threadIdx.x; i < mrows * (kW / 4); i += 256) reinterpret_cast<float4*>(x)[i] = src[i];
+}
+
+// The chunk is done: its rows join the caches.
+__global__ void advance_rows_kernel(GptState* st) {
+  st->kv += max(0, min(kPrefillRows, st->pend - st->kv));
 }
 
 // argmax_row (gpt.cpp:1297-1308), second stage: the first maximum over the
@@ -366,42 +489,56 @@ __global__ __launch_bounds__(320) void embed_kernel(const GptState* st, const fl
 // Cached attention of the current query (run_gpt_cached_attention_current_cpu,
 // gpt.cpp:1147-1170, with cpu_attention_single_query, tokenizer_tests.cpp:
 // 4034-4060) over the st->kv + 1 cache rows (the current row included: the
-// c_attn kernel already wrote it).  Block (head h, split s) handles keys
-// 128 s .. 128 s + 127 with 256 threads, every global load of a phase issued
-// before the first is used (the kernel is latency-bound): the scores (8 lanes
-// per key, 8 floats each), their max m and sum l of exp(score - m), and the
-// unnormalised output sum_t exp(score_t - m) v_t (16 lanes per key, 4 dims
-// each).  With one split the block writes the output; otherwise the last
-// split of a head to finish combines the splits.
-__global__ __launch_bounds__(256) void attn_decode_kernel(const float* q, const float* kc, const float* vc,
-                                                          const GptState* st, float* part,
-                                                          unsigned* counters, float* out, int nsplit_max) {
-  const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
-  const int kvn = min(st->kv + 1, st->cap);
-  const int nsplit = (kvn + kChunk - 1) / kChunk;
-  if (s >= nsplit) return;
-  const int t0 = s * kChunk, n = min(kChunk, kvn - t0);
+// c_attn kernel already wrote it).  One block of 512 threads per head (and,
+// in a prefill chunk, per query row: blockIdx.z) walks the keys in chunks of
+// 256 with the softmax kept online -- running max m, sum l and output o,
+// rescaled by exp(m_old - m_new) per chunk, the same sums regrouped.  A
+// chunk's key and value loads are all issued together (the kernel is
+// latency-bound; up to 256 keys cost one round trip).  Scores: 8 lanes per
+// key, 8 dims each; the output: 16 lanes per key, 4 dims each.  No block
+// waits for another.
+constexpr int kAttnThreads = 512;
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float* q, const float* kc,
+                                                                   const float* vc, const GptState* st,
+                                                                   float* out) {
+  constexpr int kWaves = kAttnThreads / 64;
+  constexpr int kKeysPerPass = kAttnThreads / 8, kPass = kChunk / kKeysPerPass;
+  constexpr int kVKeysPerPass = kAttnThreads / 16, kVPass = kChunk / kVKeysPerPass;
+  constexpr int kGroups = kAttnThreads / 16;  // output key groups
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int qrow = blockIdx.z;  // the query row of a prefill chunk (0 in a decode step)
+  if (gridDim.z > 1 && qrow >= min((int)gridDim.z, st->pend - st->kv)) return;
+  q += (size_t)qrow * kW;
+  out += (size_t)qrow * kW;
+  const int kvn = min(st->kv + qrow + 1, st->cap);
+  const int nchunks = (kvn + kChunk - 1) / kChunk;
   __shared__ float sc[kChunk];
-  __shared__ float4 red[16][kHD / 4];
-  __shared__ float wm[4], wl[4];
-  __shared__ int is_last;
-  const float* kh = kc + (size_t)t0 * kW + h * kHD;
-  const float* vh = vc + (size_t)t0 * kW + h * kHD;
+  __shared__ float4 red[kGroups][kHD / 4];
+  __shared__ float wm[kWaves], wl[kWaves];
+  // head-major caches: head h's rows are contiguous, [cap][64]
+  const float* kh = kc + (size_t)h * st->cap * kHD;
+  const float* vh = vc + (size_t)h * st->cap * kHD;
+  const int g = tid >> 3, e = tid & 7;       // scores: key group, dims 8 e ..
+  const int d4 = tid & 15, g16 = tid >> 4;   // output: dims 4 d4 .., key group
+  const int lane = tid & 63, wave = tid >> 6;
+  const float4* q4 = reinterpret_cast<const float4*>(q + h * kHD) + 2 * e;
+  const float4 qa = q4[0], qb = q4[1];
 
-  // scores: lane e (of 8) of key group g covers dims 8 e .. 8 e + 7
-  {
-    const int g = tid >> 3, e = tid & 7;
-    const float4* q4 = reinterpret_cast<const float4*>(q + h * kHD) + 2 * e;
-    const float4 qa = q4[0], qb = q4[1];
-    constexpr int kPass = kChunk / 32;
-    float4 ka[kPass], kb[kPass];
+  float m_run = -INFINITY, l_run = 0.f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int c = 0; c < nchunks; ++c) {
+    const int t0 = c * kChunk, n = min(kChunk, kvn - t0), last = kvn - 1;
+    float4 ka[kPass], kb[kPass], vv[kVPass];  // past the end: re-read the last key (dropped)
 #pragma unroll
     for (int it = 0; it < kPass; ++it) {
-      const int i = min(g + 32 * it, n - 1);  // past the end: re-read the last key, dropped below
-      const float4* k4 = reinterpret_cast<const float4*>(kh + (size_t)i * kW) + 2 * e;
+      const float4* k4 =
+          reinterpret_cast<const float4*>(kh + (size_t)min(t0 + g + kKeysPerPass * it, last) * kHD) + 2 * e;
       ka[it] = k4[0];
       kb[it] = k4[1];
     }
+#pragma unroll
+    for (int it = 0; it < kVPass; ++it)
+      vv[it] = reinterpret_cast<const float4*>(vh + (size_t)min(t0 + g16 + kVKeysPerPass * it, last) * kHD)[d4];
 #pragma unroll
     for (int it = 0; it < kPass; ++it) {
       float d = ((qa.x * ka[it].x + qa.y * ka[it].y) + (qa.z * ka[it].z + qa.w * ka[it].w)) +
@@ -409,110 +546,57 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* q, const 
       d += __shfl_xor(d, 4, kWave);
       d += __shfl_xor(d, 2, kWave);
       d += __shfl_xor(d, 1, kWave);
-      if (e == 0 && g + 32 * it < n) sc[g + 32 * it] = d * 0.125f;  // 1 / sqrt(64)
+      const int i = g + kKeysPerPass * it;
+      if (e == 0 && i < n) sc[i] = d * 0.125f;  // 1 / sqrt(64)
     }
-  }
-  // the value loads do not depend on the scores: issue them now
-  const int d4 = tid & 15, g16 = tid >> 4;
-  constexpr int kVPass = kChunk / 16;
-  float4 vv[kVPass];
+    __syncthreads();
+    // chunk max (two scores per thread of the first kChunk / 2), then the new running max
+    float v0 = -INFINITY, v1 = -INFINITY;
+    if (tid < kChunk / 2) {
+      v0 = 2 * tid < n ? sc[2 * tid] : -INFINITY;
+      v1 = 2 * tid + 1 < n ? sc[2 * tid + 1] : -INFINITY;
+    }
+    float mc = fmaxf(v0, v1);
 #pragma unroll
-  for (int it = 0; it < kVPass; ++it) {
-    const int i = min(g16 + 16 * it, n - 1);
-    vv[it] = reinterpret_cast<const float4*>(vh + (size_t)i * kW)[d4];
-  }
-  __syncthreads();
-  // max and sum over the chunk (two values per lane of each wave, then the 4 waves)
-  const int lane = tid & 63, wave = tid >> 6;
-  float v0 = -INFINITY, v1 = -INFINITY;
-  if (tid < kChunk / 2) {
-    v0 = 2 * tid < n ? sc[2 * tid] : -INFINITY;
-    v1 = 2 * tid + 1 < n ? sc[2 * tid + 1] : -INFINITY;
-  }
-  float m = fmaxf(v0, v1);
+    for (int off = 32; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off, kWave));
+    if (lane == 0) wm[wave] = mc;
+    __syncthreads();
+    float m_new = m_run;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-  if (lane == 0) wm[wave] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-  float l = 0.f;
-  if (tid < kChunk / 2) {
-    const float p0 = 2 * tid < n ? expf(v0 - m) : 0.f;
-    const float p1 = 2 * tid + 1 < n ? expf(v1 - m) : 0.f;
-    sc[2 * tid] = p0;
-    sc[2 * tid + 1] = p1;
-    l = p0 + p1;
-  }
-  l = warp_sum(l);
-  if (lane == 0) wl[wave] = l;
-  __syncthreads();
-  l = (wl[0] + wl[1]) + (wl[2] + wl[3]);
-  // o = sum_t p_t v_t: thread (d4, g16) sums keys g16, g16 + 16, ...
-  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int w2 = 0; w2 < kWaves; ++w2) m_new = fmaxf(m_new, wm[w2]);
+    const float scale = expf(m_run - m_new);  // 0 on the first chunk
+    float lc = 0.f;
+    if (tid < kChunk / 2) {
+      const float p0 = 2 * tid < n ? expf(v0 - m_new) : 0.f;
+      const float p1 = 2 * tid + 1 < n ? expf(v1 - m_new) : 0.f;
+      sc[2 * tid] = p0;
+      sc[2 * tid + 1] = p1;
+      lc = p0 + p1;
+    }
+    lc = warp_sum(lc);
+    if (lane == 0) wl[wave] = lc;
+    __syncthreads();
+    float lsum = 0.f;
 #pragma unroll
-  for (int it = 0; it < kVPass; ++it) {
-    const int i = g16 + 16 * it;
-    const float p = i < n ? sc[i] : 0.f;
-    o.x += p * vv[it].x; o.y += p * vv[it].y; o.z += p * vv[it].z; o.w += p * vv[it].w;
+    for (int w2 = 0; w2 < kWaves; ++w2) lsum += wl[w2];
+    l_run = l_run * scale + lsum;
+    o.x *= scale; o.y *= scale; o.z *= scale; o.w *= scale;
+#pragma unroll
+    for (int it = 0; it < kVPass; ++it) {
+      const int i = g16 + kVKeysPerPass * it;
+      const float p = i < n ? sc[i] : 0.f;
+      o.x += p * vv[it].x; o.y += p * vv[it].y; o.z += p * vv[it].z; o.w += p * vv[it].w;
+    }
+    m_run = m_new;
+    __syncthreads();  // sc, wm and wl are rewritten by the next chunk
   }
   red[g16][d4] = o;
   __syncthreads();
-  float od = 0.f;  // output dim tid (tid < 64): the 16 key groups
   if (tid < kHD) {
+    float od = 0.f;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) od += reinterpret_cast<const float*>(&red[g][0])[tid];
-  }
-  if (nsplit == 1) {
-    if (tid < kHD) out[h * kHD + tid] = od / l;
-    return;
-  }
-  float* pp = part + ((size_t)h * nsplit_max + s) * kPartF;
-  if (tid < kHD) pp[2 + tid] = od;
-  if (tid == 0) { pp[0] = m; pp[1] = l; }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = atomicAdd(&counters[h], 1u) == (unsigned)(nsplit - 1);
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  // combine: M = max m_s, out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s;
-  // thread (d = tid % 64, q = tid / 64) takes splits q, q + 4, ...
-  const float* ph = part + (size_t)h * nsplit_max * kPartF;
-  __shared__ float sm[4][kHD + 2];
-  float M = -INFINITY;
-  for (int s2 = tid; s2 < nsplit; s2 += 256) M = fmaxf(M, ph[(size_t)s2 * kPartF]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
-  if (lane == 0) wm[wave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-  const int d = tid & 63, qd = tid >> 6;
-  float L = 0.f, O = 0.f;
-  for (int s2 = qd; s2 < nsplit; s2 += 16) {
-    float mm[4], ll[4], oo[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {  // four splits per round trip
-      const int sx = min(s2 + 4 * u, nsplit - 1);
-      mm[u] = ph[(size_t)sx * kPartF];
-      ll[u] = ph[(size_t)sx * kPartF + 1];
-      oo[u] = ph[(size_t)sx * kPartF + 2 + d];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (s2 + 4 * u < nsplit) {
-        const float f = expf(mm[u] - M);
-        L += f * ll[u];
-        O += f * oo[u];
-      }
-    }
-  }
-  sm[qd][d] = O;
-  if (d == 0) sm[qd][kHD] = L;
-  __syncthreads();
-  if (tid < kHD) {
-    const float Ls = (sm[0][kHD] + sm[1][kHD]) + (sm[2][kHD] + sm[3][kHD]);
-    out[h * kHD + tid] = ((sm[0][tid] + sm[1][tid]) + (sm[2][tid] + sm[3][tid])) / Ls;
-    if (tid == 0) counters[h] = 0u;
+    for (int gg = 0; gg < kGroups; ++gg) od += reinterpret_cast<const float*>(&red[gg][0])[tid];
+    out[h * kHD + tid] = od / l_run;
   }
 }
 
@@ -551,6 +635,14 @@ void launch_fc(const GemvArgs& a, hipStream_t s) { launch_gemv<kW, GPT_FC_SHAPE,
 void launch_mlp_proj(const GemvArgs& a, hipStream_t s) { launch_gemv<kMLP, GPT_MP_SHAPE, PRO_PLAIN, EPI_RES>(a, s); }
 void launch_head(const GemvArgs& a, hipStream_t s) { launch_gemv<kW, GPT_HEAD_SHAPE, PRO_LN2, EPI_LOGITS>(a, s); }
 
+// The prefill chunk's GEMVs (lanes per row, waves per block).
+template <int K, int LPR, int WAVES, int PRO, int EPI>
+void launch_rows(const GemvArgs& a, hipStream_t s) {
+  constexpr int rows = WAVES * (64 / LPR);
+  hipLaunchKernelGGL((gemv_rows_kernel<K, LPR, WAVES, PRO, EPI>), dim3((a.N + rows - 1) / rows), dim3(WAVES * 64), 0,
+                     s, a);
+}
+
 inline size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
 }  // namespace
@@ -574,14 +666,13 @@ struct GptDecoder::Impl {
   int cap = 0;       // key/value cache rows
   int rows_cap = 0;  // prefix rows
   int pred_cap = 0;  // predicted tokens
-  int nsplit_max = 0;
   GptState* st = nullptr;
   uint32_t *predicted = nullptr, *inputs = nullptr;
-  float *x, *q, *att, *fc, *logits, *lnf, *fn, *blk_val, *part, *kc, *vc, *rows;
+  float *x, *q, *att, *fc, *logits, *lnf, *fn, *blk_val, *kc, *vc, *rows;
+  float *xr, *qr, *attr, *fcr;  // a prefill chunk's rows: [8][1280] x3, [8][5120]
   int* blk_idx;
-  unsigned* counters;  // [kHeads]: the attention's last-split counters
   GptState* host_state = nullptr;  // pinned
-  hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};  // row, row + head, token + head
+  hipGraphExec_t graph[4] = {nullptr, nullptr, nullptr, nullptr};  // row, row + head, token + head, chunk
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   bool use_graph = true;  // env MIT2CFM_GRAPH=0: launch every kernel directly (for profilers)
 
@@ -631,13 +722,12 @@ struct GptDecoder::Impl {
     cap = (cap + kChunk - 1) / kChunk * kChunk;
     rows_cap = std::max(std::max(prefix_rows, rows_cap), 16);
     pred_cap = std::max(std::max(steps, pred_cap), 64);
-    nsplit_max = cap / kChunk;
     const size_t f = sizeof(float);
     size_t bytes = align256(sizeof(GptState)) + align256((size_t)pred_cap * 4) +
                    align256(((size_t)pred_cap + 1) * 4) + 3 * align256(kW * f) + align256(kMLP * f) +
                    align256(kVocab * f) + 2 * align256(kW * f) + align256((size_t)head_blocks() * f) +
-                   align256((size_t)head_blocks() * 4) + align256(kHeads * 4) +
-                   align256((size_t)kHeads * nsplit_max * kPartF * f) +
+                   align256((size_t)head_blocks() * 4) +
+                   3 * align256((size_t)kPrefillRows * kW * f) + align256((size_t)kPrefillRows * kMLP * f) +
                    2 * align256((size_t)L * cap * kW * f) + align256((size_t)rows_cap * kW * f);
     ws.reserve(bytes);
     st = static_cast<GptState*>(ws.take(sizeof(GptState)));
@@ -652,13 +742,13 @@ struct GptDecoder::Impl {
     fn = static_cast<float*>(ws.take(kW * f));
     blk_val = static_cast<float*>(ws.take((size_t)head_blocks() * f));
     blk_idx = static_cast<int*>(ws.take((size_t)head_blocks() * 4));
-    counters = static_cast<unsigned*>(ws.take(kHeads * 4));
-    part = static_cast<float*>(ws.take((size_t)kHeads * nsplit_max * kPartF * f));
+    xr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
+    qr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
+    attr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
+    fcr = static_cast<float*>(ws.take((size_t)kPrefillRows * kMLP * f));
     kc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
     vc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
     rows = static_cast<float*>(ws.take((size_t)rows_cap * kW * f));
-    // The last-block counters start at zero; every user resets its own.
-    GPT_OK(hipMemsetAsync(counters, 0, kHeads * 4, s));
     GPT_OK(hipStreamSynchronize(s));
   }
 
@@ -680,8 +770,7 @@ struct GptDecoder::Impl {
       a.w = w.attn_w; a.bias = w.attn_b; a.N = kQKV; a.x = x; a.g1 = w.ln1_w; a.b1 = w.ln1_b;
       a.q = q; a.kc = K; a.vc = V;
       launch_qkv(a, s);
-      hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads, nsplit_max), dim3(256), 0, s, q, K, V, st, part,
-                         counters, att, nsplit_max);
+      hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads), dim3(kAttnThreads), 0, s, q, K, V, st, att);
       a = base_args();
       a.w = w.proj_w; a.bias = w.proj_b; a.N = kW; a.x = att; a.y = x;
       launch_attn_proj(a, s);
@@ -703,16 +792,46 @@ struct GptDecoder::Impl {
     GPT_OK(hipGetLastError());
   }
 
-  void run_step(int which) {  // 0 row, 1 row + head, 2 token + head
+  // One prefill chunk: up to kPrefillRows prefix rows through every layer.
+  void enqueue_chunk() {
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(1), dim3(256), 0, s, st, rows, xr);
+    for (int l = 0; l < L; ++l) {
+      const GptLayerDev& w = layer[l];
+      float* K = kc + (size_t)l * cap * kW;
+      float* V = vc + (size_t)l * cap * kW;
+      GemvArgs a = base_args();
+      a.w = w.attn_w; a.bias = w.attn_b; a.N = kQKV; a.x = xr; a.g1 = w.ln1_w; a.b1 = w.ln1_b;
+      a.q = qr; a.kc = K; a.vc = V;
+      launch_rows<kW, 32, 4, PRO_LN, EPI_QKV>(a, s);
+      hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads, 1, kPrefillRows), dim3(kAttnThreads), 0, s, qr, K, V, st, attr);
+      a = base_args();
+      a.w = w.proj_w; a.bias = w.proj_b; a.N = kW; a.x = attr; a.y = xr;
+      launch_rows<kW, 32, 4, PRO_PLAIN, EPI_RES>(a, s);
+      a = base_args();
+      a.w = w.fc_w; a.bias = w.fc_b; a.N = kMLP; a.x = xr; a.g1 = w.ln2_w; a.b1 = w.ln2_b; a.y = fcr;
+      launch_rows<kW, 32, 4, PRO_LN, EPI_GELU>(a, s);
+      a = base_args();
+      a.w = w.mp_w; a.bias = w.mp_b; a.N = kW; a.x = fcr; a.y = xr;
+      launch_rows<kMLP, 64, 8, PRO_PLAIN, EPI_RES>(a, s);
+    }
+    hipLaunchKernelGGL(advance_rows_kernel, dim3(1), dim3(1), 0, s, st);
+    GPT_OK(hipGetLastError());
+  }
+
+  void run_step(int which) {  // 0 row, 1 row + head, 2 token + head, 3 prefill chunk
+    auto enqueue = [&] {
+      if (which == 3) enqueue_chunk();
+      else enqueue_step(which == 2 ? 1 : 0, which != 0);
+    };
     if (!use_graph) {
-      enqueue_step(which == 2 ? 1 : 0, which != 0);
+      enqueue();
       return;
     }
     if (!graph[which]) {
       hipGraph_t g = nullptr;
       GPT_OK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
       try {
-        enqueue_step(which == 2 ? 1 : 0, which != 0);
+        enqueue();
       } catch (...) {
         (void)hipStreamEndCapture(s, &g);
         if (g) (void)hipGraphDestroy(g);
@@ -728,7 +847,19 @@ struct GptDecoder::Impl {
     GPT_OK(hipGraphLaunch(graph[which], s));
   }
 
-  void reset_state(int prefix_rows, bool hf, int steps) {
+  // Prefix rows into the caches: chunks of kPrefillRows rows (env
+  // MIT2CFM_GPT_ROW_PREFILL=1: one row at a time, through the decode
+  // step's kernels -- the same values, for checking).
+  void prefill(int n) {
+    const char* e = std::getenv("MIT2CFM_GPT_ROW_PREFILL");
+    if (e && std::atoi(e) != 0) {
+      for (int i = 0; i < n; ++i) run_step(0);
+    } else {
+      for (int i = 0; i < n; i += kPrefillRows) run_step(3);
+    }
+  }
+
+  void reset_state(int prefix_rows, int pend, bool hf, int steps) {
     GptState h{};
     h.kv = 0;
     h.step = 0;
@@ -742,6 +873,7 @@ struct GptDecoder::Impl {
     h.max_pred = pred_cap;
     h.cap = cap;
     h.rows = std::max(prefix_rows, 1);
+    h.pend = pend;
     (void)steps;
     *host_state = h;
     const uint32_t start = (uint32_t)kStart;
@@ -833,11 +965,11 @@ void GptDecoder::kv_greedy(const float* prefix, int prefix_tokens, int steps, bo
                                   std::to_string(kPos) + "-row mel position table");
   }
   d.ensure(prefix_tokens + steps + 1, prefix_tokens + 1, steps);
-  d.reset_state(prefix_tokens, hf, steps);
+  d.reset_state(prefix_tokens, prefix_tokens, hf, steps);
   if (prefix_tokens > 0)
     GPT_OK(hipMemcpyAsync(d.rows, prefix, (size_t)prefix_tokens * kW * sizeof(float), hipMemcpyHostToDevice, d.s));
   GPT_OK(hipEventRecord(d.ev[0], d.s));
-  for (int i = 0; i < prefix_tokens; ++i) d.run_step(0);
+  d.prefill(prefix_tokens);
   GPT_OK(hipEventRecord(d.ev[1], d.s));
   int done = 0;
   while (done < steps) {
@@ -872,9 +1004,9 @@ uint32_t GptDecoder::cached_decode(const float* rows, int prefix_tokens, float* 
   if (prefix_tokens < 0) throw std::invalid_argument("gpt: prefix_tokens must be >= 0");
   if (!rows) throw std::invalid_argument("gpt: rows must not be NULL");
   d.ensure(prefix_tokens + 1, prefix_tokens + 1, 1);
-  d.reset_state(prefix_tokens + 1, false, 1);
+  d.reset_state(prefix_tokens + 1, prefix_tokens, false, 1);
   GPT_OK(hipMemcpyAsync(d.rows, rows, ((size_t)prefix_tokens + 1) * kW * sizeof(float), hipMemcpyHostToDevice, d.s));
-  for (int i = 0; i < prefix_tokens; ++i) d.run_step(0);
+  d.prefill(prefix_tokens);
   d.run_step(1);
   GPT_OK(hipMemcpyAsync(d.host_state, d.st, sizeof(GptState), hipMemcpyDeviceToHost, d.s));
   GPT_OK(hipStreamSynchronize(d.s));
@@ -909,7 +1041,7 @@ const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) 
   }
   // A state with kKeys - 1 cached rows; the caches hold whatever they hold
   // (timing only).
-  d.reset_state(1, false, 1);
+  d.reset_state(1, 0, false, 1);
   d.host_state->kv = kKeys - 1;
   GPT_OK(hipMemcpyAsync(d.st, d.host_state, sizeof(GptState), hipMemcpyHostToDevice, d.s));
   GPT_OK(hipMemsetAsync(d.x, 0, kW * sizeof(float), d.s));
@@ -947,9 +1079,8 @@ const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) 
                            d.predicted, d.inputs, 0);
         break;
       default:
-        hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads, d.nsplit_max), dim3(256), 0, d.s, d.q,
-                           d.kc + (size_t)(i % d.L) * d.cap * kW, d.vc + (size_t)(i % d.L) * d.cap * kW, d.st, d.part,
-                           d.counters, d.att, d.nsplit_max);
+        hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads), dim3(kAttnThreads), 0, d.s, d.q,
+                           d.kc + (size_t)(i % d.L) * d.cap * kW, d.vc + (size_t)(i % d.L) * d.cap * kW, d.st, d.att);
         break;
     }
   }

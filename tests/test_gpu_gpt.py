@@ -8,9 +8,9 @@ gpt.cpp:2305-2371), and to 2e-3 on the cached single-row decode
 sides (the checkpoint's precision) and everything else fp32, so the only
 difference is the order of fp32 sums; the bars below are the reference's.
 
-The attention splits its keys into chunks of 64, so prefixes of 63..65 and of
-a few hundred rows exercise one chunk, the chunk boundary and the
-multi-chunk combine.
+The attention walks its keys in chunks of 512 with an online softmax, so
+prefixes of a few rows, of about 512 and of 600 exercise one chunk, the chunk
+boundary and the rescaling across chunks; prefill chunks hold 8 rows.
 """
 from __future__ import annotations
 
@@ -107,7 +107,7 @@ def test_kv_greedy_matches_oracle_24_layers(ctx24, orc24, P, steps, hf):
     _compare(ctx24.gpt_kv_greedy(prefix, steps, hf), orc24.kv_greedy(prefix, steps, hf), "  24 layers")
 
 
-@pytest.mark.parametrize("P,steps", [(0, 3), (1, 2), (62, 4), (63, 3), (64, 3), (65, 2), (300, 10)])
+@pytest.mark.parametrize("P,steps", [(0, 3), (1, 2), (63, 3), (300, 10), (509, 5), (511, 3), (600, 4)])
 def test_kv_greedy_attention_chunks(ctx2, orc2, P, steps):
     prefix = _prefix(P, seed=P)
     print(f"kv greedy 2 layers P={P} steps={steps}", flush=True)
@@ -192,3 +192,18 @@ def test_position_table_bound(ctx2, mit2):
     with pytest.raises(mit2.Mit2CfmError) as e:
         ctx2.gpt_kv_greedy(_prefix(2), 1818, hf_generate_positions=True)
     assert e.value.status == mit2.E_ARG
+
+
+@pytest.mark.parametrize("P", [1, 7, 8, 9, 100])
+def test_chunked_prefill_equals_row_prefill(ctx2, monkeypatch, P):
+    """The prefill's chunks of 8 rows give the values of prefilling one row at a
+    time through the decode step's kernels (same sums in the same order)."""
+    prefix = _prefix(P, seed=20 + P)
+    chunked = ctx2.gpt_kv_greedy(prefix, 4)
+    monkeypatch.setenv("MIT2CFM_GPT_ROW_PREFILL", "1")
+    rows = ctx2.gpt_kv_greedy(prefix, 4)
+    err = float(np.abs(chunked["last_logits"] - rows["last_logits"]).max())
+    print(f"P={P}: chunked prefill {chunked['prefill_ms']:.2f} ms, row prefill {rows['prefill_ms']:.2f} ms, "
+          f"logits max-abs {err:.2e}", flush=True)
+    assert chunked["predicted"].tolist() == rows["predicted"].tolist()
+    assert err <= 1e-5
