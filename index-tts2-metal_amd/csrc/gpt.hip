@@ -56,7 +56,7 @@ namespace {
 constexpr int kW = 1280, kQKV = 3840, kMLP = 5120, kHeads = 20, kHD = 64;
 constexpr int kVocab = GptDecoder::kVocab, kPos = GptDecoder::kPositions;
 constexpr int kStart = (int)GptDecoder::kStartToken, kStop = (int)GptDecoder::kStopToken;
-constexpr int kChunk = 256;   // keys per attention chunk
+constexpr int kChunk = 256;   // keys per attention split
 constexpr int kStepsPerCheck = 8;  // decode steps replayed between stop-flag reads
 constexpr int kPrefillRows = 8;    // prefix rows per prefill chunk
 
@@ -489,29 +489,38 @@ __global__ __launch_bounds__(320) void embed_kernel(const GptState* st, const fl
 // Cached attention of the current query (run_gpt_cached_attention_current_cpu,
 // gpt.cpp:1147-1170, with cpu_attention_single_query, tokenizer_tests.cpp:
 // 4034-4060) over the st->kv + 1 cache rows (the current row included: the
-// c_attn kernel already wrote it).  One block of 512 threads per head (and,
-// in a prefill chunk, per query row: blockIdx.z) walks the keys in chunks of
-// 256 with the softmax kept online -- running max m, sum l and output o,
-// rescaled by exp(m_old - m_new) per chunk, the same sums regrouped.  A
-// chunk's key and value loads are all issued together (the kernel is
-// latency-bound; up to 256 keys cost one round trip).  Scores: 8 lanes per
-// key, 8 dims each; the output: 16 lanes per key, 4 dims each.  No block
-// waits for another.
+// c_attn kernel already wrote it), in two launches with no waiting between
+// blocks.  attn_split_kernel: block (head h, split s, query row z) takes keys
+// 256 s .. 256 s + 255 -- all of its key and value loads issued together
+// (the kernel is latency-bound) -- and writes the split's max m_s, sum
+// l_s = sum exp(score - m_s) and unnormalised output sum exp(score - m_s) v;
+// a head with a single split writes its output directly.  attn_combine_kernel
+// merges the splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s with
+// M = max m_s.  Scores: 8 lanes per key, 8 dims each; the output: 16 lanes
+// per key, 4 dims each.  z is the query row of a prefill chunk (row z sees
+// the keys up to its own position kv + z); a decode step has one query.
 constexpr int kAttnThreads = 512;
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float* q, const float* kc,
-                                                                   const float* vc, const GptState* st,
-                                                                   float* out) {
+constexpr int kPartF = 2 + kHD;  // per split: max, sum, unnormalised output
+
+__device__ __forceinline__ int attn_keys(const GptState* st, int z) { return min(st->kv + z + 1, st->cap); }
+__device__ __forceinline__ bool attn_row_live(const GptState* st, int z) {
+  return gridDim.z == 1 || z < min((int)gridDim.z, st->pend - st->kv);
+}
+
+__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const float* q, const float* kc, const float* vc,
+                                                                  const GptState* st, float* part, float* out,
+                                                                  int nsplit_max) {
   constexpr int kWaves = kAttnThreads / 64;
   constexpr int kKeysPerPass = kAttnThreads / 8, kPass = kChunk / kKeysPerPass;
   constexpr int kVKeysPerPass = kAttnThreads / 16, kVPass = kChunk / kVKeysPerPass;
   constexpr int kGroups = kAttnThreads / 16;  // output key groups
-  const int h = blockIdx.x, tid = threadIdx.x;
-  const int qrow = blockIdx.z;  // the query row of a prefill chunk (0 in a decode step)
-  if (gridDim.z > 1 && qrow >= min((int)gridDim.z, st->pend - st->kv)) return;
-  q += (size_t)qrow * kW;
-  out += (size_t)qrow * kW;
-  const int kvn = min(st->kv + qrow + 1, st->cap);
-  const int nchunks = (kvn + kChunk - 1) / kChunk;
+  const int h = blockIdx.x, sp = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
+  if (!attn_row_live(st, z)) return;
+  const int kvn = attn_keys(st, z);
+  const int nsplit = (kvn + kChunk - 1) / kChunk;
+  if (sp >= nsplit) return;
+  q += (size_t)z * kW;
+  const int t0 = sp * kChunk, n = min(kChunk, kvn - t0), last = kvn - 1;
   __shared__ float sc[kChunk];
   __shared__ float4 red[kGroups][kHD / 4];
   __shared__ float wm[kWaves], wl[kWaves];
@@ -523,72 +532,51 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float* 
   const int lane = tid & 63, wave = tid >> 6;
   const float4* q4 = reinterpret_cast<const float4*>(q + h * kHD) + 2 * e;
   const float4 qa = q4[0], qb = q4[1];
-
-  float m_run = -INFINITY, l_run = 0.f;
+  float4 ka[kPass], kb[kPass], vv[kVPass];  // past the end: re-read the last key (dropped)
+#pragma unroll
+  for (int it = 0; it < kPass; ++it) {
+    const float4* k4 =
+        reinterpret_cast<const float4*>(kh + (size_t)min(t0 + g + kKeysPerPass * it, last) * kHD) + 2 * e;
+    ka[it] = k4[0];
+    kb[it] = k4[1];
+  }
+#pragma unroll
+  for (int it = 0; it < kVPass; ++it)
+    vv[it] = reinterpret_cast<const float4*>(vh + (size_t)min(t0 + g16 + kVKeysPerPass * it, last) * kHD)[d4];
+#pragma unroll
+  for (int it = 0; it < kPass; ++it) {
+    float d = ((qa.x * ka[it].x + qa.y * ka[it].y) + (qa.z * ka[it].z + qa.w * ka[it].w)) +
+              ((qb.x * kb[it].x + qb.y * kb[it].y) + (qb.z * kb[it].z + qb.w * kb[it].w));
+    d += __shfl_xor(d, 4, kWave);
+    d += __shfl_xor(d, 2, kWave);
+    d += __shfl_xor(d, 1, kWave);
+    const int i = g + kKeysPerPass * it;
+    if (e == 0 && i < n) sc[i] = d * 0.125f;  // 1 / sqrt(64)
+  }
+  __syncthreads();
+  float v = tid < n ? sc[tid] : -INFINITY;  // kChunk <= kAttnThreads: one score per thread
+  float m = v;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  if (lane == 0) wm[wave] = m;
+  __syncthreads();
+  m = wm[0];
+#pragma unroll
+  for (int w2 = 1; w2 < kWaves; ++w2) m = fmaxf(m, wm[w2]);
+  const float p = tid < n ? expf(v - m) : 0.f;
+  if (tid < kChunk) sc[tid] = p;
+  const float lw = warp_sum(p);
+  if (lane == 0) wl[wave] = lw;
+  __syncthreads();
+  float l = 0.f;
+#pragma unroll
+  for (int w2 = 0; w2 < kWaves; ++w2) l += wl[w2];
   float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int c = 0; c < nchunks; ++c) {
-    const int t0 = c * kChunk, n = min(kChunk, kvn - t0), last = kvn - 1;
-    float4 ka[kPass], kb[kPass], vv[kVPass];  // past the end: re-read the last key (dropped)
 #pragma unroll
-    for (int it = 0; it < kPass; ++it) {
-      const float4* k4 =
-          reinterpret_cast<const float4*>(kh + (size_t)min(t0 + g + kKeysPerPass * it, last) * kHD) + 2 * e;
-      ka[it] = k4[0];
-      kb[it] = k4[1];
-    }
-#pragma unroll
-    for (int it = 0; it < kVPass; ++it)
-      vv[it] = reinterpret_cast<const float4*>(vh + (size_t)min(t0 + g16 + kVKeysPerPass * it, last) * kHD)[d4];
-#pragma unroll
-    for (int it = 0; it < kPass; ++it) {
-      float d = ((qa.x * ka[it].x + qa.y * ka[it].y) + (qa.z * ka[it].z + qa.w * ka[it].w)) +
-                ((qb.x * kb[it].x + qb.y * kb[it].y) + (qb.z * kb[it].z + qb.w * kb[it].w));
-      d += __shfl_xor(d, 4, kWave);
-      d += __shfl_xor(d, 2, kWave);
-      d += __shfl_xor(d, 1, kWave);
-      const int i = g + kKeysPerPass * it;
-      if (e == 0 && i < n) sc[i] = d * 0.125f;  // 1 / sqrt(64)
-    }
-    __syncthreads();
-    // chunk max (two scores per thread of the first kChunk / 2), then the new running max
-    float v0 = -INFINITY, v1 = -INFINITY;
-    if (tid < kChunk / 2) {
-      v0 = 2 * tid < n ? sc[2 * tid] : -INFINITY;
-      v1 = 2 * tid + 1 < n ? sc[2 * tid + 1] : -INFINITY;
-    }
-    float mc = fmaxf(v0, v1);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off, kWave));
-    if (lane == 0) wm[wave] = mc;
-    __syncthreads();
-    float m_new = m_run;
-#pragma unroll
-    for (int w2 = 0; w2 < kWaves; ++w2) m_new = fmaxf(m_new, wm[w2]);
-    const float scale = expf(m_run - m_new);  // 0 on the first chunk
-    float lc = 0.f;
-    if (tid < kChunk / 2) {
-      const float p0 = 2 * tid < n ? expf(v0 - m_new) : 0.f;
-      const float p1 = 2 * tid + 1 < n ? expf(v1 - m_new) : 0.f;
-      sc[2 * tid] = p0;
-      sc[2 * tid + 1] = p1;
-      lc = p0 + p1;
-    }
-    lc = warp_sum(lc);
-    if (lane == 0) wl[wave] = lc;
-    __syncthreads();
-    float lsum = 0.f;
-#pragma unroll
-    for (int w2 = 0; w2 < kWaves; ++w2) lsum += wl[w2];
-    l_run = l_run * scale + lsum;
-    o.x *= scale; o.y *= scale; o.z *= scale; o.w *= scale;
-#pragma unroll
-    for (int it = 0; it < kVPass; ++it) {
-      const int i = g16 + kVKeysPerPass * it;
-      const float p = i < n ? sc[i] : 0.f;
-      o.x += p * vv[it].x; o.y += p * vv[it].y; o.z += p * vv[it].z; o.w += p * vv[it].w;
-    }
-    m_run = m_new;
-    __syncthreads();  // sc, wm and wl are rewritten by the next chunk
+  for (int it = 0; it < kVPass; ++it) {
+    const int i = g16 + kVKeysPerPass * it;
+    const float pi = i < n ? sc[i] : 0.f;
+    o.x += pi * vv[it].x; o.y += pi * vv[it].y; o.z += pi * vv[it].z; o.w += pi * vv[it].w;
   }
   red[g16][d4] = o;
   __syncthreads();
@@ -596,8 +584,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float* 
     float od = 0.f;
 #pragma unroll
     for (int gg = 0; gg < kGroups; ++gg) od += reinterpret_cast<const float*>(&red[gg][0])[tid];
-    out[h * kHD + tid] = od / l_run;
+    if (nsplit == 1) {
+      out[(size_t)z * kW + h * kHD + tid] = od / l;
+    } else {
+      float* pp = part + (((size_t)z * kHeads + h) * nsplit_max + sp) * kPartF;
+      pp[2 + tid] = od;
+      if (tid == 0) { pp[0] = m; pp[1] = l; }
+    }
   }
+}
+
+__global__ __launch_bounds__(64) void attn_combine_kernel(const GptState* st, const float* part, float* out,
+                                                          int nsplit_max) {
+  const int h = blockIdx.x, z = blockIdx.z, d = threadIdx.x;
+  if (!attn_row_live(st, z)) return;
+  const int nsplit = (attn_keys(st, z) + kChunk - 1) / kChunk;
+  if (nsplit == 1) return;  // written by the split kernel
+  const float* ph = part + ((size_t)z * kHeads + h) * nsplit_max * kPartF;
+  float M = -INFINITY;
+  for (int s2 = 0; s2 < nsplit; ++s2) M = fmaxf(M, ph[(size_t)s2 * kPartF]);
+  float L = 0.f, O = 0.f;
+  for (int s2 = 0; s2 < nsplit; ++s2) {
+    const float f = expf(ph[(size_t)s2 * kPartF] - M);
+    L += f * ph[(size_t)s2 * kPartF + 1];
+    O += f * ph[(size_t)s2 * kPartF + 2 + d];
+  }
+  out[(size_t)z * kW + h * kHD + d] = O / L;
 }
 
 // Launch shapes: rows per block = WAVES * (64 / LPR) * UR.
@@ -670,6 +682,14 @@ struct GptDecoder::Impl {
   uint32_t *predicted = nullptr, *inputs = nullptr;
   float *x, *q, *att, *fc, *logits, *lnf, *fn, *blk_val, *kc, *vc, *rows;
   float *xr, *qr, *attr, *fcr;  // a prefill chunk's rows: [8][1280] x3, [8][5120]
+  float* part = nullptr;        // attention splits: [8 query rows][20 heads][nsplit_max][66]
+  int nsplit_max = 0;
+
+  void launch_attention(const float* qv, const float* K, const float* V, float* out, int rows_z) {
+    hipLaunchKernelGGL(attn_split_kernel, dim3(kHeads, nsplit_max, rows_z), dim3(kAttnThreads), 0, s, qv, K, V, st,
+                       part, out, nsplit_max);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(kHeads, 1, rows_z), dim3(kHD), 0, s, st, part, out, nsplit_max);
+  }
   int* blk_idx;
   GptState* host_state = nullptr;  // pinned
   hipGraphExec_t graph[4] = {nullptr, nullptr, nullptr, nullptr};  // row, row + head, token + head, chunk
@@ -728,6 +748,7 @@ struct GptDecoder::Impl {
                    align256(kVocab * f) + 2 * align256(kW * f) + align256((size_t)head_blocks() * f) +
                    align256((size_t)head_blocks() * 4) +
                    3 * align256((size_t)kPrefillRows * kW * f) + align256((size_t)kPrefillRows * kMLP * f) +
+                   align256((size_t)kPrefillRows * kHeads * (cap / kChunk) * kPartF * f) +
                    2 * align256((size_t)L * cap * kW * f) + align256((size_t)rows_cap * kW * f);
     ws.reserve(bytes);
     st = static_cast<GptState*>(ws.take(sizeof(GptState)));
@@ -746,6 +767,8 @@ struct GptDecoder::Impl {
     qr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
     attr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
     fcr = static_cast<float*>(ws.take((size_t)kPrefillRows * kMLP * f));
+    nsplit_max = cap / kChunk;
+    part = static_cast<float*>(ws.take((size_t)kPrefillRows * kHeads * nsplit_max * kPartF * f));
     kc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
     vc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
     rows = static_cast<float*>(ws.take((size_t)rows_cap * kW * f));
@@ -770,7 +793,7 @@ struct GptDecoder::Impl {
       a.w = w.attn_w; a.bias = w.attn_b; a.N = kQKV; a.x = x; a.g1 = w.ln1_w; a.b1 = w.ln1_b;
       a.q = q; a.kc = K; a.vc = V;
       launch_qkv(a, s);
-      hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads), dim3(kAttnThreads), 0, s, q, K, V, st, att);
+      launch_attention(q, K, V, att, 1);
       a = base_args();
       a.w = w.proj_w; a.bias = w.proj_b; a.N = kW; a.x = att; a.y = x;
       launch_attn_proj(a, s);
@@ -803,7 +826,7 @@ struct GptDecoder::Impl {
       a.w = w.attn_w; a.bias = w.attn_b; a.N = kQKV; a.x = xr; a.g1 = w.ln1_w; a.b1 = w.ln1_b;
       a.q = qr; a.kc = K; a.vc = V;
       launch_rows<kW, 32, 4, PRO_LN, EPI_QKV>(a, s);
-      hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads, 1, kPrefillRows), dim3(kAttnThreads), 0, s, qr, K, V, st, attr);
+      launch_attention(qr, K, V, attr, kPrefillRows);
       a = base_args();
       a.w = w.proj_w; a.bias = w.proj_b; a.N = kW; a.x = attr; a.y = xr;
       launch_rows<kW, 32, 4, PRO_PLAIN, EPI_RES>(a, s);
@@ -1079,8 +1102,8 @@ const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) 
                            d.predicted, d.inputs, 0);
         break;
       default:
-        hipLaunchKernelGGL(attn_decode_kernel, dim3(kHeads), dim3(kAttnThreads), 0, d.s, d.q,
-                           d.kc + (size_t)(i % d.L) * d.cap * kW, d.vc + (size_t)(i % d.L) * d.cap * kW, d.st, d.att);
+        d.launch_attention(d.q, d.kc + (size_t)(i % d.L) * d.cap * kW, d.vc + (size_t)(i % d.L) * d.cap * kW,
+                           d.att, 1);
         break;
     }
   }
