@@ -176,12 +176,14 @@ void visit_weights(Weights& W, F&& f) {
   f(W.lr_out_b, 512);
 }
 
-// Device image layout: "MIT2HIPI", u32 version, u32 has_vocoder, u64 payload
-// bytes, u64 payload checksum, then the payload: the decoder section (u64
-// arena bytes, u8 has_lr, u64 offset per visit_weights array, the arena
-// bytes) and, when present, the vocoder section (Vocoder::append_image).
+// Device image layout: "MIT2HIPI", u32 version, u32 section flags (1 vocoder,
+// 2 GPT decoder), u64 payload bytes, u64 payload checksum, then the payload:
+// the decoder section (u64 arena bytes, u8 has_lr, u64 offset per
+// visit_weights array, the arena bytes), then each flagged section as u64
+// length + bytes (Vocoder::append_image, GptDecoder::append_image).
 constexpr char kImageMagic[8] = {'M', 'I', 'T', '2', 'H', 'I', 'P', 'I'};
-constexpr uint32_t kImageVersion = 1;
+constexpr uint32_t kImageVersion = 2;
+constexpr uint32_t kImageVocoder = 1, kImageGpt = 2;  // section flags
 
 struct HostModel {
   std::unordered_map<std::string, std::vector<float>> t;
@@ -573,12 +575,20 @@ void Engine::write_image(const std::string& path) const {
   std::vector<uint8_t> host(used);
   HIP_OK(hipMemcpy(host.data(), base, used, hipMemcpyDeviceToHost));
   w.bytes(host.data(), used);
-  if (voc_) voc_->append_image(payload);
+  // optional sections, each preceded by its length
+  auto section = [&](auto& part) {
+    std::vector<uint8_t> sec;
+    part->append_image(sec);
+    w.put<uint64_t>(sec.size());
+    w.bytes(sec.data(), sec.size());
+  };
+  if (voc_) section(voc_);
+  if (gpt_) section(gpt_);
   std::vector<uint8_t> head;
   ImageWriter h{head};
   h.bytes(kImageMagic, 8);
   h.put<uint32_t>(kImageVersion);
-  h.put<uint32_t>(voc_ ? 1u : 0u);
+  h.put<uint32_t>((voc_ ? kImageVocoder : 0u) | (gpt_ ? kImageGpt : 0u));
   h.put<uint64_t>(payload.size());
   h.put<uint64_t>(image_checksum(payload.data(), payload.size()));
   std::ofstream f(path, std::ios::binary | std::ios::trunc);
@@ -599,7 +609,8 @@ Engine::Engine(const std::string& image_path, int device) : device_(device) {
   ImageReader h{file.data(), file.size()};
   if (std::memcmp(h.bytes(8), kImageMagic, 8) != 0) throw std::runtime_error("device image: bad magic");
   if (h.get<uint32_t>() != kImageVersion) throw std::runtime_error("device image: unsupported version");
-  const uint32_t has_voc = h.get<uint32_t>();
+  const uint32_t sections = h.get<uint32_t>();
+  if (sections & ~(kImageVocoder | kImageGpt)) throw std::runtime_error("device image: unknown sections");
   const uint64_t plen = h.get<uint64_t>();
   const uint64_t sum = h.get<uint64_t>();
   const uint8_t* payload = h.bytes(plen);
@@ -631,10 +642,18 @@ Engine::Engine(const std::string& image_path, int device) : device_(device) {
     ok = ok && (!W.has_lr || (W.lr_proj_w && W.lr_out_w && W.lr_conv_w[3] && W.lr_gn_b[3]));
     if (!ok) throw std::runtime_error("device image: missing decoder arrays");
     HIP_OK(hipMemcpy(base, r.bytes(used), used, hipMemcpyHostToDevice));
-    if (has_voc) voc_ = std::make_unique<Vocoder>(payload + r.at, plen - r.at, stream_);
-    else if (r.at != plen) throw std::runtime_error("device image: trailing bytes");
+    if (sections & kImageVocoder) {
+      const uint64_t n = r.get<uint64_t>();
+      voc_ = std::make_unique<Vocoder>(r.bytes(n), n, stream_);
+    }
+    if (sections & kImageGpt) {
+      const uint64_t n = r.get<uint64_t>();
+      gpt_ = std::make_unique<GptDecoder>(r.bytes(n), n, stream_);
+    }
+    if (r.at != plen) throw std::runtime_error("device image: trailing bytes");
     ws_ = std::make_unique<Workspace>();
   } catch (...) {
+    gpt_.reset();
     voc_.reset();
     w_.reset();
     (void)hipStreamDestroy(stream_);

@@ -31,6 +31,10 @@ class GptDecoder {
   // layouts: the Conv1D matrices are [in][out]).  Layers 0..L-1 must all be
   // present (the checkpoint has 24); throws std::invalid_argument otherwise.
   GptDecoder(const std::unordered_map<std::string, std::vector<float>>& t, hipStream_t stream);
+  // From the GPT section of a device image (see append_image).
+  GptDecoder(const uint8_t* image, size_t bytes, hipStream_t stream);
+  // Appends the prepared weights (arena bytes and layout) to an image.
+  void append_image(std::vector<uint8_t>& out) const;
   ~GptDecoder();
   GptDecoder(const GptDecoder&) = delete;
   GptDecoder& operator=(const GptDecoder&) = delete;

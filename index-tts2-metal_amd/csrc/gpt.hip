@@ -37,9 +37,11 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 
 #include "device_common.h"
 #include "engine.h"
+#include "image_io.h"
 
 namespace mit2hip {
 
@@ -709,6 +711,26 @@ struct GptDecoder::Impl {
     }
   }
 
+  // Every weight array with its element count, in a fixed order (the device
+  // image's layout).
+  template <typename F>
+  void visit_weights(F&& f) {
+    for (auto& w : layer) {
+      f(w.ln1_w, kW); f(w.ln1_b, kW); f(w.attn_w, (size_t)kQKV * kW); f(w.attn_b, kQKV);
+      f(w.proj_w, (size_t)kW * kW); f(w.proj_b, kW); f(w.ln2_w, kW); f(w.ln2_b, kW);
+      f(w.fc_w, (size_t)kMLP * kW); f(w.fc_b, kMLP); f(w.mp_w, (size_t)kW * kMLP); f(w.mp_b, kW);
+    }
+    f(lnf_w, kW); f(lnf_b, kW); f(fn_w, kW); f(fn_b, kW);
+    f(head_w, (size_t)kVocab * kW); f(head_b, kVocab);
+    f(mel_emb, (size_t)kVocab * kW); f(pos_emb, (size_t)kPos * kW);
+  }
+
+  void init_host_side() {
+    if (const char* g = std::getenv("MIT2CFM_GRAPH")) use_graph = std::atoi(g) != 0;
+    GPT_OK(hipHostMalloc(reinterpret_cast<void**>(&host_state), sizeof(GptState), hipHostMallocDefault));
+    for (auto& e : ev) GPT_OK(hipEventCreate(&e));
+  }
+
   half_t* up_f16(const std::vector<float>& v) {
     std::vector<_Float16> h(v.size());
     for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
@@ -916,7 +938,6 @@ GptDecoder::GptDecoder(const std::unordered_map<std::string, std::vector<float>>
     : d_(new Impl) {
   Impl& d = *d_;
   d.s = stream;
-  if (const char* g = std::getenv("MIT2CFM_GRAPH")) d.use_graph = std::atoi(g) != 0;
   try {
     auto get = [&](const std::string& name, size_t elems) -> const std::vector<float>& {
       auto it = t.find(name);
@@ -964,8 +985,49 @@ GptDecoder::GptDecoder(const std::unordered_map<std::string, std::vector<float>>
     d.head_b = d.up_f32(get("gpt.mel_head.bias", kVocab));
     d.mel_emb = d.up_f32(get("gpt.mel_embedding.weight", (size_t)kVocab * kW));
     d.pos_emb = d.up_f32(get("gpt.mel_pos_embedding.emb.weight", (size_t)kPos * kW));
-    GPT_OK(hipHostMalloc(reinterpret_cast<void**>(&d.host_state), sizeof(GptState), hipHostMallocDefault));
-    for (auto& e : d.ev) GPT_OK(hipEventCreate(&e));
+    d.init_host_side();
+  } catch (...) {
+    delete d_;
+    throw;
+  }
+}
+
+// Image section: u64 arena bytes, i32 layers, u64 offset per weight array
+// (Impl::visit_weights order), then the arena bytes.
+void GptDecoder::append_image(std::vector<uint8_t>& out) const {
+  Impl& d = *d_;
+  ImageWriter w{out};
+  const char* base = d.wa.base();
+  const size_t used = d.wa.used();
+  w.put<uint64_t>(used);
+  w.put<int32_t>(d.L);
+  d.visit_weights([&](auto* p, size_t) { w.put<uint64_t>(arena_offset(p, base)); });
+  std::vector<uint8_t> host(used);
+  GPT_OK(hipMemcpy(host.data(), base, used, hipMemcpyDeviceToHost));
+  w.bytes(host.data(), used);
+}
+
+GptDecoder::GptDecoder(const uint8_t* image, size_t bytes, hipStream_t stream) : d_(new Impl) {
+  Impl& d = *d_;
+  d.s = stream;
+  try {
+    ImageReader r{image, bytes};
+    const uint64_t used = r.get<uint64_t>();
+    const int32_t L = r.get<int32_t>();
+    if (used == 0 || used > (uint64_t(64) << 30) || L < 1 || L > 64)
+      throw std::runtime_error("device image: bad GPT section header");
+    d.L = L;
+    d.layer.resize(L);
+    d.wa.reserve(used);
+    d.wa.set_used(used);
+    char* base = d.wa.base();
+    d.visit_weights([&](auto*& p, size_t n) {
+      using T = std::remove_pointer_t<std::remove_reference_t<decltype(p)>>;
+      p = arena_span<T>(r.get<uint64_t>(), n, base, used);
+    });
+    GPT_OK(hipMemcpy(base, r.bytes(used), used, hipMemcpyHostToDevice));
+    if (r.at != bytes) throw std::runtime_error("device image: trailing bytes in the GPT section");
+    d.init_host_side();
   } catch (...) {
     delete d_;
     throw;

@@ -78,3 +78,24 @@ def test_corrupt_images_are_model_errors(mit2, image, tmp_path):
         with pytest.raises(mit2.Mit2CfmError) as e:
             mit2.Context(image=p, device=0)
         assert e.value.status == mit2.E_MODEL, name
+
+
+def test_image_with_gpt_decoder(mit2, tensors, tmp_path):
+    """The GPT decoder's prepared weights travel in the image too (section 2)."""
+    gpt = mit2.synthetic_gpt_tensors(layers=2)
+    src = mit2.Context({**tensors, **gpt}, device=0)
+    p = tmp_path / "gpt.mit2hip"
+    try:
+        src.write_image(p)
+        c = mit2.Context(image=p, device=0)
+        try:
+            assert c.gpt_layers() == 2
+            prefix = (np.random.default_rng(4).standard_normal((20, 1280)) * 0.05).astype(np.float32)
+            a = src.gpt_kv_greedy(prefix, 6)
+            b = c.gpt_kv_greedy(prefix, 6)
+            assert a["predicted"].tolist() == b["predicted"].tolist()
+            assert np.array_equal(a["last_logits"], b["last_logits"])
+        finally:
+            c.close()
+    finally:
+        src.close()
