@@ -694,7 +694,8 @@ struct GptDecoder::Impl {
   }
   int* blk_idx;
   GptState* host_state = nullptr;  // pinned
-  hipGraphExec_t graph[4] = {nullptr, nullptr, nullptr, nullptr};  // row, row + head, token + head, chunk
+  // row, row + head, token + head, prefill chunk, kStepsPerCheck token steps
+  hipGraphExec_t graph[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   bool use_graph = true;  // env MIT2CFM_GRAPH=0: launch every kernel directly (for profilers)
 
@@ -863,10 +864,15 @@ struct GptDecoder::Impl {
     GPT_OK(hipGetLastError());
   }
 
-  void run_step(int which) {  // 0 row, 1 row + head, 2 token + head, 3 prefill chunk
+  void run_step(int which) {  // 0 row, 1 row + head, 2 token + head, 3 prefill chunk, 4 = 2 x kStepsPerCheck
     auto enqueue = [&] {
-      if (which == 3) enqueue_chunk();
-      else enqueue_step(which == 2 ? 1 : 0, which != 0);
+      if (which == 3) {
+        enqueue_chunk();
+      } else if (which == 4) {
+        for (int i = 0; i < kStepsPerCheck; ++i) enqueue_step(1, true);
+      } else {
+        enqueue_step(which == 2 ? 1 : 0, which != 0);
+      }
     };
     if (!use_graph) {
       enqueue();
@@ -1059,7 +1065,11 @@ void GptDecoder::kv_greedy(const float* prefix, int prefix_tokens, int steps, bo
   int done = 0;
   while (done < steps) {
     const int n = std::min(kStepsPerCheck, steps - done);
-    for (int i = 0; i < n; ++i) d.run_step(2);
+    if (n == kStepsPerCheck) {
+      d.run_step(4);  // one graph of kStepsPerCheck steps
+    } else {
+      for (int i = 0; i < n; ++i) d.run_step(2);
+    }
     done += n;
     GPT_OK(hipMemcpyAsync(d.host_state, d.st, sizeof(GptState), hipMemcpyDeviceToHost, d.s));
     GPT_OK(hipStreamSynchronize(d.s));
