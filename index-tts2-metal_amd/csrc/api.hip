@@ -152,6 +152,8 @@ mit2cfm_status mit2cfm_create(const mit2cfm_tensor* tensors, uint32_t count, int
   return make_ctx(ts, device, out);
 }
 
+}  // extern "C"
+
 namespace {
 // The bundle tensors a context uses: the DiT-CFM estimator, the length
 // regulator, the vocoder and the GPT decoder (not the GPT's conditioning
@@ -165,6 +167,8 @@ bool wanted_bundle_tensor(const std::string& n) {
   return false;
 }
 }  // namespace
+
+extern "C" {
 
 mit2cfm_status mit2cfm_create_from_bundle(const char* bundle_path, int32_t device,
                                           mit2cfm_ctx** out) {
@@ -205,6 +209,8 @@ mit2cfm_status mit2cfm_create_synthetic(uint64_t base_seed, float stddev, int32_
   return make_ctx(ts, device, out);
 }
 
+}  // extern "C"
+
 namespace {
 const std::vector<mit2::SynthSpec>* synth_set(int32_t set) {
   switch (set) {
@@ -222,6 +228,8 @@ std::vector<uint8_t> synth_set_bytes(int32_t set, size_t i, uint64_t base_seed, 
   return mit2::synth_bigvgan_tensor_bytes(i, base_seed, stddev);
 }
 }  // namespace
+
+extern "C" {
 
 mit2cfm_status mit2cfm_create_synthetic_acoustic(uint64_t base_seed, float stddev, int32_t device,
                                                  mit2cfm_ctx** out) {

@@ -22,8 +22,9 @@ class HipContext {
   // when the bundle holds them) to GPU `device`.
   explicit HipContext(const Bundle& bundle, int device = 0);
   // Seeded synthetic weights (N(0, stddev) f16; stddev 0 = fan-in scaled);
-  // with acoustic, also the length regulator's and the vocoder's.
-  HipContext(uint64_t synthetic_seed, float stddev, int device = 0, bool acoustic = false);
+  // with acoustic, also the length regulator's and the vocoder's; with gpt,
+  // also the 24-layer GPT decoder's (seed + 3).
+  HipContext(uint64_t synthetic_seed, float stddev, int device = 0, bool acoustic = false, bool gpt = false);
   // From a device image (mit2cfm_write_image): prepared weights, no host-side preparation.
   HipContext(const std::string& image_path, int device);
   ~HipContext();
@@ -67,6 +68,31 @@ std::vector<float> run_bigvgan_vocoder_hip(HipContext& hip, const Bundle& bundle
 // Same without a bundle argument (weights already resident in the context).
 std::vector<float> run_bigvgan_vocoder_hip(HipContext& hip, const std::vector<float>& mel,
                                            uint32_t tokens);
+
+// The GPT mel-code decoder (runtime/impl/gpt.cpp).  The context needs the
+// bundle's GPT decoder tensors (gpt.gpt.h.*, gpt.gpt.ln_f.*, gpt.final_norm.*,
+// gpt.mel_head.*, gpt.mel_embedding.weight, gpt.mel_pos_embedding.emb.weight).
+struct GptGreedyOutputs {  // gpt.cpp:1583-1590 (without the backend comparison field)
+  std::vector<uint32_t> predicted_tokens;
+  std::vector<uint32_t> input_tokens;
+  std::vector<float> last_logits;
+  int32_t first_stop_step = -1;
+};
+// run_gpt_kv_greedy_metal (gpt.cpp:1914; CPU definition :1877): prefix
+// [prefix_tokens][1280] -> greedy codes, stopping at the first stop token.
+GptGreedyOutputs run_gpt_kv_greedy_hip(HipContext& hip, const std::vector<float>& prefix,
+                                       uint32_t prefix_tokens, uint32_t steps,
+                                       bool hf_generate_positions = false);
+struct GptCachedDecodeOutputs {  // gpt.cpp:1393-1398
+  std::vector<float> ln_f;
+  std::vector<float> final_norm;
+  std::vector<float> logits;
+  uint32_t argmax = 0;
+};
+// run_gpt_cached_decode_metal (gpt.cpp:1427; CPU definition :1400): input
+// [prefix_tokens + 1][1280]; the last row decoded against the others' caches.
+GptCachedDecodeOutputs run_gpt_cached_decode_hip(HipContext& hip, const std::vector<float>& input,
+                                                 uint32_t prefix_tokens);
 
 // Euler step count for synthesis: env MIT2_CFM_STEPS, default 16, clamped to
 // the --cfm_steps range 12..25 (main.cpp:57-88, :3181-3187).

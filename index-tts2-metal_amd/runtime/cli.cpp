@@ -11,6 +11,9 @@
 //                                        dit_cfm_bigvgan.cpp:4225)
 //   --test-bigvgan-vocoder MODEL        (one mel frame, :4469)
 //   --write-image MODEL FILE            (the prepared device weights)
+//   --test-gpt-kv-decode MODEL          (gpt.cpp:1469, run_gpt_kv_decode_test)
+//   --test-gpt-kv-greedy MODEL          (gpt.cpp:2305, run_gpt_kv_greedy_test)
+//   --bench-gpt MODEL P CODES ITERS     (greedy decode of CODES after P prefix rows)
 // MODEL is a bundle path, "synthetic[:SEED[:STDDEV]]" or "image:FILE" (a
 // device image written by --write-image).  The reference's
 // --test-cfm-* compare its Metal path with its CPU path; here the CPU
@@ -36,7 +39,7 @@ namespace {
 
 using Clock = std::chrono::steady_clock;
 
-std::unique_ptr<mit2::HipContext> open_model(const std::string& model, bool acoustic = false) {
+std::unique_ptr<mit2::HipContext> open_model(const std::string& model, bool acoustic = false, bool gpt = false) {
   if (model.rfind("image:", 0) == 0) return std::make_unique<mit2::HipContext>(model.substr(6), 0);
   if (model.rfind("synthetic", 0) == 0) {
     uint64_t seed = 20240605;
@@ -47,7 +50,7 @@ std::unique_ptr<mit2::HipContext> open_model(const std::string& model, bool acou
       seed = std::stoull(model.substr(c1 + 1, c2 == std::string::npos ? std::string::npos : c2 - c1 - 1));
       if (c2 != std::string::npos) stddev = std::stof(model.substr(c2 + 1));
     }
-    return std::make_unique<mit2::HipContext>(seed, stddev, 0, acoustic);
+    return std::make_unique<mit2::HipContext>(seed, stddev, 0, acoustic, gpt);
   }
   mit2::Bundle b(model);
   return std::make_unique<mit2::HipContext>(b, 0);
@@ -130,6 +133,71 @@ int test_bigvgan_vocoder(const std::string& model) {
   return (nonfinite == 0 && peak <= 1.0f && repeat_err == 0.0f && a.size() == 256) ? 0 : 1;
 }
 
+// run_gpt_kv_decode_test's input (gpt.cpp:1469-1479): 3 prefix rows + 1 of
+// sin(0.009 i) 0.065 + cos(0.013 (i % 307)) 0.021.  Checks: finite outputs, the
+// reported argmax is the logits' first maximum, repeatable.
+int test_gpt_kv_decode(const std::string& model) {
+  auto hip = open_model(model, false, true);
+  const uint32_t prefix_tokens = 3;
+  const auto input = series((size_t)(prefix_tokens + 1) * 1280, 0.009f, 0.065f, 307, 0.013f, 0.021f, false);
+  const auto a = mit2::run_gpt_cached_decode_hip(*hip, input, prefix_tokens);
+  const auto b = mit2::run_gpt_cached_decode_hip(*hip, input, prefix_tokens);
+  size_t nonfinite = 0, first_max = 0;
+  float repeat_err = 0.0f;
+  for (size_t i = 0; i < a.logits.size(); ++i) {
+    if (!std::isfinite(a.logits[i])) ++nonfinite;
+    if (a.logits[i] > a.logits[first_max]) first_max = i;
+    repeat_err = std::max(repeat_err, std::fabs(a.logits[i] - b.logits[i]));
+  }
+  for (float v : a.final_norm) nonfinite += std::isfinite(v) ? 0 : 1;
+  const bool ok = nonfinite == 0 && a.argmax == first_max && repeat_err == 0.0f && b.argmax == a.argmax;
+  std::cout << "{\n  \"stage\": \"gpt_kv_decode\",\n  \"prefix_tokens\": " << prefix_tokens
+            << ",\n  \"decode_tokens\": 1,\n  \"argmax\": " << a.argmax << ",\n  \"nonfinite\": " << nonfinite
+            << ",\n  \"repeat_max_abs_error\": " << repeat_err << ",\n  \"ok\": " << (ok ? "true" : "false")
+            << "\n}\n";
+  return ok ? 0 : 1;
+}
+
+// run_gpt_kv_greedy_test's conditioning series (gpt.cpp:2313-2316) as the
+// prefix (its two text rows come from the text embedding, outside this
+// library), 3 steps.  Checks: finite logits, tokens in the vocabulary, the
+// inputs are the start token then the non-stop predictions, repeatable.
+int test_gpt_kv_greedy(const std::string& model) {
+  auto hip = open_model(model, false, true);
+  const uint32_t prefix_tokens = 8, steps = 3;
+  const auto prefix = series((size_t)prefix_tokens * 1280, 0.007f, 0.045f, 251, 0.011f, 0.018f, false);
+  const auto a = mit2::run_gpt_kv_greedy_hip(*hip, prefix, prefix_tokens, steps);
+  const auto b = mit2::run_gpt_kv_greedy_hip(*hip, prefix, prefix_tokens, steps);
+  size_t nonfinite = 0;
+  for (float v : a.last_logits) nonfinite += std::isfinite(v) ? 0 : 1;
+  bool ok = nonfinite == 0 && a.predicted_tokens == b.predicted_tokens && a.last_logits == b.last_logits &&
+            !a.input_tokens.empty() && a.input_tokens[0] == 8192;
+  for (size_t i = 0; i < a.predicted_tokens.size(); ++i) {
+    ok = ok && a.predicted_tokens[i] < 8194;
+    if (a.predicted_tokens[i] != 8193) ok = ok && i + 1 < a.input_tokens.size() && a.input_tokens[i + 1] == a.predicted_tokens[i];
+  }
+  std::cout << "{\n  \"stage\": \"gpt_kv_greedy_loop\",\n  \"prefix_tokens\": " << prefix_tokens
+            << ",\n  \"steps\": " << steps << ",\n  \"predicted_tokens\": [";
+  for (size_t i = 0; i < a.predicted_tokens.size(); ++i) std::cout << (i ? ", " : "") << a.predicted_tokens[i];
+  std::cout << "],\n  \"first_stop_step\": " << a.first_stop_step << ",\n  \"nonfinite\": " << nonfinite
+            << ",\n  \"ok\": " << (ok ? "true" : "false") << "\n}\n";
+  return ok ? 0 : 1;
+}
+
+int bench_gpt(const std::string& model, uint32_t prefix_tokens, uint32_t codes, uint32_t iters) {
+  auto hip = open_model(model, false, true);
+  const auto prefix = mit2::make_deterministic_normal_noise(prefix_tokens, 1280, 2, 0.05f);
+  mit2::run_gpt_kv_greedy_hip(*hip, prefix, prefix_tokens, 16);  // warm-up
+  size_t n = 0;
+  const auto t0 = Clock::now();
+  for (uint32_t i = 0; i < iters; ++i) n = mit2::run_gpt_kv_greedy_hip(*hip, prefix, prefix_tokens, codes).predicted_tokens.size();
+  const double total = std::chrono::duration<double>(Clock::now() - t0).count();
+  std::cout << "{\n  \"stage\": \"bench_gpt\",\n  \"prefix_tokens\": " << prefix_tokens << ",\n  \"codes\": " << n
+            << ",\n  \"iters\": " << iters << ",\n  \"seconds_per_call\": " << total / iters
+            << ",\n  \"ms_per_code_incl_prefill\": " << 1e3 * total / iters / std::max<size_t>(n, 1) << "\n}\n";
+  return 0;
+}
+
 int test_cfm_euler(const std::string& model, const char* stage, uint32_t steps, float cfg) {
   auto hip = open_model(model);
   const uint32_t tokens = 5, prompt_tokens = 2;
@@ -184,7 +252,8 @@ int usage() {
                "       [--seed S] [--out FILE] | --inspect-model-bundle DIR |\n"
                "       --write-synthetic-bundle DIR [SEED] [STDDEV] |\n"
                "       --bench-bigvgan MODEL T ITERS | --test-bigvgan-vocoder MODEL |\n"
-               "       --write-image MODEL FILE\n"
+               "       --write-image MODEL FILE | --test-gpt-kv-decode MODEL |\n"
+               "       --test-gpt-kv-greedy MODEL | --bench-gpt MODEL P CODES ITERS\n"
                "MODEL: bundle path, synthetic[:SEED[:STDDEV]] or image:FILE\n";
   return 2;
 }
@@ -229,6 +298,11 @@ int main(int argc, char** argv) {
       if (a == "--bench-bigvgan" && i + 3 < argc)
         return bench_bigvgan(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]));
       if (a == "--test-bigvgan-vocoder" && i + 1 < argc) return test_bigvgan_vocoder(argv[i + 1]);
+      if (a == "--test-gpt-kv-decode" && i + 1 < argc) return test_gpt_kv_decode(argv[i + 1]);
+      if (a == "--test-gpt-kv-greedy" && i + 1 < argc) return test_gpt_kv_greedy(argv[i + 1]);
+      if (a == "--bench-gpt" && i + 4 < argc)
+        return bench_gpt(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]),
+                         (uint32_t)std::stoul(argv[i + 4]));
       if (a == "--test-cfm-euler-cfg" && i + 1 < argc)
         return test_cfm_euler(argv[i + 1], "cfm_euler_cfg", 25, 0.5f);
       if (a == "--decode" && i + 3 < argc)

@@ -25,7 +25,7 @@ def _run(cli, *args, timeout=300):
 def test_usage_without_a_command(cli):
     r = _run(cli)
     assert r.returncode == 2
-    assert "--bench-bigvgan" in r.stderr and "--cfm_steps" not in r.stdout
+    assert "--bench-bigvgan" in r.stderr and "--test-gpt-kv-greedy" in r.stderr and "--cfm_steps" not in r.stdout
 
 
 @pytest.mark.parametrize("steps", ["11", "26", "0"])
@@ -78,3 +78,19 @@ def test_vocoder_harnesses(cli):
     assert r.returncode == 0, r.stderr
     d = json.loads(r.stdout)
     assert d["samples"] == 16 * 256 and d["seconds_per_call"] > 0 and d["rtf_vocoder_only"] > 0
+
+
+@pytest.mark.gpu
+def test_gpt_harnesses(cli):
+    r = _run(cli, "--test-gpt-kv-decode", "synthetic")
+    assert r.returncode == 0, r.stdout + r.stderr
+    d = json.loads(r.stdout)
+    assert d["ok"] and d["nonfinite"] == 0 and d["repeat_max_abs_error"] == 0
+    r = _run(cli, "--test-gpt-kv-greedy", "synthetic")
+    assert r.returncode == 0, r.stdout + r.stderr
+    d = json.loads(r.stdout)
+    assert d["ok"] and len(d["predicted_tokens"]) == 3
+    r = _run(cli, "--bench-gpt", "synthetic", "20", "16", "1")
+    assert r.returncode == 0, r.stderr
+    d = json.loads(r.stdout)
+    assert d["codes"] == 16 and d["seconds_per_call"] > 0
