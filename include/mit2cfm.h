@@ -378,6 +378,30 @@ mit2cfm_status mit2cfm_gpt_kv_greedy(mit2cfm_ctx* ctx, const float* prefix, uint
                                      uint32_t* input_tokens, uint32_t* n_input, int32_t* first_stop_step,
                                      float* last_logits, double* timings_ms);
 
+/* GptSamplingConfig (runtime/impl/gpt.cpp:1592-1599) with do_sample set. */
+typedef struct mit2cfm_gpt_sampling {
+  uint64_t seed;            /* splitmix64 seed, once per call */
+  float temperature;        /* > 0 */
+  uint32_t top_k;           /* 0: off */
+  float top_p;              /* (0, 1]; 1: off */
+  float repetition_penalty; /* > 0; 1: off */
+} mit2cfm_gpt_sampling;
+
+/* The sampled form of mit2cfm_gpt_kv_greedy (run_gpt_kv_greedy_metal with
+ * do_sample, gpt.cpp:2221-2240): each step's logits go through
+ * apply_gpt_sampling_processors (:1618: repetition penalty over the distinct
+ * history tokens [start token, predictions so far], temperature, top-k,
+ * top-p) and sample_gpt_token_from_logits (:1720: one splitmix64 draw) on the
+ * GPU.  Outputs as for mit2cfm_gpt_kv_greedy, plus last_processed_logits
+ * [8194] (may be NULL).  A setting the reference rejects (temperature or
+ * penalty <= 0, top_p outside (0, 1]) is MIT2CFM_E_ARG. */
+mit2cfm_status mit2cfm_gpt_kv_sample(mit2cfm_ctx* ctx, const float* prefix, uint32_t prefix_tokens,
+                                     uint32_t steps, int32_t hf_generate_positions,
+                                     const mit2cfm_gpt_sampling* sampling, uint32_t* predicted_tokens,
+                                     uint32_t* n_predicted, uint32_t* input_tokens, uint32_t* n_input,
+                                     int32_t* first_stop_step, float* last_logits,
+                                     float* last_processed_logits, double* timings_ms);
+
 /* Replaces run_gpt_cached_decode_metal (runtime/impl/gpt.cpp:1427; CPU
  * definition run_gpt_cached_decode_cpu :1400): rows [prefix_tokens + 1][1280];
  * the first prefix_tokens rows fill the key/value caches, the last row is

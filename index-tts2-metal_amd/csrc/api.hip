@@ -729,6 +729,44 @@ mit2cfm_status mit2cfm_gpt_kv_greedy(mit2cfm_ctx* ctx, const float* prefix, uint
   });
 }
 
+mit2cfm_status mit2cfm_gpt_kv_sample(mit2cfm_ctx* ctx, const float* prefix, uint32_t prefix_tokens,
+                                     uint32_t steps, int32_t hf_generate_positions,
+                                     const mit2cfm_gpt_sampling* sampling, uint32_t* predicted_tokens,
+                                     uint32_t* n_predicted, uint32_t* input_tokens, uint32_t* n_input,
+                                     int32_t* first_stop_step, float* last_logits,
+                                     float* last_processed_logits, double* timings_ms) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(sampling != nullptr, "sampling must not be NULL");
+    require(prefix_tokens == 0 || prefix != nullptr, "prefix must not be NULL");
+    require(prefix_tokens <= (1u << 16), "prefix_tokens must be <= 65536");
+    require(steps <= (uint32_t)mit2hip::GptDecoder::kPositions, "steps must be <= 1818");
+    require(steps == 0 || (predicted_tokens && n_predicted), "predicted_tokens/n_predicted must not be NULL");
+    require(input_tokens && n_input && first_stop_step, "input_tokens/n_input/first_stop_step must not be NULL");
+    mit2hip::GptDecoder::Sampling smp;
+    smp.seed = sampling->seed;
+    smp.temperature = sampling->temperature;
+    smp.top_k = sampling->top_k;
+    smp.top_p = sampling->top_p;
+    smp.repetition_penalty = sampling->repetition_penalty;
+    mit2hip::GptDecoder::Greedy g;
+    ctx->eng->gpt().kv_sample(prefix, (int)prefix_tokens, (int)steps, hf_generate_positions != 0, smp, g);
+    if (n_predicted) *n_predicted = (uint32_t)g.predicted.size();
+    if (!g.predicted.empty()) std::memcpy(predicted_tokens, g.predicted.data(), g.predicted.size() * 4);
+    *n_input = (uint32_t)g.input_tokens.size();
+    std::memcpy(input_tokens, g.input_tokens.data(), g.input_tokens.size() * 4);
+    *first_stop_step = g.first_stop_step;
+    if (last_logits && !g.last_logits.empty())
+      std::memcpy(last_logits, g.last_logits.data(), g.last_logits.size() * sizeof(float));
+    if (last_processed_logits && !g.last_processed_logits.empty())
+      std::memcpy(last_processed_logits, g.last_processed_logits.data(), g.last_processed_logits.size() * sizeof(float));
+    if (timings_ms) {
+      timings_ms[0] = g.prefill_ms;
+      timings_ms[1] = g.decode_ms;
+    }
+  });
+}
+
 mit2cfm_status mit2cfm_gpt_cached_decode(mit2cfm_ctx* ctx, const float* rows, uint32_t prefix_tokens,
                                          float* ln_f, float* final_norm, float* logits, uint32_t* argmax) {
   if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");

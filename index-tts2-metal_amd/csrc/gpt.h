@@ -48,6 +48,7 @@ class GptDecoder {
     std::vector<uint32_t> predicted;     // one per step taken (the stop token included)
     std::vector<uint32_t> input_tokens;  // start token, then every non-stop prediction
     std::vector<float> last_logits;      // [8194] logits of the last step taken
+    std::vector<float> last_processed_logits;  // [8194] after the sampling processors (greedy: = last_logits)
     int32_t first_stop_step = -1;
     double prefill_ms = 0, decode_ms = 0;  // device time of the two phases
   };
@@ -57,6 +58,22 @@ class GptDecoder {
   // Positions follow gpt_cached_generate_position (gpt.cpp:1873).
   void kv_greedy(const float* prefix, int prefix_tokens, int steps, bool hf_generate_positions,
                  Greedy& out);
+
+  // GptSamplingConfig (gpt.cpp:1592-1599) with do_sample set.
+  struct Sampling {
+    uint64_t seed = 0;
+    float temperature = 1.0f;
+    uint32_t top_k = 0;  // 0: off
+    float top_p = 1.0f;
+    float repetition_penalty = 1.0f;
+  };
+  // The sampled loop (run_gpt_kv_greedy_metal with do_sample, gpt.cpp:
+  // 2221-2240): each step's logits go through the sampling processors over
+  // the history [start token, predictions so far] and one splitmix64 draw
+  // (seeded once per call) picks the token.  Throws std::invalid_argument for
+  // the settings the reference rejects.
+  void kv_sample(const float* prefix, int prefix_tokens, int steps, bool hf_generate_positions,
+                 const Sampling& sampling, Greedy& out);
 
   // run_gpt_cached_decode (gpt.cpp:1400): HOST rows [prefix_tokens + 1][1280];
   // the last row is decoded against the caches of the others.  Outputs (host,
@@ -75,6 +92,7 @@ class GptDecoder {
   struct Impl;
 
  private:
+  void generate(const float* prefix, int prefix_tokens, int steps, bool hf, const Sampling* sampling, Greedy& out);
   Impl* d_;
 };
 

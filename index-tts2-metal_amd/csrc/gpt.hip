@@ -77,8 +77,15 @@ struct GptState {
   int32_t cap;        // rows of each key/value cache
   int32_t rows;       // rows of the prefix buffer
   int32_t pend;       // prefix rows the prefill chunks cover (rows 0..pend-1)
-  int32_t pad[3];
+  int32_t top_k;      // sampling (sample_kernel): top-k (0: off)
+  float temperature;  //   temperature, top-p, repetition penalty
+  float top_p;
+  float penalty;
+  int32_t pad0;
+  uint64_t rng;       //   splitmix64 state, advanced once per sampled step
+  int32_t pad[12];
 };
+static_assert(sizeof(GptState) == 128, "GptState layout");
 
 enum { PRO_PLAIN = 0, PRO_LN = 1, PRO_LN2 = 2 };
 enum { EPI_GELU = 0, EPI_RES = 1, EPI_QKV = 2, EPI_LOGITS = 3 };
@@ -403,6 +410,301 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs a) {
   }
 }
 
+// The do_sample path of the decode loop (run_gpt_kv_greedy_metal with
+// sampling, gpt.cpp:2221-2240): apply_gpt_sampling_processors (:1618-1718) to
+// the step's logits over the history [start token, predictions so far] --
+// repetition penalty once per distinct token, temperature, top-k (keep the
+// scores >= the k-th largest), top-p (in ascending (score, index) order drop
+// the tokens whose cumulative probability stays <= 1 - top_p; the largest
+// always stays) -- then sample_gpt_token_from_logits (:1720-1750): one
+// splitmix64 draw u, target u * sum exp(s - max), walked in index order.
+// Every float and double operation is the reference's, in its order; the
+// sequential sums run in one thread.  One block.  With top-k <= 1024 the
+// k-th largest score comes from a radix select and only the survivors are
+// sorted; otherwise every (score, index) pair is sorted in LDS (bitonic,
+// 16384 slots) -- the slow path, for settings without top-k.  The processed
+// logits go to `proc`.
+constexpr int kSortN = 16384;
+constexpr int kSampleThreads = 1024;
+constexpr int kSmallList = 1024;  // survivors listed in index order when this few
+
+__device__ __forceinline__ bool pair_less(float av, uint32_t ai, float bv, uint32_t bi) {
+  return av < bv || (av == bv && ai < bi);
+}
+
+__device__ __forceinline__ double sm64_unit(uint64_t& s) {
+  uint64_t z = (s += 0x9E3779B97F4A7C15ULL);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  z = z ^ (z >> 31);
+  return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* logits, GptState* st,
+                                                                uint32_t* predicted, uint32_t* inputs,
+                                                                float* proc) {
+  if (st->stopped) return;
+  __shared__ float sv[kSortN];
+  __shared__ uint32_t si[kSortN];
+  __shared__ uint32_t seen[(kVocab + 31) / 32];
+  __shared__ uint32_t lidx[kSmallList];  // survivors by index (small case)
+  __shared__ int s_p0;
+  const int tid = threadIdx.x;
+  const int N = kVocab;
+  const float penalty = st->penalty, temperature = st->temperature, top_p = st->top_p;
+  const int top_k = st->top_k;
+  for (int i = tid; i < kSortN; i += kSampleThreads) {
+    sv[i] = i < N ? logits[i] : -INFINITY;
+    si[i] = (uint32_t)i;
+  }
+  for (int i = tid; i < (N + 31) / 32; i += kSampleThreads) seen[i] = 0u;
+  __syncthreads();
+  if (penalty != 1.0f) {  // each distinct history token once (the order does not matter)
+    for (int h = tid; h < st->n_in; h += kSampleThreads) {
+      const uint32_t t = inputs[h];
+      if (t >= (uint32_t)N) continue;
+      const uint32_t bit = 1u << (t & 31);
+      if (atomicOr(&seen[t >> 5], bit) & bit) continue;
+      sv[t] = sv[t] < 0.0f ? sv[t] * penalty : sv[t] / penalty;
+    }
+    __syncthreads();
+  }
+  if (temperature != 1.0f) {
+    for (int i = tid; i < N; i += kSampleThreads) sv[i] /= temperature;
+    __syncthreads();
+  }
+  for (int i = tid; i < N; i += kSampleThreads) proc[i] = sv[i];  // index order, filtered below
+  const bool use_k = top_k > 0 && top_k < N, use_p = top_p < 1.0f;
+  int p0 = kSortN - N;  // first survivor in sorted order (the pads sort first)
+  bool listed_by_index = false;
+  if (use_k && top_k <= kSmallList) {
+    // Top-k without sorting every score: the k-th largest by a 4 x 8-bit radix
+    // select on order-preserving keys, the survivors (scores >= it) listed in
+    // index order by a block prefix sum, and only they sorted by (score,
+    // index), into the last slots of sv / si (pad slots: kSortN - 1024 > N).
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_prefix, s_kleft, s_wsum[kSampleThreads / 64], s_m;
+    auto key_of = [](float f) {
+      const uint32_t u = __float_as_uint(f);
+      return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    };
+    if (tid == 0) { s_prefix = 0u; s_kleft = (uint32_t)top_k; }
+    uint32_t mask = 0u;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      if (tid < 256) hist[tid] = 0u;
+      __syncthreads();
+      const uint32_t prefix = s_prefix;
+      for (int i = tid; i < N; i += kSampleThreads) {
+        const uint32_t key = key_of(sv[i]);
+        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t cum = 0u;
+        const uint32_t kleft = s_kleft;
+        for (int b = 255; b >= 0; --b) {
+          if (cum + hist[b] >= kleft) {
+            s_prefix = prefix | ((uint32_t)b << shift);
+            s_kleft = kleft - cum;
+            break;
+          }
+          cum += hist[b];
+        }
+      }
+      mask |= 255u << shift;
+      __syncthreads();
+    }
+    const uint32_t pk = s_prefix;
+    const float pivot = __uint_as_float((pk & 0x80000000u) ? (pk & 0x7fffffffu) : ~pk);
+    // survivors in index order: thread t owns indices 9 t .. 9 t + 8
+    constexpr int kPer = (kVocab + kSampleThreads - 1) / kSampleThreads;
+    int cnt = 0;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int i = tid * kPer + e;
+      cnt += (i < N && sv[i] >= pivot) ? 1 : 0;
+    }
+    int incl = cnt;  // inclusive scan within the wave
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off, kWave);
+      if ((tid & 63) >= off) incl += v;
+    }
+    if ((tid & 63) == 63) s_wsum[tid >> 6] = (uint32_t)incl;
+    __syncthreads();
+    int base = incl - cnt;
+    for (int w2 = 0; w2 < (tid >> 6); ++w2) base += (int)s_wsum[w2];
+    if (tid == kSampleThreads - 1) s_m = (uint32_t)(base + cnt);
+    __syncthreads();
+    const int mm = (int)s_m;
+    if (mm <= kSmallList) {
+      const int slot0 = kSortN - mm;
+      int q = base;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const int i = tid * kPer + e;
+        if (i < N && sv[i] >= pivot) {
+          lidx[q] = (uint32_t)i;
+          ++q;
+        }
+      }
+      __syncthreads();  // every sv[i] < kSortN - 1024 read before the tail is rewritten
+      int S = 2;
+      while (S < mm) S <<= 1;
+      const int seg = kSortN - S;
+      for (int t = tid; t < S; t += kSampleThreads) {
+        const int j = t - (S - mm);
+        if (j >= 0) { sv[seg + t] = proc[lidx[j]]; si[seg + t] = lidx[j]; }
+        else { sv[seg + t] = -INFINITY; si[seg + t] = 0xffffffffu; }
+      }
+      __syncthreads();
+      for (int k = 2; k <= S; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+          for (int i = tid; i < S; i += kSampleThreads) {
+            const int ixj = i ^ j;
+            if (ixj <= i) continue;
+            const bool up = (i & k) == 0;
+            const float a = sv[seg + i], b = sv[seg + ixj];
+            const uint32_t ai = si[seg + i], bi = si[seg + ixj];
+            if (pair_less(b, bi, a, ai) == up) {
+              sv[seg + i] = b; sv[seg + ixj] = a;
+              si[seg + i] = bi; si[seg + ixj] = ai;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      for (int i = tid; i < N; i += kSampleThreads)
+        if (proc[i] < pivot) proc[i] = -INFINITY;
+      p0 = slot0;
+      listed_by_index = true;
+      __syncthreads();
+    }
+  }
+  if ((use_k || use_p) && !listed_by_index) {
+    // ascending by (score, index)
+    for (int k = 2; k <= kSortN; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < kSortN; i += kSampleThreads) {
+          const int ixj = i ^ j;
+          if (ixj <= i) continue;
+          const bool up = (i & k) == 0;
+          const float a = sv[i], b = sv[ixj];
+          const uint32_t ai = si[i], bi = si[ixj];
+          if (pair_less(b, bi, a, ai) == up) {
+            sv[i] = b; sv[ixj] = a;
+            si[i] = bi; si[ixj] = ai;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (use_k) {  // keep the scores >= the k-th largest
+      const float pivot = sv[kSortN - top_k];
+      for (int p = tid; p < kSortN; p += kSampleThreads)
+        if (sv[p] >= pivot && (p == 0 || sv[p - 1] < pivot)) s_p0 = p;
+      __syncthreads();
+      p0 = s_p0;
+      for (int i = tid; i < N; i += kSampleThreads)
+        if (proc[i] < pivot) proc[i] = -INFINITY;
+      __syncthreads();
+    }
+  }
+  const int m = kSortN - p0;  // survivors (finite), sorted positions p0 .. kSortN-1
+  const bool small = m <= kSmallList;
+  if (small && (use_k || use_p) && !listed_by_index) {  // the survivors' indices in index order (bitonic, m <= 1024)
+    if (tid < kSmallList) lidx[tid] = tid < m ? si[p0 + tid] : 0xffffffffu;
+    __syncthreads();
+    for (int k = 2; k <= kSmallList; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const int i = tid;
+        const int ixj = i ^ j;
+        if (i < kSmallList && ixj > i) {
+          const bool up = (i & k) == 0;
+          const uint32_t a = lidx[i], b = lidx[ixj];
+          if ((b < a) == up) { lidx[i] = b; lidx[ixj] = a; }
+        }
+        __syncthreads();
+      }
+    }
+  }
+  // the largest score (sorted: the last slot; else a block-wide max)
+  __shared__ float s_wmax[kSampleThreads / 64];
+  float mx;
+  if (use_k || use_p) {
+    mx = sv[kSortN - 1];
+  } else {
+    float v = -INFINITY;
+    for (int i = tid; i < N; i += kSampleThreads) v = fmaxf(v, proc[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    if ((tid & 63) == 0) s_wmax[tid >> 6] = v;
+    __syncthreads();
+    mx = s_wmax[0];
+    for (int w2 = 1; w2 < kSampleThreads / 64; ++w2) mx = fmaxf(mx, s_wmax[w2]);
+  }
+  // small case: every survivor's exp(score - max) in parallel, by index order
+  // (pl) and by sorted order (ps); the sums stay sequential (thread 0)
+  __shared__ double pl[kSmallList], ps[kSmallList];
+  const bool listed = small && (use_k || use_p);
+  if (listed && tid < m) {
+    pl[tid] = exp((double)(proc[lidx[tid]] - mx));
+    ps[tid] = exp((double)(sv[p0 + tid] - mx));
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  // survivors in index order: (index, its exp) -- removed ones are skipped
+  auto index_walk = [&](auto&& f) {
+    if (listed) {
+      for (int q = 0; q < m; ++q) {
+        const uint32_t i = lidx[q];
+        if (proc[i] != -INFINITY) f(i, pl[q]);
+      }
+    } else {
+      for (int i = 0; i < N; ++i) {
+        const float v = proc[i];
+        if (v != -INFINITY) f((uint32_t)i, exp((double)(v - mx)));
+      }
+    }
+  };
+  if (use_p) {
+    double total = 0.0;
+    index_walk([&](uint32_t, double pr) { total += pr; });
+    const double low_tail = 1.0 - (double)top_p;
+    double cumulative = 0.0;
+    for (int p = p0; p < kSortN; ++p) {
+      cumulative += (listed ? ps[p - p0] : exp((double)(sv[p] - mx))) / total;
+      if (cumulative <= low_tail && p != kSortN - 1) proc[si[p]] = -INFINITY;
+    }
+  }
+  double total = 0.0;
+  index_walk([&](uint32_t, double pr) { total += pr; });
+  uint64_t rng = st->rng;
+  const double target = sm64_unit(rng) * total;
+  st->rng = rng;
+  double cumulative = 0.0;
+  uint32_t last = 0, pick = 0xffffffffu;
+  index_walk([&](uint32_t i, double pr) {
+    if (pick != 0xffffffffu || pr <= 0.0) return;
+    last = i;
+    cumulative += pr;
+    if (target < cumulative) pick = i;
+  });
+  const int next = (int)(pick == 0xffffffffu ? last : pick);
+  st->argmax = next;
+  if (st->n_pred < st->max_pred) predicted[st->n_pred] = (uint32_t)next;
+  st->n_pred += 1;
+  if (next == kStop) {
+    st->stopped = 1;
+    st->stop_step = st->step;
+  } else {
+    if (st->n_in < st->max_pred + 1) inputs[st->n_in] = (uint32_t)next;
+    st->n_in += 1;
+    st->cur_token = next;
+  }
+  st->step += 1;
+}
+
 // Rows kv .. kv + mrows - 1 of the prefix into the chunk buffer.
 __global__ __launch_bounds__(256) void embed_rows_kernel(const GptState* st, const float* rows, float* x) {
   const int mrows = min(kPrefillRows, st->pend - st->kv);
@@ -684,6 +986,7 @@ struct GptDecoder::Impl {
   uint32_t *predicted = nullptr, *inputs = nullptr;
   float *x, *q, *att, *fc, *logits, *lnf, *fn, *blk_val, *kc, *vc, *rows;
   float *xr, *qr, *attr, *fcr;  // a prefill chunk's rows: [8][1280] x3, [8][5120]
+  float* proc = nullptr;        // the sampler's processed logits [8194]
   float* part = nullptr;        // attention splits: [8 query rows][20 heads][nsplit_max][66]
   int nsplit_max = 0;
 
@@ -694,8 +997,9 @@ struct GptDecoder::Impl {
   }
   int* blk_idx;
   GptState* host_state = nullptr;  // pinned
-  // row, row + head, token + head, prefill chunk, kStepsPerCheck token steps
-  hipGraphExec_t graph[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+  // row, row + head, token + head, prefill chunk, kStepsPerCheck token steps,
+  // then the sampled forms of the last two token graphs
+  hipGraphExec_t graph[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   bool use_graph = true;  // env MIT2CFM_GRAPH=0: launch every kernel directly (for profilers)
 
@@ -771,7 +1075,7 @@ struct GptDecoder::Impl {
                    align256(kVocab * f) + 2 * align256(kW * f) + align256((size_t)head_blocks() * f) +
                    align256((size_t)head_blocks() * 4) +
                    3 * align256((size_t)kPrefillRows * kW * f) + align256((size_t)kPrefillRows * kMLP * f) +
-                   align256((size_t)kPrefillRows * kHeads * (cap / kChunk) * kPartF * f) +
+                   align256((size_t)kPrefillRows * kHeads * (cap / kChunk) * kPartF * f) + align256(kVocab * f) +
                    2 * align256((size_t)L * cap * kW * f) + align256((size_t)rows_cap * kW * f);
     ws.reserve(bytes);
     st = static_cast<GptState*>(ws.take(sizeof(GptState)));
@@ -790,6 +1094,7 @@ struct GptDecoder::Impl {
     qr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
     attr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
     fcr = static_cast<float*>(ws.take((size_t)kPrefillRows * kMLP * f));
+    proc = static_cast<float*>(ws.take(kVocab * f));
     nsplit_max = cap / kChunk;
     part = static_cast<float*>(ws.take((size_t)kPrefillRows * kHeads * nsplit_max * kPartF * f));
     kc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
@@ -806,7 +1111,7 @@ struct GptDecoder::Impl {
 
   // One token step: embed (mode 0: prefix row, 1: token), the layers, and the
   // head when `head` is set.
-  void enqueue_step(int mode, bool head) {
+  void enqueue_step(int mode, bool head, bool sample = false) {
     hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(320), 0, s, st, mel_emb, pos_emb, rows, mode, x);
     for (int l = 0; l < L; ++l) {
       const GptLayerDev& w = layer[l];
@@ -832,8 +1137,11 @@ struct GptDecoder::Impl {
       a.w = head_w; a.bias = head_b; a.N = kVocab; a.x = x; a.g1 = lnf_w; a.b1 = lnf_b; a.g2 = fn_w;
       a.b2 = fn_b; a.y = logits; a.blk_val = blk_val; a.blk_idx = blk_idx; a.lnf_out = lnf; a.fn_out = fn;
       launch_head(a, s);
-      hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, blk_val, blk_idx, head_blocks(), st, predicted,
-                         inputs, 1);
+      if (sample)
+        hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, s, logits, st, predicted, inputs, proc);
+      else
+        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, blk_val, blk_idx, head_blocks(), st, predicted,
+                           inputs, 1);
     }
     GPT_OK(hipGetLastError());
   }
@@ -864,12 +1172,16 @@ struct GptDecoder::Impl {
     GPT_OK(hipGetLastError());
   }
 
-  void run_step(int which) {  // 0 row, 1 row + head, 2 token + head, 3 prefill chunk, 4 = 2 x kStepsPerCheck
+  // 0 row, 1 row + head, 2 token + head, 3 prefill chunk, 4 = 2 x kStepsPerCheck,
+  // 5 token + head + sampler, 6 = 5 x kStepsPerCheck
+  void run_step(int which) {
     auto enqueue = [&] {
       if (which == 3) {
         enqueue_chunk();
-      } else if (which == 4) {
-        for (int i = 0; i < kStepsPerCheck; ++i) enqueue_step(1, true);
+      } else if (which == 4 || which == 6) {
+        for (int i = 0; i < kStepsPerCheck; ++i) enqueue_step(1, true, which == 6);
+      } else if (which == 5) {
+        enqueue_step(1, true, true);
       } else {
         enqueue_step(which == 2 ? 1 : 0, which != 0);
       }
@@ -910,8 +1222,18 @@ struct GptDecoder::Impl {
     }
   }
 
-  void reset_state(int prefix_rows, int pend, bool hf, int steps) {
+  void reset_state(int prefix_rows, int pend, bool hf, int steps, const GptDecoder::Sampling* smp = nullptr) {
     GptState h{};
+    h.temperature = 1.0f;
+    h.top_p = 1.0f;
+    h.penalty = 1.0f;
+    if (smp) {
+      h.top_k = (int32_t)smp->top_k;
+      h.temperature = smp->temperature;
+      h.top_p = smp->top_p;
+      h.penalty = smp->repetition_penalty;
+      h.rng = smp->seed;
+    }
     h.kv = 0;
     h.step = 0;
     h.n_pred = 0;
@@ -1046,6 +1368,20 @@ size_t GptDecoder::weight_bytes() const { return d_->wa.used(); }
 int GptDecoder::layers() const { return d_->L; }
 
 void GptDecoder::kv_greedy(const float* prefix, int prefix_tokens, int steps, bool hf, Greedy& out) {
+  generate(prefix, prefix_tokens, steps, hf, nullptr, out);
+}
+
+void GptDecoder::kv_sample(const float* prefix, int prefix_tokens, int steps, bool hf, const Sampling& sampling,
+                           Greedy& out) {
+  // apply_gpt_sampling_processors' checks (gpt.cpp:1624-1662)
+  if (!(sampling.temperature > 0.0f)) throw std::invalid_argument("gpt: sampling temperature must be positive");
+  if (!(sampling.repetition_penalty > 0.0f)) throw std::invalid_argument("gpt: repetition penalty must be positive");
+  if (!(sampling.top_p > 0.0f && sampling.top_p <= 1.0f)) throw std::invalid_argument("gpt: top_p must be in (0, 1]");
+  generate(prefix, prefix_tokens, steps, hf, &sampling, out);
+}
+
+void GptDecoder::generate(const float* prefix, int prefix_tokens, int steps, bool hf, const Sampling* sampling,
+                          Greedy& out) {
   Impl& d = *d_;
   if (prefix_tokens < 0 || steps < 0) throw std::invalid_argument("gpt: prefix_tokens and steps must be >= 0");
   if (prefix_tokens > 0 && !prefix) throw std::invalid_argument("gpt: prefix must not be NULL");
@@ -1056,7 +1392,7 @@ void GptDecoder::kv_greedy(const float* prefix, int prefix_tokens, int steps, bo
                                   std::to_string(kPos) + "-row mel position table");
   }
   d.ensure(prefix_tokens + steps + 1, prefix_tokens + 1, steps);
-  d.reset_state(prefix_tokens, prefix_tokens, hf, steps);
+  d.reset_state(prefix_tokens, prefix_tokens, hf, steps, sampling);
   if (prefix_tokens > 0)
     GPT_OK(hipMemcpyAsync(d.rows, prefix, (size_t)prefix_tokens * kW * sizeof(float), hipMemcpyHostToDevice, d.s));
   GPT_OK(hipEventRecord(d.ev[0], d.s));
@@ -1066,9 +1402,9 @@ void GptDecoder::kv_greedy(const float* prefix, int prefix_tokens, int steps, bo
   while (done < steps) {
     const int n = std::min(kStepsPerCheck, steps - done);
     if (n == kStepsPerCheck) {
-      d.run_step(4);  // one graph of kStepsPerCheck steps
+      d.run_step(sampling ? 6 : 4);  // one graph of kStepsPerCheck steps
     } else {
-      for (int i = 0; i < n; ++i) d.run_step(2);
+      for (int i = 0; i < n; ++i) d.run_step(sampling ? 5 : 2);
     }
     done += n;
     GPT_OK(hipMemcpyAsync(d.host_state, d.st, sizeof(GptState), hipMemcpyDeviceToHost, d.s));
@@ -1086,6 +1422,10 @@ void GptDecoder::kv_greedy(const float* prefix, int prefix_tokens, int steps, bo
   if (h.n_pred) GPT_OK(hipMemcpy(out.predicted.data(), d.predicted, (size_t)h.n_pred * 4, hipMemcpyDeviceToHost));
   GPT_OK(hipMemcpy(out.input_tokens.data(), d.inputs, (size_t)h.n_in * 4, hipMemcpyDeviceToHost));
   if (steps > 0) GPT_OK(hipMemcpy(out.last_logits.data(), d.logits, kVocab * sizeof(float), hipMemcpyDeviceToHost));
+  out.last_processed_logits.assign(steps > 0 ? kVocab : 0, 0.f);
+  if (steps > 0)
+    GPT_OK(hipMemcpy(out.last_processed_logits.data(), sampling ? d.proc : d.logits, kVocab * sizeof(float),
+                     hipMemcpyDeviceToHost));
   float ms = 0.f;
   GPT_OK(hipEventElapsedTime(&ms, d.ev[0], d.ev[1]));
   out.prefill_ms = ms;

@@ -115,6 +115,8 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_gpt_kv_greedy": (st, [vp, _f32p, u32, u32, i32, _u32p, _u32p, _u32p, _u32p,
                                        ctypes.POINTER(i32), _f32p, ctypes.POINTER(ctypes.c_double)]),
         "mit2cfm_gpt_cached_decode": (st, [vp, _f32p, u32, _f32p, _f32p, _f32p, _u32p]),
+        "mit2cfm_gpt_kv_sample": (st, [vp, _f32p, u32, u32, i32, ctypes.POINTER(_GptSampling), _u32p, _u32p, _u32p,
+                                       _u32p, ctypes.POINTER(i32), _f32p, _f32p, ctypes.POINTER(ctypes.c_double)]),
         "mit2cfm_gpt_profile_launch": (st, [vp, i32, u32, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_char_p)]),
     }
@@ -124,6 +126,11 @@ def lib() -> ctypes.CDLL:
         fn.argtypes = args
     _lib = L
     return L
+
+
+class _GptSampling(ctypes.Structure):
+    _fields_ = [("seed", ctypes.c_uint64), ("temperature", ctypes.c_float), ("top_k", ctypes.c_uint32),
+                ("top_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float)]
 
 
 def declared_symbols() -> list[str]:
@@ -593,6 +600,31 @@ class Context:
                                             _pu(inp), _pu(n_in), ctypes.byref(stop), _p(logits), t))
         return {"predicted": pred[:n_pred[0]].copy(), "input_tokens": inp[:n_in[0]].copy(),
                 "first_stop_step": int(stop.value), "last_logits": logits if steps > 0 else None,
+                "prefill_ms": float(t[0]), "decode_ms": float(t[1])}
+
+    def gpt_kv_sample(self, prefix, steps: int, seed: int, temperature: float = 1.0, top_k: int = 0,
+                      top_p: float = 1.0, repetition_penalty: float = 1.0,
+                      hf_generate_positions: bool = False) -> dict:
+        """The sampled loop (gpt.cpp:2221-2240); as gpt_kv_greedy plus
+        last_processed_logits."""
+        x = _f32(prefix).reshape(-1, GPT_WIDTH)
+        P = x.shape[0]
+        pred = np.zeros(max(steps, 1), np.uint32)
+        inp = np.zeros(steps + 1, np.uint32)
+        n_pred = np.zeros(1, np.uint32)
+        n_in = np.zeros(1, np.uint32)
+        stop = ctypes.c_int32()
+        logits = np.zeros(GPT_VOCAB, np.float32)
+        proc = np.zeros(GPT_VOCAB, np.float32)
+        t = (ctypes.c_double * 2)()
+        cfg = _GptSampling(seed, temperature, top_k, top_p, repetition_penalty)
+        self._c(lib().mit2cfm_gpt_kv_sample(self._h, _p(x) if P else None, P, steps,
+                                            1 if hf_generate_positions else 0, ctypes.byref(cfg), _pu(pred),
+                                            _pu(n_pred), _pu(inp), _pu(n_in), ctypes.byref(stop), _p(logits),
+                                            _p(proc), t))
+        return {"predicted": pred[:n_pred[0]].copy(), "input_tokens": inp[:n_in[0]].copy(),
+                "first_stop_step": int(stop.value), "last_logits": logits if steps > 0 else None,
+                "last_processed_logits": proc if steps > 0 else None,
                 "prefill_ms": float(t[0]), "decode_ms": float(t[1])}
 
     def gpt_cached_decode(self, rows, prefix_tokens: int):

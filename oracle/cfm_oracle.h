@@ -185,6 +185,15 @@ int orc_gpt_kv_greedy(const orc_gpt* m, const float* prefix, uint32_t prefix_tok
 int orc_gpt_greedy_full(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens,
                         uint32_t steps, uint32_t* predicted, uint32_t* input_tokens,
                         float* last_logits, orc_gpt_greedy_result* res); /* gpt.cpp:1833 */
+int orc_gpt_sampling_processors(const float* logits, uint32_t n, const uint32_t* history,
+                                uint32_t n_history, float temperature, uint32_t top_k, float top_p,
+                                float repetition_penalty, float* scores); /* gpt.cpp:1618 */
+uint32_t orc_gpt_sample_token(const float* processed, uint32_t n, uint64_t* rng_state); /* gpt.cpp:1720 */
+int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens, uint32_t steps,
+                      int hf_generate_positions, uint64_t seed, float temperature, uint32_t top_k,
+                      float top_p, float repetition_penalty, uint32_t* predicted,
+                      uint32_t* input_tokens, float* last_logits, float* last_processed,
+                      orc_gpt_greedy_result* res);                   /* gpt.cpp:2221-2240 */
 
 #ifdef __cplusplus
 }

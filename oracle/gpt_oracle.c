@@ -478,3 +478,185 @@ int orc_gpt_greedy_full(const orc_gpt* m, const float* prefix, uint32_t prefix_t
     free(seq); free(fnorm); free(logits);
     return rc;
 }
+
+/* ---- sampling (the do_sample path) ---------------------------------------- */
+
+/* SplitMix64 of the GPT sampler (gpt.cpp:1601-1616). */
+static uint64_t sm64_next(uint64_t* s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+static double sm64_unit(uint64_t* s) { return (double)(sm64_next(s) >> 11) * (1.0 / 9007199254740992.0); }
+
+typedef struct { float v; uint32_t i; } score_idx;
+static int cmp_desc(const void* a, const void* b) {
+    const float x = ((const score_idx*)a)->v, y = ((const score_idx*)b)->v;
+    return x > y ? -1 : (x < y ? 1 : 0);
+}
+static int cmp_asc_idx(const void* a, const void* b) {  /* the top-p order (gpt.cpp:1667-1672) */
+    const score_idx* p = (const score_idx*)a;
+    const score_idx* q = (const score_idx*)b;
+    if (p->v == q->v) return p->i < q->i ? -1 : (p->i > q->i ? 1 : 0);
+    return p->v < q->v ? -1 : 1;
+}
+
+/* apply_gpt_sampling_processors (gpt.cpp:1618-1718): repetition penalty over
+ * the distinct history tokens, temperature, top-k (keep scores >= the k-th
+ * largest), top-p (drop the low tail whose cumulative probability, in
+ * ascending score order, stays <= 1 - top_p; the largest always stays).
+ * Returns 0, or -1 for an invalid setting (the reference throws). */
+int orc_gpt_sampling_processors(const float* logits, uint32_t n, const uint32_t* history, uint32_t n_history,
+                                float temperature, uint32_t top_k, float top_p, float repetition_penalty,
+                                float* scores) {
+    memcpy(scores, logits, n * sizeof(float));
+    if (repetition_penalty != 1.0f) {
+        if (repetition_penalty <= 0.0f) return -1;
+        uint8_t* seen = (uint8_t*)calloc(n, 1);
+        for (uint32_t h = 0; h < n_history; ++h) {
+            const uint32_t t = history[h];
+            if (t >= n || seen[t]) continue;
+            seen[t] = 1;
+            if (scores[t] < 0.0f) scores[t] *= repetition_penalty;
+            else scores[t] /= repetition_penalty;
+        }
+        free(seen);
+    }
+    if (temperature <= 0.0f) return -1;
+    if (temperature != 1.0f)
+        for (uint32_t i = 0; i < n; ++i) scores[i] /= temperature;
+    score_idx* s = (score_idx*)malloc(n * sizeof(score_idx));
+    if (top_k > 0 && top_k < n) {
+        for (uint32_t i = 0; i < n; ++i) { s[i].v = scores[i]; s[i].i = i; }
+        qsort(s, n, sizeof(score_idx), cmp_desc);  /* the k-th largest value, as nth_element */
+        const float pivot = s[top_k - 1].v;
+        for (uint32_t i = 0; i < n; ++i)
+            if (scores[i] < pivot) scores[i] = -INFINITY;
+    }
+    if (top_p < 1.0f) {
+        if (top_p <= 0.0f) { free(s); return -1; }
+        for (uint32_t i = 0; i < n; ++i) { s[i].v = scores[i]; s[i].i = i; }
+        qsort(s, n, sizeof(score_idx), cmp_asc_idx);
+        float max_score = -INFINITY;
+        for (uint32_t i = 0; i < n; ++i)
+            if (isfinite(scores[i]) && scores[i] > max_score) max_score = scores[i];
+        if (!isfinite(max_score)) { free(s); return -1; }
+        double* probs = (double*)calloc(n, sizeof(double));
+        uint8_t* rem = (uint8_t*)calloc(n, 1);
+        double total = 0.0;
+        for (uint32_t i = 0; i < n; ++i)
+            if (isfinite(scores[i])) { probs[i] = exp((double)(scores[i] - max_score)); total += probs[i]; }
+        if (total <= 0.0) { free(s); free(probs); free(rem); return -1; }
+        double cumulative = 0.0;
+        const double low_tail = 1.0 - (double)top_p;
+        uint32_t finite_seen = 0;
+        for (uint32_t o = 0; o < n; ++o) {
+            const uint32_t idx = s[o].i;
+            if (!isfinite(scores[idx])) { rem[idx] = 1; continue; }
+            ++finite_seen;
+            cumulative += probs[idx] / total;
+            if (cumulative <= low_tail) rem[idx] = 1;
+        }
+        if (finite_seen > 0) rem[s[n - 1].i] = 0;
+        for (uint32_t i = 0; i < n; ++i)
+            if (rem[i]) scores[i] = -INFINITY;
+        free(probs);
+        free(rem);
+    }
+    free(s);
+    return 0;
+}
+
+/* sample_gpt_token_from_logits (gpt.cpp:1720-1750): one draw of the
+ * splitmix64 stream, scaled by the total exp mass, walked in index order. */
+uint32_t orc_gpt_sample_token(const float* processed, uint32_t n, uint64_t* rng_state) {
+    float max_score = -INFINITY;
+    for (uint32_t i = 0; i < n; ++i)
+        if (isfinite(processed[i]) && processed[i] > max_score) max_score = processed[i];
+    double* probs = (double*)calloc(n, sizeof(double));
+    double total = 0.0;
+    for (uint32_t i = 0; i < n; ++i)
+        if (isfinite(processed[i])) { probs[i] = exp((double)(processed[i] - max_score)); total += probs[i]; }
+    const double target = sm64_unit(rng_state) * total;
+    double cumulative = 0.0;
+    uint32_t last_finite = 0, pick = UINT32_MAX;
+    for (uint32_t i = 0; i < n && pick == UINT32_MAX; ++i) {
+        if (probs[i] <= 0.0) continue;
+        last_finite = i;
+        cumulative += probs[i];
+        if (target < cumulative) pick = i;
+    }
+    free(probs);
+    return pick == UINT32_MAX ? last_finite : pick;
+}
+
+/* The sampled form of the cached loop (run_gpt_kv_greedy_metal with
+ * do_sample, gpt.cpp:2221-2240): after each step's logits, the processors over
+ * the history [start token, predictions so far] and one draw; the rng is
+ * seeded once per call.  last_processed receives the last step's processed
+ * logits.  Returns 0, or -1 (a position past the table or an invalid
+ * setting). */
+int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens, uint32_t steps, int hf,
+                      uint64_t seed, float temperature, uint32_t top_k, float top_p, float repetition_penalty,
+                      uint32_t* predicted, uint32_t* input_tokens, float* last_logits, float* last_processed,
+                      orc_gpt_greedy_result* res) {
+    const uint32_t P = prefix_tokens, cap = P + steps + 1;
+    const int NL = m->layers;
+    float* ck = (float*)malloc((size_t)NL * cap * W * sizeof(float));
+    float* cv = (float*)malloc((size_t)NL * cap * W * sizeof(float));
+    float* hid = (float*)malloc(((size_t)P + 1) * W * sizeof(float));
+    float* nxt = (float*)malloc(((size_t)P + 1) * W * sizeof(float));
+    float* qkv = (float*)malloc(((size_t)P + 1) * QKV * sizeof(float));
+    float cur[W], cur_qkv[QKV], out[W], ln_f[W], fnorm[W];
+    uint64_t rng = seed;
+    int rc = 0;
+    res->n_predicted = 0;
+    res->n_input = 1;
+    res->first_stop_step = -1;
+    input_tokens[0] = START_TOKEN;
+    memcpy(hid, prefix, (size_t)P * W * sizeof(float));
+    for (int l = 0; l < NL; ++l) {
+        float* K = ck + (size_t)l * cap * W;
+        float* V = cv + (size_t)l * cap * W;
+        orc_gpt_layer_qkv(m, hid, P, (uint32_t)l, qkv);
+        for (uint32_t t = 0; t < P; ++t) {
+            memcpy(K + (size_t)t * W, qkv + (size_t)t * QKV + W, W * sizeof(float));
+            memcpy(V + (size_t)t * W, qkv + (size_t)t * QKV + 2 * W, W * sizeof(float));
+        }
+        if (P) orc_gpt_block(m, hid, P, (uint32_t)l, nxt);
+        float* t = hid; hid = nxt; nxt = t;
+    }
+    uint32_t kv = P;
+    for (uint32_t step = 0; step < steps; ++step) {
+        const uint32_t tok = input_tokens[res->n_input - 1];
+        const uint32_t pos = generate_position(step, hf);
+        if (pos >= POS || tok >= VOCAB) { rc = -1; break; }
+        for (uint32_t c = 0; c < W; ++c)
+            cur[c] = m->mel_emb[(size_t)tok * W + c] + m->pos_emb[(size_t)pos * W + c];
+        for (int l = 0; l < NL; ++l) {
+            float* K = ck + (size_t)l * cap * W;
+            float* V = cv + (size_t)l * cap * W;
+            orc_gpt_layer_qkv(m, cur, 1, (uint32_t)l, cur_qkv);
+            orc_gpt_cached_block_current(m, K, V, kv, cur, cur_qkv, (uint32_t)l, out);
+            memcpy(K + (size_t)kv * W, cur_qkv + W, W * sizeof(float));
+            memcpy(V + (size_t)kv * W, cur_qkv + 2 * W, W * sizeof(float));
+            memcpy(cur, out, sizeof(cur));
+        }
+        ++kv;
+        head_row(m, cur, ln_f, fnorm, last_logits);
+        /* the history: the start token, then every prediction so far (the loop
+         * stops at the first stop token, so these are the input tokens) */
+        if (orc_gpt_sampling_processors(last_logits, VOCAB, input_tokens, res->n_input, temperature, top_k, top_p,
+                                        repetition_penalty, last_processed) != 0) { rc = -1; break; }
+        const uint32_t next = orc_gpt_sample_token(last_processed, VOCAB, &rng);
+        predicted[res->n_predicted++] = next;
+        if (next == STOP_TOKEN) {
+            res->first_stop_step = (int32_t)step;
+            break;
+        }
+        input_tokens[res->n_input++] = next;
+    }
+    free(ck); free(cv); free(hid); free(nxt); free(qkv);
+    return rc;
+}

@@ -107,6 +107,10 @@ def lib() -> ctypes.CDLL:
                                         ctypes.POINTER(_GreedyResult)]),
             "orc_gpt_greedy_full": (i32, [vp, _f32p, u32, u32, _u32p, _u32p, _f32p,
                                           ctypes.POINTER(_GreedyResult)]),
+            "orc_gpt_sampling_processors": (i32, [_f32p, u32, _u32p, u32, f32, u32, f32, f32, _f32p]),
+            "orc_gpt_sample_token": (u32, [_f32p, u32, ctypes.POINTER(u64)]),
+            "orc_gpt_kv_sample": (i32, [vp, _f32p, u32, u32, i32, u64, f32, u32, f32, f32, _u32p, _u32p,
+                                        _f32p, _f32p, ctypes.POINTER(_GreedyResult)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -579,6 +583,27 @@ def attention_causal(q, k, v) -> np.ndarray:
     return out
 
 
+def gpt_sampling_processors(logits, history, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0):
+    """apply_gpt_sampling_processors (gpt.cpp:1618)."""
+    x = f32(logits)
+    h = u32(history)
+    out = np.empty_like(x)
+    if lib().orc_gpt_sampling_processors(P(x), x.size, PU(h), h.size, temperature, top_k, top_p,
+                                         repetition_penalty, P(out)) != 0:
+        raise ValueError("invalid sampling setting")
+    return out
+
+
+def gpt_sample_token(processed, rng_state):
+    """sample_gpt_token_from_logits (gpt.cpp:1720); rng_state is a one-element
+    numpy uint64 array, advanced in place."""
+    x = f32(processed)
+    st = ctypes.c_uint64(int(rng_state[0]))
+    tok = lib().orc_gpt_sample_token(P(x), x.size, ctypes.byref(st))
+    rng_state[0] = st.value
+    return int(tok)
+
+
 class GPT:
     """The reference's fp32 CPU GPT decoder (runtime/impl/gpt.cpp) over the given
     gpt.* tensors (checkpoint layouts; layers 0..L-1 present)."""
@@ -659,6 +684,25 @@ class GPT:
     def kv_greedy(self, prefix, steps, hf_generate_positions=False):
         """run_gpt_kv_greedy_cpu (gpt.cpp:1877)."""
         return self._greedy(lib().orc_gpt_kv_greedy, prefix, steps, 1 if hf_generate_positions else 0)
+
+    def kv_sample(self, prefix, steps, seed, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0,
+                  hf_generate_positions=False):
+        """The sampled cached loop (gpt.cpp:2221-2240); also returns
+        last_processed_logits."""
+        x = f32(prefix).reshape(-1, GPT_W)
+        pred = np.zeros(max(steps, 1), np.uint32)
+        inp = np.zeros(steps + 1, np.uint32)
+        lg = np.zeros(GPT_VOCAB, np.float32)
+        lp = np.zeros(GPT_VOCAB, np.float32)
+        r = _GreedyResult()
+        rc = lib().orc_gpt_kv_sample(self._h, P(x), x.shape[0], steps, 1 if hf_generate_positions else 0, seed,
+                                     temperature, top_k, top_p, repetition_penalty, PU(pred), PU(inp), P(lg),
+                                     P(lp), ctypes.byref(r))
+        if rc != 0:
+            raise ValueError("GPT oracle: invalid sampling setting or position beyond the table")
+        return {"predicted": pred[:r.n_predicted].copy(), "input_tokens": inp[:r.n_input].copy(),
+                "first_stop_step": int(r.first_stop_step), "last_logits": lg if steps > 0 else None,
+                "last_processed_logits": lp if steps > 0 else None}
 
     def greedy_full(self, prefix, steps):
         """run_gpt_greedy_cpu (gpt.cpp:1833): the uncached loop (no stop)."""

@@ -207,3 +207,48 @@ def test_chunked_prefill_equals_row_prefill(ctx2, monkeypatch, P):
           f"logits max-abs {err:.2e}", flush=True)
     assert chunked["predicted"].tolist() == rows["predicted"].tolist()
     assert err <= 1e-5
+
+
+# IndexTTS2's generation settings (do_sample, top_p 0.8, top_k 30, temperature
+# 0.8, repetition_penalty 10.0) and settings that take the sampler's other paths.
+SAMPLING_CASES = [
+    dict(temperature=0.8, top_k=30, top_p=0.8, repetition_penalty=10.0),
+    dict(temperature=1.0, top_k=4, top_p=0.95, repetition_penalty=2.0),
+    dict(temperature=0.7, top_k=0, top_p=0.9, repetition_penalty=1.0),   # top-p over every token
+    dict(temperature=1.3, top_k=0, top_p=1.0, repetition_penalty=1.0),   # no filter
+    dict(temperature=1.0, top_k=1, top_p=1.0, repetition_penalty=1.0),   # = greedy
+]
+
+
+def _compare_sampled(got, ref, label):
+    _compare(got, ref, label)
+    a, b = got["last_processed_logits"], ref["last_processed_logits"]
+    assert np.array_equal(np.isfinite(a), np.isfinite(b))
+    fin = np.isfinite(b)
+    assert np.abs(a[fin] - b[fin]).max() <= LOGITS_TOL * 10  # temperature / penalty scale the logits
+
+
+def test_sampled_decode_matches_oracle_24_layers(ctx24, orc24):
+    prefix = _prefix(20)
+    cfg = SAMPLING_CASES[0]
+    print(f"sampled 24 layers {cfg}", flush=True)
+    _compare_sampled(ctx24.gpt_kv_sample(prefix, 10, 20240605, **cfg),
+                     orc24.kv_sample(prefix, 10, 20240605, **cfg), "  24 layers sampled")
+
+
+@pytest.mark.parametrize("case", range(len(SAMPLING_CASES)))
+def test_sampled_decode_paths(ctx2, orc2, case):
+    prefix = _prefix(30, seed=40 + case)
+    cfg = SAMPLING_CASES[case]
+    print(f"sampled 2 layers {cfg}", flush=True)
+    got = ctx2.gpt_kv_sample(prefix, 12, 7 + case, **cfg)
+    _compare_sampled(got, orc2.kv_sample(prefix, 12, 7 + case, **cfg), "  2 layers sampled")
+    if cfg["top_k"] == 1:
+        assert got["predicted"].tolist() == ctx2.gpt_kv_greedy(prefix, 12)["predicted"].tolist()
+
+
+def test_sampling_settings_rejected(ctx2, mit2):
+    for bad in (dict(temperature=0.0), dict(repetition_penalty=0.0), dict(top_p=0.0), dict(top_p=1.5)):
+        with pytest.raises(mit2.Mit2CfmError) as e:
+            ctx2.gpt_kv_sample(_prefix(3), 2, 1, **bad)
+        assert e.value.status == mit2.E_ARG

@@ -224,3 +224,56 @@ def test_planted_mistake_is_caught(orc, gpt_t, hf):
         h = hf(inputs_embeds=torch.from_numpy(x)[None]).last_hidden_state[0].double().numpy()
     _, ref_logits = _head(gpt_t, h)
     assert np.abs(logits - ref_logits).max() / np.abs(ref_logits).max() > 1e-3
+
+
+def test_sampling_processors_reference_vector(orc):
+    """run_gpt_sampling_processors_test (gpt.cpp:1757-1800): its logits, history
+    and settings; its expected filtering, values and sampled token."""
+    logits = np.arange(-2, 8, dtype=np.float32)
+    processed = orc.gpt_sampling_processors(logits, [2, 7, 3, 7], temperature=0.5, top_k=4, top_p=0.95,
+                                            repetition_penalty=2.0)
+    assert not np.isfinite(processed[[0, 5, 6]]).any()
+    assert np.isfinite(processed[[8, 9]]).all()
+    assert abs(processed[8] - 12.0) <= 1e-6 and abs(processed[9] - 14.0) <= 1e-6
+    rng = np.array([20240605], np.uint64)
+    assert orc.gpt_sample_token(processed, rng) == 9
+
+
+def test_sampling_processors_closed_forms(orc):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(300).astype(np.float32) * 3
+    # temperature alone divides; top_k keeps the k largest (ties kept); top_p keeps the
+    # smallest set of largest scores whose mass exceeds top_p
+    assert np.array_equal(orc.gpt_sampling_processors(x, [], temperature=0.7), x / np.float32(0.7))
+    k = orc.gpt_sampling_processors(x, [], top_k=17)
+    assert np.isfinite(k).sum() == 17 and np.array_equal(np.sort(np.where(np.isfinite(k))[0]),
+                                                         np.sort(np.argsort(-x)[:17]))
+    p = orc.gpt_sampling_processors(x, [], top_p=0.6)
+    order = np.argsort(-x.astype(np.float64), kind="stable")
+    prob = np.exp(x[order].astype(np.float64) - x.max())
+    prob /= prob.sum()
+    keep = np.searchsorted(np.cumsum(prob), 0.6) + 1  # the head whose mass first passes 0.6
+    assert set(np.where(np.isfinite(p))[0]) == set(order[:keep].tolist())
+    # repetition penalty: once per distinct token, divide positives, multiply negatives
+    h = [3, 3, 9, 250]
+    r = orc.gpt_sampling_processors(x, h, repetition_penalty=1.3)
+    ref = x.copy()
+    for t in set(h):
+        ref[t] = ref[t] / np.float32(1.3) if ref[t] >= 0 else ref[t] * np.float32(1.3)
+    assert np.array_equal(r, ref)
+
+
+def test_sample_token_follows_the_distribution(orc):
+    x = np.log(np.array([0.1, 0.2, 0.3, 0.4], np.float32))
+    rng = np.array([7], np.uint64)
+    draws = [orc.gpt_sample_token(x, rng) for _ in range(4000)]
+    freq = np.bincount(draws, minlength=4) / 4000
+    assert np.abs(freq - [0.1, 0.2, 0.3, 0.4]).max() < 0.03
+
+
+def test_kv_sample_with_greedy_settings_equals_greedy(gpt):
+    """top_k = 1 leaves only the maximum, so sampling picks the greedy token."""
+    prefix = _rows(6, 12)
+    s = gpt.kv_sample(prefix, 4, seed=5, top_k=1)
+    g = gpt.kv_greedy(prefix, 4)
+    assert s["predicted"].tolist() == g["predicted"].tolist()
