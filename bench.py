@@ -222,6 +222,12 @@ def gpt_section(a, mit2cfm, tensors, torch):
     ctx.gpt_kv_greedy(prefix, 16)  # warm-up (captures the step graphs)
     runs = [ctx.gpt_kv_greedy(prefix, a.gpt_codes) for _ in range(2)]
     r = min(runs, key=lambda q: q["decode_ms"])
+    # the production setting: IndexTTS2's do_sample (top_p 0.8, top_k 30, temperature 0.8,
+    # repetition penalty 10)
+    smp = dict(temperature=0.8, top_k=30, top_p=0.8, repetition_penalty=10.0)
+    ctx.gpt_kv_sample(prefix, 16, 1, **smp)
+    rs = min((ctx.gpt_kv_sample(prefix, a.gpt_codes, 20240605 + i, **smp) for i in range(2)),
+             key=lambda q: q["decode_ms"] / max(len(q["predicted"]), 1))
     n = len(r["predicted"])
     ms_tok = r["decode_ms"] / n
     step_bytes = mit2cfm.gpt_step_bytes(24)
@@ -244,6 +250,8 @@ def gpt_section(a, mit2cfm, tensors, torch):
            "codes": n, "first_stop_step": r["first_stop_step"],
            "prefill_ms": round(r["prefill_ms"], 3), "decode_ms": round(r["decode_ms"], 3),
            "ms_per_code": round(ms_tok, 4), "codes_per_s": round(1e3 / ms_tok, 1),
+           "sampled": {"settings": smp, "codes": len(rs["predicted"]),
+                       "ms_per_code": round(rs["decode_ms"] / max(len(rs["predicted"]), 1), 4)},
            "weight_gb_per_code": round(step_bytes / 1e9, 4),
            "weight_stream_gb_s": round(step_bytes / (ms_tok / 1e3) / 1e9, 1),
            "reference_published": {"ms_per_code": 5.5, "hardware": "Apple M3 Ultra (Metal, ICB greedy decode)",
