@@ -800,7 +800,7 @@ __global__ __launch_bounds__(320) void embed_kernel(const GptState* st, const fl
 // l_s = sum exp(score - m_s) and unnormalised output sum exp(score - m_s) v;
 // a head with a single split writes its output directly.  attn_combine_kernel
 // merges the splits: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s with
-// M = max m_s.  Scores: 8 lanes per key, 8 dims each; the output: 16 lanes
+// M = max m_s (eight splits per round trip, rescaled when M grows).  Scores: 8 lanes per key, 8 dims each; the output: 16 lanes
 // per key, 4 dims each.  z is the query row of a prefill chunk (row z sees
 // the keys up to its own position kv + z); a decode step has one query.
 constexpr int kAttnThreads = 512;
@@ -905,13 +905,33 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const GptState* st, co
   const int nsplit = (attn_keys(st, z) + kChunk - 1) / kChunk;
   if (nsplit == 1) return;  // written by the split kernel
   const float* ph = part + ((size_t)z * kHeads + h) * nsplit_max * kPartF;
-  float M = -INFINITY;
-  for (int s2 = 0; s2 < nsplit; ++s2) M = fmaxf(M, ph[(size_t)s2 * kPartF]);
-  float L = 0.f, O = 0.f;
-  for (int s2 = 0; s2 < nsplit; ++s2) {
-    const float f = expf(ph[(size_t)s2 * kPartF] - M);
-    L += f * ph[(size_t)s2 * kPartF + 1];
-    O += f * ph[(size_t)s2 * kPartF + 2 + d];
+  // eight splits per round trip (the loads are issued before they are used)
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += 8) {
+    float mm[8], ll[8], oo[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int sx = min(s0 + u, nsplit - 1);
+      mm[u] = ph[(size_t)sx * kPartF];
+      ll[u] = ph[(size_t)sx * kPartF + 1];
+      oo[u] = ph[(size_t)sx * kPartF + 2 + d];
+    }
+    float Mn = M;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < nsplit) Mn = fmaxf(Mn, mm[u]);
+    const float r = expf(M - Mn);  // rescale what is summed so far (0 at the start)
+    L *= r;
+    O *= r;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s0 + u < nsplit) {
+        const float f = expf(mm[u] - Mn);
+        L += f * ll[u];
+        O += f * oo[u];
+      }
+    }
+    M = Mn;
   }
   out[(size_t)z * kW + h * kHD + d] = O / L;
 }
