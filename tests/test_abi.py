@@ -91,3 +91,31 @@ def test_synthetic_generator_is_seeded(mit2):
     assert np.array_equal(a[k], b[k]) and not np.array_equal(a[k], c[k])
     w = a[mit2.PREFIX + "transformer.layers.5.feed_forward.w2.weight"].astype(np.float64)
     assert abs(w.std() - 0.02) < 1e-3 and abs(w.mean()) < 1e-3
+
+
+def test_gpt_entry_points_reject_a_null_context(mit2):
+    """The GPT decoder's entry points check their context before anything else
+    (no GPU is touched)."""
+    L = mit2.lib()
+    u = np.zeros(4, np.uint32)
+    pu = u.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+    i = ctypes.c_int32()
+    f = np.zeros(8194, np.float32)
+    pf = f.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    assert L.mit2cfm_gpt_layers(None, pu) == mit2.E_ARG
+    assert L.mit2cfm_gpt_kv_greedy(None, None, 0, 1, 0, pu, pu, pu, pu, ctypes.byref(i), pf, None) == mit2.E_ARG
+    cfg = mit2._GptSampling(1, 0.8, 30, 0.8, 10.0)
+    assert L.mit2cfm_gpt_kv_sample(None, None, 0, 1, 0, ctypes.byref(cfg), pu, pu, pu, pu, ctypes.byref(i), pf, pf,
+                                   None) == mit2.E_ARG
+    assert L.mit2cfm_gpt_cached_decode(None, pf, 0, pf, pf, pf, pu) == mit2.E_ARG
+    assert L.mit2cfm_gpt_profile_launch(None, 0, 0, None, None) == mit2.E_ARG
+
+
+def test_gpt_synthetic_set_inventory(mit2):
+    specs = mit2.synthetic_set_specs(mit2.SYNTH_GPT)
+    assert len(specs) == 24 * 12 + 8
+    shapes = dict((n, s) for n, s, _ in specs)
+    assert shapes["gpt.gpt.h.0.attn.c_attn.weight"] == (1280, 3840)  # Conv1D [in][out]
+    assert shapes["gpt.mel_pos_embedding.emb.weight"] == (1818, 1280)
+    assert shapes["gpt.mel_head.weight"] == (8194, 1280)
+    assert abs(mit2.gpt_step_bytes(24) - 0.9647e9) < 1e6
