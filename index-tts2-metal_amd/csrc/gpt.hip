@@ -58,7 +58,11 @@ namespace {
 constexpr int kW = 1280, kQKV = 3840, kMLP = 5120, kHeads = 20, kHD = 64;
 constexpr int kVocab = GptDecoder::kVocab, kPos = GptDecoder::kPositions;
 constexpr int kStart = (int)GptDecoder::kStartToken, kStop = (int)GptDecoder::kStopToken;
-constexpr int kChunk = 256;   // keys per attention split
+#ifndef GPT_ATTN_KEYS
+#define GPT_ATTN_KEYS 256
+#endif
+constexpr int kChunk = GPT_ATTN_KEYS;  // keys per attention split
+static_assert(kChunk % 64 == 0 && kChunk <= 512, "a split is whole passes of 64 keys, one score per thread");
 constexpr int kStepsPerCheck = 8;  // decode steps replayed between stop-flag reads
 constexpr int kPrefillRows = 8;    // prefix rows per prefill chunk
 
