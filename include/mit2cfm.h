@@ -134,6 +134,24 @@ mit2cfm_status mit2cfm_synchronize(mit2cfm_ctx* ctx);
 /* Whole-decode hipGraph replay on (1, default) or off (0). */
 mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on);
 
+/* ---- arithmetic of the fp32 stages ---------------------------------------------
+ * The reference runs the length regulator (run_length_regulator_full_metal,
+ * runtime/impl/gpt.cpp:5313; its test bar max-abs 1e-4, :5382-5401) and the
+ * BigVGAN vocoder (kernels.metal:1607-1749, dit_cfm_bigvgan.cpp:4102-4223;
+ * bar max-abs 1e-3, :4469-4490) in fp32.  MIT2CFM_PREC_F32 (the default)
+ * runs their GEMMs on split f16 operand pairs (hi = f16(v), lo = the
+ * rounding remainder, three matrix-core products per term), which gives
+ * fp32-level results; MIT2CFM_PREC_F16 runs them on plain f16 operands
+ * (faster, about 1e-3 relative).  The DiT-CFM decoder itself always uses f16
+ * operands, as the reference's Metal decoder does.  A stage the context has
+ * no tensors for is MIT2CFM_E_MODEL.  No reference counterpart. */
+#define MIT2CFM_STAGE_LENGTH_REGULATOR 1
+#define MIT2CFM_STAGE_VOCODER 2
+#define MIT2CFM_PREC_F16 0
+#define MIT2CFM_PREC_F32 1
+mit2cfm_status mit2cfm_set_precision(mit2cfm_ctx* ctx, int32_t stage, int32_t mode);
+mit2cfm_status mit2cfm_get_precision(mit2cfm_ctx* ctx, int32_t stage, int32_t* mode);
+
 /* ---- measurement hook ------------------------------------------------------------
  * Enqueues `count` back-to-back launches of one decode kernel at the shape of
  * the context's last decode (operands: that decode's workspace), on the
@@ -141,8 +159,10 @@ mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on);
  * on mit2cfm_stream.  Reports the kernel's algorithmic flops and HBM bytes per
  * launch and its name.  Kernel ids: 0 FFN w1|w3 GEMM + SwiGLU, 1 WaveNet
  * k=5 conv GEMM + gate, 2 QKV GEMM + RoPE, 3 FFN w2 GEMM + residual,
- * 4 masked attention, 5 AdaRMSNorm.  No reference counterpart (the reference
- * times whole command buffers, metal_context.mm:463-477). */
+ * 4 masked attention, 5 AdaRMSNorm, 6 attention output projection wo +
+ * residual (folded-norm producer), 7 WaveNet res/skip GEMM.  No reference
+ * counterpart (the reference times whole command buffers,
+ * metal_context.mm:463-477). */
 mit2cfm_status mit2cfm_profile_launch(mit2cfm_ctx* ctx, int32_t kernel, uint32_t count,
                                       double* flops_per_launch, double* bytes_per_launch,
                                       const char** name);

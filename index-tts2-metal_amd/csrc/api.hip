@@ -383,6 +383,29 @@ mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on) {
   return MIT2CFM_OK;
 }
 
+mit2cfm_status mit2cfm_set_precision(mit2cfm_ctx* ctx, int32_t stage, int32_t mode) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  if (mode != MIT2CFM_PREC_F16 && mode != MIT2CFM_PREC_F32)
+    return fail(ctx, MIT2CFM_E_ARG, "precision mode must be MIT2CFM_PREC_F16 or MIT2CFM_PREC_F32");
+  if (stage == MIT2CFM_STAGE_LENGTH_REGULATOR && !ctx->eng->has_length_regulator())
+    return fail(ctx, MIT2CFM_E_MODEL, "the context has no length-regulator tensors");
+  if (stage == MIT2CFM_STAGE_VOCODER && !ctx->eng->has_vocoder())
+    return fail(ctx, MIT2CFM_E_MODEL, "the context has no vocoder tensors");
+  if (stage != MIT2CFM_STAGE_LENGTH_REGULATOR && stage != MIT2CFM_STAGE_VOCODER)
+    return fail(ctx, MIT2CFM_E_ARG, "stage must be MIT2CFM_STAGE_LENGTH_REGULATOR or MIT2CFM_STAGE_VOCODER");
+  return guarded(ctx, [&] { ctx->eng->set_f32(stage, mode == MIT2CFM_PREC_F32); });
+}
+
+mit2cfm_status mit2cfm_get_precision(mit2cfm_ctx* ctx, int32_t stage, int32_t* mode) {
+  if (!ctx || !mode) return fail(ctx, MIT2CFM_E_ARG, "ctx and mode must not be NULL");
+  if ((stage == MIT2CFM_STAGE_LENGTH_REGULATOR && !ctx->eng->has_length_regulator()) ||
+      (stage == MIT2CFM_STAGE_VOCODER && !ctx->eng->has_vocoder()))
+    return fail(ctx, MIT2CFM_E_MODEL, "the context has no tensors for that stage");
+  if (stage != MIT2CFM_STAGE_LENGTH_REGULATOR && stage != MIT2CFM_STAGE_VOCODER)
+    return fail(ctx, MIT2CFM_E_ARG, "stage must be MIT2CFM_STAGE_LENGTH_REGULATOR or MIT2CFM_STAGE_VOCODER");
+  return guarded(ctx, [&] { *mode = ctx->eng->f32(stage) ? MIT2CFM_PREC_F32 : MIT2CFM_PREC_F16; });
+}
+
 mit2cfm_status mit2cfm_profile_launch(mit2cfm_ctx* ctx, int32_t kernel, uint32_t count,
                                       double* flops_per_launch, double* bytes_per_launch,
                                       const char** name) {

@@ -11,8 +11,14 @@ namespace mit2hip {
 // 512-wide f16 rows (cpu_nearest_interpolate, tokenizer_tests.cpp:3127, with
 // scale = (float)in_tokens / (float)out_tokens formed by the caller); also
 // zeroes row out_tokens of dst, the padding row of the zero-padded k = 3 conv.
+// For split operand pairs, src_lo / dst_lo (both nonzero) are the element
+// offsets of the lo rows, which move the same way.
 hipError_t launch_nearest_rows(const half_t* src, int in_tokens, int out_tokens, float scale,
-                               half_t* dst, hipStream_t s);
+                               half_t* dst, size_t src_lo, size_t dst_lo, hipStream_t s);
+
+// out = f16(in), n values; with lo_off nonzero also the lo half of each split
+// pair at out + lo_off (GemmArgs::split).
+hipError_t launch_f32_to_f16(const float* in, half_t* out, size_t n, size_t lo_off, hipStream_t s);
 
 // GroupNorm with one group over rows x 512 values: the mean and 1/sqrt(var +
 // eps) from the per-row, per-32-column partial sums and sums of squares the
@@ -22,9 +28,10 @@ hipError_t launch_gn_stats(const float* sum_parts, const float* ssq_parts, int r
                            float* stats, hipStream_t s);
 
 // out[r][c] = f16(mish((y[r][c] - mean) * rstd * gamma[c] + beta[c])) for
-// r < rows (cpu_groupnorm1 + cpu_mish, tokenizer_tests.cpp:3874-3904).
+// r < rows (cpu_groupnorm1 + cpu_mish, tokenizer_tests.cpp:3874-3904); with
+// out_lo nonzero also the lo half of the split pair at out + out_lo.
 hipError_t launch_gn_mish(const float* y, const float* stats, const float* gamma,
-                          const float* beta, int rows, half_t* out, hipStream_t s);
+                          const float* beta, int rows, half_t* out, size_t out_lo, hipStream_t s);
 
 // make_deterministic_normal_noise (tokenizer_tests.cpp:2121-2140) on the GPU:
 // out[n] for n = tokens * channels values.  splitmix64 is a counter: value

@@ -3,32 +3,61 @@
 // tokenizer_tests.cpp:2102-2140).  All of them are HBM-bound row passes.
 #include "condition.h"
 
+#include "gemm.h"
+
 namespace mit2hip {
 
-// One wave per output row: 64 lanes x 8 halves = the 512 channels.
+// f16 operand of an fp32 tensor: hi = f16(v); with lo_off, also the lo half
+// of the split pair at out + lo_off (GemmArgs::split).
+__global__ void f32_to_f16_kernel(const float* __restrict__ in, half_t* __restrict__ out, size_t n,
+                                  size_t lo_off) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (lo_off) {
+    half_t h, l;
+    split_f16(in[i], h, l);
+    out[i] = h;
+    out[lo_off + i] = l;
+  } else {
+    out[i] = (half_t)in[i];
+  }
+}
+
+hipError_t launch_f32_to_f16(const float* in, half_t* out, size_t n, size_t lo_off, hipStream_t s) {
+  if (n == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n,
+                     lo_off);
+  return hipGetLastError();
+}
+
+// One wave per output row: 64 lanes x 8 halves = the 512 channels.  With
+// split operands (dst_lo nonzero) the lo rows move the same way.
 __global__ __launch_bounds__(256) void nearest_rows_kernel(const half_t* __restrict__ src,
                                                            int in_tokens, int out_tokens,
                                                            float scale,
-                                                           half_t* __restrict__ dst) {
+                                                           half_t* __restrict__ dst,
+                                                           size_t src_lo, size_t dst_lo) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t > out_tokens) return;
-  half8 v;
+  half8 v, vl;
   if (t == out_tokens) {
-    for (int i = 0; i < 8; ++i) v[i] = (half_t)0.0f;
+    for (int i = 0; i < 8; ++i) v[i] = vl[i] = (half_t)0.0f;
   } else {
     int s = (int)floorf((float)t * scale);
     if (s >= in_tokens) s = in_tokens - 1;
     v = *reinterpret_cast<const half8*>(src + (size_t)s * 512 + lane * 8);
+    if (dst_lo) vl = *reinterpret_cast<const half8*>(src + src_lo + (size_t)s * 512 + lane * 8);
   }
   *reinterpret_cast<half8*>(dst + (size_t)t * 512 + lane * 8) = v;
+  if (dst_lo) *reinterpret_cast<half8*>(dst + dst_lo + (size_t)t * 512 + lane * 8) = vl;
 }
 
 hipError_t launch_nearest_rows(const half_t* src, int in_tokens, int out_tokens, float scale,
-                               half_t* dst, hipStream_t s) {
-  if (in_tokens <= 0 || out_tokens <= 0) return hipErrorInvalidValue;
+                               half_t* dst, size_t src_lo, size_t dst_lo, hipStream_t s) {
+  if (in_tokens <= 0 || out_tokens <= 0 || (src_lo == 0) != (dst_lo == 0)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(nearest_rows_kernel, dim3((out_tokens + 1 + 3) / 4), dim3(256), 0, s, src,
-                     in_tokens, out_tokens, scale, dst);
+                     in_tokens, out_tokens, scale, dst, src_lo, dst_lo);
   return hipGetLastError();
 }
 
@@ -77,7 +106,7 @@ __global__ __launch_bounds__(256) void gn_mish_kernel(const float* __restrict__ 
                                                       const float* __restrict__ stats,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta, int rows,
-                                                      half_t* __restrict__ out) {
+                                                      half_t* __restrict__ out, size_t out_lo) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
@@ -85,20 +114,25 @@ __global__ __launch_bounds__(256) void gn_mish_kernel(const float* __restrict__ 
   const float4* yr = reinterpret_cast<const float4*>(y + (size_t)r * 512) + lane * 2;
   const float4 a = yr[0], b = yr[1];
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  half8 o;
+  half_t o[8], ol[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = lane * 8 + i;
-    o[i] = (half_t)mish_f((v[i] - mean) * rstd * gamma[c] + beta[c]);
+    split_f16(mish_f((v[i] - mean) * rstd * gamma[c] + beta[c]), o[i], ol[i]);
   }
-  *reinterpret_cast<half8*>(out + (size_t)r * 512 + lane * 8) = o;
+  const half8 h = {o[0], o[1], o[2], o[3], o[4], o[5], o[6], o[7]};
+  *reinterpret_cast<half8*>(out + (size_t)r * 512 + lane * 8) = h;
+  if (out_lo) {
+    const half8 l = {ol[0], ol[1], ol[2], ol[3], ol[4], ol[5], ol[6], ol[7]};
+    *reinterpret_cast<half8*>(out + out_lo + (size_t)r * 512 + lane * 8) = l;
+  }
 }
 
 hipError_t launch_gn_mish(const float* y, const float* stats, const float* gamma,
-                          const float* beta, int rows, half_t* out, hipStream_t s) {
+                          const float* beta, int rows, half_t* out, size_t out_lo, hipStream_t s) {
   if (rows <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(gn_mish_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, y, stats, gamma, beta,
-                     rows, out);
+                     rows, out, out_lo);
   return hipGetLastError();
 }
 

@@ -185,6 +185,12 @@ class Engine {
 
   // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
   void set_use_graph(bool on) { use_graph_ = on; }
+  // Arithmetic of the stages the reference runs in fp32 (the length
+  // regulator, stage 1; the vocoder, stage 2): f32 = true (default) runs
+  // their GEMMs on split f16 operand pairs (fp32-level products), false on
+  // plain f16 operands.
+  void set_f32(int stage, bool f32);
+  bool f32(int stage) const;
   void sync();
 
  private:
@@ -203,6 +209,7 @@ class Engine {
 
   int device_ = 0;
   int last_B_ = 0, last_T_ = 0;
+  bool lr_f32_ = true;
   hipStream_t stream_ = nullptr;
   bool use_graph_ = true;
   std::unique_ptr<Weights> w_;

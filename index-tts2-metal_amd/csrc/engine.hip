@@ -106,8 +106,12 @@ struct Weights {
   half_t* c2f_w; float* c2f_b;
   // Length regulator (condition producer), present when the bundle has it:
   // content_in_proj [512][1024]; conv k=3 taps tap-major [512][3 * 512];
-  // GroupNorm affine [512]; the k=1 output conv [512][512].
+  // GroupNorm affine [512]; the k=1 output conv [512][512].  Its GEMM
+  // weights are split pairs (hi, then lo at + the hi element count, see
+  // GemmArgs::split); lr_wsplit is 2 when some lo half is nonzero (weights
+  // not exact in f16), else 1.
   bool has_lr = false;
+  int lr_wsplit = 1;
   half_t* lr_proj_w; float* lr_proj_b;
   half_t* lr_conv_w[4]; float* lr_conv_b[4];
   float* lr_gn_w[4]; float* lr_gn_b[4];
@@ -164,25 +168,26 @@ void visit_weights(Weights& W, F&& f) {
   f(W.c2_b, 80);
   f(W.c2f_w, 80 * 512);
   f(W.c2f_b, 80);
-  f(W.lr_proj_w, 512 * 1024);
+  f(W.lr_proj_w, 2 * 512 * 1024);  // split pairs: hi then lo
   f(W.lr_proj_b, 512);
   for (int b = 0; b < 4; ++b) {
-    f(W.lr_conv_w[b], 512 * 1536);
+    f(W.lr_conv_w[b], 2 * 512 * 1536);
     f(W.lr_conv_b[b], 512);
     f(W.lr_gn_w[b], 512);
     f(W.lr_gn_b[b], 512);
   }
-  f(W.lr_out_w, 512 * 512);
+  f(W.lr_out_w, 2 * 512 * 512);
   f(W.lr_out_b, 512);
 }
 
 // Device image layout: "MIT2HIPI", u32 version, u32 section flags (1 vocoder,
 // 2 GPT decoder), u64 payload bytes, u64 payload checksum, then the payload:
-// the decoder section (u64 arena bytes, u8 has_lr, u64 offset per
-// visit_weights array, the arena bytes), then each flagged section as u64
-// length + bytes (Vocoder::append_image, GptDecoder::append_image).
+// the decoder section (u64 arena bytes, u8 length regulator: 0 absent, else
+// its weight split mode 1 or 2, u64 offset per visit_weights array, the
+// arena bytes), then each flagged section as u64 length + bytes
+// (Vocoder::append_image, GptDecoder::append_image).
 constexpr char kImageMagic[8] = {'M', 'I', 'T', '2', 'H', 'I', 'P', 'I'};
-constexpr uint32_t kImageVersion = 2;
+constexpr uint32_t kImageVersion = 3;
 constexpr uint32_t kImageVocoder = 1, kImageGpt = 2;  // section flags
 
 struct HostModel {
@@ -238,6 +243,19 @@ class Uploader {
   half_t* f16(const std::vector<float>& v) {
     std::vector<_Float16> h(v.size());
     for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
+    half_t* d = static_cast<half_t*>(a_.take(h.size() * sizeof(_Float16)));
+    HIP_OK(hipMemcpy(d, h.data(), h.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+    return d;
+  }
+  // Split pair of v (hi, then lo at + v.size(), GemmArgs::split); *lo_used
+  // is set when some lo half is nonzero.
+  half_t* f16_pair(const std::vector<float>& v, bool* lo_used) {
+    const size_t n = v.size();
+    std::vector<_Float16> h(2 * n);
+    for (size_t i = 0; i < n; ++i) {
+      split_f16_host(v[i], h[i], h[n + i]);
+      if ((float)h[n + i] != 0.0f) *lo_used = true;
+    }
     half_t* d = static_cast<half_t*>(a_.take(h.size() * sizeof(_Float16)));
     HIP_OK(hipMemcpy(d, h.data(), h.size() * sizeof(_Float16), hipMemcpyHostToDevice));
     return d;
@@ -529,7 +547,8 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
     int present = 0;
     for (const auto& kv : hm.t) present += kv.first.compare(0, lp.size(), lp) == 0;
     if (present) {
-      W.lr_proj_w = up.f16(hm.get_full(lp + "content_in_proj.weight", 512 * 1024));
+      bool lo_used = false;
+      W.lr_proj_w = up.f16_pair(hm.get_full(lp + "content_in_proj.weight", 512 * 1024), &lo_used);
       W.lr_proj_b = up.f32(hm.get_full(lp + "content_in_proj.bias", 512));
       const int conv_i[4] = {0, 3, 6, 9}, norm_i[4] = {1, 4, 7, 10};
       for (int b = 0; b < 4; ++b) {
@@ -542,13 +561,14 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
           for (int ic = 0; ic < 512; ++ic)
             for (int k = 0; k < 3; ++k)
               tw[(size_t)oc * 1536 + k * 512 + ic] = w[((size_t)oc * 512 + ic) * 3 + k];
-        W.lr_conv_w[b] = up.f16(tw);
+        W.lr_conv_w[b] = up.f16_pair(tw, &lo_used);
         W.lr_conv_b[b] = up.f32(hm.get_full(c + ".bias", 512));
         W.lr_gn_w[b] = up.f32(hm.get_full(n + ".weight", 512));
         W.lr_gn_b[b] = up.f32(hm.get_full(n + ".bias", 512));
       }
-      W.lr_out_w = up.f16(hm.get_full(lp + "model.12.weight", 512 * 512));
+      W.lr_out_w = up.f16_pair(hm.get_full(lp + "model.12.weight", 512 * 512), &lo_used);
       W.lr_out_b = up.f32(hm.get_full(lp + "model.12.bias", 512));
+      W.lr_wsplit = lo_used ? 2 : 1;
       if (present != 20)
         throw std::invalid_argument("length regulator: expected 20 tensors, found " +
                                     std::to_string(present));
@@ -570,7 +590,7 @@ void Engine::write_image(const std::string& path) const {
   const char* base = W.arena.base();
   const size_t used = W.arena.used();
   w.put<uint64_t>(used);
-  w.put<uint8_t>(W.has_lr ? 1 : 0);
+  w.put<uint8_t>(W.has_lr ? (uint8_t)W.lr_wsplit : 0);
   visit_weights(W, [&](auto* p, size_t) { w.put<uint64_t>(arena_offset(p, base)); });
   std::vector<uint8_t> host(used);
   HIP_OK(hipMemcpy(host.data(), base, used, hipMemcpyDeviceToHost));
@@ -626,7 +646,10 @@ Engine::Engine(const std::string& image_path, int device) : device_(device) {
     Weights& W = *w_;
     const uint64_t used = r.get<uint64_t>();
     if (used == 0 || used > (uint64_t(8) << 30)) throw std::runtime_error("device image: bad arena size");
-    W.has_lr = r.get<uint8_t>() != 0;
+    const uint8_t lr_mode = r.get<uint8_t>();
+    if (lr_mode > 2) throw std::runtime_error("device image: bad length-regulator mode");
+    W.has_lr = lr_mode != 0;
+    W.lr_wsplit = lr_mode == 2 ? 2 : 1;
     W.arena.reserve(used);
     W.arena.set_used(used);
     char* base = W.arena.base();
@@ -1217,6 +1240,33 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
       nm = "adarms";
       break;
     }
+    case 6: {  // attention output projection wo + residual, folded-norm producer (N = K = 512)
+      GemmArgs g;
+      g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
+      g.W = W.wo_w[0]; g.ldw = 512; g.res = ws.xa; g.ldres = 512;
+      g.C32 = ws.stage_a; g.ldc32 = 512;
+      g.C16s = ws.n16; g.ldc16s = 512; g.sc_a = tab + 13 * 1024; g.sc_g = W.gamma[13];
+      g.ssq_out = ws.ssq;
+      loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, stream_)); });
+      f = 2.0 * R * 512 * 512;
+      by = 2.0 * R * 512 + 2.0 * 512 * 512 + 4.0 * R * 512 + 4.0 * R * 512 + 2.0 * R * 512 +
+           4.0 * R * kSsqParts;
+      nm = "gemm_wo_residual_norm";
+      break;
+    }
+    case 7: {  // WaveNet res/skip k=1 GEMM with the masked update (N = 1024, K = 512)
+      GemmArgs g;
+      g.M = R; g.N = 1024; g.K = 512; g.A = ws.gate16; g.lda = 512; g.W = W.rs_w[0]; g.ldw = 512;
+      g.bias = W.rs_b[0]; g.mask = ws.mask;
+      g.C32 = ws.stage_a; g.ldc32 = 512; g.C16 = ws.x16; g.ldc16 = 512;
+      g.C32b = ws.stage_b; g.ldc32b = 512; g.flag = 1;
+      loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_RESSKIP, stream_)); });
+      f = 2.0 * R * 1024 * 512;
+      by = 2.0 * R * 512 + 2.0 * 1024 * 512 + 4.0 * R * 512 * 2 + 4.0 * R * 512 * 2 +
+           2.0 * R * 512 + 4.0 * R;
+      nm = "gemm_wavenet_resskip";
+      break;
+    }
     default:
       throw std::invalid_argument("profile_launch: unknown kernel id");
   }
@@ -1241,13 +1291,8 @@ void d2h(void* h, const void* d, size_t bytes, hipStream_t s) {
   HIP_OK(hipMemcpyAsync(h, d, bytes, hipMemcpyDeviceToHost, s));
   HIP_OK(hipStreamSynchronize(s));
 }
-__global__ void f32_to_f16_kernel(const float* __restrict__ in, half_t* __restrict__ out, size_t n) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = (half_t)in[i];
-}
 void to_f16(const float* in, half_t* out, size_t n, hipStream_t s) {
-  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n);
-  HIP_OK(hipGetLastError());
+  HIP_OK(launch_f32_to_f16(in, out, n, 0, s));
 }
 }  // namespace
 
@@ -1511,6 +1556,23 @@ void Engine::op_linear(const float* A, const float* Wt, const float* bias, int M
 // ------------------------------------------------------------------ condition producer
 bool Engine::has_length_regulator() const { return w_->has_lr; }
 
+void Engine::set_f32(int stage, bool f32) {
+  if (stage == 1) {
+    lr_f32_ = f32;
+  } else if (stage == 2) {
+    if (!voc_) throw std::runtime_error("vocoder: the context has no bigvgan.* tensors");
+    voc_->set_f32(f32);
+  } else {
+    throw std::invalid_argument("precision: stage must be 1 (length regulator) or 2 (vocoder)");
+  }
+}
+
+bool Engine::f32(int stage) const {
+  if (stage == 1) return lr_f32_;
+  if (stage == 2 && voc_) return voc_->f32();
+  throw std::invalid_argument("precision: stage must be 1 (length regulator) or 2 (vocoder, when present)");
+}
+
 int Engine::generated_frames(int codes) {
   // static_cast<uint32_t>(static_cast<float>(codes) * 1.72f), synthesis_pipeline.cpp:1012
   return (int)(uint32_t)((float)codes * 1.72f);
@@ -1524,14 +1586,15 @@ void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
   size_t bytes = 0;
   auto f = [&](size_t n) { bytes += (n * 4 + 255) / 256 * 256; };
   auto h = [&](size_t n) { bytes += (n * 2 + 255) / 256 * 256; };
-  f((size_t)ci * 1024); h((size_t)ci * 1024); h((size_t)ci * 512); h((size_t)(co + 1) * 512);
+  // The f16 GEMM operands are split pairs: hi rows, then lo rows.
+  f((size_t)ci * 1024); h((size_t)ci * 1024 * 2); h((size_t)ci * 512 * 2); h((size_t)(co + 1) * 512 * 2);
   f((size_t)co * 512); f((size_t)co * 16); f((size_t)co * 16); f(2); f((size_t)cc * 512);
   lr_.arena.reserve(bytes);
   Arena& a = lr_.arena;
   lr_.in32 = static_cast<float*>(a.take((size_t)ci * 1024 * 4));
-  lr_.s16 = static_cast<half_t*>(a.take((size_t)ci * 1024 * 2));
-  lr_.p16 = static_cast<half_t*>(a.take((size_t)ci * 512 * 2));
-  lr_.x16 = static_cast<half_t*>(a.take((size_t)(co + 1) * 512 * 2));
+  lr_.s16 = static_cast<half_t*>(a.take((size_t)ci * 1024 * 2 * 2));
+  lr_.p16 = static_cast<half_t*>(a.take((size_t)ci * 512 * 2 * 2));
+  lr_.x16 = static_cast<half_t*>(a.take((size_t)(co + 1) * 512 * 2 * 2));
   lr_.y32 = static_cast<float*>(a.take((size_t)co * 512 * 4));
   lr_.sum_p = static_cast<float*>(a.take((size_t)co * 16 * 4));
   lr_.ssq_p = static_cast<float*>(a.take((size_t)co * 16 * 4));
@@ -1547,6 +1610,9 @@ void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
 //   -> 4 x [k=3 zero-padded conv GEMM writing fp32 rows and per-row partial
 //      sums / sums of squares; GroupNorm statistics; GroupNorm + Mish -> f16]
 //   -> k=1 conv GEMM into `out`.
+// In the default fp32 mode every GEMM operand is a split pair (hi, lo), so
+// the products carry fp32-level precision like the reference's fp32 path;
+// the f16 mode uses the hi halves alone.
 void Engine::length_regulator_device(const float* s_infer, int in_tokens, int out_tokens,
                                      float* out) {
   Weights& W = *w_;
@@ -1557,28 +1623,37 @@ void Engine::length_regulator_device(const float* s_infer, int in_tokens, int ou
   HIP_OK(hipSetDevice(device_));
   ensure_lr(in_tokens, out_tokens, 0);
   hipStream_t s = stream_;
-  to_f16(s_infer, lr_.s16, (size_t)in_tokens * 1024, s);
+  const int sp = lr_f32_ ? W.lr_wsplit : 0;
+  // lo-half offsets (elements) of the split operand buffers
+  const size_t s16_lo = sp ? (size_t)lr_.cap_in * 1024 : 0;
+  const size_t p16_lo = sp ? (size_t)lr_.cap_in * 512 : 0;
+  const size_t x16_lo = sp ? (size_t)(lr_.cap_out + 1) * 512 : 0;
+  HIP_OK(launch_f32_to_f16(s_infer, lr_.s16, (size_t)in_tokens * 1024, s16_lo, s));
   {
     GemmArgs g;
     g.M = in_tokens; g.N = 512; g.K = 1024; g.A = lr_.s16; g.lda = 1024;
     g.W = W.lr_proj_w; g.ldw = 1024; g.bias = W.lr_proj_b; g.C16 = lr_.p16; g.ldc16 = 512;
+    g.split = sp; g.a_lo = s16_lo; g.w_lo = sp == 2 ? (size_t)512 * 1024 : 0; g.c16_lo = p16_lo;
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F16, s));
   }
   HIP_OK(launch_nearest_rows(lr_.p16, in_tokens, out_tokens, (float)in_tokens / (float)out_tokens,
-                             lr_.x16, s));
+                             lr_.x16, p16_lo, x16_lo, s));
   for (int b = 0; b < 4; ++b) {
     GemmArgs g;
     g.M = out_tokens; g.N = 512; g.K = 3 * 512; g.T = out_tokens; g.conv_c = 512;
     g.A = lr_.x16; g.lda = 512;
     g.W = W.lr_conv_w[b]; g.ldw = 3 * 512; g.bias = W.lr_conv_b[b];
     g.C32 = lr_.y32; g.ldc32 = 512; g.sum_out = lr_.sum_p; g.ssq_out = lr_.ssq_p;
+    g.split = sp; g.a_lo = x16_lo; g.w_lo = sp == 2 ? (size_t)512 * 1536 : 0;
     HIP_OK(launch_gemm(g, A_CONV3Z, EPI_F32, s));
     HIP_OK(launch_gn_stats(lr_.sum_p, lr_.ssq_p, out_tokens, 1e-5f, lr_.stats, s));
-    HIP_OK(launch_gn_mish(lr_.y32, lr_.stats, W.lr_gn_w[b], W.lr_gn_b[b], out_tokens, lr_.x16, s));
+    HIP_OK(launch_gn_mish(lr_.y32, lr_.stats, W.lr_gn_w[b], W.lr_gn_b[b], out_tokens, lr_.x16,
+                          x16_lo, s));
   }
   GemmArgs g;
   g.M = out_tokens; g.N = 512; g.K = 512; g.A = lr_.x16; g.lda = 512;
   g.W = W.lr_out_w; g.ldw = 512; g.bias = W.lr_out_b; g.C32 = out; g.ldc32 = 512;
+  g.split = sp; g.a_lo = x16_lo; g.w_lo = sp == 2 ? (size_t)512 * 512 : 0;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
 }
 

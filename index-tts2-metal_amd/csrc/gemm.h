@@ -96,7 +96,43 @@ struct GemmArgs {
   // EPI_F32: per-row sums of each 32-column block of the output (layout of
   // ssq_out), for a norm whose statistics span whole rows or the whole tensor.
   float* sum_out = nullptr;
+
+  // Split operands: fp32 arithmetic from f16 matrix cores.  A value v is
+  // held as the pair hi = f16(v), lo = f16((v - hi) * kSplitScale), which
+  // represents v to about 2^-22 relative.  split = 1: A is a pair (its lo
+  // half at A + a_lo, A2 + a_lo; A_CONV3Z's zero row too), W is exact in
+  // f16; split = 2: W is a pair as well (lo at W + w_lo).  The product is
+  // hi.hi + (hi_A.lo_W + lo_A.hi_W) / kSplitScale in fp32 (the lo.lo term,
+  // ~2^-22 relative, is dropped).  An f16 output (EPI_F16, EPI_RESAVG's C16)
+  // also writes its lo half at C16 + c16_lo when c16_lo is nonzero.
+  int split = 0;
+  size_t a_lo = 0;
+  size_t w_lo = 0;
+  size_t c16_lo = 0;
 };
+
+// Scale of the lo half of a split operand (2^11: lo then has the magnitude
+// of hi, so it stays a normal f16 wherever hi does).
+constexpr float kSplitScale = 2048.0f;
+constexpr float kSplitInv = 1.0f / 2048.0f;
+
+// hi / lo halves of a split operand (host side: weight uploads).
+inline void split_f16_host(float v, half_t& hi, half_t& lo) {
+  hi = (half_t)v;
+  lo = (half_t)((v - (float)hi) * kSplitScale);
+}
+
+// hi / lo halves of a split operand in a kernel.  v first passes through an
+// empty asm statement, so both halves derive from the one rounded fp32
+// value: otherwise FP contraction may rewrite the conversion feeding lo as
+// a fused mixed-precision FMA from v's unrounded producer (v_fma_mix) while
+// hi is converted from the rounded v, and the pair then misses v by one f16
+// ulp whenever the two roundings disagree.
+__device__ inline void split_f16(float v, half_t& hi, half_t& lo) {
+  __asm__ volatile("" : "+v"(v));
+  hi = (half_t)v;
+  lo = (half_t)((v - (float)hi) * kSplitScale);
+}
 
 // Number of per-row partial sums of squares a 512-wide producer writes.
 constexpr int kSsqParts = 16;

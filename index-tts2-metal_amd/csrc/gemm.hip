@@ -69,13 +69,15 @@ struct TileMap {
   }
 };
 
-template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN, int KG>
+template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN, int KG, int SP>
 __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, TileMap tmap) {
   constexpr int NW = WM * WN;                // wavefronts per K group, WM along M x WN along N
   constexpr int CPR = SK / 8;                // 16-byte slots per stage row
   constexpr int LA = BM * CPR / (64 * NW);   // DMA instructions per wave per stage (A)
   constexpr int LB = BN * CPR / (64 * NW);   // (W)
-  constexpr int L = LA + LB;
+  constexpr int AS = SP >= 1 ? 2 : 1;        // copies of each A stage (split: hi, lo)
+  constexpr int WS = SP == 2 ? 2 : 1;        // copies of each W stage
+  constexpr int L = LA * AS + LB * WS;       // DMA instructions per wave per stage
   constexpr int WTM = BM / WM;               // rows of a wave's sub-tile
   constexpr int WTN = BN / WN;               // columns of a wave's sub-tile
   constexpr int MI = WTM / 16;               // 16-row MFMA blocks per wave
@@ -87,19 +89,23 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   static_assert(CPR == 8 || CPR >= 16, "stage width");
   static_assert(KG == 1 || ((KG == 2 || KG == 4) && EPI != EPI_QKV),
                 "K groups: 2 or 4, and the QKV epilogue needs every wave");
+  static_assert(SP >= 0 && SP <= 2, "split mode");
 
   // One __shared__ object per stage and operand, declared here so each kernel
   // instantiation owns its own objects (the per-object alias scopes are what
   // let the compiler keep only the explicit vmcnt waits).
-  // With KG = 2 K groups, each group has its own region in every buffer.
-  __shared__ __attribute__((aligned(1024))) half_t sA0[KG * BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA1[KG * BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB0[KG * BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB1[KG * BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? KG * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? KG * BN * SK : 8];
+  // With KG = 2 K groups, each group has its own region in every buffer;
+  // split operands keep their lo halves after all the groups' hi halves.
+  __shared__ __attribute__((aligned(1024))) half_t sA0[AS * KG * BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA1[AS * KG * BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? AS * KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? AS * KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB0[WS * KG * BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB1[WS * KG * BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? WS * KG * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? WS * KG * BN * SK : 8];
+  constexpr int kALo = KG * BM * SK;  // offset of a stage's lo half in its buffer
+  constexpr int kWLo = KG * BN * SK;
   static_assert(NST >= 2 && NST <= 4, "two to four stages");
   const int kg = threadIdx.x / (64 * NW);  // K group of this wave
   auto bufA = [&](auto st) -> half_t* {
@@ -252,22 +258,27 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     }
   }
 
-  auto a_src = [&](int j, int m, int k0, int kc) -> const half_t* {
+  // Source of the 16-byte chunk at K position k0 + kc of load slot j's row
+  // m; `lo` selects the lo half of a split operand (the resident zero row of
+  // A_CONVP serves both halves).
+  auto a_src = [&](int j, int m, int k0, int kc, bool lo) -> const half_t* {
     const int k = k0 + kc;
+    const size_t lo_off = lo ? p.a_lo : 0;
     if constexpr (AM == A_PLAIN) {
-      return p.A + (size_t)m * p.lda + k;
+      return p.A + lo_off + (size_t)m * p.lda + k;
     } else if constexpr (AM == A_CONCAT) {
-      return k < p.K1 ? p.A + (size_t)m * p.lda + k : p.A2 + (size_t)m * p.lda2 + (k - p.K1);
+      return k < p.K1 ? p.A + lo_off + (size_t)m * p.lda + k
+                      : p.A2 + lo_off + (size_t)m * p.lda2 + (k - p.K1);
     } else if constexpr (AM == A_CONV5) {
       const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);  // stage start: uniform
       const ConvRows& cr = conv_rows[j];
       const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : tap == 2 ? cr.r2 : tap == 3 ? cr.r3 : cr.r4;
-      return p.A + ro + (k - tap * kConvC);
+      return p.A + lo_off + ro + (k - tap * kConvC);
     } else if constexpr (AM == A_CONV3Z) {
       const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);
       const ConvRows& cr = conv_rows[j];
       const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : cr.r2;
-      return p.A + ro + (k - tap * kConvC);
+      return p.A + lo_off + ro + (k - tap * kConvC);
     } else {
       // tap = k / conv_c through a float reciprocal, corrected by one either way
       int tap = (int)((float)k * p.conv_inv_c);
@@ -281,7 +292,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       }
       const int src = cp_t[j] + tap * p.conv_d - p.conv_pad;
       const bool ok = tap < p.conv_k && src >= 0 && src < p.T;
-      return ok ? p.A + (size_t)(cp_base[j] + src) * p.lda + c : p.A_zero + c;
+      return ok ? p.A + lo_off + (size_t)(cp_base[j] + src) * p.lda + c : p.A_zero + c;
     }
   };
 
@@ -297,8 +308,11 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       const int c = (q % CPR) ^ swz(row);
       int m = m0 + row;
       if (m > p.M - 1) m = p.M - 1;  // rows past M load a valid row; never stored
-      __builtin_amdgcn_global_load_lds((const void*)a_src(j, m, k0, c * 8),
+      __builtin_amdgcn_global_load_lds((const void*)a_src(j, m, k0, c * 8, false),
                                        (lds_void_t*)(sa + q0 * 8), 16, 0, 0);
+      if constexpr (AS == 2)
+        __builtin_amdgcn_global_load_lds((const void*)a_src(j, m, k0, c * 8, true),
+                                         (lds_void_t*)(sa + kALo + q0 * 8), 16, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
@@ -306,16 +320,26 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       const int q = q0 + lane;
       const int row = q / CPR;
       const int c = (q % CPR) ^ swz(row);
-      __builtin_amdgcn_global_load_lds((const void*)(p.W + (size_t)(n0 + row) * p.ldw + k0 + c * 8),
-                                       (lds_void_t*)(sb + q0 * 8), 16, 0, 0);
+      const half_t* wsrc = p.W + (size_t)(n0 + row) * p.ldw + k0 + c * 8;
+      __builtin_amdgcn_global_load_lds((const void*)wsrc, (lds_void_t*)(sb + q0 * 8), 16, 0, 0);
+      if constexpr (WS == 2)
+        __builtin_amdgcn_global_load_lds((const void*)(wsrc + p.w_lo), (lds_void_t*)(sb + kWLo + q0 * 8),
+                                         16, 0, 0);
     }
   };
 
   floatx4 acc[MI][NI];
+  floatx4 accx[SP ? MI : 1][SP ? NI : 1];  // split: the cross terms, scaled by kSplitScale
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (SP > 0) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) accx[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
 
   auto compute = [&](auto st) {
     const half_t* sa = bufA(st);
@@ -339,6 +363,30 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
+      if constexpr (SP > 0) {
+        half8 afl[MI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int row = wm * WTM + i * 16 + lr;
+          afl[i] = *reinterpret_cast<const half8*>(sa + kALo + row * SK + ((c ^ swz(row)) << 3));
+        }
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) accx[i][j] = mfma16x16x32(bf[j], afl[i], accx[i][j]);
+      }
+      if constexpr (SP == 2) {
+        half8 bfl[NI];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int row = wn * WTN + j * 16 + lr;
+          bfl[j] = *reinterpret_cast<const half8*>(sb + kWLo + row * SK + ((c ^ swz(row)) << 3));
+        }
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) accx[i][j] = mfma16x16x32(bfl[j], af[i], accx[i][j]);
+      }
     }
   };
 
@@ -401,6 +449,12 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   static_for<0, NST - 1>([&](auto st) {
     if (kt0 + (int)decltype(st)::value < KT) compute(st);
   });
+  if constexpr (SP > 0) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] += accx[i][j] * kSplitInv;
+  }
 
   // K groups: groups 1..KG-1 hand their partial tiles to group 0 through LDS
   // and leave; group 0 adds them in group order (a fixed order, so the sum is
@@ -451,6 +505,22 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     h[0] = (half_t)a; h[1] = (half_t)b; h[2] = (half_t)c; h[3] = (half_t)d;
     *reinterpret_cast<half4*>(dst) = h;
   };
+  // f16 output of a split operand: hi at dst, lo at dst + p.c16_lo (when set).
+  auto st16s = [&](half_t* dst, float a, float b, float c, float d) {
+    if (!p.c16_lo) {
+      st16(dst, a, b, c, d);
+      return;
+    }
+    half_t hv[4], lv[4];
+    split_f16(a, hv[0], lv[0]);
+    split_f16(b, hv[1], lv[1]);
+    split_f16(c, hv[2], lv[2]);
+    split_f16(d, hv[3], lv[3]);
+    const half4 h = {hv[0], hv[1], hv[2], hv[3]};
+    const half4 l = {lv[0], lv[1], lv[2], lv[3]};
+    *reinterpret_cast<half4*>(dst) = h;
+    *reinterpret_cast<half4*>(dst + p.c16_lo) = l;
+  };
 
   if constexpr (EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_DUAL || EPI == EPI_RESSKIP ||
                 EPI == EPI_FINALSKIP || EPI == EPI_RESAVG) {
@@ -477,7 +547,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
           const float4 g1 = make_float4(g0.x + v.x / 3.0f, g0.y + v.y / 3.0f, g0.z + v.z / 3.0f,
                                         g0.w + v.w / 3.0f);
           *g = g1;
-          if (p.C16) st16(p.C16 + (size_t)m * p.ldc16 + n, g1.x, g1.y, g1.z, g1.w);
+          if (p.C16) st16s(p.C16 + (size_t)m * p.ldc16 + n, g1.x, g1.y, g1.z, g1.w);
           continue;
         }
         if (p.n_store && n >= p.n_store) continue;  // zero-padded weight rows
@@ -498,7 +568,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
         }
         if (!live) continue;
         if constexpr (EPI == EPI_F16) {
-          st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
+          st16s(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
         } else if constexpr (EPI == EPI_DUAL) {
           const int half_n = p.N >> 1;
           if (n < half_n) {
@@ -700,15 +770,32 @@ static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
   return t;
 }
 
-template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2, int KG = 1>
+template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2, int KG = 1,
+          int SP = 0>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
   if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K groups need equal stage counts
   const TileMap tm = make_tile_map(
       a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z || AM == A_CONVP ? a.conv_c : a.K, BM, BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG>), dim3(8 * tm.per_xcd),
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG, SP>), dim3(8 * tm.per_xcd),
                      dim3(64 * WM * WN * KG), 0, s,
                      a, tm);
   return hipGetLastError();
+}
+
+// Split-operand launches (fp32-level products, GemmArgs::split): the
+// vocoder's convs keep the f16 tile choice (their rings double, still one
+// or two workgroups per CU); everything else runs 64 x 64 tiles with one K
+// group, so the doubled ring stays within the LDS.
+template <int AM, int EPI, int SP>
+static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
+  if constexpr (AM == A_CONVP) {
+    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 1, SP>(a, s);
+    if (a.N % 64 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
+    if (a.N % 32 == 0) return launch_tile<64, 32, 64, 3, AM, EPI, 4, 1, 1, SP>(a, s);
+    return hipErrorInvalidValue;
+  } else {
+    return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
+  }
 }
 
 // Tile, stage and wavefront choice, swept at M = 1720 (B = 2, T = 860) on
@@ -758,6 +845,38 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t stream) {
+  if (a.split != 0 || a.c16_lo != 0) {
+    // Split operands: the condition producer's and the vocoder's GEMMs.
+    if (a.split < 0 || a.split > 2 || (a.split >= 1 && a.a_lo == 0) || (a.split == 2 && a.w_lo == 0) ||
+        a.M <= 0 || a.N <= 0 || !a.A || !a.W || a.K <= 0 || a.K % 64 != 0)
+      return hipErrorInvalidValue;
+    if (a.c16_lo != 0 && epi != EPI_F16 && epi != EPI_RESAVG) return hipErrorInvalidValue;
+    if (amode == A_CONVP) {
+      if (a.N % 32 != 0 || a.T <= 0 || a.M % a.T != 0 || a.conv_c <= 0 || a.conv_c % 8 != 0 ||
+          a.lda < a.conv_c || a.conv_k <= 0 || a.conv_d <= 0 || a.conv_pad < 0 ||
+          a.K < a.conv_k * a.conv_c || a.conv_inv_c != 1.0f / (float)a.conv_c || !a.A_zero ||
+          a.n_store < 0 || a.n_store > a.N || a.n_store % 4 != 0)
+        return hipErrorInvalidValue;
+    } else {
+      if (a.n_store != 0 || a.N % 64 != 0 || a.K % 128 != 0) return hipErrorInvalidValue;
+      if (amode == A_CONV3Z && (a.T <= 0 || a.M % a.T != 0 || a.conv_c != kConvC || a.K != 3 * kConvC))
+        return hipErrorInvalidValue;
+    }
+#define MIT2_SPLIT(AMV, EPV)                                                      \
+  if (amode == AMV && epi == EPV) {                                               \
+    if (a.split == 2) return launch_split<AMV, EPV, 2>(a, stream);                \
+    if (a.split == 1) return launch_split<AMV, EPV, 1>(a, stream);                \
+    return launch_split<AMV, EPV, 0>(a, stream);                                  \
+  }
+    MIT2_SPLIT(A_PLAIN, EPI_F16)
+    MIT2_SPLIT(A_PLAIN, EPI_F32)
+    MIT2_SPLIT(A_CONV3Z, EPI_F32)
+    MIT2_SPLIT(A_CONVP, EPI_F32)
+    MIT2_SPLIT(A_CONVP, EPI_F16)
+    if (a.C32b) MIT2_SPLIT(A_CONVP, EPI_RESAVG)
+#undef MIT2_SPLIT
+    return hipErrorInvalidValue;
+  }
   if (amode == A_CONVP) {
     if (a.M <= 0 || a.N <= 0 || a.N % 32 != 0 || a.K <= 0 || a.K % 64 != 0 || !a.A || !a.W ||
         a.T <= 0 || a.M % a.T != 0 || a.conv_c <= 0 || a.conv_c % 8 != 0 || a.lda < a.conv_c ||

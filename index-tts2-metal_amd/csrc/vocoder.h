@@ -30,6 +30,12 @@ class Vocoder {
   Vocoder(const Vocoder&) = delete;
   Vocoder& operator=(const Vocoder&) = delete;
 
+  // Arithmetic of the convs: f32 = true (default) runs them on split f16
+  // operand pairs (fp32-level products, as the reference's fp32 vocoder),
+  // false on plain f16 operands.
+  void set_f32(bool on);
+  bool f32() const;
+
   // True when any "bigvgan.*" tensor is present (then all of them must be).
   static bool present(const std::unordered_map<std::string, std::vector<float>>& t);
   size_t weight_bytes() const;

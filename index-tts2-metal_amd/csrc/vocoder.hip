@@ -6,9 +6,11 @@
 // add, avg3, clamp).
 //
 // Differences in HOW, not WHAT:
-//  * convs are implicit GEMMs on the matrix cores with f16 operands and fp32
-//    accumulation; weights are weight-normed once at create and laid out
-//    tap-major [out][tap * in + ic];
+//  * convs are implicit GEMMs on the matrix cores with fp32 accumulation;
+//    weights are weight-normed once at create and laid out tap-major
+//    [out][tap * in + ic].  The reference runs the vocoder in fp32, so by
+//    default every operand is a split f16 pair (hi, lo: GemmArgs::split),
+//    which gives fp32-level products; an f16 mode uses the hi halves alone;
 //  * a transposed conv with stride s, kernel 2s and padding s/2 is a k = 3
 //    conv over the input (taps q-1, q, q+1) whose s * out output columns are
 //    the s phases of the upsampled signal: output row q, column r * out + oc
@@ -80,7 +82,7 @@ template <bool OUT16>
 __global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__ x, ActFilters f,
                                                        const float* __restrict__ alpha,
                                                        const float* __restrict__ inv_beta, int T,
-                                                       int C, void* __restrict__ out) {
+                                                       int C, void* __restrict__ out, size_t out_lo) {
   constexpr int R = kActR;
   constexpr int XW = R + 12;      // x window
   constexpr int ZW = 2 * R + 10;  // Z window: u = 2 t0 - 5 + i
@@ -131,9 +133,17 @@ __global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < 12; ++k) acc += z[2 * r + k] * f.down[k];
-    if constexpr (OUT16)
-      static_cast<half_t*>(out)[(size_t)(t0 + r) * C + c] = (half_t)acc;
-    else
+    if constexpr (OUT16) {
+      half_t* o = static_cast<half_t*>(out) + (size_t)(t0 + r) * C + c;
+      if (out_lo) {
+        half_t h, l;
+        split_f16(acc, h, l);
+        o[0] = h;
+        o[out_lo] = l;
+      } else {
+        o[0] = (half_t)acc;
+      }
+    } else
       static_cast<float*>(out)[(size_t)(t0 + r) * C + c] = acc;
   }
 }
@@ -167,9 +177,17 @@ __global__ __launch_bounds__(256) void conv_post_clamp_kernel(const float* __res
 }
 
 __global__ void voc_f32_to_f16_kernel(const float* __restrict__ in, half_t* __restrict__ out,
-                                      size_t n) {
+                                      size_t n, size_t lo_off) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = (half_t)in[i];
+  if (i >= n) return;
+  if (lo_off) {
+    half_t h, l;
+    split_f16(in[i], h, l);
+    out[i] = h;
+    out[lo_off + i] = l;
+  } else {
+    out[i] = (half_t)in[i];
+  }
 }
 
 const std::vector<float>& get(const std::unordered_map<std::string, std::vector<float>>& t,
@@ -200,7 +218,7 @@ std::vector<float> wnorm(const std::vector<float>& g, const std::vector<float>& 
 
 // ---------------------------------------------------------------- weights
 struct Vocoder::Conv {
-  half_t* w = nullptr;  // [N][K] f16, tap-major, zero-padded
+  half_t* w = nullptr;  // [N][K] f16 hi halves, tap-major, zero-padded; lo halves follow ([N][K])
   float* b = nullptr;   // [N]
   int N = 0, n_out = 0, K = 0, cin = 0, k = 0;
 };
@@ -223,12 +241,18 @@ struct Vocoder::Impl {
   // workspace, sized for cap mel tokens
   Arena ws;
   int cap = 0;
+  // f16 operand buffers, each a split pair: hi values, then lo values at
+  // + the *_lo element offset.
   half_t *mel16, *pre16, *a16, *g16;
+  size_t mel16_lo = 0, pre16_lo = 0, a16_lo = 0, g16_lo = 0;
   float *x32, *h32, *t32, *g32, *act32;
+  bool f32 = true;  // split operands (fp32-level products); false: f16 operands
 
+  // Weights as split pairs: [n] hi halves, then [n] lo halves.
   void upload_f16(half_t*& d, const std::vector<float>& v) {
-    std::vector<_Float16> h(v.size());
-    for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
+    const size_t n = v.size();
+    std::vector<_Float16> h(2 * n);
+    for (size_t i = 0; i < n; ++i) split_f16_host(v[i], h[i], h[n + i]);
     d = static_cast<half_t*>(wa.take(h.size() * 2));
     VOC_OK(hipMemcpy(d, h.data(), h.size() * 2, hipMemcpyHostToDevice));
   }
@@ -315,13 +339,16 @@ struct Vocoder::Impl {
   void ensure(int T) {
     if (T <= cap) return;
     const size_t big = (size_t)T * 6144;  // C * T_s of every stage from the second on
-    const size_t need = (size_t)T * 80 * 2 + (size_t)T * 1536 * 2 + 2 * big * 2 + 5 * big * 4 + 9 * 256;
+    const size_t need = 2 * ((size_t)T * 80 * 2 + (size_t)T * 1536 * 2 + 2 * big * 2) + 5 * big * 4 + 9 * 256;
     VOC_OK(hipStreamSynchronize(s));
     ws.reserve(need + 4096);
-    mel16 = static_cast<half_t*>(ws.take((size_t)T * 80 * 2));
-    pre16 = static_cast<half_t*>(ws.take((size_t)T * 1536 * 2));
-    a16 = static_cast<half_t*>(ws.take(big * 2));
-    g16 = static_cast<half_t*>(ws.take(big * 2));
+    mel16_lo = (size_t)T * 80;
+    pre16_lo = (size_t)T * 1536;
+    a16_lo = g16_lo = big;
+    mel16 = static_cast<half_t*>(ws.take(mel16_lo * 2 * 2));
+    pre16 = static_cast<half_t*>(ws.take(pre16_lo * 2 * 2));
+    a16 = static_cast<half_t*>(ws.take(big * 2 * 2));
+    g16 = static_cast<half_t*>(ws.take(big * 2 * 2));
     x32 = static_cast<float*>(ws.take(big * 4));
     h32 = static_cast<float*>(ws.take(big * 4));
     t32 = static_cast<float*>(ws.take(big * 4));
@@ -331,9 +358,17 @@ struct Vocoder::Impl {
   }
 
   // ---------------------------------------------------------- launches
-  void conv(const Conv& c, const half_t* A, int T, int d, int pad, int epi, float* C32, const float* res,
-            float* C32b, half_t* C16, int flag) {
+  // Conv of the f16 operand A (a split pair with lo at + a_lo); C16 (when
+  // given) is a split pair buffer with lo at + c16_lo.
+  void conv(const Conv& c, const half_t* A, size_t a_lo, int T, int d, int pad, int epi, float* C32,
+            const float* res, float* C32b, half_t* C16, size_t c16_lo, int flag) {
     GemmArgs g;
+    if (f32) {
+      g.split = 2;
+      g.a_lo = a_lo;
+      g.w_lo = (size_t)c.N * c.K;
+      g.c16_lo = C16 ? c16_lo : 0;
+    }
     g.M = T;
     g.N = c.N;
     g.K = c.K;
@@ -362,15 +397,16 @@ struct Vocoder::Impl {
     VOC_OK(launch_gemm(g, A_CONVP, (EpiMode)epi, s));
   }
 
-  void activation(const Act& a, const float* in, int T, void* out, bool out16) {
+  // out16: out is a split pair buffer (lo at + out_lo, written in f32 mode).
+  void activation(const Act& a, const float* in, int T, void* out, bool out16, size_t out_lo = 0) {
     const size_t lanes = (size_t)((T + kActR - 1) / kActR) * a.C;
     const dim3 grid((unsigned)((lanes + 255) / 256));
     if (out16)
       hipLaunchKernelGGL(snake_aa_kernel<true>, grid, dim3(256), 0, s, in, a.filt, a.alpha, a.inv_beta,
-                         T, a.C, out);
+                         T, a.C, out, f32 ? out_lo : 0);
     else
       hipLaunchKernelGGL(snake_aa_kernel<false>, grid, dim3(256), 0, s, in, a.filt, a.alpha, a.inv_beta,
-                         T, a.C, out);
+                         T, a.C, out, (size_t)0);
     VOC_OK(hipGetLastError());
   }
 
@@ -382,15 +418,15 @@ struct Vocoder::Impl {
     const int k = kRbKernel[j % 3];
     const float* h = x;
     for (int pr = 0; pr < 3; ++pr) {
-      activation(act[j][2 * pr], h, T, a16, true);
+      activation(act[j][2 * pr], h, T, a16, true, a16_lo);
       const int d = kDil[pr];
-      conv(rb[j][pr][0], a16, T, d, (k - 1) * d / 2, EPI_F32, t32, nullptr, nullptr, nullptr, 0);
-      activation(act[j][2 * pr + 1], t32, T, a16, true);
+      conv(rb[j][pr][0], a16, a16_lo, T, d, (k - 1) * d / 2, EPI_F32, t32, nullptr, nullptr, nullptr, 0, 0);
+      activation(act[j][2 * pr + 1], t32, T, a16, true, a16_lo);
       if (pr < 2) {
-        conv(rb[j][pr][1], a16, T, 1, (k - 1) / 2, EPI_F32, h32, h, nullptr, nullptr, 0);
+        conv(rb[j][pr][1], a16, a16_lo, T, 1, (k - 1) / 2, EPI_F32, h32, h, nullptr, nullptr, 0, 0);
         h = h32;
       } else {
-        conv(rb[j][pr][1], a16, T, 1, (k - 1) / 2, EPI_RESAVG, out32, h, g, g16o, flag);
+        conv(rb[j][pr][1], a16, a16_lo, T, 1, (k - 1) / 2, EPI_RESAVG, out32, h, g, g16o, g16_lo, flag);
       }
     }
   }
@@ -401,8 +437,9 @@ struct Vocoder::Impl {
     for (int r = 0; r < 3; ++r) resblock(3 * i + r, x, T, nullptr, g, r > 0, r == 2 ? g16o : nullptr);
   }
 
-  void to_f16(const float* in, half_t* out, size_t n) {
-    hipLaunchKernelGGL(voc_f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n);
+  void to_f16(const float* in, half_t* out, size_t n, size_t lo_off) {
+    hipLaunchKernelGGL(voc_f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n,
+                       f32 ? lo_off : 0);
     VOC_OK(hipGetLastError());
   }
 
@@ -414,15 +451,17 @@ struct Vocoder::Impl {
 
   // mel [T][80] (device) -> g32 [256 T][24] (the body's output).
   void body(const float* mel, int T) {
-    to_f16(mel, mel16, (size_t)T * 80);
-    conv(pre, mel16, T, 1, 3, EPI_F16, nullptr, nullptr, nullptr, pre16, 0);
+    to_f16(mel, mel16, (size_t)T * 80, mel16_lo);
+    conv(pre, mel16, mel16_lo, T, 1, 3, EPI_F16, nullptr, nullptr, nullptr, pre16, pre16_lo, 0);
     const half_t* cur = pre16;
+    size_t cur_lo = pre16_lo;
     int Ts = T;
     for (int i = 0; i < 6; ++i) {
-      conv(ups[i], cur, Ts, 1, 1, EPI_F32, x32, nullptr, nullptr, nullptr, 0);
+      conv(ups[i], cur, cur_lo, Ts, 1, 1, EPI_F32, x32, nullptr, nullptr, nullptr, 0, 0);
       Ts *= kUps[i].stride;
       group(i, x32, Ts, g32, g16);
       cur = g16;
+      cur_lo = g16_lo;
     }
   }
 };
@@ -437,7 +476,7 @@ Vocoder::Vocoder(const std::unordered_map<std::string, std::vector<float>>& t, h
     : d_(new Impl) {
   Impl& d = *d_;
   d.s = stream;
-  d.wa.reserve(size_t(300) << 20);
+  d.wa.reserve(size_t(600) << 20);  // ~236 MB of f16 weights, twice (split pairs)
   try {
     d.make_conv(d.pre, t, "bigvgan.conv_pre", 1536, 80, 7, true);
     for (int i = 0; i < 6; ++i) d.make_ups(d.ups[i], t, kUps[i]);
@@ -537,7 +576,7 @@ Vocoder::Vocoder(const uint8_t* image, size_t bytes, hipStream_t stream) : d_(ne
       if (c.n_out != e[0] || c.cin != e[1] || c.k != e[2] || c.N != round_up(e[0], 32) ||
           c.K != round_up(e[2] * e[1], 64))
         throw std::runtime_error("device image: vocoder conv shape differs from the model");
-      c.w = arena_span<half_t>(wo, (size_t)c.N * c.K, base, used);
+      c.w = arena_span<half_t>(wo, (size_t)2 * c.N * c.K, base, used);  // split pairs
       c.b = arena_span<float>(bo, (size_t)c.N, base, used);
     });
     auto get_act = [&](Act& a, int C) {
@@ -563,6 +602,9 @@ Vocoder::Vocoder(const uint8_t* image, size_t bytes, hipStream_t stream) : d_(ne
 }
 
 Vocoder::~Vocoder() { delete d_; }
+
+void Vocoder::set_f32(bool on) { d_->f32 = on; }
+bool Vocoder::f32() const { return d_->f32; }
 
 size_t Vocoder::weight_bytes() const { return d_->bytes; }
 
@@ -615,12 +657,12 @@ size_t Vocoder::stage_host(int stage, int index, const float* in, int tokens, fl
     VOC_OK(hipMemcpyAsync(din, in, nin * 4, hipMemcpyHostToDevice, d.s));
     switch (stage) {
       case 0:
-        d.to_f16(din, d.mel16, nin);
-        d.conv(d.pre, d.mel16, tokens, 1, 3, EPI_F32, dout, nullptr, nullptr, nullptr, 0);
+        d.to_f16(din, d.mel16, nin, d.mel16_lo);
+        d.conv(d.pre, d.mel16, d.mel16_lo, tokens, 1, 3, EPI_F32, dout, nullptr, nullptr, nullptr, 0, 0);
         break;
       case 1:
-        d.to_f16(din, d.a16, nin);
-        d.conv(d.ups[index], d.a16, tokens, 1, 1, EPI_F32, dout, nullptr, nullptr, nullptr, 0);
+        d.to_f16(din, d.a16, nin, d.a16_lo);
+        d.conv(d.ups[index], d.a16, d.a16_lo, tokens, 1, 1, EPI_F32, dout, nullptr, nullptr, nullptr, 0, 0);
         break;
       case 2:
         d.activation(index == 108 ? d.act_post : d.act[index / 6][index % 6], din, tokens, dout, false);

@@ -24,6 +24,8 @@ PREFIX = "s2mel.net.cfm.estimator."
 OK, E_ARG, E_MODEL, E_HIP, E_INTERNAL = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16 = 0, 1
 FLAG_SYNC = 1
+STAGES = {"length_regulator": 1, "vocoder": 2}  # MIT2CFM_STAGE_*
+PRECISIONS = {"f16": 0, "f32": 1}  # MIT2CFM_PREC_*
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
@@ -68,6 +70,8 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_stream": (vp, [vp]),
         "mit2cfm_synchronize": (st, [vp]),
         "mit2cfm_set_graph": (st, [vp, i32]),
+        "mit2cfm_set_precision": (st, [vp, i32, i32]),
+        "mit2cfm_get_precision": (st, [vp, i32, ctypes.POINTER(i32)]),
         "mit2cfm_stage_timestep_embedder": (st, [vp, f32, i32, _f32p]),
         "mit2cfm_stage_input_merge": (st, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, _f32p]),
         "mit2cfm_stage_adaptive_norm": (st, [vp, _f32p, _f32p, u32, i32, _f32p]),
@@ -501,6 +505,16 @@ class Context:
 
     def set_graph(self, on: bool) -> None:
         self._c(lib().mit2cfm_set_graph(self._h, 1 if on else 0))
+
+    def set_precision(self, stage: str, mode: str) -> None:
+        """Arithmetic of a stage the reference runs in fp32: stage "length_regulator" or
+        "vocoder", mode "f32" (split f16 operand pairs, the default) or "f16"."""
+        self._c(lib().mit2cfm_set_precision(self._h, STAGES[stage], PRECISIONS[mode]))
+
+    def precision(self, stage: str) -> str:
+        m = ctypes.c_int32()
+        self._c(lib().mit2cfm_get_precision(self._h, STAGES[stage], ctypes.byref(m)))
+        return {v: k for k, v in PRECISIONS.items()}[m.value]
 
     def profile_launch(self, kernel: int, count: int):
         """Enqueues `count` launches of decode kernel `kernel` on self.stream (no sync);

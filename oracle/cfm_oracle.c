@@ -229,14 +229,38 @@ void orc_mish(const float* x, size_t n, float* out) {
     for (size_t i = 0; i < n; ++i) out[i] = x[i] * tanhf(log1pf(expf(x[i])));
 }
 
+/* cpu_groupnorm1 with its two statistics (the mean, then the mean of the
+ * squared deviations) reduced in double and rounded to float once, instead of
+ * the reference's sequential float sums.  Not the reference's arithmetic: a
+ * checker for how far those sequential sums alone move the result (over
+ * 10^5 values they carry ~1e-5 relative rounding error). */
+void orc_groupnorm1_f64stats(const float* x, const float* gamma, const float* beta, uint32_t tokens,
+                             uint32_t channels, float eps, float* out) {
+    const size_t count = (size_t)tokens * channels;
+    double m = 0.0;
+    for (size_t i = 0; i < count; ++i) m += x[i];
+    m /= (double)count;
+    double v = 0.0;
+    for (size_t i = 0; i < count; ++i) v += ((double)x[i] - m) * ((double)x[i] - m);
+    v /= (double)count;
+    const float mean = (float)m;
+    const float inv_std = (float)(1.0 / sqrt(v + (double)eps));
+    for (uint32_t t = 0; t < tokens; ++t)
+        for (uint32_t c = 0; c < channels; ++c) {
+            const size_t i = (size_t)t * channels + c;
+            out[i] = (x[i] - mean) * inv_std * gamma[c] + beta[c];
+        }
+}
+
 /* run_length_regulator_full_cpu (gpt.cpp:5298-5313) with its front
  * (gpt.cpp:5271-5281): content_in_proj per input token, nearest
- * interpolation, 4 x (conv k=3, groupnorm1 eps 1e-5, mish), conv k=1. */
-void orc_length_regulator(const float* input, uint32_t in_tokens, uint32_t out_tokens,
-                          const float* proj_w, const float* proj_b,
-                          const float* const* conv_w, const float* const* conv_b,
-                          const float* const* gn_w, const float* const* gn_b,
-                          const float* out_w, const float* out_b, float* out) {
+ * interpolation, 4 x (conv k=3, groupnorm1 eps 1e-5, mish), conv k=1.
+ * f64_stats != 0 swaps in orc_groupnorm1_f64stats (checker only). */
+void orc_length_regulator_ex(const float* input, uint32_t in_tokens, uint32_t out_tokens,
+                             const float* proj_w, const float* proj_b,
+                             const float* const* conv_w, const float* const* conv_b,
+                             const float* const* gn_w, const float* const* gn_b,
+                             const float* out_w, const float* out_b, int f64_stats, float* out) {
     float* projected = fbuf((size_t)in_tokens * 512);
     orc_linear_rows(proj_w, proj_b, input, in_tokens, 512, 1024, projected);
     float* x = fbuf((size_t)out_tokens * 512);
@@ -244,13 +268,25 @@ void orc_length_regulator(const float* input, uint32_t in_tokens, uint32_t out_t
     orc_nearest_interpolate(projected, in_tokens, out_tokens, 512, x);
     for (int blk = 0; blk < 4; ++blk) {
         orc_conv1d_same(x, conv_w[blk], conv_b[blk], out_tokens, 512, 512, 3, y);
-        orc_groupnorm1(y, gn_w[blk], gn_b[blk], out_tokens, 512, 1e-5f, x);
+        if (f64_stats)
+            orc_groupnorm1_f64stats(y, gn_w[blk], gn_b[blk], out_tokens, 512, 1e-5f, x);
+        else
+            orc_groupnorm1(y, gn_w[blk], gn_b[blk], out_tokens, 512, 1e-5f, x);
         orc_mish(x, (size_t)out_tokens * 512, x);
     }
     orc_conv1d_same(x, out_w, out_b, out_tokens, 512, 512, 1, out);
     free(projected);
     free(x);
     free(y);
+}
+
+void orc_length_regulator(const float* input, uint32_t in_tokens, uint32_t out_tokens,
+                          const float* proj_w, const float* proj_b,
+                          const float* const* conv_w, const float* const* conv_b,
+                          const float* const* gn_w, const float* const* gn_b,
+                          const float* out_w, const float* out_b, float* out) {
+    orc_length_regulator_ex(input, in_tokens, out_tokens, proj_w, proj_b, conv_w, conv_b, gn_w, gn_b,
+                            out_w, out_b, 0, out);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -78,6 +78,15 @@ void orc_length_regulator(const float* input, uint32_t in_tokens, uint32_t out_t
                           const float* const* conv_w, const float* const* conv_b,
                           const float* const* gn_w, const float* const* gn_b,
                           const float* out_w, const float* out_b, float* out);
+/* The same with f64_stats != 0 computing each GroupNorm's mean and variance in
+ * double (orc_groupnorm1_f64stats): a checker, not the reference's arithmetic. */
+void orc_length_regulator_ex(const float* input, uint32_t in_tokens, uint32_t out_tokens,
+                             const float* proj_w, const float* proj_b,
+                             const float* const* conv_w, const float* const* conv_b,
+                             const float* const* gn_w, const float* const* gn_b,
+                             const float* out_w, const float* out_b, int f64_stats, float* out);
+void orc_groupnorm1_f64stats(const float* x, const float* gamma, const float* beta, uint32_t tokens,
+                             uint32_t channels, float eps, float* out);
 void orc_timestep_embedding(const float* t, uint32_t n_t, const float* freqs,
                             uint32_t half, float scale, float* out); /* tokenizer_tests.cpp:3947 */
 void orc_attention_head_masked(const float* q, const float* k, const float* v,

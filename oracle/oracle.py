@@ -57,6 +57,10 @@ def lib() -> ctypes.CDLL:
             "orc_length_regulator": (None, [_f32p, u32, u32, _f32p, _f32p, ctypes.POINTER(_f32p),
                                             ctypes.POINTER(_f32p), ctypes.POINTER(_f32p),
                                             ctypes.POINTER(_f32p), _f32p, _f32p, _f32p]),
+            "orc_length_regulator_ex": (None, [_f32p, u32, u32, _f32p, _f32p, ctypes.POINTER(_f32p),
+                                               ctypes.POINTER(_f32p), ctypes.POINTER(_f32p),
+                                               ctypes.POINTER(_f32p), _f32p, _f32p, ctypes.c_int, _f32p]),
+            "orc_groupnorm1_f64stats": (None, [_f32p, _f32p, _f32p, u32, u32, f32, _f32p]),
             "orc_conv1d_reflect_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, _f32p]),
             "orc_conv1d_dilated_same": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, u32, _f32p]),
             "orc_conv_transpose1d": (None, [_f32p, _f32p, _f32p, u32, u32, u32, u32, u32, u32, _f32p]),
@@ -194,11 +198,12 @@ def nearest_interpolate(x, out_tokens) -> np.ndarray:
     return out
 
 
-def groupnorm1(x, gamma, beta, eps=1e-5) -> np.ndarray:
+def groupnorm1(x, gamma, beta, eps=1e-5, f64_stats: bool = False) -> np.ndarray:
     x, g, b = f32(x), f32(gamma), f32(beta)
     tokens, channels = x.shape
     out = np.empty_like(x)
-    lib().orc_groupnorm1(P(x), P(g), P(b), tokens, channels, eps, P(out))
+    fn = lib().orc_groupnorm1_f64stats if f64_stats else lib().orc_groupnorm1
+    fn(P(x), P(g), P(b), tokens, channels, eps, P(out))
     return out
 
 
@@ -212,9 +217,11 @@ def mish(x) -> np.ndarray:
 LR_PREFIX = "s2mel.net.length_regulator."
 
 
-def length_regulator(tensors: dict, s_infer, out_tokens: int) -> np.ndarray:
+def length_regulator(tensors: dict, s_infer, out_tokens: int, f64_stats: bool = False) -> np.ndarray:
     """run_length_regulator_full_cpu (gpt.cpp:5298): s_infer [in_tokens, 1024]
-    -> [out_tokens, 512]; tensors holds the s2mel.net.length_regulator.* weights."""
+    -> [out_tokens, 512]; tensors holds the s2mel.net.length_regulator.* weights.
+    f64_stats: the GroupNorm statistics in double instead of the reference's
+    sequential float sums (a checker, not the reference's arithmetic)."""
     t = {k[len(LR_PREFIX):]: f32(v) for k, v in tensors.items() if k.startswith(LR_PREFIX)}
     x = f32(s_infer)
     in_tokens = x.shape[0]
@@ -224,9 +231,10 @@ def length_regulator(tensors: dict, s_infer, out_tokens: int) -> np.ndarray:
     gn_b = [t[f"model.{i}.bias"] for i in (1, 4, 7, 10)]
     arrs = lambda lst: (_f32p * 4)(*[P(a) for a in lst])
     out = np.empty((out_tokens, 512), np.float32)
-    lib().orc_length_regulator(P(x), in_tokens, out_tokens, P(t["content_in_proj.weight"]),
-                               P(t["content_in_proj.bias"]), arrs(conv), arrs(conv_b), arrs(gn),
-                               arrs(gn_b), P(t["model.12.weight"]), P(t["model.12.bias"]), P(out))
+    lib().orc_length_regulator_ex(P(x), in_tokens, out_tokens, P(t["content_in_proj.weight"]),
+                                  P(t["content_in_proj.bias"]), arrs(conv), arrs(conv_b), arrs(gn),
+                                  arrs(gn_b), P(t["model.12.weight"]), P(t["model.12.bias"]),
+                                  1 if f64_stats else 0, P(out))
     return out
 
 

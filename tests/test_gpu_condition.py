@@ -3,21 +3,50 @@
 synthesis_pipeline.cpp:1012-1035; the seeded noise, tokenizer_tests.cpp:2121)
 -- through the C ABI, against the CPU oracle on identical seeded inputs.
 
-Bar: the length regulator's output within rel-L2 5e-3 of the oracle.  The
-reference computes this stage in fp32; here the five GEMMs take f16 operands
-with fp32 accumulation (GroupNorm statistics, GroupNorm and Mish stay fp32),
-and each GroupNorm renormalises, so the f16 rounding does not compound.  The
-merge is a copy and is checked bit for bit; the noise's uniforms are integer
-work and bit-identical, so the normals differ only by the GPU's log/cos/sin.
+Bar: the reference's own, max-abs 1e-4 between its fp32 Metal and CPU paths
+(run_length_regulator_full_test, gpt.cpp:5382-5401), on the reference's input
+and on random inputs from 1 to 860 frames.  The default fp32 mode runs the
+five GEMMs on split f16 operand pairs (hi + lo, fp32-level products); the f16
+mode (plain f16 operands, fp32 accumulation) is held to rel-L2 5e-3.  The
+GroupNorm, Mish and the statistics are fp32 in both, the statistics reduced
+in double.
+
+The reference CPU path sums each GroupNorm's statistics sequentially in float
+over rows x 512 values (tokenizer_tests.cpp:3874-3896); past a few hundred
+rows that rounding alone moves its output by 1e-4 or more, and no reduction in
+another order can reproduce it.  So each case is checked twice: against the
+oracle with its statistics in double at max-abs 1e-5 (everything else is the
+reference's fp32 arithmetic), and against the faithful oracle at 1e-4 plus
+the difference between the two oracles, which the test measures.  The merge is a
+copy and is checked bit for bit; the noise's uniforms are integer work and
+bit-identical, so the normals differ only by the GPU's log/cos/sin.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
+from conftest import sincos_series
+
 pytestmark = pytest.mark.gpu
 
-LR_TOL = 5e-3
+LR_MAXABS = 1e-4   # fp32 mode: the reference's bar (gpt.cpp:5399)
+LR_MAXABS_F64STATS = 1e-5  # fp32 mode vs the oracle with double-precision statistics
+LR_TOL_F16 = 5e-3  # f16 mode: rel-L2
+
+
+def _check_fp32(orc, tensors, s_infer, out_tokens, got, label):
+    ref = orc.length_regulator(tensors, s_infer, out_tokens)
+    ref64 = orc.length_regulator(tensors, s_infer, out_tokens, f64_stats=True)
+    mx = float(np.abs(got - ref).max())
+    mx64 = float(np.abs(got - ref64).max())
+    drift = float(np.abs(ref - ref64).max())  # the reference's own statistic rounding
+    print(f"{label}: max-abs {mx:.3e} vs oracle, {mx64:.3e} vs f64-statistics oracle "
+          f"(oracle statistic drift {drift:.3e}; rel-L2 {orc.rel_l2(got, ref):.3e}; "
+          f"|ref| max {np.abs(ref).max():.2f})", flush=True)
+    assert np.isfinite(got).all()
+    assert mx64 <= LR_MAXABS_F64STATS
+    assert mx <= LR_MAXABS + drift
 
 
 @pytest.fixture(scope="module")
@@ -32,17 +61,60 @@ def ctx_lr(mit2, tensors, lr_tensors):
     c.close()
 
 
-@pytest.mark.parametrize("in_tokens,out_tokens", [(1, 3), (11, 18), (20, 34), (300, 516), (500, 860),
-                                                  (40, 25)])
+@pytest.mark.parametrize("in_tokens,out_tokens", [(1, 3), (11, 18), (20, 34), (300, 516), (350, 602),
+                                                  (500, 860), (40, 25)])
 def test_length_regulator_matches_oracle(mit2, orc, ctx_lr, lr_tensors, in_tokens, out_tokens):
+    """fp32 mode (the default) at the reference's bar; (350, 602) is the bench's
+    condition (350 codes for the 602 generated frames of a T=860 decode)."""
+    assert ctx_lr.precision("length_regulator") == "f32"
     s_infer = mit2.normal_noise(in_tokens, 1024, 7 + in_tokens)
     print(f"length regulator in={in_tokens} out={out_tokens}", flush=True)
     got = ctx_lr.length_regulator(s_infer, out_tokens)
+    _check_fp32(orc, lr_tensors, s_infer, out_tokens, got, f"length regulator in={in_tokens} out={out_tokens}")
+
+
+def test_length_regulator_reference_input(orc, ctx_lr, lr_tensors):
+    """run_length_regulator_full_test's case (gpt.cpp:5382-5401): 7 -> 11 tokens,
+    input[i] = sin(0.017 i) 0.1 + cos(0.013 (i % 131)) 0.2; bar max-abs 1e-4."""
+    s_infer = sincos_series(7 * 1024, 0.017, 0.013, 0.1, 0.2, 131).reshape(7, 1024)
+    got = ctx_lr.length_regulator(s_infer, 11)
+    ref = orc.length_regulator(lr_tensors, s_infer, 11)
+    mx = float(np.abs(got - ref).max())
+    print(f"length regulator (reference input 7 -> 11): max-abs {mx:.3e}", flush=True)
+    assert mx <= LR_MAXABS  # the reference's bar with no allowance
+
+
+def test_length_regulator_f32_weights(mit2, orc, tensors):
+    """Weights that are not exact in f16 (fp32 values) take the two-sided split
+    (lo halves of the weights too) and still meet the reference's bar."""
+    rng = np.random.default_rng(77)
+    lr32 = {k: (v.astype(np.float32) + rng.standard_normal(v.shape).astype(np.float32) * 1e-4).astype(np.float32)
+            for k, v in mit2.synthetic_lr_tensors(20240606, 0.02).items()}
+    c = mit2.Context({**tensors, **lr32}, device=0)
+    try:
+        for in_tokens, out_tokens in ((7, 11), (350, 602)):
+            s_infer = mit2.normal_noise(in_tokens, 1024, 90 + in_tokens)
+            got = c.length_regulator(s_infer, out_tokens)
+            _check_fp32(orc, lr32, s_infer, out_tokens, got,
+                        f"length regulator, fp32 weights, in={in_tokens} out={out_tokens}")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("in_tokens,out_tokens", [(11, 18), (350, 602)])
+def test_length_regulator_f16_mode(mit2, orc, ctx_lr, lr_tensors, in_tokens, out_tokens):
+    s_infer = mit2.normal_noise(in_tokens, 1024, 7 + in_tokens)
+    ctx_lr.set_precision("length_regulator", "f16")
+    try:
+        assert ctx_lr.precision("length_regulator") == "f16"
+        got = ctx_lr.length_regulator(s_infer, out_tokens)
+    finally:
+        ctx_lr.set_precision("length_regulator", "f32")
     ref = orc.length_regulator(lr_tensors, s_infer, out_tokens)
     err = orc.rel_l2(got, ref)
-    print(f"length regulator in={in_tokens} out={out_tokens}: rel-L2 {err:.3e}", flush=True)
-    assert np.isfinite(got).all()
-    assert err <= LR_TOL
+    print(f"length regulator f16 mode in={in_tokens} out={out_tokens}: rel-L2 {err:.3e} "
+          f"max-abs {np.abs(got - ref).max():.3e}", flush=True)
+    assert err <= LR_TOL_F16
 
 
 def test_length_regulator_repeatable_and_shape_independent(mit2, ctx_lr):
@@ -115,6 +187,9 @@ def test_noise_device_matches_host_generator(mit2, orc, ctx_lr, tokens, channels
 def test_missing_length_regulator_is_a_model_error(mit2, ctx):
     with pytest.raises(mit2.Mit2CfmError) as e:
         ctx.length_regulator(mit2.normal_noise(4, 1024, 1), 6)
+    assert e.value.status == mit2.E_MODEL
+    with pytest.raises(mit2.Mit2CfmError) as e:
+        ctx.set_precision("length_regulator", "f16")
     assert e.value.status == mit2.E_MODEL
 
 

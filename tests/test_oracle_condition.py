@@ -92,3 +92,43 @@ def test_synthetic_lr_tensors_shapes(mit2):
     assert len(t) == 20
     assert t[oracle.LR_PREFIX + "model.0.weight"].shape == (512, 512, 3)
     assert abs(float(t[oracle.LR_PREFIX + "model.1.weight"].astype(np.float32).mean()) - 1.0) < 0.01
+
+
+@pytest.mark.parametrize("tokens", [1, 9, 602])
+def test_groupnorm1_f64stats_matches_torch(tokens):
+    """The checker variant (statistics in double) is torch's float64 group_norm
+    up to the final float rounding."""
+    rng = np.random.default_rng(50 + tokens)
+    x = (rng.standard_normal((tokens, 512)) * 3 + 0.7).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(512)).astype(np.float32)
+    got = oracle.groupnorm1(x, g, b, f64_stats=True)
+    ref = F.group_norm(_t(x).T[None], 1, _t(g), _t(b), eps=1e-5)[0].T.numpy()
+    assert np.abs(got - ref).max() <= 2e-6 * np.abs(ref).max()
+
+
+def test_reference_groupnorm_statistics_drift_with_size():
+    """The reference's sequential float sums of the GroupNorm statistics
+    (tokenizer_tests.cpp:3874-3896) carry rounding error that grows with the
+    element count: about 1e-6 of the output scale at 11 x 512 values, 1e-4 at
+    602 x 512.  A GPU reduction in a different order cannot reproduce it; the
+    GPU parity tests measure it with the f64-statistics checker and allow for it."""
+    rng = np.random.default_rng(9)
+    g = np.ones(512, np.float32)
+    b = np.zeros(512, np.float32)
+    drift = {}
+    for tokens in (11, 602):
+        x = (rng.standard_normal((tokens, 512)) * 1.3 + 0.2).astype(np.float32)
+        ref = F.group_norm(_t(x).T[None], 1, _t(g), _t(b), eps=1e-5)[0].T.numpy()
+        drift[tokens] = float(np.abs(oracle.groupnorm1(x, g, b) - ref).max())
+        assert np.abs(oracle.groupnorm1(x, g, b, f64_stats=True) - ref).max() <= 2e-6 * np.abs(ref).max()
+    assert drift[11] < 2e-5 and drift[602] > 2e-5
+
+
+@pytest.mark.parametrize("in_tokens,out_tokens", [(7, 11), (20, 34)])
+def test_length_regulator_f64stats_matches_torch(mit2, in_tokens, out_tokens):
+    t = mit2.synthetic_lr_tensors(300 + in_tokens, 0.02)
+    s_infer = mit2.normal_noise(in_tokens, 1024, 9 + in_tokens)
+    got = oracle.length_regulator(t, s_infer, out_tokens, f64_stats=True)
+    ref = _torch_length_regulator(t, s_infer, out_tokens)
+    assert oracle.rel_l2(got, ref) <= 1e-5
