@@ -302,6 +302,19 @@ mit2cfm_status mit2cfm_condition(mit2cfm_ctx* ctx, const float* s_infer, uint32_
 mit2cfm_status mit2cfm_condition_device(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
                                         const float* prompt_cond, uint32_t prompt_tokens,
                                         float* cond_out, uint32_t* generated_out, uint32_t flags);
+/* mit2cfm_condition_device that allocates nothing: no reference counterpart.
+ * It is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * scratch (the length regulator's operand, conv and statistics buffers) is
+ * a static device array of about 13.7 MB that every GPU the library runs on
+ * holds until the process ends, shared by every context on that GPU: calls
+ * that overlap on one GPU (two streams or threads) race.  codes above
+ * MIT2CFM_NOALLOC_MAX_CODES (1,761 generated frames) is MIT2CFM_E_ARG.
+ * Arguments, outputs, flags and results as for mit2cfm_condition_device. */
+#define MIT2CFM_NOALLOC_MAX_CODES 1024u
+mit2cfm_status mit2cfm_condition_device_noalloc(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                                const float* prompt_cond, uint32_t prompt_tokens,
+                                                float* cond_out, uint32_t* generated_out, uint32_t flags);
 /* Frames the condition producer makes from `codes` semantic tokens:
  * floor(codes * 1.72f) (synthesis_pipeline.cpp:1012). */
 uint32_t mit2cfm_generated_frames(uint32_t codes);

@@ -637,6 +637,24 @@ mit2cfm_status mit2cfm_condition_device(mit2cfm_ctx* ctx, const float* s_infer, 
   });
 }
 
+static_assert(MIT2CFM_NOALLOC_MAX_CODES == (unsigned)mit2hip::Engine::kNoAllocMaxCodes,
+              "the header's no-alloc limit is the engine's scratch limit");
+
+mit2cfm_status mit2cfm_condition_device_noalloc(mit2cfm_ctx* ctx, const float* s_infer, uint32_t codes,
+                                                const float* prompt_cond, uint32_t prompt_tokens,
+                                                float* cond_out, uint32_t* generated_out, uint32_t flags) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(s_infer && prompt_cond && cond_out, "s_infer, prompt_cond and cond_out must not be NULL");
+    require(codes > 0 && prompt_tokens > 0, "codes and prompt_tokens must be positive");
+    require(codes <= MIT2CFM_NOALLOC_MAX_CODES, "codes exceeds MIT2CFM_NOALLOC_MAX_CODES (the scratch limit)");
+    const int gen = ctx->eng->condition_device_noalloc(s_infer, (int)codes, prompt_cond,
+                                                       (int)prompt_tokens, cond_out);
+    if (generated_out) *generated_out = (uint32_t)gen;
+    if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}
+
 uint32_t mit2cfm_generated_frames(uint32_t codes) {
   return (uint32_t)mit2hip::Engine::generated_frames((int)codes);
 }

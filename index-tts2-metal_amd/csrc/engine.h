@@ -142,6 +142,13 @@ class Engine {
   // DEVICE pointers, enqueued on stream(); returns generated.
   int condition_device(const float* s_infer, int codes, const float* prompt_cond,
                        int prompt_tokens, float* cond);
+  // condition_device with every scratch buffer taken from the library's
+  // static per-GPU scratch array instead of the context's workspace: it
+  // allocates nothing, for callers that cannot (graph capture, serving
+  // loops).  codes <= kNoAllocMaxCodes; calls that overlap on one GPU race.
+  int condition_device_noalloc(const float* s_infer, int codes, const float* prompt_cond,
+                               int prompt_tokens, float* cond);
+  static constexpr int kNoAllocMaxCodes = 1024;
   // Host-pointer versions of the two above (synchronous).
   void length_regulator_host(const float* s_infer, int in_tokens, int out_tokens, float* out);
   int condition_host(const float* s_infer, int codes, const float* prompt_cond,
@@ -241,6 +248,20 @@ class Engine {
   };
   LrBufs lr_;
   void ensure_lr(int in_tokens, int out_tokens, int cond_rows);
+  // The length regulator's device buffers (split operand pairs: lo halves at
+  // + cap_in * 1024, + cap_in * 512 and + (cap_out + 1) * 512 elements).
+  struct LrView {
+    half_t* s16;
+    half_t* p16;
+    half_t* x16;
+    float* y32;
+    float* sum_p;
+    float* ssq_p;
+    float* stats;
+    int cap_in, cap_out;
+  };
+  void length_regulator_on(const LrView& v, const float* s_infer, int in_tokens, int out_tokens,
+                           float* out);
   // Decode tables per step count, computed once per context (decode_tables).
   struct TableSet {
     Arena arena;

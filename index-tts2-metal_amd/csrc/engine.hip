@@ -21,6 +21,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <mutex>
 #include <type_traits>
 #include <unordered_map>
 
@@ -45,6 +46,54 @@ static const char* kPfx = "s2mel.net.cfm.estimator.";
 constexpr int kTcondPerStep = 36864;  // [13 attn | 13 ffn | final norm] x 1024, final ss 1024, wn cond 8192
 constexpr int kFinalSsOff = 27 * 1024;
 constexpr int kWnCondOff = 28 * 1024;
+
+// ------------------------------------------------------------------ no-alloc scratch
+// Scratch of the allocation-free condition producer
+// (Engine::condition_device_noalloc): the length regulator's buffers for up
+// to kNoAllocMaxCodes codes, as LrView lays them out, in one static device
+// array.  Each GPU the library runs on holds its own copy until the process
+// ends; every context on that GPU shares it.
+namespace {
+constexpr int kNoAllocMaxFrames = (int)((float)Engine::kNoAllocMaxCodes * 1.72f);  // generated_frames
+constexpr size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+constexpr size_t kScrS16 = 0;
+constexpr size_t kScrP16 = kScrS16 + al256((size_t)Engine::kNoAllocMaxCodes * 1024 * 2 * 2);
+constexpr size_t kScrX16 = kScrP16 + al256((size_t)Engine::kNoAllocMaxCodes * 512 * 2 * 2);
+constexpr size_t kScrY32 = kScrX16 + al256((size_t)(kNoAllocMaxFrames + 1) * 512 * 2 * 2);
+constexpr size_t kScrSum = kScrY32 + al256((size_t)kNoAllocMaxFrames * 512 * 4);
+constexpr size_t kScrSsq = kScrSum + al256((size_t)kNoAllocMaxFrames * 16 * 4);
+constexpr size_t kScrStats = kScrSsq + al256((size_t)kNoAllocMaxFrames * 16 * 4);
+constexpr size_t kScratchBytes = kScrStats + 256;  // 13.7 MB
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+// Device address of `scratch` per GPU (hipGetSymbolAddress with that GPU
+// current); the array's name is only a host-side stand-in.
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Resolves this GPU's scratch address once; the caller has made `device`
+// current.  Called when a context is created.
+void resolve_scratch(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return;  // the no-alloc call then reports it
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    throw HipError(std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+  g_scratch_ptr[device] = p;
+}
+
+char* scratch_ptr(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return static_cast<char*>(g_scratch_ptr[device]);
+}
+}  // namespace
 
 // ------------------------------------------------------------------ arena
 Arena::~Arena() {
@@ -358,6 +407,7 @@ struct Workspace {
 // ------------------------------------------------------------------ engine
 Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(device) {
   HIP_OK(hipSetDevice(device_));
+  resolve_scratch(device_);
   HIP_OK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   if (const char* g = std::getenv("MIT2CFM_GRAPH")) use_graph_ = std::atoi(g) != 0;
 
@@ -638,6 +688,7 @@ Engine::Engine(const std::string& image_path, int device) : device_(device) {
   if (image_checksum(payload, plen) != sum) throw std::runtime_error("device image: checksum mismatch");
 
   HIP_OK(hipSetDevice(device_));
+  resolve_scratch(device_);
   HIP_OK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   try {
     if (const char* g = std::getenv("MIT2CFM_GRAPH")) use_graph_ = std::atoi(g) != 0;
@@ -1615,43 +1666,50 @@ void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
 // the f16 mode uses the hi halves alone.
 void Engine::length_regulator_device(const float* s_infer, int in_tokens, int out_tokens,
                                      float* out) {
-  Weights& W = *w_;
-  if (!W.has_lr)
+  if (!w_->has_lr)
     throw std::runtime_error("length regulator: the context has no s2mel.net.length_regulator.* tensors");
   if (in_tokens <= 0 || out_tokens <= 0)
     throw std::invalid_argument("length regulator: token counts must be positive");
   HIP_OK(hipSetDevice(device_));
   ensure_lr(in_tokens, out_tokens, 0);
+  const LrView v{lr_.s16, lr_.p16, lr_.x16, lr_.y32, lr_.sum_p, lr_.ssq_p, lr_.stats, lr_.cap_in, lr_.cap_out};
+  length_regulator_on(v, s_infer, in_tokens, out_tokens, out);
+}
+
+// The regulator's launches on the buffers of `lr` (enqueued on stream_).
+void Engine::length_regulator_on(const LrView& lr, const float* s_infer, int in_tokens, int out_tokens,
+                                 float* out) {
+  Weights& W = *w_;
   hipStream_t s = stream_;
   const int sp = lr_f32_ ? W.lr_wsplit : 0;
   // lo-half offsets (elements) of the split operand buffers
-  const size_t s16_lo = sp ? (size_t)lr_.cap_in * 1024 : 0;
-  const size_t p16_lo = sp ? (size_t)lr_.cap_in * 512 : 0;
-  const size_t x16_lo = sp ? (size_t)(lr_.cap_out + 1) * 512 : 0;
-  HIP_OK(launch_f32_to_f16(s_infer, lr_.s16, (size_t)in_tokens * 1024, s16_lo, s));
+  const size_t s16_lo = sp ? (size_t)lr.cap_in * 1024 : 0;
+  const size_t p16_lo = sp ? (size_t)lr.cap_in * 512 : 0;
+  const size_t x16_lo = sp ? (size_t)(lr.cap_out + 1) * 512 : 0;
+  HIP_OK(launch_f32_to_f16(s_infer, lr.s16, (size_t)in_tokens * 1024, s16_lo, s));
   {
     GemmArgs g;
-    g.M = in_tokens; g.N = 512; g.K = 1024; g.A = lr_.s16; g.lda = 1024;
-    g.W = W.lr_proj_w; g.ldw = 1024; g.bias = W.lr_proj_b; g.C16 = lr_.p16; g.ldc16 = 512;
+    g.M = in_tokens; g.N = 512; g.K = 1024; g.A = lr.s16; g.lda = 1024;
+    g.W = W.lr_proj_w; g.ldw = 1024; g.bias = W.lr_proj_b; g.C16 = lr.p16; g.ldc16 = 512;
     g.split = sp; g.a_lo = s16_lo; g.w_lo = sp == 2 ? (size_t)512 * 1024 : 0; g.c16_lo = p16_lo;
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F16, s));
   }
-  HIP_OK(launch_nearest_rows(lr_.p16, in_tokens, out_tokens, (float)in_tokens / (float)out_tokens,
-                             lr_.x16, p16_lo, x16_lo, s));
+  HIP_OK(launch_nearest_rows(lr.p16, in_tokens, out_tokens, (float)in_tokens / (float)out_tokens,
+                             lr.x16, p16_lo, x16_lo, s));
   for (int b = 0; b < 4; ++b) {
     GemmArgs g;
     g.M = out_tokens; g.N = 512; g.K = 3 * 512; g.T = out_tokens; g.conv_c = 512;
-    g.A = lr_.x16; g.lda = 512;
+    g.A = lr.x16; g.lda = 512;
     g.W = W.lr_conv_w[b]; g.ldw = 3 * 512; g.bias = W.lr_conv_b[b];
-    g.C32 = lr_.y32; g.ldc32 = 512; g.sum_out = lr_.sum_p; g.ssq_out = lr_.ssq_p;
+    g.C32 = lr.y32; g.ldc32 = 512; g.sum_out = lr.sum_p; g.ssq_out = lr.ssq_p;
     g.split = sp; g.a_lo = x16_lo; g.w_lo = sp == 2 ? (size_t)512 * 1536 : 0;
     HIP_OK(launch_gemm(g, A_CONV3Z, EPI_F32, s));
-    HIP_OK(launch_gn_stats(lr_.sum_p, lr_.ssq_p, out_tokens, 1e-5f, lr_.stats, s));
-    HIP_OK(launch_gn_mish(lr_.y32, lr_.stats, W.lr_gn_w[b], W.lr_gn_b[b], out_tokens, lr_.x16,
+    HIP_OK(launch_gn_stats(lr.sum_p, lr.ssq_p, out_tokens, 1e-5f, lr.stats, s));
+    HIP_OK(launch_gn_mish(lr.y32, lr.stats, W.lr_gn_w[b], W.lr_gn_b[b], out_tokens, lr.x16,
                           x16_lo, s));
   }
   GemmArgs g;
-  g.M = out_tokens; g.N = 512; g.K = 512; g.A = lr_.x16; g.lda = 512;
+  g.M = out_tokens; g.N = 512; g.K = 512; g.A = lr.x16; g.lda = 512;
   g.W = W.lr_out_w; g.ldw = 512; g.bias = W.lr_out_b; g.C32 = out; g.ldc32 = 512;
   g.split = sp; g.a_lo = x16_lo; g.w_lo = sp == 2 ? (size_t)512 * 512 : 0;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
@@ -1667,6 +1725,34 @@ int Engine::condition_device(const float* s_infer, int codes, const float* promp
   HIP_OK(hipMemcpyAsync(cond, prompt_cond, (size_t)prompt_tokens * 512 * 4,
                         hipMemcpyDeviceToDevice, stream_));
   length_regulator_device(s_infer, codes, gen, cond + (size_t)prompt_tokens * 512);
+  return gen;
+}
+
+// condition_device on the static scratch: no device or host memory is
+// allocated, and nothing is cleared (every scratch value the kernels read is
+// written earlier in the same call: the split operands, the zero padding
+// row, the partial sums and the statistics).
+int Engine::condition_device_noalloc(const float* s_infer, int codes, const float* prompt_cond,
+                                     int prompt_tokens, float* cond) {
+  if (!w_->has_lr)
+    throw std::runtime_error("length regulator: the context has no s2mel.net.length_regulator.* tensors");
+  if (codes <= 0 || prompt_tokens <= 0)
+    throw std::invalid_argument("condition: codes and prompt_tokens must be positive");
+  if (codes > kNoAllocMaxCodes)
+    throw std::invalid_argument("condition (no-alloc): codes exceeds the scratch limit of " +
+                                std::to_string(kNoAllocMaxCodes));
+  const int gen = generated_frames(codes);
+  if (gen <= 0) throw std::invalid_argument("condition: generated frame count is zero");
+  HIP_OK(hipSetDevice(device_));
+  char* base = scratch_ptr(device_);
+  if (!base) throw HipError("condition (no-alloc): no scratch address for this device");
+  const LrView v{reinterpret_cast<half_t*>(base + kScrS16), reinterpret_cast<half_t*>(base + kScrP16),
+                 reinterpret_cast<half_t*>(base + kScrX16), reinterpret_cast<float*>(base + kScrY32),
+                 reinterpret_cast<float*>(base + kScrSum),  reinterpret_cast<float*>(base + kScrSsq),
+                 reinterpret_cast<float*>(base + kScrStats), kNoAllocMaxCodes, kNoAllocMaxFrames};
+  HIP_OK(hipMemcpyAsync(cond, prompt_cond, (size_t)prompt_tokens * 512 * 4, hipMemcpyDeviceToDevice,
+                        stream_));
+  length_regulator_on(v, s_infer, codes, gen, cond + (size_t)prompt_tokens * 512);
   return gen;
 }
 

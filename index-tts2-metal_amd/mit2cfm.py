@@ -26,6 +26,7 @@ DTYPE_F32, DTYPE_F16 = 0, 1
 FLAG_SYNC = 1
 STAGES = {"length_regulator": 1, "vocoder": 2}  # MIT2CFM_STAGE_*
 PRECISIONS = {"f16": 0, "f32": 1}  # MIT2CFM_PREC_*
+NOALLOC_MAX_CODES = 1024  # MIT2CFM_NOALLOC_MAX_CODES
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
@@ -99,6 +100,7 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_length_regulator": (st, [vp, _f32p, u32, u32, _f32p]),
         "mit2cfm_condition": (st, [vp, _f32p, u32, _f32p, u32, _f32p, _u32p]),
         "mit2cfm_condition_device": (st, [vp, vp, u32, vp, u32, vp, _u32p, u32]),
+        "mit2cfm_condition_device_noalloc": (st, [vp, vp, u32, vp, u32, vp, _u32p, u32]),
         "mit2cfm_generated_frames": (u32, [u32]),
         "mit2cfm_noise_device": (st, [vp, u32, u32, u64, f32, vp, u32]),
         "mit2cfm_bigvgan": (st, [vp, _f32p, u32, _f32p]),
@@ -557,6 +559,15 @@ class Context:
         g = np.zeros(1, np.uint32)
         self._c(lib().mit2cfm_condition_device(self._h, s_infer_ptr, codes, prompt_ptr, prompt_tokens,
                                                cond_ptr, _pu(g), FLAG_SYNC if sync else 0))
+        return int(g[0])
+
+    def condition_device_noalloc(self, s_infer_ptr: int, codes: int, prompt_ptr: int, prompt_tokens: int,
+                                 cond_ptr: int, sync: bool = False) -> int:
+        """condition_device on the library's static scratch (allocates nothing;
+        codes <= NOALLOC_MAX_CODES); returns the generated frames."""
+        g = np.zeros(1, np.uint32)
+        self._c(lib().mit2cfm_condition_device_noalloc(self._h, s_infer_ptr, codes, prompt_ptr, prompt_tokens,
+                                                       cond_ptr, _pu(g), FLAG_SYNC if sync else 0))
         return int(g[0])
 
     def noise_device(self, tokens: int, channels: int, seed: int, temperature: float, out_ptr: int,
