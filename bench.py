@@ -45,6 +45,20 @@ Prints ONE JSON line.  Extra fields:
                 time per call from HIP events, its real-time factor, and the
                 reference's published time for that segment on its own
                 hardware (a different machine and the real weights).
+  configs       every other workload of the benchmark set on the same
+                context, inputs resident in HBM, median of the timed
+                decodes: one estimator forward at T=256 (B=2 CFG pair),
+                T=128 with 12 steps (launch-bound), T=3000 with 25 steps
+                (O(T^2) attention), and 8 right-padded requests (B=16) with 16
+                steps; each with frames/s, CFM steps/s and whole-decode MFMA
+                utilisation on valid rows and keys only.
+  pcie_inclusive
+                the headline decode through the host-pointer entry point
+                (upload, decode, readback), median of 10 -- reported beside
+                `value`, never as it.
+  first_call_ms the first decode of a length the context has not seen:
+                graph capture and instantiation included, beside the
+                replay time of the same shape.
   gpt_decode    the GPT mel-code decoder (the stage that makes the semantic
                 codes) on the GPU: greedy decode of 553 codes after a
                 150-row prefix with the 24-layer synthetic model (seed
@@ -97,6 +111,11 @@ def parse():
     p.add_argument("--gpt-codes", type=int, default=553,
                    help="mel codes of the timed GPT greedy decode (0 = skip)")
     p.add_argument("--gpt-prefix", type=int, default=150, help="prefix rows of the GPT decode")
+    p.add_argument("--pcie-reps", type=int, default=10, help="host-pointer decodes (median)")
+    p.add_argument("--no-configs", dest="configs", action="store_false",
+                   help="skip the other workloads of the benchmark set")
+    p.add_argument("--no-cpu-1thread", dest="cpu_1thread", action="store_false",
+                   help="skip the one-thread CPU baseline")
     p.add_argument("--calib-mib", type=int, default=256,
                    help="size of the counter-calibration copy (0 = skip)")
     return p.parse_args()
@@ -145,6 +164,142 @@ def cpu_baseline(tensors, T, P, cfm_steps, cfg, threads):
         "sample": f"1 of {cfm_steps} Euler steps (cond + null estimator forwards) at T={T}, "
                   f"{step_s:.1f} s measured, decode time extrapolated x{cfm_steps}",
     }
+
+
+def cpu_baseline_1thread(tensors, T=256, P=96):
+    """The reference CPU path is single-threaded (cpu_linear, tokenizer_tests.cpp:3026):
+    the oracle on one thread for one estimator forward pair at T=256 (the
+    benchmark set's CPU-runnable case), scaled to the T=860 decode by
+    algorithmic FLOPs."""
+    import numpy as np
+    import mit2cfm
+    from oracle import oracle
+
+    oracle.set_threads(1)
+    model = oracle.Model(tensors)
+    x = mit2cfm.normal_noise(T, 80, 1)
+    cond = mit2cfm.normal_noise(T, 512, 2)
+    style = mit2cfm.normal_noise(1, 192, 3)[0]
+    px = np.zeros((T, 80), np.float32)
+    px[:P] = mit2cfm.normal_noise(P, 80, 4, 2.0) - 5.0
+    mask = np.ones(T, np.uint32)
+    t0 = time.perf_counter()
+    model.estimator_step(x, px, cond, style, 0.5, mask)
+    model.estimator_step(x, np.zeros_like(px), np.zeros_like(cond), np.zeros_like(style), 0.5, mask)
+    sec = time.perf_counter() - t0
+    model.close()
+    f_sample = FLOPS_PER_ROW * 2 * T + FLOPS_PER_T2 * 2 * T * T
+    f_decode = 25 * (FLOPS_PER_ROW * 2 * 860 + FLOPS_PER_T2 * 2 * 860 * 860)
+    return {"value": round(860 / (sec * f_decode / f_sample), 4), "unit": "mel frames/s", "cores": 1,
+            "kind": "port", "gflop_per_s": round(f_sample / sec / 1e9, 2),
+            "sample": f"one estimator forward pair (cond + null) at T={T}, {sec:.1f} s on one thread, "
+                      "scaled to the 25-step T=860 decode by algorithmic FLOPs"}
+
+
+def request_lengths(n: int, lo: int, hi: int, seed: int) -> list[int]:
+    """Target lengths of the padded-batch workload: uniform in [lo, hi] from one
+    seed by splitmix64 modulo (the same draw as the test fixtures)."""
+    out, st = [], seed
+    for _ in range(n):
+        st = (st + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
+        z = st
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
+        out.append(lo + (z ^ (z >> 31)) % (hi - lo + 1))
+    return out
+
+
+def decode_flops(valid_T, steps):
+    """Algorithmic FLOPs of a CFG decode: each request is a cond + null branch
+    pair; valid rows and keys only."""
+    rows = sum(2 * t for t in valid_T)
+    keys2 = sum(2 * t * t for t in valid_T)
+    return steps * (FLOPS_PER_ROW * rows + FLOPS_PER_T2 * keys2)
+
+
+def timed_median(fn, sync, reps):
+    """Median wall time (ms) of `reps` calls, each bracketed by device synchronisation."""
+    ts = []
+    for _ in range(reps):
+        sync()
+        t0 = time.perf_counter()
+        fn()
+        sync()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2], ts
+
+
+def configs_section(a, mit2cfm, ctx, torch, dev):
+    """The benchmark set's other workloads on resident inputs."""
+    import numpy as np
+
+    def sync():
+        ctx.synchronize()
+        torch.cuda.synchronize()
+
+    out = {}
+    singles = [("config1_forward_T256", 256, 96, 1, 20), ("config3_T128_S12", 128, 48, 12, 20),
+               ("config4_T3000_S25", 3000, 258, 25, 5)]
+    for name, T, P, S, reps in singles:
+        x0 = torch.from_numpy(mit2cfm.normal_noise(T, 80, 1)).to(dev)
+        cond = torch.from_numpy(mit2cfm.normal_noise(T, 512, 2)).to(dev)
+        style = torch.from_numpy(mit2cfm.normal_noise(1, 192, 3)[0]).to(dev)
+        prompt = torch.from_numpy(np.ascontiguousarray(mit2cfm.normal_noise(P, 80, 4, 2.0) - 5.0)).to(dev)
+        o = torch.empty((T, 80), dtype=torch.float32, device=dev)
+        sync()
+
+        def run():
+            ctx.decode_device(x0.data_ptr(), prompt.data_ptr(), cond.data_ptr(), style.data_ptr(), T, P, S,
+                              a.cfg, o.data_ptr())
+
+        for _ in range(2):
+            run()
+        med, _ = timed_median(run, sync, reps)
+        fl = decode_flops([T], S)
+        r = {"tokens": T, "prompt_tokens": P, "cfm_steps": S, "cfg_rate": a.cfg, "branches": 2,
+             "ms_per_decode": round(med, 3), "frames_per_s": round(T / (med / 1e3), 1),
+             "cfm_steps_per_s": round(S / (med / 1e3), 1),
+             "algorithmic_tflop": round(fl / 1e12, 4),
+             "decode_mfma_util": round(fl / (med / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4), "timed": reps}
+        if S == 1:
+            r["note"] = "one CFG Euler step: the estimator forward pair (B=2) plus the fused conv2/CFG/Euler update"
+        out[name] = r
+    # 8 right-padded requests (B = 16), 16 steps
+    P, S, nreq = 258, 16, 8
+    toks = [P + L for L in request_lengths(nreq, 300, 1500, 5)]
+    tmax = max(toks)
+    x0 = np.zeros((nreq, tmax, 80), np.float32)
+    pr = np.zeros((nreq, tmax, 80), np.float32)
+    co = np.zeros((nreq, tmax, 512), np.float32)
+    st = np.zeros((nreq, 192), np.float32)
+    for r_, T in enumerate(toks):
+        x0[r_, :T] = mit2cfm.normal_noise(T, 80, 100 + 10 * r_)
+        co[r_, :T] = mit2cfm.normal_noise(T, 512, 101 + 10 * r_)
+        st[r_] = mit2cfm.normal_noise(1, 192, 102 + 10 * r_)[0]
+        pr[r_, :P] = mit2cfm.normal_noise(P, 80, 103 + 10 * r_, 2.0) - 5.0
+    d = [torch.from_numpy(v).to(dev) for v in (x0, pr, co, st)]
+    o = torch.empty((nreq, tmax, 80), dtype=torch.float32, device=dev)
+    sync()
+
+    def runb():
+        ctx.decode_batched_device(toks, [P] * nreq, d[0].data_ptr(), d[1].data_ptr(), d[2].data_ptr(),
+                                  d[3].data_ptr(), tmax, S, a.cfg, o.data_ptr())
+
+    for _ in range(2):
+        runb()
+    med, _ = timed_median(runb, sync, 5)
+    fl = decode_flops(toks, S)
+    out["config5_8req_padded_B16_S16"] = {
+        "requests": nreq, "tokens": toks, "t_max": tmax, "prompt_tokens": P, "cfm_steps": S,
+        "cfg_rate": a.cfg, "branches": 2 * nreq, "ms_per_decode": round(med, 3),
+        "frames_per_s": round(sum(toks) / (med / 1e3), 1),
+        "padded_frames_per_s": round(nreq * tmax / (med / 1e3), 1),
+        "cfm_steps_per_s": round(S / (med / 1e3), 1), "algorithmic_tflop": round(fl / 1e12, 4),
+        "decode_mfma_util": round(fl / (med / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4),
+        "note": "frames/s and utilisation count valid frames, rows and keys only (padding is waste)",
+        "timed": 5}
+    return out
 
 
 def cpu_threads(a) -> int:
@@ -387,22 +542,31 @@ def main():
         d_pc = torch.from_numpy(mit2cfm.normal_noise(P, 512, 7)).to(dev)
         d_c = torch.empty((P + gen, 512), dtype=torch.float32, device=dev)
         torch.cuda.synchronize()
-        for _ in range(3):
-            ctx.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, d_c.data_ptr())
-        ctx.synchronize()
-        c0 = torch.cuda.Event(enable_timing=True)
-        c1 = torch.cuda.Event(enable_timing=True)
-        c0.record(stream)
-        for _ in range(a.cond_calls):
-            ctx.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, d_c.data_ptr())
-        c1.record(stream)
-        ctx.synchronize()
-        torch.cuda.synchronize()
-        c_ms = c0.elapsed_time(c1) / a.cond_calls
+        def time_condition():
+            for _ in range(3):
+                ctx.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, d_c.data_ptr())
+            ctx.synchronize()
+            c0 = torch.cuda.Event(enable_timing=True)
+            c1 = torch.cuda.Event(enable_timing=True)
+            c0.record(stream)
+            for _ in range(a.cond_calls):
+                ctx.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, d_c.data_ptr())
+            c1.record(stream)
+            ctx.synchronize()
+            torch.cuda.synchronize()
+            return c0.elapsed_time(c1) / a.cond_calls
+
+        c_ms = time_condition()  # fp32 mode (split operands), the default
+        ctx.set_precision("length_regulator", "f16")
+        c16_ms = time_condition()
+        ctx.set_precision("length_regulator", "f32")
         lr_flops = 2.0 * codes * 512 * 1024 + 4 * 2.0 * gen * 512 * 1536 + 2.0 * gen * 512 * 512
         cp = {"workload": f"length regulator {codes} codes -> {gen} frames + merge with {P} prompt rows",
+              "precision": "f32 (split f16 operand pairs)",
               "us_per_call": round(c_ms * 1e3, 2), "algorithmic_gflop": round(lr_flops / 1e9, 3),
-              "tflops": round(lr_flops / (c_ms / 1e3) / 1e12, 2)}
+              "tflops": round(lr_flops / (c_ms / 1e3) / 1e12, 2),
+              "f16_mode": {"us_per_call": round(c16_ms * 1e3, 2),
+                           "tflops": round(lr_flops / (c16_ms / 1e3) / 1e12, 2)}}
         if not a.no_cpu_baseline:
             cp["cpu_baseline"] = condition_cpu_baseline(lr_tensors, s_infer, gen, cpu_threads(a))
 
@@ -411,24 +575,36 @@ def main():
     if a.voc_calls:
         d_wav = torch.empty(256 * T, dtype=torch.float32, device=dev)
         torch.cuda.synchronize()
-        for _ in range(2):
-            ctx.bigvgan_device(d_out.data_ptr(), T, d_wav.data_ptr())
-        ctx.synchronize()
-        v0 = torch.cuda.Event(enable_timing=True)
-        v1 = torch.cuda.Event(enable_timing=True)
-        v0.record(stream)
-        for _ in range(a.voc_calls):
-            ctx.bigvgan_device(d_out.data_ptr(), T, d_wav.data_ptr())
-        v1.record(stream)
-        ctx.synchronize()
-        torch.cuda.synchronize()
-        v_ms = v0.elapsed_time(v1) / a.voc_calls
+
+        def time_vocoder():
+            for _ in range(2):
+                ctx.bigvgan_device(d_out.data_ptr(), T, d_wav.data_ptr())
+            ctx.synchronize()
+            v0 = torch.cuda.Event(enable_timing=True)
+            v1 = torch.cuda.Event(enable_timing=True)
+            v0.record(stream)
+            for _ in range(a.voc_calls):
+                ctx.bigvgan_device(d_out.data_ptr(), T, d_wav.data_ptr())
+            v1.record(stream)
+            ctx.synchronize()
+            torch.cuda.synchronize()
+            return v0.elapsed_time(v1) / a.voc_calls
+
+        v_ms = time_vocoder()  # fp32 mode (split operands), the default
+        ctx.set_precision("vocoder", "f16")
+        v16_ms = time_vocoder()
+        ctx.set_precision("vocoder", "f32")
         vflops = mit2cfm.bigvgan_flops(T)
         voc = {"workload": f"BigVGAN v2 256x, {T} mel frames -> {256 * T} samples",
+               "precision": "f32 (split f16 operand pairs: three matrix-core products per term)",
                "ms_per_call": round(v_ms, 3), "samples_per_s": round(256 * T / (v_ms / 1e3), 1),
                "algorithmic_tflop": round(vflops / 1e12, 4),
                "tflops": round(vflops / (v_ms / 1e3) / 1e12, 1),
-               "mfma_util": round(vflops / (v_ms / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4)}
+               "mfma_util": round(vflops / (v_ms / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4),
+               "f16_mode": {"ms_per_call": round(v16_ms, 3),
+                            "samples_per_s": round(256 * T / (v16_ms / 1e3), 1),
+                            "tflops": round(vflops / (v16_ms / 1e3) / 1e12, 1),
+                            "mfma_util": round(vflops / (v16_ms / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4)}}
         if not a.no_cpu_baseline:
             voc["cpu_baseline"] = vocoder_cpu_baseline(bv_tensors, d_out.cpu().numpy(), cpu_threads(a))
 
@@ -470,12 +646,37 @@ def main():
                                       "source": "docs/evolution.md:27, segment 1"},
               "speedup_vs_published": round(5390.0 / a_ms, 1)}
 
-    # Host-pointer decode (PCIe-inclusive; reported, never the headline value).
+    # Host-pointer decode (upload, decode, readback): PCIe-inclusive, median of
+    # 10, reported beside the headline value, never as it.
     ctx.decode(x0, prompt, cond, style, S, cfg)
-    t1 = time.perf_counter()
-    for _ in range(3):
-        ctx.decode(x0, prompt, cond, style, S, cfg)
-    pcie_ms = (time.perf_counter() - t1) * 1e3 / 3
+    pcie_ms, pcie_all = timed_median(lambda: ctx.decode(x0, prompt, cond, style, S, cfg),
+                                     lambda: None, a.pcie_reps)
+
+    # First decode of a length this context has not seen: graph capture and
+    # instantiation, then the replay of the same shape.
+    Tn = T + 1
+    d_x0n = torch.from_numpy(mit2cfm.normal_noise(Tn, 80, 11)).to(dev)
+    d_cn = torch.from_numpy(mit2cfm.normal_noise(Tn, 512, 12)).to(dev)
+    d_on = torch.empty((Tn, 80), dtype=torch.float32, device=dev)
+
+    def new_t():
+        ctx.decode_device(d_x0n.data_ptr(), d_prompt.data_ptr(), d_cn.data_ptr(), d_style.data_ptr(), Tn, P, S,
+                          cfg, d_on.data_ptr())
+
+    def sync_all():
+        ctx.synchronize()
+        torch.cuda.synchronize()
+
+    first_ms, _ = timed_median(new_t, sync_all, 1)
+    replay_ms, _ = timed_median(new_t, sync_all, 3)
+    first_call = {"tokens": Tn, "first_call_ms": round(first_ms, 3), "replay_ms": round(replay_ms, 3),
+                  "capture_and_instantiate_ms": round(first_ms - replay_ms, 3),
+                  "graph_cache": dict(zip(("held", "capacity"), ctx.graph_count()))}
+    ctx.set_graph(False)
+    first_call["no_graph_ms"] = round(timed_median(new_t, sync_all, 3)[0], 3)
+    ctx.set_graph(True)
+
+    configs = configs_section(a, mit2cfm, ctx, torch, dev) if a.configs else None
     ctx.close()
 
     result = {
@@ -500,9 +701,15 @@ def main():
         "event_ms_per_decode": round(ev_ms, 4),
         "decode_mfma_util": round(flops_decode / (ms_per_decode / 1e3) / 1e12 / PEAK_F16_TFLOPS, 4),
         "algorithmic_tflop_per_decode": round(flops_decode / 1e12, 4),
-        "pcie_inclusive_frames_per_s": round(T / (pcie_ms / 1e3), 1),
+        "pcie_inclusive": {"frames_per_s": round(T / (pcie_ms / 1e3), 1), "median_ms": round(pcie_ms, 3),
+                           "runs": len(pcie_all), "min_ms": round(pcie_all[0], 3),
+                           "max_ms": round(pcie_all[-1], 3),
+                           "what": "host-pointer decode: upload, decode, readback"},
+        "first_call": first_call,
         "roofline": roof,
     }
+    if configs:
+        result["configs"] = configs
     if cp:
         result["condition_producer"] = cp
     if voc:
@@ -515,6 +722,9 @@ def main():
                                   "image_mib": round(img_mb, 1)}
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(tensors, T, P, S, cfg, cpu_threads(a))
+        result["cpu_baseline"]["nproc"] = os.cpu_count()
+        if a.cpu_1thread:
+            result["cpu_baseline_1thread"] = cpu_baseline_1thread(tensors)
     print(json.dumps(result), flush=True)
 
 

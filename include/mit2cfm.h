@@ -118,6 +118,16 @@ mit2cfm_status mit2cfm_decode_batched(mit2cfm_ctx* ctx, uint32_t nreq, uint32_t 
                                       const float* style, uint32_t steps, float cfg_rate,
                                       float* x_out);
 
+/* The same batched decode on DEVICE buffers already resident in HBM (x0,
+ * prompt, cond, style, x_out as above); tokens and prompt_tokens stay host
+ * arrays of nreq values.  Enqueued on the context's stream (flags as for
+ * mit2cfm_decode_device).  No reference counterpart. */
+mit2cfm_status mit2cfm_decode_batched_device(mit2cfm_ctx* ctx, uint32_t nreq, uint32_t t_max,
+                                             const uint32_t* tokens, const uint32_t* prompt_tokens,
+                                             const float* x0, const float* prompt, const float* cond,
+                                             const float* style, uint32_t steps, float cfg_rate,
+                                             float* x_out, uint32_t flags);
+
 /* ---- one estimator forward ---------------------------------------------------
  * Replaces run_dit_estimator_step_metal (dit_cfm_bigvgan.cpp:2778); semantics
  * of run_dit_estimator_step_cpu (:1768) for each of `batch` independent
@@ -131,8 +141,14 @@ mit2cfm_status mit2cfm_estimator_step(mit2cfm_ctx* ctx, const float* x, const fl
 /* ---- stream control ----------------------------------------------------------- */
 void* mit2cfm_stream(mit2cfm_ctx* ctx); /* the context's hipStream_t */
 mit2cfm_status mit2cfm_synchronize(mit2cfm_ctx* ctx);
-/* Whole-decode hipGraph replay on (1, default) or off (0). */
+/* Whole-decode hipGraph replay on (1, default) or off (0).  Each decode
+ * shape (request count, length, steps, cfg rate and the io pointers) is
+ * captured once into a graph; at most *capacity (8) graphs are kept per
+ * context, the least recently used destroyed first.
+ * mit2cfm_decode_graph_count reports how many are held now.  No reference
+ * counterpart (the reference records one command buffer per decode). */
 mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on);
+mit2cfm_status mit2cfm_decode_graph_count(mit2cfm_ctx* ctx, uint32_t* count, uint32_t* capacity);
 
 /* ---- arithmetic of the fp32 stages ---------------------------------------------
  * The reference runs the length regulator (run_length_regulator_full_metal,

@@ -341,6 +341,22 @@ mit2cfm_status mit2cfm_decode_batched(mit2cfm_ctx* ctx, uint32_t nreq, uint32_t 
   });
 }
 
+mit2cfm_status mit2cfm_decode_batched_device(mit2cfm_ctx* ctx, uint32_t nreq, uint32_t t_max,
+                                             const uint32_t* tokens, const uint32_t* prompt_tokens,
+                                             const float* x0, const float* prompt, const float* cond,
+                                             const float* style, uint32_t steps, float cfg_rate,
+                                             float* x_out, uint32_t flags) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  return guarded(ctx, [&] {
+    require(nreq > 0 && t_max > 0, "nreq and t_max must be positive");
+    require(tokens && prompt_tokens && x0 && prompt && cond && style && x_out,
+            "pointer arguments must not be NULL");
+    ctx->eng->decode_device(x0, prompt, cond, style, (int)nreq, (int)t_max, tokens, prompt_tokens,
+                            (int)steps, cfg_rate, x_out, nullptr);
+    if (flags & MIT2CFM_FLAG_SYNC) ctx->eng->sync();
+  });
+}
+
 mit2cfm_status mit2cfm_estimator_step(mit2cfm_ctx* ctx, const float* x, const float* prompt_x,
                                       const float* cond, const float* style,
                                       const uint32_t* key_mask, float t, uint32_t batch,
@@ -380,6 +396,13 @@ mit2cfm_status mit2cfm_synchronize(mit2cfm_ctx* ctx) {
 mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on) {
   if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
   ctx->eng->set_use_graph(on != 0);
+  return MIT2CFM_OK;
+}
+
+mit2cfm_status mit2cfm_decode_graph_count(mit2cfm_ctx* ctx, uint32_t* count, uint32_t* capacity) {
+  if (!ctx || !count) return fail(ctx, MIT2CFM_E_ARG, "ctx and count must not be NULL");
+  *count = (uint32_t)ctx->eng->graph_count();
+  if (capacity) *capacity = (uint32_t)mit2hip::Engine::kMaxGraphs;
   return MIT2CFM_OK;
 }
 

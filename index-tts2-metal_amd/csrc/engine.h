@@ -271,13 +271,20 @@ class Engine {
   struct GraphEntry {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    uint64_t last_use = 0;  // use_tick_ of the latest launch
   };
-  // key: nreq, T, steps, cfg bits, vtrace ptr, io pointers
+  // Captured whole-decode graphs, least recently used evicted past
+  // kMaxGraphs.  key: nreq, T, steps, cfg bits, vtrace ptr, io pointers.
   std::map<std::tuple<int, int, int, uint32_t, const void*, const void*, const void*, const void*,
                       const void*, const void*>,
            GraphEntry>
       graphs_;
+  uint64_t use_tick_ = 0;
   void clear_graphs();
+
+ public:
+  static constexpr size_t kMaxGraphs = 8;
+  size_t graph_count() const { return graphs_.size(); }
 };
 
 }  // namespace mit2hip

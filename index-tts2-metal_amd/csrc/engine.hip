@@ -1179,6 +1179,18 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
                              (const void*)x_out);
   auto it = graphs_.find(key);
   if (it == graphs_.end()) {
+    if (graphs_.size() >= kMaxGraphs) {
+      // Evict the least recently used graph.  Launches already enqueued on
+      // the stream may still read its executable, so wait for them first
+      // (a new shape pays a capture anyway).
+      auto lru = graphs_.begin();
+      for (auto g = graphs_.begin(); g != graphs_.end(); ++g)
+        if (g->second.last_use < lru->second.last_use) lru = g;
+      HIP_OK(hipStreamSynchronize(stream_));
+      (void)hipGraphExecDestroy(lru->second.exec);
+      (void)hipGraphDestroy(lru->second.graph);
+      graphs_.erase(lru);
+    }
     GraphEntry ge;
     HIP_OK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
     try {
@@ -1190,9 +1202,14 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
       throw;
     }
     HIP_OK(hipStreamEndCapture(stream_, &ge.graph));
-    HIP_OK(hipGraphInstantiate(&ge.exec, ge.graph, nullptr, nullptr, 0));
+    const hipError_t ie = hipGraphInstantiate(&ge.exec, ge.graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+      (void)hipGraphDestroy(ge.graph);
+      throw HipError(std::string("hipGraphInstantiate failed: ") + hipGetErrorString(ie));
+    }
     it = graphs_.emplace(key, ge).first;
   }
+  it->second.last_use = ++use_tick_;
   HIP_OK(hipGraphLaunch(it->second.exec, stream_));
 }
 

@@ -67,11 +67,13 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_decode_trace": (st, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, u32, f32, _f32p, _f32p]),
         "mit2cfm_decode_batched": (st, [vp, u32, u32, _u32p, _u32p, _f32p, _f32p, _f32p, _f32p,
                                         u32, f32, _f32p]),
+        "mit2cfm_decode_batched_device": (st, [vp, u32, u32, _u32p, _u32p, vp, vp, vp, vp, u32, f32, vp, u32]),
         "mit2cfm_estimator_step": (st, [vp, _f32p, _f32p, _f32p, _f32p, _u32p, f32, u32, u32, _f32p]),
         "mit2cfm_stream": (vp, [vp]),
         "mit2cfm_synchronize": (st, [vp]),
         "mit2cfm_set_graph": (st, [vp, i32]),
         "mit2cfm_set_precision": (st, [vp, i32, i32]),
+        "mit2cfm_decode_graph_count": (st, [vp, _u32p, _u32p]),
         "mit2cfm_get_precision": (st, [vp, i32, ctypes.POINTER(i32)]),
         "mit2cfm_stage_timestep_embedder": (st, [vp, f32, i32, _f32p]),
         "mit2cfm_stage_input_merge": (st, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, _f32p]),
@@ -476,6 +478,16 @@ class Context:
                                              cfg_rate, _p(out)))
         return out
 
+    def decode_batched_device(self, tokens, prompt_tokens, x0_ptr: int, prompt_ptr: int, cond_ptr: int,
+                              style_ptr: int, t_max: int, steps: int, cfg_rate: float, out_ptr: int,
+                              sync: bool = False) -> None:
+        """decode_batched on device buffers (raw addresses; tokens / prompt_tokens host arrays)."""
+        tokens = _u32(tokens)
+        prompt_tokens = _u32(prompt_tokens)
+        self._c(lib().mit2cfm_decode_batched_device(self._h, tokens.size, t_max, _pu(tokens), _pu(prompt_tokens),
+                                                    x0_ptr, prompt_ptr, cond_ptr, style_ptr, steps, cfg_rate,
+                                                    out_ptr, FLAG_SYNC if sync else 0))
+
     def decode_device(self, x0_ptr: int, prompt_ptr: int, cond_ptr: int, style_ptr: int,
                       tokens: int, prompt_tokens: int, steps: int, cfg_rate: float, out_ptr: int,
                       sync: bool = False) -> None:
@@ -507,6 +519,13 @@ class Context:
 
     def set_graph(self, on: bool) -> None:
         self._c(lib().mit2cfm_set_graph(self._h, 1 if on else 0))
+
+    def graph_count(self) -> tuple[int, int]:
+        """(decode graphs held now, capacity)."""
+        n = np.zeros(1, np.uint32)
+        c = np.zeros(1, np.uint32)
+        self._c(lib().mit2cfm_decode_graph_count(self._h, _pu(n), _pu(c)))
+        return int(n[0]), int(c[0])
 
     def set_precision(self, stage: str, mode: str) -> None:
         """Arithmetic of a stage the reference runs in fp32: stage "length_regulator" or

@@ -2,8 +2,8 @@
 //
 // Keeps the reference CLI's flags for this path (runtime/main.cpp):
 //   --bench-cfm MODEL T STEPS ITERS     (main.cpp:2925-2930, run_bench_cfm :3065)
-//   --test-cfm-euler MODEL              (3 steps, cfg 0; :3342)
-//   --test-cfm-euler-cfg MODEL          (25 steps, cfg 0.5; :3405)
+//   --test-cfm-euler MODEL [--expect FILE]      (3 steps, cfg 0; :3342)
+//   --test-cfm-euler-cfg MODEL [--expect FILE]  (25 steps, cfg 0.5; :3405)
 //   --decode MODEL T P [--cfm_steps N] [--cfg R] [--seed S] [--out FILE]
 //   --cfm_steps N                       (12..25, main.cpp:3181-3187)
 //   --inspect-model-bundle DIR, --write-synthetic-bundle DIR [SEED] [STDDEV]
@@ -16,11 +16,16 @@
 //   --bench-gpt MODEL P CODES ITERS     (greedy decode of CODES after P prefix rows)
 // MODEL is a bundle path, "synthetic[:SEED[:STDDEV]]" or "image:FILE" (a
 // device image written by --write-image).  The reference's
-// --test-cfm-* compare its Metal path with its CPU path; here the CPU
-// comparison lives in the test suite (the library never links the CPU
-// restatement), so these harnesses check the invariants the reference's
-// tests also rely on: finiteness, zero prompt rows, repeat determinism and
-// batched-vs-single equality.
+// --test-cfm-* compare its Metal path with its CPU path (max-abs 1e-4 on
+// its real weights, dit_cfm_bigvgan.cpp:3306-3340).  The library never links
+// a CPU restatement, so here the CPU path's output for the same inputs comes
+// from a file (--expect FILE: raw float32 [5][80], as the test suite writes
+// it from the CPU oracle); the harness reports the max-abs and relative L2
+// error against it and passes at the decode's parity bar (final mel
+// rel-L2 <= 1e-2), printing whether the reference's max-abs bar also holds.
+// Without --expect it checks the invariants the reference's tests also rely
+// on: finiteness, zero prompt rows and repeat determinism.
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -198,7 +203,8 @@ int bench_gpt(const std::string& model, uint32_t prefix_tokens, uint32_t codes, 
   return 0;
 }
 
-int test_cfm_euler(const std::string& model, const char* stage, uint32_t steps, float cfg) {
+int test_cfm_euler(const std::string& model, const char* stage, uint32_t steps, float cfg,
+                   const std::string& expect) {
   auto hip = open_model(model);
   const uint32_t tokens = 5, prompt_tokens = 2;
   const auto x = series((size_t)tokens * 80, 0.018f, 0.07f, 61, 0.011f, 0.03f, false);
@@ -215,12 +221,39 @@ int test_cfm_euler(const std::string& model, const char* stage, uint32_t steps, 
     if (i < (size_t)prompt_tokens * 80) prompt_abs = std::max(prompt_abs, std::fabs(a[i]));
     repeat_err = std::max(repeat_err, std::fabs(a[i] - b[i]));
   }
+  bool ok = nonfinite == 0 && prompt_abs == 0.0f && repeat_err == 0.0f;
   std::cout << "{\n  \"stage\": \"" << stage << "\",\n  \"tokens\": " << tokens
             << ",\n  \"prompt_tokens\": " << prompt_tokens << ",\n  \"steps\": " << steps
             << ",\n  \"cfg_rate\": " << cfg << ",\n  \"nonfinite\": " << nonfinite
             << ",\n  \"prompt_rows_max_abs\": " << prompt_abs
-            << ",\n  \"repeat_max_abs_error\": " << repeat_err << "\n}\n";
-  return (nonfinite == 0 && prompt_abs == 0.0f && repeat_err == 0.0f) ? 0 : 1;
+            << ",\n  \"repeat_max_abs_error\": " << repeat_err;
+  if (!expect.empty()) {
+    std::ifstream f(expect, std::ios::binary | std::ios::ate);
+    const size_t bytes = f ? (size_t)f.tellg() : 0;
+    if (bytes != a.size() * 4) {
+      std::cout << "\n}\n";
+      std::cerr << "error: --expect " << expect << " must hold " << a.size() << " float32 values\n";
+      return 1;
+    }
+    std::vector<float> ref(a.size());
+    f.seekg(0);
+    f.read(reinterpret_cast<char*>(ref.data()), (std::streamsize)bytes);
+    double num = 0.0, den = 0.0;
+    float max_abs = 0.0f;
+    for (size_t i = 0; i < a.size(); ++i) {
+      const double d = (double)a[i] - (double)ref[i];
+      num += d * d;
+      den += (double)ref[i] * ref[i];
+      max_abs = std::max(max_abs, (float)std::fabs(d));
+    }
+    const double rel = std::sqrt(num / std::max(den, 1e-60));
+    ok = ok && rel <= 1e-2;
+    std::cout << ",\n  \"max_abs_error\": " << max_abs << ",\n  \"rel_l2_error\": " << rel
+              << ",\n  \"parity_bar_rel_l2\": 0.01,\n  \"reference_bar_max_abs\": 0.0001"
+              << ",\n  \"meets_reference_bar\": " << (max_abs <= 1e-4f ? "true" : "false");
+  }
+  std::cout << "\n}\n";
+  return ok ? 0 : 1;
 }
 
 int decode(const std::string& model, uint32_t tokens, uint32_t prompt_tokens, uint32_t steps, float cfg,
@@ -247,8 +280,8 @@ int decode(const std::string& model, uint32_t tokens, uint32_t prompt_tokens, ui
 }
 
 int usage() {
-  std::cerr << "usage: mtts-cfm --bench-cfm MODEL T STEPS ITERS | --test-cfm-euler MODEL |\n"
-               "       --test-cfm-euler-cfg MODEL | --decode MODEL T P [--cfm_steps N] [--cfg R]\n"
+  std::cerr << "usage: mtts-cfm --bench-cfm MODEL T STEPS ITERS | --test-cfm-euler MODEL [--expect FILE] |\n"
+               "       --test-cfm-euler-cfg MODEL [--expect FILE] | --decode MODEL T P [--cfm_steps N] [--cfg R]\n"
                "       [--seed S] [--out FILE] | --inspect-model-bundle DIR |\n"
                "       --write-synthetic-bundle DIR [SEED] [STDDEV] |\n"
                "       --bench-bigvgan MODEL T ITERS | --test-bigvgan-vocoder MODEL |\n"
@@ -265,7 +298,7 @@ int main(int argc, char** argv) {
     uint32_t steps = mit2::cfm_synthesis_steps();
     float cfg = 0.7f;
     uint64_t seed = 1;
-    std::string out;
+    std::string out, expect;
     for (int i = 1; i < argc; ++i) {
       const std::string a = argv[i];
       if (a == "--cfm_steps" && i + 1 < argc) {
@@ -281,6 +314,8 @@ int main(int argc, char** argv) {
         seed = std::stoull(argv[i + 1]);
       } else if (a == "--out" && i + 1 < argc) {
         out = argv[i + 1];
+      } else if (a == "--expect" && i + 1 < argc) {
+        expect = argv[i + 1];
       }
     }
     for (int i = 1; i < argc; ++i) {
@@ -288,7 +323,8 @@ int main(int argc, char** argv) {
       if (a == "--bench-cfm" && i + 4 < argc)
         return bench_cfm(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]),
                          (uint32_t)std::stoul(argv[i + 4]));
-      if (a == "--test-cfm-euler" && i + 1 < argc) return test_cfm_euler(argv[i + 1], "cfm_euler", 3, 0.0f);
+      if (a == "--test-cfm-euler" && i + 1 < argc)
+        return test_cfm_euler(argv[i + 1], "cfm_euler", 3, 0.0f, expect);
       if (a == "--write-image" && i + 2 < argc) {
         auto hip = open_model(argv[i + 1], true);
         const mit2cfm_status st = mit2cfm_write_image(hip->get(), argv[i + 2]);
@@ -304,7 +340,7 @@ int main(int argc, char** argv) {
         return bench_gpt(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]),
                          (uint32_t)std::stoul(argv[i + 4]));
       if (a == "--test-cfm-euler-cfg" && i + 1 < argc)
-        return test_cfm_euler(argv[i + 1], "cfm_euler_cfg", 25, 0.5f);
+        return test_cfm_euler(argv[i + 1], "cfm_euler_cfg", 25, 0.5f, expect);
       if (a == "--decode" && i + 3 < argc)
         return decode(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]), steps,
                       cfg, seed, out);

@@ -174,6 +174,39 @@ def test_decode_deterministic_and_graph_equal(mit2, ctx):
     assert np.array_equal(a, c)
 
 
+def test_decode_graph_cache_stays_bounded(mit2, tensors):
+    """50 distinct lengths through one context (production T changes every
+    segment): the captured decode graphs stay within the cache capacity (least
+    recently used evicted), and results do not depend on the cache state: the
+    first lengths decoded again after all 50 give the same bits, and so does a
+    decode with graph replay off."""
+    c = mit2.Context(tensors, device=0)
+    try:
+        first = {}
+        n0, cap = c.graph_count()
+        assert n0 == 0 and cap >= 1
+        # the longest first: later lengths fit the workspace, so only the LRU evicts
+        x0, prompt, cond, style = inputs(mit2, 70, 5, 110)
+        c.decode(x0, prompt, cond, style, 2, 0.7)
+        for i, T in enumerate(range(20, 70)):
+            x0, prompt, cond, style = inputs(mit2, T, 5, 40 + T)
+            out = c.decode(x0, prompt, cond, style, 2, 0.7)
+            n, _ = c.graph_count()
+            assert n == min(i + 2, cap)
+            if i < 3:
+                first[T] = out
+        print(f"graph cache after 50 lengths: {c.graph_count()}", flush=True)
+        for T, ref in first.items():
+            x0, prompt, cond, style = inputs(mit2, T, 5, 40 + T)
+            assert np.array_equal(c.decode(x0, prompt, cond, style, 2, 0.7), ref)
+        c.set_graph(False)
+        x0, prompt, cond, style = inputs(mit2, 20, 5, 60)
+        assert np.array_equal(c.decode(x0, prompt, cond, style, 2, 0.7), first[20])
+        assert c.graph_count()[0] <= cap
+    finally:
+        c.close()
+
+
 def test_decode_cfg_zero_runs_cond_branch_only(mit2, orc, model, ctx):
     T, P = 24, 6
     x0, prompt, cond, style = inputs(mit2, T, P, 9)
