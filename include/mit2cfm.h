@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MIT2CFM_ABI_VERSION 1
+#define MIT2CFM_ABI_VERSION 2
 
 typedef struct mit2cfm_ctx mit2cfm_ctx;
 typedef int32_t mit2cfm_status;
@@ -439,14 +439,20 @@ typedef struct mit2cfm_gpt_sampling {
 /* The sampled form of mit2cfm_gpt_kv_greedy (run_gpt_kv_greedy_metal with
  * do_sample, gpt.cpp:2221-2240): each step's logits go through
  * apply_gpt_sampling_processors (:1618: repetition penalty over the distinct
- * history tokens [start token, predictions so far], temperature, top-k,
- * top-p) and sample_gpt_token_from_logits (:1720: one splitmix64 draw) on the
- * GPU.  Outputs as for mit2cfm_gpt_kv_greedy, plus last_processed_logits
- * [8194] (may be NULL).  A setting the reference rejects (temperature or
- * penalty <= 0, top_p outside (0, 1]) is MIT2CFM_E_ARG. */
+ * history tokens, temperature, top-k, top-p) and sample_gpt_token_from_logits
+ * (:1720: one splitmix64 draw) on the GPU.  The history is the reference's
+ * repetition_history_prefix (:1918, :2224-2229) followed by the predictions
+ * so far: history_prefix [history_prefix_count] (host, at most 8192 tokens;
+ * the synthesis path passes the prefix's fake_inputs, [1] x n + [8192],
+ * synthesis_pipeline.cpp:795-802), or with history_prefix NULL and the count
+ * 0 the start token alone.  Outputs as for mit2cfm_gpt_kv_greedy, plus
+ * last_processed_logits [8194] (may be NULL).  A setting the reference
+ * rejects (temperature or penalty <= 0, top_p outside (0, 1]) is
+ * MIT2CFM_E_ARG. */
 mit2cfm_status mit2cfm_gpt_kv_sample(mit2cfm_ctx* ctx, const float* prefix, uint32_t prefix_tokens,
                                      uint32_t steps, int32_t hf_generate_positions,
-                                     const mit2cfm_gpt_sampling* sampling, uint32_t* predicted_tokens,
+                                     const mit2cfm_gpt_sampling* sampling, const uint32_t* history_prefix,
+                                     uint32_t history_prefix_count, uint32_t* predicted_tokens,
                                      uint32_t* n_predicted, uint32_t* input_tokens, uint32_t* n_input,
                                      int32_t* first_stop_step, float* last_logits,
                                      float* last_processed_logits, double* timings_ms);

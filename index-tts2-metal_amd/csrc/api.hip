@@ -795,13 +795,17 @@ mit2cfm_status mit2cfm_gpt_kv_greedy(mit2cfm_ctx* ctx, const float* prefix, uint
 
 mit2cfm_status mit2cfm_gpt_kv_sample(mit2cfm_ctx* ctx, const float* prefix, uint32_t prefix_tokens,
                                      uint32_t steps, int32_t hf_generate_positions,
-                                     const mit2cfm_gpt_sampling* sampling, uint32_t* predicted_tokens,
+                                     const mit2cfm_gpt_sampling* sampling, const uint32_t* history_prefix,
+                                     uint32_t history_prefix_count, uint32_t* predicted_tokens,
                                      uint32_t* n_predicted, uint32_t* input_tokens, uint32_t* n_input,
                                      int32_t* first_stop_step, float* last_logits,
                                      float* last_processed_logits, double* timings_ms) {
   if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
   return guarded(ctx, [&] {
     require(sampling != nullptr, "sampling must not be NULL");
+    require(history_prefix_count == 0 || history_prefix != nullptr,
+            "history_prefix must not be NULL when history_prefix_count > 0");
+    require(history_prefix_count <= mit2hip::GptDecoder::kMaxHistory, "history_prefix_count must be <= 8192");
     require(prefix_tokens == 0 || prefix != nullptr, "prefix must not be NULL");
     require(prefix_tokens <= (1u << 16), "prefix_tokens must be <= 65536");
     require(steps <= (uint32_t)mit2hip::GptDecoder::kPositions, "steps must be <= 1818");
@@ -813,6 +817,8 @@ mit2cfm_status mit2cfm_gpt_kv_sample(mit2cfm_ctx* ctx, const float* prefix, uint
     smp.top_k = sampling->top_k;
     smp.top_p = sampling->top_p;
     smp.repetition_penalty = sampling->repetition_penalty;
+    smp.history = history_prefix;
+    smp.n_history = history_prefix_count;
     mit2hip::GptDecoder::Greedy g;
     ctx->eng->gpt().kv_sample(prefix, (int)prefix_tokens, (int)steps, hf_generate_positions != 0, smp, g);
     if (n_predicted) *n_predicted = (uint32_t)g.predicted.size();

@@ -66,12 +66,18 @@ class GptDecoder {
     uint32_t top_k = 0;  // 0: off
     float top_p = 1.0f;
     float repetition_penalty = 1.0f;
+    // repetition_history_prefix (gpt.cpp:1918, :2224-2229): when given, the
+    // repetition-penalty history is these tokens followed by the predictions
+    // so far, instead of the start token followed by them.  Host array.
+    const uint32_t* history = nullptr;
+    uint32_t n_history = 0;
   };
+  static constexpr uint32_t kMaxHistory = 8192;  // history-prefix tokens one call may pass
   // The sampled loop (run_gpt_kv_greedy_metal with do_sample, gpt.cpp:
   // 2221-2240): each step's logits go through the sampling processors over
-  // the history [start token, predictions so far] and one splitmix64 draw
-  // (seeded once per call) picks the token.  Throws std::invalid_argument for
-  // the settings the reference rejects.
+  // the history ([start token] or the caller's prefix, then the predictions
+  // so far) and one splitmix64 draw (seeded once per call) picks the token.
+  // Throws std::invalid_argument for the settings the reference rejects.
   void kv_sample(const float* prefix, int prefix_tokens, int steps, bool hf_generate_positions,
                  const Sampling& sampling, Greedy& out);
 

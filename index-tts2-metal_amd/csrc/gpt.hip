@@ -85,7 +85,7 @@ struct GptState {
   float temperature;  //   temperature, top-p, repetition penalty
   float top_p;
   float penalty;
-  int32_t pad0;
+  int32_t n_hist;     //   repetition-history prefix tokens (0: the start token)
   uint64_t rng;       //   splitmix64 state, advanced once per sampled step
   int32_t pad[12];
 };
@@ -109,7 +109,7 @@ struct GemvArgs {
   float* kc = nullptr;
   float* vc = nullptr;
   int advance = 0;            // RES: block 0 advances st->kv
-  int check_stop = 1;         // LOGITS: skip the launch once stopped
+  int check_stop = 1;         // skip the launch once the stop token was predicted
   float* blk_val = nullptr;   // LOGITS: per-block maxima and their rows
   int* blk_idx = nullptr;
   float* lnf_out = nullptr;   // LOGITS: block 0 writes the two LayerNorm outputs
@@ -195,7 +195,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
   static_assert(K % (8 * LPR) == 0, "K must be a multiple of 8 * LPR");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPR, j = lane % LPR;
-  if (EPI == EPI_LOGITS && a.check_stop && a.st->stopped) return;
+  // After a stop, the rest of a replayed group of steps does nothing (the
+  // cache length stops advancing too).
+  if (a.check_stop && a.st->stopped) return;
   const int rbase = blockIdx.x * ROWS + wave * RPW * UR;
 
   // 1. the input vector at this lane's positions 8 (j + c LPR) + e (a lane
@@ -416,7 +418,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs a) {
 
 // The do_sample path of the decode loop (run_gpt_kv_greedy_metal with
 // sampling, gpt.cpp:2221-2240): apply_gpt_sampling_processors (:1618-1718) to
-// the step's logits over the history [start token, predictions so far] --
+// the step's logits over the history (the caller's repetition_history_prefix,
+// else the start token; then the predictions so far) --
 // repetition penalty once per distinct token, temperature, top-k (keep the
 // scores >= the k-th largest), top-p (in ascending (score, index) order drop
 // the tokens whose cumulative probability stays <= 1 - top_p; the largest
@@ -446,7 +449,7 @@ __device__ __forceinline__ double sm64_unit(uint64_t& s) {
 
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* logits, GptState* st,
                                                                 uint32_t* predicted, uint32_t* inputs,
-                                                                float* proc) {
+                                                                float* proc, const uint32_t* hist_prefix) {
   if (st->stopped) return;
   __shared__ float sv[kSortN];
   __shared__ uint32_t si[kSortN];
@@ -464,8 +467,13 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* log
   for (int i = tid; i < (N + 31) / 32; i += kSampleThreads) seen[i] = 0u;
   __syncthreads();
   if (penalty != 1.0f) {  // each distinct history token once (the order does not matter)
-    for (int h = tid; h < st->n_in; h += kSampleThreads) {
-      const uint32_t t = inputs[h];
+    // history = hist_prefix[0..n_hist) ++ predictions (inputs[1..n_in)) when a prefix
+    // is given, else inputs[0..n_in) (the start token, then the predictions)
+    const int nh = st->n_hist;
+    const int h0 = nh > 0 ? 1 : 0;
+    const int total = nh + st->n_in - h0;
+    for (int h = tid; h < total; h += kSampleThreads) {
+      const uint32_t t = h < nh ? hist_prefix[h] : inputs[h - nh + h0];
       if (t >= (uint32_t)N) continue;
       const uint32_t bit = 1u << (t & 31);
       if (atomicOr(&seen[t >> 5], bit) & bit) continue;
@@ -779,6 +787,7 @@ __global__ __launch_bounds__(320) void embed_kernel(const GptState* st, const fl
                                                      const float* pos_emb, const float* rows, int mode,
                                                      float* x) {
   const int i = threadIdx.x;  // float4 index, 320 x 4 = 1280
+  if (mode == 1 && st->stopped) return;
   float4 v;
   if (mode == 0) {
     const int r = min(st->kv, st->rows - 1);
@@ -817,12 +826,13 @@ __device__ __forceinline__ bool attn_row_live(const GptState* st, int z) {
 
 __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const float* q, const float* kc, const float* vc,
                                                                   const GptState* st, float* part, float* out,
-                                                                  int nsplit_max) {
+                                                                  int nsplit_max, int check_stop) {
   constexpr int kWaves = kAttnThreads / 64;
   constexpr int kKeysPerPass = kAttnThreads / 8, kPass = kChunk / kKeysPerPass;
   constexpr int kVKeysPerPass = kAttnThreads / 16, kVPass = kChunk / kVKeysPerPass;
   constexpr int kGroups = kAttnThreads / 16;  // output key groups
   const int h = blockIdx.x, sp = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
+  if (check_stop && st->stopped) return;
   if (!attn_row_live(st, z)) return;
   const int kvn = attn_keys(st, z);
   const int nsplit = (kvn + kChunk - 1) / kChunk;
@@ -903,8 +913,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const float* q
 }
 
 __global__ __launch_bounds__(64) void attn_combine_kernel(const GptState* st, const float* part, float* out,
-                                                          int nsplit_max) {
+                                                          int nsplit_max, int check_stop) {
   const int h = blockIdx.x, z = blockIdx.z, d = threadIdx.x;
+  if (check_stop && st->stopped) return;
   if (!attn_row_live(st, z)) return;
   const int nsplit = (attn_keys(st, z) + kChunk - 1) / kChunk;
   if (nsplit == 1) return;  // written by the split kernel
@@ -1011,13 +1022,18 @@ struct GptDecoder::Impl {
   float *x, *q, *att, *fc, *logits, *lnf, *fn, *blk_val, *kc, *vc, *rows;
   float *xr, *qr, *attr, *fcr;  // a prefill chunk's rows: [8][1280] x3, [8][5120]
   float* proc = nullptr;        // the sampler's processed logits [8194]
+  uint32_t* hist = nullptr;     // the repetition-history prefix [kMaxHistory]
   float* part = nullptr;        // attention splits: [8 query rows][20 heads][nsplit_max][66]
   int nsplit_max = 0;
 
-  void launch_attention(const float* qv, const float* K, const float* V, float* out, int rows_z) {
+  // check_stop: the launch does nothing once the stop token was predicted
+  // (decode steps; the timing hook passes 0).
+  void launch_attention(const float* qv, const float* K, const float* V, float* out, int rows_z,
+                        int check_stop = 1) {
     hipLaunchKernelGGL(attn_split_kernel, dim3(kHeads, nsplit_max, rows_z), dim3(kAttnThreads), 0, s, qv, K, V, st,
-                       part, out, nsplit_max);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(kHeads, 1, rows_z), dim3(kHD), 0, s, st, part, out, nsplit_max);
+                       part, out, nsplit_max, check_stop);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(kHeads, 1, rows_z), dim3(kHD), 0, s, st, part, out, nsplit_max,
+                       check_stop);
   }
   int* blk_idx;
   GptState* host_state = nullptr;  // pinned
@@ -1100,7 +1116,8 @@ struct GptDecoder::Impl {
                    align256((size_t)head_blocks() * 4) +
                    3 * align256((size_t)kPrefillRows * kW * f) + align256((size_t)kPrefillRows * kMLP * f) +
                    align256((size_t)kPrefillRows * kHeads * (cap / kChunk) * kPartF * f) + align256(kVocab * f) +
-                   2 * align256((size_t)L * cap * kW * f) + align256((size_t)rows_cap * kW * f);
+                   2 * align256((size_t)L * cap * kW * f) + align256((size_t)rows_cap * kW * f) +
+                   align256((size_t)GptDecoder::kMaxHistory * 4);
     ws.reserve(bytes);
     st = static_cast<GptState*>(ws.take(sizeof(GptState)));
     predicted = static_cast<uint32_t*>(ws.take((size_t)pred_cap * 4));
@@ -1119,6 +1136,7 @@ struct GptDecoder::Impl {
     attr = static_cast<float*>(ws.take((size_t)kPrefillRows * kW * f));
     fcr = static_cast<float*>(ws.take((size_t)kPrefillRows * kMLP * f));
     proc = static_cast<float*>(ws.take(kVocab * f));
+    hist = static_cast<uint32_t*>(ws.take((size_t)GptDecoder::kMaxHistory * 4));
     nsplit_max = cap / kChunk;
     part = static_cast<float*>(ws.take((size_t)kPrefillRows * kHeads * nsplit_max * kPartF * f));
     kc = static_cast<float*>(ws.take((size_t)L * cap * kW * f));
@@ -1162,7 +1180,8 @@ struct GptDecoder::Impl {
       a.b2 = fn_b; a.y = logits; a.blk_val = blk_val; a.blk_idx = blk_idx; a.lnf_out = lnf; a.fn_out = fn;
       launch_head(a, s);
       if (sample)
-        hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, s, logits, st, predicted, inputs, proc);
+        hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, s, logits, st, predicted, inputs, proc,
+                           hist);
       else
         hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, blk_val, blk_idx, head_blocks(), st, predicted,
                            inputs, 1);
@@ -1257,6 +1276,7 @@ struct GptDecoder::Impl {
       h.top_p = smp->top_p;
       h.penalty = smp->repetition_penalty;
       h.rng = smp->seed;
+      h.n_hist = (int32_t)smp->n_history;
     }
     h.kv = 0;
     h.step = 0;
@@ -1276,7 +1296,9 @@ struct GptDecoder::Impl {
     const uint32_t start = (uint32_t)kStart;
     GPT_OK(hipMemcpyAsync(st, host_state, sizeof(GptState), hipMemcpyHostToDevice, s));
     GPT_OK(hipMemcpyAsync(inputs, &start, 4, hipMemcpyHostToDevice, s));
-    GPT_OK(hipStreamSynchronize(s));  // host_state and `start` are reused below
+    if (smp && smp->n_history)
+      GPT_OK(hipMemcpyAsync(hist, smp->history, (size_t)smp->n_history * 4, hipMemcpyHostToDevice, s));
+    GPT_OK(hipStreamSynchronize(s));  // host_state, `start` and the history are reused below
   }
 };
 
@@ -1401,6 +1423,11 @@ void GptDecoder::kv_sample(const float* prefix, int prefix_tokens, int steps, bo
   if (!(sampling.temperature > 0.0f)) throw std::invalid_argument("gpt: sampling temperature must be positive");
   if (!(sampling.repetition_penalty > 0.0f)) throw std::invalid_argument("gpt: repetition penalty must be positive");
   if (!(sampling.top_p > 0.0f && sampling.top_p <= 1.0f)) throw std::invalid_argument("gpt: top_p must be in (0, 1]");
+  if (sampling.n_history > kMaxHistory)
+    throw std::invalid_argument("gpt: the repetition history prefix holds more than " + std::to_string(kMaxHistory) +
+                                " tokens");
+  if (sampling.n_history && !sampling.history)
+    throw std::invalid_argument("gpt: history prefix must not be NULL when its count is nonzero");
   generate(prefix, prefix_tokens, steps, hf, &sampling, out);
 }
 
@@ -1511,6 +1538,7 @@ const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) 
     // not already in the caches
     const GptLayerDev& w = d.layer[i % d.L];
     GemvArgs a = d.base_args();
+    a.check_stop = 0;  // time the kernels whatever the last decode left in the state
     switch (kernel) {
       case 0:
         a.w = w.attn_w; a.bias = w.attn_b; a.N = kQKV; a.x = d.x; a.g1 = w.ln1_w; a.b1 = w.ln1_b;
@@ -1539,7 +1567,7 @@ const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) 
         break;
       default:
         d.launch_attention(d.q, d.kc + (size_t)(i % d.L) * d.cap * kW, d.vc + (size_t)(i % d.L) * d.cap * kW,
-                           d.att, 1);
+                           d.att, 1, 0);
         break;
     }
   }

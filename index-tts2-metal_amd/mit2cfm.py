@@ -123,8 +123,9 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_gpt_kv_greedy": (st, [vp, _f32p, u32, u32, i32, _u32p, _u32p, _u32p, _u32p,
                                        ctypes.POINTER(i32), _f32p, ctypes.POINTER(ctypes.c_double)]),
         "mit2cfm_gpt_cached_decode": (st, [vp, _f32p, u32, _f32p, _f32p, _f32p, _u32p]),
-        "mit2cfm_gpt_kv_sample": (st, [vp, _f32p, u32, u32, i32, ctypes.POINTER(_GptSampling), _u32p, _u32p, _u32p,
-                                       _u32p, ctypes.POINTER(i32), _f32p, _f32p, ctypes.POINTER(ctypes.c_double)]),
+        "mit2cfm_gpt_kv_sample": (st, [vp, _f32p, u32, u32, i32, ctypes.POINTER(_GptSampling), _u32p, u32, _u32p,
+                                       _u32p, _u32p, _u32p, ctypes.POINTER(i32), _f32p, _f32p,
+                                       ctypes.POINTER(ctypes.c_double)]),
         "mit2cfm_gpt_profile_launch": (st, [vp, i32, u32, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_char_p)]),
     }
@@ -648,9 +649,11 @@ class Context:
 
     def gpt_kv_sample(self, prefix, steps: int, seed: int, temperature: float = 1.0, top_k: int = 0,
                       top_p: float = 1.0, repetition_penalty: float = 1.0,
-                      hf_generate_positions: bool = False) -> dict:
+                      hf_generate_positions: bool = False, history=None) -> dict:
         """The sampled loop (gpt.cpp:2221-2240); as gpt_kv_greedy plus
-        last_processed_logits."""
+        last_processed_logits.  history: the repetition-history prefix
+        (repetition_history_prefix, gpt.cpp:1918), e.g. the prefix's
+        fake_inputs [1] * n + [8192]; None: the start token."""
         x = _f32(prefix).reshape(-1, GPT_WIDTH)
         P = x.shape[0]
         pred = np.zeros(max(steps, 1), np.uint32)
@@ -662,8 +665,11 @@ class Context:
         proc = np.zeros(GPT_VOCAB, np.float32)
         t = (ctypes.c_double * 2)()
         cfg = _GptSampling(seed, temperature, top_k, top_p, repetition_penalty)
+        hist = _u32(history) if history is not None else None
         self._c(lib().mit2cfm_gpt_kv_sample(self._h, _p(x) if P else None, P, steps,
-                                            1 if hf_generate_positions else 0, ctypes.byref(cfg), _pu(pred),
+                                            1 if hf_generate_positions else 0, ctypes.byref(cfg),
+                                            _pu(hist) if hist is not None and hist.size else None,
+                                            0 if hist is None else hist.size, _pu(pred),
                                             _pu(n_pred), _pu(inp), _pu(n_in), ctypes.byref(stop), _p(logits),
                                             _p(proc), t))
         return {"predicted": pred[:n_pred[0]].copy(), "input_tokens": inp[:n_in[0]].copy(),

@@ -136,7 +136,9 @@ std::vector<float> run_bigvgan_vocoder_hip(HipContext& hip, const Bundle& /*bund
 }
 
 GptGreedyOutputs run_gpt_kv_greedy_hip(HipContext& hip, const std::vector<float>& prefix,
-                                       uint32_t prefix_tokens, uint32_t steps, bool hf_generate_positions) {
+                                       uint32_t prefix_tokens, uint32_t steps, bool hf_generate_positions,
+                                       const GptSamplingConfig* sampling,
+                                       const std::vector<uint32_t>* repetition_history_prefix) {
   if (prefix.size() != (size_t)prefix_tokens * 1280)
     throw std::runtime_error("run_gpt_kv_greedy_hip: prefix must have shape [prefix_tokens,1280]");
   GptGreedyOutputs out;
@@ -144,14 +146,34 @@ GptGreedyOutputs run_gpt_kv_greedy_hip(HipContext& hip, const std::vector<float>
   out.input_tokens.resize((size_t)steps + 1);
   out.last_logits.resize(steps ? 8194 : 0);
   uint32_t n_pred = 0, n_in = 0;
-  check(mit2cfm_gpt_kv_greedy(hip.get(), prefix_tokens ? prefix.data() : nullptr, prefix_tokens, steps,
-                              hf_generate_positions ? 1 : 0, out.predicted_tokens.data(), &n_pred,
-                              out.input_tokens.data(), &n_in, &out.first_stop_step,
-                              steps ? out.last_logits.data() : nullptr, nullptr),
-        hip.get());
+  if (sampling && sampling->do_sample) {
+    mit2cfm_gpt_sampling s{sampling->seed, sampling->temperature, sampling->top_k, sampling->top_p,
+                           sampling->repetition_penalty};
+    const bool h = repetition_history_prefix && !repetition_history_prefix->empty();
+    check(mit2cfm_gpt_kv_sample(hip.get(), prefix_tokens ? prefix.data() : nullptr, prefix_tokens, steps,
+                                hf_generate_positions ? 1 : 0, &s, h ? repetition_history_prefix->data() : nullptr,
+                                h ? (uint32_t)repetition_history_prefix->size() : 0u, out.predicted_tokens.data(),
+                                &n_pred, out.input_tokens.data(), &n_in, &out.first_stop_step,
+                                steps ? out.last_logits.data() : nullptr, nullptr, nullptr),
+          hip.get());
+  } else {
+    check(mit2cfm_gpt_kv_greedy(hip.get(), prefix_tokens ? prefix.data() : nullptr, prefix_tokens, steps,
+                                hf_generate_positions ? 1 : 0, out.predicted_tokens.data(), &n_pred,
+                                out.input_tokens.data(), &n_in, &out.first_stop_step,
+                                steps ? out.last_logits.data() : nullptr, nullptr),
+          hip.get());
+  }
   out.predicted_tokens.resize(n_pred);
   out.input_tokens.resize(n_in);
   return out;
+}
+
+GptGreedyOutputs run_gpt_kv_greedy_hip(HipContext& hip, const Bundle& /*bundle*/, const std::vector<float>& prefix,
+                                       uint32_t prefix_tokens, uint32_t steps, bool hf_generate_positions,
+                                       const GptSamplingConfig* sampling,
+                                       const std::vector<uint32_t>* repetition_history_prefix) {
+  return run_gpt_kv_greedy_hip(hip, prefix, prefix_tokens, steps, hf_generate_positions, sampling,
+                               repetition_history_prefix);
 }
 
 GptCachedDecodeOutputs run_gpt_cached_decode_hip(HipContext& hip, const std::vector<float>& input,

@@ -78,11 +78,30 @@ struct GptGreedyOutputs {  // gpt.cpp:1583-1590 (without the backend comparison 
   std::vector<float> last_logits;
   int32_t first_stop_step = -1;
 };
-// run_gpt_kv_greedy_metal (gpt.cpp:1914; CPU definition :1877): prefix
-// [prefix_tokens][1280] -> greedy codes, stopping at the first stop token.
+struct GptSamplingConfig {  // gpt.cpp:1592-1599
+  bool do_sample = false;
+  uint64_t seed = 0;
+  float temperature = 1.0f;
+  uint32_t top_k = 0;
+  float top_p = 1.0f;
+  float repetition_penalty = 1.0f;
+};
+// run_gpt_kv_greedy_metal (gpt.cpp:1914-1918; CPU definition :1877): prefix
+// [prefix_tokens][1280] -> codes, stopping at the first stop token; greedy,
+// or sampled when sampling->do_sample (gpt.cpp:2221-2240), with the
+// repetition penalty over repetition_history_prefix (else the start token)
+// followed by the predictions so far.  The reference's argument order; the
+// bundle is not read (the weights are resident in the context).
+GptGreedyOutputs run_gpt_kv_greedy_hip(HipContext& hip, const Bundle& bundle, const std::vector<float>& prefix,
+                                       uint32_t prefix_tokens, uint32_t steps, bool hf_generate_positions = false,
+                                       const GptSamplingConfig* sampling = nullptr,
+                                       const std::vector<uint32_t>* repetition_history_prefix = nullptr);
+// The same without a bundle argument.
 GptGreedyOutputs run_gpt_kv_greedy_hip(HipContext& hip, const std::vector<float>& prefix,
                                        uint32_t prefix_tokens, uint32_t steps,
-                                       bool hf_generate_positions = false);
+                                       bool hf_generate_positions = false,
+                                       const GptSamplingConfig* sampling = nullptr,
+                                       const std::vector<uint32_t>* repetition_history_prefix = nullptr);
 struct GptCachedDecodeOutputs {  // gpt.cpp:1393-1398
   std::vector<float> ln_f;
   std::vector<float> final_norm;

@@ -200,7 +200,8 @@ int orc_gpt_sampling_processors(const float* logits, uint32_t n, const uint32_t*
 uint32_t orc_gpt_sample_token(const float* processed, uint32_t n, uint64_t* rng_state); /* gpt.cpp:1720 */
 int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens, uint32_t steps,
                       int hf_generate_positions, uint64_t seed, float temperature, uint32_t top_k,
-                      float top_p, float repetition_penalty, uint32_t* predicted,
+                      float top_p, float repetition_penalty, const uint32_t* history_prefix,
+                      uint32_t n_history_prefix, uint32_t* predicted,
                       uint32_t* input_tokens, float* last_logits, float* last_processed,
                       orc_gpt_greedy_result* res);                   /* gpt.cpp:2221-2240 */
 

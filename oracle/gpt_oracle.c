@@ -593,15 +593,20 @@ uint32_t orc_gpt_sample_token(const float* processed, uint32_t n, uint64_t* rng_
 
 /* The sampled form of the cached loop (run_gpt_kv_greedy_metal with
  * do_sample, gpt.cpp:2221-2240): after each step's logits, the processors over
- * the history [start token, predictions so far] and one draw; the rng is
- * seeded once per call.  last_processed receives the last step's processed
+ * the history and one draw; the rng is seeded once per call.  The history is
+ * repetition_history_prefix followed by the predictions so far, or with no
+ * prefix (n_history_prefix 0) the start token followed by them
+ * (gpt.cpp:2224-2229).  last_processed receives the last step's processed
  * logits.  Returns 0, or -1 (a position past the table or an invalid
  * setting). */
 int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens, uint32_t steps, int hf,
                       uint64_t seed, float temperature, uint32_t top_k, float top_p, float repetition_penalty,
+                      const uint32_t* history_prefix, uint32_t n_history_prefix,
                       uint32_t* predicted, uint32_t* input_tokens, float* last_logits, float* last_processed,
                       orc_gpt_greedy_result* res) {
     const uint32_t P = prefix_tokens, cap = P + steps + 1;
+    uint32_t* history = (uint32_t*)malloc(((size_t)n_history_prefix + steps + 1) * sizeof(uint32_t));
+    if (n_history_prefix) memcpy(history, history_prefix, (size_t)n_history_prefix * sizeof(uint32_t));
     const int NL = m->layers;
     float* ck = (float*)malloc((size_t)NL * cap * W * sizeof(float));
     float* cv = (float*)malloc((size_t)NL * cap * W * sizeof(float));
@@ -645,9 +650,17 @@ int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tok
         }
         ++kv;
         head_row(m, cur, ln_f, fnorm, last_logits);
-        /* the history: the start token, then every prediction so far (the loop
-         * stops at the first stop token, so these are the input tokens) */
-        if (orc_gpt_sampling_processors(last_logits, VOCAB, input_tokens, res->n_input, temperature, top_k, top_p,
+        /* the history: the caller's prefix, or else the start token; then
+         * every prediction so far (the loop stops at the first stop token, so
+         * these are input tokens 1..) */
+        const uint32_t* hist = input_tokens;
+        uint32_t n_hist = res->n_input;
+        if (n_history_prefix) {
+            for (uint32_t i = 1; i < res->n_input; ++i) history[n_history_prefix + i - 1] = input_tokens[i];
+            hist = history;
+            n_hist = n_history_prefix + res->n_input - 1;
+        }
+        if (orc_gpt_sampling_processors(last_logits, VOCAB, hist, n_hist, temperature, top_k, top_p,
                                         repetition_penalty, last_processed) != 0) { rc = -1; break; }
         const uint32_t next = orc_gpt_sample_token(last_processed, VOCAB, &rng);
         predicted[res->n_predicted++] = next;
@@ -657,6 +670,6 @@ int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tok
         }
         input_tokens[res->n_input++] = next;
     }
-    free(ck); free(cv); free(hid); free(nxt); free(qkv);
+    free(ck); free(cv); free(hid); free(nxt); free(qkv); free(history);
     return rc;
 }

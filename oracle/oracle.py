@@ -113,8 +113,8 @@ def lib() -> ctypes.CDLL:
                                           ctypes.POINTER(_GreedyResult)]),
             "orc_gpt_sampling_processors": (i32, [_f32p, u32, _u32p, u32, f32, u32, f32, f32, _f32p]),
             "orc_gpt_sample_token": (u32, [_f32p, u32, ctypes.POINTER(u64)]),
-            "orc_gpt_kv_sample": (i32, [vp, _f32p, u32, u32, i32, u64, f32, u32, f32, f32, _u32p, _u32p,
-                                        _f32p, _f32p, ctypes.POINTER(_GreedyResult)]),
+            "orc_gpt_kv_sample": (i32, [vp, _f32p, u32, u32, i32, u64, f32, u32, f32, f32, _u32p, u32, _u32p,
+                                        _u32p, _f32p, _f32p, ctypes.POINTER(_GreedyResult)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -694,9 +694,11 @@ class GPT:
         return self._greedy(lib().orc_gpt_kv_greedy, prefix, steps, 1 if hf_generate_positions else 0)
 
     def kv_sample(self, prefix, steps, seed, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0,
-                  hf_generate_positions=False):
+                  hf_generate_positions=False, history=None):
         """The sampled cached loop (gpt.cpp:2221-2240); also returns
-        last_processed_logits."""
+        last_processed_logits.  history: repetition_history_prefix (None: the
+        start token)."""
+        hist = np.ascontiguousarray(np.asarray(history if history is not None else [], np.uint32))
         x = f32(prefix).reshape(-1, GPT_W)
         pred = np.zeros(max(steps, 1), np.uint32)
         inp = np.zeros(steps + 1, np.uint32)
@@ -704,7 +706,8 @@ class GPT:
         lp = np.zeros(GPT_VOCAB, np.float32)
         r = _GreedyResult()
         rc = lib().orc_gpt_kv_sample(self._h, P(x), x.shape[0], steps, 1 if hf_generate_positions else 0, seed,
-                                     temperature, top_k, top_p, repetition_penalty, PU(pred), PU(inp), P(lg),
+                                     temperature, top_k, top_p, repetition_penalty,
+                                     PU(hist) if hist.size else None, hist.size, PU(pred), PU(inp), P(lg),
                                      P(lp), ctypes.byref(r))
         if rc != 0:
             raise ValueError("GPT oracle: invalid sampling setting or position beyond the table")

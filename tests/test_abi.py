@@ -105,8 +105,8 @@ def test_gpt_entry_points_reject_a_null_context(mit2):
     assert L.mit2cfm_gpt_layers(None, pu) == mit2.E_ARG
     assert L.mit2cfm_gpt_kv_greedy(None, None, 0, 1, 0, pu, pu, pu, pu, ctypes.byref(i), pf, None) == mit2.E_ARG
     cfg = mit2._GptSampling(1, 0.8, 30, 0.8, 10.0)
-    assert L.mit2cfm_gpt_kv_sample(None, None, 0, 1, 0, ctypes.byref(cfg), pu, pu, pu, pu, ctypes.byref(i), pf, pf,
-                                   None) == mit2.E_ARG
+    assert L.mit2cfm_gpt_kv_sample(None, None, 0, 1, 0, ctypes.byref(cfg), None, 0, pu, pu, pu, pu, ctypes.byref(i),
+                                   pf, pf, None) == mit2.E_ARG
     assert L.mit2cfm_gpt_cached_decode(None, pf, 0, pf, pf, pf, pu) == mit2.E_ARG
     assert L.mit2cfm_gpt_profile_launch(None, 0, 0, None, None) == mit2.E_ARG
 

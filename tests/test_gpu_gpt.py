@@ -8,9 +8,13 @@ gpt.cpp:2305-2371), and to 2e-3 on the cached single-row decode
 sides (the checkpoint's precision) and everything else fp32, so the only
 difference is the order of fp32 sums; the bars below are the reference's.
 
-The attention walks its keys in chunks of 512 with an online softmax, so
-prefixes of a few rows, of about 512 and of 600 exercise one chunk, the chunk
-boundary and the rescaling across chunks; prefill chunks hold 8 rows.
+The cached attention splits its keys into blocks of 256 (the GPT_ATTN_KEYS
+build knob): each split writes its max, exp-sum and unnormalised output, and
+a combine launch merges the splits eight at a time, rescaling the running
+sums when a later group raises the max.  Prefixes of a few rows, of 509 / 511
+(a split boundary), 600 (three splits), 2,100 (nine splits: the combine's
+second pass) and 2,303 (the cache ends exactly on a split boundary) exercise
+one split, the boundary and the rescaling; prefill chunks hold 8 rows.
 """
 from __future__ import annotations
 
@@ -107,7 +111,8 @@ def test_kv_greedy_matches_oracle_24_layers(ctx24, orc24, P, steps, hf):
     _compare(ctx24.gpt_kv_greedy(prefix, steps, hf), orc24.kv_greedy(prefix, steps, hf), "  24 layers")
 
 
-@pytest.mark.parametrize("P,steps", [(0, 3), (1, 2), (63, 3), (300, 10), (509, 5), (511, 3), (600, 4)])
+@pytest.mark.parametrize("P,steps", [(0, 3), (1, 2), (63, 3), (300, 10), (509, 5), (511, 3), (600, 4),
+                                     (2100, 4), (2303, 2)])
 def test_kv_greedy_attention_chunks(ctx2, orc2, P, steps):
     prefix = _prefix(P, seed=P)
     print(f"kv greedy 2 layers P={P} steps={steps}", flush=True)
@@ -245,6 +250,40 @@ def test_sampled_decode_paths(ctx2, orc2, case):
     _compare_sampled(got, orc2.kv_sample(prefix, 12, 7 + case, **cfg), "  2 layers sampled")
     if cfg["top_k"] == 1:
         assert got["predicted"].tolist() == ctx2.gpt_kv_greedy(prefix, 12)["predicted"].tolist()
+
+
+def test_sampled_decode_with_fake_inputs_history_24_layers(ctx24, orc24):
+    """The synthesis path's sampled call (synthesis_pipeline.cpp:795-802) passes
+    the prefix's fake_inputs, [1] x P + [8192] (gpt.cpp:66-67), as the
+    repetition-history prefix, so token 1 is penalised from the first step;
+    IndexTTS2's settings, tokens and logits against the oracle."""
+    P = 20
+    prefix = _prefix(P, seed=77)
+    hist = [1] * P + [8192]
+    cfg = SAMPLING_CASES[0]
+    got = ctx24.gpt_kv_sample(prefix, 10, 20240609, history=hist, **cfg)
+    ref = orc24.kv_sample(prefix, 10, 20240609, history=hist, **cfg)
+    _compare_sampled(got, ref, "  24 layers sampled, fake_inputs history")
+
+
+def test_history_prefix_penalises_its_tokens(ctx2, orc2):
+    """With no temperature or filtering the processed logits are the raw ones
+    except the history's tokens, scaled by the penalty (divided when positive,
+    multiplied when negative): token 1 from a fake_inputs history; a history of
+    [8192] alone is the default."""
+    prefix = _prefix(12, seed=78)
+    cfg = dict(temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=2.0)
+    with_h = ctx2.gpt_kv_sample(prefix, 1, 5, history=[1] * 12 + [8192], **cfg)
+    without = ctx2.gpt_kv_sample(prefix, 1, 5, **cfg)
+    start_only = ctx2.gpt_kv_sample(prefix, 1, 5, history=[8192], **cfg)
+    raw = with_h["last_logits"]
+    want = raw.copy()
+    for t in (1, 8192):
+        want[t] = raw[t] / 2.0 if raw[t] >= 0 else raw[t] * 2.0
+    assert np.array_equal(with_h["last_processed_logits"], want.astype(np.float32))
+    assert without["last_processed_logits"][1] == raw[1]
+    assert np.array_equal(start_only["last_processed_logits"], without["last_processed_logits"])
+    _compare_sampled(with_h, orc2.kv_sample(prefix, 1, 5, history=[1] * 12 + [8192], **cfg), "  2 layers history")
 
 
 def test_sampling_settings_rejected(ctx2, mit2):

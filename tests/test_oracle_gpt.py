@@ -277,3 +277,25 @@ def test_kv_sample_with_greedy_settings_equals_greedy(gpt):
     s = gpt.kv_sample(prefix, 4, seed=5, top_k=1)
     g = gpt.kv_greedy(prefix, 4)
     assert s["predicted"].tolist() == g["predicted"].tolist()
+
+
+def test_kv_sample_history_prefix(gpt):
+    """repetition_history_prefix (gpt.cpp:2224-2229): a prefix of [8192] alone is
+    the default history; a fake_inputs-shaped prefix ([1] x n + [8192],
+    gpt.cpp:66-67) additionally penalises token 1 from the first step, and
+    nothing else (no temperature or filter: the other scores stay raw)."""
+    prefix = _rows(6, seed=31)
+    cfg = dict(temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=3.0)
+    default = gpt.kv_sample(prefix, 1, 9, **cfg)
+    start = gpt.kv_sample(prefix, 1, 9, history=[8192], **cfg)
+    fake = gpt.kv_sample(prefix, 1, 9, history=[1] * 6 + [8192], **cfg)
+    assert np.array_equal(default["last_processed_logits"], start["last_processed_logits"])
+    raw = fake["last_logits"]
+    want = raw.copy()
+    for t in (1, 8192):
+        want[t] = raw[t] / np.float32(3.0) if raw[t] >= 0 else raw[t] * np.float32(3.0)
+    assert np.array_equal(fake["last_processed_logits"], want)
+    # later steps: the predictions join the prefix in the history
+    long = gpt.kv_sample(prefix, 4, 9, history=[1] * 6 + [8192], **cfg)
+    again = gpt.kv_sample(prefix, 4, 9, history=[1] * 6 + [8192] + [8192], **cfg)
+    assert long["predicted"].tolist() == again["predicted"].tolist()  # duplicates count once
