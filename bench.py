@@ -535,7 +535,7 @@ def main():
     # condition is exactly this decode's T frames.
     codes = condition_codes(T - P)
     cp = None
-    if codes:
+    if codes and a.cond_calls:
         gen = mit2cfm.generated_frames(codes)
         s_infer = mit2cfm.normal_noise(codes, 1024, 6)
         d_s = torch.from_numpy(s_infer).to(dev)

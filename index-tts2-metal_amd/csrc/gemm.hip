@@ -100,26 +100,38 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   __shared__ __attribute__((aligned(1024))) half_t sA1[AS * KG * BM * SK];
   __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? AS * KG * BM * SK : 8];
   __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? AS * KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA4[NST > 4 ? AS * KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA5[NST > 5 ? AS * KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA6[NST > 6 ? AS * KG * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA7[NST > 7 ? AS * KG * BM * SK : 8];
   __shared__ __attribute__((aligned(1024))) half_t sB0[WS * KG * BN * SK];
   __shared__ __attribute__((aligned(1024))) half_t sB1[WS * KG * BN * SK];
   __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? WS * KG * BN * SK : 8];
   __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? WS * KG * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB4[NST > 4 ? WS * KG * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB5[NST > 5 ? WS * KG * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB6[NST > 6 ? WS * KG * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB7[NST > 7 ? WS * KG * BN * SK : 8];
   constexpr int kALo = KG * BM * SK;  // offset of a stage's lo half in its buffer
   constexpr int kWLo = KG * BN * SK;
-  static_assert(NST >= 2 && NST <= 4, "two to four stages");
+  static_assert(NST >= 2 && NST <= 8, "two to eight stages");
   const int kg = threadIdx.x / (64 * NW);  // K group of this wave
   auto bufA = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
     half_t* b;
     if constexpr (s == 0) b = sA0; else if constexpr (s == 1) b = sA1;
-    else if constexpr (s == 2) b = sA2; else b = sA3;
+    else if constexpr (s == 2) b = sA2; else if constexpr (s == 3) b = sA3;
+    else if constexpr (s == 4) b = sA4; else if constexpr (s == 5) b = sA5;
+    else if constexpr (s == 6) b = sA6; else b = sA7;
     return KG == 1 ? b : b + kg * BM * SK;
   };
   auto bufB = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
     half_t* b;
     if constexpr (s == 0) b = sB0; else if constexpr (s == 1) b = sB1;
-    else if constexpr (s == 2) b = sB2; else b = sB3;
+    else if constexpr (s == 2) b = sB2; else if constexpr (s == 3) b = sB3;
+    else if constexpr (s == 4) b = sB4; else if constexpr (s == 5) b = sB5;
+    else if constexpr (s == 6) b = sB6; else b = sB7;
     return KG == 1 ? b : b + kg * BN * SK;
   };
 
@@ -296,10 +308,22 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     }
   };
 
+  // Stage kt >= KT (the ring running past the last stage) keeps the per-stage
+  // load count, which the vmcnt waits rely on, but every lane reads the same
+  // 16 bytes (the first of W) into a buffer that is not read again: one
+  // request per load.  The choice is a mask on the address, hidden from the
+  // optimiser, so it stays a select: a branch here makes the compiler give
+  // up tracking the ring and wait for every load in flight.
   auto issue = [&](auto st, int kt) {
     half_t* sa = bufA(st);
     half_t* sb = bufB(st);
-    const int k0 = (kt_lo + kt) * SK;
+    const int k0 = ((kt < KT ? kt : KT - 1) + kt_lo) * SK;
+    uint64_t keep = kt < KT ? ~0ull : 0ull;
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("" : "+v"(keep));
+#endif
+    const uint64_t dummy = (uint64_t)(uintptr_t)p.W & ~keep;
+#define MIT2_PICK(real) ((const void*)(uintptr_t)(((uint64_t)(uintptr_t)(real) & keep) | dummy))
 #pragma unroll
     for (int j = 0; j < LA; ++j) {
       const int q0 = (wave * LA + j) * 64;
@@ -308,10 +332,10 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       const int c = (q % CPR) ^ swz(row);
       int m = m0 + row;
       if (m > p.M - 1) m = p.M - 1;  // rows past M load a valid row; never stored
-      __builtin_amdgcn_global_load_lds((const void*)a_src(j, m, k0, c * 8, false),
-                                       (lds_void_t*)(sa + q0 * 8), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(MIT2_PICK(a_src(j, m, k0, c * 8, false)), (lds_void_t*)(sa + q0 * 8),
+                                       16, 0, 0);
       if constexpr (AS == 2)
-        __builtin_amdgcn_global_load_lds((const void*)a_src(j, m, k0, c * 8, true),
+        __builtin_amdgcn_global_load_lds(MIT2_PICK(a_src(j, m, k0, c * 8, true)),
                                          (lds_void_t*)(sa + kALo + q0 * 8), 16, 0, 0);
     }
 #pragma unroll
@@ -321,10 +345,10 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       const int row = q / CPR;
       const int c = (q % CPR) ^ swz(row);
       const half_t* wsrc = p.W + (size_t)(n0 + row) * p.ldw + k0 + c * 8;
-      __builtin_amdgcn_global_load_lds((const void*)wsrc, (lds_void_t*)(sb + q0 * 8), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(MIT2_PICK(wsrc), (lds_void_t*)(sb + q0 * 8), 16, 0, 0);
       if constexpr (WS == 2)
-        __builtin_amdgcn_global_load_lds((const void*)(wsrc + p.w_lo), (lds_void_t*)(sb + kWLo + q0 * 8),
-                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(MIT2_PICK(wsrc + p.w_lo), (lds_void_t*)(sb + kWLo + q0 * 8), 16, 0, 0);
+#undef MIT2_PICK
     }
   };
 
@@ -395,10 +419,10 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   // the barrier then says every wave's share has landed AND every wave has
   // finished reading stage kt-1, whose buffer is refilled with stage
   // kt+NST-1 before stage kt is computed.  The body is branch-free (an issue
-  // past the last stage repeats stage KT-1, an L2 hit, into a buffer that is
-  // not read again), which keeps the compiler from adding waits of its own;
-  // the last KT % NST stages are resident when the loop exits.
-  static_for<0, NST - 1>([&](auto st) { issue(st, min((int)decltype(st)::value, KT - 1)); });
+  // past the last stage is a one-address load into a buffer that is not read
+  // again), which keeps the compiler from adding waits of its own; the last
+  // KT % NST stages are resident when the loop exits.
+  static_for<0, NST - 1>([&](auto st) { issue(st, (int)decltype(st)::value); });
   float rsv[kNormIn ? MI : 1];
   if constexpr (kNormIn) {
     wait_vmcnt<L * (NST - 1)>();  // the partials (issued before the stages) have landed
@@ -418,7 +442,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       wait_vmcnt<L * (NST - 2)>();   // this wave's share of stage kt0+s has landed
       wait_lgkmcnt0();               // this wave's reads of stage kt0+s-1 have returned
       __builtin_amdgcn_s_barrier();  // ... for every wave
-      issue(std::integral_constant<int, (s + NST - 1) % NST>{}, min(kt0 + s + NST - 1, KT - 1));
+      issue(std::integral_constant<int, (s + NST - 1) % NST>{}, kt0 + s + NST - 1);
       compute(st);
     });
   }

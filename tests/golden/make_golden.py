@@ -13,11 +13,14 @@ Configs (benchmark workloads):
   config1  one estimator forward, B=2 CFG pair, T=256 (P=96), t=0.5
   config2  full decode T=860 (P=258), 25 steps, cfg 0.7  (~15 min on 8 threads)
   config3  full decode T=128 (P=48), 12 steps, cfg 0.7
-  config4  T=3000 (P=258): the CFG-pair velocity at two Euler states, t=0 on x0
-           and step 12 of 25 on a blend of x0 and a mel-like state (~6 min on 8 threads)
+  config4  T=3000 (P=258): the CFG-pair velocity at three Euler states, t=0 on x0
+           and steps 12 and 24 of 25 on blends of x0 and a mel-like state (~9 min on
+           8 threads)
   config5  8 requests, P=258, target lengths U{300..1500} from one seed, right-padded
            (B=16 rows): the masked CFG-pair velocity at t=0 of the shortest and the
            longest request at the padded length (~4 min on 8 threads)
+  config5t the same batch decoded for 2 Euler steps: the shortest request's final mel
+           from the masked oracle decode at the padded length (~2 min on 8 threads)
 """
 from __future__ import annotations
 
@@ -44,9 +47,12 @@ CONFIGS = {
     "config1": dict(kind="forward", T=256, P=96, t=0.5, seed=1),
     "config2": dict(kind="decode", T=860, P=258, steps=25, cfg=0.7, seed=1, keep_steps=[0, 12, 24]),
     "config3": dict(kind="decode", T=128, P=48, steps=12, cfg=0.7, seed=1, keep_steps=[0, 11]),
-    "config4": dict(kind="states", T=3000, P=258, steps=25, cfg=0.7, seed=1, mid_step=12),
+    "config4": dict(kind="states", T=3000, P=258, steps=25, cfg=0.7, seed=1, mid_step=12,
+                    late_step=24),
     "config5": dict(kind="padded", nreq=8, P=258, lo=300, hi=1500, len_seed=5, steps=16, cfg=0.7,
                     seed=100),
+    "config5t": dict(kind="padded_decode", nreq=8, P=258, lo=300, hi=1500, len_seed=5, steps=2,
+                     cfg=0.7, seed=100),
 }
 
 
@@ -155,6 +161,9 @@ def make(name: str, model, digest: str) -> None:
         tm = step_time(c["mid_step"], c["steps"])
         out["v_mid"] = pair_velocity(model, mid_state(x0, T, P, c["seed"], tm), prompt, cond, style,
                                      T, P, tm, c["cfg"], mask)
+        tl = step_time(c["late_step"], c["steps"])
+        out["v_late"] = pair_velocity(model, mid_state(x0, T, P, c["seed"], tl), prompt, cond, style,
+                                      T, P, tl, c["cfg"], mask)
     elif c["kind"] == "padded":
         toks, tmax, X0, PR, CO, ST = padded_requests(c)
         picks = [int(np.argmin(toks)), int(np.argmax(toks))]
@@ -165,6 +174,13 @@ def make(name: str, model, digest: str) -> None:
             v = pair_velocity(model, x, PR[r], CO[r], ST[r], tmax, c["P"], 0.0, c["cfg"], mask)
             out[f"v_t0_req{r}"] = v[:toks[r]]
         c = dict(c, tokens=toks, t_max=tmax, picked=picks)
+    elif c["kind"] == "padded_decode":
+        toks, tmax, X0, PR, CO, ST = padded_requests(c)
+        r = int(np.argmin(toks))
+        mask = (np.arange(tmax) < toks[r]).astype(np.uint32)
+        final = model.cfm_euler_masked(X0[r], PR[r][:c["P"]], CO[r], ST[r], mask, c["steps"], c["cfg"])
+        out[f"final_req{r}"] = final[:toks[r]]
+        c = dict(c, tokens=toks, t_max=tmax, picked=[r])
     else:
         final, xt, vt = model.cfm_euler(x0, prompt, cond, style, c["steps"], c["cfg"], trace=True)
         out["final"] = final

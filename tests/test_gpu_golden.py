@@ -4,6 +4,9 @@ fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
   config1  one estimator forward of the CFG pair, T=256, P=96, t=0.5
   config2  full decode T=860 (P=258), 25 steps, cfg 0.7 -- the headline decode
   config3  full decode T=128 (P=48), 12 steps, cfg 0.7
+  config4  T=3000 (P=258): CFG-pair velocity at three Euler states
+  config5  8 right-padded requests (B=16 rows): masked velocity at t=0, and
+           (config5t) the shortest request after a 2-step batched decode
 
 Inputs and synthetic weights are regenerated from the seeds stored beside each
 fixture (splitmix64 + Box-Muller, bit-exact on any host); the weights digest
@@ -147,18 +150,20 @@ def _make_golden():
 
 
 def test_config4_long_form_velocity(mit2, orc, golden_ctx):
-    """T=3000 (P=258): the CFG-pair velocity at t=0 on x0 and at step 12 of 25
-    on a mid-flow state, against the oracle (Tpad > 2048 takes the one-group
-    attention path)."""
+    """T=3000 (P=258): the CFG-pair velocity at t=0 on x0 and at steps 12 and 24
+    of 25 on flow states blended towards a mel-like field, against the oracle
+    (Tpad > 2048 takes the 32-query attention path)."""
     mg = _make_golden()
     meta, ref = load("config4")
     T, P, steps, cfg = meta["T"], meta["P"], meta["steps"], meta["cfg"]
     x0, prompt, cond, style = inputs(mit2, T, P, meta["seed"])
     mask = np.ones((2, T), np.uint32)
     tm = step_time(meta["mid_step"], steps)
+    tl = step_time(meta["late_step"], steps)
     x = x0.copy()
     x[:P] = 0
-    for key, state, t in (("v_t0", x, 0.0), ("v_mid", mg.mid_state(x0, T, P, meta["seed"], tm), tm)):
+    for key, state, t in (("v_t0", x, 0.0), ("v_mid", mg.mid_state(x0, T, P, meta["seed"], tm), tm),
+                          ("v_late", mg.mid_state(x0, T, P, meta["seed"], tl), tl)):
         X, PX, C, S = branches(state, prompt, cond, style, T, P)
         d = golden_ctx.estimator_step(X, PX, C, S, mask, t)
         v = np.float32(1 + cfg) * d[0] - np.float32(cfg) * d[1]
@@ -213,6 +218,23 @@ def test_config5_padded_batch_velocity(mit2, orc, golden_ctx):
         err = orc.rel_l2(v[:toks[r]], ref[f"v_t0_req{r}"])
         print(f"config5 request {r} (T={toks[r]}): velocity rel-L2 {err:.3e}", flush=True)
         assert err <= VEL_TOL
+
+
+def test_config5_padded_batch_trajectory(mit2, orc, golden_ctx):
+    """The 8-request right-padded batch (B=16 rows, T_max=1348) decoded for 2
+    Euler steps: the shortest request's final mel against the oracle's masked
+    decode of that request at the padded length."""
+    mg = _make_golden()
+    meta, ref = load("config5t")
+    toks, tmax, X0, PR, CO, ST = mg.padded_requests(dict(meta))
+    assert toks == meta["tokens"] and tmax == meta["t_max"]
+    P, steps, cfg = meta["P"], meta["steps"], meta["cfg"]
+    out = golden_ctx.decode_batched(toks, [P] * len(toks), X0, PR, CO, ST, steps, cfg)
+    for r in meta["picked"]:
+        err = orc.rel_l2(out[r, :toks[r]], ref[f"final_req{r}"])
+        print(f"config5t request {r} (T={toks[r]}, {steps} steps): final mel rel-L2 {err:.3e}", flush=True)
+        assert err <= MEL_TOL
+        assert np.all(out[r, :P] == 0)
 
 
 def test_config5_padded_batch_decode(mit2, golden_ctx):
