@@ -232,17 +232,15 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
     }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      float tmax = fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3]));
+      float lmax = fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3]));
 #pragma unroll
       for (int kb = 1; kb < 4; ++kb)
-        tmax = fmaxf(tmax, fmaxf(fmaxf(sc[kb][qb][0], sc[kb][qb][1]), fmaxf(sc[kb][qb][2], sc[kb][qb][3])));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-      // Lazy max: move m only when this tile's max exceeds it by > kLazyMax
-      // (from -inf: as soon as any key is valid).
+        lmax = fmaxf(lmax, fmaxf(fmaxf(sc[kb][qb][0], sc[kb][qb][1]), fmaxf(sc[kb][qb][2], sc[kb][qb][3])));
       const float m_old = m_run[qb];
-      const bool need = tmax > m_old + kLazyMax;
-      if (__any(need)) {
+      if (__any(lmax > m_old + kLazyMax)) {
+        float tmax = fmaxf(lmax, __shfl_xor(lmax, 16, kWave));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        const bool need = tmax > m_old + kLazyMax;
         const float m_new = need ? tmax : m_old;
         const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);  // -inf -> 0; unchanged -> 1
 #pragma unroll

@@ -837,8 +837,19 @@ static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
 //    tiles to cover the CUs.  The long-K ones (K >= 1024) add a second
 //    group of four wavefronts that takes half of the K stages, and so does
 //    the k=5 conv (a second group of eight).
-// The choice depends on N and K only, never on M, so a request's result
+// The K split depends on N and K only, never on M, so a request's result
 // does not depend on the batch it is decoded with.
+//
+// Whether a BM x BN tiling leaves most CUs idle: then 32-row tiles with the
+// same K split spread the product over more CUs (the per-CU operand rate,
+// not the total, limits these K loops).  At M = 256 (a T = 128 CFG pair):
+// the k=5 conv 10.5 vs 15.5 us, w1|w3 5.2 vs 8.7, w2 5.9 vs 7.0.  Only the
+// tile shape changes, never the K split or the order of the MFMAs over K, so
+// a row's result is the same bits whichever tiling the batch gets.
+static bool few_tiles(const GemmArgs& a, int BM, int BN) {
+  return (long)((a.M + BM - 1) / BM) * (a.N / BN) < 128;
+}
+
 template <int AM, int EPI>
 static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
   if constexpr (AM == A_CONVP) {
@@ -850,21 +861,34 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
     return hipErrorInvalidValue;
   }
   if constexpr (EPI == EPI_SWIGLU) {
-    if (a.N % 192 == 0) return launch_tile<128, 192, 64, 3, AM, EPI, 4, 2>(a, s);
+    if (a.N % 192 == 0) {
+      if (few_tiles(a, 128, 192) && a.N % 128 == 0) return launch_tile<32, 128, 64, 3, AM, EPI, 2, 2>(a, s);
+      return launch_tile<128, 192, 64, 3, AM, EPI, 4, 2>(a, s);
+    }
   }
   if constexpr (AM == A_CONV5) {
     // Two K groups (16 wavefronts, the partial tile reduced through the idle
     // ring): 17.1 vs 18.3 us.
-    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 2>(a, s);
+    if (a.N % 128 == 0) {
+      if (few_tiles(a, 64, 128)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
+      return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 2>(a, s);
+    }
   }
   if constexpr (EPI == EPI_RESSKIP || EPI == EPI_DUAL) {
-    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
+    if (a.N % 128 == 0) {
+      if (few_tiles(a, 64, 128)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2>(a, s);
+      return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
+    }
   }
   if constexpr (EPI == EPI_F32) {
     // Long-K N = 512 products (w2 K = 1536, skip-in K = 1024) split K over
     // two wave groups: 9.4 vs 9.8 us and 7.25 vs 7.7 us.
-    if (a.K >= 1024 && (a.K / 64) % 2 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
+    if (a.K >= 1024 && (a.K / 64) % 2 == 0) {
+      if (few_tiles(a, 64, 64)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
+      return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
+    }
   }
+  if (few_tiles(a, 64, 64)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2>(a, s);
   return launch_tile<64, 64, 64, 3, AM, EPI>(a, s);
 }
 

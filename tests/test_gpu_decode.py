@@ -236,6 +236,27 @@ def test_batched_requests_match_oracle(mit2, orc, model_unit, ctx_unit):
         assert np.array_equal(single[0], got[r])
 
 
+def test_row_tiling_does_not_change_results(mit2, ctx):
+    """A short request alone (B=2, M=256 rows: the GEMMs take 32-row tiles)
+    and the same request in a batch of eight (M=2048: the wide tiles) give the
+    same mel bit for bit -- the tile shape follows M, the K split does not."""
+    T, P, steps, cfg = 128, 48, 4, 0.7
+    n = 8
+    reqs = [inputs(mit2, T, P, seed=500 + 10 * r) for r in range(n)]
+    X0 = np.stack([q[0] for q in reqs])
+    PR = np.zeros((n, T, 80), np.float32)
+    for r in range(n):
+        PR[r, :P] = reqs[r][1]
+    CO = np.stack([q[2] for q in reqs])
+    ST = np.stack([q[3] for q in reqs])
+    batch = ctx.decode_batched([T] * n, [P] * n, X0, PR, CO, ST, steps, cfg)
+    for r in (0, 5):
+        alone = ctx.decode(X0[r], reqs[r][1], CO[r], ST[r], steps, cfg)
+        diff = np.abs(alone - batch[r])
+        print(f"request {r}: max |alone - batched| {diff.max():.3e}", flush=True)
+        assert np.array_equal(alone, batch[r])
+
+
 def test_single_token_decode_is_finite(mit2, ctx):
     """T=1: the reference CPU reflect pad never terminates for one token;
     the HIP path follows the reference GPU kernel (reflect index 0)."""
