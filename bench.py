@@ -596,7 +596,7 @@ def main():
         ctx.set_precision("vocoder", "f32")
         vflops = mit2cfm.bigvgan_flops(T)
         voc = {"workload": f"BigVGAN v2 256x, {T} mel frames -> {256 * T} samples",
-               "precision": "f32 (split f16 operand pairs: three matrix-core products per term)",
+               "precision": "f32 (split f16 activation pairs; weight-norm directions exact in f16 with the g/|v| scale in the epilogue: two matrix-core products per term, three for the transposed convs)",
                "ms_per_call": round(v_ms, 3), "samples_per_s": round(256 * T / (v_ms / 1e3), 1),
                "algorithmic_tflop": round(vflops / 1e12, 4),
                "tflops": round(vflops / (v_ms / 1e3) / 1e12, 1),

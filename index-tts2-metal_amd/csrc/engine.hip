@@ -236,7 +236,7 @@ void visit_weights(Weights& W, F&& f) {
 // arena bytes), then each flagged section as u64 length + bytes
 // (Vocoder::append_image, GptDecoder::append_image).
 constexpr char kImageMagic[8] = {'M', 'I', 'T', '2', 'H', 'I', 'P', 'I'};
-constexpr uint32_t kImageVersion = 3;
+constexpr uint32_t kImageVersion = 4;
 constexpr uint32_t kImageVocoder = 1, kImageGpt = 2;  // section flags
 
 struct HostModel {

@@ -109,6 +109,12 @@ struct GemmArgs {
   size_t a_lo = 0;
   size_t w_lo = 0;
   size_t c16_lo = 0;
+
+  // EPI_F32 / EPI_F16 / EPI_RESAVG: when set, the product of column n is
+  // multiplied by colscale[n] (N floats) before the bias is added -- a
+  // weight-normed conv stored as its direction v (exact in f16) with the
+  // per-output-channel g / ||v|| applied here.
+  const float* colscale = nullptr;
 };
 
 // Scale of the lo half of a split operand (2^11: lo then has the magnitude

@@ -454,6 +454,14 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   for (int j = 0; j < NI; ++j)
     bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + col_base + 16 * j)
                    : make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr bool kColScale = EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_RESAVG;
+  float4 csv[kColScale ? NI : 1];
+  if constexpr (kColScale) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      csv[j] = p.colscale ? *reinterpret_cast<const float4*>(p.colscale + col_base + 16 * j)
+                          : make_float4(1.f, 1.f, 1.f, 1.f);
+  }
   constexpr bool kNormOut = EPI == EPI_F32;
   float4 nsc[kNormOut ? NI : 1];  // producer of a folded norm: aw * gamma per column
   if constexpr (kNormOut) {
@@ -520,6 +528,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j) acc[i][j] += red[((wave * MI + i) * NI + j) * 64 + lane];
+    }
+  }
+
+  if constexpr (kColScale) {
+    if (p.colscale) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] *= floatx4{csv[j].x, csv[j].y, csv[j].z, csv[j].w};
     }
   }
 

@@ -7,10 +7,13 @@
 //
 // Differences in HOW, not WHAT:
 //  * convs are implicit GEMMs on the matrix cores with fp32 accumulation;
-//    weights are weight-normed once at create and laid out tap-major
-//    [out][tap * in + ic].  The reference runs the vocoder in fp32, so by
-//    default every operand is a split f16 pair (hi, lo: GemmArgs::split),
-//    which gives fp32-level products; an f16 mode uses the hi halves alone;
+//    weights are laid out tap-major [out][tap * in + ic].  The reference runs
+//    the vocoder in fp32, so by default every activation operand is a split
+//    f16 pair (hi, lo: GemmArgs::split), which gives fp32-level products.  A
+//    conv whose weight norm is per output channel keeps its direction v
+//    (exact in f16) and applies g / ||v|| to its outputs (GemmArgs::colscale);
+//    the transposed convs, normed per input channel, keep the weight-normed
+//    weight as a split pair.  An f16 mode uses the hi halves alone;
 //  * a transposed conv with stride s, kernel 2s and padding s/2 is a k = 3
 //    conv over the input (taps q-1, q, q+1) whose s * out output columns are
 //    the s phases of the upsampled signal: output row q, column r * out + oc
@@ -218,8 +221,14 @@ std::vector<float> wnorm(const std::vector<float>& g, const std::vector<float>& 
 
 // ---------------------------------------------------------------- weights
 struct Vocoder::Conv {
-  half_t* w = nullptr;  // [N][K] f16 hi halves, tap-major, zero-padded; lo halves follow ([N][K])
-  float* b = nullptr;   // [N]
+  // [N][K] f16, tap-major, zero-padded.  Without `scale`: the weight-normed
+  // weight as split pairs (hi halves, then the lo halves, [N][K] each).  With
+  // `scale`: the direction v itself, exact in f16, one copy, and the product
+  // of output channel n is multiplied by scale[n] = g / ||v|| in the GEMM
+  // epilogue.
+  half_t* w = nullptr;
+  float* b = nullptr;      // [N]
+  float* scale = nullptr;  // [N] or null
   int N = 0, n_out = 0, K = 0, cin = 0, k = 0;
 };
 
@@ -261,17 +270,45 @@ struct Vocoder::Impl {
     VOC_OK(hipMemcpy(d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
   }
 
-  // Zero-padded conv (weight_v [out][in][k], weight_g [out]).
+  // One f16 copy of values that are exact in f16.
+  void upload_exact(half_t*& d, const std::vector<float>& v) {
+    std::vector<_Float16> h(v.size());
+    for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
+    d = static_cast<half_t*>(wa.take(h.size() * 2));
+    VOC_OK(hipMemcpy(d, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+  }
+
+  // Zero-padded conv (weight_v [out][in][k], weight_g [out]).  Weight norm is
+  // per output channel, w = (g / ||v||) v, so when v is exact in f16 (the
+  // checkpoint's values are) the conv keeps v and applies g / ||v|| to its
+  // outputs: fp32-level products need A split only (two matrix-core
+  // products per term instead of three) and the weight bytes halve.
   void make_conv(Conv& c, const std::unordered_map<std::string, std::vector<float>>& t,
                  const std::string& prefix, int cout, int cin, int k, bool bias) {
-    const auto w = wnorm(get(t, prefix + ".weight_g", cout), get(t, prefix + ".weight_v", (size_t)cout * cin * k),
-                         cout, (size_t)cin * k);
+    const auto& g = get(t, prefix + ".weight_g", cout);
+    const auto& v = get(t, prefix + ".weight_v", (size_t)cout * cin * k);
+    bool exact = true;
+    for (float x : v)
+      if ((float)(_Float16)x != x) {
+        exact = false;
+        break;
+      }
     c.n_out = cout;
     c.N = round_up(cout, 32);
     c.K = round_up(k * cin, 64);
     c.cin = cin;
     c.k = k;
-    std::vector<float> wt((size_t)c.N * c.K, 0.f), bt(c.N, 0.f);
+    std::vector<float> wt((size_t)c.N * c.K, 0.f), bt(c.N, 0.f), st(c.N, 0.f);
+    if (exact) {
+      // ||v|| of each output row in the order wnorm sums it.
+      for (int oc = 0; oc < cout; ++oc) {
+        float n = 0.f;
+        const float* vr = v.data() + (size_t)oc * cin * k;
+        for (size_t i = 0; i < (size_t)cin * k; ++i) n += vr[i] * vr[i];
+        st[oc] = g[oc] / std::sqrt(n);
+      }
+    }
+    const std::vector<float> w = exact ? v : wnorm(g, v, cout, (size_t)cin * k);
     for (int oc = 0; oc < cout; ++oc)
       for (int ic = 0; ic < cin; ++ic)
         for (int tap = 0; tap < k; ++tap)
@@ -280,7 +317,12 @@ struct Vocoder::Impl {
       const auto& b = get(t, prefix + ".bias", cout);
       for (int oc = 0; oc < cout; ++oc) bt[oc] = b[oc];
     }
-    upload_f16(c.w, wt);
+    if (exact) {
+      upload_exact(c.w, wt);
+      upload_f32(c.scale, st);
+    } else {
+      upload_f16(c.w, wt);
+    }
     upload_f32(c.b, bt);
   }
 
@@ -364,11 +406,12 @@ struct Vocoder::Impl {
             const float* res, float* C32b, half_t* C16, size_t c16_lo, int flag) {
     GemmArgs g;
     if (f32) {
-      g.split = 2;
+      g.split = c.scale ? 1 : 2;  // A split; W split too unless it holds v exactly
       g.a_lo = a_lo;
-      g.w_lo = (size_t)c.N * c.K;
+      g.w_lo = c.scale ? 0 : (size_t)c.N * c.K;
       g.c16_lo = C16 ? c16_lo : 0;
     }
+    g.colscale = c.scale;
     g.M = T;
     g.N = c.N;
     g.K = c.K;
@@ -501,8 +544,9 @@ Vocoder::Vocoder(const std::unordered_map<std::string, std::vector<float>>& t, h
   }
 }
 
-// Image section: arena bytes used, then every conv (weight and bias offsets,
-// N, stored columns, K, input channels, taps) and activation (filters,
+// Image section: arena bytes used, then every conv (weight, bias and output
+// scale offsets -- ~0 when the weight is a split pair --, N, stored columns,
+// K, input channels, taps) and activation (filters,
 // alpha and 1/beta offsets, channels) in construction order, conv_post and
 // the zero buffer's offsets, then the arena bytes.
 namespace {
@@ -525,6 +569,7 @@ void Vocoder::append_image(std::vector<uint8_t>& out) const {
   visit_convs(d.pre, d.ups, d.rb, [&](Conv& c) {
     w.put<uint64_t>(arena_offset(c.w, base));
     w.put<uint64_t>(arena_offset(c.b, base));
+    w.put<uint64_t>(c.scale ? arena_offset(c.scale, base) : ~uint64_t(0));  // ~0: no scale (split weight)
     w.put<int32_t>(c.N);
     w.put<int32_t>(c.n_out);
     w.put<int32_t>(c.K);
@@ -566,7 +611,7 @@ Vocoder::Vocoder(const uint8_t* image, size_t bytes, hipStream_t stream) : d_(ne
       for (int n = 0; n < 6; ++n) shapes.push_back({rb_channels(j), rb_channels(j), kRbKernel[j % 3]});
     size_t ci = 0;
     visit_convs(d.pre, d.ups, d.rb, [&](Conv& c) {
-      const uint64_t wo = r.get<uint64_t>(), bo = r.get<uint64_t>();
+      const uint64_t wo = r.get<uint64_t>(), bo = r.get<uint64_t>(), so = r.get<uint64_t>();
       c.N = r.get<int32_t>();
       c.n_out = r.get<int32_t>();
       c.K = r.get<int32_t>();
@@ -576,8 +621,10 @@ Vocoder::Vocoder(const uint8_t* image, size_t bytes, hipStream_t stream) : d_(ne
       if (c.n_out != e[0] || c.cin != e[1] || c.k != e[2] || c.N != round_up(e[0], 32) ||
           c.K != round_up(e[2] * e[1], 64))
         throw std::runtime_error("device image: vocoder conv shape differs from the model");
-      c.w = arena_span<half_t>(wo, (size_t)2 * c.N * c.K, base, used);  // split pairs
+      // split pairs, or v alone with its output scale
+      c.w = arena_span<half_t>(wo, (size_t)(so == ~uint64_t(0) ? 2 : 1) * c.N * c.K, base, used);
       c.b = arena_span<float>(bo, (size_t)c.N, base, used);
+      c.scale = so == ~uint64_t(0) ? nullptr : arena_span<float>(so, (size_t)c.N, base, used);
     });
     auto get_act = [&](Act& a, int C) {
       a.filt = r.get<ActFilters>();
