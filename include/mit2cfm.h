@@ -156,8 +156,9 @@ mit2cfm_status mit2cfm_decode_graph_count(mit2cfm_ctx* ctx, uint32_t* count, uin
  * BigVGAN vocoder (kernels.metal:1607-1749, dit_cfm_bigvgan.cpp:4102-4223;
  * bar max-abs 1e-3, :4469-4490) in fp32.  MIT2CFM_PREC_F32 (the default)
  * runs their GEMMs on split f16 operand pairs (hi = f16(v), lo = the
- * rounding remainder, three matrix-core products per term), which gives
- * fp32-level results; MIT2CFM_PREC_F16 runs them on plain f16 operands
+ * rounding remainder; three matrix-core products per term, two where the
+ * weight is exact in f16), which gives fp32-level results;
+ * MIT2CFM_PREC_F16 runs them on plain f16 operands
  * (faster, about 1e-3 relative).  The DiT-CFM decoder itself always uses f16
  * operands, as the reference's Metal decoder does.  A stage the context has
  * no tensors for is MIT2CFM_E_MODEL.  No reference counterpart. */
