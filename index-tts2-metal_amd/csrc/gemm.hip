@@ -281,15 +281,19 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     } else if constexpr (AM == A_CONCAT) {
       return k < p.K1 ? p.A + lo_off + (size_t)m * p.lda + k
                       : p.A2 + lo_off + (size_t)m * p.lda2 + (k - p.K1);
-    } else if constexpr (AM == A_CONV5) {
+    } else if constexpr (AM == A_CONV5 || AM == A_CONV3Z) {
+      // The row offset is chosen by value selects on the wave-uniform tap: a
+      // select of the members' addresses would put conv_rows in scratch
+      // memory, and its loads would wait for the ring's DMA (one counter).
       const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);  // stage start: uniform
-      const ConvRows& cr = conv_rows[j];
-      const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : tap == 2 ? cr.r2 : tap == 3 ? cr.r3 : cr.r4;
-      return p.A + lo_off + ro + (k - tap * kConvC);
-    } else if constexpr (AM == A_CONV3Z) {
-      const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);
-      const ConvRows& cr = conv_rows[j];
-      const int ro = tap == 0 ? cr.r0 : tap == 1 ? cr.r1 : cr.r2;
+      const ConvRows cr = conv_rows[j];
+      int ro = cr.r0;
+      ro = tap == 1 ? cr.r1 : ro;
+      ro = tap == 2 ? cr.r2 : ro;
+      if constexpr (AM == A_CONV5) {
+        ro = tap == 3 ? cr.r3 : ro;
+        ro = tap == 4 ? cr.r4 : ro;
+      }
       return p.A + lo_off + ro + (k - tap * kConvC);
     } else {
       // tap = k / conv_c through a float reciprocal, corrected by one either way
