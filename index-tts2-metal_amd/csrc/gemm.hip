@@ -369,24 +369,37 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       for (int j = 0; j < NI; ++j) accx[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Fragment reads.  Every fragment row of this lane has the same swizzle
+  // (rows differ by multiples of 16), so a read's address is the stage
+  // buffer plus one per-(operand, kk) lane offset plus a constant.  The lane
+  // offsets (K group region included) are opaque to the optimizer: it would
+  // otherwise split each sum into a chain of one-term address steps, and the
+  // LDS lowering gives a load its buffer's alias scope only within a few
+  // steps of the buffer.  A read without a scope may alias every ring buffer,
+  // so the compiler would wait for all DMA in flight before it.
+  int a_lane[SK / 32], b_lane[SK / 32];
+#pragma unroll
+  for (int kk = 0; kk < SK / 32; ++kk) {
+    const int sw = ((kk * 4 + lg) ^ swz(lr)) << 3;
+    a_lane[kk] = (KG == 1 ? 0 : kg * BM * SK) + (wm * WTM + lr) * SK + sw;
+    b_lane[kk] = (KG == 1 ? 0 : kg * BN * SK) + (wn * WTN + lr) * SK + sw;
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__("" : "+v"(a_lane[kk]), "+v"(b_lane[kk]));
+#endif
+  }
   auto compute = [&](auto st) {
-    const half_t* sa = bufA(st);
-    const half_t* sb = bufB(st);
+    const half_t* sa = bufA(st) - (KG == 1 ? 0 : kg * BM * SK);
+    const half_t* sb = bufB(st) - (KG == 1 ? 0 : kg * BN * SK);
 #pragma unroll
     for (int kk = 0; kk < SK / 32; ++kk) {
-      const int c = kk * 4 + lg;
       half8 af[MI];
       half8 bf[NI];
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int row = wm * WTM + i * 16 + lr;
-        af[i] = *reinterpret_cast<const half8*>(sa + row * SK + ((c ^ swz(row)) << 3));
-      }
+      for (int i = 0; i < MI; ++i)
+        af[i] = *reinterpret_cast<const half8*>(sa + a_lane[kk] + i * 16 * SK);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        const int row = wn * WTN + j * 16 + lr;
-        bf[j] = *reinterpret_cast<const half8*>(sb + row * SK + ((c ^ swz(row)) << 3));
-      }
+      for (int j = 0; j < NI; ++j)
+        bf[j] = *reinterpret_cast<const half8*>(sb + b_lane[kk] + j * 16 * SK);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -394,10 +407,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       if constexpr (SP > 0) {
         half8 afl[MI];
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-          const int row = wm * WTM + i * 16 + lr;
-          afl[i] = *reinterpret_cast<const half8*>(sa + kALo + row * SK + ((c ^ swz(row)) << 3));
-        }
+        for (int i = 0; i < MI; ++i)
+          afl[i] = *reinterpret_cast<const half8*>(sa + kALo + a_lane[kk] + i * 16 * SK);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -406,10 +417,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       if constexpr (SP == 2) {
         half8 bfl[NI];
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const int row = wn * WTN + j * 16 + lr;
-          bfl[j] = *reinterpret_cast<const half8*>(sb + kWLo + row * SK + ((c ^ swz(row)) << 3));
-        }
+        for (int j = 0; j < NI; ++j)
+          bfl[j] = *reinterpret_cast<const half8*>(sb + kWLo + b_lane[kk] + j * 16 * SK);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
