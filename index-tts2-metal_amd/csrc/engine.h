@@ -207,7 +207,8 @@ class Engine {
   void enqueue_norm_bias(const TableBufs& tb, int S);
   const TableBufs& decode_tables(int steps);
   void enqueue_layer(int l, int B, int T, const float* tab, const float* nbq, const float* nbw,
-                     float* cur, float* hbuf, const half_t* skip16, half_t* out16);
+                     float* cur, float* hbuf, const half_t* skip16, half_t* out16,
+                     bool skip_in_done = false, const half_t* next_skip16 = nullptr);
   void enqueue_transformer(int B, int T, const float* tab, const float* nbq, const float* nbw);
   void enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw);
   void enqueue_decode(const float* x0, const float* prompt, const float* cond, const float* style,

@@ -22,6 +22,7 @@
 #include <cstring>
 #include <fstream>
 #include <mutex>
+#include <thread>
 #include <type_traits>
 #include <unordered_map>
 
@@ -46,6 +47,8 @@ static const char* kPfx = "s2mel.net.cfm.estimator.";
 constexpr int kTcondPerStep = 36864;  // [13 attn | 13 ffn | final norm] x 1024, final ss 1024, wn cond 8192
 constexpr int kFinalSsOff = 27 * 1024;
 constexpr int kWnCondOff = 28 * 1024;
+// Row pitch of Workspace::hg16: f16(h) (512) | SwiGLU output (1536).
+constexpr int kHgLd = 2048;
 
 // ------------------------------------------------------------------ no-alloc scratch
 // Scratch of the allocation-free condition producer
@@ -142,6 +145,10 @@ struct Weights {
   half_t* w13_w[13];
   half_t* w2_w[13];
   half_t* si_w[13]; float* si_b[13];
+  // Blocks 7..12: skip_in_l([out_{l-1} | skip]) with out_{l-1} = h + w2 . g
+  // (block l-1's FFN output, read by nothing else) as one map over
+  // [f16(h) | g | skip]: [Wsi_x | Wsi_x . W2_{l-1} | Wsi_skip], [512][2560].
+  half_t* fold_w[13];
   half_t* sl_w;  float* sl_b;  // [512][512 + kMelPad]
   // conv1|res_projection . skip_linear as one map (nothing else reads the
   // skip_linear output): [1024][512 + kMelPad] and [1024].
@@ -200,6 +207,7 @@ void visit_weights(Weights& W, F&& f) {
     f(W.w2_w[l], 512 * 1536);
     f(W.si_w[l], 512 * 1024);
     f(W.si_b[l], 512);
+    f(W.fold_w[l], 512 * 2560);
   }
   f(W.sl_w, 512 * (512 + kMelPad));
   f(W.sl_b, 512);
@@ -236,7 +244,7 @@ void visit_weights(Weights& W, F&& f) {
 // arena bytes), then each flagged section as u64 length + bytes
 // (Vocoder::append_image, GptDecoder::append_image).
 constexpr char kImageMagic[8] = {'M', 'I', 'T', '2', 'H', 'I', 'P', 'I'};
-constexpr uint32_t kImageVersion = 4;
+constexpr uint32_t kImageVersion = 5;
 constexpr uint32_t kImageVocoder = 1, kImageGpt = 2;  // section flags
 
 struct HostModel {
@@ -365,6 +373,10 @@ struct Workspace {
   half_t* k;
   half_t* vt;
   half_t* o16;
+  // [R][kHgLd]: columns 0..511 f16(h) (the post-attention stream, written by
+  // the wo GEMM of a block whose w2 is folded into the next skip-in),
+  // columns 512..2047 the SwiGLU output g16 points at.
+  half_t* hg16;
   half_t* g16;
   half_t* ls16;
   float* wn_x;
@@ -498,6 +510,40 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
       W.si_w[l] = nullptr;
       W.si_b[l] = nullptr;
     }
+    W.fold_w[l] = nullptr;
+  }
+  {
+    // Blocks 7..12: skip_in_l([h + W2 g | skip]) = Wsi_x h + (Wsi_x W2) g +
+    // Wsi_skip skip + b (block l-1's w2 has no bias), Wsi_x W2 summed in
+    // double from the fp32 weights and rounded once to f16.  One thread per
+    // block (about 0.4 G multiply-adds each).
+    std::vector<std::vector<float>> fw(13);
+    std::vector<std::thread> th;
+    for (int l = 7; l < 13; ++l) {
+      const auto& si = hm.get(std::string("transformer.layers.") + std::to_string(l) +
+                                  ".skip_in_linear.weight", 512 * 1024);
+      const auto& w2 = hm.get(std::string("transformer.layers.") + std::to_string(l - 1) +
+                                  ".feed_forward.w2.weight", 512 * 1536);
+      fw[l].assign((size_t)512 * 2560, 0.f);
+      th.emplace_back([&si, &w2, out = fw[l].data()] {
+        std::vector<double> row(1536);
+        for (int n = 0; n < 512; ++n) {
+          std::fill(row.begin(), row.end(), 0.0);
+          const float* sn = si.data() + (size_t)n * 1024;
+          for (int j = 0; j < 512; ++j) {
+            const double c = sn[j];
+            const float* wj = w2.data() + (size_t)j * 1536;
+            for (int k = 0; k < 1536; ++k) row[k] += c * wj[k];
+          }
+          float* on = out + (size_t)n * 2560;
+          std::memcpy(on, sn, 512 * sizeof(float));
+          for (int k = 0; k < 1536; ++k) on[512 + k] = (float)row[k];
+          std::memcpy(on + 2048, sn + 512, 512 * sizeof(float));
+        }
+      });
+    }
+    for (auto& t : th) t.join();
+    for (int l = 7; l < 13; ++l) W.fold_w[l] = up.f16(fw[l]);
   }
   {
     const auto& sw = hm.get("skip_linear.weight", 512 * 592);
@@ -711,7 +757,8 @@ Engine::Engine(const std::string& image_path, int device) : device_(device) {
     });
     // Arrays every decode reads must be present; the length regulator's all or none.
     bool ok = W.proj_w && W.wnc_w && W.cp_w && W.mc_w && W.sl_w && W.post_w && W.c2f_w;
-    for (int l = 0; l < 13; ++l) ok = ok && W.qkv_w[l] && W.w13_w[l] && W.w2_w[l] && (l <= 6 || W.si_w[l]);
+    for (int l = 0; l < 13; ++l)
+      ok = ok && W.qkv_w[l] && W.w13_w[l] && W.w2_w[l] && (l <= 6 || (W.si_w[l] && W.fold_w[l]));
     for (int l = 0; l < 8; ++l) ok = ok && W.in_w[l] && W.rs_w[l];
     ok = ok && (!W.has_lr || (W.lr_proj_w && W.lr_out_w && W.lr_conv_w[3] && W.lr_gn_b[3]));
     if (!ok) throw std::runtime_error("device image: missing decoder arrays");
@@ -788,7 +835,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   for (int i = 0; i < 6; ++i) h(r * 512);
   h(r * 512); h(r * 512);
   h((size_t)cRpad * 512); h((size_t)cRpad * 512); h((size_t)cRpad * 512);
-  h(r * 512); h(r * 1536); h(r * 512);
+  h(r * 512); h(r * kHgLd); h(r * 512);
   f(r * 512); h(r * 512); f(r * 512); f(r * 512); h(r * 512); f(r * 512);
   bytes += (r * 4 + 255) / 256 * 256 + ((size_t)cReq * 4 + 255) / 256 * 256;
   f((size_t)cRpad);
@@ -818,7 +865,8 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   ws.k = H((size_t)cRpad * 512);
   ws.vt = H((size_t)cRpad * 512);
   ws.o16 = H(r * 512);
-  ws.g16 = H(r * 1536);
+  ws.hg16 = H(r * kHgLd);
+  ws.g16 = ws.hg16 + 512;
   ws.ls16 = H(r * 512);
   ws.wn_x = F(r * 512);
   ws.wn_x16 = H(r * 512);
@@ -958,9 +1006,14 @@ const TableBufs& Engine::decode_tables(int steps) {
 // hold block l's attention-norm operand when l <= 6 (written by the merge
 // GEMM or block l-1); x16 must hold f16(x) when l > 6.  out16 receives
 // f16(out); for l < 6 the w2 GEMM also leaves block l+1's operand.
+// Within the stack, a block l in 6..11 is followed by block l+1's skip-in,
+// which is linear in out = h + w2 . g: given next_skip16 (block l+1's skip
+// input), the w2 GEMM is replaced by that skip-in over [f16(h) | g | skip]
+// with the folded weight (Weights::fold_w), so cur leaves as block l+1's x
+// with its attention-norm operand, and block l+1 runs with skip_in_done.
 void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* nbq,
                            const float* nbw, float* cur, float* hbuf, const half_t* skip16,
-                           half_t* out16) {
+                           half_t* out16, bool skip_in_done, const half_t* next_skip16) {
   Weights& W = *w_;
   Workspace& ws = *ws_;
   hipStream_t s = stream_;
@@ -971,7 +1024,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.sc_a = tab + norm_id * 1024; g.sc_g = W.gamma[norm_id];
     g.ssq_out = ws.ssq;
   };
-  if (l > 6) {
+  if (l > 6 && !skip_in_done) {
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 1024; g.K1 = 512;
     g.A = ws.x16; g.lda = 512; g.A2 = skip16; g.lda2 = 512;
@@ -993,20 +1046,32 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
     g.W = W.wo_w[l]; g.ldw = 512; g.res = cur; g.ldres = 512;
-    g.C32 = hbuf; g.ldc32 = 512;
+    if (next_skip16) {
+      g.C16 = ws.hg16; g.ldc16 = kHgLd;  // h is read only by the folded skip-in, in f16
+    } else {
+      g.C32 = hbuf; g.ldc32 = 512;
+    }
     norm_out(g, 13 + l);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
   }
   {
     GemmArgs g;
     g.M = R; g.N = 3072; g.K = 512; g.A = ws.n16; g.lda = 512;
-    g.W = W.w13_w[l]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = 1536;
+    g.W = W.w13_w[l]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = kHgLd;
     g.bias = nbw + l * 3072; g.ssq_in = ws.ssq;
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, s));
   }
-  {
+  if (next_skip16) {
     GemmArgs g;
-    g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = 1536;
+    g.M = R; g.N = 512; g.K = 2560; g.K1 = kHgLd;
+    g.A = ws.hg16; g.lda = kHgLd; g.A2 = next_skip16; g.lda2 = 512;
+    g.W = W.fold_w[l + 1]; g.ldw = 2560; g.bias = W.si_b[l + 1];
+    g.C32 = cur; g.ldc32 = 512;
+    norm_out(g, l + 1);
+    HIP_OK(launch_gemm(g, A_CONCAT, EPI_F32, s));
+  } else {
+    GemmArgs g;
+    g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = kHgLd;
     g.W = W.w2_w[l]; g.ldw = 1536; g.res = hbuf; g.ldres = 512;
     g.C32 = cur; g.ldc32 = 512; g.C16 = out16; g.ldc16 = 512;
     if (l < 6) norm_out(g, l + 1);
@@ -1024,7 +1089,8 @@ void Engine::enqueue_transformer(int B, int T, const float* tab, const float* nb
   Workspace& ws = *ws_;
   for (int l = 0; l < 13; ++l)
     enqueue_layer(l, B, T, tab, nbq, nbw, ws.xa, ws.xb, l > 6 ? ws.skip16[12 - l] : nullptr,
-                  l < 6 ? ws.skip16[l] : ws.x16);
+                  l < 6 ? ws.skip16[l] : ws.x16, l > 6,
+                  l >= 6 && l < 12 ? ws.skip16[11 - l] : nullptr);
   HIP_OK(launch_adarms(ws.xa, W.gamma[26], tab + 26 * 1024, tab + 26 * 1024 + 512, ws.n16, B * T,
                        stream_));
 }
@@ -1254,7 +1320,7 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
     case 0: {  // FFN w1|w3 GEMM + SwiGLU (N = 3072, K = 512)
       GemmArgs g;
       g.M = R; g.N = 3072; g.K = 512; g.A = ws.n16; g.lda = 512;
-      g.W = W.w13_w[0]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = 1536;
+      g.W = W.w13_w[0]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = kHgLd;
       g.bias = ws.nbw; g.ssq_in = ws.ssq;
       loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, stream_)); });
       f = 2.0 * R * 3072 * 512;
@@ -1286,7 +1352,7 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
     }
     case 3: {  // FFN w2 GEMM + residual (N = 512, K = 1536)
       GemmArgs g;
-      g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = 1536; g.W = W.w2_w[0]; g.ldw = 1536;
+      g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = kHgLd; g.W = W.w2_w[0]; g.ldw = 1536;
       g.res = ws.xb; g.ldres = 512; g.C32 = ws.stage_a; g.ldc32 = 512;
       loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, stream_)); });
       f = 2.0 * R * 512 * 1536;
@@ -1463,10 +1529,10 @@ void Engine::stage_feed_forward(const float* in, int rows, int layer, float* out
   to_f16(ws.stage_a, ws.n16, (size_t)rows * 512, stream_);
   GemmArgs g;
   g.M = rows; g.N = 3072; g.K = 512; g.A = ws.n16; g.lda = 512; g.W = W.w13_w[layer]; g.ldw = 512;
-  g.C16 = ws.g16; g.ldc16 = 1536;
+  g.C16 = ws.g16; g.ldc16 = kHgLd;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, stream_));
   GemmArgs o;
-  o.M = rows; o.N = 512; o.K = 1536; o.A = ws.g16; o.lda = 1536; o.W = W.w2_w[layer]; o.ldw = 1536;
+  o.M = rows; o.N = 512; o.K = 1536; o.A = ws.g16; o.lda = kHgLd; o.W = W.w2_w[layer]; o.ldw = 1536;
   o.C32 = ws.stage_b; o.ldc32 = 512;
   HIP_OK(launch_gemm(o, A_PLAIN, EPI_F32, stream_));
   d2h(out, ws.stage_b, (size_t)rows * 512 * 4, stream_);

@@ -26,8 +26,9 @@ enum AMode : int {
 };
 
 enum EpiMode : int {
-  EPI_F32 = 0,        // C32 = acc + bias + res (bias/res optional); optional f16 copy C16,
-                      // optional normalised-operand outputs (C16s, ssq_out; see below)
+  EPI_F32 = 0,        // C32 = acc + bias + res (bias/res optional; C32 may be null when
+                      // another output is set); optional f16 copy C16, optional
+                      // normalised-operand outputs (C16s, ssq_out; see below)
   EPI_F16 = 1,        // C16 = acc + bias
   EPI_SWIGLU = 2,     // W rows interleaved [w1 x16 | w3 x16]: C16[m][c] = silu(h1) * h3
   EPI_GATE = 3,       // W rows interleaved [a x16 | b x16]: C16 = tanh(a+ca) * sigmoid(b+cb)

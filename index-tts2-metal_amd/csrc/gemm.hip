@@ -613,7 +613,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
           ssq[j / 2] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
           s1[j / 2] += (v.x + v.y) + (v.z + v.w);
           if (!live) continue;
-          *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
+          if (p.C32) *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
           if (p.C16) st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
           if (p.C16s)
             st16(p.C16s + (size_t)m * p.ldc16s + n, v.x * nsc[j].x, v.y * nsc[j].y,
