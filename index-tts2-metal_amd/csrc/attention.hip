@@ -31,9 +31,8 @@
 
 namespace mit2hip {
 
-constexpr int kAttnDeepMaxTpad = 2048;  // longest padded sequence with a 3-tile ring
+constexpr int kAttnDeepMaxTpad = 1024;  // longest padded sequence with a 3-tile ring
 
-typedef __attribute__((address_space(3))) void attn_lds_t;
 
 template <int N>
 __device__ __forceinline__ void attn_wait_vmcnt() {
@@ -126,7 +125,7 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int qw = wv % NQW;  // query wave within the group
   const int grp = wv / NQW; // key group
   const int lr = lane & 15;
@@ -146,17 +145,30 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
   const float* brow = kbias + (size_t)b * Tpad;
   const int ntiles = Tpad / 64;
   // Group grp walks tiles [grp*tpg, grp*tpg + tpg).  A tile index past the
-  // end loads the last tile again (clamped) and its scores are forced to
-  // -inf, so every group runs the same iterations and meets at the same
-  // barriers.
+  // end loads the last tile again (clamped) and is not computed, so every
+  // group runs the same iterations and meets at the same barriers.
   const int tpg = (ntiles + G - 1) / G;
   const int tbase = grp * tpg;
 
   // Per tile the NQW waves of a group split its K and V^T tiles (8 KB each,
   // 8 / NQW direct loads of 1 KB per wave and tile), and each wave loads its
-  // own copy of the 64 bias words.
+  // own copy of the 64 bias words.  The loads go through buffer resources
+  // over this head's K and V^T and this branch's bias row: a lane's byte
+  // offset within a tile is fixed for the whole loop, and the tile's offset
+  // is a scalar, so issuing a tile costs no vector instructions.
   constexpr int kPer = 8 / NQW;
   constexpr int kLoads = 2 * kPer + 1;
+  const buffer_rsrc_t rK = make_buffer_rsrc(Kh, Tpad * 64 * 2);
+  const buffer_rsrc_t rV = make_buffer_rsrc(Vh, Tpad * 64 * 2);
+  const buffer_rsrc_t rB = make_buffer_rsrc(brow, Tpad * 4);
+  int voK[kPer], voV[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int q = (qw * kPer + u) * 64 + lane;  // this lane's 16-byte slot of the tile
+    const int row = q >> 3;
+    voK[u] = (row * 64 + attn_kslot(row, q & 7) * 8) * 2;
+    voV[u] = (row * Tpad + attn_vslot(row, q & 7) * 8) * 2;
+  }
   auto issue = [&](auto st, int j) {
     const int kt = min(tbase + j, ntiles - 1);
     half_t* sk = bufK(st) + grp * TILE;
@@ -165,16 +177,10 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int s0 = (qw * kPer + u) * 64;  // first 16-byte slot of this load
-      const int q = s0 + lane;
-      const int row = q >> 3;
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(Kh + (size_t)(kt * 64 + row) * 64 + attn_kslot(row, q & 7) * 8),
-          (attn_lds_t*)(sk + s0 * 8), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(Vh + (size_t)row * Tpad + kt * 64 + attn_vslot(row, q & 7) * 8),
-          (attn_lds_t*)(sv + s0 * 8), 16, 0, 0);
+      buffer_load_lds16(rK, (lds_ptr_t*)(sk + s0 * 8), voK[u], kt * 8192);
+      buffer_load_lds16(rV, (lds_ptr_t*)(sv + s0 * 8), voV[u], kt * 128);
     }
-    __builtin_amdgcn_global_load_lds((const void*)(brow + kt * 64 + lane), (attn_lds_t*)sb, 4, 0, 0);
+    buffer_load_lds4(rB, (lds_ptr_t*)sb, lane * 4, kt * 256);
   };
 
   // B operands of S^T = K.Q^T: query rows q0 + 16 qb + lr, d-slots of lane group lg.
@@ -202,7 +208,10 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
   }
 
   auto compute = [&](auto st, int j) {
-    const int kt = tbase + j;  // unclamped: a tile past the end is masked out entirely
+    const int kt = tbase + j;
+    // A tile past the end (its group's share is short) would contribute
+    // exp2(-inf) = 0 to every sum and leave the maxima alone: skip it.
+    if (kt >= ntiles) return;
     const half_t* sk = bufK(st) + grp * TILE;
     const half_t* sv = bufV(st) + grp * TILE;
     const float* sb = bufB(st) + wv * 64;
@@ -220,11 +229,10 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
         sc[kb][qb] = mfma16x16x32(kf1, qf[qb][1], z);
       }
     }
-    const float past = kt < ntiles ? 0.0f : -INFINITY;  // a clamped tile past the end
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const float4 bb = *reinterpret_cast<const float4*>(sb + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1));
-      const float bv[4] = {bb.x + past, bb.y + past, bb.z + past, bb.w + past};
+      const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
@@ -404,9 +412,10 @@ hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             hipStream_t stream) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
   // Shapes swept on MI355X (B = 2, us per launch, head-per-XCD mapping):
-  //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves, 2 buffers   3.5 / 5.4
-  //   T = 860:        64 queries x 2 key groups, 16-query waves, 3 buffers  10.3
-  //   T = 3000:       64 queries x 2 key groups, 16-query waves, 2 buffers  69.7
+  //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves, 2 buffers   3.5 / 4.9
+  //   T = 860:        64 queries x 2 key groups, 16-query waves, 3 buffers   8.7 (2 buffers: 8.8)
+  //   T = 1348:       64 queries x 2 key groups, 16-query waves, 2 buffers  17.9 (3 buffers: 21.4)
+  //   T = 3000:       64 queries x 2 key groups, 16-query waves, 2 buffers  55.0
   // Every shape splits the keys into the same two groups, so the result is
   // bit-identical whichever is chosen; the choice depends on the padded
   // length only, never on the batch.

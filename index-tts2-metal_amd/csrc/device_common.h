@@ -21,6 +21,37 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Word 3 of a raw buffer resource on gfx9-family GPUs (gfx950): 32-bit data,
+// no swizzle, byte offsets checked against word 2 (the byte range), so a
+// load past the range returns zeros without a memory access.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+typedef __attribute__((address_space(3))) void lds_ptr_t;
+
+// Buffer resources and direct buffer -> LDS loads.  The resource type and
+// the builtins exist only for the GPU target; the host pass (which parses
+// kernel bodies but never runs them) sees inert stand-ins, without which it
+// would drop the kernels' launch stubs.
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t buffer_rsrc_t;
+__device__ __forceinline__ buffer_rsrc_t make_buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kBufferRsrcWord3);
+}
+// Each lane's 16 (or 4) bytes at base + voffset + soffset land at
+// M0 + 16*lane (4*lane), M0 = lds (wave-uniform); soffset is wave-uniform.
+__device__ __forceinline__ void buffer_load_lds16(buffer_rsrc_t r, lds_ptr_t* lds, int voffset, int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voffset, soffset, 0, 0);
+}
+__device__ __forceinline__ void buffer_load_lds4(buffer_rsrc_t r, lds_ptr_t* lds, int voffset, int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, voffset, soffset, 0, 0);
+}
+#else
+struct buffer_rsrc_t { const void* base; };
+__device__ inline buffer_rsrc_t make_buffer_rsrc(const void* base, int) { return buffer_rsrc_t{base}; }
+__device__ inline void buffer_load_lds16(buffer_rsrc_t, lds_ptr_t*, int, int) {}
+__device__ inline void buffer_load_lds4(buffer_rsrc_t, lds_ptr_t*, int, int) {}
+#endif
+
 // Padded operand widths (every GEMM K is a multiple of 128 so that K stages
 // of 64/128/256 divide it and concatenated operands switch source on a stage
 // boundary).

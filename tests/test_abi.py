@@ -30,6 +30,19 @@ def test_exports_are_exactly_the_declared_functions(mit2):
     assert exported == mit2.declared_symbols()
 
 
+def test_every_kernel_launch_stub_is_defined(mit2):
+    """A kernel whose body the host compilation pass rejects (a GPU-only
+    builtin or type reaching it) loses its launch stub without a build error;
+    a shared library then links with the stub undefined and the first launch
+    fails at load time."""
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-u", str(mit2.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    assert [s for s in out.split() if "__device_stub__" in s] == []
+
+
 def test_abi_version_matches_header(mit2):
     text = mit2.HEADER_PATH.read_text()
     v = int(re.search(r"#define MIT2CFM_ABI_VERSION (\d+)", text).group(1))
