@@ -30,8 +30,6 @@
 
 namespace mit2hip {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -115,7 +113,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   constexpr int kALo = KG * BM * SK;  // offset of a stage's lo half in its buffer
   constexpr int kWLo = KG * BN * SK;
   static_assert(NST >= 2 && NST <= 8, "two to eight stages");
-  const int kg = threadIdx.x / (64 * NW);  // K group of this wave
+  const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / (64 * NW));  // K group of this wave
   auto bufA = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
     half_t* b;
@@ -142,7 +140,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = (tid >> 6) % NW;  // wave within its K group
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) % NW;  // wave within its K group
   const int wm = wave / WN;
   const int wn = wave - wm * WN;
   const int lr = lane & 15;
@@ -270,89 +268,113 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     }
   }
 
-  // Source of the 16-byte chunk at K position k0 + kc of load slot j's row
-  // m; `lo` selects the lo half of a split operand (the resident zero row of
-  // A_CONVP serves both halves).
-  auto a_src = [&](int j, int m, int k0, int kc, bool lo) -> const half_t* {
+  // A_CONVP: source of the 16-byte chunk at K position k0 + kc of load slot
+  // j's row m; `lo` selects the lo half of a split operand (the resident
+  // zero row serves both halves).
+  auto convp_src = [&](int j, int k0, int kc, bool lo) -> const half_t* {
     const int k = k0 + kc;
     const size_t lo_off = lo ? p.a_lo : 0;
-    if constexpr (AM == A_PLAIN) {
-      return p.A + lo_off + (size_t)m * p.lda + k;
-    } else if constexpr (AM == A_CONCAT) {
-      return k < p.K1 ? p.A + lo_off + (size_t)m * p.lda + k
-                      : p.A2 + lo_off + (size_t)m * p.lda2 + (k - p.K1);
-    } else if constexpr (AM == A_CONV5 || AM == A_CONV3Z) {
-      // The row offset is chosen by value selects on the wave-uniform tap: a
-      // select of the members' addresses would put conv_rows in scratch
-      // memory, and its loads would wait for the ring's DMA (one counter).
-      const int tap = __builtin_amdgcn_readfirstlane(k0 / kConvC);  // stage start: uniform
-      const ConvRows cr = conv_rows[j];
-      int ro = cr.r0;
-      ro = tap == 1 ? cr.r1 : ro;
-      ro = tap == 2 ? cr.r2 : ro;
-      if constexpr (AM == A_CONV5) {
-        ro = tap == 3 ? cr.r3 : ro;
-        ro = tap == 4 ? cr.r4 : ro;
-      }
-      return p.A + lo_off + ro + (k - tap * kConvC);
-    } else {
-      // tap = k / conv_c through a float reciprocal, corrected by one either way
-      int tap = (int)((float)k * p.conv_inv_c);
-      int c = k - tap * p.conv_c;
-      if (c < 0) {
-        --tap;
-        c += p.conv_c;
-      } else if (c >= p.conv_c) {
-        ++tap;
-        c -= p.conv_c;
-      }
-      const int src = cp_t[j] + tap * p.conv_d - p.conv_pad;
-      const bool ok = tap < p.conv_k && src >= 0 && src < p.T;
-      return ok ? p.A + lo_off + (size_t)(cp_base[j] + src) * p.lda + c : p.A_zero + c;
+    // tap = k / conv_c through a float reciprocal, corrected by one either way
+    int tap = (int)((float)k * p.conv_inv_c);
+    int c = k - tap * p.conv_c;
+    if (c < 0) {
+      --tap;
+      c += p.conv_c;
+    } else if (c >= p.conv_c) {
+      ++tap;
+      c -= p.conv_c;
     }
+    const int src = cp_t[j] + tap * p.conv_d - p.conv_pad;
+    const bool ok = tap < p.conv_k && src >= 0 && src < p.T;
+    return ok ? p.A + lo_off + (size_t)(cp_base[j] + src) * p.lda + c : p.A_zero + c;
   };
 
+  // Every other operand is read through a buffer resource: a lane's byte
+  // offset (its row and swizzled 16-byte chunk) is fixed for the kernel and
+  // the stage's column offset is a scalar, so issuing a stage costs no
+  // vector instructions beyond the conv taps' row selects.  The host keeps
+  // every span below 2^31 bytes (gemm_spans_fit).
+  const int a_rows = AM == A_CONV3Z ? p.M + 1 : p.M;  // A_CONV3Z: row M is the zero row
+  const buffer_rsrc_t rW = make_buffer_rsrc(p.W, (int)(((size_t)(p.N - 1) * p.ldw + p.K + p.w_lo) * 2));
+  const buffer_rsrc_t rA =
+      make_buffer_rsrc(p.A, AM == A_CONVP ? 0 : (int)(((size_t)a_rows * p.lda + p.a_lo) * 2));
+  const buffer_rsrc_t rA2 =
+      AM == A_CONCAT ? make_buffer_rsrc(p.A2, (int)(((size_t)p.M * p.lda2 + p.a_lo) * 2)) : rA;
+  int voA[LA], voA2[AM == A_CONCAT ? LA : 1], voW[LB];
+#pragma unroll
+  for (int j = 0; j < LA; ++j) {
+    const int q = (wave * LA + j) * 64 + lane;
+    const int row = q / CPR;
+    const int c = (q % CPR) ^ swz(row);
+    const int m = min(m0 + row, p.M - 1);  // rows past M load a valid row; never stored
+    if constexpr (kConv) {
+      voA[j] = c * 16;  // + the tap's row, chosen per stage
+    } else {
+      voA[j] = (m * p.lda + c * 8) * 2;
+      if constexpr (AM == A_CONCAT) voA2[j] = (m * p.lda2 + c * 8) * 2;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < LB; ++j) {
+    const int q = (wave * LB + j) * 64 + lane;
+    const int row = q / CPR;
+    voW[j] = ((n0 + row) * p.ldw + ((q % CPR) ^ swz(row)) * 8) * 2;
+  }
+
   // Stage kt >= KT (the ring running past the last stage) keeps the per-stage
-  // load count, which the vmcnt waits rely on, but every lane reads the same
-  // 16 bytes (the first of W) into a buffer that is not read again: one
-  // request per load.  The choice is a mask on the address, hidden from the
-  // optimiser, so it stays a select: a branch here makes the compiler give
-  // up tracking the ring and wait for every load in flight.
+  // load count, which the vmcnt waits rely on: it loads the last stage again
+  // (an L2 hit) into a buffer that is not read again.  The clamp is a scalar
+  // select, so the loop body stays branch-free.
   auto issue = [&](auto st, int kt) {
     half_t* sa = bufA(st);
     half_t* sb = bufB(st);
-    const int k0 = ((kt < KT ? kt : KT - 1) + kt_lo) * SK;
-    uint64_t keep = kt < KT ? ~0ull : 0ull;
-#if defined(__HIP_DEVICE_COMPILE__)
-    __asm__ volatile("" : "+v"(keep));
-#endif
-    const uint64_t dummy = (uint64_t)(uintptr_t)p.W & ~keep;
-#define MIT2_PICK(real) ((const void*)(uintptr_t)(((uint64_t)(uintptr_t)(real) & keep) | dummy))
+    const int k0 = ((kt < KT ? kt : KT - 1) + kt_lo) * SK;  // wave-uniform
 #pragma unroll
     for (int j = 0; j < LA; ++j) {
       const int q0 = (wave * LA + j) * 64;
-      const int q = q0 + lane;
-      const int row = q / CPR;
-      const int c = (q % CPR) ^ swz(row);
-      int m = m0 + row;
-      if (m > p.M - 1) m = p.M - 1;  // rows past M load a valid row; never stored
-      __builtin_amdgcn_global_load_lds(MIT2_PICK(a_src(j, m, k0, c * 8, false)), (lds_void_t*)(sa + q0 * 8),
-                                       16, 0, 0);
-      if constexpr (AS == 2)
-        __builtin_amdgcn_global_load_lds(MIT2_PICK(a_src(j, m, k0, c * 8, true)),
-                                         (lds_void_t*)(sa + kALo + q0 * 8), 16, 0, 0);
+      lds_ptr_t* dst = (lds_ptr_t*)(sa + q0 * 8);
+      lds_ptr_t* dst_lo = (lds_ptr_t*)(sa + kALo + q0 * 8);
+      if constexpr (AM == A_CONVP) {
+        const int q = q0 + lane;
+        const int c = (q % CPR) ^ swz(q / CPR);
+        __builtin_amdgcn_global_load_lds((const void*)convp_src(j, k0, c * 8, false), dst, 16, 0, 0);
+        if constexpr (AS == 2)
+          __builtin_amdgcn_global_load_lds((const void*)convp_src(j, k0, c * 8, true), dst_lo, 16, 0, 0);
+      } else if constexpr (kConv) {
+        // The tap's row offset by value selects on the wave-uniform tap: a
+        // select of the members' addresses would put conv_rows in scratch
+        // memory, and its loads would wait for the ring's DMA (one counter).
+        const int tap = k0 / kConvC;  // a stage never straddles a tap
+        const ConvRows cr = conv_rows[j];
+        int ro = cr.r0;
+        ro = tap == 1 ? cr.r1 : ro;
+        ro = tap == 2 ? cr.r2 : ro;
+        if constexpr (AM == A_CONV5) {
+          ro = tap == 3 ? cr.r3 : ro;
+          ro = tap == 4 ? cr.r4 : ro;
+        }
+        const int vo = ro * 2 + voA[j];
+        const int so = (k0 - tap * kConvC) * 2;
+        buffer_load_lds16(rA, dst, vo, so);
+        if constexpr (AS == 2) buffer_load_lds16(rA, dst_lo, vo, so + (int)p.a_lo * 2);
+      } else if constexpr (AM == A_CONCAT) {
+        const bool first = k0 < p.K1;  // a stage never straddles K1
+        const buffer_rsrc_t r = first ? rA : rA2;
+        const int vo = first ? voA[j] : voA2[j];
+        const int so = (first ? k0 : k0 - p.K1) * 2;
+        buffer_load_lds16(r, dst, vo, so);
+        if constexpr (AS == 2) buffer_load_lds16(r, dst_lo, vo, so + (int)p.a_lo * 2);
+      } else {
+        buffer_load_lds16(rA, dst, voA[j], k0 * 2);
+        if constexpr (AS == 2) buffer_load_lds16(rA, dst_lo, voA[j], k0 * 2 + (int)p.a_lo * 2);
+      }
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
       const int q0 = (wave * LB + j) * 64;
-      const int q = q0 + lane;
-      const int row = q / CPR;
-      const int c = (q % CPR) ^ swz(row);
-      const half_t* wsrc = p.W + (size_t)(n0 + row) * p.ldw + k0 + c * 8;
-      __builtin_amdgcn_global_load_lds(MIT2_PICK(wsrc), (lds_void_t*)(sb + q0 * 8), 16, 0, 0);
+      buffer_load_lds16(rW, (lds_ptr_t*)(sb + q0 * 8), voW[j], k0 * 2);
       if constexpr (WS == 2)
-        __builtin_amdgcn_global_load_lds(MIT2_PICK(wsrc + p.w_lo), (lds_void_t*)(sb + kWLo + q0 * 8), 16, 0, 0);
-#undef MIT2_PICK
+        buffer_load_lds16(rW, (lds_ptr_t*)(sb + kWLo + q0 * 8), voW[j], k0 * 2 + (int)p.w_lo * 2);
     }
   };
 
@@ -922,7 +944,21 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
   return launch_tile<64, 64, 64, 3, AM, EPI>(a, s);
 }
 
+// Every operand gemm_kernel reads through a buffer resource spans less than
+// 2^31 bytes (buffer offsets are 32-bit; the A_CONVP operand is read with
+// global addresses instead).
+static bool gemm_spans_fit(const GemmArgs& a, AMode am) {
+  constexpr size_t kMax = size_t(1) << 31;
+  if (a.N <= 0 || a.M <= 0 || a.K <= 0 || a.ldw < 0 || a.lda < 0 || a.lda2 < 0) return false;
+  const size_t w = ((size_t)(a.N - 1) * a.ldw + a.K + a.w_lo) * 2;
+  const size_t rows = am == A_CONV3Z ? (size_t)a.M + 1 : (size_t)a.M;
+  const size_t aa = am == A_CONVP ? 0 : (rows * a.lda + a.a_lo) * 2;
+  const size_t a2 = am == A_CONCAT ? ((size_t)a.M * a.lda2 + a.a_lo) * 2 : 0;
+  return w < kMax && aa < kMax && a2 < kMax;
+}
+
 hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t stream) {
+  if (!gemm_spans_fit(a, amode)) return hipErrorInvalidValue;
   if (a.split != 0 || a.c16_lo != 0) {
     // Split operands: the condition producer's and the vocoder's GEMMs.
     if (a.split < 0 || a.split > 2 || (a.split >= 1 && a.a_lo == 0) || (a.split == 2 && a.w_lo == 0) ||
