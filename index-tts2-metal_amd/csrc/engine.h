@@ -210,8 +210,7 @@ class Engine {
                      float* cur, float* hbuf, const half_t* skip16, half_t* out16,
                      bool skip_in_done = false, const half_t* next_skip16 = nullptr);
   void enqueue_transformer(int B, int T, const float* tab, const float* nbq, const float* nbw);
-  void enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw,
-                         bool final_norm = true);
+  void enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw);
   void enqueue_decode(const float* x0, const float* prompt, const float* cond, const float* style,
                       int nreq, int T, int steps, float cfg, float* vtrace, const TableBufs& tb);
   void upload_stage_tables(const float* t1_host, const float* t2_host);

@@ -1099,8 +1099,7 @@ void Engine::enqueue_transformer(int B, int T, const float* tab, const float* nb
 // Runs the estimator from x (ws.xa, fp32, already merged) to the final
 // layer's AdaLN output (ws.n16, f16) for B branches of T rows, using one
 // step's tables; the caller applies the folded final linear + conv2.
-void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw,
-                               bool final_norm) {
+void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq, const float* nbw) {
   Weights& W = *w_;
   Workspace& ws = *ws_;
   const int R = B * T;
@@ -1138,9 +1137,8 @@ void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq,
     }
   }
   // The final layer's AdaLN output stays in ws.n16; its linear map is folded
-  // into conv2 (W.c2f_w), which the caller applies.  Without final_norm the
-  // caller's conv2 kernel normalises ws.fin itself (the decode step).
-  if (final_norm) HIP_OK(launch_adaln(ws.fin, tab + kFinalSsOff, tab + kFinalSsOff + 512, ws.n16, R, s));
+  // into conv2 (W.c2f_w), which the caller applies.
+  HIP_OK(launch_adaln(ws.fin, tab + kFinalSsOff, tab + kFinalSsOff + 512, ws.n16, R, s));
 }
 
 // Input merge constant part: cond projection into mc16[:, kMcContent:+512], then
@@ -1186,11 +1184,10 @@ void Engine::enqueue_decode(const float* x0, const float* prompt, const float* c
   for (int s = 0; s < steps; ++s) {
     const float* tab = tb.tab + (size_t)s * kTcondPerStep;
     enqueue_merge_step(W, ws, R, stream_, tab);
-    enqueue_estimator(B, T, tab, tb.nbq + (size_t)s * 13 * 1536, tb.nbw + (size_t)s * 13 * 3072,
-                      false);
-    HIP_OK(launch_conv2_euler(ws.fin, tab + kFinalSsOff, tab + kFinalSsOff + 512, W.c2f_w, W.c2f_b,
-                              ws.P, nreq, T, cfg_on, cfg, dt, ws.x_cur, ws.xmel16,
-                              vtrace ? vtrace + (size_t)s * nreq * T * 80 : nullptr, stream_));
+    enqueue_estimator(B, T, tab, tb.nbq + (size_t)s * 13 * 1536, tb.nbw + (size_t)s * 13 * 3072);
+    HIP_OK(launch_conv2_euler(ws.n16, W.c2f_w, W.c2f_b, ws.P, nreq, T, cfg_on, cfg, dt, ws.x_cur,
+                              ws.xmel16, vtrace ? vtrace + (size_t)s * nreq * T * 80 : nullptr,
+                              stream_));
   }
 }
 

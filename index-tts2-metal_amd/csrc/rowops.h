@@ -48,15 +48,13 @@ hipError_t launch_step_prep(const float* x, const float* prompt_x, const float* 
                             const float* style, int B, int T, half_t* xmel16, half_t* cond16,
                             half_t* mc16, hipStream_t s);
 
-// Final AdaLN + conv2 (512 -> 80, k=1) + CFG blend + Euler update for nreq
-// requests: y_b = f16(AdaLN(xfin[b]; shift, scale)) as launch_adaln gives it;
-//   dphi_b = y_b . W2^T + bias2;  v = (1+cfg)*dphi_cond - cfg*dphi_null (cfg on) or dphi_cond;
+// conv2 (512 -> 80, k=1) + CFG blend + Euler update for nreq requests:
+//   dphi_b = y16[b] . W2^T + bias2;  v = (1+cfg)*dphi_cond - cfg*dphi_null (cfg on) or dphi_cond;
 //   x_cur += dt * v; rows t < P[r] set to 0; xmel16 of every branch refreshed.
 // vtrace (optional) receives v as [nreq][T][80].
-hipError_t launch_conv2_euler(const float* xfin, const float* shift, const float* scale,
-                              const half_t* w2, const float* b2, const uint32_t* P, int nreq, int T,
-                              int cfg_on, float cfg, float dt, float* x_cur, half_t* xmel16,
-                              float* vtrace, hipStream_t s);
+hipError_t launch_conv2_euler(const half_t* y16, const half_t* w2, const float* b2,
+                              const uint32_t* P, int nreq, int T, int cfg_on, float cfg, float dt,
+                              float* x_cur, half_t* xmel16, float* vtrace, hipStream_t s);
 // conv2 only: dphi[m][80] = y16[m] . W2^T + bias2 for every row.
 hipError_t launch_conv2_rows(const half_t* y16, const half_t* w2, const float* b2, int rows,
                              float* dphi, hipStream_t s);

@@ -36,12 +36,14 @@ __global__ __launch_bounds__(256) void adarms_kernel(const float* __restrict__ x
   *reinterpret_cast<half8*>(out + (size_t)row * 512 + lane * 8) = o;
 }
 
-// Adaptive LayerNorm of one 512-wide row by one wavefront: lane `lane` gets
-// the f16 outputs of columns 8 lane .. 8 lane + 7.  Shared by adaln_kernel
-// and the decode's fused conv2 kernel, so both give the same bits.
-__device__ __forceinline__ half8 adaln_row(const float* __restrict__ xrow, const float* __restrict__ shift,
-                                           const float* __restrict__ scale, int lane) {
-  const float4* xr = reinterpret_cast<const float4*>(xrow) + lane * 2;
+__global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ x,
+                                                    const float* __restrict__ shift,
+                                                    const float* __restrict__ scale,
+                                                    half_t* __restrict__ out, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * 512) + lane * 2;
   const float4 a = xr[0], b = xr[1];
   float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   float s = 0.f;
@@ -52,7 +54,7 @@ __device__ __forceinline__ half8 adaln_row(const float* __restrict__ xrow, const
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float d = v[i] - mean;
-    var = fmaf(d, d, var);
+    var += d * d;
   }
   var = warp_sum(var) / 512.0f;
   const float inv = 1.0f / sqrtf(var + 1e-6f);
@@ -60,20 +62,9 @@ __device__ __forceinline__ half8 adaln_row(const float* __restrict__ xrow, const
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = lane * 8 + i;
-    o[i] = (half_t)fmaf((v[i] - mean) * inv, 1.0f + scale[c], shift[c]);
+    o[i] = (half_t)(((v[i] - mean) * inv) * (1.0f + scale[c]) + shift[c]);
   }
-  return o;
-}
-
-__global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ x,
-                                                    const float* __restrict__ shift,
-                                                    const float* __restrict__ scale,
-                                                    half_t* __restrict__ out, int rows) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  *reinterpret_cast<half8*>(out + (size_t)row * 512 + lane * 8) =
-      adaln_row(x + (size_t)row * 512, shift, scale, lane);
+  *reinterpret_cast<half8*>(out + (size_t)row * 512 + lane * 8) = o;
 }
 
 __global__ __launch_bounds__(256) void norm_prep_kernel(const float* __restrict__ x,
@@ -240,21 +231,17 @@ __device__ __forceinline__ void conv2_block(const half_t* __restrict__ y16, size
   }
 }
 
-// Final AdaLN + conv2 + CFG blend + Euler update.  One workgroup per
-// 16-token block of one request: the four waves first normalise the block's
-// rows of both branches (adaln_row, into LDS), then wave w computes the
-// partial product over K = [128 w, 128 w + 128) for both branches (five
-// 16-wide MFMA column blocks each), the partials meet in LDS, and the 256
-// threads apply the update to the 16 x 80 block.
-constexpr int kYsPitch = 512 + 8;  // LDS row pitch (halves): 16-row fragment reads hit distinct banks
+// conv2 + CFG blend + Euler update.  One workgroup per 16-token block of
+// one request: wave w computes the partial product over K = [128 w, 128 w +
+// 128) for both branches (five 16-wide MFMA column blocks each), the
+// partials meet in LDS, and the 256 threads apply the update to the
+// 16 x 80 block.
 __global__ __launch_bounds__(256) void conv2_euler_kernel(
-    const float* __restrict__ xfin, const float* __restrict__ shift, const float* __restrict__ scale,
-    const half_t* __restrict__ w2, const float* __restrict__ b2,
+    const half_t* __restrict__ y16, const half_t* __restrict__ w2, const float* __restrict__ b2,
     const uint32_t* __restrict__ P, int T, int cfg_on, float cfg, float dt,
     float* __restrict__ x_cur, half_t* __restrict__ xmel16, float* __restrict__ vtrace) {
   // red[wave][branch][block nb][lane][i]: partial of token 4*(lane/16)+i, channel 16*nb + lane%16
   __shared__ float red[4][2][5][64][4];
-  __shared__ __attribute__((aligned(16))) half_t ys[2][16][kYsPitch];  // AdaLN'd rows (0 past T)
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
@@ -263,21 +250,16 @@ __global__ __launch_bounds__(256) void conv2_euler_kernel(
   const int nvalid = min(16, T - t0);
   const int bc = cfg_on ? 2 * r : r;
   const int nbr = cfg_on ? 2 : 1;
-  for (int q = wave; q < nbr * 16; q += 4) {
-    const int br = q >> 4, tok = q & 15;
-    half8 o = {};
-    if (tok < nvalid) o = adaln_row(xfin + ((size_t)(bc + br) * T + t0 + tok) * 512, shift, scale, lane);
-    *reinterpret_cast<half8*>(&ys[br][tok][lane * 8]) = o;
-  }
-  __syncthreads();
   for (int br = 0; br < nbr; ++br) {
+    const size_t row0 = (size_t)(bc + br) * T + t0;
     floatx4 acc[5];
 #pragma unroll
     for (int nb = 0; nb < 5; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int k = wave * 128 + ks * 32 + lg * 8;
-      const half8 av = *reinterpret_cast<const half8*>(&ys[br][lr][k]);
+      half8 av = {};
+      if (lr < nvalid) av = *reinterpret_cast<const half8*>(y16 + (row0 + lr) * 512 + k);
 #pragma unroll
       for (int nb = 0; nb < 5; ++nb) {
         const half8 bw = *reinterpret_cast<const half8*>(w2 + (size_t)(nb * 16 + lr) * 512 + k);
@@ -316,12 +298,11 @@ __global__ __launch_bounds__(256) void conv2_euler_kernel(
   }
 }
 
-hipError_t launch_conv2_euler(const float* xfin, const float* shift, const float* scale,
-                              const half_t* w2, const float* b2, const uint32_t* P, int nreq, int T,
-                              int cfg_on, float cfg, float dt, float* x_cur, half_t* xmel16,
-                              float* vtrace, hipStream_t s) {
-  hipLaunchKernelGGL(conv2_euler_kernel, dim3((T + 15) / 16, nreq), dim3(256), 0, s, xfin, shift, scale,
-                     w2, b2, P, T, cfg_on, cfg, dt, x_cur, xmel16, vtrace);
+hipError_t launch_conv2_euler(const half_t* y16, const half_t* w2, const float* b2,
+                              const uint32_t* P, int nreq, int T, int cfg_on, float cfg, float dt,
+                              float* x_cur, half_t* xmel16, float* vtrace, hipStream_t s) {
+  hipLaunchKernelGGL(conv2_euler_kernel, dim3((T + 15) / 16, nreq), dim3(256), 0, s, y16, w2, b2, P,
+                     T, cfg_on, cfg, dt, x_cur, xmel16, vtrace);
   return hipGetLastError();
 }
 
