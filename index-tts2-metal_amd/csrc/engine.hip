@@ -244,7 +244,7 @@ void visit_weights(Weights& W, F&& f) {
 // arena bytes), then each flagged section as u64 length + bytes
 // (Vocoder::append_image, GptDecoder::append_image).
 constexpr char kImageMagic[8] = {'M', 'I', 'T', '2', 'H', 'I', 'P', 'I'};
-constexpr uint32_t kImageVersion = 5;
+constexpr uint32_t kImageVersion = 6;
 constexpr uint32_t kImageVocoder = 1, kImageGpt = 2;  // section flags
 
 struct HostModel {
@@ -345,6 +345,11 @@ std::vector<float> permute_rows(const std::vector<float>& w, int rows, int cols,
 
 int rope_map(int c, int) { return rope_pair_row(c); }
 int halves_map(int c, int half) { return halves_row(c, half); }
+// Column pairs (GemmArgs::colperm): GEMM row 32q + 16h + 4g + r holds output
+// column 32q + 8g + 4h + r, so a lane's two MFMA blocks write 8 consecutive
+// columns.  Used for the weights of the GEMMs that produce a folded-norm
+// operand (wo, w2, the folded w2|skip-in, skip-in, the per-step merge).
+int colpair_map(int c, int) { return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3); }
 
 // Copies a column block [c0, c0+n) of src [rows][scols] into dst [rows][dcols] at column d0.
 void copy_cols(const std::vector<float>& src, int rows, int scols, int c0, int n,
@@ -485,7 +490,7 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
     copy_cols(mw, 512, 864, 80, 80, mc, kMcWidth, 0);             // prompt_x
     copy_cols(mw, 512, 864, 160, 512, mc, kMcWidth, kMcContent);  // content projection
     copy_cols(mw, 512, 864, 672, 192, mc, kMcWidth, kMcStyle);    // style
-    W.mx_w = up.f16(mx);
+    W.mx_w = up.f16(permute_rows(mx, 512, kMelPad, colpair_map, 0));
     W.mc_w = up.f16(mc);
     W.mc_b = up.f32(hm.get("cond_x_merge_linear.bias", 512));
   }
@@ -493,7 +498,7 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
     const std::string p = "transformer.layers." + std::to_string(l);
     W.qkv_w[l] = up.f16(permute_rows(hm.get(p + ".attention.wqkv.weight", 1536 * 512), 1536, 512,
                                      rope_map, 0));
-    W.wo_w[l] = up.f16(hm.get(p + ".attention.wo.weight", 512 * 512));
+    W.wo_w[l] = up.f16(permute_rows(hm.get(p + ".attention.wo.weight", 512 * 512), 512, 512, colpair_map, 0));
     {
       const auto& w1 = hm.get(p + ".feed_forward.w1.weight", 1536 * 512);
       const auto& w3 = hm.get(p + ".feed_forward.w3.weight", 1536 * 512);
@@ -502,9 +507,9 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
       std::memcpy(w13.data() + w1.size(), w3.data(), w3.size() * sizeof(float));
       W.w13_w[l] = up.f16(permute_rows(w13, 3072, 512, halves_map, 1536));
     }
-    W.w2_w[l] = up.f16(hm.get(p + ".feed_forward.w2.weight", 512 * 1536));
+    W.w2_w[l] = up.f16(permute_rows(hm.get(p + ".feed_forward.w2.weight", 512 * 1536), 512, 1536, colpair_map, 0));
     if (l > 6) {
-      W.si_w[l] = up.f16(hm.get(p + ".skip_in_linear.weight", 512 * 1024));
+      W.si_w[l] = up.f16(permute_rows(hm.get(p + ".skip_in_linear.weight", 512 * 1024), 512, 1024, colpair_map, 0));
       W.si_b[l] = up.f32(hm.get(p + ".skip_in_linear.bias", 512));
     } else {
       W.si_w[l] = nullptr;
@@ -543,7 +548,7 @@ Engine::Engine(const std::vector<HostTensor>& tensors, int device) : device_(dev
       });
     }
     for (auto& t : th) t.join();
-    for (int l = 7; l < 13; ++l) W.fold_w[l] = up.f16(fw[l]);
+    for (int l = 7; l < 13; ++l) W.fold_w[l] = up.f16(permute_rows(fw[l], 512, 2560, colpair_map, 0));
   }
   {
     const auto& sw = hm.get("skip_linear.weight", 512 * 592);
@@ -1028,7 +1033,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 1024; g.K1 = 512;
     g.A = ws.x16; g.lda = 512; g.A2 = skip16; g.lda2 = 512;
-    g.W = W.si_w[l]; g.ldw = 1024; g.bias = W.si_b[l];
+    g.W = W.si_w[l]; g.ldw = 1024; g.bias = W.si_b[l]; g.colperm = 1;
     g.C32 = cur; g.ldc32 = 512;
     norm_out(g, l);
     HIP_OK(launch_gemm(g, A_CONCAT, EPI_F32, s));
@@ -1045,7 +1050,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
   {
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
-    g.W = W.wo_w[l]; g.ldw = 512; g.res = cur; g.ldres = 512;
+    g.W = W.wo_w[l]; g.ldw = 512; g.res = cur; g.ldres = 512; g.colperm = 1;
     if (next_skip16) {
       g.C16 = ws.hg16; g.ldc16 = kHgLd;  // h is read only by the folded skip-in, in f16
     } else {
@@ -1065,14 +1070,14 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 2560; g.K1 = kHgLd;
     g.A = ws.hg16; g.lda = kHgLd; g.A2 = next_skip16; g.lda2 = 512;
-    g.W = W.fold_w[l + 1]; g.ldw = 2560; g.bias = W.si_b[l + 1];
+    g.W = W.fold_w[l + 1]; g.ldw = 2560; g.bias = W.si_b[l + 1]; g.colperm = 1;
     g.C32 = cur; g.ldc32 = 512;
     norm_out(g, l + 1);
     HIP_OK(launch_gemm(g, A_CONCAT, EPI_F32, s));
   } else {
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = kHgLd;
-    g.W = W.w2_w[l]; g.ldw = 1536; g.res = hbuf; g.ldres = 512;
+    g.W = W.w2_w[l]; g.ldw = 1536; g.res = hbuf; g.ldres = 512; g.colperm = 1;
     g.C32 = cur; g.ldc32 = 512; g.C16 = out16; g.ldc16 = 512;
     if (l < 6) norm_out(g, l + 1);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
@@ -1162,6 +1167,7 @@ static void enqueue_merge_step(Weights& W, Workspace& ws, int R, hipStream_t s,
   GemmArgs g;
   g.M = R; g.N = 512; g.K = kMelPad; g.A = ws.xmel16; g.lda = kMelPad;
   g.W = W.mx_w; g.ldw = kMelPad; g.res = ws.xin_const; g.ldres = 512; g.C32 = ws.xa; g.ldc32 = 512;
+  g.colperm = 1;
   if (tab) {
     g.C16s = ws.n16; g.ldc16s = 512; g.sc_a = tab; g.sc_g = W.gamma[0]; g.ssq_out = ws.ssq;
   }
@@ -1353,6 +1359,7 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
     case 3: {  // FFN w2 GEMM + residual (N = 512, K = 1536)
       GemmArgs g;
       g.M = R; g.N = 512; g.K = 1536; g.A = ws.g16; g.lda = kHgLd; g.W = W.w2_w[0]; g.ldw = 1536;
+      g.colperm = 1;
       g.res = ws.xb; g.ldres = 512; g.C32 = ws.stage_a; g.ldc32 = 512;
       loop([&] { HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, stream_)); });
       f = 2.0 * R * 512 * 1536;
@@ -1377,7 +1384,7 @@ void Engine::profile_launch(int kernel, int count, double* flops, double* bytes,
     case 6: {  // attention output projection wo + residual, folded-norm producer (N = K = 512)
       GemmArgs g;
       g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
-      g.W = W.wo_w[0]; g.ldw = 512; g.res = ws.xa; g.ldres = 512;
+      g.W = W.wo_w[0]; g.ldw = 512; g.res = ws.xa; g.ldres = 512; g.colperm = 1;
       g.C32 = ws.stage_a; g.ldc32 = 512;
       g.C16s = ws.n16; g.ldc16s = 512; g.sc_a = tab + 13 * 1024; g.sc_g = W.gamma[13];
       g.ssq_out = ws.ssq;
@@ -1515,6 +1522,7 @@ void Engine::stage_attention_core(const float* in, const uint32_t* mask, int B, 
   HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, stream_));
   GemmArgs o;
   o.M = R; o.N = 512; o.K = 512; o.A = ws.o16; o.lda = 512; o.W = W.wo_w[layer]; o.ldw = 512;
+  o.colperm = 1;
   o.C32 = ws.stage_b; o.ldc32 = 512;
   HIP_OK(launch_gemm(o, A_PLAIN, EPI_F32, stream_));
   d2h(out, ws.stage_b, (size_t)R * 512 * 4, stream_);
@@ -1533,6 +1541,7 @@ void Engine::stage_feed_forward(const float* in, int rows, int layer, float* out
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, stream_));
   GemmArgs o;
   o.M = rows; o.N = 512; o.K = 1536; o.A = ws.g16; o.lda = kHgLd; o.W = W.w2_w[layer]; o.ldw = 1536;
+  o.colperm = 1;
   o.C32 = ws.stage_b; o.ldc32 = 512;
   HIP_OK(launch_gemm(o, A_PLAIN, EPI_F32, stream_));
   d2h(out, ws.stage_b, (size_t)rows * 512 * 4, stream_);

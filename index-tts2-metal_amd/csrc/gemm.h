@@ -111,6 +111,13 @@ struct GemmArgs {
   size_t w_lo = 0;
   size_t c16_lo = 0;
 
+  // EPI_F32: the weight rows are stored in column-pair order.  Within each
+  // 32 output columns, row 16 h + 4 g + r (h < 2, g < 4, r < 4) holds column
+  // 8 g + 4 h + r, so a lane's two 16-column MFMA blocks cover 8 consecutive
+  // columns and its f16 outputs (C16, C16s) are 16-byte stores.  Every
+  // result is the same as with unpermuted rows.  N must be a multiple of 32.
+  int colperm = 0;
+
   // EPI_F32 / EPI_F16 / EPI_RESAVG: when set, the product of column n is
   // multiplied by colscale[n] (N floats) before the bias is added -- a
   // weight-normed conv stored as its direction v (exact in f16) with the

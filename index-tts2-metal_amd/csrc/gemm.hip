@@ -157,6 +157,11 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   // (fp32) or 8-byte (f16) vector per lane.
   const int row_base = m0 + wm * WTM + lr;
   const int col_base = n0 + wn * WTN + 4 * lg;
+  // First of the four output columns this lane holds in block j: col_base +
+  // 16 j, or with column-pair rows (GemmArgs::colperm) 8 consecutive columns
+  // per block pair (2 q, 2 q + 1) starting at n0 + wn*WTN + 32 q + 8 lg.
+  const bool perm = EPI == EPI_F32 && p.colperm;
+  auto colj = [&](int j) { return perm ? col_base + 32 * (j >> 1) + 4 * lg + 4 * (j & 1) : col_base + 16 * j; };
 
   // Epilogue operands that do not depend on the product are fetched now, so
   // their latency hides behind the K loop.
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       const int m = row_base + 16 * i;
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const int n = col_base + 16 * j;
+        const int n = colj(j);
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (m < p.M && kg == 0 && (p.n_store == 0 || n < p.n_store)) {
           if constexpr (EPI == EPI_F32 || EPI == EPI_RESAVG) {
@@ -487,14 +492,13 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   float4 bv[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j)
-    bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + col_base + 16 * j)
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
   constexpr bool kColScale = EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_RESAVG;
   float4 csv[kColScale ? NI : 1];
   if constexpr (kColScale) {
 #pragma unroll
     for (int j = 0; j < NI; ++j)
-      csv[j] = p.colscale ? *reinterpret_cast<const float4*>(p.colscale + col_base + 16 * j)
+      csv[j] = p.colscale ? *reinterpret_cast<const float4*>(p.colscale + colj(j))
                           : make_float4(1.f, 1.f, 1.f, 1.f);
   }
   constexpr bool kNormOut = EPI == EPI_F32;
@@ -503,8 +507,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       if (p.C16s) {
-        const float4 a = *reinterpret_cast<const float4*>(p.sc_a + col_base + 16 * j);
-        const float4 g = *reinterpret_cast<const float4*>(p.sc_g + col_base + 16 * j);
+        const float4 a = *reinterpret_cast<const float4*>(p.sc_a + colj(j));
+        const float4 g = *reinterpret_cast<const float4*>(p.sc_g + colj(j));
         nsc[j] = make_float4(a.x * g.x, a.y * g.y, a.z * g.z, a.w * g.w);
       } else {
         nsc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -608,9 +612,10 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
       float s1[(NI + 1) / 2];   // ... and with sum_out
 #pragma unroll
       for (int q = 0; q < (NI + 1) / 2; ++q) ssq[q] = s1[q] = 0.0f;
+      float4 pv = make_float4(0.f, 0.f, 0.f, 0.f);  // column pairs: the even block's outputs
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const int n = col_base + 16 * j;
+        const int n = colj(j);
         float4 v = make_float4(acc[i][j][0] + bv[j].x, acc[i][j][1] + bv[j].y,
                                acc[i][j][2] + bv[j].z, acc[i][j][3] + bv[j].w);
         if constexpr (EPI == EPI_RESAVG) {
@@ -636,6 +641,29 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
           s1[j / 2] += (v.x + v.y) + (v.z + v.w);
           if (!live) continue;
           if (p.C32) *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = v;
+          if (perm) {
+            // blocks j - 1 and j hold columns n - 4 .. n + 3: one 16-byte store each
+            if ((j & 1) == 0) {
+              pv = v;
+            } else {
+              const float4 pn = nsc[j - 1], cn = nsc[j];
+              if (p.C16) {
+                half8 h;
+                h[0] = (half_t)pv.x; h[1] = (half_t)pv.y; h[2] = (half_t)pv.z; h[3] = (half_t)pv.w;
+                h[4] = (half_t)v.x; h[5] = (half_t)v.y; h[6] = (half_t)v.z; h[7] = (half_t)v.w;
+                *reinterpret_cast<half8*>(p.C16 + (size_t)m * p.ldc16 + n - 4) = h;
+              }
+              if (p.C16s) {
+                half8 h;
+                h[0] = (half_t)(pv.x * pn.x); h[1] = (half_t)(pv.y * pn.y);
+                h[2] = (half_t)(pv.z * pn.z); h[3] = (half_t)(pv.w * pn.w);
+                h[4] = (half_t)(v.x * cn.x); h[5] = (half_t)(v.y * cn.y);
+                h[6] = (half_t)(v.z * cn.z); h[7] = (half_t)(v.w * cn.w);
+                *reinterpret_cast<half8*>(p.C16s + (size_t)m * p.ldc16s + n - 4) = h;
+              }
+            }
+            continue;
+          }
           if (p.C16) st16(p.C16 + (size_t)m * p.ldc16 + n, v.x, v.y, v.z, v.w);
           if (p.C16s)
             st16(p.C16s + (size_t)m * p.ldc16s + n, v.x * nsc[j].x, v.y * nsc[j].y,
@@ -959,6 +987,9 @@ static bool gemm_spans_fit(const GemmArgs& a, AMode am) {
 
 hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t stream) {
   if (!gemm_spans_fit(a, amode)) return hipErrorInvalidValue;
+  // Column-pair rows: EPI_F32 only, whole 32-column groups, every column stored.
+  if (a.colperm && (epi != EPI_F32 || a.N % 32 != 0 || a.n_store != 0 || a.split != 0))
+    return hipErrorInvalidValue;
   if (a.split != 0 || a.c16_lo != 0) {
     // Split operands: the condition producer's and the vocoder's GEMMs.
     if (a.split < 0 || a.split > 2 || (a.split >= 1 && a.a_lo == 0) || (a.split == 2 && a.w_lo == 0) ||
