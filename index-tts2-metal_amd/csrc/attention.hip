@@ -10,8 +10,11 @@
 // RoPE-rotated by the QKV GEMM epilogue); V is stored transposed,
 // Vt [B][8][64][Tpad].  The key mask arrives as kbias [B][Tpad] fp32 (0 for
 // a valid key, -inf for a masked or padding key; key_bias_kernel builds it
-// once per mask).  Output O is token-major [B*T][512] f16, heads
-// concatenated in head order.
+// once per mask, followed by B int words: each branch's key count, one past
+// its last valid key).  Output O is token-major [B*T][512] f16, heads
+// concatenated in head order.  The BRANCH_KEYS variant stops each branch
+// after the tile holding its last valid key; the tiles it skips are fully
+// masked, so both variants give bit-identical results.
 //
 // Keys are consumed in tiles of 64: the K tile, the V^T tile and the tile's
 // bias words are copied global -> LDS with direct loads into a ring of NBUF
@@ -86,7 +89,7 @@ __device__ __forceinline__ int attn_vslot(int r, int c) { return c ^ (r & 7); }
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;  // log2 headroom before the running max moves
 
-template <int NBUF, int G, int QB, int NQW>
+template <int NBUF, int G, int QB, int NQW, bool BRANCH_KEYS>
 __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* __restrict__ Q,
                                                                 const half_t* __restrict__ K,
                                                                 const half_t* __restrict__ Vt,
@@ -143,7 +146,14 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
   const half_t* Kh = K + head * Tpad * 64;
   const half_t* Vh = Vt + head * 64 * Tpad;
   const float* brow = kbias + (size_t)b * Tpad;
-  const int ntiles = Tpad / 64;
+  // Key tiles: every tile, or with BRANCH_KEYS only this branch's tiles up
+  // to its last valid key (the tiles after it are fully masked and would add
+  // exact zeros), at least one.
+  int ntiles = Tpad / 64;
+  if constexpr (BRANCH_KEYS) {
+    const int nk = reinterpret_cast<const int*>(kbias + (size_t)(gridDim.x / (8 * nqb)) * Tpad)[b];
+    ntiles = max(1, min(ntiles, (nk + 63) / 64));
+  }
   // Group grp walks tiles [grp*tpg, grp*tpg + tpg).  A tile index past the
   // end loads the last tile again (clamped) and is not computed, so every
   // group runs the same iterations and meets at the same barriers.
@@ -381,35 +391,50 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
 
 // kbias[b][t] = 0 for a valid key (t < T, mask != 0), -inf otherwise, for
 // t < Tpad: the additive key mask of attention_kernel (log2 units).
-__global__ void key_bias_kernel(const uint32_t* __restrict__ mask, int B, int T, int Tpad,
-                                float* __restrict__ kbias) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= B * Tpad) return;
-  const int b = i / Tpad, t = i - b * Tpad;
-  kbias[i] = (t < T && mask[(size_t)b * T + t] != 0u) ? 0.0f : -INFINITY;
+// One block per branch b: its Tpad bias words, and after all B rows of them
+// the branch's key count (one past its last valid key; 0 if none).
+__global__ __launch_bounds__(256) void key_bias_kernel(const uint32_t* __restrict__ mask, int T, int Tpad,
+                                                       float* __restrict__ kbias, int* __restrict__ nkeys) {
+  const int b = blockIdx.x;
+  int last = 0;
+  for (int t = threadIdx.x; t < Tpad; t += 256) {
+    const bool valid = t < T && mask[(size_t)b * T + t] != 0u;
+    kbias[(size_t)b * Tpad + t] = valid ? 0.0f : -INFINITY;
+    if (valid) last = t + 1;
+  }
+  __shared__ int wmax[4];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off, kWave));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = last;
+  __syncthreads();
+  if (threadIdx.x == 0) nkeys[b] = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
 }
 
 hipError_t launch_key_bias(const uint32_t* mask, int B, int T, int Tpad, float* kbias,
                            hipStream_t stream) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
-  const int n = B * Tpad;
-  hipLaunchKernelGGL(key_bias_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, mask, B, T, Tpad,
-                     kbias);
+  hipLaunchKernelGGL(key_bias_kernel, dim3(B), dim3(256), 0, stream, mask, T, Tpad, kbias,
+                     reinterpret_cast<int*>(kbias + (size_t)B * Tpad));
   return hipGetLastError();
 }
 
 template <int NBUF, int G, int QB, int NQW>
 static void launch_attention_shape(const half_t* Q, const half_t* K, const half_t* Vt,
                                    const float* kbias, half_t* O, int B, int T, int Tpad,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, bool branch_keys = false) {
   constexpr int qwg = 16 * QB * NQW;
-  hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW>), dim3((T + qwg - 1) / qwg * 8 * B),
-                     dim3(64 * G * NQW), 0, stream, Q, K, Vt, kbias, O, T, Tpad);
+  const dim3 grid((T + qwg - 1) / qwg * 8 * B), block(64 * G * NQW);
+  if (branch_keys)
+    hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW, true>), grid, block, 0, stream, Q, K, Vt,
+                       kbias, O, T, Tpad);
+  else
+    hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW, false>), grid, block, 0, stream, Q, K, Vt,
+                       kbias, O, T, Tpad);
 }
 
 hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             const float* kbias, half_t* O, int B, int T, int Tpad,
-                            hipStream_t stream) {
+                            hipStream_t stream, bool branch_keys) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
   // Shapes swept on MI355X (B = 2, us per launch, head-per-XCD mapping):
   //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves, 2 buffers   3.5 / 4.9
@@ -420,11 +445,11 @@ hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
   // bit-identical whichever is chosen; the choice depends on the padded
   // length only, never on the batch.
   if (Tpad <= 512)
-    launch_attention_shape<2, 2, 1, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
+    launch_attention_shape<2, 2, 1, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
   else if (Tpad <= kAttnDeepMaxTpad)
-    launch_attention_shape<3, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
+    launch_attention_shape<3, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
   else
-    launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream);
+    launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
   return hipGetLastError();
 }
 

@@ -220,6 +220,9 @@ class Engine {
   bool lr_f32_ = true;
   hipStream_t stream_ = nullptr;
   bool use_graph_ = true;
+  // Set while a decode of a batch with a request shorter than T is enqueued:
+  // its attention launches skip each branch's fully masked key tiles.
+  bool branch_keys_ = false;
   std::unique_ptr<Weights> w_;
   std::unique_ptr<Workspace> ws_;
   std::unique_ptr<Vocoder> voc_;
@@ -275,9 +278,10 @@ class Engine {
     uint64_t last_use = 0;  // use_tick_ of the latest launch
   };
   // Captured whole-decode graphs, least recently used evicted past
-  // kMaxGraphs.  key: nreq, T, steps, cfg bits, vtrace ptr, io pointers.
+  // kMaxGraphs.  key: nreq, T, steps, cfg bits, vtrace ptr, io pointers,
+  // whether some request is shorter than T.
   std::map<std::tuple<int, int, int, uint32_t, const void*, const void*, const void*, const void*,
-                      const void*, const void*>,
+                      const void*, const void*, bool>,
            GraphEntry>
       graphs_;
   uint64_t use_tick_ = 0;

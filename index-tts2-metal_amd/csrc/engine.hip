@@ -391,7 +391,7 @@ struct Workspace {
   half_t* gate16;
   float* fin;
   uint32_t* mask;
-  float* kbias;  // [B][Tpad] attention key bias (0 valid, -inf masked/padding), from mask
+  float* kbias;  // [B][Tpad] attention key bias (0 valid, -inf masked/padding), then [B] key counts
   uint32_t* P;
   float2* rope;
   float* tvals;
@@ -843,7 +843,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   h(r * 512); h(r * kHgLd); h(r * 512);
   f(r * 512); h(r * 512); f(r * 512); f(r * 512); h(r * 512); f(r * 512);
   bytes += (r * 4 + 255) / 256 * 256 + ((size_t)cReq * 4 + 255) / 256 * 256;
-  f((size_t)cRpad);
+  f((size_t)cRpad + cB);
   f((size_t)cT * 64);
   f(cS); f((size_t)cS * 256); f((size_t)cS * 512); f((size_t)cS * 512); f((size_t)cS * 512);
   f((size_t)cS * kTcondPerStep);
@@ -880,7 +880,7 @@ void Engine::ensure_workspace(int B, int T, int S, int nreq) {
   ws.gate16 = H(r * 512);
   ws.fin = F(r * 512);
   ws.mask = static_cast<uint32_t*>(a.take(r * 4));
-  ws.kbias = F((size_t)cRpad);
+  ws.kbias = F((size_t)cRpad + cB);
   ws.P = static_cast<uint32_t*>(a.take((size_t)cReq * 4));
   ws.rope = reinterpret_cast<float2*>(F((size_t)cT * 64));
   ws.tvals = F(cS);
@@ -1046,7 +1046,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, s));
   }
-  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, s));
+  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, s, branch_keys_));
   {
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
@@ -1235,9 +1235,21 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
     }
   }
 
+  // A batch with a request shorter than T lets the attention skip each
+  // branch's key tiles after its last valid key (a different graph than a
+  // full-length batch of the same shape; either is correct for both).
+  bool ragged = false;
+  for (int r = 0; r < nreq; ++r) ragged = ragged || valid_T[r] < (uint32_t)T;
   // The Euler state lives in ws.x_cur; x_out receives a copy at the end.
   auto enqueue_all = [&]() {
-    enqueue_decode(x0, prompt, cond, style, nreq, T, steps, cfg, vtrace, tb);
+    branch_keys_ = ragged;
+    try {
+      enqueue_decode(x0, prompt, cond, style, nreq, T, steps, cfg, vtrace, tb);
+    } catch (...) {
+      branch_keys_ = false;
+      throw;
+    }
+    branch_keys_ = false;
     HIP_OK(launch_copy_f32(ws.x_cur, x_out, (size_t)nreq * T * 80, stream_));
   };
   if (!use_graph_) {
@@ -1248,7 +1260,7 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
   std::memcpy(&cfg_bits, &cfg, 4);
   auto key = std::make_tuple(nreq, T, steps, cfg_bits, (const void*)vtrace, (const void*)x0,
                              (const void*)prompt, (const void*)cond, (const void*)style,
-                             (const void*)x_out);
+                             (const void*)x_out, ragged);
   auto it = graphs_.find(key);
   if (it == graphs_.end()) {
     if (graphs_.size() >= kMaxGraphs) {
@@ -1519,7 +1531,9 @@ void Engine::stage_attention_core(const float* in, const uint32_t* mask, int B, 
   g.M = R; g.N = 1536; g.K = 512; g.A = ws.n16; g.lda = 512; g.W = W.qkv_w[layer]; g.ldw = 512;
   g.T = T; g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, stream_));
-  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, stream_));
+  // Per-branch key tiles: each branch stops after the key tile holding its
+  // last unmasked key (the decode takes this form for ragged batches).
+  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, stream_, true));
   GemmArgs o;
   o.M = R; o.N = 512; o.K = 512; o.A = ws.o16; o.lda = 512; o.W = W.wo_w[layer]; o.ldw = 512;
   o.colperm = 1;

@@ -21,11 +21,15 @@ hipError_t launch_norm_bias(const float* ab, int ab_ld, int S, const half_t* W, 
 hipError_t launch_adaln(const float* x, const float* shift, const float* scale, half_t* out16,
                         int rows, hipStream_t s);
 // Masked attention (attention.hip).  kbias [B][Tpad]: 0 for a valid key,
-// -inf for a masked or padding key, as launch_key_bias builds it from the
-// [B][T] 0/1 key mask.
+// -inf for a masked or padding key, followed by B int32 key counts (one past
+// each branch's last valid key), as launch_key_bias builds them from the
+// [B][T] 0/1 key mask into a buffer of B * Tpad + B words.  With
+// branch_keys, a branch's key tiles after its last valid key are skipped
+// (they are fully masked: the result is the same up to the split of the
+// keys between the kernel's two groups); worth it for padded batches.
 hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             const float* kbias, half_t* O, int B, int T, int Tpad,
-                            hipStream_t stream);
+                            hipStream_t stream, bool branch_keys = false);
 hipError_t launch_key_bias(const uint32_t* mask, int B, int T, int Tpad, float* kbias,
                            hipStream_t stream);
 
