@@ -13,8 +13,11 @@
 // once per mask, followed by B int words: each branch's key count, one past
 // its last valid key).  Output O is token-major [B*T][512] f16, heads
 // concatenated in head order.  The BRANCH_KEYS variant stops each branch
-// after the tile holding its last valid key; the tiles it skips are fully
-// masked, so both variants give bit-identical results.
+// after the tile holding its last valid key.  The tiles it skips are fully
+// masked (they would add exact zeros), but the two key groups then split the
+// branch's own tile count, so the partial sums associate as they would for
+// that branch decoded at its own padded length: the two variants agree to
+// rounding, not bit for bit.
 //
 // Keys are consumed in tiles of 64: the K tile, the V^T tile and the tile's
 // bias words are copied global -> LDS with direct loads into a ring of NBUF
@@ -147,8 +150,8 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
   const half_t* Vh = Vt + head * 64 * Tpad;
   const float* brow = kbias + (size_t)b * Tpad;
   // Key tiles: every tile, or with BRANCH_KEYS only this branch's tiles up
-  // to its last valid key (the tiles after it are fully masked and would add
-  // exact zeros), at least one.
+  // to its last valid key (the tiles after it are fully masked), at least
+  // one.  The groups below split whichever count this is.
   int ntiles = Tpad / 64;
   if constexpr (BRANCH_KEYS) {
     const int nk = reinterpret_cast<const int*>(kbias + (size_t)(gridDim.x / (8 * nqb)) * Tpad)[b];
