@@ -267,7 +267,20 @@ def test_single_token_decode_is_finite(mit2, ctx):
 
 def test_invalid_arguments_raise(mit2, ctx):
     x0, prompt, cond, style = inputs(mit2, 8, 2, 3)
-    with pytest.raises(mit2.Mit2CfmError):
-        ctx.decode(x0, np.zeros((9, 80), np.float32), cond, style, 2, 0.7)  # P > T
-    with pytest.raises(mit2.Mit2CfmError):
-        ctx.decode(x0, prompt, cond, style, 0, 0.7)  # no steps
+    before = ctx.decode(x0, prompt, cond, style, 2, 0.7)
+
+    def rejected(call):
+        with pytest.raises(mit2.Mit2CfmError) as e:
+            call()
+        assert e.value.status == mit2.E_ARG
+
+    rejected(lambda: ctx.decode(x0, np.zeros((9, 80), np.float32), cond, style, 2, 0.7))  # P > T
+    rejected(lambda: ctx.decode(x0, prompt, cond, style, 0, 0.7))  # no steps
+    rejected(lambda: ctx.decode(x0, prompt, cond, style, 2, -0.5))  # negative cfg_rate
+    rejected(lambda: ctx.decode(x0, prompt, cond, style, 2, float("nan")))
+    X0, PR, CO, ST = x0[None], np.zeros((1, 8, 80), np.float32), cond[None], style[None]
+    rejected(lambda: ctx.decode_batched([0], [0], X0, PR, CO, ST, 2, 0.7))  # empty request
+    rejected(lambda: ctx.decode_batched([9], [2], X0, PR, CO, ST, 2, 0.7))  # longer than T
+    rejected(lambda: ctx.decode_batched([4], [5], X0, PR, CO, ST, 2, 0.7))  # prompt > request
+    # Rejected calls leave the context as it was: the same decode gives the same bits.
+    assert np.array_equal(ctx.decode(x0, prompt, cond, style, 2, 0.7), before)
