@@ -74,14 +74,23 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
-__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + __expf(-v)); }
+// The GEMM epilogues' activations (the decode's gated WaveNet conv and the
+// SwiGLU feed-forward, whose outputs are stored as f16) use the hardware
+// exponential and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each)
+// instead of an IEEE division and libm's tanhf: the epilogue of the k=5 conv
+// GEMM runs 5% faster and w1|w3's 3%.
+__device__ __forceinline__ float fast_rcp(float v) { return __builtin_amdgcn_rcpf(v); }
+__device__ __forceinline__ float sigmoid_f(float v) { return fast_rcp(1.0f + __expf(-v)); }
+__device__ __forceinline__ float silu_fast(float v) { return v * fast_rcp(1.0f + __expf(-v)); }
 
-// tanh with the reference kernel's saturation (|a| > 20 -> +-1).
+// tanh with the reference kernel's saturation (|a| > 20 -> +-1), as
+// 1 - 2 / (e^(2a) + 1): the absolute error is a few 1e-8 (near 0 the
+// rounding of e^(2a) to fp32 dominates), below the f16 rounding of the
+// gated product it feeds.
 __device__ __forceinline__ float tanh_sat(float a) {
   if (a > 20.0f) return 1.0f;
   if (a < -20.0f) return -1.0f;
-  return tanhf(a);
+  return 1.0f - 2.0f * fast_rcp(__expf(2.0f * a) + 1.0f);
 }
 
 // Reflect index for padding (k-tap conv, reflect mode).  Any integer maps into

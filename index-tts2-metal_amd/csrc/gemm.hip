@@ -799,7 +799,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
           const int c = group * 16 + 4 * lg;
           float y[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) y[r] = (ve[r] / (1.0f + __expf(-ve[r]))) * vo[r];
+          for (int r = 0; r < 4; ++r) y[r] = silu_fast(ve[r]) * vo[r];
           st16(p.C16 + (size_t)m * p.ldc16 + c, y[0], y[1], y[2], y[3]);
         } else if constexpr (EPI == EPI_GATE) {
           const int c = group * 16 + 4 * lg;
