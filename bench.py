@@ -423,7 +423,7 @@ def gpt_section(a, mit2cfm, tensors, torch):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py: this build targets one GPU; --gpus {a.gpus} is not supported "
+        print(f"bench.py: the library runs on one GPU; --gpus {a.gpus} is not supported "
               "(multi-GPU sharding is design-only).", file=sys.stderr)
         sys.exit(2)
 

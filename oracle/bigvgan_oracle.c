@@ -3,7 +3,8 @@
  * primitives (the consumer of the DiT-CFM mel).
  *
  * TEST INFRASTRUCTURE ONLY (see cfm_oracle.h): loaded by tests/, smoke() and
- * bench.py's cpu_baseline leg as the checker or the timed CPU baseline.
+ * bench.py's cpu_baseline leg, to compare results with or as the timed CPU
+ * baseline.
  *
  * Each function keeps the reference's loop order and scalar fp32
  * accumulation; threads split output tokens only, so results are bit-identical

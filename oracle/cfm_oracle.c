@@ -1,8 +1,8 @@
 /*
  * cfm_oracle.c -- CPU restatement of the reference's fp32 DiT-CFM path.
  *
- * TEST INFRASTRUCTURE ONLY (see cfm_oracle.h): the checker for the HIP path
- * and the timed CPU baseline.  Nothing in the product library calls it.
+ * TEST INFRASTRUCTURE ONLY (see cfm_oracle.h): the reference the HIP path is
+ * compared with, and the timed CPU baseline.  Nothing in the product library calls it.
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp, no fast-math).
  * -ffp-contract=off keeps every multiply and add a separately rounded IEEE

@@ -3,8 +3,8 @@
  * reference path (the "oracle").
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * or the timed CPU baseline.  The product library never links or calls it.
+ * cpu_baseline leg of bench.py may load this library, and only to compare
+ * results with or as the timed CPU baseline.  The product library never links or calls it.
  *
  * Every function restates one reference function (file:line given beside it,
  * paths relative to the reference repository root) with the same loop order

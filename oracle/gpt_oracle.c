@@ -4,8 +4,8 @@
  * gelu_new, learned mel position embeddings, ln_f + final_norm + mel_head)
  * as the reference's fp32 CPU path computes it (runtime/impl/gpt.cpp).
  *
- * TEST INFRASTRUCTURE ONLY (see cfm_oracle.h): the checker of the GPU decode
- * and the timed CPU baseline; the product never links it.
+ * TEST INFRASTRUCTURE ONLY (see cfm_oracle.h): the reference the GPU decode
+ * is compared with, and the timed CPU baseline; the product never links it.
  *
  * Weights are set by their checkpoint names in the checkpoint's layouts:
  * the GPT-2 Conv1D matrices are [in][out] and are transposed to [out][in]

@@ -1,7 +1,8 @@
 """ctypes binding of the CPU oracle (oracle/build/libcfm_oracle.so).
 
 TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+cpu_baseline leg of bench.py, to compare results with or as the timed CPU
+baseline.
 The product path never imports this module.
 """
 from __future__ import annotations

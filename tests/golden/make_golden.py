@@ -3,8 +3,8 @@
 The reference holds no golden vectors for this path (its PyTorch golden
 generators need the upstream checkpoints), so these fixtures are the
 oracle's outputs on seeded synthetic weights and inputs; the oracle itself is
-pinned by tests/test_oracle_*.py.  Inputs are regenerated from their seeds on
-the GPU box, so only outputs (and the oracle states the per-step velocity
+pinned by tests/test_oracle_*.py.  Inputs are regenerated from their seeds
+where the tests run, so only outputs (and the oracle states the per-step velocity
 check starts from) are stored.
 
     python tests/golden/make_golden.py [config1|config2|config3 ...]

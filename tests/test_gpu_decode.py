@@ -1,7 +1,7 @@
 """GPU parity of the estimator forward and of the full CFG Euler decode, through
 the C ABI, against the CPU oracle on identical seeded inputs.
 
-Bars (north_star): per-step velocity rel-L2 <= 2e-3 (one estimator forward on
+Bars: per-step velocity rel-L2 <= 2e-3 (one estimator forward on
 the oracle's own state for that step) and final mel rel-L2 <= 1e-2 after the
 decode.  The f16 GEMM operands are the only source of difference (see
 test_gpu_stages.py), so both bars are met with margin; the measured values

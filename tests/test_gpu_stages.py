@@ -8,8 +8,8 @@ and {1,0,1,1,1,0}); larger T adds multi-tile attention and real widths.
 Tolerances.  The HIP path feeds the matrix cores f16 operands (activations
 rounded to f16, fp32 accumulation; the reference's Metal path stages A in half
 the same way, kernels.metal:68-76) while the oracle is fp32 throughout, so a
-stage agrees to f16 rounding: rel-L2 <= 2e-3, the north_star's per-step
-velocity bar.  op_linear on f16-representable operands differs only by fp32
+stage agrees to f16 rounding: rel-L2 <= 2e-3, the per-step velocity bar of
+the decode.  op_linear on f16-representable operands differs only by fp32
 summation order: rel-L2 <= 1e-5.
 """
 from __future__ import annotations
@@ -47,7 +47,7 @@ def f16r(a):
 
 
 # ------------------------------------------------------------------ GEMM
-HOT_SHAPES = [  # (N, K) of every GEMM in one estimator step
+HOT_SHAPES = [  # (N, K) of every GEMM in one estimator step (the GEMM family)
     (512, 512), (512, 128), (512, 896), (1536, 512), (3072, 512), (512, 1536), (512, 1024),
     (512, 640), (1024, 512), (1024, 2560), (512, 512),
 ]

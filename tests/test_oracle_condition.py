@@ -96,7 +96,7 @@ def test_synthetic_lr_tensors_shapes(mit2):
 
 @pytest.mark.parametrize("tokens", [1, 9, 602])
 def test_groupnorm1_f64stats_matches_torch(tokens):
-    """The checker variant (statistics in double) is torch's float64 group_norm
+    """The double-statistics variant is torch's float64 group_norm
     up to the final float rounding."""
     rng = np.random.default_rng(50 + tokens)
     x = (rng.standard_normal((tokens, 512)) * 3 + 0.7).astype(np.float32)
