@@ -37,8 +37,6 @@
 
 namespace mit2hip {
 
-constexpr int kAttnDeepMaxTpad = 1024;  // longest padded sequence with a 3-tile ring
-
 
 template <int N>
 __device__ __forceinline__ void attn_wait_vmcnt() {
@@ -441,16 +439,16 @@ hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
   // Shapes swept on MI355X (B = 2, us per launch, head-per-XCD mapping):
   //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves, 2 buffers   3.5 / 4.9
-  //   T = 860:        64 queries x 2 key groups, 16-query waves, 3 buffers   8.7 (2 buffers: 8.8)
-  //   T = 1348:       64 queries x 2 key groups, 16-query waves, 2 buffers  17.9 (3 buffers: 21.4)
-  //   T = 3000:       64 queries x 2 key groups, 16-query waves, 2 buffers  55.0
-  // Every shape splits the keys into the same two groups, so the result is
-  // bit-identical whichever is chosen; the choice depends on the padded
-  // length only, never on the batch.
+  //   T = 860:        64 queries x 2 key groups, 16-query waves, 2 buffers   8.5 (3 buffers: 8.6)
+  //   T = 1348:       64 queries x 2 key groups, 16-query waves, 2 buffers  17.5 (3 buffers: 21.4)
+  //   T = 3000:       64 queries x 2 key groups, 16-query waves, 2 buffers  52-54
+  // 32-query waves (two 16-query blocks per wave) are slower at every length
+  // (T = 860 / 1348 / 3000: 10.4 / 20.9 / 59-68).  Every shape splits the
+  // keys into the same two groups, so the result is bit-identical whichever
+  // is chosen; the choice depends on the padded length only, never on the
+  // batch.
   if (Tpad <= 512)
     launch_attention_shape<2, 2, 1, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
-  else if (Tpad <= kAttnDeepMaxTpad)
-    launch_attention_shape<3, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
   else
     launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
   return hipGetLastError();

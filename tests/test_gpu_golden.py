@@ -152,7 +152,7 @@ def _make_golden():
 def test_config4_long_form_velocity(mit2, orc, golden_ctx):
     """T=3000 (P=258): the CFG-pair velocity at t=0 on x0 and at steps 12 and 24
     of 25 on flow states blended towards a mel-like field, against the oracle
-    (Tpad > 2048 takes the 32-query attention path)."""
+    (the long-sequence attention: 47 key tiles in two groups)."""
     mg = _make_golden()
     meta, ref = load("config4")
     T, P, steps, cfg = meta["T"], meta["P"], meta["steps"], meta["cfg"]
