@@ -50,6 +50,20 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Issue order for one K step of the pipelined loop: each of ND fragment
+// reads beside one MFMA (the next K step needs them first), then each of NV
+// stage loads beside one, then the remaining MFMAs; reads or loads left over
+// when the NM MFMAs run out follow in the same order.
+template <int ND, int NV, int NM>
+__device__ __forceinline__ void interleave() {
+  static_for<0, (ND + NV > NM ? ND + NV : NM)>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    if constexpr (i < ND) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);            // DS read
+    else if constexpr (i < ND + NV) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM
+    if constexpr (i < NM) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // MFMA
+  });
+}
+
 struct TileMap {
   int nM, nN;  // tile grid
   int Xm, Xn;  // XCD rectangle grid, Xm * Xn == 8
@@ -67,9 +81,16 @@ struct TileMap {
   }
 };
 
-template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN, int KG, int SP>
-__global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, TileMap tmap) {
-  constexpr int NW = WM * WN;                // wavefronts per K group, WM along M x WN along N
+template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN, int KG, int SP, int PIPE>
+__global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(GemmArgs p, TileMap tmap) {
+  // K split.  The product over K is summed in KG parts of equal length, added
+  // in part order at the end (the same bits whichever form computes them).
+  // PIPE = 0: part g is walked by its own group of WM x WN wavefronts with
+  // its own LDS region.  PIPE = 1: one group of wavefronts walks all of K,
+  // holding one accumulator set per part, with the pipelined main loop
+  // below.
+  constexpr int KW = PIPE ? 1 : KG;          // wavefront groups
+  constexpr int NW = WM * WN;                // wavefronts per group, WM along M x WN along N
   constexpr int CPR = SK / 8;                // 16-byte slots per stage row
   constexpr int LA = BM * CPR / (64 * NW);   // DMA instructions per wave per stage (A)
   constexpr int LB = BN * CPR / (64 * NW);   // (W)
@@ -83,10 +104,11 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   static_assert(LA >= 1 && LB >= 1, "tile too small for the workgroup");
   static_assert(LA * 64 * NW == BM * CPR && LB * 64 * NW == BN * CPR, "uneven DMA split");
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave sub-tile must be whole MFMA blocks");
-  static_assert(L * (NST - 1) < 64, "too many loads in flight");
+  static_assert(L * (NST - 1 + PIPE) < 64, "too many loads in flight");
   static_assert(CPR == 8 || CPR >= 16, "stage width");
   static_assert(KG == 1 || ((KG == 2 || KG == 4) && EPI != EPI_QKV),
                 "K groups: 2 or 4, and the QKV epilogue needs every wave");
+  static_assert(!PIPE || (SP == 0 && (KG == 1 || KG == 2)), "pipelined loop: f16 operands, K in 1 or 2 parts");
   static_assert(SP >= 0 && SP <= 2, "split mode");
 
   // One __shared__ object per stage and operand, declared here so each kernel
@@ -94,24 +116,24 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   // let the compiler keep only the explicit vmcnt waits).
   // With KG = 2 K groups, each group has its own region in every buffer;
   // split operands keep their lo halves after all the groups' hi halves.
-  __shared__ __attribute__((aligned(1024))) half_t sA0[AS * KG * BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA1[AS * KG * BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? AS * KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? AS * KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA4[NST > 4 ? AS * KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA5[NST > 5 ? AS * KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA6[NST > 6 ? AS * KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA7[NST > 7 ? AS * KG * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB0[WS * KG * BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB1[WS * KG * BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? WS * KG * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? WS * KG * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB4[NST > 4 ? WS * KG * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB5[NST > 5 ? WS * KG * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB6[NST > 6 ? WS * KG * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB7[NST > 7 ? WS * KG * BN * SK : 8];
-  constexpr int kALo = KG * BM * SK;  // offset of a stage's lo half in its buffer
-  constexpr int kWLo = KG * BN * SK;
+  __shared__ __attribute__((aligned(1024))) half_t sA0[AS * KW * BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA1[AS * KW * BM * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? AS * KW * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? AS * KW * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA4[NST > 4 ? AS * KW * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA5[NST > 5 ? AS * KW * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA6[NST > 6 ? AS * KW * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA7[NST > 7 ? AS * KW * BM * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB0[WS * KW * BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB1[WS * KW * BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? WS * KW * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? WS * KW * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB4[NST > 4 ? WS * KW * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB5[NST > 5 ? WS * KW * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB6[NST > 6 ? WS * KW * BN * SK : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sB7[NST > 7 ? WS * KW * BN * SK : 8];
+  constexpr int kALo = KW * BM * SK;  // offset of a stage's lo half in its buffer
+  constexpr int kWLo = KW * BN * SK;
   static_assert(NST >= 2 && NST <= 8, "two to eight stages");
   const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / (64 * NW));  // K group of this wave
   auto bufA = [&](auto st) -> half_t* {
@@ -121,7 +143,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     else if constexpr (s == 2) b = sA2; else if constexpr (s == 3) b = sA3;
     else if constexpr (s == 4) b = sA4; else if constexpr (s == 5) b = sA5;
     else if constexpr (s == 6) b = sA6; else b = sA7;
-    return KG == 1 ? b : b + kg * BM * SK;
+    return KW == 1 ? b : b + kg * BM * SK;
   };
   auto bufB = [&](auto st) -> half_t* {
     constexpr int s = decltype(st)::value;
@@ -130,7 +152,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     else if constexpr (s == 2) b = sB2; else if constexpr (s == 3) b = sB3;
     else if constexpr (s == 4) b = sB4; else if constexpr (s == 5) b = sB5;
     else if constexpr (s == 6) b = sB6; else b = sB7;
-    return KG == 1 ? b : b + kg * BN * SK;
+    return KW == 1 ? b : b + kg * BN * SK;
   };
 
   int tile_m, tile_n;
@@ -147,7 +169,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   const int lg = lane >> 4;
   // K group kg walks stages [kg * KT, kg * KT + KT) (the host makes K / SK a
   // multiple of KG, so both groups meet the same barriers).
-  const int KT = p.K / SK / KG;
+  const int KT = p.K / SK / KW;
   const int kt_lo = kg * KT;
 
   // Output ownership.  The MFMA is issued with W as its first operand, so the
@@ -163,14 +185,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   const bool perm = EPI == EPI_F32 && p.colperm;
   auto colj = [&](int j) { return perm ? col_base + 32 * (j >> 1) + 4 * lg + 4 * (j & 1) : col_base + 16 * j; };
 
-  // Epilogue operands that do not depend on the product are fetched now, so
-  // their latency hides behind the K loop.
+  // Epilogue operands that do not depend on the product are fetched before
+  // the K loop, so their latency hides behind it (PIPE = 1: after the loop,
+  // so they do not hold registers beside its larger tiles).
   constexpr bool kPreA =
       EPI == EPI_F32 || EPI == EPI_RESSKIP || EPI == EPI_FINALSKIP || EPI == EPI_RESAVG;
   constexpr bool kPreB = EPI == EPI_FINALSKIP;
   float4 pre_a[kPreA ? MI : 1][kPreA ? NI : 1];
   float4 pre_b[kPreB ? MI : 1][kPreB ? NI : 1];
-  if constexpr (kPreA) {
+  auto load_pre = [&]() {
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int m = row_base + 16 * i;
@@ -195,7 +218,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
         }
       }
     }
-  }
+  };
+  if constexpr (kPreA && !PIPE) load_pre();
 
   // Consumer side of a folded AdaRMSNorm: the producer's kSsqParts partial
   // sums of squares of each of this lane's rows (K = 512 values) are fetched
@@ -408,15 +432,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
 #pragma unroll
   for (int kk = 0; kk < SK / 32; ++kk) {
     const int sw = ((kk * 4 + lg) ^ swz(lr)) << 3;
-    a_lane[kk] = (KG == 1 ? 0 : kg * BM * SK) + (wm * WTM + lr) * SK + sw;
-    b_lane[kk] = (KG == 1 ? 0 : kg * BN * SK) + (wn * WTN + lr) * SK + sw;
+    a_lane[kk] = (KW == 1 ? 0 : kg * BM * SK) + (wm * WTM + lr) * SK + sw;
+    b_lane[kk] = (KW == 1 ? 0 : kg * BN * SK) + (wn * WTN + lr) * SK + sw;
 #if defined(__HIP_DEVICE_COMPILE__)
     __asm__("" : "+v"(a_lane[kk]), "+v"(b_lane[kk]));
 #endif
   }
   auto compute = [&](auto st) {
-    const half_t* sa = bufA(st) - (KG == 1 ? 0 : kg * BM * SK);
-    const half_t* sb = bufB(st) - (KG == 1 ? 0 : kg * BN * SK);
+    const half_t* sa = bufA(st) - (KW == 1 ? 0 : kg * BM * SK);
+    const half_t* sb = bufB(st) - (KW == 1 ? 0 : kg * BN * SK);
 #pragma unroll
     for (int kk = 0; kk < SK / 32; ++kk) {
       half8 af[MI];
@@ -454,6 +478,102 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
     }
   };
 
+  float rsv[kNormIn ? MI : 1];
+  auto norm_in = [&]() {
+    if constexpr (kNormIn) {
+      // the partials (issued before the NST - 1 + PIPE first stages) have landed
+      wait_vmcnt<L * (NST - 1 + PIPE)>();
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kSsqParts / 4; ++u)
+          ss += (ssq_pre[i][u].x + ssq_pre[i][u].y) + (ssq_pre[i][u].z + ssq_pre[i][u].w);
+        rsv[i] = p.ssq_in ? 1.0f / sqrtf(ss / 512.0f + 1e-5f) : 1.0f;
+      }
+    }
+  };
+  int kt0 = 0;
+  floatx4 acc1[PIPE && KG == 2 ? MI : 1][PIPE && KG == 2 ? NI : 1];  // PIPE: the second K part
+  if constexpr (PIPE) {
+    // Pipelined loop.  The fragments of a K step are read into one of two
+    // register slots while the MFMAs of the previous step run, and the one
+    // barrier of a stage sits before its last K step:
+    //   step kk < KK-1: read step kk+1's fragments; MFMAs of step kk;
+    //   last step:      wait for this wave's reads (the stage buffer is free)
+    //                   and for its share of stage kt+1; barrier; refill this
+    //                   stage's buffer with stage kt+NST; read step 0 of stage
+    //                   kt+1; MFMAs of the last step.
+    // So the MFMAs after the barrier need no LDS read, and a stage is in
+    // flight for NST-1 stage times.  The MFMAs per output element are the
+    // same instructions in the same K order as with PIPE = 0.
+    constexpr int KK = SK / 32;
+    static_assert(KK % 2 == 0, "two register slots alternate over an even number of K steps");
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc1[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    half8 fa[2][MI], fb[2][NI];
+    auto frag_read = [&](auto st, auto kkc, auto slot) {
+      constexpr int kk = decltype(kkc)::value;
+      constexpr int sl = decltype(slot)::value;
+      const half_t* sa = bufA(st);
+      const half_t* sb = bufB(st);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) fa[sl][i] = *reinterpret_cast<const half8*>(sa + a_lane[kk] + i * 16 * SK);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) fb[sl][j] = *reinterpret_cast<const half8*>(sb + b_lane[kk] + j * 16 * SK);
+    };
+    auto mma = [&](floatx4 (&c)[MI][NI], auto slot) {
+      constexpr int sl = decltype(slot)::value;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) c[i][j] = mfma16x16x32(fb[sl][j], fa[sl][i], c[i][j]);
+    };
+    // Every ring buffer is filled before the loop: stage kt's buffer is
+    // refilled at stage kt's barrier.
+    static_for<0, NST>([&](auto st) { issue(st, (int)decltype(st)::value); });
+    norm_in();
+    wait_vmcnt<L * (NST - 1)>();  // this wave's share of stage 0 has landed
+    __builtin_amdgcn_s_barrier();  // ... for every wave
+    frag_read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{},
+              std::integral_constant<int, 0>{});
+    // Branch-free loop bodies (a branch would make the compiler's wait
+    // counts conservative where paths join): the host launches this form
+    // only when each K part is a whole number of NST-stage rounds, so the
+    // second part starts again at ring buffer 0.
+    auto stage = [&](auto st, int kt, floatx4 (&c)[MI][NI]) {
+      constexpr int s = decltype(st)::value;
+      static_for<0, KK>([&](auto kkc) {
+        constexpr int kk = decltype(kkc)::value;
+        constexpr int cur = kk & 1;
+        using Nxt = std::integral_constant<int, cur ^ 1>;
+        if constexpr (kk + 1 < KK) {
+          frag_read(st, std::integral_constant<int, kk + 1>{}, Nxt{});
+          mma(c, std::integral_constant<int, cur>{});
+          interleave<MI + NI, 0, MI * NI>();
+        } else {
+          wait_lgkmcnt0();               // this wave's reads of stage kt have returned
+          wait_vmcnt<L * (NST - 2)>();   // its share of stage kt+1 has landed
+          __builtin_amdgcn_s_barrier();  // ... for every wave
+          issue(st, kt + NST);
+          frag_read(std::integral_constant<int, (s + 1) % NST>{}, std::integral_constant<int, 0>{}, Nxt{});
+          mma(c, std::integral_constant<int, cur>{});
+          interleave<MI + NI, L, MI * NI>();
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the K steps in program order
+      });
+    };
+    const int kpart = KT / KG;  // stages per K part, a multiple of NST
+    for (; kt0 < kpart; kt0 += NST)
+      static_for<0, NST>([&](auto st) { stage(st, kt0 + (int)decltype(st)::value, acc); });
+    if constexpr (KG == 2) {
+      for (; kt0 < KT; kt0 += NST)
+        static_for<0, NST>([&](auto st) { stage(st, kt0 + (int)decltype(st)::value, acc1); });
+    }
+    if constexpr (kPreA) load_pre();
+  }
   // Pipeline, one barrier per stage.  At the top of stage kt this wave waits
   // for its own share of stage kt (NST-2 younger stages may stay in flight);
   // the barrier then says every wave's share has landed AND every wave has
@@ -462,29 +582,19 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   // past the last stage is a one-address load into a buffer that is not read
   // again), which keeps the compiler from adding waits of its own; the last
   // KT % NST stages are resident when the loop exits.
-  static_for<0, NST - 1>([&](auto st) { issue(st, (int)decltype(st)::value); });
-  float rsv[kNormIn ? MI : 1];
-  if constexpr (kNormIn) {
-    wait_vmcnt<L * (NST - 1)>();  // the partials (issued before the stages) have landed
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      float ss = 0.0f;
-#pragma unroll
-      for (int u = 0; u < kSsqParts / 4; ++u)
-        ss += (ssq_pre[i][u].x + ssq_pre[i][u].y) + (ssq_pre[i][u].z + ssq_pre[i][u].w);
-      rsv[i] = p.ssq_in ? 1.0f / sqrtf(ss / 512.0f + 1e-5f) : 1.0f;
+  if constexpr (!PIPE) {
+    static_for<0, NST - 1>([&](auto st) { issue(st, (int)decltype(st)::value); });
+    norm_in();
+    for (; kt0 + NST <= KT; kt0 += NST) {
+      static_for<0, NST>([&](auto st) {
+        constexpr int s = decltype(st)::value;
+        wait_vmcnt<L * (NST - 2)>();   // this wave's share of stage kt0+s has landed
+        wait_lgkmcnt0();               // this wave's reads of stage kt0+s-1 have returned
+        __builtin_amdgcn_s_barrier();  // ... for every wave
+        issue(std::integral_constant<int, (s + NST - 1) % NST>{}, kt0 + s + NST - 1);
+        compute(st);
+      });
     }
-  }
-  int kt0 = 0;
-  for (; kt0 + NST <= KT; kt0 += NST) {
-    static_for<0, NST>([&](auto st) {
-      constexpr int s = decltype(st)::value;
-      wait_vmcnt<L * (NST - 2)>();   // this wave's share of stage kt0+s has landed
-      wait_lgkmcnt0();               // this wave's reads of stage kt0+s-1 have returned
-      __builtin_amdgcn_s_barrier();  // ... for every wave
-      issue(std::integral_constant<int, (s + NST - 1) % NST>{}, kt0 + s + NST - 1);
-      compute(st);
-    });
   }
   // Late prefetch: the small per-column epilogue operands are requested
   // before the resident tail stages are computed, so their latency overlaps
@@ -517,9 +627,16 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   }
   wait_vmcnt<0>();  // the tail stages have landed; no DMA outstanding at exit
   __builtin_amdgcn_s_barrier();
-  static_for<0, NST - 1>([&](auto st) {
-    if (kt0 + (int)decltype(st)::value < KT) compute(st);
-  });
+  if constexpr (!PIPE) {
+    static_for<0, NST - 1>([&](auto st) {
+      if (kt0 + (int)decltype(st)::value < KT) compute(st);
+    });
+  } else if constexpr (KG == 2) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] += acc1[i][j];  // part 0 + part 1
+  }
   if constexpr (SP > 0) {
 #pragma unroll
     for (int i = 0; i < MI; ++i)
@@ -532,7 +649,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
   // deterministic) and runs the epilogue.  Each partial (BM x BN fp32) goes
   // into one of the idle ring buffers sB0, sA0, sB1 when those hold a tile,
   // else into a buffer of its own.
-  if constexpr (KG > 1) {
+  if constexpr (KG > 1 && !PIPE) {
     constexpr int kTileBytes = BM * BN * 4;
     constexpr bool kRedInRing = kTileBytes <= KG * BN * SK * 2 &&
                                 (KG < 3 || kTileBytes <= KG * BM * SK * 2) && (KG < 4 || NST >= 2);
@@ -735,8 +852,18 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
         // V tile = BN/64 heads x BM tokens.  Transpose through LDS so that
         // V^T[d][t] is written by consecutive lanes at consecutive t.
         static_assert(BN % 64 == 0, "a v tile must hold whole heads");
-        static_assert(SK >= BM, "the V^T staging tile reuses the first W stage buffer");
-        half_t* st = sB0;  // [BN channels][BM rows], free once every wave is past its last MFMA
+        // The staging tile [BN channels][BM rows] reuses ring buffers, free
+        // once every wave is past its last MFMA: the first W stage buffer when
+        // it is large enough, else 64 channels in each A stage buffer.
+        static_assert(SK >= BM || (SK == 64 && BN <= 64 * NST), "no ring buffer holds the V^T staging tile");
+        auto stg = [&](int c) -> half_t* {
+          if constexpr (SK >= BM) {
+            return sB0 + c * BM;
+          } else {
+            half_t* b = c < 64 ? sA0 : c < 128 ? sA1 : sA2;
+            return b + (c & 63) * BM;
+          }
+        };
         wait_lgkmcnt0();
         __builtin_amdgcn_s_barrier();
         // Blocks (2q, 2q+1) of this wave hold the even / odd channels of one
@@ -753,8 +880,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
             for (int r = 0; r < 4; ++r) {
               const int rl = wm * WTM + i * 16 + lr;
               const int c = 32 * g + 2 * (4 * lg + r);
-              st[c * BM + rl] = (half_t)(rsv[i] * acc[i][2 * q][r] + bev[r]);
-              st[(c + 1) * BM + rl] = (half_t)(rsv[i] * acc[i][2 * q + 1][r] + bov[r]);
+              stg(c)[rl] = (half_t)(rsv[i] * acc[i][2 * q][r] + bev[r]);
+              stg(c + 1)[rl] = (half_t)(rsv[i] * acc[i][2 * q + 1][r] + bov[r]);
             }
         }
         wait_lgkmcnt0();  // this wave's stores have landed before the barrier releases readers
@@ -768,7 +895,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void gemm_kernel(GemmArgs p, Til
             const int b = m / p.T;
             const int t = m - b * p.T;
             for (int c = wave; c < BN; c += NW)
-              p.vt[(((size_t)b * 8 + h0 + (c >> 6)) * 64 + (c & 63)) * p.Tpad + t] = st[c * BM + rl];
+              p.vt[(((size_t)b * 8 + h0 + (c >> 6)) * 64 + (c & 63)) * p.Tpad + t] = stg(c)[rl];
           }
         }
         return;
@@ -875,13 +1002,14 @@ static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
 }
 
 template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM = 2, int WN = 2, int KG = 1,
-          int SP = 0>
+          int SP = 0, int PIPE = 0>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
-  if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K groups need equal stage counts
+  if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K parts need equal stage counts
+  if (PIPE && (a.K / SK / KG) % NST != 0) return hipErrorInvalidValue;  // whole rounds per part
   const TileMap tm = make_tile_map(
       a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z || AM == A_CONVP ? a.conv_c : a.K, BM, BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG, SP>), dim3(8 * tm.per_xcd),
-                     dim3(64 * WM * WN * KG), 0, s,
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG, SP, PIPE>), dim3(8 * tm.per_xcd),
+                     dim3(64 * WM * WN * (PIPE ? 1 : KG)), 0, s,
                      a, tm);
   return hipGetLastError();
 }
@@ -930,6 +1058,26 @@ static bool few_tiles(const GemmArgs& a, int BM, int BN) {
   return (long)((a.M + BM - 1) / BM) * (a.N / BN) < 128;
 }
 
+// Large products (the padded multi-request and long-form decodes) take the
+// pipelined loop (PIPE = 1) with bigger tiles once the tiling still gives
+// every CU a tile: it computes the same MFMAs in the same K order as the
+// tiles above, so the choice changes no bit of a row's result.  Swept at
+// M = 1720 / 6000 / 21568 (B = 2 x T = 860 / 3000, B = 16 x T = 1348):
+//  * k=5 conv (N = 1024, K = 2560): 192x128 tiles, eight wavefronts, a
+//    4-stage ring: 36.0 vs 46.7 us at M = 6000, 139.5 vs 200.9 at 21568
+//    (slower at 1720, where it leaves 184 CUs idle);
+//  * long-K N = 512 products (w2 K = 1536): 192x128 at M = 21568, 46.4 vs
+//    83.2 us; 128x128 at M = 6000, 17.0 vs 24.0 us.
+// The short-K products (K = 512: w1|w3, QKV, wo, res/skip) stay on the
+// tiles above, which the pipelined loop did not beat at any M.
+static long tile_count(const GemmArgs& a, int BM, int BN) {
+  return (long)((a.M + BM - 1) / BM) * (a.N / BN);
+}
+template <int KG, int NST>
+static bool pipe_fits(const GemmArgs& a) {
+  return a.K % (64 * KG * NST) == 0;  // each K part a whole number of rounds of the ring
+}
+
 template <int AM, int EPI>
 static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
   if constexpr (AM == A_CONVP) {
@@ -950,6 +1098,8 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
     // Two K groups (16 wavefronts, the partial tile reduced through the idle
     // ring): 17.1 vs 18.3 us.
     if (a.N % 128 == 0) {
+      if (tile_count(a, 192, 128) >= 256 && pipe_fits<2, 4>(a))
+        return launch_tile<192, 128, 64, 4, AM, EPI, 4, 2, 2, 0, 1>(a, s);
       if (few_tiles(a, 64, 128)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
       return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 2>(a, s);
     }
@@ -964,6 +1114,10 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
     // Long-K N = 512 products (w2 K = 1536, skip-in K = 1024) split K over
     // two wave groups: 9.4 vs 9.8 us and 7.25 vs 7.7 us.
     if (a.K >= 1024 && (a.K / 64) % 2 == 0) {
+      if (a.N % 128 == 0 && pipe_fits<2, 4>(a)) {
+        if (tile_count(a, 192, 128) >= 256) return launch_tile<192, 128, 64, 4, AM, EPI, 4, 2, 2, 0, 1>(a, s);
+        if (tile_count(a, 128, 128) >= 160) return launch_tile<128, 128, 64, 4, AM, EPI, 2, 4, 2, 0, 1>(a, s);
+      }
       if (few_tiles(a, 64, 64)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
       return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
     }
