@@ -150,6 +150,21 @@ mit2cfm_status mit2cfm_synchronize(mit2cfm_ctx* ctx);
 mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on);
 mit2cfm_status mit2cfm_decode_graph_count(mit2cfm_ctx* ctx, uint32_t* count, uint32_t* capacity);
 
+/* Padded rows of a ragged batched decode (mit2cfm_decode_batched[_device]
+ * with some tokens[r] < t_max).  MIT2CFM_PADDING_COMPUTE (default): every
+ * row is computed, the masked estimator at the padded length.
+ * MIT2CFM_PADDING_SKIP: rows from two past each request's valid length on
+ * are not computed (row tiles of every product and query blocks of the
+ * attention stop there; the two rows after the valid ones are kept because
+ * the WaveNet's k=5 conv at the last valid rows reads them).  Valid rows are
+ * bit-identical in both modes; x_out's padded rows are unspecified with
+ * SKIP.  Full-length batches and single decodes are unaffected.  No
+ * reference counterpart (the reference decodes one request per call). */
+#define MIT2CFM_PADDING_COMPUTE 0
+#define MIT2CFM_PADDING_SKIP 1
+mit2cfm_status mit2cfm_set_padding(mit2cfm_ctx* ctx, int32_t mode);
+mit2cfm_status mit2cfm_get_padding(mit2cfm_ctx* ctx, int32_t* mode);
+
 /* ---- arithmetic of the fp32 stages ---------------------------------------------
  * The reference runs the length regulator (run_length_regulator_full_metal,
  * runtime/impl/gpt.cpp:5313; its test bar max-abs 1e-4, :5382-5401) and the
@@ -324,8 +339,13 @@ mit2cfm_status mit2cfm_condition_device(mit2cfm_ctx* ctx, const float* s_infer, 
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Its
  * scratch (the length regulator's operand, conv and statistics buffers) is
  * a static device array of about 13.7 MB that every GPU the library runs on
- * holds until the process ends, shared by every context on that GPU: calls
- * that overlap on one GPU (two streams or threads) race.  codes above
+ * holds until the process ends, shared by every context on that GPU.  Calls
+ * on one GPU are run one after another: each call's stream waits for an
+ * event the previous call recorded after its last kernel (contexts on other
+ * streams or threads included).  A call enqueued while its stream is being
+ * captured into a graph is not ordered that way (a capture may not wait on
+ * work outside it), so replays of such a graph must not overlap other calls
+ * on that GPU: they would race on the scratch.  codes above
  * MIT2CFM_NOALLOC_MAX_CODES (1,761 generated frames) is MIT2CFM_E_ARG.
  * Arguments, outputs, flags and results as for mit2cfm_condition_device. */
 #define MIT2CFM_NOALLOC_MAX_CODES 1024u
@@ -446,7 +466,9 @@ typedef struct mit2cfm_gpt_sampling {
  * so far: history_prefix [history_prefix_count] (host, at most 8192 tokens;
  * the synthesis path passes the prefix's fake_inputs, [1] x n + [8192],
  * synthesis_pipeline.cpp:795-802), or with history_prefix NULL and the count
- * 0 the start token alone.  Outputs as for mit2cfm_gpt_kv_greedy, plus
+ * 0 the start token alone.  A non-NULL history_prefix with count 0 is an
+ * empty prefix, as the reference's empty vector is: the history is then the
+ * predictions alone.  Outputs as for mit2cfm_gpt_kv_greedy, plus
  * last_processed_logits [8194] (may be NULL).  A setting the reference
  * rejects (temperature or penalty <= 0, top_p outside (0, 1]) is
  * MIT2CFM_E_ARG. */
@@ -467,8 +489,12 @@ mit2cfm_status mit2cfm_gpt_cached_decode(mit2cfm_ctx* ctx, const float* rows, ui
                                          float* ln_f, float* final_norm, float* logits, uint32_t* argmax);
 
 /* Measurement hook of the GPT decode step: enqueues `count` launches of one of
- * its kernels (layer 0's weights) on the context's stream without waiting,
- * for timing with events on mit2cfm_stream; count 0 launches nothing.
+ * its kernels (cycling the layers' weights) on the context's stream without
+ * waiting, for timing with events on mit2cfm_stream; count 0 launches
+ * nothing.  With graph replay on, the launches are captured into a graph the
+ * first time a (kernel, count) pair is asked for and replayed after that, so
+ * a second call times the kernels back to back, without the host's launch
+ * rate between them.
  * Kernel ids: 0 c_attn GEMV (3840 x 1280, LayerNorm prologue, K/V written to
  * the cache), 1 attention c_proj GEMV (1280 x 1280, + residual), 2 c_fc GEMV
  * (5120 x 1280, LayerNorm prologue, gelu_new), 3 MLP c_proj GEMV

@@ -399,6 +399,20 @@ mit2cfm_status mit2cfm_set_graph(mit2cfm_ctx* ctx, int32_t on) {
   return MIT2CFM_OK;
 }
 
+mit2cfm_status mit2cfm_set_padding(mit2cfm_ctx* ctx, int32_t mode) {
+  if (!ctx) return fail(nullptr, MIT2CFM_E_ARG, "ctx must not be NULL");
+  if (mode != MIT2CFM_PADDING_COMPUTE && mode != MIT2CFM_PADDING_SKIP)
+    return fail(ctx, MIT2CFM_E_ARG, "padding mode must be MIT2CFM_PADDING_COMPUTE or MIT2CFM_PADDING_SKIP");
+  ctx->eng->set_skip_padding(mode == MIT2CFM_PADDING_SKIP);
+  return MIT2CFM_OK;
+}
+
+mit2cfm_status mit2cfm_get_padding(mit2cfm_ctx* ctx, int32_t* mode) {
+  if (!ctx || !mode) return fail(ctx, MIT2CFM_E_ARG, "ctx and mode must not be NULL");
+  *mode = ctx->eng->skip_padding() ? MIT2CFM_PADDING_SKIP : MIT2CFM_PADDING_COMPUTE;
+  return MIT2CFM_OK;
+}
+
 mit2cfm_status mit2cfm_decode_graph_count(mit2cfm_ctx* ctx, uint32_t* count, uint32_t* capacity) {
   if (!ctx || !count) return fail(ctx, MIT2CFM_E_ARG, "ctx and count must not be NULL");
   *count = (uint32_t)ctx->eng->graph_count();

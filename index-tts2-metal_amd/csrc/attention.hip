@@ -90,7 +90,7 @@ __device__ __forceinline__ int attn_vslot(int r, int c) { return c ^ (r & 7); }
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;  // log2 headroom before the running max moves
 
-template <int NBUF, int G, int QB, int NQW, bool BRANCH_KEYS>
+template <int NBUF, int G, int QB, int NQW, bool BRANCH_KEYS, bool QSKIP>
 __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* __restrict__ Q,
                                                                 const half_t* __restrict__ K,
                                                                 const half_t* __restrict__ Vt,
@@ -154,6 +154,13 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
   if constexpr (BRANCH_KEYS) {
     const int nk = reinterpret_cast<const int*>(kbias + (size_t)(gridDim.x / (8 * nqb)) * Tpad)[b];
     ntiles = max(1, min(ntiles, (nk + 63) / 64));
+    // QSKIP (padded batches whose padded rows are left unspecified): query
+    // rows from two past the branch's last valid key on are not needed --
+    // the two rows after it are, because the WaveNet's k=5 conv at the last
+    // valid rows reads them -- so a workgroup holding none of them leaves.
+    if constexpr (QSKIP) {
+      if ((slot - b * nqb) * QWG >= min(nk + 2, T)) return;
+    }
   }
   // Group grp walks tiles [grp*tpg, grp*tpg + tpg).  A tile index past the
   // end loads the last tile again (clamped) and is not computed, so every
@@ -422,20 +429,23 @@ hipError_t launch_key_bias(const uint32_t* mask, int B, int T, int Tpad, float* 
 template <int NBUF, int G, int QB, int NQW>
 static void launch_attention_shape(const half_t* Q, const half_t* K, const half_t* Vt,
                                    const float* kbias, half_t* O, int B, int T, int Tpad,
-                                   hipStream_t stream, bool branch_keys = false) {
+                                   hipStream_t stream, bool branch_keys, bool qskip) {
   constexpr int qwg = 16 * QB * NQW;
   const dim3 grid((T + qwg - 1) / qwg * 8 * B), block(64 * G * NQW);
-  if (branch_keys)
-    hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW, true>), grid, block, 0, stream, Q, K, Vt,
-                       kbias, O, T, Tpad);
+  if (qskip)
+    hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW, true, true>), grid, block, 0, stream, Q, K,
+                       Vt, kbias, O, T, Tpad);
+  else if (branch_keys)
+    hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW, true, false>), grid, block, 0, stream, Q, K,
+                       Vt, kbias, O, T, Tpad);
   else
-    hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW, false>), grid, block, 0, stream, Q, K, Vt,
-                       kbias, O, T, Tpad);
+    hipLaunchKernelGGL((attention_kernel<NBUF, G, QB, NQW, false, false>), grid, block, 0, stream, Q,
+                       K, Vt, kbias, O, T, Tpad);
 }
 
 hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             const float* kbias, half_t* O, int B, int T, int Tpad,
-                            hipStream_t stream, bool branch_keys) {
+                            hipStream_t stream, bool branch_keys, bool qskip) {
   if (B <= 0 || T <= 0 || Tpad < T || Tpad % 64 != 0) return hipErrorInvalidValue;
   // Shapes swept on MI355X (B = 2, us per launch, head-per-XCD mapping):
   //   T = 128 / 300:  32 queries x 2 key groups, 16-query waves, 2 buffers   3.5 / 4.9
@@ -448,9 +458,9 @@ hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
   // is chosen; the choice depends on the padded length only, never on the
   // batch.
   if (Tpad <= 512)
-    launch_attention_shape<2, 2, 1, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
+    launch_attention_shape<2, 2, 1, 2>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys, qskip);
   else
-    launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys);
+    launch_attention_shape<2, 2, 1, 4>(Q, K, Vt, kbias, O, B, T, Tpad, stream, branch_keys, qskip);
   return hipGetLastError();
 }
 

@@ -93,6 +93,18 @@ __device__ __forceinline__ float tanh_sat(float a) {
   return 1.0f - 2.0f * fast_rcp(__expf(2.0f * a) + 1.0f);
 }
 
+// Most row sequences a product can name for row-tile skipping (8 requests
+// with their cond and null branches).
+constexpr int kMaxRowSeq = 16;
+
+// The needed rows of a padded batch: nb sequences of T rows, of which the
+// first need[b] rows of sequence b are needed (nb = 0: every row).
+struct RowSkip {
+  int T = 0;
+  int nb = 0;
+  int need[kMaxRowSeq] = {};
+};
+
 // Reflect index for padding (k-tap conv, reflect mode).  Any integer maps into
 // [0, T) by repeated mirroring at 0 and T-1; a one-token sequence maps to 0.
 __device__ __forceinline__ int reflect_index(int src, int T) {

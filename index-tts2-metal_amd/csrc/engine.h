@@ -192,6 +192,12 @@ class Engine {
 
   // Graph replay on/off (default on; env MIT2CFM_GRAPH=0 turns it off).
   void set_use_graph(bool on) { use_graph_ = on; }
+  // Padded rows of a ragged multi-request decode: computed (default; the
+  // masked estimator at the padded length), or skipped -- every product,
+  // and the attention's query blocks, stop two rows past each request's
+  // valid length, and the rest of the padded rows' outputs are unspecified.
+  void set_skip_padding(bool on) { skip_padding_ = on; }
+  bool skip_padding() const { return skip_padding_; }
   // Arithmetic of the stages the reference runs in fp32 (the length
   // regulator, stage 1; the vocoder, stage 2): f32 = true (default) runs
   // their GEMMs on split f16 operand pairs (fp32-level products), false on
@@ -223,6 +229,10 @@ class Engine {
   // Set while a decode of a batch with a request shorter than T is enqueued:
   // its attention launches skip each branch's fully masked key tiles.
   bool branch_keys_ = false;
+  bool skip_padding_ = false;
+  // Set while a decode with skipped padding is enqueued: each branch's
+  // needed rows (valid length + 2, at most T).
+  RowSkip row_skip_;
   std::unique_ptr<Weights> w_;
   std::unique_ptr<Workspace> ws_;
   std::unique_ptr<Vocoder> voc_;
@@ -279,9 +289,9 @@ class Engine {
   };
   // Captured whole-decode graphs, least recently used evicted past
   // kMaxGraphs.  key: nreq, T, steps, cfg bits, vtrace ptr, io pointers,
-  // whether some request is shorter than T.
+  // whether some request is shorter than T, whether its padding is skipped.
   std::map<std::tuple<int, int, int, uint32_t, const void*, const void*, const void*, const void*,
-                      const void*, const void*, bool>,
+                      const void*, const void*, bool, bool>,
            GraphEntry>
       graphs_;
   uint64_t use_tick_ = 0;

@@ -77,9 +77,17 @@ namespace {
 constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxScratchDevices] = {};
+// Orders the calls that use a GPU's scratch: each call's stream waits for the
+// event the previous call recorded after its last kernel, then records it
+// again after its own, so calls from contexts on different streams run one
+// after another instead of overlapping.  Held under g_scratch_call_mu while
+// a call is enqueued, so two host threads cannot interleave their wait and
+// record.
+hipEvent_t g_scratch_ev[kMaxScratchDevices] = {};
+std::mutex g_scratch_call_mu;
 
-// Resolves this GPU's scratch address once; the caller has made `device`
-// current.  Called when a context is created.
+// Resolves this GPU's scratch address (and creates its ordering event) once;
+// the caller has made `device` current.  Called when a context is created.
 void resolve_scratch(int device) {
   if (device < 0 || device >= kMaxScratchDevices) return;  // the no-alloc call then reports it
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -88,6 +96,10 @@ void resolve_scratch(int device) {
   const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !p)
     throw HipError(std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+  hipEvent_t ev = nullptr;
+  const hipError_t ee = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (ee != hipSuccess) throw HipError(std::string("hipEventCreate failed: ") + hipGetErrorString(ee));
+  g_scratch_ev[device] = ev;
   g_scratch_ptr[device] = p;
 }
 
@@ -1036,6 +1048,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.W = W.si_w[l]; g.ldw = 1024; g.bias = W.si_b[l]; g.colperm = 1;
     g.C32 = cur; g.ldc32 = 512;
     norm_out(g, l);
+    apply_rows(row_skip_, g);
     HIP_OK(launch_gemm(g, A_CONCAT, EPI_F32, s));
   }
   {
@@ -1044,9 +1057,11 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.W = W.qkv_w[l]; g.ldw = 512; g.T = T;
     g.bias = nbq + l * 1536; g.ssq_in = ws.ssq;
     g.rope = ws.rope; g.q = ws.q; g.k = ws.k; g.vt = ws.vt; g.Tpad = Tpad;
+    apply_rows(row_skip_, g);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_QKV, s));
   }
-  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, s, branch_keys_));
+  HIP_OK(launch_attention(ws.q, ws.k, ws.vt, ws.kbias, ws.o16, B, T, Tpad, s, branch_keys_,
+                          row_skip_.nb > 0));
   {
     GemmArgs g;
     g.M = R; g.N = 512; g.K = 512; g.A = ws.o16; g.lda = 512;
@@ -1057,6 +1072,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
       g.C32 = hbuf; g.ldc32 = 512;
     }
     norm_out(g, 13 + l);
+    apply_rows(row_skip_, g);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
   }
   {
@@ -1064,6 +1080,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.M = R; g.N = 3072; g.K = 512; g.A = ws.n16; g.lda = 512;
     g.W = W.w13_w[l]; g.ldw = 512; g.C16 = ws.g16; g.ldc16 = kHgLd;
     g.bias = nbw + l * 3072; g.ssq_in = ws.ssq;
+    apply_rows(row_skip_, g);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_SWIGLU, s));
   }
   if (next_skip16) {
@@ -1073,6 +1090,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.W = W.fold_w[l + 1]; g.ldw = 2560; g.bias = W.si_b[l + 1]; g.colperm = 1;
     g.C32 = cur; g.ldc32 = 512;
     norm_out(g, l + 1);
+    apply_rows(row_skip_, g);
     HIP_OK(launch_gemm(g, A_CONCAT, EPI_F32, s));
   } else {
     GemmArgs g;
@@ -1080,6 +1098,7 @@ void Engine::enqueue_layer(int l, int B, int T, const float* tab, const float* n
     g.W = W.w2_w[l]; g.ldw = 1536; g.res = hbuf; g.ldres = 512; g.colperm = 1;
     g.C32 = cur; g.ldc32 = 512; g.C16 = out16; g.ldc16 = 512;
     if (l < 6) norm_out(g, l + 1);
+    apply_rows(row_skip_, g);
     HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
   }
 }
@@ -1119,6 +1138,7 @@ void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq,
     g.W = W.post_w; g.ldw = 512 + kMelPad; g.bias = W.post_b;
     g.C32 = ws.wn_x; g.ldc32 = 512; g.C16 = ws.wn_x16; g.ldc16 = 512;
     g.C32b = ws.rp; g.ldc32b = 512;
+    apply_rows(row_skip_, g);
     HIP_OK(launch_gemm(g, A_CONCAT, EPI_DUAL, s));
   }
   for (int l = 0; l < 8; ++l) {
@@ -1127,6 +1147,7 @@ void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq,
       g.M = R; g.N = 1024; g.K = 2560; g.A = ws.wn_x16; g.lda = 512; g.T = T; g.conv_c = 512;
       g.W = W.in_w[l]; g.ldw = 2560; g.bias = W.in_b[l]; g.cond = tab + kWnCondOff + l * 1024;
       g.C16 = ws.gate16; g.ldc16 = 512;
+      apply_rows(row_skip_, g);
       HIP_OK(launch_gemm(g, A_CONV5, EPI_GATE, s));
     }
     GemmArgs g;
@@ -1135,9 +1156,11 @@ void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq,
     if (l < 7) {
       g.N = 1024; g.C32 = ws.wn_x; g.ldc32 = 512; g.C16 = ws.wn_x16; g.ldc16 = 512;
       g.C32b = ws.wn_out; g.ldc32b = 512; g.flag = l > 0;
+      apply_rows(row_skip_, g);
       HIP_OK(launch_gemm(g, A_PLAIN, EPI_RESSKIP, s));
     } else {
       g.N = 512; g.C32b = ws.wn_out; g.ldc32b = 512; g.C32 = ws.fin; g.ldc32 = 512; g.rp = ws.rp;
+      apply_rows(row_skip_, g);
       HIP_OK(launch_gemm(g, A_PLAIN, EPI_FINALSKIP, s));
     }
   }
@@ -1148,14 +1171,17 @@ void Engine::enqueue_estimator(int B, int T, const float* tab, const float* nbq,
 
 // Input merge constant part: cond projection into mc16[:, kMcContent:+512], then
 // xin_const = mc16 . Wc^T + b_merge.
-static void enqueue_merge_const(Weights& W, Workspace& ws, int R, hipStream_t s) {
+static void enqueue_merge_const(Weights& W, Workspace& ws, int R, hipStream_t s,
+                                const RowSkip& rows = RowSkip()) {
   GemmArgs g;
   g.M = R; g.N = 512; g.K = 512; g.A = ws.cond16; g.lda = 512;
   g.W = W.cp_w; g.ldw = 512; g.bias = W.cp_b; g.C16 = ws.mc16 + kMcContent; g.ldc16 = kMcWidth;
+  apply_rows(rows, g);
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F16, s));
   GemmArgs c;
   c.M = R; c.N = 512; c.K = kMcWidth; c.A = ws.mc16; c.lda = kMcWidth;
   c.W = W.mc_w; c.ldw = kMcWidth; c.bias = W.mc_b; c.C32 = ws.xin_const; c.ldc32 = 512;
+  apply_rows(rows, c);
   HIP_OK(launch_gemm(c, A_PLAIN, EPI_F32, s));
 }
 
@@ -1163,7 +1189,7 @@ static void enqueue_merge_const(Weights& W, Workspace& ws, int R, hipStream_t s)
 // table row) it also leaves block 0's folded attention-norm operand in
 // ws.n16 / ws.ssq.
 static void enqueue_merge_step(Weights& W, Workspace& ws, int R, hipStream_t s,
-                               const float* tab) {
+                               const float* tab, const RowSkip& rows = RowSkip()) {
   GemmArgs g;
   g.M = R; g.N = 512; g.K = kMelPad; g.A = ws.xmel16; g.lda = kMelPad;
   g.W = W.mx_w; g.ldw = kMelPad; g.res = ws.xin_const; g.ldres = 512; g.C32 = ws.xa; g.ldc32 = 512;
@@ -1171,6 +1197,7 @@ static void enqueue_merge_step(Weights& W, Workspace& ws, int R, hipStream_t s,
   if (tab) {
     g.C16s = ws.n16; g.ldc16s = 512; g.sc_a = tab; g.sc_g = W.gamma[0]; g.ssq_out = ws.ssq;
   }
+  apply_rows(rows, g);
   HIP_OK(launch_gemm(g, A_PLAIN, EPI_F32, s));
 }
 
@@ -1186,10 +1213,10 @@ void Engine::enqueue_decode(const float* x0, const float* prompt, const float* c
   HIP_OK(launch_decode_prep(x0, prompt, cond, style, ws.P, nreq, T, cfg_on, ws.x_cur, ws.xmel16,
                             ws.cond16, ws.mc16, stream_));
   HIP_OK(launch_key_bias(ws.mask, B, T, (T + 63) / 64 * 64, ws.kbias, stream_));
-  enqueue_merge_const(W, ws, R, stream_);
+  enqueue_merge_const(W, ws, R, stream_, row_skip_);
   for (int s = 0; s < steps; ++s) {
     const float* tab = tb.tab + (size_t)s * kTcondPerStep;
-    enqueue_merge_step(W, ws, R, stream_, tab);
+    enqueue_merge_step(W, ws, R, stream_, tab, row_skip_);
     enqueue_estimator(B, T, tab, tb.nbq + (size_t)s * 13 * 1536, tb.nbw + (size_t)s * 13 * 3072);
     HIP_OK(launch_conv2_euler(ws.n16, W.c2f_w, W.c2f_b, ws.P, nreq, T, cfg_on, cfg, dt, ws.x_cur,
                               ws.xmel16, vtrace ? vtrace + (size_t)s * nreq * T * 80 : nullptr,
@@ -1240,16 +1267,29 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
   // full-length batch of the same shape; either is correct for both).
   bool ragged = false;
   for (int r = 0; r < nreq; ++r) ragged = ragged || valid_T[r] < (uint32_t)T;
+  // With skipped padding each branch's rows are needed up to two past its
+  // valid length: the k=5 WaveNet conv at the last valid rows reads them
+  // (layer 0's input there is the transformer's output, not masked).
+  RowSkip rows;
+  const bool skip = skip_padding_ && ragged && B <= kMaxRowSeq;
+  if (skip) {
+    rows.T = T;
+    rows.nb = B;
+    for (int b = 0; b < B; ++b) rows.need[b] = std::min<int>(T, (int)valid_T[cfg_on ? b / 2 : b] + 2);
+  }
   // The Euler state lives in ws.x_cur; x_out receives a copy at the end.
   auto enqueue_all = [&]() {
     branch_keys_ = ragged;
+    row_skip_ = rows;
     try {
       enqueue_decode(x0, prompt, cond, style, nreq, T, steps, cfg, vtrace, tb);
     } catch (...) {
       branch_keys_ = false;
+      row_skip_ = RowSkip();
       throw;
     }
     branch_keys_ = false;
+    row_skip_ = RowSkip();
     HIP_OK(launch_copy_f32(ws.x_cur, x_out, (size_t)nreq * T * 80, stream_));
   };
   if (!use_graph_) {
@@ -1260,7 +1300,7 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
   std::memcpy(&cfg_bits, &cfg, 4);
   auto key = std::make_tuple(nreq, T, steps, cfg_bits, (const void*)vtrace, (const void*)x0,
                              (const void*)prompt, (const void*)cond, (const void*)style,
-                             (const void*)x_out, ragged);
+                             (const void*)x_out, ragged, skip);
   auto it = graphs_.find(key);
   if (it == graphs_.end()) {
     if (graphs_.size() >= kMaxGraphs) {
@@ -1856,9 +1896,19 @@ int Engine::condition_device_noalloc(const float* s_infer, int codes, const floa
                  reinterpret_cast<half_t*>(base + kScrX16), reinterpret_cast<float*>(base + kScrY32),
                  reinterpret_cast<float*>(base + kScrSum),  reinterpret_cast<float*>(base + kScrSsq),
                  reinterpret_cast<float*>(base + kScrStats), kNoAllocMaxCodes, kNoAllocMaxFrames};
+  // Calls on this GPU are ordered through its event, except while the stream
+  // is being captured into a graph (a captured stream may not wait on work
+  // outside the capture): replays of such a graph must not overlap other
+  // calls on this GPU.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_OK(hipStreamIsCapturing(stream_, &cs));
+  const bool order = cs == hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> lock(g_scratch_call_mu);
+  if (order) HIP_OK(hipStreamWaitEvent(stream_, g_scratch_ev[device_], 0));
   HIP_OK(hipMemcpyAsync(cond, prompt_cond, (size_t)prompt_tokens * 512 * 4, hipMemcpyDeviceToDevice,
                         stream_));
   length_regulator_on(v, s_infer, codes, gen, cond + (size_t)prompt_tokens * 512);
+  if (order) HIP_OK(hipEventRecord(g_scratch_ev[device_], stream_));
   return gen;
 }
 

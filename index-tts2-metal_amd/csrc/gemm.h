@@ -14,6 +14,7 @@ namespace mit2hip {
 // Channels per tap of the k=5 WaveNet conv (the model's hidden width).
 constexpr int kConvC = 512;
 
+
 enum AMode : int {
   A_PLAIN = 0,   // A[m][k] = A[m*lda + k]
   A_CONCAT = 1,  // k <  K1: A[m*lda + k];  k >= K1: A2[m*lda2 + k - K1]
@@ -123,7 +124,26 @@ struct GemmArgs {
   // weight-normed conv stored as its direction v (exact in f16) with the
   // per-output-channel g / ||v|| applied here.
   const float* colscale = nullptr;
+
+  // Row-tile skipping (the padded multi-request decode).  When row_nb > 0
+  // the M rows are row_nb sequences of row_T rows, and only the first
+  // row_need[b] rows of sequence b are needed (1 <= row_need[b] <= row_T).
+  // A row tile that holds none of them is not computed: its outputs keep
+  // whatever they held.  Rows of a computed tile are computed as without
+  // skipping, so a needed row's result does not change.
+  int row_T = 0;
+  int row_nb = 0;
+  int row_need[kMaxRowSeq] = {};
 };
+
+// Names a padded batch's needed-row prefixes (RowSkip) in a product over
+// its rows; a product over other rows is left as it is (host side).
+inline void apply_rows(const RowSkip& rows, GemmArgs& g) {
+  if (rows.nb <= 0 || g.M != rows.nb * rows.T) return;
+  g.row_T = rows.T;
+  g.row_nb = rows.nb;
+  for (int b = 0; b < rows.nb; ++b) g.row_need[b] = rows.need[b];
+}
 
 // Scale of the lo half of a split operand (2^11: lo then has the magnitude
 // of hi, so it stays a normal f16 wherever hi does).

@@ -65,9 +65,14 @@ __device__ __forceinline__ void interleave() {
 }
 
 struct TileMap {
-  int nM, nN;  // tile grid
+  int nM, nN;  // tile grid (nM: the row tiles that are computed)
   int Xm, Xn;  // XCD rectangle grid, Xm * Xn == 8
   int per_xcd; // workgroups per XCD (grid = 8 * per_xcd)
+  // Row-tile skipping: the computed row tiles are nseg runs; run s starts at
+  // row tile seg_first[s] and holds computed tiles [seg_cum[s], seg_cum[s+1]).
+  int nseg;
+  int seg_first[kMaxRowSeq];
+  int seg_cum[kMaxRowSeq];
   __device__ __forceinline__ bool map(int b, int& tm, int& tn) const {
     const int xcd = b & 7, slot = b >> 3;
     const int rx = xcd / Xn, ry = xcd - (xcd / Xn) * Xn;
@@ -77,6 +82,18 @@ struct TileMap {
     if (rn <= 0 || slot >= (mhi - mlo) * rn) return false;
     tm = mlo + slot / rn;
     tn = nlo + slot % rn;
+    if (nseg > 0) {
+      // static indices only (the map stays in kernel-argument registers)
+      int first = seg_first[0], cum = 0;
+#pragma unroll
+      for (int s = 1; s < kMaxRowSeq; ++s) {
+        if (s < nseg && tm >= seg_cum[s]) {
+          first = seg_first[s];
+          cum = seg_cum[s];
+        }
+      }
+      tm = first + (tm - cum);
+    }
     return true;
   }
 };
@@ -967,10 +984,36 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
 // A (M x a_cols distinct values; a_cols < K for the k=5 conv, whose taps
 // re-read the same rows) is read once per rectangle column, W (N x K) once
 // per rectangle row.
-static TileMap make_tile_map(int M, int N, int K, int a_cols, int BM, int BN) {
+static TileMap make_tile_map(const GemmArgs& a, int M, int N, int K, int a_cols, int BM, int BN) {
   TileMap t;
   t.nM = (M + BM - 1) / BM;
   t.nN = N / BN;
+  t.nseg = 0;
+  for (int s = 0; s < kMaxRowSeq; ++s) t.seg_first[s] = t.seg_cum[s] = 0;
+  if (a.row_nb > 0) {
+    // Row tiles [lo, hi] of each sequence's needed rows, merged where they
+    // touch; sequences come in row order, so the runs do too.
+    int lo = -1, hi = -1, total = 0;
+    auto flush = [&]() {
+      t.seg_first[t.nseg] = lo;
+      t.seg_cum[t.nseg] = total;
+      total += hi - lo + 1;
+      ++t.nseg;
+    };
+    for (int b = 0; b < a.row_nb; ++b) {
+      const int blo = b * a.row_T / BM, bhi = (b * a.row_T + a.row_need[b] - 1) / BM;
+      if (lo >= 0 && blo <= hi + 1) {
+        hi = std::max(hi, bhi);
+      } else {
+        if (lo >= 0) flush();
+        lo = blo;
+        hi = bhi;
+      }
+    }
+    flush();
+    t.nM = total;
+    M = total * BM;
+  }
   const double a_bytes = 2.0 * M * a_cols, w_bytes = 2.0 * N * K;
   const int opts[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
   double best = 1e300;
@@ -1007,7 +1050,7 @@ static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
   if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K parts need equal stage counts
   if (PIPE && (a.K / SK / KG) % NST != 0) return hipErrorInvalidValue;  // whole rounds per part
   const TileMap tm = make_tile_map(
-      a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z || AM == A_CONVP ? a.conv_c : a.K, BM, BN);
+      a, a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z || AM == A_CONVP ? a.conv_c : a.K, BM, BN);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG, SP, PIPE>), dim3(8 * tm.per_xcd),
                      dim3(64 * WM * WN * (PIPE ? 1 : KG)), 0, s,
                      a, tm);
@@ -1141,6 +1184,12 @@ static bool gemm_spans_fit(const GemmArgs& a, AMode am) {
 
 hipError_t launch_gemm(const GemmArgs& a, AMode amode, EpiMode epi, hipStream_t stream) {
   if (!gemm_spans_fit(a, amode)) return hipErrorInvalidValue;
+  if (a.row_nb != 0) {
+    if (a.row_nb < 0 || a.row_nb > kMaxRowSeq || a.row_T <= 0 || (long)a.row_nb * a.row_T != a.M)
+      return hipErrorInvalidValue;
+    for (int b = 0; b < a.row_nb; ++b)
+      if (a.row_need[b] < 1 || a.row_need[b] > a.row_T) return hipErrorInvalidValue;
+  }
   // Column-pair rows: EPI_F32 only, whole 32-column groups, every column stored.
   if (a.colperm && (epi != EPI_F32 || a.N % 32 != 0 || a.n_store != 0 || a.split != 0))
     return hipErrorInvalidValue;

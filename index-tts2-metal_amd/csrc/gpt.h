@@ -66,9 +66,10 @@ class GptDecoder {
     uint32_t top_k = 0;  // 0: off
     float top_p = 1.0f;
     float repetition_penalty = 1.0f;
-    // repetition_history_prefix (gpt.cpp:1918, :2224-2229): when given, the
-    // repetition-penalty history is these tokens followed by the predictions
-    // so far, instead of the start token followed by them.  Host array.
+    // repetition_history_prefix (gpt.cpp:1918, :2224-2229): when given
+    // (non-NULL, even with n_history 0), the repetition-penalty history is
+    // these tokens followed by the predictions so far, instead of the start
+    // token followed by them.  Host array.
     const uint32_t* history = nullptr;
     uint32_t n_history = 0;
   };

@@ -13,7 +13,7 @@
 //                       head-major [head][row][64], so a head's keys are
 //                       contiguous)
 //              attention  softmax(q K^T / 8) V over the kv + 1 cached rows,
-//                       per head, split over chunks of 64 keys
+//                       per head, split over chunks of GPT_ATTN_KEYS (256) keys
 //              c_proj   x += W_proj att + b
 //              c_fc     f = gelu_new(W_fc LN2(x) + b)
 //              c_proj   x += W_mp f + b          (the last layer advances kv)
@@ -85,9 +85,11 @@ struct GptState {
   float temperature;  //   temperature, top-p, repetition penalty
   float top_p;
   float penalty;
-  int32_t n_hist;     //   repetition-history prefix tokens (0: the start token)
+  int32_t n_hist;     //   repetition-history prefix tokens
   uint64_t rng;       //   splitmix64 state, advanced once per sampled step
-  int32_t pad[12];
+  int32_t hist_given; //   1: the history starts with the caller's prefix (even an
+                      //   empty one), 0: with the start token
+  int32_t pad[11];
 };
 static_assert(sizeof(GptState) == 128, "GptState layout");
 
@@ -195,9 +197,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
   static_assert(K % (8 * LPR) == 0, "K must be a multiple of 8 * LPR");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPR, j = lane % LPR;
-  // After a stop, the rest of a replayed group of steps does nothing (the
-  // cache length stops advancing too).
-  if (a.check_stop && a.st->stopped) return;
+  // After a stop, the rest of a replayed group of steps stores nothing (the
+  // cache length stops advancing too).  The flag is requested here, beside
+  // the input vector, and tested only where the results are stored, so the
+  // weight rows are requested without waiting for it (the row reductions
+  // between are cross-lane operations, which keep those loads above the test).
+  const bool stopped = a.check_stop && a.st->stopped;
   const int rbase = blockIdx.x * ROWS + wave * RPW * UR;
 
   // 1. the input vector at this lane's positions 8 (j + c LPR) + e (a lane
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
   if constexpr (PRO != PRO_PLAIN) {
     group_layernorm<LPR, CH>(xv, gv, bv);
     if constexpr (PRO == PRO_LN2) {
-      const bool out = blockIdx.x == 0 && wave == 0 && sub == 0 && a.lnf_out;
+      const bool out = blockIdx.x == 0 && wave == 0 && sub == 0 && a.lnf_out && !stopped;
       if (out) store_chunks<LPR, CH>(xv, a.lnf_out, j);
       load_chunks<LPR, CH>(gv, a.g2, j);
       load_chunks<LPR, CH>(bv, a.b2, j);
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
   for (int u = 0; u < UR; ++u) {
     const int r = rbase + u * RPW + sub;
     rv[u] = -INFINITY;
-    if (j != 0 || r >= a.N) continue;
+    if (j != 0 || r >= a.N || stopped) continue;
     const float v = acc[u] + a.bias[r];
     if constexpr (EPI == EPI_GELU) {
       a.y[r] = gelu_new(v);
@@ -282,7 +287,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     }
   }
   if constexpr (EPI == EPI_RES) {
-    if (a.advance && blockIdx.x == 0 && threadIdx.x == 0) a.st->kv += 1;
+    if (a.advance && blockIdx.x == 0 && threadIdx.x == 0 && !stopped) a.st->kv += 1;
   }
   if constexpr (EPI == EPI_LOGITS) {
     // argmax_row (gpt.cpp:1297-1308), first stage: each block's first
@@ -298,7 +303,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
       }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == 0 && !stopped) {
       float bv = sv[0];
       int bi = si[0];
       for (int i = 1; i < ROWS; ++i)
@@ -468,9 +473,10 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* log
   __syncthreads();
   if (penalty != 1.0f) {  // each distinct history token once (the order does not matter)
     // history = hist_prefix[0..n_hist) ++ predictions (inputs[1..n_in)) when a prefix
-    // is given, else inputs[0..n_in) (the start token, then the predictions)
+    // is given (even an empty one), else inputs[0..n_in) (the start token, then
+    // the predictions)
     const int nh = st->n_hist;
-    const int h0 = nh > 0 ? 1 : 0;
+    const int h0 = st->hist_given ? 1 : 0;
     const int total = nh + st->n_in - h0;
     for (int h = tid; h < total; h += kSampleThreads) {
       const uint32_t t = h < nh ? hist_prefix[h] : inputs[h - nh + h0];
@@ -1042,6 +1048,11 @@ struct GptDecoder::Impl {
   hipGraphExec_t graph[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   bool use_graph = true;  // env MIT2CFM_GRAPH=0: launch every kernel directly (for profilers)
+  // The measurement hook's launch loop, captured once per (kernel, count)
+  // and replayed, so that back-to-back launches are timed without the host's
+  // launch rate between them.
+  hipGraphExec_t prof_graph = nullptr;
+  int prof_kernel = -1, prof_launches = -1;
 
   ~Impl() {
     drop_graphs();
@@ -1054,6 +1065,9 @@ struct GptDecoder::Impl {
       if (g) (void)hipGraphExecDestroy(g);
       g = nullptr;
     }
+    if (prof_graph) (void)hipGraphExecDestroy(prof_graph);
+    prof_graph = nullptr;
+    prof_kernel = prof_launches = -1;
   }
 
   // Every weight array with its element count, in a fixed order (the device
@@ -1277,6 +1291,7 @@ struct GptDecoder::Impl {
       h.penalty = smp->repetition_penalty;
       h.rng = smp->seed;
       h.n_hist = (int32_t)smp->n_history;
+      h.hist_given = smp->history != nullptr ? 1 : 0;
     }
     h.kv = 0;
     h.step = 0;
@@ -1533,6 +1548,20 @@ const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) 
   GPT_OK(hipMemsetAsync(d.x, 0, kW * sizeof(float), d.s));
   GPT_OK(hipMemsetAsync(d.fc, 0, kMLP * sizeof(float), d.s));
   GPT_OK(hipMemsetAsync(d.att, 0, kW * sizeof(float), d.s));
+  const bool graphed = d.use_graph && launches > 0;
+  if (graphed && d.prof_graph && d.prof_kernel == kernel && d.prof_launches == launches) {
+    GPT_OK(hipGraphLaunch(d.prof_graph, d.s));
+    if (bytes) *bytes = 0;
+    return names[kernel];
+  }
+  if (graphed) {
+    if (d.prof_graph) {
+      GPT_OK(hipStreamSynchronize(d.s));  // the previous loop may still be replaying
+      (void)hipGraphExecDestroy(d.prof_graph);
+      d.prof_graph = nullptr;
+    }
+    GPT_OK(hipStreamBeginCapture(d.s, hipStreamCaptureModeThreadLocal));
+  }
   for (int i = 0; i < launches; ++i) {
     // cycle through the layers so that, as in a decode step, the weights are
     // not already in the caches
@@ -1570,6 +1599,20 @@ const char* GptDecoder::profile_launch(int kernel, int launches, double* bytes) 
                            d.att, 1, 0);
         break;
     }
+  }
+  if (graphed) {
+    hipGraph_t g = nullptr;
+    const hipError_t ce = hipStreamEndCapture(d.s, &g);
+    if (ce != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      GPT_OK(ce);
+    }
+    const hipError_t ie = hipGraphInstantiate(&d.prof_graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    GPT_OK(ie);
+    d.prof_kernel = kernel;
+    d.prof_launches = launches;
+    GPT_OK(hipGraphLaunch(d.prof_graph, d.s));
   }
   GPT_OK(hipGetLastError());
   if (bytes) *bytes = 0;

@@ -26,10 +26,12 @@ hipError_t launch_adaln(const float* x, const float* shift, const float* scale, 
 // [B][T] 0/1 key mask into a buffer of B * Tpad + B words.  With
 // branch_keys, a branch's key tiles after its last valid key are skipped
 // (they are fully masked: the result is the same up to the split of the
-// keys between the kernel's two groups); worth it for padded batches.
+// keys between the kernel's two groups); worth it for padded batches.  With
+// qskip (implies branch_keys) the query rows from two past a branch's last
+// valid key on are not computed: their outputs keep what they held.
 hipError_t launch_attention(const half_t* Q, const half_t* K, const half_t* Vt,
                             const float* kbias, half_t* O, int B, int T, int Tpad,
-                            hipStream_t stream, bool branch_keys = false);
+                            hipStream_t stream, bool branch_keys = false, bool qskip = false);
 hipError_t launch_key_bias(const uint32_t* mask, int B, int T, int Tpad, float* kbias,
                            hipStream_t stream);
 

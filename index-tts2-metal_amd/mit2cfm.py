@@ -26,6 +26,7 @@ DTYPE_F32, DTYPE_F16 = 0, 1
 FLAG_SYNC = 1
 STAGES = {"length_regulator": 1, "vocoder": 2}  # MIT2CFM_STAGE_*
 PRECISIONS = {"f16": 0, "f32": 1}  # MIT2CFM_PREC_*
+PADDING = {"compute": 0, "skip": 1}  # MIT2CFM_PADDING_*
 NOALLOC_MAX_CODES = 1024  # MIT2CFM_NOALLOC_MAX_CODES
 
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -72,6 +73,8 @@ def lib() -> ctypes.CDLL:
         "mit2cfm_stream": (vp, [vp]),
         "mit2cfm_synchronize": (st, [vp]),
         "mit2cfm_set_graph": (st, [vp, i32]),
+        "mit2cfm_set_padding": (st, [vp, i32]),
+        "mit2cfm_get_padding": (st, [vp, ctypes.POINTER(ctypes.c_int32)]),
         "mit2cfm_set_precision": (st, [vp, i32, i32]),
         "mit2cfm_decode_graph_count": (st, [vp, _u32p, _u32p]),
         "mit2cfm_get_precision": (st, [vp, i32, ctypes.POINTER(i32)]),
@@ -521,6 +524,17 @@ class Context:
     def set_graph(self, on: bool) -> None:
         self._c(lib().mit2cfm_set_graph(self._h, 1 if on else 0))
 
+    def set_padding(self, mode: str) -> None:
+        """Padded rows of a ragged batched decode: "compute" (default) or "skip"
+        (rows from two past each request's valid length are not computed and
+        come back unspecified; valid rows are bit-identical)."""
+        self._c(lib().mit2cfm_set_padding(self._h, PADDING[mode]))
+
+    def padding(self) -> str:
+        m = ctypes.c_int32()
+        self._c(lib().mit2cfm_get_padding(self._h, ctypes.byref(m)))
+        return {v: k for k, v in PADDING.items()}[m.value]
+
     def graph_count(self) -> tuple[int, int]:
         """(decode graphs held now, capacity)."""
         n = np.zeros(1, np.uint32)
@@ -653,7 +667,8 @@ class Context:
         """The sampled loop (gpt.cpp:2221-2240); as gpt_kv_greedy plus
         last_processed_logits.  history: the repetition-history prefix
         (repetition_history_prefix, gpt.cpp:1918), e.g. the prefix's
-        fake_inputs [1] * n + [8192]; None: the start token."""
+        fake_inputs [1] * n + [8192]; None: the start token; []: an empty
+        prefix (the history is the predictions alone)."""
         x = _f32(prefix).reshape(-1, GPT_WIDTH)
         P = x.shape[0]
         pred = np.zeros(max(steps, 1), np.uint32)
@@ -666,9 +681,13 @@ class Context:
         t = (ctypes.c_double * 2)()
         cfg = _GptSampling(seed, temperature, top_k, top_p, repetition_penalty)
         hist = _u32(history) if history is not None else None
+        hbuf = None
+        if hist is not None:  # a valid pointer for an empty prefix too
+            hbuf = np.zeros(max(hist.size, 1), np.uint32)
+            hbuf[:hist.size] = hist
         self._c(lib().mit2cfm_gpt_kv_sample(self._h, _p(x) if P else None, P, steps,
                                             1 if hf_generate_positions else 0, ctypes.byref(cfg),
-                                            _pu(hist) if hist is not None and hist.size else None,
+                                            _pu(hbuf) if hbuf is not None else None,
                                             0 if hist is None else hist.size, _pu(pred),
                                             _pu(n_pred), _pu(inp), _pu(n_in), ctypes.byref(stop), _p(logits),
                                             _p(proc), t))

@@ -976,9 +976,12 @@ void orc_estimator_step(const orc_model* m, const float* x, const float* prompt_
 /* dit_cfm_bigvgan.cpp:2908-2937.  The reference always passes an all-ones
  * mask; key_mask (NULL = all ones) extends it to a right-padded request,
  * using the estimator's masked semantics at the padded length. */
+/* The first run_steps steps of the steps-step schedule (run_steps >= steps:
+ * the whole decode). */
 static void cfm_euler_impl(const orc_model* m, float* x, const float* prompt, const float* cond,
                            const float* style, const uint32_t* key_mask, uint32_t T, uint32_t P,
-                           uint32_t steps, float cfg_rate, float* x_trace, float* v_trace) {
+                           uint32_t steps, uint32_t run_steps, float cfg_rate, float* x_trace,
+                           float* v_trace) {
     const size_t nx = (size_t)T * 80;
     float* prompt_x = fzeros(nx);
     for (uint32_t t = 0; t < P; ++t) {
@@ -994,7 +997,7 @@ static void cfm_euler_impl(const orc_model* m, float* x, const float* prompt, co
     float* cfg_dphi = fbuf(nx);
     float t = 0.0f;
     const float dt = 1.0f / (float)steps;
-    for (uint32_t step = 1; step <= steps; ++step) {
+    for (uint32_t step = 1; step <= steps && step <= run_steps; ++step) {
         if (x_trace) memcpy(x_trace + (size_t)(step - 1) * nx, x, nx * sizeof(float));
         orc_estimator_step(m, x, prompt_x, cond, style, t, mask, T, dphi);
         if (cfg_rate > 0.0f) {
@@ -1014,16 +1017,23 @@ static void cfm_euler_impl(const orc_model* m, float* x, const float* prompt, co
 void orc_cfm_euler_trace(const orc_model* m, float* x, const float* prompt, const float* cond,
                          const float* style, uint32_t T, uint32_t P, uint32_t steps, float cfg_rate,
                          float* x_trace, float* v_trace) {
-    cfm_euler_impl(m, x, prompt, cond, style, NULL, T, P, steps, cfg_rate, x_trace, v_trace);
+    cfm_euler_impl(m, x, prompt, cond, style, NULL, T, P, steps, steps, cfg_rate, x_trace, v_trace);
+}
+
+void orc_cfm_euler_partial(const orc_model* m, float* x, const float* prompt, const float* cond,
+                           const float* style, uint32_t T, uint32_t P, uint32_t steps,
+                           uint32_t run_steps, float cfg_rate, float* x_trace, float* v_trace) {
+    cfm_euler_impl(m, x, prompt, cond, style, NULL, T, P, steps, run_steps, cfg_rate, x_trace,
+                   v_trace);
 }
 
 void orc_cfm_euler(const orc_model* m, float* x, const float* prompt, const float* cond,
                    const float* style, uint32_t T, uint32_t P, uint32_t steps, float cfg_rate) {
-    cfm_euler_impl(m, x, prompt, cond, style, NULL, T, P, steps, cfg_rate, NULL, NULL);
+    cfm_euler_impl(m, x, prompt, cond, style, NULL, T, P, steps, steps, cfg_rate, NULL, NULL);
 }
 
 void orc_cfm_euler_masked(const orc_model* m, float* x, const float* prompt, const float* cond,
                           const float* style, const uint32_t* key_mask, uint32_t T, uint32_t P,
                           uint32_t steps, float cfg_rate) {
-    cfm_euler_impl(m, x, prompt, cond, style, key_mask, T, P, steps, cfg_rate, NULL, NULL);
+    cfm_euler_impl(m, x, prompt, cond, style, key_mask, T, P, steps, steps, cfg_rate, NULL, NULL);
 }

@@ -153,6 +153,13 @@ void orc_cfm_euler(const orc_model* m, float* x, const float* prompt, const floa
 void orc_cfm_euler_trace(const orc_model* m, float* x, const float* prompt,
                          const float* cond, const float* style, uint32_t T, uint32_t P,
                          uint32_t steps, float cfg_rate, float* x_trace, float* v_trace);
+/* The first run_steps Euler steps of the steps-step schedule (dt = 1/steps),
+ * traced as orc_cfm_euler_trace ([run_steps, T, 80] each, either may be NULL);
+ * x holds the state after them. */
+void orc_cfm_euler_partial(const orc_model* m, float* x, const float* prompt,
+                           const float* cond, const float* style, uint32_t T, uint32_t P,
+                           uint32_t steps, uint32_t run_steps, float cfg_rate, float* x_trace,
+                           float* v_trace);
 /* The decode of one right-padded request: key_mask [T] (0/1) is passed to
  * both estimator calls of every step (the reference passes all ones). */
 void orc_cfm_euler_masked(const orc_model* m, float* x, const float* prompt, const float* cond,

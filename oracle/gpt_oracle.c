@@ -594,9 +594,10 @@ uint32_t orc_gpt_sample_token(const float* processed, uint32_t n, uint64_t* rng_
 /* The sampled form of the cached loop (run_gpt_kv_greedy_metal with
  * do_sample, gpt.cpp:2221-2240): after each step's logits, the processors over
  * the history and one draw; the rng is seeded once per call.  The history is
- * repetition_history_prefix followed by the predictions so far, or with no
- * prefix (n_history_prefix 0) the start token followed by them
- * (gpt.cpp:2224-2229).  last_processed receives the last step's processed
+ * repetition_history_prefix followed by the predictions so far whenever a
+ * prefix is given (history_prefix non-NULL, even with n_history_prefix 0: the
+ * reference inserts the vector it points to, however short), or with no
+ * prefix (NULL) the start token followed by them (gpt.cpp:2224-2229).  last_processed receives the last step's processed
  * logits.  Returns 0, or -1 (a position past the table or an invalid
  * setting). */
 int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tokens, uint32_t steps, int hf,
@@ -655,7 +656,7 @@ int orc_gpt_kv_sample(const orc_gpt* m, const float* prefix, uint32_t prefix_tok
          * these are input tokens 1..) */
         const uint32_t* hist = input_tokens;
         uint32_t n_hist = res->n_input;
-        if (n_history_prefix) {
+        if (history_prefix) {
             for (uint32_t i = 1; i < res->n_input; ++i) history[n_history_prefix + i - 1] = input_tokens[i];
             hist = history;
             n_hist = n_history_prefix + res->n_input - 1;

@@ -95,6 +95,8 @@ def lib() -> ctypes.CDLL:
                                            _f32p, _f32p]),
             "orc_cfm_euler_masked": (None, [vp, _f32p, _f32p, _f32p, _f32p, _u32p, u32, u32, u32,
                                             f32]),
+            "orc_cfm_euler_partial": (None, [vp, _f32p, _f32p, _f32p, _f32p, u32, u32, u32, u32, f32,
+                                             _f32p, _f32p]),
             "orc_gpt_new": (vp, [i32]),
             "orc_gpt_free": (None, [vp]),
             "orc_gpt_set": (i32, [vp, ctypes.c_char_p, _f32p, u64]),
@@ -421,6 +423,19 @@ class Model:
                                   T, Pn, steps, cfg, P(xt), P(vt))
         return x.reshape(T, 80), xt, vt
 
+    def cfm_euler_partial(self, x0, prompt, cond, style, steps, run_steps, cfg):
+        """The first run_steps Euler steps of the steps-step schedule: (state after
+        them, states before each, guided velocities of each)."""
+        x = f32(x0).copy()
+        T = x.size // 80
+        pr = f32(prompt)
+        Pn = pr.size // 80
+        xt = np.empty((run_steps, T, 80), np.float32)
+        vt = np.empty((run_steps, T, 80), np.float32)
+        lib().orc_cfm_euler_partial(self._m, P(x), P(pr) if Pn else None, P(f32(cond)), P(f32(style)),
+                                    T, Pn, steps, run_steps, cfg, P(xt), P(vt))
+        return x.reshape(T, 80), xt, vt
+
     def cfm_euler_masked(self, x0, prompt, cond, style, mask, steps, cfg):
         """Euler decode at the padded length with key mask (one request)."""
         x = f32(x0).copy()
@@ -698,8 +713,10 @@ class GPT:
                   hf_generate_positions=False, history=None):
         """The sampled cached loop (gpt.cpp:2221-2240); also returns
         last_processed_logits.  history: repetition_history_prefix (None: the
-        start token)."""
+        start token; an empty list: an empty prefix, the predictions alone)."""
         hist = np.ascontiguousarray(np.asarray(history if history is not None else [], np.uint32))
+        hbuf = np.zeros(max(hist.size, 1), np.uint32)  # a valid pointer for an empty prefix too
+        hbuf[:hist.size] = hist
         x = f32(prefix).reshape(-1, GPT_W)
         pred = np.zeros(max(steps, 1), np.uint32)
         inp = np.zeros(steps + 1, np.uint32)
@@ -708,7 +725,7 @@ class GPT:
         r = _GreedyResult()
         rc = lib().orc_gpt_kv_sample(self._h, P(x), x.shape[0], steps, 1 if hf_generate_positions else 0, seed,
                                      temperature, top_k, top_p, repetition_penalty,
-                                     PU(hist) if hist.size else None, hist.size, PU(pred), PU(inp), P(lg),
+                                     PU(hbuf) if history is not None else None, hist.size, PU(pred), PU(inp), P(lg),
                                      P(lp), ctypes.byref(r))
         if rc != 0:
             raise ValueError("GPT oracle: invalid sampling setting or position beyond the table")

@@ -19,8 +19,11 @@ Configs (benchmark workloads):
   config5  8 requests, P=258, target lengths U{300..1500} from one seed, right-padded
            (B=16 rows): the masked CFG-pair velocity at t=0 of the shortest and the
            longest request at the padded length (~4 min on 8 threads)
-  config5t the same batch decoded for 2 Euler steps: the shortest request's final mel
-           from the masked oracle decode at the padded length (~2 min on 8 threads)
+  config5t the same batch decoded for 2 Euler steps: the final mel of the shortest and of
+           the longest request from the masked oracle decode at the padded length (~4 min
+           on 8 threads)
+  config4t T=3000 (P=258): the first 2 Euler steps of the 25-step schedule -- the guided
+           velocity of each step and the state after them (~4 min on 8 threads)
 """
 from __future__ import annotations
 
@@ -53,6 +56,7 @@ CONFIGS = {
                     seed=100),
     "config5t": dict(kind="padded_decode", nreq=8, P=258, lo=300, hi=1500, len_seed=5, steps=2,
                      cfg=0.7, seed=100),
+    "config4t": dict(kind="partial", T=3000, P=258, steps=25, run_steps=2, cfg=0.7, seed=1),
 }
 
 
@@ -176,11 +180,19 @@ def make(name: str, model, digest: str) -> None:
         c = dict(c, tokens=toks, t_max=tmax, picked=picks)
     elif c["kind"] == "padded_decode":
         toks, tmax, X0, PR, CO, ST = padded_requests(c)
-        r = int(np.argmin(toks))
-        mask = (np.arange(tmax) < toks[r]).astype(np.uint32)
-        final = model.cfm_euler_masked(X0[r], PR[r][:c["P"]], CO[r], ST[r], mask, c["steps"], c["cfg"])
-        out[f"final_req{r}"] = final[:toks[r]]
-        c = dict(c, tokens=toks, t_max=tmax, picked=[r])
+        picks = [int(np.argmin(toks)), int(np.argmax(toks))]
+        for r in picks:
+            mask = (np.arange(tmax) < toks[r]).astype(np.uint32)
+            final = model.cfm_euler_masked(X0[r], PR[r][:c["P"]], CO[r], ST[r], mask, c["steps"],
+                                           c["cfg"])
+            out[f"final_req{r}"] = final[:toks[r]]
+        c = dict(c, tokens=toks, t_max=tmax, picked=picks)
+    elif c["kind"] == "partial":
+        x_after, xt, vt = model.cfm_euler_partial(x0, prompt, cond, style, c["steps"], c["run_steps"],
+                                                  c["cfg"])
+        out["x_after"] = x_after
+        for s in range(c["run_steps"]):
+            out[f"v_step{s}"] = vt[s]
     else:
         final, xt, vt = model.cfm_euler(x0, prompt, cond, style, c["steps"], c["cfg"], trace=True)
         out["final"] = final

@@ -70,6 +70,10 @@ def test_null_context_and_arguments_are_rejected(mit2):
     assert L.mit2cfm_synchronize(None) == mit2.E_ARG
     assert L.mit2cfm_create_from_bundle(None, 0, None) == mit2.E_ARG
     assert L.mit2cfm_normal_noise(2, 2, 1, 1.0, None) == mit2.E_ARG
+    u = (ctypes.c_uint32 * 1)(8)
+    assert L.mit2cfm_decode_batched_device(None, 1, 8, u, u, p, p, p, p, 1, 0.7, p, 0) == mit2.E_ARG
+    assert L.mit2cfm_set_padding(None, 1) == mit2.E_ARG
+    assert L.mit2cfm_get_padding(None, None) == mit2.E_ARG
     L.mit2cfm_destroy(None)  # a no-op
 
 

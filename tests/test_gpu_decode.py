@@ -282,5 +282,8 @@ def test_invalid_arguments_raise(mit2, ctx):
     rejected(lambda: ctx.decode_batched([0], [0], X0, PR, CO, ST, 2, 0.7))  # empty request
     rejected(lambda: ctx.decode_batched([9], [2], X0, PR, CO, ST, 2, 0.7))  # longer than T
     rejected(lambda: ctx.decode_batched([4], [5], X0, PR, CO, ST, 2, 0.7))  # prompt > request
+    rejected(lambda: ctx.decode_batched_device([8], [2], 0, 0, 0, 0, 8, 2, 0.7, 0))  # NULL buffers
+    rejected(lambda: ctx._c(mit2.lib().mit2cfm_set_padding(ctx._h, 7)))  # unknown padding mode
+    assert ctx.padding() == "compute"
     # Rejected calls leave the context as it was: the same decode gives the same bits.
     assert np.array_equal(ctx.decode(x0, prompt, cond, style, 2, 0.7), before)

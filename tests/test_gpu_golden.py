@@ -5,8 +5,11 @@ fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
   config2  full decode T=860 (P=258), 25 steps, cfg 0.7 -- the headline decode
   config3  full decode T=128 (P=48), 12 steps, cfg 0.7
   config4  T=3000 (P=258): CFG-pair velocity at three Euler states
+  config4t T=3000: the first 2 Euler steps of the 25-step schedule (the decode's
+           own trajectory against the oracle's)
   config5  8 right-padded requests (B=16 rows): masked velocity at t=0, and
-           (config5t) the shortest request after a 2-step batched decode
+           (config5t) the shortest and the longest request after a 2-step batched
+           decode, with the padded rows computed and skipped
 
 Inputs and synthetic weights are regenerated from the seeds stored beside each
 fixture (splitmix64 + Box-Muller, bit-exact on any host); the weights digest
@@ -192,6 +195,36 @@ def test_config4_long_form_decode_properties(mit2, golden_ctx):
     X0[1, :900], PR[1, :100], CO[1, :900], ST[1] = s0, s1, s2, s3
     out = golden_ctx.decode_batched([T, 900], [P, 100], X0, PR, CO, ST, steps, cfg)
     assert np.array_equal(out[0], a)
+    golden_ctx.set_padding("skip")
+    try:
+        skip = golden_ctx.decode_batched([T, 900], [P, 100], X0, PR, CO, ST, steps, cfg)
+    finally:
+        golden_ctx.set_padding("compute")
+    assert np.array_equal(skip[0], a)
+    assert np.array_equal(skip[1, :900], out[1, :900])
+
+
+def test_config4_trajectory_first_steps(mit2, orc, golden_ctx):
+    """T=3000 (P=258), the 25-step schedule: the guided velocity of steps 0 and 1
+    along the decode's own trajectory (mit2cfm_decode_trace) against the oracle's
+    trajectory, and the state after those two steps, rebuilt from the decode's
+    velocities (x += dt v, prompt rows zeroed), against the oracle's."""
+    meta, ref = load("config4t")
+    T, P, steps, cfg = meta["T"], meta["P"], meta["steps"], meta["cfg"]
+    x0, prompt, cond, style = inputs(mit2, T, P, meta["seed"])
+    _, vt = golden_ctx.decode_trace(x0, prompt, cond, style, steps, cfg)
+    x = x0.copy()
+    x[:P] = 0
+    dt = np.float32(1.0 / steps)
+    for s in range(meta["run_steps"]):
+        err = orc.rel_l2(vt[s], ref[f"v_step{s}"])
+        print(f"config4t step {s}: velocity rel-L2 {err:.3e}", flush=True)
+        assert err <= VEL_TOL
+        x = (x + dt * vt[s]).astype(np.float32)
+        x[:P] = 0
+    err = orc.rel_l2(x, ref["x_after"])
+    print(f"config4t state after {meta['run_steps']} steps: rel-L2 {err:.3e}", flush=True)
+    assert err <= MEL_TOL
 
 
 def test_config5_padded_batch_velocity(mit2, orc, golden_ctx):
@@ -220,19 +253,26 @@ def test_config5_padded_batch_velocity(mit2, orc, golden_ctx):
         assert err <= VEL_TOL
 
 
-def test_config5_padded_batch_trajectory(mit2, orc, golden_ctx):
+@pytest.mark.parametrize("padding", ["compute", "skip"])
+def test_config5_padded_batch_trajectory(mit2, orc, golden_ctx, padding):
     """The 8-request right-padded batch (B=16 rows, T_max=1348) decoded for 2
-    Euler steps: the shortest request's final mel against the oracle's masked
-    decode of that request at the padded length."""
+    Euler steps: the final mel of the shortest (T=624) and of the longest
+    (T=1348) request against the oracle's masked decode of that request at the
+    padded length, with the padded rows computed and with them skipped."""
     mg = _make_golden()
     meta, ref = load("config5t")
     toks, tmax, X0, PR, CO, ST = mg.padded_requests(dict(meta))
     assert toks == meta["tokens"] and tmax == meta["t_max"]
     P, steps, cfg = meta["P"], meta["steps"], meta["cfg"]
-    out = golden_ctx.decode_batched(toks, [P] * len(toks), X0, PR, CO, ST, steps, cfg)
+    golden_ctx.set_padding(padding)
+    try:
+        out = golden_ctx.decode_batched(toks, [P] * len(toks), X0, PR, CO, ST, steps, cfg)
+    finally:
+        golden_ctx.set_padding("compute")
     for r in meta["picked"]:
         err = orc.rel_l2(out[r, :toks[r]], ref[f"final_req{r}"])
-        print(f"config5t request {r} (T={toks[r]}, {steps} steps): final mel rel-L2 {err:.3e}", flush=True)
+        print(f"config5t request {r} (T={toks[r]}, {steps} steps, padding {padding}): final mel "
+              f"rel-L2 {err:.3e}", flush=True)
         assert err <= MEL_TOL
         assert np.all(out[r, :P] == 0)
 
@@ -254,3 +294,24 @@ def test_config5_padded_batch_decode(mit2, golden_ctx):
         one = golden_ctx.decode_batched(toks[r:r + 1], [P], X0[r:r + 1], PR[r:r + 1], CO[r:r + 1],
                                         ST[r:r + 1], steps, cfg)
         assert np.array_equal(one[0], out[r])
+    # The same decode from device buffers (mit2cfm_decode_batched_device), bit for bit.
+    import torch
+
+    dev = torch.device("cuda:0")
+    d_in = [torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev) for a in (X0, PR, CO, ST)]
+    d_out = torch.full((n, tmax, 80), float("nan"), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    golden_ctx.decode_batched_device(toks, [P] * n, d_in[0].data_ptr(), d_in[1].data_ptr(),
+                                     d_in[2].data_ptr(), d_in[3].data_ptr(), tmax, steps, cfg,
+                                     d_out.data_ptr(), sync=True)
+    assert np.array_equal(d_out.cpu().numpy(), out)
+    # Padded rows skipped (MIT2CFM_PADDING_SKIP): every request's valid rows are
+    # the same bits; the padded rows are unspecified.
+    golden_ctx.set_padding("skip")
+    try:
+        assert golden_ctx.padding() == "skip"
+        skip = golden_ctx.decode_batched(toks, [P] * n, X0, PR, CO, ST, steps, cfg)
+    finally:
+        golden_ctx.set_padding("compute")
+    for r in range(n):
+        assert np.array_equal(skip[r, :toks[r]], out[r, :toks[r]]), f"request {r}"

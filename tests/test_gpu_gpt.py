@@ -284,6 +284,13 @@ def test_history_prefix_penalises_its_tokens(ctx2, orc2):
     assert without["last_processed_logits"][1] == raw[1]
     assert np.array_equal(start_only["last_processed_logits"], without["last_processed_logits"])
     _compare_sampled(with_h, orc2.kv_sample(prefix, 1, 5, history=[1] * 12 + [8192], **cfg), "  2 layers history")
+    # An empty prefix (non-NULL, count 0) replaces the start token, as the
+    # reference's empty vector does: nothing is penalised at the first step,
+    # and later steps penalise the predictions alone.
+    empty = ctx2.gpt_kv_sample(prefix, 1, 5, history=[], **cfg)
+    assert np.array_equal(empty["last_processed_logits"], empty["last_logits"])
+    _compare_sampled(ctx2.gpt_kv_sample(prefix, 6, 5, history=[], **cfg),
+                     orc2.kv_sample(prefix, 6, 5, history=[], **cfg), "  2 layers empty history")
 
 
 def test_sampling_settings_rejected(ctx2, mit2):

@@ -295,6 +295,11 @@ def test_kv_sample_history_prefix(gpt):
     for t in (1, 8192):
         want[t] = raw[t] / np.float32(3.0) if raw[t] >= 0 else raw[t] * np.float32(3.0)
     assert np.array_equal(fake["last_processed_logits"], want)
+    # an empty prefix (the reference's empty vector) replaces the start token:
+    # nothing is penalised at the first step
+    empty = gpt.kv_sample(prefix, 1, 9, history=[], **cfg)
+    assert np.array_equal(empty["last_processed_logits"], empty["last_logits"])
+    assert not np.array_equal(empty["last_processed_logits"], default["last_processed_logits"])
     # later steps: the predictions join the prefix in the history
     long = gpt.kv_sample(prefix, 4, 9, history=[1] * 6 + [8192], **cfg)
     again = gpt.kv_sample(prefix, 4, 9, history=[1] * 6 + [8192] + [8192], **cfg)

@@ -164,3 +164,21 @@ def test_oracle_tensor_table_matches_synthetic_inventory(orc, mit2):
              for i in range(L.orc_model_tensor_count())}
     inv = {name: int(np.prod(shape)) for name, shape, _ in mit2.synthetic_tensor_specs()}
     assert table == inv
+
+
+def test_partial_euler_is_a_prefix_of_the_schedule(mit2, model_unit):
+    """orc_cfm_euler_partial (the config-4 trajectory fixture): its k steps of the
+    S-step schedule are the first k traced steps of the whole decode (same dt),
+    not a k-step decode; k = S is the whole decode."""
+    T, P, S = 6, 2, 5
+    x0 = mit2.normal_noise(T, 80, 25)
+    prompt = mit2.normal_noise(P, 80, 26, 2.0) - 5.0
+    cond = mit2.normal_noise(T, 512, 27)
+    style = mit2.normal_noise(1, 192, 28)[0]
+    final, xt, vt = model_unit.cfm_euler(x0, prompt, cond, style, S, 0.7, trace=True)
+    x2, xt2, vt2 = model_unit.cfm_euler_partial(x0, prompt, cond, style, S, 2, 0.7)
+    assert np.array_equal(vt2, vt[:2]) and np.array_equal(xt2, xt[:2])
+    assert np.array_equal(x2, xt[2])
+    assert not np.array_equal(x2, model_unit.cfm_euler(x0, prompt, cond, style, 2, 0.7))
+    xs, _, _ = model_unit.cfm_euler_partial(x0, prompt, cond, style, S, S, 0.7)
+    assert np.array_equal(xs, final)
