@@ -4,6 +4,14 @@
 //   --bench-cfm MODEL T STEPS ITERS     (main.cpp:2925-2930, run_bench_cfm :3065)
 //   --test-cfm-euler MODEL [--expect FILE]      (3 steps, cfg 0; :3342)
 //   --test-cfm-euler-cfg MODEL [--expect FILE]  (25 steps, cfg 0.5; :3405)
+//   --test-cfm-euler-cfg-large MODEL [--expect FILE]
+//                                       (T=173, P=8, cfg 0.5, steps 1 and 3;
+//                                        :3411-3443)
+//   --test-s2mel-full-inputs MODEL NOISE PROMPT COND STYLE STEPS CFG EXPECTED
+//                                       (caller's tensor files; :3516-3604)
+//   --test-dit-attention-tokens MODEL N [--expect FILE]
+//                                       (layer-0 attention core at N tokens,
+//                                        batch 2, repeat determinism; :584-638)
 //   --decode MODEL T P [--cfm_steps N] [--cfg R] [--seed S] [--out FILE]
 //   --cfm_steps N                       (12..25, main.cpp:3181-3187)
 //   --inspect-model-bundle DIR, --write-synthetic-bundle DIR [SEED] [STDDEV]
@@ -34,6 +42,7 @@
 #include <fstream>
 #include <iostream>
 #include <memory>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -256,6 +265,183 @@ int test_cfm_euler(const std::string& model, const char* stage, uint32_t steps, 
   return ok ? 0 : 1;
 }
 
+// Raw float32 file (native byte order), as the reference's read_raw_f32.
+std::vector<float> read_raw_f32(const std::string& path) {
+  std::ifstream f(path, std::ios::binary | std::ios::ate);
+  if (!f) throw std::runtime_error("cannot open " + path);
+  const std::streamsize bytes = f.tellg();
+  if (bytes < 0 || bytes % 4 != 0) throw std::runtime_error(path + " is not a whole number of float32 values");
+  std::vector<float> v((size_t)bytes / 4);
+  f.seekg(0);
+  f.read(reinterpret_cast<char*>(v.data()), bytes);
+  if (!f) throw std::runtime_error("short read from " + path);
+  return v;
+}
+
+struct Errors {
+  float max_abs = 0.0f;
+  double rel_l2 = 0.0;
+};
+
+// max |got - ref| and ||got - ref|| / ||ref|| over [begin, end) of both.
+Errors errors(const std::vector<float>& got, const std::vector<float>& ref, size_t begin, size_t end) {
+  Errors e;
+  double num = 0.0, den = 0.0;
+  for (size_t i = begin; i < end; ++i) {
+    const double d = (double)got[i] - (double)ref[i];
+    num += d * d;
+    den += (double)ref[i] * ref[i];
+    e.max_abs = std::max(e.max_abs, (float)std::fabs(d));
+  }
+  e.rel_l2 = std::sqrt(num / std::max(den, 1e-60));
+  return e;
+}
+
+size_t count_nonfinite(const std::vector<float>& v) {
+  size_t n = 0;
+  for (float x : v) n += std::isfinite(x) ? 0 : 1;
+  return n;
+}
+
+// run_cfm_euler_cfg_large_test (dit_cfm_bigvgan.cpp:3411-3443): T=173, P=8,
+// cfg 0.5, the reference's input series, decoded with 1 and with 3 steps.
+// The reference compares each with its CPU path at max-abs 3e-3; here the CPU
+// path's outputs come from --expect FILE (raw float32 [2][173][80]: the
+// 1-step decode, then the 3-step one, as the test suite writes them from
+// the CPU oracle).  Without it: finiteness, zero prompt rows, repeatability.
+int test_cfm_euler_cfg_large(const std::string& model, const std::string& expect) {
+  auto hip = open_model(model);
+  constexpr uint32_t tokens = 173, prompt_tokens = 8;
+  constexpr float cfg = 0.5f;
+  const auto x = series((size_t)tokens * 80, 0.018f, 0.07f, 61, 0.011f, 0.03f, false);
+  const auto prompt = series((size_t)prompt_tokens * 80, 0.022f, 0.09f, 37, 0.019f, 0.02f, true);
+  const auto cond = series((size_t)tokens * 512, 0.009f, 0.08f, 109, 0.014f, 0.04f, false);
+  std::vector<float> style(192);
+  for (size_t i = 0; i < style.size(); ++i) style[i] = std::cos((float)i * 0.015f) * 0.18f;
+  const size_t n = (size_t)tokens * 80;
+  std::vector<float> ref;
+  if (!expect.empty()) {
+    ref = read_raw_f32(expect);
+    if (ref.size() != 2 * n) throw std::runtime_error("--expect must hold 2 x 173 x 80 float32 values");
+  }
+  std::cout << "{\n  \"stage\": \"cfm_euler_cfg_large\",\n  \"tokens\": " << tokens
+            << ",\n  \"prompt_tokens\": " << prompt_tokens << ",\n  \"cfg_rate\": " << cfg
+            << ",\n  \"steps\": [\n";
+  bool ok = true;
+  const uint32_t step_counts[2] = {1u, 3u};
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t steps = step_counts[k];
+    const auto a = mit2::run_cfm_euler_hip(*hip, x, prompt, cond, style, tokens, prompt_tokens, steps, cfg);
+    const auto b = mit2::run_cfm_euler_hip(*hip, x, prompt, cond, style, tokens, prompt_tokens, steps, cfg);
+    float prompt_abs = 0.0f;
+    for (size_t i = 0; i < (size_t)prompt_tokens * 80; ++i) prompt_abs = std::max(prompt_abs, std::fabs(a[i]));
+    const float repeat = errors(a, b, 0, n).max_abs;
+    const size_t nonfinite = count_nonfinite(a);
+    bool pass = nonfinite == 0 && prompt_abs == 0.0f && repeat == 0.0f;
+    std::cout << "    {\"steps\": " << steps << ", \"nonfinite\": " << nonfinite
+              << ", \"prompt_rows_max_abs\": " << prompt_abs << ", \"repeat_max_abs_error\": " << repeat;
+    if (!ref.empty()) {
+      std::vector<float> r(ref.begin() + (std::ptrdiff_t)(k * n), ref.begin() + (std::ptrdiff_t)((k + 1) * n));
+      const Errors e = errors(a, r, 0, n);
+      pass = pass && e.max_abs <= 3e-3f;
+      std::cout << ", \"max_abs_error\": " << e.max_abs << ", \"rel_l2_error\": " << e.rel_l2;
+    }
+    std::cout << ", \"pass\": " << (pass ? "true" : "false") << "}" << (k == 0 ? ",\n" : "\n");
+    ok = ok && pass;
+  }
+  std::cout << "  ],\n  \"bar_max_abs\": 0.003,\n  \"ok\": " << (ok ? "true" : "false") << "\n}\n";
+  return ok ? 0 : 1;
+}
+
+// run_s2mel_full_inputs_test (dit_cfm_bigvgan.cpp:3516-3604): the decode of
+// the caller's tensors -- noise [T][80], prompt mel [P][80], condition
+// [T][512], style [192], raw float32 files -- against the expected full mel
+// [T][80], over the full mel and the generated rows, at the reference's
+// max-abs 3e-3.  Unlike the reference, a failing comparison is reported as
+// it is (no second attempt).
+int test_s2mel_full_inputs(const std::string& model, const std::string& noise_path,
+                           const std::string& prompt_path, const std::string& cond_path,
+                           const std::string& style_path, uint32_t steps, float cfg,
+                           const std::string& expected_path) {
+  const auto started = Clock::now();
+  const auto noise = read_raw_f32(noise_path);
+  const auto prompt = read_raw_f32(prompt_path);
+  const auto cond = read_raw_f32(cond_path);
+  const auto style = read_raw_f32(style_path);
+  const auto expected = read_raw_f32(expected_path);
+  if (noise.empty() || noise.size() % 80 != 0) throw std::runtime_error("noise must have shape [tokens,80]");
+  if (prompt.empty() || prompt.size() % 80 != 0)
+    throw std::runtime_error("prompt_mel must have shape [prompt_tokens,80]");
+  if (steps == 0) throw std::runtime_error("steps must be positive");
+  const uint32_t tokens = (uint32_t)(noise.size() / 80), prompt_tokens = (uint32_t)(prompt.size() / 80);
+  if (prompt_tokens > tokens) throw std::runtime_error("prompt_tokens exceeds total tokens");
+  if (cond.size() != (size_t)tokens * 512) throw std::runtime_error("condition must have shape [tokens,512]");
+  if (style.size() != 192) throw std::runtime_error("style must have shape [192]");
+  if (expected.size() != noise.size()) throw std::runtime_error("expected full mel size mismatch");
+  auto hip = open_model(model);  // after the inputs are checked: a bad file needs no GPU
+  const auto got = mit2::run_cfm_euler_hip(*hip, noise, prompt, cond, style, tokens, prompt_tokens, steps, cfg);
+  const Errors full = errors(got, expected, 0, got.size());
+  const Errors gen = errors(got, expected, (size_t)prompt_tokens * 80, got.size());
+  const bool ok = full.max_abs <= 3e-3f && gen.max_abs <= 3e-3f && count_nonfinite(got) == 0;
+  const double elapsed = std::chrono::duration<double>(Clock::now() - started).count();
+  std::cout << "{\n  \"stage\": \"s2mel_full_inputs_test\",\n  \"tokens\": " << tokens
+            << ",\n  \"prompt_tokens\": " << prompt_tokens << ",\n  \"generated_tokens\": "
+            << tokens - prompt_tokens << ",\n  \"steps\": " << steps << ",\n  \"cfg_rate\": " << cfg
+            << ",\n  \"full_vs_expected_max_abs_error\": " << full.max_abs
+            << ",\n  \"generated_vs_expected_max_abs_error\": " << gen.max_abs
+            << ",\n  \"full_vs_expected_rel_l2_error\": " << full.rel_l2
+            << ",\n  \"bar_max_abs\": 0.003,\n  \"ok\": " << (ok ? "true" : "false")
+            << ",\n  \"elapsed_seconds\": " << elapsed << "\n}\n";
+  return ok ? 0 : 1;
+}
+
+// run_dit_attention_core_tokens_test (dit_cfm_bigvgan.cpp:584-638): the layer-0
+// attention core (wqkv, RoPE, attention, wo) on the reference's input series
+// at N tokens.  Against the CPU path's output for that input (--expect FILE,
+// raw float32 [N][512], written by the test suite from the CPU oracle) at the
+// reference's max-abs 1e-3; a batch of two (the series, then a second one)
+// whose first branch must match the single run at that bar, and which must
+// repeat exactly (repeat error 0, the reference's determinism gate).
+int test_dit_attention_tokens(const std::string& model, uint32_t tokens, const std::string& expect) {
+  if (tokens == 0) throw std::runtime_error("N must be positive");
+  auto hip = open_model(model);
+  const size_t n = (size_t)tokens * 512;
+  std::vector<float> input(n);
+  for (size_t i = 0; i < n; ++i)
+    input[i] = std::sin((float)i * 0.017f) * 0.13f + std::cos((float)(i % 97) * 0.011f) * 0.09f;
+  auto stage = [&](const std::vector<float>& in, uint32_t batch) {
+    std::vector<uint32_t> mask((size_t)batch * tokens, 1u);
+    std::vector<float> out(in.size());
+    const mit2cfm_status st =
+        mit2cfm_stage_attention_core(hip->get(), in.data(), mask.data(), batch, tokens, 0, out.data());
+    if (st != MIT2CFM_OK) throw std::runtime_error(mit2cfm_last_error(hip->get()));
+    return out;
+  };
+  const auto single = stage(input, 1);
+  std::vector<float> input_b(2 * n);
+  std::copy(input.begin(), input.end(), input_b.begin());
+  for (size_t i = 0; i < n; ++i) input_b[n + i] = std::cos((float)i * 0.019f) * 0.11f;
+  const auto b1 = stage(input_b, 2);
+  const auto b2 = stage(input_b, 2);
+  const float repeat = errors(b1, b2, 0, 2 * n).max_abs;
+  const std::vector<float> branch0(b1.begin(), b1.begin() + (std::ptrdiff_t)n);
+  const float batched = errors(branch0, single, 0, n).max_abs;
+  bool ok = repeat == 0.0f && batched <= 1e-3f && count_nonfinite(b1) == 0;
+  std::cout << "{\n  \"stage\": \"dit_attention_core_tokens\",\n  \"tokens\": " << tokens;
+  if (!expect.empty()) {
+    const auto ref = read_raw_f32(expect);
+    if (ref.size() != n) throw std::runtime_error("--expect must hold N x 512 float32 values");
+    const Errors e = errors(single, ref, 0, n);
+    const Errors eb = errors(branch0, ref, 0, n);
+    ok = ok && e.max_abs <= 1e-3f && eb.max_abs <= 1e-3f;
+    std::cout << ",\n  \"max_abs_error\": " << e.max_abs << ",\n  \"rel_l2_error\": " << e.rel_l2
+              << ",\n  \"batched_branch0_err\": " << eb.max_abs;
+  }
+  std::cout << ",\n  \"batched_vs_single_max_abs\": " << batched << ",\n  \"batched_repeat_err\": " << repeat
+            << ",\n  \"ok\": " << (ok ? "true" : "false") << "\n}\n";
+  return ok ? 0 : 1;
+}
+
 int decode(const std::string& model, uint32_t tokens, uint32_t prompt_tokens, uint32_t steps, float cfg,
            uint64_t seed, const std::string& out) {
   auto hip = open_model(model);
@@ -281,7 +467,10 @@ int decode(const std::string& model, uint32_t tokens, uint32_t prompt_tokens, ui
 
 int usage() {
   std::cerr << "usage: mtts-cfm --bench-cfm MODEL T STEPS ITERS | --test-cfm-euler MODEL [--expect FILE] |\n"
-               "       --test-cfm-euler-cfg MODEL [--expect FILE] | --decode MODEL T P [--cfm_steps N] [--cfg R]\n"
+               "       --test-cfm-euler-cfg MODEL [--expect FILE] | --test-cfm-euler-cfg-large MODEL [--expect FILE] |\n"
+               "       --test-s2mel-full-inputs MODEL NOISE PROMPT COND STYLE STEPS CFG EXPECTED |\n"
+               "       --test-dit-attention-tokens MODEL N [--expect FILE] |\n"
+               "       --decode MODEL T P [--cfm_steps N] [--cfg R]\n"
                "       [--seed S] [--out FILE] | --inspect-model-bundle DIR |\n"
                "       --write-synthetic-bundle DIR [SEED] [STDDEV] |\n"
                "       --bench-bigvgan MODEL T ITERS | --test-bigvgan-vocoder MODEL |\n"
@@ -341,6 +530,12 @@ int main(int argc, char** argv) {
                          (uint32_t)std::stoul(argv[i + 4]));
       if (a == "--test-cfm-euler-cfg" && i + 1 < argc)
         return test_cfm_euler(argv[i + 1], "cfm_euler_cfg", 25, 0.5f, expect);
+      if (a == "--test-cfm-euler-cfg-large" && i + 1 < argc) return test_cfm_euler_cfg_large(argv[i + 1], expect);
+      if (a == "--test-s2mel-full-inputs" && i + 8 < argc)
+        return test_s2mel_full_inputs(argv[i + 1], argv[i + 2], argv[i + 3], argv[i + 4], argv[i + 5],
+                                      (uint32_t)std::stoul(argv[i + 6]), std::stof(argv[i + 7]), argv[i + 8]);
+      if (a == "--test-dit-attention-tokens" && i + 2 < argc)
+        return test_dit_attention_tokens(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), expect);
       if (a == "--decode" && i + 3 < argc)
         return decode(argv[i + 1], (uint32_t)std::stoul(argv[i + 2]), (uint32_t)std::stoul(argv[i + 3]), steps,
                       cfg, seed, out);

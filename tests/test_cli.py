@@ -1,7 +1,9 @@
 """The mtts-cfm command line (the reference CLI's flags for this path,
 runtime/main.cpp:57-88, :2925-2936, :3181-3187, :3293-3342): argument handling
 on the CPU; the GPU harnesses (--decode, --test-cfm-euler, --bench-bigvgan,
---test-bigvgan-vocoder) on a GPU."""
+--test-bigvgan-vocoder) on a GPU.  The file-driven harnesses against the CPU
+oracle (--test-cfm-euler-cfg-large, --test-s2mel-full-inputs,
+--test-dit-attention-tokens) are in test_gpu_bundle.py."""
 from __future__ import annotations
 
 import json
@@ -34,6 +36,27 @@ def test_cfm_steps_out_of_range_exits_1(cli, steps):
     r = _run(cli, "--cfm_steps", steps, "--decode", "synthetic", "8", "2")
     assert r.returncode == 1
     assert "between 12 and 25" in r.stderr
+
+
+def test_s2mel_full_inputs_rejects_bad_shapes_before_the_gpu(cli, tmp_path):
+    """--test-s2mel-full-inputs checks its files first (dit_cfm_bigvgan.cpp:3537-3559):
+    a noise file that is not [tokens,80] and a style that is not [192] exit 1."""
+    import numpy as np
+
+    def f(name, n):
+        p = tmp_path / f"{name}.f32"
+        np.zeros(n, np.float32).tofile(p)
+        return str(p)
+
+    good = dict(noise=f("noise", 8 * 80), prompt=f("prompt", 2 * 80), cond=f("cond", 8 * 512),
+                style=f("style", 192), expected=f("expected", 8 * 80))
+    for bad, msg in ((dict(noise=f("noise_bad", 8 * 80 + 3)), "[tokens,80]"),
+                     (dict(style=f("style_bad", 191)), "[192]"),
+                     (dict(prompt=f("prompt_bad", 9 * 80)), "exceeds")):
+        a = {**good, **bad}
+        r = _run(cli, "--test-s2mel-full-inputs", "synthetic", a["noise"], a["prompt"], a["cond"], a["style"],
+                 "2", "0.7", a["expected"])
+        assert r.returncode == 1 and msg in r.stderr, r.stderr
 
 
 def test_synthetic_bundle_roundtrip(mit2, cli, tmp_path):

@@ -135,3 +135,86 @@ def test_two_contexts_on_two_threads(mit2, tensors):
     finally:
         ca.close()
         cb.close()
+
+
+def _reference_series(T, P):
+    """The reference harnesses' inputs (dit_cfm_bigvgan.cpp:3306-3326, :3415-3422)."""
+    x = sincos_series(T * 80, 0.018, 0.011, 0.07, 0.03, 61).reshape(T, 80)
+    i = np.arange(P * 80)
+    prompt = (np.cos(i.astype(np.float32) * np.float32(0.022)) * np.float32(0.09)
+              + np.sin((i % 37).astype(np.float32) * np.float32(0.019)) * np.float32(0.02)).astype(np.float32).reshape(P, 80)
+    cond = sincos_series(T * 512, 0.009, 0.014, 0.08, 0.04, 109).reshape(T, 512)
+    style = (np.cos(np.arange(192, dtype=np.float32) * np.float32(0.015)) * np.float32(0.18)).astype(np.float32)
+    return x, prompt, cond, style
+
+
+def test_cli_cfm_euler_cfg_large_against_cpu_path(model, cli, bundle_dir, tmp_path):
+    """--test-cfm-euler-cfg-large (dit_cfm_bigvgan.cpp:3411-3443): T=173, P=8,
+    cfg 0.5, decoded with 1 and with 3 steps; the CPU path's two results come
+    from the oracle through --expect, held to the reference's max-abs 3e-3."""
+    T, P = 173, 8
+    x, prompt, cond, style = _reference_series(T, P)
+    ref = np.stack([model.cfm_euler(x, prompt, cond, style, s, 0.5) for s in (1, 3)])
+    exp = tmp_path / "expect_large.f32"
+    ref.astype(np.float32).tofile(exp)
+    r = subprocess.run([cli, "--test-cfm-euler-cfg-large", str(bundle_dir), "--expect", str(exp)],
+                       capture_output=True, text=True, timeout=300)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    d = json.loads(r.stdout)
+    assert d["ok"] and [s["steps"] for s in d["steps"]] == [1, 3]
+    for s in d["steps"]:
+        assert s["pass"] and s["max_abs_error"] <= 3e-3 and s["repeat_max_abs_error"] == 0
+        assert s["rel_l2_error"] <= MEL_TOL
+
+
+def test_cli_s2mel_full_inputs_round_trips_config3(mit2, cli, bundle_dir, tmp_path):
+    """--test-s2mel-full-inputs (dit_cfm_bigvgan.cpp:3516-3604) on the caller's
+    tensor files: the T=128 (P=48) 12-step fixture's inputs, regenerated from
+    its seeds, against the oracle's decode of them (tests/golden/config3), at
+    the reference's max-abs 3e-3 over the full and the generated mel."""
+    import json as _json
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    meta = _json.loads((golden / "config3.json").read_text())
+    with np.load(golden / "config3.npz") as z:
+        expected = z["final"]
+    T, P, S, cfg = meta["T"], meta["P"], meta["steps"], meta["cfg"]
+    x0, prompt, cond, style = _inputs(mit2, T, P, meta["seed"])
+    files = {}
+    for name, arr in (("noise", x0), ("prompt", prompt), ("cond", cond), ("style", style), ("expected", expected)):
+        files[name] = tmp_path / f"{name}.f32"
+        np.ascontiguousarray(arr, np.float32).tofile(files[name])
+    args = [cli, "--test-s2mel-full-inputs", str(bundle_dir), str(files["noise"]), str(files["prompt"]),
+            str(files["cond"]), str(files["style"]), str(S), str(cfg), str(files["expected"])]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=300)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    d = json.loads(r.stdout)
+    assert d["ok"] and (d["tokens"], d["prompt_tokens"], d["generated_tokens"], d["steps"]) == (T, P, T - P, S)
+    assert d["full_vs_expected_max_abs_error"] <= 3e-3 and d["generated_vs_expected_max_abs_error"] <= 3e-3
+    assert d["full_vs_expected_rel_l2_error"] <= MEL_TOL
+
+
+@pytest.mark.parametrize("tokens", [64, 300])
+def test_cli_dit_attention_tokens_against_cpu_path(model, cli, bundle_dir, tmp_path, tokens):
+    """--test-dit-attention-tokens (dit_cfm_bigvgan.cpp:584-638): the layer-0
+    attention core on the reference's input series at N tokens, against the
+    oracle's attention core through --expect (max-abs 1e-3), a batch of two
+    whose first branch matches, and the reference's determinism gate (repeat
+    error exactly 0)."""
+    n = tokens * 512
+    i = np.arange(n)
+    x = (np.sin(i.astype(np.float32) * np.float32(0.017)) * np.float32(0.13)
+         + np.cos((i % 97).astype(np.float32) * np.float32(0.011)) * np.float32(0.09)).astype(np.float32)
+    ref = model.attention_core(x.reshape(tokens, 512), np.ones(tokens, np.uint32), 0)
+    exp = tmp_path / "expect_attn.f32"
+    ref.astype(np.float32).tofile(exp)
+    r = subprocess.run([cli, "--test-dit-attention-tokens", str(bundle_dir), str(tokens), "--expect", str(exp)],
+                       capture_output=True, text=True, timeout=300)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    d = json.loads(r.stdout)
+    assert d["ok"] and d["tokens"] == tokens and d["batched_repeat_err"] == 0
+    assert d["max_abs_error"] <= 1e-3 and d["batched_branch0_err"] <= 1e-3
