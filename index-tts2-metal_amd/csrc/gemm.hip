@@ -98,6 +98,14 @@ struct TileMap {
   }
 };
 
+// Rotary rotation of the pair (x, y) by (cos, sin) = cs.  Each output is one
+// fused multiply-add over one rounded product, written out so that every
+// tile shape's instantiation rounds alike (left to the contraction pass, the
+// choice of which product to fuse varied between instantiations).
+__device__ inline float2 rope_rotate(float x, float y, float2 cs) {
+  return make_float2(__builtin_fmaf(x, cs.x, -(y * cs.y)), __builtin_fmaf(y, cs.x, x * cs.y));
+}
+
 template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN, int KG, int SP, int PIPE>
 __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(GemmArgs p, TileMap tmap) {
   // K split.  The product over K is summed in KG parts of equal length, added
@@ -126,6 +134,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   static_assert(KG == 1 || ((KG == 2 || KG == 4) && EPI != EPI_QKV),
                 "K groups: 2 or 4, and the QKV epilogue needs every wave");
   static_assert(!PIPE || (SP == 0 && (KG == 1 || KG == 2)), "pipelined loop: f16 operands, K in 1 or 2 parts");
+  static_assert(EPI != EPI_QKV || 512 % BN == 0, "a qkv tile must lie inside one of the q, k, v sections");
   static_assert(SP >= 0 && SP <= 2, "split mode");
 
   // One __shared__ object per stage and operand, declared here so each kernel
@@ -897,8 +906,8 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
             for (int r = 0; r < 4; ++r) {
               const int rl = wm * WTM + i * 16 + lr;
               const int c = 32 * g + 2 * (4 * lg + r);
-              stg(c)[rl] = (half_t)(rsv[i] * acc[i][2 * q][r] + bev[r]);
-              stg(c + 1)[rl] = (half_t)(rsv[i] * acc[i][2 * q + 1][r] + bov[r]);
+              stg(c)[rl] = (half_t)__builtin_fmaf(rsv[i], acc[i][2 * q][r], bev[r]);
+              stg(c + 1)[rl] = (half_t)__builtin_fmaf(rsv[i], acc[i][2 * q + 1][r], bov[r]);
             }
         }
         wait_lgkmcnt0();  // this wave's stores have landed before the barrier releases readers
@@ -933,12 +942,14 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
         if (m >= p.M) continue;
         float rs_row = 1.0f;  // rs of the row when the AdaRMSNorm is folded in
         if constexpr (kNormIn) rs_row = rsv[i];
-        const float ve[4] = {rs_row * acc[i][2 * q][0] + be.x, rs_row * acc[i][2 * q][1] + be.y,
-                             rs_row * acc[i][2 * q][2] + be.z, rs_row * acc[i][2 * q][3] + be.w};
-        const float vo[4] = {rs_row * acc[i][2 * q + 1][0] + bo.x,
-                             rs_row * acc[i][2 * q + 1][1] + bo.y,
-                             rs_row * acc[i][2 * q + 1][2] + bo.z,
-                             rs_row * acc[i][2 * q + 1][3] + bo.w};
+        const float ve[4] = {__builtin_fmaf(rs_row, acc[i][2 * q][0], be.x),
+                             __builtin_fmaf(rs_row, acc[i][2 * q][1], be.y),
+                             __builtin_fmaf(rs_row, acc[i][2 * q][2], be.z),
+                             __builtin_fmaf(rs_row, acc[i][2 * q][3], be.w)};
+        const float vo[4] = {__builtin_fmaf(rs_row, acc[i][2 * q + 1][0], bo.x),
+                             __builtin_fmaf(rs_row, acc[i][2 * q + 1][1], bo.y),
+                             __builtin_fmaf(rs_row, acc[i][2 * q + 1][2], bo.z),
+                             __builtin_fmaf(rs_row, acc[i][2 * q + 1][3], bo.w)};
         if constexpr (EPI == EPI_SWIGLU) {
           const int c = group * 16 + 4 * lg;
           float y[4];
@@ -968,9 +979,9 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
           half8 h;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float2 c2 = cs[r];
-            h[2 * r] = (half_t)((ve[r] * c2.x - vo[r] * c2.y) * sc);
-            h[2 * r + 1] = (half_t)((vo[r] * c2.x + ve[r] * c2.y) * sc);
+            const float2 rot = rope_rotate(ve[r], vo[r], cs[r]);
+            h[2 * r] = (half_t)(rot.x * sc);
+            h[2 * r + 1] = (half_t)(rot.y * sc);
           }
           half_t* dst = (sec == 0 ? p.q : p.k) + (head * p.Tpad + t) * 64 + d0;
           *reinterpret_cast<half8*>(dst) = h;
@@ -1146,6 +1157,11 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
       if (few_tiles(a, 64, 128)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
       return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 2>(a, s);
     }
+  }
+  if constexpr (EPI == EPI_QKV) {
+    // Long sequences (both CFG branches of T = 10784: 76.5 vs 86.0 us; equal
+    // at T = 3000, slower at T = 860); the same bits as the 64 x 64 tile.
+    if (tile_count(a, 64, 128) >= 1024) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 2>(a, s);
   }
   if constexpr (EPI == EPI_RESSKIP || EPI == EPI_DUAL) {
     if (a.N % 128 == 0) {
