@@ -20,18 +20,16 @@ hipError_t launch_nearest_rows(const half_t* src, int in_tokens, int out_tokens,
 // pair at out + lo_off (GemmArgs::split).
 hipError_t launch_f32_to_f16(const float* in, half_t* out, size_t n, size_t lo_off, hipStream_t s);
 
-// GroupNorm with one group over rows x 512 values: the mean and 1/sqrt(var +
-// eps) from the per-row, per-32-column partial sums and sums of squares the
-// producing GEMM wrote ([rows][16] each), reduced in double.  stats[0] =
-// mean, stats[1] = inverse standard deviation.
-hipError_t launch_gn_stats(const float* sum_parts, const float* ssq_parts, int rows, float eps,
-                           float* stats, hipStream_t s);
-
+// GroupNorm with one group over rows x 512 values, then Mish:
 // out[r][c] = f16(mish((y[r][c] - mean) * rstd * gamma[c] + beta[c])) for
-// r < rows (cpu_groupnorm1 + cpu_mish, tokenizer_tests.cpp:3874-3904); with
-// out_lo nonzero also the lo half of the split pair at out + out_lo.
-hipError_t launch_gn_mish(const float* y, const float* stats, const float* gamma,
-                          const float* beta, int rows, half_t* out, size_t out_lo, hipStream_t s);
+// r < rows (cpu_groupnorm1 + cpu_mish, tokenizer_tests.cpp:3874-3904), the
+// mean and rstd = 1/sqrt(var + eps) reduced in double from the per-row,
+// per-32-column partial sums and sums of squares the producing GEMM wrote
+// ([rows][16] each).  With out_lo nonzero also the lo half of the split pair
+// at out + out_lo.
+hipError_t launch_gn_mish(const float* sum_parts, const float* ssq_parts, float eps, const float* y,
+                          const float* gamma, const float* beta, int rows, half_t* out, size_t out_lo,
+                          hipStream_t s);
 
 // make_deterministic_normal_noise (tokenizer_tests.cpp:2121-2140) on the GPU:
 // out[n] for n = tokens * channels values.  splitmix64 is a counter: value

@@ -61,78 +61,77 @@ hipError_t launch_nearest_rows(const half_t* src, int in_tokens, int out_tokens,
   return hipGetLastError();
 }
 
-// One workgroup of 1024 threads: each thread folds a strided share of the
-// partials in double, then a tree over the workgroup.
-__global__ __launch_bounds__(1024) void gn_stats_kernel(const float* __restrict__ sum_parts,
-                                                        const float* __restrict__ ssq_parts,
-                                                        int nparts, double count, float eps,
-                                                        float* __restrict__ stats) {
-  __shared__ double s1[1024], s2[1024];
+// Mish as x * tanh(softplus(x)) = x * n / (n + 2) with n = e^x (e^x + 2):
+// one exponential and one division.  Past x = 15 the ratio rounds to 1 in
+// fp32 (and e^x would overflow further on), so x is returned there.
+__device__ __forceinline__ float mish_f(float x) {
+  if (x > 15.0f) return x;
+  const float e = expf(x);
+  const float n = e * (e + 2.0f);
+  return x * (n / (n + 2.0f));
+}
+
+// GroupNorm (one group over rows x 512 values) + Mish, statistics included.
+// Every workgroup first reduces all of the producing GEMM's per-row partial
+// sums and sums of squares in double, in one fixed order (a strided share per
+// thread, a wave reduction, the 16 wave sums in order), so all of them hold
+// the same mean and 1/std; then it normalises its own 4 rows, 2 values per
+// thread.
+constexpr int kGnRowsPerBlock = 4;
+__global__ __launch_bounds__(1024) void gn_mish_kernel(const float* __restrict__ sum_parts,
+                                                       const float* __restrict__ ssq_parts,
+                                                       int nparts, double count, float eps,
+                                                       const float* __restrict__ y,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta, int rows,
+                                                       half_t* __restrict__ out, size_t out_lo) {
+  __shared__ double w1[16], w2[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   double a = 0.0, b = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += 1024) {
+  for (int i = tid; i < nparts; i += 1024) {
     a += (double)sum_parts[i];
     b += (double)ssq_parts[i];
   }
-  s1[threadIdx.x] = a;
-  s2[threadIdx.x] = b;
-  __syncthreads();
-  for (int w = 512; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) {
-      s1[threadIdx.x] += s1[threadIdx.x + w];
-      s2[threadIdx.x] += s2[threadIdx.x + w];
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    const double mean = s1[0] / count;
-    double var = s2[0] / count - mean * mean;
-    if (var < 0.0) var = 0.0;
-    stats[0] = (float)mean;
-    stats[1] = (float)(1.0 / sqrt(var + (double)eps));
-  }
-}
-
-hipError_t launch_gn_stats(const float* sum_parts, const float* ssq_parts, int rows, float eps,
-                           float* stats, hipStream_t s) {
-  if (rows <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gn_stats_kernel, dim3(1), dim3(1024), 0, s, sum_parts, ssq_parts, rows * 16,
-                     (double)rows * 512.0, eps, stats);
-  return hipGetLastError();
-}
-
-__device__ __forceinline__ float mish_f(float x) { return x * tanhf(log1pf(expf(x))); }
-
-__global__ __launch_bounds__(256) void gn_mish_kernel(const float* __restrict__ y,
-                                                      const float* __restrict__ stats,
-                                                      const float* __restrict__ gamma,
-                                                      const float* __restrict__ beta, int rows,
-                                                      half_t* __restrict__ out, size_t out_lo) {
-  const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  const float mean = stats[0], rstd = stats[1];
-  const float4* yr = reinterpret_cast<const float4*>(y + (size_t)r * 512) + lane * 2;
-  const float4 a = yr[0], b = yr[1];
-  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  half_t o[8], ol[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int c = lane * 8 + i;
-    split_f16(mish_f((v[i] - mean) * rstd * gamma[c] + beta[c]), o[i], ol[i]);
+  for (int off = 32; off > 0; off >>= 1) {
+    a += __shfl_xor(a, off, 64);
+    b += __shfl_xor(b, off, 64);
   }
-  const half8 h = {o[0], o[1], o[2], o[3], o[4], o[5], o[6], o[7]};
-  *reinterpret_cast<half8*>(out + (size_t)r * 512 + lane * 8) = h;
-  if (out_lo) {
-    const half8 l = {ol[0], ol[1], ol[2], ol[3], ol[4], ol[5], ol[6], ol[7]};
-    *reinterpret_cast<half8*>(out + out_lo + (size_t)r * 512 + lane * 8) = l;
+  if (lane == 0) {
+    w1[wave] = a;
+    w2[wave] = b;
   }
+  __syncthreads();
+  double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    s1 += w1[w];
+    s2 += w2[w];
+  }
+  const double mean_d = s1 / count;
+  double var = s2 / count - mean_d * mean_d;
+  if (var < 0.0) var = 0.0;
+  const float mean = (float)mean_d;
+  const float rstd = (float)(1.0 / sqrt(var + (double)eps));
+
+  const int r = blockIdx.x * kGnRowsPerBlock + (tid >> 8);
+  if (r >= rows) return;
+  const int c = (tid & 255) * 2;
+  const float2 v = *reinterpret_cast<const float2*>(y + (size_t)r * 512 + c);
+  half_t o0, o1, l0, l1;
+  split_f16(mish_f((v.x - mean) * rstd * gamma[c] + beta[c]), o0, l0);
+  split_f16(mish_f((v.y - mean) * rstd * gamma[c + 1] + beta[c + 1]), o1, l1);
+  *reinterpret_cast<half2v*>(out + (size_t)r * 512 + c) = half2v{o0, o1};
+  if (out_lo) *reinterpret_cast<half2v*>(out + out_lo + (size_t)r * 512 + c) = half2v{l0, l1};
 }
 
-hipError_t launch_gn_mish(const float* y, const float* stats, const float* gamma,
-                          const float* beta, int rows, half_t* out, size_t out_lo, hipStream_t s) {
+hipError_t launch_gn_mish(const float* sum_parts, const float* ssq_parts, float eps, const float* y,
+                          const float* gamma, const float* beta, int rows, half_t* out, size_t out_lo,
+                          hipStream_t s) {
   if (rows <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gn_mish_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, y, stats, gamma, beta,
-                     rows, out, out_lo);
+  hipLaunchKernelGGL(gn_mish_kernel, dim3((rows + kGnRowsPerBlock - 1) / kGnRowsPerBlock), dim3(1024), 0,
+                     s, sum_parts, ssq_parts, rows * 16, (double)rows * 512.0, eps, y, gamma, beta, rows,
+                     out, out_lo);
   return hipGetLastError();
 }
 

@@ -256,7 +256,6 @@ class Engine {
     float* y32;    // [cap_out][512]  conv output
     float* sum_p;  // [cap_out][16]   per-row partial sums
     float* ssq_p;  // [cap_out][16]   per-row partial sums of squares
-    float* stats;  // [2]             GroupNorm mean, 1/std
     float* out32;  // [cap_out + prompt][512] host staging of the result
     int cap_cond = 0;
   };
@@ -271,7 +270,6 @@ class Engine {
     float* y32;
     float* sum_p;
     float* ssq_p;
-    float* stats;
     int cap_in, cap_out;
   };
   void length_regulator_on(const LrView& v, const float* s_infer, int in_tokens, int out_tokens,
@@ -296,6 +294,21 @@ class Engine {
       graphs_;
   uint64_t use_tick_ = 0;
   void clear_graphs();
+  // Captured condition-producer graphs (condition_device and
+  // length_regulator_device).  key: input tokens, output tokens, prompt
+  // rows, s_infer, prompt and output pointers, f32 mode.  Dropped when the
+  // regulator's buffers grow.
+  std::map<std::tuple<int, int, int, const void*, const void*, const void*, bool>, GraphEntry>
+      cond_graphs_;
+  // Enqueues `enqueue`'s launches on stream_ as a replay of the graph cached
+  // in `graphs` under `key`, capturing it first when there is none (the least
+  // recently used graph evicted past kMaxGraphs).  With graphs off, or while
+  // stream_ is being captured by the caller, the launches are enqueued
+  // directly.
+  template <typename Key, typename F>
+  void run_graph(std::map<Key, GraphEntry>& graphs, const Key& key, F&& enqueue);
+  template <typename Map>
+  static void destroy_graphs(Map& graphs);
 
  public:
   static constexpr size_t kMaxGraphs = 8;

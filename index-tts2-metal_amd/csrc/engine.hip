@@ -65,8 +65,7 @@ constexpr size_t kScrX16 = kScrP16 + al256((size_t)Engine::kNoAllocMaxCodes * 51
 constexpr size_t kScrY32 = kScrX16 + al256((size_t)(kNoAllocMaxFrames + 1) * 512 * 2 * 2);
 constexpr size_t kScrSum = kScrY32 + al256((size_t)kNoAllocMaxFrames * 512 * 4);
 constexpr size_t kScrSsq = kScrSum + al256((size_t)kNoAllocMaxFrames * 16 * 4);
-constexpr size_t kScrStats = kScrSsq + al256((size_t)kNoAllocMaxFrames * 16 * 4);
-constexpr size_t kScratchBytes = kScrStats + 256;  // 13.7 MB
+constexpr size_t kScratchBytes = kScrSsq + al256((size_t)kNoAllocMaxFrames * 16 * 4);  // 13.7 MB
 }  // namespace
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
@@ -802,6 +801,7 @@ Engine::Engine(const std::string& image_path, int device) : device_(device) {
 
 Engine::~Engine() {
   clear_graphs();
+  destroy_graphs(cond_graphs_);
   if (voc_io_) (void)hipFree(voc_io_);
   gpt_.reset();
   voc_.reset();
@@ -820,12 +820,59 @@ GptDecoder& Engine::gpt() {
   return *gpt_;
 }
 
-void Engine::clear_graphs() {
-  for (auto& kv : graphs_) {
+template <typename Map>
+void Engine::destroy_graphs(Map& graphs) {
+  for (auto& kv : graphs) {
     if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
     if (kv.second.graph) (void)hipGraphDestroy(kv.second.graph);
   }
-  graphs_.clear();
+  graphs.clear();
+}
+
+void Engine::clear_graphs() { destroy_graphs(graphs_); }
+
+template <typename Key, typename F>
+void Engine::run_graph(std::map<Key, GraphEntry>& graphs, const Key& key, F&& enqueue) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_OK(hipStreamIsCapturing(stream_, &cs));
+  if (!use_graph_ || cs != hipStreamCaptureStatusNone) {
+    enqueue();
+    return;
+  }
+  auto it = graphs.find(key);
+  if (it == graphs.end()) {
+    if (graphs.size() >= kMaxGraphs) {
+      // Evict the least recently used graph.  Launches already enqueued on
+      // the stream may still read its executable, so wait for them first
+      // (a new shape pays a capture anyway).
+      auto lru = graphs.begin();
+      for (auto g = graphs.begin(); g != graphs.end(); ++g)
+        if (g->second.last_use < lru->second.last_use) lru = g;
+      HIP_OK(hipStreamSynchronize(stream_));
+      (void)hipGraphExecDestroy(lru->second.exec);
+      (void)hipGraphDestroy(lru->second.graph);
+      graphs.erase(lru);
+    }
+    GraphEntry ge;
+    HIP_OK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    try {
+      enqueue();
+    } catch (...) {
+      hipGraph_t g = nullptr;
+      (void)hipStreamEndCapture(stream_, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    HIP_OK(hipStreamEndCapture(stream_, &ge.graph));
+    const hipError_t ie = hipGraphInstantiate(&ge.exec, ge.graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+      (void)hipGraphDestroy(ge.graph);
+      throw HipError(std::string("hipGraphInstantiate failed: ") + hipGetErrorString(ie));
+    }
+    it = graphs.emplace(key, ge).first;
+  }
+  it->second.last_use = ++use_tick_;
+  HIP_OK(hipGraphLaunch(it->second.exec, stream_));
 }
 
 void Engine::sync() { HIP_OK(hipStreamSynchronize(stream_)); }
@@ -1292,49 +1339,12 @@ void Engine::decode_device(const float* x0, const float* prompt, const float* co
     row_skip_ = RowSkip();
     HIP_OK(launch_copy_f32(ws.x_cur, x_out, (size_t)nreq * T * 80, stream_));
   };
-  if (!use_graph_) {
-    enqueue_all();
-    return;
-  }
   uint32_t cfg_bits;
   std::memcpy(&cfg_bits, &cfg, 4);
   auto key = std::make_tuple(nreq, T, steps, cfg_bits, (const void*)vtrace, (const void*)x0,
                              (const void*)prompt, (const void*)cond, (const void*)style,
                              (const void*)x_out, ragged, skip);
-  auto it = graphs_.find(key);
-  if (it == graphs_.end()) {
-    if (graphs_.size() >= kMaxGraphs) {
-      // Evict the least recently used graph.  Launches already enqueued on
-      // the stream may still read its executable, so wait for them first
-      // (a new shape pays a capture anyway).
-      auto lru = graphs_.begin();
-      for (auto g = graphs_.begin(); g != graphs_.end(); ++g)
-        if (g->second.last_use < lru->second.last_use) lru = g;
-      HIP_OK(hipStreamSynchronize(stream_));
-      (void)hipGraphExecDestroy(lru->second.exec);
-      (void)hipGraphDestroy(lru->second.graph);
-      graphs_.erase(lru);
-    }
-    GraphEntry ge;
-    HIP_OK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-    try {
-      enqueue_all();
-    } catch (...) {
-      hipGraph_t g = nullptr;
-      (void)hipStreamEndCapture(stream_, &g);
-      if (g) (void)hipGraphDestroy(g);
-      throw;
-    }
-    HIP_OK(hipStreamEndCapture(stream_, &ge.graph));
-    const hipError_t ie = hipGraphInstantiate(&ge.exec, ge.graph, nullptr, nullptr, 0);
-    if (ie != hipSuccess) {
-      (void)hipGraphDestroy(ge.graph);
-      throw HipError(std::string("hipGraphInstantiate failed: ") + hipGetErrorString(ie));
-    }
-    it = graphs_.emplace(key, ge).first;
-  }
-  it->second.last_use = ++use_tick_;
-  HIP_OK(hipGraphLaunch(it->second.exec, stream_));
+  run_graph(graphs_, key, enqueue_all);
 }
 
 void Engine::estimator_step_device(const float* x, const float* prompt_x, const float* cond,
@@ -1778,6 +1788,7 @@ int Engine::generated_frames(int codes) {
 void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
   if (in_tokens <= lr_.cap_in && out_tokens <= lr_.cap_out && cond_rows <= lr_.cap_cond) return;
   HIP_OK(hipStreamSynchronize(stream_));
+  destroy_graphs(cond_graphs_);  // captured on the old buffers
   const int ci = std::max(in_tokens, lr_.cap_in), co = std::max(out_tokens, lr_.cap_out);
   const int cc = std::max(cond_rows, lr_.cap_cond);
   size_t bytes = 0;
@@ -1785,7 +1796,7 @@ void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
   auto h = [&](size_t n) { bytes += (n * 2 + 255) / 256 * 256; };
   // The f16 GEMM operands are split pairs: hi rows, then lo rows.
   f((size_t)ci * 1024); h((size_t)ci * 1024 * 2); h((size_t)ci * 512 * 2); h((size_t)(co + 1) * 512 * 2);
-  f((size_t)co * 512); f((size_t)co * 16); f((size_t)co * 16); f(2); f((size_t)cc * 512);
+  f((size_t)co * 512); f((size_t)co * 16); f((size_t)co * 16); f((size_t)cc * 512);
   lr_.arena.reserve(bytes);
   Arena& a = lr_.arena;
   lr_.in32 = static_cast<float*>(a.take((size_t)ci * 1024 * 4));
@@ -1795,7 +1806,6 @@ void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
   lr_.y32 = static_cast<float*>(a.take((size_t)co * 512 * 4));
   lr_.sum_p = static_cast<float*>(a.take((size_t)co * 16 * 4));
   lr_.ssq_p = static_cast<float*>(a.take((size_t)co * 16 * 4));
-  lr_.stats = static_cast<float*>(a.take(2 * 4));
   lr_.out32 = static_cast<float*>(a.take((size_t)cc * 512 * 4));
   lr_.cap_in = ci;
   lr_.cap_out = co;
@@ -1805,7 +1815,8 @@ void Engine::ensure_lr(int in_tokens, int out_tokens, int cond_rows) {
 // run_length_regulator_full (gpt.cpp:5271-5313):
 //   content_in_proj GEMM (f16 out) -> nearest rows (+ the zero padding row)
 //   -> 4 x [k=3 zero-padded conv GEMM writing fp32 rows and per-row partial
-//      sums / sums of squares; GroupNorm statistics; GroupNorm + Mish -> f16]
+//      sums / sums of squares; GroupNorm, its statistics reduced in the same
+//      kernel, + Mish -> f16]
 //   -> k=1 conv GEMM into `out`.
 // In the default fp32 mode every GEMM operand is a split pair (hi, lo), so
 // the products carry fp32-level precision like the reference's fp32 path;
@@ -1818,8 +1829,11 @@ void Engine::length_regulator_device(const float* s_infer, int in_tokens, int ou
     throw std::invalid_argument("length regulator: token counts must be positive");
   HIP_OK(hipSetDevice(device_));
   ensure_lr(in_tokens, out_tokens, 0);
-  const LrView v{lr_.s16, lr_.p16, lr_.x16, lr_.y32, lr_.sum_p, lr_.ssq_p, lr_.stats, lr_.cap_in, lr_.cap_out};
-  length_regulator_on(v, s_infer, in_tokens, out_tokens, out);
+  const LrView v{lr_.s16, lr_.p16, lr_.x16, lr_.y32, lr_.sum_p, lr_.ssq_p, lr_.cap_in, lr_.cap_out};
+  run_graph(cond_graphs_,
+            std::make_tuple(in_tokens, out_tokens, 0, (const void*)s_infer, (const void*)nullptr,
+                            (const void*)out, lr_f32_),
+            [&] { length_regulator_on(v, s_infer, in_tokens, out_tokens, out); });
 }
 
 // The regulator's launches on the buffers of `lr` (enqueued on stream_).
@@ -1850,9 +1864,8 @@ void Engine::length_regulator_on(const LrView& lr, const float* s_infer, int in_
     g.C32 = lr.y32; g.ldc32 = 512; g.sum_out = lr.sum_p; g.ssq_out = lr.ssq_p;
     g.split = sp; g.a_lo = x16_lo; g.w_lo = sp == 2 ? (size_t)512 * 1536 : 0;
     HIP_OK(launch_gemm(g, A_CONV3Z, EPI_F32, s));
-    HIP_OK(launch_gn_stats(lr.sum_p, lr.ssq_p, out_tokens, 1e-5f, lr.stats, s));
-    HIP_OK(launch_gn_mish(lr.y32, lr.stats, W.lr_gn_w[b], W.lr_gn_b[b], out_tokens, lr.x16,
-                          x16_lo, s));
+    HIP_OK(launch_gn_mish(lr.sum_p, lr.ssq_p, 1e-5f, lr.y32, W.lr_gn_w[b], W.lr_gn_b[b], out_tokens,
+                          lr.x16, x16_lo, s));
   }
   GemmArgs g;
   g.M = out_tokens; g.N = 512; g.K = 512; g.A = lr.x16; g.lda = 512;
@@ -1867,17 +1880,26 @@ int Engine::condition_device(const float* s_infer, int codes, const float* promp
     throw std::invalid_argument("condition: codes and prompt_tokens must be positive");
   const int gen = generated_frames(codes);
   if (gen <= 0) throw std::invalid_argument("condition: generated frame count is zero");
+  if (!w_->has_lr)
+    throw std::runtime_error("length regulator: the context has no s2mel.net.length_regulator.* tensors");
   HIP_OK(hipSetDevice(device_));
-  HIP_OK(hipMemcpyAsync(cond, prompt_cond, (size_t)prompt_tokens * 512 * 4,
-                        hipMemcpyDeviceToDevice, stream_));
-  length_regulator_device(s_infer, codes, gen, cond + (size_t)prompt_tokens * 512);
+  ensure_lr(codes, gen, 0);
+  const LrView v{lr_.s16, lr_.p16, lr_.x16, lr_.y32, lr_.sum_p, lr_.ssq_p, lr_.cap_in, lr_.cap_out};
+  run_graph(cond_graphs_,
+            std::make_tuple(codes, gen, prompt_tokens, (const void*)s_infer, (const void*)prompt_cond,
+                            (const void*)cond, lr_f32_),
+            [&] {
+              HIP_OK(hipMemcpyAsync(cond, prompt_cond, (size_t)prompt_tokens * 512 * 4,
+                                    hipMemcpyDeviceToDevice, stream_));
+              length_regulator_on(v, s_infer, codes, gen, cond + (size_t)prompt_tokens * 512);
+            });
   return gen;
 }
 
 // condition_device on the static scratch: no device or host memory is
 // allocated, and nothing is cleared (every scratch value the kernels read is
 // written earlier in the same call: the split operands, the zero padding
-// row, the partial sums and the statistics).
+// row and the partial sums).
 int Engine::condition_device_noalloc(const float* s_infer, int codes, const float* prompt_cond,
                                      int prompt_tokens, float* cond) {
   if (!w_->has_lr)
@@ -1895,7 +1917,7 @@ int Engine::condition_device_noalloc(const float* s_infer, int codes, const floa
   const LrView v{reinterpret_cast<half_t*>(base + kScrS16), reinterpret_cast<half_t*>(base + kScrP16),
                  reinterpret_cast<half_t*>(base + kScrX16), reinterpret_cast<float*>(base + kScrY32),
                  reinterpret_cast<float*>(base + kScrSum),  reinterpret_cast<float*>(base + kScrSsq),
-                 reinterpret_cast<float*>(base + kScrStats), kNoAllocMaxCodes, kNoAllocMaxFrames};
+                 kNoAllocMaxCodes, kNoAllocMaxFrames};
   // Calls on this GPU are ordered through its event, except while the stream
   // is being captured into a graph (a captured stream may not wait on work
   // outside the capture): replays of such a graph must not overlap other

@@ -227,21 +227,22 @@ def conv_roofline_loop(rows: list[dict], B: int = 2, T: int = 860) -> tuple | No
 COND_NAMES = ["copy_prompt", "to_f16", "content_in_proj", "nearest_rows"]
 COND_KERN = ["copyBuffer", "f32_to_f16_kernel", "gemm_kernel", "nearest_rows_kernel"]
 for _b in range(4):
-    COND_NAMES += [f"conv{_b}_k3", f"gn_stats{_b}", f"gn_mish{_b}"]
-    COND_KERN += ["gemm_kernel", "gn_stats_kernel", "gn_mish_kernel"]
+    COND_NAMES += [f"conv{_b}_k3", f"gn_mish{_b}"]
+    COND_KERN += ["gemm_kernel", "gn_mish_kernel"]
 COND_NAMES.append("out_conv_k1")
 COND_KERN.append("gemm_kernel")
 
 
 def condition_tables(rows: list[dict]) -> str:
     """Every condition-producer call (a prompt copy, then the length regulator's
-    15 kernels), grouped by the grid signature of its GEMMs (the default split
+    11 kernels), grouped by the grid signature of its GEMMs (the default split
     mode and the f16 mode launch different tilings)."""
     groups = collections.defaultdict(list)
     for i, r in enumerate(rows):
-        if "nearest_rows_kernel" not in r["Kernel_Name"] or i < 3 or i + 14 > len(rows):
+        n_call = len(COND_KERN)
+        if "nearest_rows_kernel" not in r["Kernel_Name"] or i < 3 or i - 3 + n_call > len(rows):
             continue
-        seg = rows[i - 3:i + 14]
+        seg = rows[i - 3:i - 3 + n_call]
         if all(k in s["Kernel_Name"] for s, k in zip(seg, COND_KERN)):
             sig = tuple(s["Grid_Size_X"] for s in seg if "gemm_kernel" in s["Kernel_Name"])
             groups[sig].append(seg)
@@ -470,9 +471,9 @@ Same run as profiles/cfm_decode_T860_S25_B2_kernel_trace.md:
 
 bench.py `condition_producer` without the profiler: {cp['us_per_call']:.1f} us per call in the default mode (split f16
 operand pairs, fp32-level products), f16 mode {cp.get('f16_mode', {}).get('us_per_call', float('nan')):.1f} us.  Each call is
-`mit2cfm_condition_device`: a device copy of the 258 prompt rows, then the length regulator's 15 kernels (conv k=3 is the
-zero-padded implicit GEMM A_CONV3Z, M = 602, N = 512, K = 1536; gn_stats reduces the conv's per-row partial sums in
-double; gn_mish applies GroupNorm and Mish).  Groups below are the two precision modes (their GEMM grids differ).
+`mit2cfm_condition_device`, replayed as one graph: a device copy of the 258 prompt rows, then the length regulator's
+11 kernels (conv k=3 is the zero-padded implicit GEMM A_CONV3Z, M = 602, N = 512, K = 1536; gn_mish reduces the conv's
+per-row partial sums in double, the same in every workgroup, then applies GroupNorm and Mish).  Groups below are the two precision modes (their GEMM grids differ).
 
 {cond}
 """
