@@ -29,6 +29,8 @@ It reads whichever of these inputs exist and writes the summary each one feeds:
       the same with MIT2CFM_GRAPH=0 and the GPT section of bench.py (see GPT_CMDS)
     -> gpt_decode_P150_553codes_kernel_trace.md, traffic_gemv_gpt_c_fc.json
 
+Any of these CSVs may come gzip-compressed (NAME.csv.gz); it is unpacked first.
+
 HBM bytes come from FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by what the
 same counters read for the bench's 256 MiB streaming copy (`calibration` in the bench
 line): FETCH_SIZE reads half the bytes a copy fetches on MI355X, so its factor is
@@ -39,7 +41,9 @@ from __future__ import annotations
 import argparse
 import collections
 import csv
+import gzip
 import json
+import shutil
 from pathlib import Path
 
 PEAK_TF = 2500.0  # MI355X f16 dense MFMA, TFLOP/s
@@ -155,7 +159,18 @@ def find_decodes(rows: list[dict]):
     return out
 
 
-def decode_table(group: list, B: int, T: int, S: int) -> tuple[str, dict]:
+def skipped_padding_flops(tokens: list[int], T: int) -> dict:
+    """Algorithmic FLOPs per launch of each op when padded rows are skipped:
+    every product covers min(valid + 2, T) rows of each of a request's two
+    branches, the attention those rows' queries against the valid keys."""
+    need = [min(t + 2, T) for t in tokens for _ in range(2)]
+    keys = [t for t in tokens for _ in range(2)]
+    out = {op: op_flops(op, 1, 1) * sum(need) for op in STEP_ORDER if op != "attn" and op_flops(op, 1, 1)}
+    out["attn"] = 2048.0 * sum(n * k for n, k in zip(need, keys))
+    return out
+
+
+def decode_table(group: list, B: int, T: int, S: int, flops: dict | None = None) -> tuple[str, dict]:
     per = collections.defaultdict(list)
     spans, busy = [], []
     for seg in group:
@@ -171,7 +186,7 @@ def decode_table(group: list, B: int, T: int, S: int) -> tuple[str, dict]:
     summary = {}
     for op in sorted(tot, key=lambda o: -tot[o]):
         avg = tot[op] / cnt[op]
-        fl = op_flops(op, B, T)
+        fl = flops[op] if flops and op in flops else op_flops(op, B, T)
         tf = fl / (avg * 1e-6) / 1e12 if fl else None
         summary[op] = (avg, tf / PEAK_TF if tf else None)
         rows.append([f"`{op}`", cnt[op], f"{tot[op]:.1f}", f"{avg:.2f}", f"{100 * tot[op] / step:.1f}%",
@@ -445,16 +460,21 @@ skip-in (blocks 6..11, K = 2560); `post` is conv1|res_projection with skip_linea
             if (B, T, S) == (16, 1348, 16) and bt:
                 # the bench times this shape twice: padded rows computed, then skipped
                 half = len(segs) // 2
-                for label, ss in (("padded rows computed", segs[:half]), ("padded rows skipped (MIT2CFM_PADDING_SKIP)", segs[half:])):
+                toks = bt.get("configs", {}).get("config5_8req_padded_B16_S16_skip_padding", {}).get("tokens")
+                skip_fl = skipped_padding_flops(toks, T) if toks else None
+                for label, ss, fl in (("padded rows computed", segs[:half], None),
+                                      ("padded rows skipped (MIT2CFM_PADDING_SKIP)", segs[half:], skip_fl)):
                     if ss:
-                        t, _ = decode_table(ss, B, T, S)
+                        t, _ = decode_table(ss, B, T, S, fl)
                         parts.append(f"## {title}; {label}\n\n{t}")
             else:
                 t, _ = decode_table(segs, B, T, S)
                 parts.append(f"## {title}\n\n{t}")
         md = (f"# DiT-CFM decode at the other benchmark workloads -- rocprofv3 kernel trace\n\nThe same run as "
-              f"profiles/cfm_decode_T860_S25_B2_kernel_trace.md.\n\n{head}\n{legend}  For the padded batch the "
-              f"utilisation counts the padded rows, so it is the kernels' rate on the work they did; bench.py's "
+              f"profiles/cfm_decode_T860_S25_B2_kernel_trace.md.\n\n{head}\n{legend}  For the padded batch with its "
+              f"padded rows computed the utilisation counts them, so it is the kernels' rate on the work they did; with "
+              f"them skipped it counts the rows each product computes (each request's valid length + 2, both "
+              f"branches) and, for the attention, those queries against the valid keys.  bench.py's "
               f"`decode_mfma_util` counts valid rows and keys only.\n\n" + "\n\n".join(parts) + "\n")
         (out / "cfm_decode_configs_kernel_trace.md").write_text(md)
         print("wrote cfm_decode_configs_kernel_trace.md")
@@ -654,6 +674,16 @@ weights): {loop} (kernel execution from the trace timestamps).
             print("wrote traffic_gemv_gpt_c_fc.json")
 
 
+def unpack_raw(raw: Path) -> None:
+    """Raw CSVs may arrive gzip-compressed (NAME.csv.gz, to keep a run's output
+    small); each is unpacked beside itself once."""
+    for gz in sorted(raw.rglob("*.csv.gz")):
+        dst = gz.with_suffix("")
+        if not dst.exists():
+            with gzip.open(gz, "rb") as f, open(dst, "wb") as o:
+                shutil.copyfileobj(f, o)
+
+
 def main() -> None:
     root = Path(__file__).resolve().parent.parent
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
@@ -661,6 +691,7 @@ def main() -> None:
     p.add_argument("--out", type=Path, default=root / "profiles", help="where the summaries go")
     a = p.parse_args()
     a.out.mkdir(parents=True, exist_ok=True)
+    unpack_raw(a.raw)
     write_decode_profiles(a.raw, a.out)
     write_counter_profiles(a.raw, a.out)
     write_gpt_profiles(a.raw, a.out)
