@@ -1124,8 +1124,34 @@ static bool few_tiles(const GemmArgs& a, int BM, int BN) {
 //    83.2 us; 128x128 at M = 6000, 17.0 vs 24.0 us.
 // The short-K products (K = 512: w1|w3, QKV, wo, res/skip) stay on the
 // tiles above, which the pipelined loop did not beat at any M.
-static long tile_count(const GemmArgs& a, int BM, int BN) {
-  return (long)((a.M + BM - 1) / BM) * (a.N / BN);
+// Row tiles a launch covers: ceil(M / BM), or with row skipping the merged
+// runs of each sequence's needed rows, as make_tile_map lays them out.
+static long row_tiles(const GemmArgs& a, int BM) {
+  if (a.row_nb <= 0) return (a.M + BM - 1) / BM;
+  long total = 0;
+  int lo = -1, hi = -1;
+  for (int b = 0; b < a.row_nb; ++b) {
+    const int blo = b * a.row_T / BM, bhi = (b * a.row_T + a.row_need[b] - 1) / BM;
+    if (lo >= 0 && blo <= hi + 1) {
+      hi = std::max(hi, bhi);
+    } else {
+      if (lo >= 0) total += hi - lo + 1;
+      lo = blo;
+      hi = bhi;
+    }
+  }
+  return total + hi - lo + 1;
+}
+static long tile_count(const GemmArgs& a, int BM, int BN) { return row_tiles(a, BM) * (a.N / BN); }
+
+// Relative time of a pipelined tiling: its rounds of tiles over the 256 CUs
+// (one workgroup per CU at these ring sizes) times the tile's area over the
+// fraction of peak it reaches at large M (measured standalone at M = 21568).
+// At the full padded batch this picks 192 x 128 for the conv (139.5 vs 149.7
+// us measured against 128 x 128); with the padding skipped the needed row
+// tiles leave 192 x 128 a last round mostly idle, and 128 x 128 wins.
+static double pipe_cost(long tiles, int BM, int BN, double rate) {
+  return (double)((tiles + 255) / 256) * BM * BN / rate;
 }
 template <int KG, int NST>
 static bool pipe_fits(const GemmArgs& a) {
@@ -1152,8 +1178,12 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
     // Two K groups (16 wavefronts, the partial tile reduced through the idle
     // ring): 17.1 vs 18.3 us.
     if (a.N % 128 == 0) {
-      if (tile_count(a, 192, 128) >= 256 && pipe_fits<2, 4>(a))
+      const long t192 = tile_count(a, 192, 128), t128 = tile_count(a, 128, 128);
+      if (t192 >= 256 && pipe_fits<2, 4>(a)) {
+        if (pipe_cost(t128, 128, 128, 0.302) < pipe_cost(t192, 192, 128, 0.324))
+          return launch_tile<128, 128, 64, 4, AM, EPI, 2, 4, 2, 0, 1>(a, s);
         return launch_tile<192, 128, 64, 4, AM, EPI, 4, 2, 2, 0, 1>(a, s);
+      }
       if (few_tiles(a, 64, 128)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
       return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 2>(a, s);
     }
@@ -1174,8 +1204,10 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
     // two wave groups: 9.4 vs 9.8 us and 7.25 vs 7.7 us.
     if (a.K >= 1024 && (a.K / 64) % 2 == 0) {
       if (a.N % 128 == 0 && pipe_fits<2, 4>(a)) {
-        if (tile_count(a, 192, 128) >= 256) return launch_tile<192, 128, 64, 4, AM, EPI, 4, 2, 2, 0, 1>(a, s);
-        if (tile_count(a, 128, 128) >= 160) return launch_tile<128, 128, 64, 4, AM, EPI, 2, 4, 2, 0, 1>(a, s);
+        const long t192 = tile_count(a, 192, 128), t128 = tile_count(a, 128, 128);
+        if (t192 >= 256 && pipe_cost(t192, 192, 128, 0.292) <= pipe_cost(t128, 128, 128, 0.257))
+          return launch_tile<192, 128, 64, 4, AM, EPI, 4, 2, 2, 0, 1>(a, s);
+        if (t128 >= 160) return launch_tile<128, 128, 64, 4, AM, EPI, 2, 4, 2, 0, 1>(a, s);
       }
       if (few_tiles(a, 64, 64)) return launch_tile<32, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
       return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 2>(a, s);
