@@ -584,17 +584,42 @@ Raw counters (per dispatch):
 GPT_WHAT = {"c_attn": "c_attn GEMV 3840x1280 + LN, K/V to cache", "attn_proj": "attn c_proj GEMV 1280x1280 + residual",
             "c_fc": "c_fc GEMV 5120x1280 + LN + gelu_new", "mlp_proj": "mlp c_proj GEMV 1280x5120 + residual",
             "mel_head": "mel_head GEMV 8194x1280 + ln_f + final_norm"}
-GPT_BLOCKS = {"480": "c_attn", "320": None, "640": "c_fc", "1025": "mel_head"}
+def gemv_roles(rows: list[dict], grid_key: str, wg_key: str) -> dict:
+    """Kernel id -> product for the decode-step GEMVs, from their launch order
+    within a layer (c_attn, the attention, attn c_proj, c_fc, mlp c_proj):
+    two products can share a grid, so the grid alone does not name them.
+    `rows` are dispatches in launch order."""
+    g = [r for r in rows if "gemv_kernel" in r["Kernel_Name"] and "gemv_rows" not in r["Kernel_Name"]]
+    roles = {}
+    # attn c_proj is the GEMV launched right after an attention combine; the
+    # first layer where the pattern is whole names all four
+    seq = [r for r in rows if any(k in r["Kernel_Name"] for k in ("gemv_kernel", "attn_combine_kernel"))
+           and "gemv_rows" not in r["Kernel_Name"]]
+    for i in range(len(seq) - 3):
+        if "attn_combine_kernel" in seq[i]["Kernel_Name"] and all("gemv_kernel" in seq[i + k]["Kernel_Name"]
+                                                                   for k in (1, 2, 3)):
+            roles.setdefault(seq[i + 1]["Kernel_Id"], "attn_proj")
+            roles.setdefault(seq[i + 2]["Kernel_Id"], "c_fc")
+            roles.setdefault(seq[i + 3]["Kernel_Id"], "mlp_proj")
+            if i >= 1 and "gemv_kernel" in seq[i - 1]["Kernel_Name"]:
+                roles.setdefault(seq[i - 1]["Kernel_Id"], "c_attn")
+        if len(roles) >= 4:
+            break
+    for r in g:  # the head: the widest grid
+        if int(r[grid_key]) // int(r[wg_key]) > 1000:
+            roles.setdefault(r["Kernel_Id"], "mel_head")
+    return roles
 
 
-def gpt_kernel_key(r: dict) -> str:
+def gpt_kernel_key(r: dict, roles: dict) -> str:
     n = r["Kernel_Name"]
     for k in ("gemv_rows_kernel", "gemv_kernel", "attn_split_kernel", "attn_combine_kernel", "sample_kernel",
               "embed_rows_kernel", "embed_kernel", "argmax_kernel", "advance_rows_kernel"):
         if k in n:
             if k.startswith("gemv"):
                 blocks = int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"])
-                return f"{k} grid {blocks}x{r['Workgroup_Size_X']}"
+                role = roles.get(r["Kernel_Id"]) if k == "gemv_kernel" else "prefill"
+                return f"{k} {role or '?'} (grid {blocks}x{r['Workgroup_Size_X']})"
             return k
     return n[:40]
 
@@ -608,19 +633,20 @@ def write_gpt_profiles(raw: Path, out: Path) -> None:
     rows = [r for r in load_trace(tr) if any(k in r["Kernel_Name"] for k in ("gemv", "attn_split", "attn_combine",
                                                                               "sample_kernel", "embed", "argmax",
                                                                               "advance_rows"))]
+    roles = gemv_roles(rows, "Grid_Size_X", "Workgroup_Size_X")
     per = collections.defaultdict(list)
     for r in rows:
-        per[gpt_kernel_key(r)].append(dur(r))
+        per[gpt_kernel_key(r, roles)].append(dur(r))
     body = [[f"`{k}`", len(v), f"{sum(v) / len(v):.2f}", f"{min(v):.2f}", f"{max(v):.2f}", f"{sum(v) / 1e3:.2f}"]
             for k, v in sorted(per.items(), key=lambda kv: -sum(kv[1]))]
     g = bt["gpt_decode"]
-    # the c_fc timing loop: the longest run of back-to-back 640-block GEMVs
+    # the c_fc timing loop: the longest run of back-to-back c_fc GEMVs
     best, i = (0, 0), 0
-    key_fc = next((k for k in per if k.startswith("gemv_kernel grid 640x")), None)
+    key_fc = next((k for k in per if k.startswith("gemv_kernel c_fc ")), None)
     while i < len(rows):
-        if gpt_kernel_key(rows[i]) == key_fc:
+        if gpt_kernel_key(rows[i], roles) == key_fc:
             j = i
-            while j < len(rows) and gpt_kernel_key(rows[j]) == key_fc:
+            while j < len(rows) and gpt_kernel_key(rows[j], roles) == key_fc:
                 j += 1
             if j - i > best[1] - best[0]:
                 best = (i, j)
@@ -643,7 +669,7 @@ ended in a host SIGSEGV inside hipGraphLaunch of the GPT step graph.
 bench.py `gpt_decode` of the traced run (direct launches, profiler attached): {g['ms_per_code']:.4f} ms per code, prefill
 {g['prefill_ms']:.3f} ms.  Without the profiler and with graph replay the bench's figure is the one in the round's bench line.
 
-## Per kernel (all dispatches of the GPT section; GEMVs keyed by blocks x threads)
+## Per kernel (all dispatches of the GPT section; GEMVs named by product, with blocks x threads)
 
 {md_table(['kernel', 'dispatches', 'avg us', 'min us', 'max us', 'total ms'], body)}
 
@@ -656,9 +682,16 @@ weights): {loop} (kernel execution from the trace timestamps).
     wr = raw / "gptpmc_write" / "write_counter_collection.csv"
     cal = calibration(fe, wr)
     if cal:
-        match = lambda r: "gemv_kernel" in r["Kernel_Name"] and int(r["Grid_Size"]) // int(r["Workgroup_Size"]) == 640
-        f = pmc_per_dispatch(fe, "FETCH_SIZE", match)
-        w = pmc_per_dispatch(wr, "WRITE_SIZE", match)
+        def fc_match(path: Path, counter: str):
+            disp = {}
+            for r in csv.DictReader(open(path)):
+                if r["Counter_Name"] == counter:
+                    disp.setdefault(int(r["Dispatch_Id"]), r)
+            ordered = [disp[k] for k in sorted(disp)]
+            fc = [k for k, v in gemv_roles(ordered, "Grid_Size", "Workgroup_Size").items() if v == "c_fc"]
+            return lambda r: r["Kernel_Id"] in fc
+        f = pmc_per_dispatch(fe, "FETCH_SIZE", fc_match(fe, "FETCH_SIZE"))
+        w = pmc_per_dispatch(wr, "WRITE_SIZE", fc_match(wr, "WRITE_SIZE"))
         if f and w:
             fk, wk = sum(f) / len(f), sum(w) / len(w)
             j = {"kernel": "gemv_gpt_c_fc",
