@@ -1,9 +1,9 @@
 """Builds the summaries under profiles/ from raw rocprofv3 output (measurement tooling).
 
 One command rebuilds every table from the CSVs a profiling run leaves in a
-directory RAW (default gpurun_out/; the commands below write there):
+directory RAW (the commands below write there):
 
-    python3 index-tts2-metal_amd/profile_tables.py [--raw RAW] [--out profiles]
+    python3 index-tts2-metal_amd/profile_tables.py --raw RAW [--out profiles]
 
 It reads whichever of these inputs exist and writes the summary each one feeds:
 
@@ -720,7 +720,7 @@ def unpack_raw(raw: Path) -> None:
 def main() -> None:
     root = Path(__file__).resolve().parent.parent
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    p.add_argument("--raw", type=Path, default=root / "gpurun_out", help="directory of the rocprofv3 output")
+    p.add_argument("--raw", type=Path, required=True, help="directory of the rocprofv3 output")
     p.add_argument("--out", type=Path, default=root / "profiles", help="where the summaries go")
     a = p.parse_args()
     a.out.mkdir(parents=True, exist_ok=True)
