@@ -171,6 +171,52 @@ def test_condition_device_feeds_decode(mit2, ctx_lr):
     assert np.array_equal(got, ref)
 
 
+def test_condition_device_inside_a_callers_graph(mit2, ctx_lr):
+    """mit2cfm_condition_device replays a graph of its own per shape; on a
+    stream the caller is capturing it enqueues its kernels into the caller's
+    graph instead.  Three replays of that graph give the eager call's
+    condition bit for bit, with an eager call of another shape (which captures
+    and replays the library's own graph) run between them."""
+    import ctypes
+
+    torch = pytest.importorskip("torch")
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    dev = torch.device("cuda:0")
+    codes, P = 120, 40
+    gen = mit2.generated_frames(codes)
+    d_s = torch.from_numpy(mit2.normal_noise(codes, 1024, 31)).to(dev)
+    d_pc = torch.from_numpy(mit2.normal_noise(P, 512, 32)).to(dev)
+    ref = torch.full((P + gen, 512), float("nan"), dtype=torch.float32, device=dev)
+    got = torch.full_like(ref, float("nan"))
+    o_s = torch.from_numpy(mit2.normal_noise(60, 1024, 33)).to(dev)
+    o_pc = torch.from_numpy(mit2.normal_noise(10, 512, 34)).to(dev)
+    other = torch.empty((10 + mit2.generated_frames(60), 512), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    # the eager call sizes the regulator's buffers (a call inside a capture must not grow them)
+    assert ctx_lr.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, ref.data_ptr(), sync=True) == gen
+    stream = ctypes.c_void_p(ctx_lr.stream)
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    print(f"condition inside a caller's graph: codes={codes} P={P}", flush=True)
+    assert hip.hipStreamBeginCapture(stream, 1) == 0  # hipStreamCaptureModeThreadLocal
+    try:
+        ctx_lr.condition_device(d_s.data_ptr(), codes, d_pc.data_ptr(), P, got.data_ptr())
+    finally:
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(graph)) == 0
+    try:
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
+        for rep in range(3):
+            got.fill_(float("nan"))
+            torch.cuda.synchronize()
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            assert torch.equal(got, ref), f"replay {rep}"
+            ctx_lr.condition_device(o_s.data_ptr(), 60, o_pc.data_ptr(), 10, other.data_ptr(), sync=True)
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)
+
+
 @pytest.mark.parametrize("tokens,channels,seed,temp", [(860, 80, 1, 1.0), (7, 9, 20240605, 0.5),
                                                        (1, 1, 42, 1.0)])
 def test_noise_device_matches_host_generator(mit2, orc, ctx_lr, tokens, channels, seed, temp):
