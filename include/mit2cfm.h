@@ -158,7 +158,8 @@ mit2cfm_status mit2cfm_decode_graph_count(mit2cfm_ctx* ctx, uint32_t* count, uin
  * attention stop there; the two rows after the valid ones are kept because
  * the WaveNet's k=5 conv at the last valid rows reads them).  Valid rows are
  * bit-identical in both modes; x_out's padded rows are unspecified with
- * SKIP.  Full-length batches and single decodes are unaffected.  No
+ * SKIP.  Full-length batches, single decodes and batches of more than 16
+ * branches (8 requests with CFG) compute every row in either mode.  No
  * reference counterpart (the reference decodes one request per call). */
 #define MIT2CFM_PADDING_COMPUTE 0
 #define MIT2CFM_PADDING_SKIP 1

@@ -257,6 +257,36 @@ def test_row_tiling_does_not_change_results(mit2, ctx):
         assert np.array_equal(alone, batch[r])
 
 
+@pytest.mark.parametrize("toks", [[5, 63, 64, 130, 199, 200], [200, 5, 198], [40 + 17 * r for r in range(9)]],
+                         ids=["edges", "first-full", "nine-requests"])
+def test_skipped_padding_keeps_valid_rows(mit2, ctx, toks):
+    """MIT2CFM_PADDING_SKIP at its edges: requests shorter than a row tile,
+    of exactly a tile, one and two rows short of the padded length (their
+    needed rows are clamped to it), a full-length request first, and nine
+    requests (18 branches, more than the row skip covers: every row is
+    computed).  Each request's valid rows equal the padding-computed decode's
+    bit for bit."""
+    T, P, steps, cfg = max(toks), 4, 2, 0.7
+    n = len(toks)
+    reqs = [inputs(mit2, T, P, seed=700 + 10 * r) for r in range(n)]
+    X0 = np.stack([q[0] for q in reqs])
+    PR = np.zeros((n, T, 80), np.float32)
+    for r in range(n):
+        PR[r, :P] = reqs[r][1]
+    CO = np.stack([q[2] for q in reqs])
+    ST = np.stack([q[3] for q in reqs])
+    print(f"skipped padding: requests {toks}", flush=True)
+    ref = ctx.decode_batched(toks, [P] * n, X0, PR, CO, ST, steps, cfg)
+    ctx.set_padding("skip")
+    try:
+        got = ctx.decode_batched(toks, [P] * n, X0, PR, CO, ST, steps, cfg)
+    finally:
+        ctx.set_padding("compute")
+    for r, t in enumerate(toks):
+        assert np.isfinite(got[r, :t]).all()
+        assert np.array_equal(got[r, :t], ref[r, :t]), f"request {r} (T={t})"
+
+
 def test_single_token_decode_is_finite(mit2, ctx):
     """T=1: the reference CPU reflect pad never terminates for one token;
     the HIP path follows the reference GPU kernel (reflect index 0)."""
