@@ -6,8 +6,8 @@
 // cpu_attention_single_head_masked (runtime/impl/tokenizer_tests.cpp:3960):
 // softmax over unmasked keys of (q.k)/8, then the weighted sum of V.
 //
-// Layout: Q, K are [B][8][Tpad][64] f16 (Q already scaled by 1/8 and both
-// RoPE-rotated by the QKV GEMM epilogue); V is stored transposed,
+// Layout: Q, K are [B][8][Tpad][64] f16 (Q already scaled by log2(e)/8 and
+// both RoPE-rotated by the QKV GEMM epilogue); V is stored transposed,
 // Vt [B][8][64][Tpad].  The key mask arrives as kbias [B][Tpad] fp32 (0 for
 // a valid key, -inf for a masked or padding key; key_bias_kernel builds it
 // once per mask, followed by B int words: each branch's key count, one past
@@ -63,11 +63,15 @@ __device__ __forceinline__ void attn_static_for(F&& f) {
 // merge (m, l, O) at the end.
 //
 // Softmax arithmetic per score is what bounds this kernel (the matrix cores
-// have slack), so it is kept to one FMA, a share of a max, a subtract and an
-// exp2:
-//  * scores are kept in log2 units, s2 = s * log2(e) + kbias[key], where the
-//    per-key bias is 0 for a valid key and -inf for a masked or padding key
-//    (built once per mask by key_bias_kernel), so masking costs nothing;
+// have slack), so it is kept to a share of a max, an exp2 and a share of
+// the f16 pack:
+//  * scores are in log2 units (the QKV epilogue scales q by log2(e) / 8),
+//    and the QK^T accumulators start at minus the running max, so the
+//    matrix cores return s2 - m directly;
+//  * the key mask is an additive per-key bias, 0 for a valid key and -inf
+//    for a masked or padding key (built once per mask by key_bias_kernel),
+//    added only on the tiles that hold a masked key (a ballot over the
+//    tile's bias words);
 //  * the running max m moves only when a tile's max exceeds it by more than
 //    8: probabilities exp2(s2 - m) then stay <= 2^8, well inside f16, and the
 //    O rescale is skipped for the whole wave in the common case;
@@ -87,7 +91,6 @@ __device__ __forceinline__ void attn_static_for(F&& f) {
 __device__ __forceinline__ int attn_kslot(int r, int c) { return c ^ ((r & 3) | (((r >> 3) & 1) << 2)); }
 __device__ __forceinline__ int attn_vslot(int r, int c) { return c ^ (r & 7); }
 
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;  // log2 headroom before the running max moves
 
 template <int NBUF, int G, int QB, int NQW, bool BRANCH_KEYS, bool QSKIP>
@@ -217,10 +220,18 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
   floatx4 o[4][QB];  // o[db][qb][i] = O[query q0+16qb+lr][d = 16 db + 4 lg + i] (unnormalised)
   floatx4 o5[QB];    // o5[qb][0] in lane group 0: the running denominator of query q0+16qb+lr
   float m_run[QB];   // running max (log2 units), same in a query's 4 lanes
+  // The QK^T accumulators start at -m_use (m_use = m_run, or 0 while no key
+  // of the query is valid yet), so the matrix cores return the scores
+  // already shifted by the running max; thr is how far a shifted score may
+  // rise before the max moves (-inf while m_run is -inf: any valid key moves it).
+  float negm[QB];
+  float thr[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     o5[qb] = floatx4{0.f, 0.f, 0.f, 0.f};
     m_run[qb] = -INFINITY;
+    negm[qb] = 0.0f;
+    thr[qb] = -INFINITY;
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
@@ -233,7 +244,12 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
     const half_t* sk = bufK(st) + grp * TILE;
     const half_t* sv = bufV(st) + grp * TILE;
     const float* sb = bufB(st) + wv * 64;
+    // Whether any key of the tile is masked (one bias word per lane; the
+    // same answer in every lane, so the bias pass below is a uniform branch
+    // that only tiles holding a masked or padding key take).
+    const bool masked = __any(sb[lane] != 0.0f);
     // sc[kb][qb][i] = S[key kt*64 + 32 (kb>>1) + 8 lg + 4 (kb&1) + i][query q0 + 16 qb + lr]
+    //                 - m_use[query]   (log2 units: q carries log2(e) / 8)
     floatx4 sc[4][QB];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -242,43 +258,55 @@ __global__ __launch_bounds__(64 * NQW * G) void attention_kernel(const half_t* _
       const half8 kf1 = *reinterpret_cast<const half8*>(sk + row * 64 + attn_kslot(row, 4 + lg) * 8);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        floatx4 z = {0.f, 0.f, 0.f, 0.f};
-        z = mfma16x16x32(kf0, qf[qb][0], z);
+        const floatx4 z = mfma16x16x32(kf0, qf[qb][0], floatx4{negm[qb], negm[qb], negm[qb], negm[qb]});
         sc[kb][qb] = mfma16x16x32(kf1, qf[qb][1], z);
       }
     }
+    if (masked) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const float4 bb = *reinterpret_cast<const float4*>(sb + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1));
-      const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
+      for (int kb = 0; kb < 4; ++kb) {
+        const float4 bb = *reinterpret_cast<const float4*>(sb + 32 * (kb >> 1) + 8 * lg + 4 * (kb & 1));
+        const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[kb][qb][i] = fmaf(sc[kb][qb][i], kLog2e, bv[i]);
+          for (int i = 0; i < 4; ++i) sc[kb][qb][i] += bv[i];
+      }
     }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      float lmax = fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3]));
+      // NaN-propagating maximum (v_maximum3_f32): no canonicalising pass over
+      // the matrix-core results, three inputs per instruction
+      float lmax = __builtin_elementwise_maximum(sc[0][qb][0], sc[0][qb][1]);
 #pragma unroll
-      for (int kb = 1; kb < 4; ++kb)
-        lmax = fmaxf(lmax, fmaxf(fmaxf(sc[kb][qb][0], sc[kb][qb][1]), fmaxf(sc[kb][qb][2], sc[kb][qb][3])));
-      const float m_old = m_run[qb];
-      if (__any(lmax > m_old + kLazyMax)) {
+      for (int e = 2; e < 16; e += 2)
+        lmax = __builtin_elementwise_maximum(
+            __builtin_elementwise_maximum(lmax, sc[e >> 2][qb][e & 3]), sc[e >> 2][qb][(e & 3) + 1]);
+      if (__any(lmax > thr[qb])) {
         float tmax = fmaxf(lmax, __shfl_xor(lmax, 16, kWave));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-        const bool need = tmax > m_old + kLazyMax;
-        const float m_new = need ? tmax : m_old;
-        const float alpha = __builtin_amdgcn_exp2f(m_old - m_new);  // -inf -> 0; unchanged -> 1
+        const bool need = tmax > thr[qb];
+        const float delta = need ? tmax : 0.0f;  // the max's move, in the shifted frame
+        // o and l are all zero while m_run is -inf: alpha 0 keeps them so
+        // (exp2(-delta) could overflow for a very negative first max)
+        const float alpha = m_run[qb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-delta);
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
         o5[qb] *= alpha;
-        m_run[qb] = m_new;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sc[kb][qb][i] -= delta;
+        if (need) {
+          m_run[qb] = (m_run[qb] == -INFINITY ? 0.0f : m_run[qb]) + tmax;
+          thr[qb] = kLazyMax;
+          negm[qb] = -m_run[qb];
+        }
       }
-      const float m_use = m_run[qb] == -INFINITY ? 0.0f : m_run[qb];  // nothing valid yet
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[kb][qb][i] = __builtin_amdgcn_exp2f(sc[kb][qb][i] - m_use);
+        for (int i = 0; i < 4; ++i) sc[kb][qb][i] = __builtin_amdgcn_exp2f(sc[kb][qb][i]);
     }
     // O^T += V^T . P^T over two 32-key chunks; K-slot j of lane group lg is
     // key 32 c + 8 lg + j in both operands.  The ones block sums P.

@@ -33,7 +33,7 @@ enum EpiMode : int {
   EPI_F16 = 1,        // C16 = acc + bias
   EPI_SWIGLU = 2,     // W rows interleaved [w1 x16 | w3 x16]: C16[m][c] = silu(h1) * h3
   EPI_GATE = 3,       // W rows interleaved [a x16 | b x16]: C16 = tanh(a+ca) * sigmoid(b+cb)
-  EPI_QKV = 4,        // W rows paired for RoPE: write Q (rotated, x1/8), K (rotated), V^T
+  EPI_QKV = 4,        // W rows paired for RoPE: write Q (rotated, x log2(e)/8), K (rotated), V^T
   EPI_RESSKIP = 5,    // WaveNet res/skip update (N = 2*512)
   EPI_FINALSKIP = 6,  // last WaveNet layer (N = 512), plus the res_projection add
   EPI_DUAL = 7,       // cols < N/2 -> C32 (+ f16 copy C16); cols >= N/2 -> C32b

@@ -975,7 +975,10 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
           const int t = m - b * p.T;
           const size_t head = (size_t)b * 8 + hh;
           const float2* cs = p.rope + t * 32 + (d0 >> 1);
-          const float sc = sec == 0 ? 0.125f : 1.0f;  // 1/sqrt(64): a power of two, exact
+          // q carries the softmax scale in log2 units, log2(e) / sqrt(64), so the
+          // attention's scores come out of the matrix cores ready for exp2
+          // (one rounding to f16 either way)
+          const float sc = sec == 0 ? 0.125f * 1.4426950408889634f : 1.0f;
           half8 h;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
