@@ -133,7 +133,8 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   static_assert(CPR == 8 || CPR >= 16, "stage width");
   static_assert(KG == 1 || ((KG == 2 || KG == 4) && EPI != EPI_QKV),
                 "K groups: 2 or 4, and the QKV epilogue needs every wave");
-  static_assert(!PIPE || (SP == 0 && (KG == 1 || KG == 2)), "pipelined loop: f16 operands, K in 1 or 2 parts");
+  static_assert(!PIPE || ((KG == 1 || KG == 2) && (SP == 0 || KG == 1)),
+                "pipelined loop: K in 1 or 2 parts; split operands with one part");
   static_assert(EPI != EPI_QKV || 512 % BN == 0, "a qkv tile must lie inside one of the q, k, v sections");
   static_assert(SP >= 0 && SP <= 2, "split mode");
 
@@ -540,6 +541,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
 #pragma unroll
       for (int j = 0; j < NI; ++j) acc1[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     half8 fa[2][MI], fb[2][NI];
+    half8 fal[SP >= 1 ? 2 : 1][SP >= 1 ? MI : 1], fbl[SP == 2 ? 2 : 1][SP == 2 ? NI : 1];  // split: lo halves
     auto frag_read = [&](auto st, auto kkc, auto slot) {
       constexpr int kk = decltype(kkc)::value;
       constexpr int sl = decltype(slot)::value;
@@ -549,14 +551,40 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
       for (int i = 0; i < MI; ++i) fa[sl][i] = *reinterpret_cast<const half8*>(sa + a_lane[kk] + i * 16 * SK);
 #pragma unroll
       for (int j = 0; j < NI; ++j) fb[sl][j] = *reinterpret_cast<const half8*>(sb + b_lane[kk] + j * 16 * SK);
+      if constexpr (SP >= 1) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          fal[sl][i] = *reinterpret_cast<const half8*>(sa + kALo + a_lane[kk] + i * 16 * SK);
+      }
+      if constexpr (SP == 2) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+          fbl[sl][j] = *reinterpret_cast<const half8*>(sb + kWLo + b_lane[kk] + j * 16 * SK);
+      }
     };
+    // Per K step the same MFMAs in the same order as compute() above: the
+    // hi.hi products into c, then (split operands) the cross terms into accx.
     auto mma = [&](floatx4 (&c)[MI][NI], auto slot) {
       constexpr int sl = decltype(slot)::value;
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j) c[i][j] = mfma16x16x32(fb[sl][j], fa[sl][i], c[i][j]);
+      if constexpr (SP >= 1) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) accx[i][j] = mfma16x16x32(fb[sl][j], fal[sl][i], accx[i][j]);
+      }
+      if constexpr (SP == 2) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) accx[i][j] = mfma16x16x32(fbl[sl][j], fa[sl][i], accx[i][j]);
+      }
     };
+    constexpr int kFragReads = MI + NI + (SP >= 1 ? MI : 0) + (SP == 2 ? NI : 0);
+    constexpr int kMfmas = MI * NI * (1 + SP);
     // Every ring buffer is filled before the loop: stage kt's buffer is
     // refilled at stage kt's barrier.
     static_for<0, NST>([&](auto st) { issue(st, (int)decltype(st)::value); });
@@ -578,7 +606,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
         if constexpr (kk + 1 < KK) {
           frag_read(st, std::integral_constant<int, kk + 1>{}, Nxt{});
           mma(c, std::integral_constant<int, cur>{});
-          interleave<MI + NI, 0, MI * NI>();
+          interleave<kFragReads, 0, kMfmas>();
         } else {
           wait_lgkmcnt0();               // this wave's reads of stage kt have returned
           wait_vmcnt<L * (NST - 2)>();   // its share of stage kt+1 has landed
@@ -586,7 +614,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
           issue(st, kt + NST);
           frag_read(std::integral_constant<int, (s + 1) % NST>{}, std::integral_constant<int, 0>{}, Nxt{});
           mma(c, std::integral_constant<int, cur>{});
-          interleave<MI + NI, L, MI * NI>();
+          interleave<kFragReads, L, kMfmas>();
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the K steps in program order
       });
@@ -1071,22 +1099,6 @@ static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Split-operand launches (fp32-level products, GemmArgs::split): the
-// vocoder's convs keep the f16 tile choice (their rings double, still one
-// or two workgroups per CU); everything else runs 64 x 64 tiles with one K
-// group, so the doubled ring stays within the LDS.
-template <int AM, int EPI, int SP>
-static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
-  if constexpr (AM == A_CONVP) {
-    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 1, SP>(a, s);
-    if (a.N % 64 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
-    if (a.N % 32 == 0) return launch_tile<64, 32, 64, 3, AM, EPI, 4, 1, 1, SP>(a, s);
-    return hipErrorInvalidValue;
-  } else {
-    return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
-  }
-}
-
 // Tile, stage and wavefront choice, swept at M = 1720 (B = 2, T = 860) on
 // MI355X.  Two limits decide it: the L2 -> CU path delivers about 48 B/clk
 // per CU whatever the load method or depth, so a K loop's time is its total
@@ -1159,6 +1171,45 @@ static double pipe_cost(long tiles, int BM, int BN, double rate) {
 template <int KG, int NST>
 static bool pipe_fits(const GemmArgs& a) {
   return a.K % (64 * KG * NST) == 0;  // each K part a whole number of rounds of the ring
+}
+
+// Split-operand launches (fp32-level products, GemmArgs::split): everything
+// but the vocoder runs 64 x 64 tiles with one K group, so the doubled ring
+// stays within the LDS.  The vocoder's convs (A split, weight-normed v exact
+// in f16: SP = 1) take the pipelined loop once a stage's row tiles fill most
+// of the chip, else the f16 tile choice (their rings double, still one or
+// two workgroups per CU).  Swept at the 860-frame call (every candidate
+// bit-equal to the 64 x 128 tile; us per launch, first conv of each pair
+// at dilation 1 / 3 / 5 and the second at 1 alike):
+//  * M = 3,440, N = 768 (after the first upsampler): 128 x 128, 3-stage
+//    ring: k = 3 / 7 / 11 at 43.3-44.4 / 88.5-90.0 / 131.6-135.2 against
+//    52.3 / 109.2-110.0 / 165.5-170.2 (192 x 128 tiles are too few there);
+//  * M = 13,760, N = 384: 192 x 128 with a 2-stage ring at k = 3 / 7 (one
+//    round of 216 tiles against 1.27 rounds of 128 x 128): 39.5-40.1 /
+//    73.4-74.9 against 47.4 / 92.0-92.1; at k = 11 (K = 4224) the 2-stage
+//    ring falls behind (199-201) and 128 x 128 with three stages wins:
+//    137.6-142.7 against 169.7-172.6.
+// The transposed convs (SP = 2) and the narrower stages found nothing faster.
+template <int AM, int EPI, int SP>
+static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
+  if constexpr (AM == A_CONVP) {
+    if constexpr (SP == 1) {
+      if (a.N % 128 == 0 && a.row_nb == 0) {
+        const long t128 = tile_count(a, 128, 128), t192 = tile_count(a, 192, 128);
+        const long r128 = (t128 + 255) / 256, r192 = (t192 + 255) / 256;
+        const int stages = a.K / 64;
+        if (t192 >= 128 && r192 < r128 && a.K <= 2688 && stages % 2 == 0)
+          return launch_tile<192, 128, 64, 2, AM, EPI, 4, 2, 1, SP, 1>(a, s);
+        if (t128 >= 128 && stages % 3 == 0) return launch_tile<128, 128, 64, 3, AM, EPI, 4, 2, 1, SP, 1>(a, s);
+      }
+    }
+    if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 1, SP>(a, s);
+    if (a.N % 64 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
+    if (a.N % 32 == 0) return launch_tile<64, 32, 64, 3, AM, EPI, 4, 1, 1, SP>(a, s);
+    return hipErrorInvalidValue;
+  } else {
+    return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
+  }
 }
 
 template <int AM, int EPI>
