@@ -1188,8 +1188,14 @@ static bool pipe_fits(const GemmArgs& a) {
 //    round of 216 tiles against 1.27 rounds of 128 x 128): 39.5-40.1 /
 //    73.4-74.9 against 47.4 / 92.0-92.1; at k = 11 (K = 4224) the 2-stage
 //    ring falls behind (199-201) and 128 x 128 with three stages wins:
-//    137.6-142.7 against 169.7-172.6.
-// The transposed convs (SP = 2) and the narrower stages found nothing faster.
+//    137.6-142.7 against 169.7-172.6;
+//  * M = 27,520, N = 192: 64 x 192 (4 x 2 wavefronts of 16 x 96), 3-stage
+//    ring: k = 3 / 7 / 11 at 29.3 / 45.5 / 62.0 against 36.0 / 62.8-63.4 /
+//    90.9-91.0;
+//  * M = 55,040, N = 96 (K = 320 / 704 / 1088: a prime number of stages, so
+//    the plain loop): 64 x 96 tiles of 4 x 1 wavefronts, 30.4 / 46.7 / 63.8
+//    against 31.4 / 51.7 / 72.6 with 64 x 32.
+// The transposed convs (SP = 2) found nothing faster.
 template <int AM, int EPI, int SP>
 static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
   if constexpr (AM == A_CONVP) {
@@ -1202,6 +1208,9 @@ static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
           return launch_tile<192, 128, 64, 2, AM, EPI, 4, 2, 1, SP, 1>(a, s);
         if (t128 >= 128 && stages % 3 == 0) return launch_tile<128, 128, 64, 3, AM, EPI, 4, 2, 1, SP, 1>(a, s);
       }
+      if (a.N == 192 && a.row_nb == 0 && tile_count(a, 64, 192) >= 128 && (a.K / 64) % 3 == 0)
+        return launch_tile<64, 192, 64, 3, AM, EPI, 4, 2, 1, SP, 1>(a, s);
+      if (a.N == 96) return launch_tile<64, 96, 64, 3, AM, EPI, 4, 1, 1, SP>(a, s);
     }
     if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 1, SP>(a, s);
     if (a.N % 64 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
