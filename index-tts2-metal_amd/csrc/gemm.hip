@@ -1193,8 +1193,10 @@ static bool pipe_fits(const GemmArgs& a) {
 //    ring: k = 3 / 7 / 11 at 29.3 / 45.5 / 62.0 against 36.0 / 62.8-63.4 /
 //    90.9-91.0;
 //  * M = 55,040, N = 96 (K = 320 / 704 / 1088: a prime number of stages, so
-//    the plain loop): 64 x 96 tiles of 4 x 1 wavefronts, 30.4 / 46.7 / 63.8
-//    against 31.4 / 51.7 / 72.6 with 64 x 32.
+//    the plain loop): 128 x 96 tiles of 4 x 1 wavefronts, k = 3 / 11 at
+//    27.4 / 57.5 against 30.2-30.4 / 63.5-63.8 for 64 x 96 and 31.4 / 72.6
+//    for 64 x 32 (64 x 96 below 256 tiles).  128- and 256-row tiles lose at
+//    the 48- and 24-channel stages (one workgroup per CU).
 // The transposed convs (SP = 2) found nothing faster.
 template <int AM, int EPI, int SP>
 static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
@@ -1210,7 +1212,10 @@ static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
       }
       if (a.N == 192 && a.row_nb == 0 && tile_count(a, 64, 192) >= 128 && (a.K / 64) % 3 == 0)
         return launch_tile<64, 192, 64, 3, AM, EPI, 4, 2, 1, SP, 1>(a, s);
-      if (a.N == 96) return launch_tile<64, 96, 64, 3, AM, EPI, 4, 1, 1, SP>(a, s);
+      if (a.N == 96) {
+        if (tile_count(a, 128, 96) >= 256) return launch_tile<128, 96, 64, 3, AM, EPI, 4, 1, 1, SP>(a, s);
+        return launch_tile<64, 96, 64, 3, AM, EPI, 4, 1, 1, SP>(a, s);
+      }
     }
     if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4, 1, SP>(a, s);
     if (a.N % 64 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2, 1, SP>(a, s);
