@@ -105,6 +105,24 @@ def test_resblock(orc, ctx_bv, bv, index, tokens):
     assert err <= BLOCK_TOL
 
 
+# Lengths at which the fp32-level convs take the pipelined and the wider
+# tiles (the 860-frame call's stages run at 3,440 / 13,760 / 27,520 / 55,040
+# rows): 128 x 128 (768 channels at 2,816 rows; 384 at 6,000), 192 x 128 with
+# a 2-stage ring (384 channels at 13,760 rows, k = 3), 64 x 192 (192 channels
+# at 8,192 rows) and 128 x 96 (96 channels at 32,768 rows).
+@pytest.mark.parametrize("index,tokens", [(0, 2816), (3, 6000), (3, 13760), (6, 8192), (9, 32768)])
+def test_resblock_long(orc, ctx_bv, bv, index, tokens):
+    C = 768 >> (index // 3)
+    k = (3, 7, 11)[index % 3]
+    x = _x(tokens, C, 400 + index)
+    print(f"resblock {index} T={tokens} C={C} k={k}", flush=True)
+    got = ctx_bv.bigvgan_stage("resblock", index, x)
+    ref = bv.resblock(f"bigvgan.resblocks.{index}", x, k)
+    err = orc.rel_l2(got, ref)
+    print(f"  rel-L2 {err:.3e}", flush=True)
+    assert err <= BLOCK_TOL
+
+
 @pytest.mark.parametrize("index,tokens", [(0, 16), (3, 128), (5, 600)])
 def test_resblock_group(orc, ctx_bv, bv, index, tokens):
     C = 768 >> index
