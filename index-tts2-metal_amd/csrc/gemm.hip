@@ -106,6 +106,17 @@ __device__ inline float2 rope_rotate(float x, float y, float2 cs) {
   return make_float2(__builtin_fmaf(x, cs.x, -(y * cs.y)), __builtin_fmaf(y, cs.x, x * cs.y));
 }
 
+// f16 of v as computed in fp32.  The empty asm statement keeps v a register
+// value, so the conversion is never merged with v's producing multiply or
+// fused multiply-add into one mixed-precision instruction (v_fma_mix, which
+// rounds once, straight to f16).  The compiler made that choice differently
+// in different kernels, so a row's q and V bits depended on the kernel that
+// computed them; with this every QKV kernel rounds twice, alike.
+__device__ inline half_t f16_of(float v) {
+  __asm__ volatile("" : "+v"(v));
+  return (half_t)v;
+}
+
 template <int BM, int BN, int SK, int NST, int AM, int EPI, int WM, int WN, int KG, int SP, int PIPE>
 __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(GemmArgs p, TileMap tmap) {
   // K split.  The product over K is summed in KG parts of equal length, added
@@ -934,8 +945,8 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
             for (int r = 0; r < 4; ++r) {
               const int rl = wm * WTM + i * 16 + lr;
               const int c = 32 * g + 2 * (4 * lg + r);
-              stg(c)[rl] = (half_t)__builtin_fmaf(rsv[i], acc[i][2 * q][r], bev[r]);
-              stg(c + 1)[rl] = (half_t)__builtin_fmaf(rsv[i], acc[i][2 * q + 1][r], bov[r]);
+              stg(c)[rl] = f16_of(__builtin_fmaf(rsv[i], acc[i][2 * q][r], bev[r]));
+              stg(c + 1)[rl] = f16_of(__builtin_fmaf(rsv[i], acc[i][2 * q + 1][r], bov[r]));
             }
         }
         wait_lgkmcnt0();  // this wave's stores have landed before the barrier releases readers
@@ -1011,8 +1022,8 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float2 rot = rope_rotate(ve[r], vo[r], cs[r]);
-            h[2 * r] = (half_t)(rot.x * sc);
-            h[2 * r + 1] = (half_t)(rot.y * sc);
+            h[2 * r] = f16_of(rot.x * sc);
+            h[2 * r + 1] = f16_of(rot.y * sc);
           }
           half_t* dst = (sec == 0 ? p.q : p.k) + (head * p.Tpad + t) * 64 + d0;
           *reinterpret_cast<half8*>(dst) = h;
@@ -1020,6 +1031,243 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
       }
     }
   }
+}
+
+// QKV product of long sequences (K = 512, N = 1536) with the row block kept
+// resident.  A persistent grid of kQkvRowsGrid workgroups; workgroup r takes
+// a contiguous range of the work items (row block, 128-column tile), ordered
+// row block first, so it loads each 64 x 512 A block into LDS once and then
+// streams only W's 128-row column tiles through a 4-stage ring that runs on
+// from one item to the next (no per-tile fill or drain).  Eight wavefronts of
+// 32 x 32.  The MFMAs run in the same K order as gemm_kernel's and the
+// epilogue is its QKV epilogue (rs, bias, RoPE, the q scale, f16_of), so
+// every output has the same bits as with the 64 x 64 / 64 x 128 tiles.  The
+// row blocks are tm's computed row tiles (row skipping included); the
+// workgroups of one XCD take neighbouring ranges.
+constexpr int kQkvRowsGrid = 256;
+
+__global__ __launch_bounds__(512) void qkv_rows_kernel(GemmArgs p, TileMap tm) {
+  constexpr int BM = 64, BN = 128, K = 512, SK = 64, KT = K / SK, WN = 4, NW = 8, NSTW = 4;
+  constexpr int WTM = 32, WTN = 32, MI = 2, NI = 2;
+  constexpr int LAB = BM * (K / 8) / (64 * NW);  // 16-byte A loads per lane per row block
+  constexpr int LB = BN * (SK / 8) / (64 * NW);  // 16-byte W loads per lane per stage
+  constexpr int nN = 1536 / BN;
+  __shared__ __attribute__((aligned(1024))) half_t sA[BM * K];
+  __shared__ __attribute__((aligned(1024))) half_t sW0[BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sW1[BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sW2[BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sW3[BN * SK];
+  __shared__ __attribute__((aligned(1024))) half_t sV[BN * BM];  // V^T staging [channel][row]
+  auto bufW = [&](auto st) -> half_t* {
+    constexpr int s = decltype(st)::value;
+    if constexpr (s == 0) return sW0;
+    else if constexpr (s == 1) return sW1;
+    else if constexpr (s == 2) return sW2;
+    else return sW3;
+  };
+  const int items = tm.nM * nN;
+  const int bid = blockIdx.x;
+  const int r8 = (bid & 7) * (kQkvRowsGrid / 8) + (bid >> 3);
+  const int i0 = (int)((long)r8 * items / kQkvRowsGrid), i1 = (int)((long)(r8 + 1) * items / kQkvRowsGrid);
+  if (i0 >= i1) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave - wm * WN;
+  const int lr = lane & 15, lg = lane >> 4;
+  const buffer_rsrc_t rA = make_buffer_rsrc(p.A, (int)((size_t)p.M * p.lda * 2));
+  const buffer_rsrc_t rW = make_buffer_rsrc(p.W, (int)((size_t)p.N * p.ldw * 2));
+  // W stage rows hold 8 slots, slot of chunk c at c ^ ((row >> 1) & 7); A
+  // rows hold 64, chunk c at c ^ (row & 15) (16 consecutive rows read at one
+  // chunk hit distinct banks either way).
+  int voW[LB];
+#pragma unroll
+  for (int j = 0; j < LB; ++j) {
+    const int q = (wave * LB + j) * 64 + lane;
+    const int row = q >> 3;
+    voW[j] = (row * p.ldw + (((q & 7) ^ ((row >> 1) & 7)) * 8)) * 2;
+  }
+  // A fragment offsets: K stage kt reads chunk 8 kt + 4 kk + lg of row
+  // wm*32 + 16 i + lr, at slot (8 kt + 4 kk + lg) ^ lr = 8 (kt ^ (lr >> 3)) +
+  // ((4 kk + lg) ^ (lr & 7)); the kt-parity part is a_off[kt & 1].
+  const int h8 = lr >> 3;
+  int a_off[2][2];
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      a_off[pp][kk] = (wm * WTM + lr) * K + ((pp ^ h8) * 64) + (((kk * 4 + lg) ^ (lr & 7)) * 8);
+  int b_off[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) b_off[kk] = (wn * WTN + lr) * SK + (((kk * 4 + lg) ^ ((lr >> 1) & 7)) * 8);
+  __asm__("" : "+v"(a_off[0][0]), "+v"(a_off[0][1]), "+v"(a_off[1][0]), "+v"(a_off[1][1]), "+v"(b_off[0]),
+          "+v"(b_off[1]));
+  // head dims d0 .. d0 + 7 of this lane's q / k outputs (the same in every column tile)
+  const int d0 = (wn * WTN + 8 * lg) & 63;
+  float rsv[MI];
+  float2 csv[MI][4];
+  auto row_block = [&](int rc) {  // computed row tile -> row tile
+    int first = tm.seg_first[0], cum = 0;
+    if (tm.nseg == 0) return rc;
+#pragma unroll
+    for (int s = 1; s < kMaxRowSeq; ++s) {
+      if (s < tm.nseg && rc >= tm.seg_cum[s]) {
+        first = tm.seg_first[s];
+        cum = tm.seg_cum[s];
+      }
+    }
+    return first + (rc - cum);
+  };
+  // A block, rs and the rotary (cos, sin) of this lane's rows
+  auto load_rows = [&](int rb) {
+#pragma unroll
+    for (int j = 0; j < LAB; ++j) {
+      const int q = (wave * LAB + j) * 64 + lane;
+      const int row = q >> 6;
+      const int c = (q & 63) ^ (row & 15);
+      const int m = min(rb * BM + row, p.M - 1);
+      buffer_load_lds16(rA, (lds_ptr_t*)(sA + (wave * LAB + j) * 64 * 8), (m * p.lda + c * 8) * 2, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = rb * BM + wm * WTM + 16 * i + lr;
+      float4 sp[kSsqParts / 4];
+#pragma unroll
+      for (int u = 0; u < kSsqParts / 4; ++u)
+        sp[u] = (p.ssq_in && m < p.M) ? reinterpret_cast<const float4*>(p.ssq_in + (size_t)m * kSsqParts)[u]
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      float ss = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kSsqParts / 4; ++u) ss += (sp[u].x + sp[u].y) + (sp[u].z + sp[u].w);
+      rsv[i] = p.ssq_in ? 1.0f / sqrtf(ss / 512.0f + 1e-5f) : 1.0f;
+      const int mc = min(m, p.M - 1);
+      const int t = mc - (mc / p.T) * p.T;
+      const float2* cs = p.rope + t * 32 + (d0 >> 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) csv[i][r] = cs[r];
+    }
+  };
+  // W stage kt of item's column tile into ring buffer st; past the range's
+  // last item it re-reads that item's last stage (never used).
+  auto issue = [&](auto st, int item, int kt) {
+    if (item >= i1) {
+      item = i1 - 1;
+      kt = KT - 1;
+    }
+    const int cb = item % nN;
+    half_t* sw = bufW(st);
+#pragma unroll
+    for (int j = 0; j < LB; ++j)
+      buffer_load_lds16(rW, (lds_ptr_t*)(sw + (wave * LB + j) * 64 * 8), voW[j], (cb * BN * p.ldw + kt * SK) * 2);
+  };
+  floatx4 acc[MI][NI];
+  int item = i0;
+  int rc = item / nN;
+  int rb = row_block(rc);
+  load_rows(rb);
+  static_for<0, NSTW - 1>([&](auto st) { issue(st, item, (int)decltype(st)::value); });
+  while (true) {
+    const int n0 = (item % nN) * BN;
+    float4 bv[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + n0 + wn * WTN + 16 * j + 4 * lg)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    static_for<0, KT>([&](auto ktc) {
+      constexpr int kt = decltype(ktc)::value;
+      // stage kt has landed (vector memory operations complete in issue
+      // order; at most NSTW - 2 stages stay in flight behind it)
+      wait_vmcnt<LB * (NSTW - 2)>();
+      wait_lgkmcnt0();
+      __builtin_amdgcn_s_barrier();
+      {
+        // the buffer of stage kt - 1, free now that every wave is past it
+        constexpr int kn = kt + NSTW - 1;
+        issue(std::integral_constant<int, kn % NSTW>{}, kn < KT ? item : item + 1, kn < KT ? kn : kn - KT);
+      }
+      const half_t* sw = bufW(std::integral_constant<int, kt % NSTW>{});
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        half8 af[MI], bf[NI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          af[i] = *reinterpret_cast<const half8*>(sA + a_off[kt & 1][kk] + (kt - (kt & 1)) * 64 + i * 16 * K);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) bf[j] = *reinterpret_cast<const half8*>(sw + b_off[kk] + j * 16 * SK);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
+      }
+    });
+    const int m0 = rb * BM;
+    const float be[4] = {bv[0].x, bv[0].y, bv[0].z, bv[0].w};
+    const float bo[4] = {bv[1].x, bv[1].y, bv[1].z, bv[1].w};
+    if (n0 >= 1024) {
+      // V: stage [128 channels][64 rows]; then consecutive lanes write consecutive t of V^T
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rl = wm * WTM + i * 16 + lr;
+          const int c = 32 * wn + 2 * (4 * lg + r);
+          sV[c * BM + rl] = f16_of(__builtin_fmaf(rsv[i], acc[i][0][r], be[r]));
+          sV[(c + 1) * BM + rl] = f16_of(__builtin_fmaf(rsv[i], acc[i][1][r], bo[r]));
+        }
+      wait_lgkmcnt0();
+      __builtin_amdgcn_s_barrier();
+      const int h0 = (n0 - 1024) >> 6;
+      const int m = m0 + lane;
+      if (m < p.M) {
+        const int b = m / p.T;
+        const int t = m - b * p.T;
+        for (int c = wave; c < BN; c += NW)
+          p.vt[(((size_t)b * 8 + h0 + (c >> 6)) * 64 + (c & 63)) * p.Tpad + t] = sV[c * BM + lane];
+      }
+    } else {
+      const int o = n0 + wn * WTN + 8 * lg;  // original column of the first even element
+      const int sec = o >> 9;                 // 0 = q, 1 = k
+      const int hh = (o & 511) >> 6;
+      const float sc = sec == 0 ? 0.125f * 1.4426950408889634f : 1.0f;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = m0 + wm * WTM + 16 * i + lr;
+        if (m >= p.M) continue;
+        const float ve[4] = {__builtin_fmaf(rsv[i], acc[i][0][0], be[0]), __builtin_fmaf(rsv[i], acc[i][0][1], be[1]),
+                             __builtin_fmaf(rsv[i], acc[i][0][2], be[2]), __builtin_fmaf(rsv[i], acc[i][0][3], be[3])};
+        const float vo[4] = {__builtin_fmaf(rsv[i], acc[i][1][0], bo[0]), __builtin_fmaf(rsv[i], acc[i][1][1], bo[1]),
+                             __builtin_fmaf(rsv[i], acc[i][1][2], bo[2]), __builtin_fmaf(rsv[i], acc[i][1][3], bo[3])};
+        const int b = m / p.T;
+        const int t = m - b * p.T;
+        const size_t head = (size_t)b * 8 + hh;
+        half8 h;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float2 rot = rope_rotate(ve[r], vo[r], csv[i][r]);
+          h[2 * r] = f16_of(rot.x * sc);
+          h[2 * r + 1] = f16_of(rot.y * sc);
+        }
+        half_t* dst = (sec == 0 ? p.q : p.k) + (head * p.Tpad + t) * 64 + d0;
+        *reinterpret_cast<half8*>(dst) = h;
+      }
+    }
+    ++item;
+    if (item >= i1) break;
+    if (item / nN != rc) {
+      // next row block: every wave is done with sA (and sV) before it is refilled
+      wait_lgkmcnt0();
+      __builtin_amdgcn_s_barrier();
+      rc = item / nN;
+      rb = row_block(rc);
+      load_rows(rb);
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+    }
+  }
+  wait_vmcnt<0>();  // the range's trailing stage loads have landed before the LDS is released
 }
 
 // Chooses the XCD rectangle split minimising the bytes the XCDs re-read:
@@ -1261,9 +1509,15 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
     }
   }
   if constexpr (EPI == EPI_QKV) {
-    // Long sequences (both CFG branches of T = 10784: 76.5 vs 86.0 us; equal
-    // at T = 3000, slower at T = 860); the same bits as the 64 x 64 tile.
-    if (tile_count(a, 64, 128) >= 1024) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 2>(a, s);
+    // Long sequences: the row-resident loop once there are four or more
+    // items per workgroup (M = 21,568: 61.1-64.1 vs 74.2-77.1 us for 64 x 128
+    // tiles, 84.8 for 64 x 64; M = 6,000: 22.8 vs 24.4; slower at M = 2,000,
+    // 11.4 vs 10.4).  The same bits as the 64 x 64 tile.
+    if (AM == A_PLAIN && a.K == 512 && a.N == 1536 && tile_count(a, 64, 128) >= 1024) {
+      const TileMap tm = make_tile_map(a, a.M, a.N, a.K, a.K, 64, 128);
+      hipLaunchKernelGGL(qkv_rows_kernel, dim3(kQkvRowsGrid), dim3(512), 0, s, a, tm);
+      return hipGetLastError();
+    }
   }
   if constexpr (EPI == EPI_RESSKIP || EPI == EPI_DUAL) {
     if (a.N % 128 == 0) {
