@@ -161,9 +161,10 @@ inline void split_f16_host(float v, half_t& hi, half_t& lo) {
 // value: otherwise FP contraction may rewrite the conversion feeding lo as
 // a fused mixed-precision FMA from v's unrounded producer (v_fma_mix) while
 // hi is converted from the rounded v, and the pair then misses v by one f16
-// ulp whenever the two roundings disagree.
+// ulp whenever the two roundings disagree.  (Not volatile, so the statement
+// does not also fix the position of the loads around it.)
 __device__ inline void split_f16(float v, half_t& hi, half_t& lo) {
-  __asm__ volatile("" : "+v"(v));
+  __asm__("" : "+v"(v));
   hi = (half_t)v;
   lo = (half_t)((v - (float)hi) * kSplitScale);
 }

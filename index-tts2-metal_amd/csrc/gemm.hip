@@ -111,9 +111,11 @@ __device__ inline float2 rope_rotate(float x, float y, float2 cs) {
 // fused multiply-add into one mixed-precision instruction (v_fma_mix, which
 // rounds once, straight to f16).  The compiler made that choice differently
 // in different kernels, so a row's q and V bits depended on the kernel that
-// computed them; with this every QKV kernel rounds twice, alike.
+// computed them; with this every QKV kernel rounds twice, alike.  (Not
+// volatile: a volatile statement also pinned the epilogue's RoPE loads in
+// place, one dependent load at a time.)
 __device__ inline half_t f16_of(float v) {
-  __asm__ volatile("" : "+v"(v));
+  __asm__("" : "+v"(v));
   return (half_t)v;
 }
 

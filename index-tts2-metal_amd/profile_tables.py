@@ -153,7 +153,8 @@ def find_decodes(rows: list[dict]):
             for k, op in enumerate(STEP_ORDER):
                 name = seg[4 + s * 86 + k]["Kernel_Name"]
                 want = KERNEL_OF.get(op, "gemm_kernel")
-                ok = ok and want in name
+                # long sequences run the QKV product in its row-resident kernel
+                ok = ok and (want in name or (op == "qkv" and "qkv_rows_kernel" in name))
         if ok:
             out.append((B, T, S, seg))
     return out
