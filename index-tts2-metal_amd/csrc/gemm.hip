@@ -225,15 +225,88 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   const bool perm = EPI == EPI_F32 && p.colperm;
   auto colj = [&](int j) { return perm ? col_base + 32 * (j >> 1) + 4 * lg + 4 * (j & 1) : col_base + 16 * j; };
 
+  // Per-column epilogue operands: bias, column scale, and the folded-norm
+  // producer's aw and gamma (multiplied where they are used, so no wait
+  // follows the loads).  They are requested after the K loop's last wait,
+  // so their latency overlaps the resident tail stages' compute and they
+  // hold no registers through the loop.
+  float4 bv[NI];
+  constexpr bool kColScale = EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_RESAVG;
+  float4 csv[kColScale ? NI : 1];
+  constexpr bool kNormOut = EPI == EPI_F32;
+  float4 nsa[kNormOut ? NI : 1], nsg[kNormOut ? NI : 1];
+  auto load_epi = [&]() {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (kColScale) {
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+        csv[j] = p.colscale ? *reinterpret_cast<const float4*>(p.colscale + colj(j))
+                            : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+    if constexpr (kNormOut) {
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        nsa[j] = p.C16s ? *reinterpret_cast<const float4*>(p.sc_a + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+        nsg[j] = p.C16s ? *reinterpret_cast<const float4*>(p.sc_g + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+
   // Epilogue operands that do not depend on the product are fetched before
   // the K loop, so their latency hides behind it (PIPE = 1: after the loop,
   // so they do not hold registers beside its larger tiles).
   constexpr bool kPreA =
       EPI == EPI_F32 || EPI == EPI_RESSKIP || EPI == EPI_FINALSKIP || EPI == EPI_RESAVG;
   constexpr bool kPreB = EPI == EPI_FINALSKIP;
+  // The WaveNet epilogues' row mask (one word per row) and the gate's
+  // global conditioning (one float4 pair per column group) as well: fetched
+  // in the epilogue, each load's wait also drained the stores before it.
+  // The WaveNet epilogues' loads are unconditional (rows past M read row
+  // M - 1, which no epilogue uses; the skip accumulator is read even when it
+  // starts at zero, and the epilogue drops it): a load under a per-lane
+  // branch made the compiler wait for it where the branches join, ahead of
+  // the first K stages.
+  constexpr bool kPreMask = EPI == EPI_RESSKIP || EPI == EPI_FINALSKIP;
+  constexpr bool kPreCond = EPI == EPI_GATE;
+  constexpr bool kPre = kPreA || kPreCond;
   float4 pre_a[kPreA ? MI : 1][kPreA ? NI : 1];
   float4 pre_b[kPreB ? MI : 1][kPreB ? NI : 1];
+  uint32_t pre_mask[kPreMask ? MI : 1];
+  float4 pre_ca[kPreCond ? NI / 2 : 1], pre_cb[kPreCond ? NI / 2 : 1];
   auto load_pre = [&]() {
+    if constexpr (kPreMask) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int mc = min(row_base + 16 * i, p.M - 1);
+        pre_mask[i] = p.mask[mc];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int n = colj(j);
+          if constexpr (EPI == EPI_RESSKIP) {
+            // a tile lies wholly below or above column 512 (BN divides 512)
+            const float* src = n < 512 ? p.C32 + (size_t)mc * p.ldc32 + n
+                                       : p.C32b + (size_t)mc * p.ldc32b + (n - 512);
+            pre_a[i][j] = *reinterpret_cast<const float4*>(src);
+          } else {
+            pre_a[i][j] = *reinterpret_cast<const float4*>(p.C32b + (size_t)mc * p.ldc32b + n);
+            pre_b[i][j] = *reinterpret_cast<const float4*>(p.rp + (size_t)mc * 512 + n);
+          }
+        }
+      }
+      return;
+    }
+    if constexpr (kPreCond) {
+      // channel block of the pair (2 q, 2 q + 1): c = 16 group + 4 lg, as in the epilogue
+#pragma unroll
+      for (int q = 0; q < NI / 2; ++q) {
+        const int c = ((col_base + q * 32 - 4 * lg) >> 5) * 16 + 4 * lg;
+        pre_ca[q] = *reinterpret_cast<const float4*>(p.cond + c);
+        pre_cb[q] = *reinterpret_cast<const float4*>(p.cond + 512 + c);
+      }
+    }
+    if constexpr (!kPreA) return;
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int m = row_base + 16 * i;
@@ -244,22 +317,13 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
         if (m < p.M && kg == 0 && (p.n_store == 0 || n < p.n_store)) {
           if constexpr (EPI == EPI_F32 || EPI == EPI_RESAVG) {
             if (p.res) v = *reinterpret_cast<const float4*>(p.res + (size_t)m * p.ldres + n);
-          } else if constexpr (EPI == EPI_RESSKIP) {
-            if (n < 512) v = *reinterpret_cast<const float4*>(p.C32 + (size_t)m * p.ldc32 + n);
-            else if (p.flag) v = *reinterpret_cast<const float4*>(p.C32b + (size_t)m * p.ldc32b + (n - 512));
-          } else {
-            v = *reinterpret_cast<const float4*>(p.C32b + (size_t)m * p.ldc32b + n);
           }
         }
         pre_a[i][j] = v;
-        if constexpr (kPreB) {
-          pre_b[i][j] = m < p.M && kg == 0 ? *reinterpret_cast<const float4*>(p.rp + (size_t)m * 512 + n)
-                                           : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
       }
     }
   };
-  if constexpr (kPreA && !PIPE) load_pre();
+  if constexpr (kPre && !PIPE) load_pre();
 
   // Consumer side of a folded AdaRMSNorm: the producer's kSsqParts partial
   // sums of squares of each of this lane's rows (K = 512 values) are fetched
@@ -639,7 +703,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
       for (; kt0 < KT; kt0 += NST)
         static_for<0, NST>([&](auto st) { stage(st, kt0 + (int)decltype(st)::value, acc1); });
     }
-    if constexpr (kPreA) load_pre();
+    if constexpr (kPre) load_pre();
   }
   // Pipeline, one barrier per stage.  At the top of stage kt this wave waits
   // for its own share of stage kt (NST-2 younger stages may stay in flight);
@@ -663,37 +727,15 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
       });
     }
   }
-  // Late prefetch: the small per-column epilogue operands are requested
-  // before the resident tail stages are computed, so their latency overlaps
-  // that compute without holding registers through the K loop.
-  float4 bv[NI];
-#pragma unroll
-  for (int j = 0; j < NI; ++j)
-    bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
-  constexpr bool kColScale = EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_RESAVG;
-  float4 csv[kColScale ? NI : 1];
-  if constexpr (kColScale) {
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-      csv[j] = p.colscale ? *reinterpret_cast<const float4*>(p.colscale + colj(j))
-                          : make_float4(1.f, 1.f, 1.f, 1.f);
-  }
-  constexpr bool kNormOut = EPI == EPI_F32;
+  wait_vmcnt<0>();  // the tail stages have landed; no DMA outstanding at exit
+  __builtin_amdgcn_s_barrier();
+  load_epi();
   float4 nsc[kNormOut ? NI : 1];  // producer of a folded norm: aw * gamma per column
   if constexpr (kNormOut) {
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      if (p.C16s) {
-        const float4 a = *reinterpret_cast<const float4*>(p.sc_a + colj(j));
-        const float4 g = *reinterpret_cast<const float4*>(p.sc_g + colj(j));
-        nsc[j] = make_float4(a.x * g.x, a.y * g.y, a.z * g.z, a.w * g.w);
-      } else {
-        nsc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+    for (int j = 0; j < NI; ++j) nsc[j] = make_float4(nsa[j].x * nsg[j].x, nsa[j].y * nsg[j].y,
+                                                      nsa[j].z * nsg[j].z, nsa[j].w * nsg[j].w);
   }
-  wait_vmcnt<0>();  // the tail stages have landed; no DMA outstanding at exit
-  __builtin_amdgcn_s_barrier();
   if constexpr (!PIPE) {
     static_for<0, NST - 1>([&](auto st) {
       if (kt0 + (int)decltype(st)::value < KT) compute(st);
@@ -867,20 +909,20 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
           }
         } else if constexpr (EPI == EPI_RESSKIP) {
           // v is the res_skip conv output (bias included).
-          const float mk = p.mask[m] ? 1.0f : 0.0f;
-          const float4 o = pre_a[i][j];
+          const float mk = pre_mask[i] ? 1.0f : 0.0f;
+          // the skip accumulator starts at zero when flag is 0
+          const float4 o = n < 512 || p.flag ? pre_a[i][j] : make_float4(0.f, 0.f, 0.f, 0.f);
           if (n < 512) {
             const float4 xn = make_float4((o.x + v.x) * mk, (o.y + v.y) * mk, (o.z + v.z) * mk,
                                           (o.w + v.w) * mk);
             *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) = xn;
             st16(p.C16 + (size_t)m * p.ldc16 + n, xn.x, xn.y, xn.z, xn.w);
           } else {
-            // pre_a is zero when the skip accumulator starts at zero (flag 0)
             *reinterpret_cast<float4*>(p.C32b + (size_t)m * p.ldc32b + (n - 512)) =
                 make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
           }
         } else {  // EPI_FINALSKIP: out = (out + rs) * mask; final_in = out + rp
-          const float mk = p.mask[m] ? 1.0f : 0.0f;
+          const float mk = pre_mask[i] ? 1.0f : 0.0f;
           const float4 o = pre_a[i][j];
           const float4 r = pre_b[i][j];
           *reinterpret_cast<float4*>(p.C32 + (size_t)m * p.ldc32 + n) =
@@ -999,8 +1041,8 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
           st16(p.C16 + (size_t)m * p.ldc16 + c, y[0], y[1], y[2], y[3]);
         } else if constexpr (EPI == EPI_GATE) {
           const int c = group * 16 + 4 * lg;
-          const float4 ca = *reinterpret_cast<const float4*>(p.cond + c);
-          const float4 cb = *reinterpret_cast<const float4*>(p.cond + 512 + c);
+          const float4 ca = pre_ca[q];
+          const float4 cb = pre_cb[q];
           const float cav[4] = {ca.x, ca.y, ca.z, ca.w};
           const float cbv[4] = {cb.x, cb.y, cb.z, cb.w};
           float y[4];
