@@ -225,35 +225,6 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   const bool perm = EPI == EPI_F32 && p.colperm;
   auto colj = [&](int j) { return perm ? col_base + 32 * (j >> 1) + 4 * lg + 4 * (j & 1) : col_base + 16 * j; };
 
-  // Per-column epilogue operands: bias, column scale, and the folded-norm
-  // producer's aw and gamma (multiplied where they are used, so no wait
-  // follows the loads).  They are requested after the K loop's last wait,
-  // so their latency overlaps the resident tail stages' compute and they
-  // hold no registers through the loop.
-  float4 bv[NI];
-  constexpr bool kColScale = EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_RESAVG;
-  float4 csv[kColScale ? NI : 1];
-  constexpr bool kNormOut = EPI == EPI_F32;
-  float4 nsa[kNormOut ? NI : 1], nsg[kNormOut ? NI : 1];
-  auto load_epi = [&]() {
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-      bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (kColScale) {
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-        csv[j] = p.colscale ? *reinterpret_cast<const float4*>(p.colscale + colj(j))
-                            : make_float4(1.f, 1.f, 1.f, 1.f);
-    }
-    if constexpr (kNormOut) {
-#pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        nsa[j] = p.C16s ? *reinterpret_cast<const float4*>(p.sc_a + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
-        nsg[j] = p.C16s ? *reinterpret_cast<const float4*>(p.sc_g + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-  };
-
   // Epilogue operands that do not depend on the product are fetched before
   // the K loop, so their latency hides behind it (PIPE = 1: after the loop,
   // so they do not hold registers beside its larger tiles).
@@ -729,12 +700,33 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   }
   wait_vmcnt<0>();  // the tail stages have landed; no DMA outstanding at exit
   __builtin_amdgcn_s_barrier();
-  load_epi();
-  float4 nsc[kNormOut ? NI : 1];  // producer of a folded norm: aw * gamma per column
+  // Late prefetch: the small per-column epilogue operands are requested after
+  // the K loop's last wait, so their latency overlaps the resident tail
+  // stages' compute without holding registers through the K loop; the
+  // folded-norm producer's aw and gamma are multiplied in the epilogue, so
+  // nothing waits for them before the tail.  (Issued ahead of that wait, they
+  // were covered by it; kept in a lambda or issued before the K loop, the
+  // compiler moved the loop's accumulators between registers every stage.)
+  float4 bv[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+    bv[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr bool kColScale = EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_RESAVG;
+  float4 csv[kColScale ? NI : 1];
+  if constexpr (kColScale) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      csv[j] = p.colscale ? *reinterpret_cast<const float4*>(p.colscale + colj(j))
+                          : make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  constexpr bool kNormOut = EPI == EPI_F32;
+  float4 nsa[kNormOut ? NI : 1], nsg[kNormOut ? NI : 1];
   if constexpr (kNormOut) {
 #pragma unroll
-    for (int j = 0; j < NI; ++j) nsc[j] = make_float4(nsa[j].x * nsg[j].x, nsa[j].y * nsg[j].y,
-                                                      nsa[j].z * nsg[j].z, nsa[j].w * nsg[j].w);
+    for (int j = 0; j < NI; ++j) {
+      nsa[j] = p.C16s ? *reinterpret_cast<const float4*>(p.sc_a + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+      nsg[j] = p.C16s ? *reinterpret_cast<const float4*>(p.sc_g + colj(j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
   if constexpr (!PIPE) {
     static_for<0, NST - 1>([&](auto st) {
@@ -828,6 +820,12 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
     *reinterpret_cast<half4*>(dst + p.c16_lo) = l;
   };
 
+  float4 nsc[kNormOut ? NI : 1];  // producer of a folded norm: aw * gamma per column
+  if constexpr (kNormOut) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) nsc[j] = make_float4(nsa[j].x * nsg[j].x, nsa[j].y * nsg[j].y,
+                                                      nsa[j].z * nsg[j].z, nsa[j].w * nsg[j].w);
+  }
   if constexpr (EPI == EPI_F32 || EPI == EPI_F16 || EPI == EPI_DUAL || EPI == EPI_RESSKIP ||
                 EPI == EPI_FINALSKIP || EPI == EPI_RESAVG) {
 #pragma unroll
