@@ -250,35 +250,62 @@ __global__ __launch_bounds__(256) void conv2_euler_kernel(
   const int nvalid = min(16, T - t0);
   const int bc = cfg_on ? 2 * r : r;
   const int nbr = cfg_on ? 2 : 1;
-  for (int br = 0; br < nbr; ++br) {
-    const size_t row0 = (size_t)(bc + br) * T + t0;
+  // Every operand this lane needs is requested up front (the weights once for
+  // both branches, the rows clamped to the last valid one), then the
+  // products run; loaded where they were used, each K step waited for its
+  // own loads.
+  half8 bw[4][5], av[2][4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int k = wave * 128 + ks * 32 + lg * 8;
+#pragma unroll
+    for (int nb = 0; nb < 5; ++nb) bw[ks][nb] = *reinterpret_cast<const half8*>(w2 + (size_t)(nb * 16 + lr) * 512 + k);
+#pragma unroll
+    for (int br = 0; br < 2; ++br) {
+      const size_t row = (size_t)(bc + (br < nbr ? br : 0)) * T + t0 + min(lr, nvalid - 1);
+      av[br][ks] = *reinterpret_cast<const half8*>(y16 + row * 512 + k);
+    }
+  }
+#pragma unroll
+  for (int br = 0; br < 2; ++br) {
+    if (br >= nbr) break;
     floatx4 acc[5];
 #pragma unroll
     for (int nb = 0; nb < 5; ++nb) acc[nb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int k = wave * 128 + ks * 32 + lg * 8;
-      half8 av = {};
-      if (lr < nvalid) av = *reinterpret_cast<const half8*>(y16 + (row0 + lr) * 512 + k);
+      half8 a = av[br][ks];
+      if (lr >= nvalid) a = half8{};
 #pragma unroll
-      for (int nb = 0; nb < 5; ++nb) {
-        const half8 bw = *reinterpret_cast<const half8*>(w2 + (size_t)(nb * 16 + lr) * 512 + k);
-        acc[nb] = mfma16x16x32(av, bw, acc[nb]);
-      }
+      for (int nb = 0; nb < 5; ++nb) acc[nb] = mfma16x16x32(a, bw[ks][nb], acc[nb]);
     }
 #pragma unroll
     for (int nb = 0; nb < 5; ++nb)
       *reinterpret_cast<floatx4*>(&red[wave][br][nb][lane][0]) = acc[nb];
   }
+  // The update's state (5 values per thread) is read before any of it is written.
+  constexpr int kPer = 16 * 80 / 256;
+  float xo[kPer], bo[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int idx = threadIdx.x + 256 * u;
+    const int tok = idx / 80;
+    const int n = idx - tok * 80;
+    const int t = min(t0 + tok, T - 1);
+    xo[u] = x_cur[((size_t)r * T + t) * 80 + n];
+    bo[u] = b2[n];
+  }
   __syncthreads();
   const uint32_t Pr = P[r];
-  for (int idx = threadIdx.x; idx < 16 * 80; idx += 256) {
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int idx = threadIdx.x + 256 * u;
     const int tok = idx / 80;
     const int n = idx - tok * 80;
     const int t = t0 + tok;
     if (t >= T) continue;
     const int nb = n >> 4, ln = (tok >> 2) * 16 + (n & 15), i = tok & 3;
-    const float bias = b2[n];
+    const float bias = bo[u];
     float v = bias;
 #pragma unroll
     for (int w = 0; w < 4; ++w) v += red[w][0][nb][ln][i];
@@ -290,7 +317,7 @@ __global__ __launch_bounds__(256) void conv2_euler_kernel(
     }
     const size_t xi = ((size_t)r * T + t) * 80 + n;
     if (vtrace) vtrace[xi] = v;
-    float xn = x_cur[xi] + dt * v;
+    float xn = xo[u] + dt * v;
     if ((uint32_t)t < Pr) xn = 0.0f;
     x_cur[xi] = xn;
     xmel16[((size_t)bc * T + t) * kMelPad + n] = (half_t)xn;
