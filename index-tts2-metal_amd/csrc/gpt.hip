@@ -825,9 +825,20 @@ __global__ __launch_bounds__(320) void embed_kernel(const GptState* st, const fl
 constexpr int kAttnThreads = 512;
 constexpr int kPartF = 2 + kHD;  // per split: max, sum, unnormalised output
 
-__device__ __forceinline__ int attn_keys(const GptState* st, int z) { return min(st->kv + z + 1, st->cap); }
-__device__ __forceinline__ bool attn_row_live(const GptState* st, int z) {
-  return gridDim.z == 1 || z < min((int)gridDim.z, st->pend - st->kv);
+// What an attention block needs from the state: whether it has nothing to do
+// (the decode stopped, row z is past the prefill chunk, or the caches have
+// no rows) and row z's key count.  The four fields are read before anything
+// is decided, and all of them decide, so the loads are issued together and
+// their latencies overlap; tested one after another (as short-circuit tests
+// with the key count read after them), each load waited for the one before.
+struct AttnRow {
+  bool idle;
+  int keys;
+};
+__device__ __forceinline__ AttnRow attn_row(const GptState* st, int z, int check_stop) {
+  const int kv = st->kv, stopped = st->stopped, cap = st->cap, pend = st->pend;
+  const bool live = gridDim.z == 1 || z < min((int)gridDim.z, pend - kv);
+  return {(check_stop && stopped) || !live || cap <= 0, min(kv + z + 1, cap)};
 }
 
 __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const float* q, const float* kc, const float* vc,
@@ -838,9 +849,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const float* q
   constexpr int kVKeysPerPass = kAttnThreads / 16, kVPass = kChunk / kVKeysPerPass;
   constexpr int kGroups = kAttnThreads / 16;  // output key groups
   const int h = blockIdx.x, sp = blockIdx.y, z = blockIdx.z, tid = threadIdx.x;
-  if (check_stop && st->stopped) return;
-  if (!attn_row_live(st, z)) return;
-  const int kvn = attn_keys(st, z);
+  const AttnRow row = attn_row(st, z, check_stop);
+  if (row.idle) return;
+  const int kvn = row.keys;
   const int nsplit = (kvn + kChunk - 1) / kChunk;
   if (sp >= nsplit) return;
   q += (size_t)z * kW;
@@ -921,9 +932,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const float* q
 __global__ __launch_bounds__(64) void attn_combine_kernel(const GptState* st, const float* part, float* out,
                                                           int nsplit_max, int check_stop) {
   const int h = blockIdx.x, z = blockIdx.z, d = threadIdx.x;
-  if (check_stop && st->stopped) return;
-  if (!attn_row_live(st, z)) return;
-  const int nsplit = (attn_keys(st, z) + kChunk - 1) / kChunk;
+  const AttnRow row = attn_row(st, z, check_stop);
+  if (row.idle) return;
+  const int nsplit = (row.keys + kChunk - 1) / kChunk;
   if (nsplit == 1) return;  // written by the split kernel
   const float* ph = part + ((size_t)z * kHeads + h) * nsplit_max * kPartF;
   // eight splits per round trip (the loads are issued before they are used)
