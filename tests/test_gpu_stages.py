@@ -169,6 +169,31 @@ def test_block_batched(orc, model_unit, ctx_unit, layer):
     assert np.array_equal(single[0], got[0])
 
 
+@pytest.mark.parametrize("layer", [0, 7])
+def test_block_long_rows_bit_identical(orc, model_unit, ctx_unit, layer):
+    """Four branches of T=1400 (5,600 rows: the QKV product takes the
+    row-resident loop, which keeps a 64-row block in LDS and streams the
+    weight) against the same block for one branch (1,400 rows: the 64x64
+    tiles): every row bit-identical, and branch 0 against the oracle."""
+    T, B = 1400, 4
+    x = np.stack([sincos_series(T * 512, 0.019 + 0.002 * b, 0.017, 0.12, 0.07, 113 + b)
+                  for b in range(B)]).reshape(B, T, 512)
+    t1 = (np.cos(np.arange(512, dtype=np.float32) * np.float32(0.014)) * 0.25).astype(np.float32)
+    masks = np.ones((B, T), np.uint32)
+    masks[1, 1100:] = 0
+    skip = None
+    if layer > 6:
+        skip = np.stack([sincos_series(T * 512, 0.031, 0.019 + 0.001 * b, 0.11, 0.05, 79 + b)
+                         for b in range(B)]).reshape(B, T, 512)
+    print(f"block layer={layer} B={B} T={T}", flush=True)
+    got = ctx_unit.block(x, t1, masks, layer, skip)
+    for b in (0, 1):
+        single = ctx_unit.block(x[b:b + 1], t1, masks[b:b + 1], layer, None if skip is None else skip[b:b + 1])
+        assert np.array_equal(single[0], got[b])
+    ref = model_unit.block(x[0], t1, masks[0], layer, None if skip is None else skip[0])
+    assert rel(orc, got[0], ref) <= STAGE_TOL
+
+
 def test_stack(orc, model_unit, ctx_unit):
     T = 6
     x = np.stack([sincos_series(T * 512, 0.015, 0.019, 0.11, 0.06, 131),
