@@ -517,16 +517,42 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* log
         if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
       __syncthreads();
-      if (tid == 0) {
-        uint32_t cum = 0u;
+      if (tid < 64) {
+        // The highest bin b whose count, with every count above it, reaches
+        // kleft.  Lane l holds bins 255 - 4 l .. 252 - 4 l; an exclusive scan
+        // over the lanes gives each lane the count above its bins, and the
+        // first lane (from the top) that reaches kleft names b -- the bin a
+        // walk from 255 down would stop at, in a few wave steps instead of up
+        // to 256 dependent steps on one thread.
         const uint32_t kleft = s_kleft;
-        for (int b = 255; b >= 0; --b) {
-          if (cum + hist[b] >= kleft) {
-            s_prefix = prefix | ((uint32_t)b << shift);
-            s_kleft = kleft - cum;
-            break;
+        uint32_t h4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h4[j] = hist[255 - 4 * tid - j];
+        const uint32_t t4 = (h4[0] + h4[1]) + (h4[2] + h4[3]);
+        uint32_t incl = t4;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t v = __shfl_up(incl, off, kWave);
+          if (tid >= off) incl += v;
+        }
+        uint32_t cum = incl - t4;
+        int fj = -1;
+        uint32_t fcum = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (fj < 0) {
+            if (cum + h4[j] >= kleft) {
+              fj = j;
+              fcum = cum;
+            } else {
+              cum += h4[j];
+            }
           }
-          cum += hist[b];
+        }
+        const uint64_t hit = __ballot(fj >= 0);
+        if (hit != 0ull && tid == __ffsll((unsigned long long)hit) - 1) {
+          s_prefix = prefix | ((uint32_t)(255 - 4 * tid - fj) << shift);
+          s_kleft = kleft - fcum;
         }
       }
       mask |= 255u << shift;
@@ -576,20 +602,47 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* log
         else { sv[seg + t] = -INFINITY; si[seg + t] = 0xffffffffu; }
       }
       __syncthreads();
-      for (int k = 2; k <= S; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-          for (int i = tid; i < S; i += kSampleThreads) {
-            const int ixj = i ^ j;
-            if (ixj <= i) continue;
-            const bool up = (i & k) == 0;
-            const float a = sv[seg + i], b = sv[seg + ixj];
-            const uint32_t ai = si[seg + i], bi = si[seg + ixj];
-            if (pair_less(b, bi, a, ai) == up) {
-              sv[seg + i] = b; sv[seg + ixj] = a;
-              si[seg + i] = bi; si[seg + ixj] = ai;
+      if (S <= 64) {
+        // The same bitonic network in one wavefront's registers: lane i holds
+        // element i; of each compared pair (i, i ^ j) the lower lane keeps the
+        // smaller (ascending block) or the larger, the upper lane the other.
+        if (tid < 64) {
+          float v = tid < S ? sv[seg + tid] : -INFINITY;
+          uint32_t id = tid < S ? si[seg + tid] : 0xffffffffu;
+          for (int k = 2; k <= S; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+              const float pv = __shfl_xor(v, j, kWave);
+              const uint32_t pid = (uint32_t)__shfl_xor((int)id, j, kWave);
+              const bool keep_min = (tid < (tid ^ j)) == ((tid & k) == 0);
+              const bool take = keep_min ? pair_less(pv, pid, v, id) : pair_less(v, id, pv, pid);
+              if (take) {
+                v = pv;
+                id = pid;
+              }
             }
           }
-          __syncthreads();
+          if (tid < S) {
+            sv[seg + tid] = v;
+            si[seg + tid] = id;
+          }
+        }
+        __syncthreads();
+      } else {
+        for (int k = 2; k <= S; k <<= 1) {
+          for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < S; i += kSampleThreads) {
+              const int ixj = i ^ j;
+              if (ixj <= i) continue;
+              const bool up = (i & k) == 0;
+              const float a = sv[seg + i], b = sv[seg + ixj];
+              const uint32_t ai = si[seg + i], bi = si[seg + ixj];
+              if (pair_less(b, bi, a, ai) == up) {
+                sv[seg + i] = b; sv[seg + ixj] = a;
+                si[seg + i] = bi; si[seg + ixj] = ai;
+              }
+            }
+            __syncthreads();
+          }
         }
       }
       for (int i = tid; i < N; i += kSampleThreads)
