@@ -375,22 +375,26 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   // A_CONVP: source of the 16-byte chunk at K position k0 + kc of load slot
   // j's row m; `lo` selects the lo half of a split operand (the resident
   // zero row serves both halves).
+  // Branch-free (the corrections and the zero-row choice are selects: as
+  // if / else on per-lane values they made divergent branches around every
+  // load), with one 32-bit element offset (the host keeps M x lda below
+  // 2^31) added to the chosen base.
   auto convp_src = [&](int j, int k0, int kc, bool lo) -> const half_t* {
     const int k = k0 + kc;
-    const size_t lo_off = lo ? p.a_lo : 0;
     // tap = k / conv_c through a float reciprocal, corrected by one either way
     int tap = (int)((float)k * p.conv_inv_c);
     int c = k - tap * p.conv_c;
-    if (c < 0) {
-      --tap;
-      c += p.conv_c;
-    } else if (c >= p.conv_c) {
-      ++tap;
-      c -= p.conv_c;
-    }
+    const bool under = c < 0;
+    tap = under ? tap - 1 : tap;
+    c = under ? c + p.conv_c : c;
+    const bool over = c >= p.conv_c;
+    tap = over ? tap + 1 : tap;
+    c = over ? c - p.conv_c : c;
     const int src = cp_t[j] + tap * p.conv_d - p.conv_pad;
     const bool ok = tap < p.conv_k && src >= 0 && src < p.T;
-    return ok ? p.A + lo_off + (size_t)(cp_base[j] + src) * p.lda + c : p.A_zero + c;
+    const half_t* base = ok ? p.A + (lo ? p.a_lo : 0) : p.A_zero;
+    const int off = ok ? (cp_base[j] + src) * p.lda + c : c;
+    return base + off;
   };
 
   // Every other operand is read through a buffer resource: a lane's byte
@@ -1586,14 +1590,15 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
 }
 
 // Every operand gemm_kernel reads through a buffer resource spans less than
-// 2^31 bytes (buffer offsets are 32-bit; the A_CONVP operand is read with
-// global addresses instead).
+// 2^31 bytes (buffer offsets are 32-bit).  The A_CONVP operand is read with
+// global addresses instead, formed from a 32-bit element offset within each
+// half of the pair: its M x lda halves stay below 2^31.
 static bool gemm_spans_fit(const GemmArgs& a, AMode am) {
   constexpr size_t kMax = size_t(1) << 31;
   if (a.N <= 0 || a.M <= 0 || a.K <= 0 || a.ldw < 0 || a.lda < 0 || a.lda2 < 0) return false;
   const size_t w = ((size_t)(a.N - 1) * a.ldw + a.K + a.w_lo) * 2;
   const size_t rows = am == A_CONV3Z ? (size_t)a.M + 1 : (size_t)a.M;
-  const size_t aa = am == A_CONVP ? 0 : (rows * a.lda + a.a_lo) * 2;
+  const size_t aa = am == A_CONVP ? (size_t)a.M * a.lda : (rows * a.lda + a.a_lo) * 2;
   const size_t a2 = am == A_CONCAT ? ((size_t)a.M * a.lda2 + a.a_lo) * 2 : 0;
   return w < kMax && aa < kMax && a2 < kMax;
 }
