@@ -378,8 +378,16 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   // Branch-free (the corrections and the zero-row choice are selects: as
   // if / else on per-lane values they made divergent branches around every
   // load), with one 32-bit element offset (the host keeps M x lda below
-  // 2^31) added to the chosen base.
-  auto convp_src = [&](int j, int k0, int kc, bool lo) -> const half_t* {
+  // 2^31) added to the chosen base.  The row offset is formed for every
+  // lane (in wrapping arithmetic: a padding tap's row may lie outside the
+  // tensor, and its offset is then replaced) and pinned by an empty asm
+  // statement, so the compiler cannot move it back under a branch.  Both
+  // halves of a split operand share it.
+  struct ConvpSrc {
+    const half_t* hi;
+    const half_t* lo;
+  };
+  auto convp_src = [&](int j, int k0, int kc) -> ConvpSrc {
     const int k = k0 + kc;
     // tap = k / conv_c through a float reciprocal, corrected by one either way
     int tap = (int)((float)k * p.conv_inv_c);
@@ -392,9 +400,10 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
     c = over ? c - p.conv_c : c;
     const int src = cp_t[j] + tap * p.conv_d - p.conv_pad;
     const bool ok = tap < p.conv_k && src >= 0 && src < p.T;
-    const half_t* base = ok ? p.A + (lo ? p.a_lo : 0) : p.A_zero;
-    const int off = ok ? (cp_base[j] + src) * p.lda + c : c;
-    return base + off;
+    uint32_t row_off = (uint32_t)(cp_base[j] + src) * (uint32_t)p.lda + (uint32_t)c;
+    __asm__("" : "+v"(row_off));
+    const int off = ok ? (int)row_off : c;
+    return {(ok ? p.A : p.A_zero) + off, (ok ? p.A + p.a_lo : p.A_zero) + off};
   };
 
   // Every other operand is read through a buffer resource: a lane's byte
@@ -445,9 +454,9 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
       if constexpr (AM == A_CONVP) {
         const int q = q0 + lane;
         const int c = (q % CPR) ^ swz(q / CPR);
-        __builtin_amdgcn_global_load_lds((const void*)convp_src(j, k0, c * 8, false), dst, 16, 0, 0);
-        if constexpr (AS == 2)
-          __builtin_amdgcn_global_load_lds((const void*)convp_src(j, k0, c * 8, true), dst_lo, 16, 0, 0);
+        const ConvpSrc src = convp_src(j, k0, c * 8);
+        __builtin_amdgcn_global_load_lds((const void*)src.hi, dst, 16, 0, 0);
+        if constexpr (AS == 2) __builtin_amdgcn_global_load_lds((const void*)src.lo, dst_lo, 16, 0, 0);
       } else if constexpr (kConv) {
         // The tap's row offset by value selects on the wave-uniform tap: a
         // select of the members' addresses would put conv_rows in scratch
