@@ -45,11 +45,25 @@ __device__ __forceinline__ void buffer_load_lds16(buffer_rsrc_t r, lds_ptr_t* ld
 __device__ __forceinline__ void buffer_load_lds4(buffer_rsrc_t r, lds_ptr_t* lds, int voffset, int soffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 4, voffset, soffset, 0, 0);
 }
+// Register loads and stores through a resource: one 32-bit byte offset per
+// lane; a store past the resource's byte range is dropped.
+__device__ __forceinline__ float buffer_load_f32(buffer_rsrc_t r, int voffset) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voffset, 0, 0));
+}
+__device__ __forceinline__ void buffer_store_f32(buffer_rsrc_t r, int voffset, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voffset, 0, 0);
+}
+__device__ __forceinline__ void buffer_store_f16(buffer_rsrc_t r, int voffset, half_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, voffset, 0, 0);
+}
 #else
 struct buffer_rsrc_t { const void* base; };
 __device__ inline buffer_rsrc_t make_buffer_rsrc(const void* base, int) { return buffer_rsrc_t{base}; }
 __device__ inline void buffer_load_lds16(buffer_rsrc_t, lds_ptr_t*, int, int) {}
 __device__ inline void buffer_load_lds4(buffer_rsrc_t, lds_ptr_t*, int, int) {}
+__device__ inline float buffer_load_f32(buffer_rsrc_t, int) { return 0.0f; }
+__device__ inline void buffer_store_f32(buffer_rsrc_t, int, float) {}
+__device__ inline void buffer_store_f16(buffer_rsrc_t, int, half_t) {}
 #endif
 
 // Padded operand widths (every GEMM K is a multiple of 128 so that K stages

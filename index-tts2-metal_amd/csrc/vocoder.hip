@@ -94,13 +94,17 @@ __global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__
   const int c = (int)(g - (long)run * C);
   const int t0 = run * R;
   if (t0 >= T) return;
+  // The activation is read and written through buffer resources: one 32-bit
+  // byte offset per access (T x C < 2^29, checked on the host), and the
+  // hardware drops the stores of rows past T.
+  const buffer_rsrc_t rX = make_buffer_rsrc(x, T * C * 4);
+  // Rows t0 - 6 + i, clamped to [0, T): consecutive rows are C values
+  // apart, so the offsets advance by additions and the clamp applies to them.
+  const int e_first = c, e_last = (T - 1) * C + c;
   float xw[XW];
+  int e = (t0 - 6) * C + c;
 #pragma unroll
-  for (int i = 0; i < XW; ++i) {
-    int src = t0 - 6 + i;
-    src = src < 0 ? 0 : (src >= T ? T - 1 : src);
-    xw[i] = x[(size_t)src * C + c];
-  }
+  for (int i = 0; i < XW; ++i, e += C) xw[i] = buffer_load_f32(rX, min(max(e, e_first), e_last) * 4);
   const float a = alpha[c], ib = inv_beta[c];
   float z[ZW];
 #pragma unroll
@@ -130,24 +134,27 @@ __global__ __launch_bounds__(256) void snake_aa_kernel(const float* __restrict__
 #pragma unroll
     for (int i = 0; i < ZW; ++i) z[i] = i > i_end ? ze : z[i];
   }
+  const buffer_rsrc_t rO = make_buffer_rsrc(out, T * C * (OUT16 ? 2 : 4));
+  const buffer_rsrc_t rL = make_buffer_rsrc(static_cast<half_t*>(out) + out_lo, T * C * 2);
+  e = t0 * C + c;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (t0 + r >= T) break;
+  for (int r = 0; r < R; ++r, e += C) {
+    // rows t0 + r >= T fall past the resources' ranges: their stores are dropped
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < 12; ++k) acc += z[2 * r + k] * f.down[k];
     if constexpr (OUT16) {
-      half_t* o = static_cast<half_t*>(out) + (size_t)(t0 + r) * C + c;
       if (out_lo) {
         half_t h, l;
         split_f16(acc, h, l);
-        o[0] = h;
-        o[out_lo] = l;
+        buffer_store_f16(rO, e * 2, h);
+        buffer_store_f16(rL, e * 2, l);
       } else {
-        o[0] = (half_t)acc;
+        buffer_store_f16(rO, e * 2, (half_t)acc);
       }
-    } else
-      static_cast<float*>(out)[(size_t)(t0 + r) * C + c] = acc;
+    } else {
+      buffer_store_f32(rO, e * 4, acc);
+    }
   }
 }
 
@@ -442,6 +449,8 @@ struct Vocoder::Impl {
 
   // out16: out is a split pair buffer (lo at + out_lo, written in f32 mode).
   void activation(const Act& a, const float* in, int T, void* out, bool out16, size_t out_lo = 0) {
+    // the kernel addresses the T x C activation with 32-bit byte offsets
+    if ((size_t)T * (size_t)a.C >= (size_t(1) << 29)) VOC_OK(hipErrorInvalidValue);
     const size_t lanes = (size_t)((T + kActR - 1) / kActR) * a.C;
     const dim3 grid((unsigned)((lanes + 255) / 256));
     if (out16)
