@@ -24,7 +24,25 @@ enum AMode : int {
   A_CONVP = 4,   // any zero-padded conv, k = tap*conv_c + c (conv_c a multiple of 8, K padded
                  // to the stage width): A[(b*T + t + tap*conv_d - conv_pad)*lda + c], zero
                  // (read from A_zero) outside [0, T) and for tap >= conv_k
+  A_CONVW = 5,   // internal: an A_CONVP product of one sequence (M = T) whose row block's
+                 // input window sits in LDS (see conv_window_halves); launch_gemm picks it
+                 // for A_CONVP when the window fits and conv_window is set
 };
+
+// A_CONVW: LDS halves of a BM-row block's input window.  The window holds
+// rows m0 - conv_pad .. m0 + BM - 1 + (conv_k - 1) conv_d - conv_pad of the
+// operand, each padded to conv_window_chunks(conv_c) 16-byte chunks (the
+// extra ones zero: the padded K positions read them), for each half of a
+// split pair.  Sized for BM + 56 rows of BN + 16 halves (the vocoder's
+// resblock convs have conv_c <= N and (conv_k - 1) conv_d <= 50), rounded to
+// whole 512-lane fill rounds.
+constexpr int conv_window_halves(int bm, int bn, int copies) {
+  return (copies * (bm + 56) * (bn + 16) + 4095) / 4096 * 4096;
+}
+// 16-byte chunks per window row: conv_c / 8 data chunks and at least one zero
+// chunk, an odd count (a row stride of an odd number of 16-byte chunks puts
+// the 16 rows a fragment read spans in distinct LDS banks).
+constexpr int conv_window_chunks(int conv_c) { return conv_c / 8 + 1 + ((conv_c / 8) & 1); }
 
 enum EpiMode : int {
   EPI_F32 = 0,        // C32 = acc + bias + res (bias/res optional; C32 may be null when
@@ -57,6 +75,9 @@ struct GemmArgs {
   float conv_inv_c = 0.f;
   int n_store = 0;  // if nonzero: only columns < n_store are stored (weights zero-padded to N)
   const half_t* A_zero = nullptr;  // A_CONVP: >= conv_c zero halves, read by the padding taps
+  int conv_window = 1;             // A_CONVP with M = T: 0 streams every tap's rows (no A_CONVW)
+  uint32_t conv_magic = 0;         // A_CONVW, set by launch_gemm: ceil(2^32 / conv_c), so that
+                                   // k / conv_c = umulhi(k, conv_magic) for k conv_c < 2^32
   // weights
   const half_t* W = nullptr;
   int ldw = 0;

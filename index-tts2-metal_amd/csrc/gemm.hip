@@ -134,7 +134,8 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   constexpr int LB = BN * CPR / (64 * NW);   // (W)
   constexpr int AS = SP >= 1 ? 2 : 1;        // copies of each A stage (split: hi, lo)
   constexpr int WS = SP == 2 ? 2 : 1;        // copies of each W stage
-  constexpr int L = LA * AS + LB * WS;       // DMA instructions per wave per stage
+  constexpr bool kWin = AM == A_CONVW;       // A from the LDS window: only W is streamed
+  constexpr int L = (kWin ? 0 : LA * AS) + LB * WS;  // DMA instructions per wave per stage
   constexpr int WTM = BM / WM;               // rows of a wave's sub-tile
   constexpr int WTN = BN / WN;               // columns of a wave's sub-tile
   constexpr int MI = WTM / 16;               // 16-row MFMA blocks per wave
@@ -150,20 +151,26 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
                 "pipelined loop: K in 1 or 2 parts; split operands with one part");
   static_assert(EPI != EPI_QKV || 512 % BN == 0, "a qkv tile must lie inside one of the q, k, v sections");
   static_assert(SP >= 0 && SP <= 2, "split mode");
+  static_assert(!kWin || (!PIPE && KG == 1), "window convs: the one-group stage loop");
 
   // One __shared__ object per stage and operand, declared here so each kernel
   // instantiation owns its own objects (the per-object alias scopes are what
   // let the compiler keep only the explicit vmcnt waits).
   // With KG = 2 K groups, each group has its own region in every buffer;
   // split operands keep their lo halves after all the groups' hi halves.
-  __shared__ __attribute__((aligned(1024))) half_t sA0[AS * KW * BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA1[AS * KW * BM * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? AS * KW * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? AS * KW * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA4[NST > 4 ? AS * KW * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA5[NST > 5 ? AS * KW * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA6[NST > 6 ? AS * KW * BM * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA7[NST > 7 ? AS * KW * BM * SK : 8];
+  constexpr int kAStage = kWin ? 8 : AS * KW * BM * SK;
+  __shared__ __attribute__((aligned(1024))) half_t sA0[kAStage];
+  __shared__ __attribute__((aligned(1024))) half_t sA1[kAStage];
+  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? kAStage : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? kAStage : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA4[NST > 4 ? kAStage : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA5[NST > 5 ? kAStage : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA6[NST > 6 ? kAStage : 8];
+  __shared__ __attribute__((aligned(1024))) half_t sA7[NST > 7 ? kAStage : 8];
+  // A_CONVW: the row block's input window (hi rows, then lo rows)
+  constexpr int kWinH = kWin ? conv_window_halves(BM, BN, AS) : 8;
+  __shared__ __attribute__((aligned(1024))) half_t sWin[kWinH];
+  static_assert(!kWin || kWinH / (8 * 64 * NW) + L * (NST - 1) < 64, "too many loads in flight");
   __shared__ __attribute__((aligned(1024))) half_t sB0[WS * KW * BN * SK];
   __shared__ __attribute__((aligned(1024))) half_t sB1[WS * KW * BN * SK];
   __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? WS * KW * BN * SK : 8];
@@ -406,6 +413,66 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
     return {(ok ? p.A : p.A_zero) + off, (ok ? p.A + p.a_lo : p.A_zero) + off};
   };
 
+  // A_CONVW (one sequence, M = T): the block's output rows m0 .. m0+BM-1 read
+  // the input rows m0 - conv_pad + w, w < BM + (conv_k-1) conv_d, whatever
+  // their tap; those rows (zero outside [0, T)) are loaded into LDS once per
+  // tile, win_cw halves per row (the last chunks zero), the lo halves of a
+  // split pair after all the hi rows.  Only W then runs through the ring.
+  // The fill is issued ahead of the ring's first stages, so the loop's first
+  // wait (every load older than the stages left in flight) covers it.
+  int win_cw = 8, win_lo = 0, win_row = 0, win_rc = 0;
+  if constexpr (kWin) {
+    win_cw = conv_window_chunks(p.conv_c) * 8;
+    win_rc = (BM + (p.conv_k - 1) * p.conv_d) * (win_cw >> 3);  // chunks per half
+    win_lo = win_rc * 8;
+    win_row = (wm * WTM + lr) * win_cw;
+  }
+  auto fill_window = [&]() {
+    constexpr int NT = 64 * NW;
+    const int cc = p.conv_c >> 3, ccp = win_cw >> 3;
+    const int total = AS * win_rc;
+    const float inv = 1.0f / (float)ccp;
+    const int row0 = m0 - p.conv_pad;
+    // chunk s of the window, s < total rounded up to NT (the host keeps that
+    // inside sWin; the chunks past total read zeros)
+    for (int q0 = 0; q0 < total; q0 += NT) {
+      const int sq = q0 + wave * 64 + lane;
+      const int h = sq >= win_rc ? 1 : 0;
+      const int sl = h ? sq - win_rc : sq;
+      int w = (int)((float)sl * inv);  // row and chunk through a float reciprocal, corrected
+      int c = sl - w * ccp;
+      const bool under = c < 0;
+      w = under ? w - 1 : w;
+      c = under ? c + ccp : c;
+      const bool over = c >= ccp;
+      w = over ? w + 1 : w;
+      c = over ? c - ccp : c;
+      const int src = row0 + w;
+      const bool ok = sq < total && c < cc && src >= 0 && src < p.T;
+      uint32_t off = (uint32_t)src * (uint32_t)p.lda + (uint32_t)(c * 8);
+      __asm__("" : "+v"(off));
+      const half_t* g = ok ? p.A + (h ? p.a_lo : (size_t)0) + off : p.A_zero;
+      __builtin_amdgcn_global_load_lds((const void*)g, (lds_ptr_t*)(sWin + (q0 + wave * 64) * 8), 16, 0, 0);
+    }
+  };
+  // Window offset of the 8 K positions kb + 8 lg .. (one tap) of this lane:
+  // the tap's row shift plus the channel, or the zero chunk for the padded
+  // K positions.  The wave-uniform part (tap and channel of kb, by a scalar
+  // multiply-high) is scalar work; a lane's 8 lg < 32 <= 2 conv_c moves it
+  // at most one tap on.
+  const int lg8 = lg * 8;
+  auto win_off = [&](int kb) -> int {
+    const int dcw = p.conv_d * win_cw;
+    const int tb = (int)__umulhi((uint32_t)kb, p.conv_magic);
+    const int cb = kb - tb * p.conv_c;
+    const int off_a = tb * dcw + cb;             // K positions still in tap tb
+    const int off_b = off_a + dcw - p.conv_c;    // ... moved on to tap tb + 1
+    const bool ok_a = tb < p.conv_k, ok_b = tb + 1 < p.conv_k;
+    const bool wrap = cb + lg8 >= p.conv_c;
+    const int off = (wrap ? off_b : off_a) + lg8;
+    return (wrap ? ok_b : ok_a) ? off : p.conv_c;
+  };
+
   // Every other operand is read through a buffer resource: a lane's byte
   // offset (its row and swizzled 16-byte chunk) is fixed for the kernel and
   // the stage's column offset is a scalar, so issuing a stage costs no
@@ -414,7 +481,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   const int a_rows = AM == A_CONV3Z ? p.M + 1 : p.M;  // A_CONV3Z: row M is the zero row
   const buffer_rsrc_t rW = make_buffer_rsrc(p.W, (int)(((size_t)(p.N - 1) * p.ldw + p.K + p.w_lo) * 2));
   const buffer_rsrc_t rA =
-      make_buffer_rsrc(p.A, AM == A_CONVP ? 0 : (int)(((size_t)a_rows * p.lda + p.a_lo) * 2));
+      make_buffer_rsrc(p.A, AM == A_CONVP || AM == A_CONVW ? 0 : (int)(((size_t)a_rows * p.lda + p.a_lo) * 2));
   const buffer_rsrc_t rA2 =
       AM == A_CONCAT ? make_buffer_rsrc(p.A2, (int)(((size_t)p.M * p.lda2 + p.a_lo) * 2)) : rA;
   int voA[LA], voA2[AM == A_CONCAT ? LA : 1], voW[LB];
@@ -451,7 +518,10 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
       const int q0 = (wave * LA + j) * 64;
       lds_ptr_t* dst = (lds_ptr_t*)(sa + q0 * 8);
       lds_ptr_t* dst_lo = (lds_ptr_t*)(sa + kALo + q0 * 8);
-      if constexpr (AM == A_CONVP) {
+      if constexpr (kWin) {
+        (void)dst;
+        (void)dst_lo;
+      } else if constexpr (AM == A_CONVP) {
         const int q = q0 + lane;
         const int c = (q % CPR) ^ swz(q / CPR);
         const ConvpSrc src = convp_src(j, k0, c * 8);
@@ -526,16 +596,26 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
     __asm__("" : "+v"(a_lane[kk]), "+v"(b_lane[kk]));
 #endif
   }
-  auto compute = [&](auto st) {
+  auto compute = [&](auto st, int kt) {
     const half_t* sa = bufA(st) - (KW == 1 ? 0 : kg * BM * SK);
     const half_t* sb = bufB(st) - (KW == 1 ? 0 : kg * BN * SK);
 #pragma unroll
     for (int kk = 0; kk < SK / 32; ++kk) {
       half8 af[MI];
       half8 bf[NI];
+      int wo = 0;  // A_CONVW: this lane's window offset for K step kk
+      if constexpr (kWin) {
+        wo = win_row + win_off((kt + kt_lo) * SK + kk * 32);
+#if defined(__HIP_DEVICE_COMPILE__)
+        __asm__("" : "+v"(wo));
+#endif
 #pragma unroll
-      for (int i = 0; i < MI; ++i)
-        af[i] = *reinterpret_cast<const half8*>(sa + a_lane[kk] + i * 16 * SK);
+        for (int i = 0; i < MI; ++i) af[i] = *reinterpret_cast<const half8*>(sWin + wo + i * 16 * win_cw);
+      } else {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          af[i] = *reinterpret_cast<const half8*>(sa + a_lane[kk] + i * 16 * SK);
+      }
 #pragma unroll
       for (int j = 0; j < NI; ++j)
         bf[j] = *reinterpret_cast<const half8*>(sb + b_lane[kk] + j * 16 * SK);
@@ -547,7 +627,8 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
         half8 afl[MI];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
-          afl[i] = *reinterpret_cast<const half8*>(sa + kALo + a_lane[kk] + i * 16 * SK);
+          afl[i] = kWin ? *reinterpret_cast<const half8*>(sWin + win_lo + wo + i * 16 * win_cw)
+                        : *reinterpret_cast<const half8*>(sa + kALo + a_lane[kk] + i * 16 * SK);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -698,6 +779,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   // again), which keeps the compiler from adding waits of its own; the last
   // KT % NST stages are resident when the loop exits.
   if constexpr (!PIPE) {
+    if constexpr (kWin) fill_window();
     static_for<0, NST - 1>([&](auto st) { issue(st, (int)decltype(st)::value); });
     norm_in();
     for (; kt0 + NST <= KT; kt0 += NST) {
@@ -707,7 +789,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
         wait_lgkmcnt0();               // this wave's reads of stage kt0+s-1 have returned
         __builtin_amdgcn_s_barrier();  // ... for every wave
         issue(std::integral_constant<int, (s + NST - 1) % NST>{}, kt0 + s + NST - 1);
-        compute(st);
+        compute(st, kt0 + s);
       });
     }
   }
@@ -743,7 +825,7 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   }
   if constexpr (!PIPE) {
     static_for<0, NST - 1>([&](auto st) {
-      if (kt0 + (int)decltype(st)::value < KT) compute(st);
+      if (kt0 + (int)decltype(st)::value < KT) compute(st, kt0 + (int)decltype(st)::value);
     });
   } else if constexpr (KG == 2) {
 #pragma unroll
@@ -1395,7 +1477,8 @@ static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
   if ((a.K / SK) % KG != 0) return hipErrorInvalidValue;  // both K parts need equal stage counts
   if (PIPE && (a.K / SK / KG) % NST != 0) return hipErrorInvalidValue;  // whole rounds per part
   const TileMap tm = make_tile_map(
-      a, a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z || AM == A_CONVP ? a.conv_c : a.K, BM, BN);
+      a, a.M, a.N, a.K, AM == A_CONV5 || AM == A_CONV3Z || AM == A_CONVP || AM == A_CONVW ? a.conv_c : a.K,
+      BM, BN);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, SK, NST, AM, EPI, WM, WN, KG, SP, PIPE>), dim3(8 * tm.per_xcd),
                      dim3(64 * WM * WN * (PIPE ? 1 : KG)), 0, s,
                      a, tm);
@@ -1501,9 +1584,51 @@ static bool pipe_fits(const GemmArgs& a) {
 //    for 64 x 32 (64 x 96 below 256 tiles).  128- and 256-row tiles lose at
 //    the 48- and 24-channel stages (one workgroup per CU).
 // The transposed convs (SP = 2) found nothing faster.
+// A_CONVW: the vocoder's narrow convs (24 to 96 channels, N <= 96), whose
+// streamed form re-reads every input row once per tap, keep the row block's
+// input window in LDS and stream only W, with the tiles the streamed form
+// uses for those widths (the same MFMAs in the same K order, so the same
+// bits).  The window must fit its LDS buffer, and conv_c >= 24 (a lane's K
+// chunk is at most one tap past its K step's first position).
+template <int BM, int BN, int NW, int SP>
+static bool conv_window_fits(const GemmArgs& a) {
+  constexpr long AS = SP >= 1 ? 2 : 1;
+  const long chunks = AS * (BM + (long)(a.conv_k - 1) * a.conv_d) * conv_window_chunks(a.conv_c);
+  const long nt = 64L * NW;
+  return a.conv_c >= 24 && (chunks + nt - 1) / nt * nt * 8 <= conv_window_halves(BM, BN, (int)AS);
+}
+
+template <int EPI, int SP>
+static bool launch_conv_window(const GemmArgs& a0, hipStream_t s, hipError_t& e) {
+  GemmArgs a = a0;
+  a.conv_magic = (uint32_t)(((uint64_t(1) << 32) + (uint64_t)a.conv_c - 1) / (uint64_t)a.conv_c);
+  if ((uint64_t)a.K * (uint64_t)a.conv_c >= (uint64_t(1) << 32)) return false;
+  if (a.N == 96) {
+    if (tile_count(a, 128, 96) >= 256 && conv_window_fits<128, 96, 4, SP>(a)) {
+      e = launch_tile<128, 96, 64, 3, A_CONVW, EPI, 4, 1, 1, SP>(a, s);
+      return true;
+    }
+    if (conv_window_fits<64, 96, 4, SP>(a)) {
+      e = launch_tile<64, 96, 64, 3, A_CONVW, EPI, 4, 1, 1, SP>(a, s);
+      return true;
+    }
+  } else if (a.N == 64 && conv_window_fits<64, 64, 4, SP>(a)) {
+    e = launch_tile<64, 64, 64, 3, A_CONVW, EPI, 2, 2, 1, SP>(a, s);
+    return true;
+  } else if (a.N == 32 && conv_window_fits<64, 32, 4, SP>(a)) {
+    e = launch_tile<64, 32, 64, 3, A_CONVW, EPI, 4, 1, 1, SP>(a, s);
+    return true;
+  }
+  return false;
+}
+
 template <int AM, int EPI, int SP>
 static hipError_t launch_split(const GemmArgs& a, hipStream_t s) {
   if constexpr (AM == A_CONVP) {
+    if constexpr (SP >= 1 && (EPI == EPI_F32 || EPI == EPI_RESAVG)) {
+      hipError_t e;
+      if (a.conv_window && a.M == a.T && a.row_nb == 0 && launch_conv_window<EPI, SP>(a, s, e)) return e;
+    }
     if constexpr (SP == 1) {
       if (a.N % 128 == 0 && a.row_nb == 0) {
         const long t128 = tile_count(a, 128, 128), t192 = tile_count(a, 192, 128);
@@ -1607,7 +1732,7 @@ static bool gemm_spans_fit(const GemmArgs& a, AMode am) {
   if (a.N <= 0 || a.M <= 0 || a.K <= 0 || a.ldw < 0 || a.lda < 0 || a.lda2 < 0) return false;
   const size_t w = ((size_t)(a.N - 1) * a.ldw + a.K + a.w_lo) * 2;
   const size_t rows = am == A_CONV3Z ? (size_t)a.M + 1 : (size_t)a.M;
-  const size_t aa = am == A_CONVP ? (size_t)a.M * a.lda : (rows * a.lda + a.a_lo) * 2;
+  const size_t aa = am == A_CONVP || am == A_CONVW ? (size_t)a.M * a.lda : (rows * a.lda + a.a_lo) * 2;
   const size_t a2 = am == A_CONCAT ? ((size_t)a.M * a.lda2 + a.a_lo) * 2 : 0;
   return w < kMax && aa < kMax && a2 < kMax;
 }

@@ -27,6 +27,7 @@
 
 #include <array>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 
@@ -263,6 +264,10 @@ struct Vocoder::Impl {
   size_t mel16_lo = 0, pre16_lo = 0, a16_lo = 0, g16_lo = 0;
   float *x32, *h32, *t32, *g32, *act32;
   bool f32 = true;  // split operands (fp32-level products); false: f16 operands
+  // Narrow convs with their input window resident in LDS (the same bits as
+  // streaming every tap's rows; MIT2CFM_CONV_WINDOW=0 at construction turns
+  // it off, for comparison).
+  int conv_window = 1;
 
   // Weights as split pairs: [n] hi halves, then [n] lo halves.
   void upload_f16(half_t*& d, const std::vector<float>& v) {
@@ -431,6 +436,7 @@ struct Vocoder::Impl {
     g.conv_pad = pad;
     g.conv_inv_c = 1.0f / (float)c.cin;
     g.A_zero = zero;
+    g.conv_window = conv_window;
     g.W = c.w;
     g.ldw = c.K;
     g.bias = c.b;
@@ -528,6 +534,7 @@ Vocoder::Vocoder(const std::unordered_map<std::string, std::vector<float>>& t, h
     : d_(new Impl) {
   Impl& d = *d_;
   d.s = stream;
+  if (const char* e = std::getenv("MIT2CFM_CONV_WINDOW")) d.conv_window = std::atoi(e) != 0;
   d.wa.reserve(size_t(600) << 20);  // ~236 MB of f16 weights, twice (split pairs)
   try {
     d.make_conv(d.pre, t, "bigvgan.conv_pre", 1536, 80, 7, true);
@@ -604,6 +611,7 @@ void Vocoder::append_image(std::vector<uint8_t>& out) const {
 Vocoder::Vocoder(const uint8_t* image, size_t bytes, hipStream_t stream) : d_(new Impl) {
   Impl& d = *d_;
   d.s = stream;
+  if (const char* e = std::getenv("MIT2CFM_CONV_WINDOW")) d.conv_window = std::atoi(e) != 0;
   try {
     ImageReader r{image, bytes};
     const uint64_t used = r.get<uint64_t>();

@@ -161,6 +161,56 @@ def test_vocoder_matches_oracle(orc, ctx_bv, bv, tokens, amp):
 
 
 @pytest.fixture(scope="module")
+def ctx_bv_stream(mit2, tensors, bv_tensors):
+    """A context whose narrow convs stream every tap's rows (the window form
+    off: MIT2CFM_CONV_WINDOW=0 is read when the vocoder is built)."""
+    import os
+    old = os.environ.get("MIT2CFM_CONV_WINDOW")
+    os.environ["MIT2CFM_CONV_WINDOW"] = "0"
+    try:
+        c = mit2.Context({**tensors, **bv_tensors}, device=0)
+    finally:
+        if old is None:
+            del os.environ["MIT2CFM_CONV_WINDOW"]
+        else:
+            os.environ["MIT2CFM_CONV_WINDOW"] = old
+    yield c
+    c.close()
+
+
+# The narrow convs (96, 48 and 24 channels, the upsamplers into them) read
+# their operand from a row block's input window held in LDS; the products are
+# the same MFMAs in the same K order as the streamed form's, so every output
+# bit must match.  Cases: rows fewer than one tile, ragged last tiles, the
+# 128-row tile of the 96-channel convs (>= 256 row tiles), every kernel size
+# (3, 7, 11) and dilation (1, 3, 5) through the resblocks, and a whole call.
+@pytest.mark.parametrize("stage,index,tokens", [
+    ("resblock", 9, 37), ("resblock", 10, 1000), ("resblock", 11, 32768 + 77),
+    ("resblock", 12, 5), ("resblock", 13, 4099), ("resblock", 14, 20000),
+    ("resblock", 15, 63), ("resblock", 16, 12345), ("resblock", 17, 65536 + 3),
+    ("upsample", 4, 300), ("upsample", 5, 1031)])
+def test_conv_window_same_bits(ctx_bv, ctx_bv_stream, stage, index, tokens):
+    if stage == "resblock":
+        C = 768 >> (index // 3)
+    else:
+        C = [1536, 768, 384, 192, 96, 48][index]
+    x = _x(tokens, C, 500 + index)
+    print(f"{stage} {index} T={tokens} C={C}", flush=True)
+    got = ctx_bv.bigvgan_stage(stage, index, x)
+    ref = ctx_bv_stream.bigvgan_stage(stage, index, x)
+    assert got.shape == ref.shape
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_conv_window_same_bits_vocoder(ctx_bv, ctx_bv_stream):
+    tokens = 97
+    mel = (sincos_series(tokens * 80, 0.013, 0.031, 2.0, 1.0, 19).reshape(tokens, 80) - 5.0).astype(np.float32)
+    got = ctx_bv.bigvgan(mel)
+    ref = ctx_bv_stream.bigvgan(mel)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
 def ctx_bv16(mit2, tensors, bv_tensors):
     c = mit2.Context({**tensors, **bv_tensors}, device=0)
     c.set_precision("vocoder", "f16")
