@@ -33,11 +33,11 @@ enum AMode : int {
 // rows m0 - conv_pad .. m0 + BM - 1 + (conv_k - 1) conv_d - conv_pad of the
 // operand, each padded to conv_window_chunks(conv_c) 16-byte chunks (the
 // extra ones zero: the padded K positions read them), for each half of a
-// split pair.  Sized for BM + 56 rows of BN + 16 halves (the vocoder's
-// resblock convs have conv_c <= N and (conv_k - 1) conv_d <= 50), rounded to
-// whole 512-lane fill rounds.
+// split pair.  Sized for BM + 50 rows of BN + 8 halves (the vocoder's convs
+// have conv_c <= N and (conv_k - 1) conv_d <= 50), rounded to whole 512-lane
+// fill rounds.
 constexpr int conv_window_halves(int bm, int bn, int copies) {
-  return (copies * (bm + 56) * (bn + 16) + 4095) / 4096 * 4096;
+  return (copies * (bm + 50) * (bn + 8) + 4095) / 4096 * 4096;
 }
 // 16-byte chunks per window row: conv_c / 8 data chunks and at least one zero
 // chunk, an odd count (a row stride of an odd number of 16-byte chunks puts

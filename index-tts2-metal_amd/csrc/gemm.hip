@@ -158,27 +158,37 @@ __global__ __launch_bounds__(64 * WM * WN * (PIPE ? 1 : KG)) void gemm_kernel(Ge
   // let the compiler keep only the explicit vmcnt waits).
   // With KG = 2 K groups, each group has its own region in every buffer;
   // split operands keep their lo halves after all the groups' hi halves.
-  constexpr int kAStage = kWin ? 8 : AS * KW * BM * SK;
-  __shared__ __attribute__((aligned(1024))) half_t sA0[kAStage];
-  __shared__ __attribute__((aligned(1024))) half_t sA1[kAStage];
-  __shared__ __attribute__((aligned(1024))) half_t sA2[NST > 2 ? kAStage : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA3[NST > 3 ? kAStage : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA4[NST > 4 ? kAStage : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA5[NST > 5 ? kAStage : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA6[NST > 6 ? kAStage : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sA7[NST > 7 ? kAStage : 8];
+  constexpr int kAStage = kWin ? 8 : AS * KW * BM * SK;  // halves of an A ring buffer
+  constexpr int kBStage = WS * KW * BN * SK;
+  constexpr int kA2 = NST > 2 ? kAStage : 8, kA3 = NST > 3 ? kAStage : 8, kA4 = NST > 4 ? kAStage : 8,
+                kA5 = NST > 5 ? kAStage : 8, kA6 = NST > 6 ? kAStage : 8, kA7 = NST > 7 ? kAStage : 8;
+  constexpr int kB2 = NST > 2 ? kBStage : 8, kB3 = NST > 3 ? kBStage : 8, kB4 = NST > 4 ? kBStage : 8,
+                kB5 = NST > 5 ? kBStage : 8, kB6 = NST > 6 ? kBStage : 8, kB7 = NST > 7 ? kBStage : 8;
+  // Unused buffers are 8 halves; with the window they are 16-byte aligned
+  // (a 1024-byte slot each would not leave the window room).
+  constexpr int kPad = kWin ? 16 : 1024;
+#define MIT2_LDS_ALIGN(n) alignas((n) > 8 ? 1024 : kPad)
+  __shared__ MIT2_LDS_ALIGN(kAStage) half_t sA0[kAStage];
+  __shared__ MIT2_LDS_ALIGN(kAStage) half_t sA1[kAStage];
+  __shared__ MIT2_LDS_ALIGN(kA2) half_t sA2[kA2];
+  __shared__ MIT2_LDS_ALIGN(kA3) half_t sA3[kA3];
+  __shared__ MIT2_LDS_ALIGN(kA4) half_t sA4[kA4];
+  __shared__ MIT2_LDS_ALIGN(kA5) half_t sA5[kA5];
+  __shared__ MIT2_LDS_ALIGN(kA6) half_t sA6[kA6];
+  __shared__ MIT2_LDS_ALIGN(kA7) half_t sA7[kA7];
   // A_CONVW: the row block's input window (hi rows, then lo rows)
   constexpr int kWinH = kWin ? conv_window_halves(BM, BN, AS) : 8;
-  __shared__ __attribute__((aligned(1024))) half_t sWin[kWinH];
+  __shared__ MIT2_LDS_ALIGN(kWinH) half_t sWin[kWinH];
   static_assert(!kWin || kWinH / (8 * 64 * NW) + L * (NST - 1) < 64, "too many loads in flight");
-  __shared__ __attribute__((aligned(1024))) half_t sB0[WS * KW * BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB1[WS * KW * BN * SK];
-  __shared__ __attribute__((aligned(1024))) half_t sB2[NST > 2 ? WS * KW * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB3[NST > 3 ? WS * KW * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB4[NST > 4 ? WS * KW * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB5[NST > 5 ? WS * KW * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB6[NST > 6 ? WS * KW * BN * SK : 8];
-  __shared__ __attribute__((aligned(1024))) half_t sB7[NST > 7 ? WS * KW * BN * SK : 8];
+  __shared__ MIT2_LDS_ALIGN(kBStage) half_t sB0[kBStage];
+  __shared__ MIT2_LDS_ALIGN(kBStage) half_t sB1[kBStage];
+  __shared__ MIT2_LDS_ALIGN(kB2) half_t sB2[kB2];
+  __shared__ MIT2_LDS_ALIGN(kB3) half_t sB3[kB3];
+  __shared__ MIT2_LDS_ALIGN(kB4) half_t sB4[kB4];
+  __shared__ MIT2_LDS_ALIGN(kB5) half_t sB5[kB5];
+  __shared__ MIT2_LDS_ALIGN(kB6) half_t sB6[kB6];
+  __shared__ MIT2_LDS_ALIGN(kB7) half_t sB7[kB7];
+#undef MIT2_LDS_ALIGN
   constexpr int kALo = KW * BM * SK;  // offset of a stage's lo half in its buffer
   constexpr int kWLo = KW * BN * SK;
   static_assert(NST >= 2 && NST <= 8, "two to eight stages");
@@ -1584,12 +1594,14 @@ static bool pipe_fits(const GemmArgs& a) {
 //    for 64 x 32 (64 x 96 below 256 tiles).  128- and 256-row tiles lose at
 //    the 48- and 24-channel stages (one workgroup per CU).
 // The transposed convs (SP = 2) found nothing faster.
-// A_CONVW: the vocoder's narrow convs (24 to 96 channels, N <= 96), whose
+// A_CONVW: the vocoder's narrower convs (24 to 192 channels), whose
 // streamed form re-reads every input row once per tap, keep the row block's
-// input window in LDS and stream only W, with the tiles the streamed form
-// uses for those widths (the same MFMAs in the same K order, so the same
-// bits).  The window must fit its LDS buffer, and conv_c >= 24 (a lane's K
-// chunk is at most one tap past its K step's first position).
+// input window in LDS and stream only W (the same MFMAs in the same K order
+// as the streamed form, so the same bits).  Tiles: the streamed form's for
+// 24 and 96 channels; 128 x 64 (4 x 1 waves) for 48 channels at >= 256 row
+// tiles; 64 x 192 with a 2-stage W ring for 192 channels (the window leaves
+// no room for a third).  The window must fit its LDS buffer, and conv_c >= 24
+// (a lane's K chunk is at most one tap past its K step's first position).
 template <int BM, int BN, int NW, int SP>
 static bool conv_window_fits(const GemmArgs& a) {
   constexpr long AS = SP >= 1 ? 2 : 1;
@@ -1612,9 +1624,22 @@ static bool launch_conv_window(const GemmArgs& a0, hipStream_t s, hipError_t& e)
       e = launch_tile<64, 96, 64, 3, A_CONVW, EPI, 4, 1, 1, SP>(a, s);
       return true;
     }
-  } else if (a.N == 64 && conv_window_fits<64, 64, 4, SP>(a)) {
-    e = launch_tile<64, 64, 64, 3, A_CONVW, EPI, 2, 2, 1, SP>(a, s);
-    return true;
+  } else if (a.N == 192) {
+    if constexpr (SP == 1) {  // (a split W would not leave the window room)
+      if (conv_window_fits<64, 192, 8, SP>(a)) {
+        e = launch_tile<64, 192, 64, 2, A_CONVW, EPI, 4, 2, 1, SP>(a, s);
+        return true;
+      }
+    }
+  } else if (a.N == 64) {
+    if (tile_count(a, 128, 64) >= 256 && conv_window_fits<128, 64, 4, SP>(a)) {
+      e = launch_tile<128, 64, 64, 3, A_CONVW, EPI, 4, 1, 1, SP>(a, s);
+      return true;
+    }
+    if (conv_window_fits<64, 64, 4, SP>(a)) {
+      e = launch_tile<64, 64, 64, 3, A_CONVW, EPI, 2, 2, 1, SP>(a, s);
+      return true;
+    }
   } else if (a.N == 32 && conv_window_fits<64, 32, 4, SP>(a)) {
     e = launch_tile<64, 32, 64, 3, A_CONVW, EPI, 4, 1, 1, SP>(a, s);
     return true;

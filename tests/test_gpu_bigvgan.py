@@ -178,17 +178,19 @@ def ctx_bv_stream(mit2, tensors, bv_tensors):
     c.close()
 
 
-# The narrow convs (96, 48 and 24 channels, the upsamplers into them) read
+# The narrow convs (192, 96, 48 and 24 channels, the upsamplers into them) read
 # their operand from a row block's input window held in LDS; the products are
 # the same MFMAs in the same K order as the streamed form's, so every output
 # bit must match.  Cases: rows fewer than one tile, ragged last tiles, the
-# 128-row tile of the 96-channel convs (>= 256 row tiles), every kernel size
-# (3, 7, 11) and dilation (1, 3, 5) through the resblocks, and a whole call.
+# 128-row tiles of the 96- and 48-channel convs (>= 256 row tiles), every
+# kernel size (3, 7, 11) and dilation (1, 3, 5) through the resblocks, and a
+# whole call.
 @pytest.mark.parametrize("stage,index,tokens", [
     ("resblock", 9, 37), ("resblock", 10, 1000), ("resblock", 11, 32768 + 77),
-    ("resblock", 12, 5), ("resblock", 13, 4099), ("resblock", 14, 20000),
+    ("resblock", 12, 5), ("resblock", 13, 4099), ("resblock", 14, 40000 + 11),
     ("resblock", 15, 63), ("resblock", 16, 12345), ("resblock", 17, 65536 + 3),
-    ("upsample", 4, 300), ("upsample", 5, 1031)])
+    ("resblock", 6, 70), ("resblock", 7, 3001), ("resblock", 8, 27520 + 9),
+    ("upsample", 3, 500), ("upsample", 4, 300), ("upsample", 5, 1031)])
 def test_conv_window_same_bits(ctx_bv, ctx_bv_stream, stage, index, tokens):
     if stage == "resblock":
         C = 768 >> (index // 3)
