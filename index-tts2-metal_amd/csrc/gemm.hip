@@ -1625,7 +1625,7 @@ static bool launch_conv_window(const GemmArgs& a0, hipStream_t s, hipError_t& e)
       return true;
     }
   } else if (a.N == 192) {
-    if constexpr (SP == 1) {  // (a split W would not leave the window room)
+    if constexpr (SP <= 1) {  // (a split W would not leave the window room)
       if (conv_window_fits<64, 192, 8, SP>(a)) {
         e = launch_tile<64, 192, 64, 2, A_CONVW, EPI, 4, 2, 1, SP>(a, s);
         return true;
@@ -1688,6 +1688,10 @@ static hipError_t launch_am_epi(const GemmArgs& a, hipStream_t s) {
   if constexpr (AM == A_CONVP) {
     // The vocoder's convs: M is long (thousands to hundreds of thousands of
     // samples), N is the channel count (zero-padded to the tile width).
+    if constexpr (EPI == EPI_F32 || EPI == EPI_RESAVG) {
+      hipError_t e;
+      if (a.conv_window && a.M == a.T && a.row_nb == 0 && launch_conv_window<EPI, 0>(a, s, e)) return e;
+    }
     if (a.N % 128 == 0) return launch_tile<64, 128, 64, 3, AM, EPI, 2, 4>(a, s);
     if (a.N % 64 == 0) return launch_tile<64, 64, 64, 3, AM, EPI, 2, 2>(a, s);
     if (a.N % 32 == 0) return launch_tile<64, 32, 64, 3, AM, EPI, 4, 1>(a, s);

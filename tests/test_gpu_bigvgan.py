@@ -204,6 +204,27 @@ def test_conv_window_same_bits(ctx_bv, ctx_bv_stream, stage, index, tokens):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+def test_conv_window_same_bits_f16_mode(ctx_bv, ctx_bv_stream):
+    """The window form in f16 mode (plain f16 operands): 128 x 96 tiles where
+    the streamed form takes 64 x 32, the same bits all the same (one K part,
+    so every tiling sums each output in one order)."""
+    try:
+        for c in (ctx_bv, ctx_bv_stream):
+            c.set_precision("vocoder", "f16")
+        for index, tokens in ((8, 3001), (10, 40000), (13, 4099), (16, 12345)):
+            C = 768 >> (index // 3)
+            x = _x(tokens, C, 700 + index)
+            print(f"f16 resblock {index} T={tokens} C={C}", flush=True)
+            got = ctx_bv.bigvgan_stage("resblock", index, x)
+            ref = ctx_bv_stream.bigvgan_stage("resblock", index, x)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        mel = (sincos_series(97 * 80, 0.013, 0.031, 2.0, 1.0, 23).reshape(97, 80) - 5.0).astype(np.float32)
+        assert np.array_equal(ctx_bv.bigvgan(mel).view(np.uint32), ctx_bv_stream.bigvgan(mel).view(np.uint32))
+    finally:
+        for c in (ctx_bv, ctx_bv_stream):
+            c.set_precision("vocoder", "f32")
+
+
 def test_conv_window_same_bits_vocoder(ctx_bv, ctx_bv_stream):
     tokens = 97
     mel = (sincos_series(tokens * 80, 0.013, 0.031, 2.0, 1.0, 19).reshape(tokens, 80) - 5.0).astype(np.float32)
