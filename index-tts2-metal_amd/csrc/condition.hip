@@ -88,9 +88,28 @@ __global__ __launch_bounds__(1024) void gn_mish_kernel(const float* __restrict__
   __shared__ double w1[16], w2[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   double a = 0.0, b = 0.0;
-  for (int i = tid; i < nparts; i += 1024) {
-    a += (double)sum_parts[i];
-    b += (double)ssq_parts[i];
+  // The thread's share, 16 loads issued before the adds that use them (one
+  // at a time, each add waited for its own load: a chain of L2 round trips);
+  // the adds keep the share's order.  Buffer loads past nparts return zero,
+  // so the loads need no branch (a branch around each made it wait again).
+  constexpr int kU = 16;
+  const buffer_rsrc_t rs = make_buffer_rsrc(sum_parts, nparts * 4);
+  const buffer_rsrc_t rq = make_buffer_rsrc(ssq_parts, nparts * 4);
+  for (int i0 = tid; i0 < nparts; i0 += 1024 * kU) {
+    float va[kU], vb[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = i0 + u * 1024;
+      va[u] = buffer_load_f32(rs, i * 4);
+      vb[u] = buffer_load_f32(rq, i * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (i0 + u * 1024 < nparts) {
+        a += (double)va[u];
+        b += (double)vb[u];
+      }
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
