@@ -512,9 +512,10 @@ Same run as profiles/cfm_decode_T860_S25_B2_kernel_trace.md:
 ```
 
 bench.py `vocoder` without the profiler: default (fp32-level) mode {vp['ms_per_call']:.3f} ms per call, f16 mode
-{vp.get('f16_mode', {}).get('ms_per_call', float('nan')):.3f} ms.  `gemm_kernel` rows are the implicit-GEMM convs (A_CONVP), keyed by
-grid size and workgroup size; `snake` rows are the anti-aliased SnakeBeta activations.  Algorithmic conv work:
-1.551 TFLOP per call.
+{vp.get('f16_mode', {}).get('ms_per_call', float('nan')):.3f} ms.  `gemm_kernel` rows are the implicit-GEMM convs, keyed by
+grid size and workgroup size: the 768- and 384-channel stages streaming every tap's rows (A_CONVP), the 192- to
+24-channel stages and the upsamplers that read them with the row block's input window in LDS (A_CONVW); `snake` rows
+are the anti-aliased SnakeBeta activations.  Algorithmic conv work: 1.551 TFLOP per call.
 
 ```
 {voc}
