@@ -171,10 +171,23 @@ __global__ __launch_bounds__(256) void conv_post_clamp_kernel(const float* __res
   __shared__ float as[262 * RS];
   const int t0 = blockIdx.x * 256;
   if (threadIdx.x < 24 * 7) ws[threadIdx.x] = w[threadIdx.x];
-  for (int idx = threadIdx.x; idx < 262 * 24; idx += 256) {
-    const int row = idx / 24, ic = idx - (idx / 24) * 24;
-    const int src = t0 - 3 + row;
-    as[row * RS + ic] = (src >= 0 && src < T) ? a[(size_t)src * 24 + ic] : 0.0f;
+  // The block's rows through a buffer resource, every load issued before the
+  // first LDS store: rows outside [0, T) fall outside its range (a negative
+  // offset too, read as unsigned) and load zero, so no branch surrounds a
+  // load (one per element made each wait for the one before).  The host
+  // keeps T x 24 x 4 bytes below 2^31.
+  const buffer_rsrc_t rA = make_buffer_rsrc(a, T * 24 * 4);
+  constexpr int kN = (262 * 24 + 255) / 256;
+  float v[kN];
+#pragma unroll
+  for (int u = 0; u < kN; ++u) {
+    const int idx = threadIdx.x + u * 256;
+    v[u] = buffer_load_f32(rA, ((t0 - 3) * 24 + idx) * 4);  // row t0 - 3 + idx / 24, channel idx % 24
+  }
+#pragma unroll
+  for (int u = 0; u < kN; ++u) {
+    const int idx = threadIdx.x + u * 256;
+    if (idx < 262 * 24) as[(idx / 24) * RS + idx % 24] = v[u];
   }
   __syncthreads();
   const int t = t0 + threadIdx.x;
