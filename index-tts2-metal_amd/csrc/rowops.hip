@@ -109,13 +109,25 @@ __global__ __launch_bounds__(256) void norm_bias_kernel(const float* __restrict_
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const half8 w = *reinterpret_cast<const half8*>(W + (size_t)n * 512 + lane * 8);
-  for (int st = 0; st < S; ++st) {
-    const float4* ar = reinterpret_cast<const float4*>(ab + (size_t)st * ab_ld) + lane * 2;
-    const float4 a = ar[0], b = ar[1];
-    float acc = a.x * (float)w[0] + a.y * (float)w[1] + a.z * (float)w[2] + a.w * (float)w[3] +
-                b.x * (float)w[4] + b.y * (float)w[5] + b.z * (float)w[6] + b.w * (float)w[7];
-    acc = warp_sum(acc);
-    if (lane == 0) out[(size_t)st * out_ld + n] = acc;
+  // Four steps' rows requested together (a step's loads each waited for the
+  // previous step's sum); rows past S are clamped to the last and not stored.
+  constexpr int kSteps = 4;
+  for (int s0 = 0; s0 < S; s0 += kSteps) {
+    float4 a[kSteps], b[kSteps];
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const float4* ar = reinterpret_cast<const float4*>(ab + (size_t)min(s0 + u, S - 1) * ab_ld) + lane * 2;
+      a[u] = ar[0];
+      b[u] = ar[1];
+    }
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      if (s0 + u >= S) break;
+      float acc = a[u].x * (float)w[0] + a[u].y * (float)w[1] + a[u].z * (float)w[2] + a[u].w * (float)w[3] +
+                  b[u].x * (float)w[4] + b[u].y * (float)w[5] + b[u].z * (float)w[6] + b[u].w * (float)w[7];
+      acc = warp_sum(acc);
+      if (lane == 0) out[(size_t)(s0 + u) * out_ld + n] = acc;
+    }
   }
 }
 
